@@ -1,0 +1,188 @@
+"""Seeded synthetic models with Seoul's shapes, written as GGUF files the engine (and imi) read.
+
+Brain ("lfm3" keys, tensor names as imi/core/seoul.cpp:93-165 reads them): gated short-conv blocks and GQA attention
+blocks with q/k norms and a per-head sigmoid gate, SwiGLU FFN, post-norm residuals, tied Q4_0 word table.
+Voice generator ("a.gen.code." names as imi/core/voice.cpp:78-139 reads them): Q8_0 depthformer layers, proj_in,
+per-codebook code tables (also the score tables) and feedback rows.
+
+Weights: Q4_0 blocks with scale fp16(|N(0, 0.02)| / 8) and uniform 4-bit codes 0..15 (random bytes are exactly two
+uniform nibbles); Q8_0 blocks with the same scales and int8 codes uniform in [-127, 127]. Norm weights
+1 + 0.05 N(0, 1), conv taps N(0, 0.3) (fp32). Every tensor has its own seed derived from the model seed and its
+name, so a model is reproducible tensor by tensor.
+"""
+from __future__ import annotations
+
+import hashlib
+import os
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from .gguf import GGUFWriter, Q4_0_BLOCK, Q8_0_BLOCK, T_F32, T_Q4_0, T_Q8_0
+
+
+@dataclass
+class BrainShape:
+    n_embd: int = 2048
+    n_layer: int = 16
+    attn_layers: tuple = (2, 5, 8, 10, 12, 14)   # the other layers are short-conv blocks
+    n_head: int = 32
+    n_head_kv: int = 8
+    head_dim: int = 64
+    n_ff: int = 8192
+    n_vocab: int = 97496
+    conv_kernel: int = 3                          # lfm3.shortconv.l_cache (d_conv = kernel - 1 taps of memory)
+    rope_base: float = 1e6
+    eps: float = 1e-5
+
+
+SEOUL = BrainShape()
+# small model with every feature of the path, for tests that must finish in seconds on the CPU oracle
+TINY = BrainShape(n_embd=256, n_layer=4, attn_layers=(1, 3), n_head=8, n_head_kv=2, head_dim=32, n_ff=512,
+                  n_vocab=1000, conv_kernel=3)
+
+
+@dataclass
+class VoiceShape:
+    n_embd: int = 1024
+    n_layer: int = 6
+    n_head: int = 16
+    n_head_kv: int = 4
+    head_dim: int = 64
+    n_ff: int = 4096
+    n_vocab: int = 2048      # codes per codebook
+    n_cb: int = 8            # codebooks
+    n_in: int = 2048         # brain hidden width
+    eps: float = 1e-5
+    rope_theta: float = 1e6
+
+
+VOICE = VoiceShape()
+TINY_VOICE = VoiceShape(n_embd=256, n_layer=2, n_head=4, n_head_kv=2, head_dim=64, n_ff=512, n_vocab=256, n_cb=8,
+                        n_in=256)
+
+
+def _rng(seed: int, name: str) -> np.random.Generator:
+    h = hashlib.sha256(f"{seed}:{name}".encode()).digest()
+    return np.random.default_rng(int.from_bytes(h[:8], "little"))
+
+
+def q4_0_random(rng: np.random.Generator, rows: int, cols: int) -> np.ndarray:
+    """[rows][cols/32] Q4_0 blocks: d = fp16(|N(0,0.02)|/8), 16 random bytes = 32 uniform codes 0..15."""
+    nb = rows * (cols // 32)
+    blk = np.empty(nb, dtype=Q4_0_BLOCK)
+    blk["d"] = (np.abs(rng.standard_normal(nb, dtype=np.float32) * np.float32(0.02)) / np.float32(8)).astype(np.float16)
+    blk["qs"] = np.frombuffer(rng.bytes(nb * 16), dtype=np.uint8).reshape(nb, 16)
+    return blk
+
+
+def q8_0_random(rng: np.random.Generator, rows: int, cols: int) -> np.ndarray:
+    nb = rows * (cols // 32)
+    blk = np.empty(nb, dtype=Q8_0_BLOCK)
+    blk["d"] = (np.abs(rng.standard_normal(nb, dtype=np.float32) * np.float32(0.02)) / np.float32(8)).astype(np.float16)
+    blk["qs"] = rng.integers(-127, 128, size=(nb, 32), dtype=np.int8)
+    return blk
+
+
+def _norm_w(rng, n):
+    return (1.0 + 0.05 * rng.standard_normal(n)).astype(np.float32)
+
+
+def write_brain(path: str, shape: BrainShape = SEOUL, seed: int = 0) -> str:
+    s = shape
+    E, D = s.n_embd, s.head_dim
+    w = GGUFWriter()
+    w.add_str("general.architecture", "lfm3")
+    w.add_u32("lfm3.block_count", s.n_layer)
+    w.add_u32("lfm3.attention.head_count", s.n_head)
+    w.add_u32("lfm3.attention.head_count_kv", s.n_head_kv)
+    w.add_u32("lfm3.attention.key_length", D)
+    w.add_f32("lfm3.attention.layer_norm_rms_epsilon", s.eps)
+    w.add_f32("lfm3.rope.freq_base", s.rope_base)
+    w.add_u32("lfm3.attention.sliding_window", 0)
+    w.add_u32("lfm3.shortconv.l_cache", s.conv_kernel)
+    w.add_u32("lfm3.feed_forward_length", s.n_ff)
+
+    def q4(name, rows, cols):
+        w.add_tensor(name, T_Q4_0, (cols, rows), q4_0_random(_rng(seed, name), rows, cols))
+
+    def f32(name, arr, ne):
+        w.add_tensor(name, T_F32, ne, np.ascontiguousarray(arr, dtype=np.float32))
+
+    q4("token_embd.weight", s.n_vocab, E)
+    f32("output_norm.weight", _norm_w(_rng(seed, "output_norm.weight"), E), (E,))
+    for il in range(s.n_layer):
+        p = f"blk.{il}."
+        for n in ("attn_norm", "post_attention_norm", "ffn_norm", "post_ffw_norm"):
+            f32(p + n + ".weight", _norm_w(_rng(seed, p + n), E), (E,))
+        if il in s.attn_layers:
+            q4(p + "attn_q.weight", s.n_head * D, E)
+            q4(p + "attn_k.weight", s.n_head_kv * D, E)
+            q4(p + "attn_v.weight", s.n_head_kv * D, E)
+            q4(p + "attn_gate.weight", s.n_head, E)
+            q4(p + "attn_output.weight", E, s.n_head * D)
+            f32(p + "attn_q_norm.weight", _norm_w(_rng(seed, p + "q_norm"), D), (D,))
+            f32(p + "attn_k_norm.weight", _norm_w(_rng(seed, p + "k_norm"), D), (D,))
+        else:
+            K = s.conv_kernel
+            cw = (0.3 * _rng(seed, p + "conv").standard_normal((E, K))).astype(np.float32)   # [channel][tap]
+            f32(p + "shortconv.conv.weight", cw, (K, E))
+            q4(p + "shortconv.in_proj.weight", 3 * E, E)
+            q4(p + "shortconv.out_proj.weight", E, E)
+        q4(p + "ffn_gate.weight", s.n_ff, E)
+        q4(p + "ffn_up.weight", s.n_ff, E)
+        q4(p + "ffn_down.weight", E, s.n_ff)
+    w.write(path)
+    return path
+
+
+def write_voice(path: str, shape: VoiceShape = VOICE, seed: int = 1) -> str:
+    s = shape
+    E, D = s.n_embd, s.head_dim
+    w = GGUFWriter()
+    w.add_str("general.architecture", "lfm3-gen")
+    g = "a.gen.code."
+
+    def q8(name, rows, cols, planes=1):
+        ne = (cols, rows) if planes == 1 else (cols, rows, planes)
+        w.add_tensor(g + name, T_Q8_0, ne, q8_0_random(_rng(seed, name), rows * planes, cols))
+
+    def f32(name, arr, ne):
+        w.add_tensor(g + name, T_F32, ne, np.ascontiguousarray(arr, dtype=np.float32))
+
+    q8("embd.weight", s.n_vocab, E, planes=s.n_cb)          # [n_cb][n_vocab][E]: inputs and score tables
+    q8("out_embd.weight", s.n_vocab * s.n_cb, s.n_in)       # feedback rows, n_in wide
+    q8("proj_in.weight", s.n_cb * E, s.n_in)
+    f32("proj_in.bias", (0.1 * _rng(seed, "proj_in.bias").standard_normal(s.n_cb * E)), (s.n_cb * E,))
+    f32("mask_embd", (0.1 * _rng(seed, "mask_embd").standard_normal(E)), (E,))
+    f32("output_norm.weight", _norm_w(_rng(seed, "output_norm"), E), (E,))
+    f32("head_norm.weight", _norm_w(_rng(seed, "head_norm"), s.n_cb * E), (E, s.n_cb))
+    for il in range(s.n_layer):
+        p = f"blk.{il}."
+        f32(p + "ln1.weight", _norm_w(_rng(seed, p + "ln1"), E), (E,))
+        f32(p + "ln2.weight", _norm_w(_rng(seed, p + "ln2"), E), (E,))
+        f32(p + "attn_q_norm.weight", _norm_w(_rng(seed, p + "qn"), D), (D,))
+        f32(p + "attn_k_norm.weight", _norm_w(_rng(seed, p + "kn"), D), (D,))
+        q8(p + "attn_q.weight", s.n_head * D, E)
+        q8(p + "attn_k.weight", s.n_head_kv * D, E)
+        q8(p + "attn_v.weight", s.n_head_kv * D, E)
+        q8(p + "attn_gate.weight", s.n_head, E)
+        q8(p + "attn_out.weight", E, s.n_head * D)
+        q8(p + "ffn_gate.weight", s.n_ff, E)
+        q8(p + "ffn_up.weight", s.n_ff, E)
+        q8(p + "ffn_down.weight", E, s.n_ff)
+    w.write(path)
+    return path
+
+
+def cached(kind: str, shape, seed: int, directory: str | None = None) -> str:
+    """Write the model once per (kind, shape, seed) into a cache directory and return its path."""
+    directory = directory or os.environ.get("NUNCHI_MODEL_DIR", "/tmp/nunchi_models")
+    os.makedirs(directory, exist_ok=True)
+    tag = hashlib.sha256(repr((kind, shape, seed)).encode()).hexdigest()[:16]
+    path = os.path.join(directory, f"{kind}-{tag}.gguf")
+    if not os.path.exists(path):
+        tmp = f"{path}.{os.getpid()}.tmp"
+        (write_brain if kind == "brain" else write_voice)(tmp, shape, seed)
+        os.replace(tmp, path)
+    return path

@@ -1,0 +1,200 @@
+"""ORACLE — test infrastructure only. Float64 "truth key" of the brain and the voice generator.
+
+Restates imi/ref/ref_exact.py:37-87 (brain) and imi/ref/gen_exact.py:27-54 (voice generator): the file's own
+dequantized weights, run in float64 with no input rounding. Used to pin the int8-cut restatement (liboracle) at the
+model level: a dropped term, a wrong sign or a transposed table moves it far outside the cut's error.
+Dequantization is written here from the GGUF block formats (closed forms), not shared with the product code.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from nunchi_amd.gguf import GGUFFile, Q4_0_BLOCK, Q8_0_BLOCK, T_F16, T_F32, T_Q4_0, T_Q8_0
+
+
+def dequant_q4_0(raw: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """Q4_0: weight i of a block = ((qs[i] & 15) if i < 16 else (qs[i-16] >> 4)) - 8, times the fp16 scale."""
+    b = np.frombuffer(np.ascontiguousarray(raw).tobytes(), dtype=Q4_0_BLOCK).reshape(rows, cols // 32)
+    qs = b["qs"].astype(np.int64)
+    codes = np.concatenate([qs & 15, qs >> 4], axis=-1) - 8              # [rows][nb][32]
+    return (codes * b["d"].astype(np.float64)[..., None]).reshape(rows, cols)
+
+
+def dequant_q8_0(raw: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    b = np.frombuffer(np.ascontiguousarray(raw).tobytes(), dtype=Q8_0_BLOCK).reshape(rows, cols // 32)
+    return (b["qs"].astype(np.float64) * b["d"].astype(np.float64)[..., None]).reshape(rows, cols)
+
+
+class Weights:
+    def __init__(self, path: str, prefix: str = ""):
+        self.f = GGUFFile(path)
+        self.prefix = prefix
+        self._cache = {}
+
+    def has(self, name):
+        return self.prefix + name in self.f.tensors
+
+    def __call__(self, name) -> np.ndarray:
+        name = self.prefix + name
+        if name in self._cache:
+            return self._cache[name]
+        t = self.f.tensors[name]
+        cols, rows = t.ne[0], t.rows
+        if t.gtype == T_Q4_0:
+            w = dequant_q4_0(t.data, rows, cols)
+        elif t.gtype == T_Q8_0:
+            w = dequant_q8_0(t.data, rows, cols)
+        elif t.gtype == T_F32:
+            w = np.frombuffer(np.ascontiguousarray(t.data).tobytes(), np.float32).astype(np.float64).reshape(rows, cols)
+        elif t.gtype == T_F16:
+            w = np.frombuffer(np.ascontiguousarray(t.data).tobytes(), np.float16).astype(np.float64).reshape(rows, cols)
+        else:
+            raise ValueError(name)
+        if rows == 1:
+            w = w[0]
+        self._cache[name] = w
+        return w
+
+
+def cut_dequant(x: np.ndarray) -> np.ndarray:
+    """imi's input cut (imi/core/vec.h:47-75) applied in place of a table input, returned as float64 values
+    q * d: per 32 values d = amax / 127 and q = rint(x / d) in float32 arithmetic, as the engine computes them."""
+    x32 = np.asarray(x, np.float32).reshape(*np.shape(x)[:-1], -1, 32)
+    amax = np.abs(x32).max(-1, keepdims=True)
+    d = (amax / np.float32(127)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        idv = np.where(d != 0, np.float32(1) / d, np.float32(0)).astype(np.float32)
+    q = np.rint((x32 * idv).astype(np.float32))
+    return (q.astype(np.float64) * d.astype(np.float64)).reshape(np.shape(x))
+
+
+def brain(path: str, tokens=None, embd=None, cut: bool = False):
+    """Hidden states and logits for every position of one sequence, float64 (ref_exact.py:37-87).
+
+    cut=True also cuts every table input to int8 per 32 exactly where imi's engine does (imi/core/seoul.cpp:405,
+    415, 457, 465, 469, 480) and rounds keys and values through fp16 as its cache does, so what is left between
+    this and the engine is fp32 rounding alone."""
+    C = cut_dequant if cut else (lambda v: v)
+    W = Weights(path)
+    kv = W.f.kv
+    eps = float(kv.get("lfm3.attention.layer_norm_rms_epsilon", 1e-5))
+    base, base_swa = float(kv.get("lfm3.rope.freq_base", 1e6)), float(kv.get("lfm3.rope.freq_base_swa", 1e4))
+    n_swa = int(kv.get("lfm3.attention.sliding_window", 0))
+    n_layer = int(kv["lfm3.block_count"])
+    swa_pat = [bool(x) for x in kv.get("lfm3.attention.sliding_window_pattern", [False] * n_layer)]
+    H, D = int(kv.get("lfm3.attention.head_count", 16)), int(kv.get("lfm3.attention.key_length", 128))
+    ff = W("rope_freqs.weight") if W.has("rope_freqs.weight") else None
+    emb = W("token_embd.weight")
+    X = emb[np.asarray(tokens)] if tokens is not None else np.asarray(embd, np.float64)
+    T = X.shape[0]
+
+    def norm(x, w):
+        return x / np.sqrt((x * x).mean(-1, keepdims=True) + eps) * w
+
+    def rope(v, b, fr):
+        half = D // 2
+        inv = b ** (-np.arange(half) * 2.0 / D)
+        if fr is not None:
+            inv = inv / fr
+        ang = np.arange(T)[:, None] * inv[None, :]
+        c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+        x0, x1 = v[..., :half], v[..., half:]
+        return np.concatenate([x0 * c - x1 * s, x0 * s + x1 * c], -1)
+
+    for il in range(n_layer):
+        p = f"blk.{il}."
+        h = C(norm(X, W(p + "attn_norm.weight")))
+        if W.has(p + "shortconv.conv.weight"):
+            E = X.shape[1]
+            bcx = h @ W(p + "shortconv.in_proj.weight").T
+            b, c, xx = bcx[:, :E], bcx[:, E:2 * E], bcx[:, 2 * E:]
+            cw = W(p + "shortconv.conv.weight")            # [E, K]
+            K = cw.shape[1]
+            bx = np.concatenate([np.zeros((K - 1, E)), b * xx], 0)
+            co = np.stack([(bx[t:t + K] * cw.T).sum(0) for t in range(T)])
+            y = C(c * co) @ W(p + "shortconv.out_proj.weight").T
+        else:
+            q = (h @ W(p + "attn_q.weight").T).reshape(T, H, D)
+            k = h @ W(p + "attn_k.weight").T
+            Hk = k.shape[1] // D
+            k = k.reshape(T, Hk, D)
+            v = (h @ W(p + "attn_v.weight").T).reshape(T, Hk, D)
+            g = 1 / (1 + np.exp(-(h @ W(p + "attn_gate.weight").T)))
+            q, k = norm(q, W(p + "attn_q_norm.weight")), norm(k, W(p + "attn_k_norm.weight"))
+            sw = swa_pat[il] if il < len(swa_pat) else False
+            q = rope(q, base_swa if sw else base, None if sw else ff)
+            k = rope(k, base_swa if sw else base, None if sw else ff)
+            if cut:   # the engine keeps keys and values in an fp16 cache (imi/core/seoul.cpp:438)
+                k = k.astype(np.float32).astype(np.float16).astype(np.float64)
+                v = v.astype(np.float32).astype(np.float16).astype(np.float64)
+            a = np.zeros((T, H, D))
+            for t in range(T):
+                s0 = max(0, t - n_swa + 1) if (sw and n_swa > 0) else 0
+                for hh in range(H):
+                    kv_h = hh // (H // Hk)
+                    sc = k[s0:t + 1, kv_h] @ q[t, hh] / np.sqrt(D)
+                    pr = np.exp(sc - sc.max())
+                    pr /= pr.sum()
+                    a[t, hh] = pr @ v[s0:t + 1, kv_h]
+            a *= g[:, :, None]
+            y = C(a.reshape(T, H * D)) @ W(p + "attn_output.weight").T
+        X = X + norm(y, W(p + "post_attention_norm.weight"))
+        h = C(norm(X, W(p + "ffn_norm.weight")))
+        gg, uu = h @ W(p + "ffn_gate.weight").T, h @ W(p + "ffn_up.weight").T
+        fo = C(gg / (1 + np.exp(-gg)) * uu) @ W(p + "ffn_down.weight").T
+        X = X + norm(fo, W(p + "post_ffw_norm.weight"))
+    hid = norm(X, W("output_norm.weight"))
+    return hid, C(hid) @ emb.T
+
+
+def voice_pass(path: str, hidden, codes, eps=1e-5, theta=1e6):
+    """Scores of every codebook for one pass (gen_exact.py:27-54), float64: [n_cb][n_vocab]."""
+    W = Weights(path, "a.gen.code.")
+    embd_t = W.f.tensors["a.gen.code.embd.weight"]
+    E, V, P = embd_t.ne[0], embd_t.ne[1], embd_t.ne[2]
+    embd = dequant_q8_0(embd_t.data, V * P, E).reshape(P, V, E)
+    mask, onorm = W("mask_embd"), W("output_norm.weight")
+    hnorm = W("head_norm.weight").reshape(P, E)
+    pw, pb = W("proj_in.weight"), W("proj_in.bias")
+    layers = []
+    i = 0
+    while W.has(f"blk.{i}.ln1.weight"):
+        p = f"blk.{i}."
+        layers.append({k: W(p + k + ".weight") for k in ["ln1", "ln2", "attn_q", "attn_k", "attn_v", "attn_out", "attn_gate",
+                                                           "attn_q_norm", "attn_k_norm", "ffn_gate", "ffn_up", "ffn_down"]})
+        i += 1
+    D = layers[0]["attn_q_norm"].shape[0]
+    H = layers[0]["attn_q"].shape[0] // D
+    Hk = layers[0]["attn_k"].shape[0] // D
+
+    def norm(x, w):
+        return x / np.sqrt((x * x).mean(-1, keepdims=True) + eps) * w
+
+    def rope(v):
+        half = D // 2
+        inv = theta ** (-np.arange(half) * 2.0 / D)
+        ang = np.arange(P)[:, None] * inv[None]
+        c, s = np.cos(ang)[:, None], np.sin(ang)[:, None]
+        a, b = v[..., :half], v[..., half:]
+        return np.concatenate([a * c - b * s, a * s + b * c], -1)
+
+    base = (pw @ np.asarray(hidden, np.float64) + pb).reshape(P, -1)
+    x = base + np.stack([embd[c, codes[c]] if codes[c] >= 0 else mask for c in range(P)])
+    for l in layers:
+        hh = norm(x, l["ln1"])
+        q = norm((hh @ l["attn_q"].T).reshape(P, H, D), l["attn_q_norm"])
+        k = norm((hh @ l["attn_k"].T).reshape(P, Hk, D), l["attn_k_norm"])
+        v = (hh @ l["attn_v"].T).reshape(P, Hk, D)
+        g = 1 / (1 + np.exp(-(hh @ l["attn_gate"].T)))
+        q, k = rope(q), rope(k)
+        k, v = np.repeat(k, H // Hk, 1), np.repeat(v, H // Hk, 1)
+        s = np.einsum("phd,thd->hpt", q, k) / np.sqrt(D)
+        s = np.exp(s - s.max(-1, keepdims=True))
+        s /= s.sum(-1, keepdims=True)
+        a = np.einsum("hpt,thd->phd", s, v) * g[:, :, None]
+        x = x + a.reshape(P, -1) @ l["attn_out"].T
+        hh = norm(x, l["ln2"])
+        gg = hh @ l["ffn_gate"].T
+        x = x + (gg / (1 + np.exp(-gg)) * (hh @ l["ffn_up"].T)) @ l["ffn_down"].T
+    z = norm(norm(x, onorm), hnorm)
+    return np.stack([embd[c] @ z[c] for c in range(P)])

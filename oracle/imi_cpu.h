@@ -1,0 +1,111 @@
+// ORACLE — test infrastructure only. Nothing under nunchi_amd/ includes, links or calls this.
+//
+// A from-scratch CPU restatement of imi's arithmetic for the brain step (the reference's AVX2 engine,
+// imi/core/{vec.h,tables.cpp,seoul.cpp}, imi/kernels/q4x8.cpp, imi/core/voice.cpp). It is the checker the HIP path
+// is compared with, and, timed on the host cores, the CPU baseline ("imi-cpu").
+//
+// Every function cites the reference file:line it follows. Where the reference fixes an op order (AVX2 lane
+// layouts, FMA chains), the restatement keeps it, because that order is what parity is measured against.
+// Parity pins for each function live in tests/ (closed forms, brute force, invariants); see the header of
+// tests/test_oracle_*.py.
+#pragma once
+#include <cstddef>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+namespace orc {
+
+// ---- fp16 <-> fp32 (imi/core/tables.cpp:20-38) ----
+float    h2f(uint16_t h);          // exact, bit construction as imi_h2f
+uint16_t f2h(float f);             // round to nearest even (F16C _cvtss_sh(f, 0))
+
+// ---- GGUF (minimal reader, own code; format: GGUF v3) ----
+enum gtype : int { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q4_1 = 3, T_Q8_0 = 8, T_Q6_K = 14 };
+struct gtensor {
+    std::string name;
+    int type = 0, n_dims = 0;
+    int64_t ne[4] = {1, 1, 1, 1};
+    size_t offset = 0, nbytes = 0, row_bytes = 0;
+    const uint8_t* data = nullptr;
+};
+struct gfile {
+    std::vector<gtensor> tensors;
+    struct kv { std::string key; int type; int64_t i; double f; std::vector<int64_t> arr; };
+    std::vector<kv> kvs;
+    void* map = nullptr;
+    size_t map_size = 0;
+    bool open(const std::string& path);
+    const gtensor* get(const std::string& name) const;
+    int64_t key_i(const std::string& key, int64_t def) const;
+    float key_f(const std::string& key, float def) const;
+    const std::vector<int64_t>* key_arr(const std::string& key) const;
+    ~gfile();
+};
+
+// ---- 4-bit tables in imi's 8-row layout (imi/core/tables.h:80-114, tables.cpp:67-97) ----
+// per group of 8 rows and block of 32 columns: 128 B of codes (chunk t, bytes 4r..4r+3 = row r, columns 4t..4t+3
+// low nibble, 16+4t..16+4t+3 high nibble), then fp16 scales [group][block][8]
+struct q4tab {
+    int rows = 0, cols = 0, nb = 0;
+    std::vector<uint8_t> codes;    // [rows/8][nb][128]
+    std::vector<uint16_t> d;       // [rows/8][nb][8]
+};
+// rows given as pointers to Q4_0 rows (nb blocks of 18 B each); rows.size() % 8 == 0
+bool q4_build(q4tab& t, const std::vector<const uint8_t*>& rows, int cols);
+int  q4_code_at(const uint8_t* blk128, int r, int k);   // imi/core/tables.cpp:167-169
+
+// ---- activation cut to int8 per 32 (imi/core/vec.h:47-75) ----
+float cut32(const float* x, int8_t* q, int* sum);          // d = amax/127, id = d ? 1/d : 0, q = rint(x*id)
+struct q8in {                                              // imi_q8 (imi/core/tables.h:116-122, tables.cpp:100-109)
+    int n = 0;
+    std::vector<int8_t> q;
+    std::vector<float> d, s;                               // per block: scale, scale * sum of codes
+    void from(const float* x, int n);
+};
+struct q8b {                                               // imi_q8b, block-major (tables.cpp:405-416)
+    int n = 0, cols = 0, nb = 0;
+    std::vector<int8_t> q;                                 // [nb][n][32]
+    std::vector<float> d, s;                               // [nb][n]
+    void shape(int n_in, int n_cols);
+    void set(int i, const float* x);
+};
+
+// ---- Q4 GEMV kernels (imi/core/tables.cpp:115-198, 419-477) ----
+void q4_group(const q4tab& W, const q8in& X, int g, float* out);                                 // AVX2 op order
+void q4_group2(const q4tab& W, const q8in& X, const q8in& X2, int g, float* out, float* out2);
+void q4_group_batch(const q4tab& W, const q8b& X, int g, float* out);                            // out [n][8]
+void q4_group_scalar(const q4tab& W, const q8in& X, int g, float* out);                          // same ops, scalar
+void q4_block_sums(const q4tab& W, const q8in& X, int g, int32_t* sums);                         // [8][nb] integer sums
+
+// ---- cfg-0 kernel: imi/kernels/q4x8.cpp ----
+struct q4x8tab {                                            // imi/kernels/q4x8.h:8-12
+    int rows = 0, cols = 0, nb = 0;
+    std::vector<uint8_t> codes;    // [rows/8][nb][4][32]: byte i of chunk k = code(2k, i) | code(2k+1, i) << 4
+    std::vector<float> scales;     // [rows/8][nb][8]
+};
+void q4x8_build(q4x8tab& t, const uint8_t* q4_0, int rows, int cols);            // q4x8.cpp:105-119
+struct q4x8in { std::vector<int8_t> q; std::vector<float> d, corr; };            // q4x8.cpp:36
+void q4x8_quant_in(const float* x, int n, q4x8in& o);                           // q4x8.cpp:38-48 (roundf)
+void q4x8_rows(const q4x8tab& W, const q4x8in& X, float* y, int g0, int g1);     // q4x8.cpp:51-77
+
+// ---- Q8_0 tables, k-major 8-row layout (imi/core/tables.cpp:289-402) ----
+struct q8gtab {
+    int rows = 0, rows_pad = 0, cols = 0, nb = 0;
+    std::vector<int8_t> codes;     // [rows_pad/8][cols][8]
+    std::vector<uint16_t> d;       // [rows_pad/8][nb][8]
+};
+bool q8g_build(q8gtab& t, const std::vector<const uint8_t*>& rows, int cols);
+void q8g_group(const q8gtab& W, const float* xt, int C, int g, float* out);     // xt [cols][C] -> out [C][8]
+void q8_0_dequant_row(const uint8_t* row, float* y, int cols);
+
+// ---- small vector math (imi/core/vec.h:20-44) ----
+float rms_scale(const float* x, int n, float eps);
+void  norm_mul(const float* x, const float* w, float* o, int n, float eps);
+void  norm_mul_add(const float* y, const float* w, float* x, int n, float eps);
+void  rope(float* v, int n, int pos, float base, const float* ff);              // imi/core/seoul.cpp:19-28
+float dot_h(const float* q, const uint16_t* k, int n);                          // seoul.cpp:29-39
+void  axpy_h(float p, const uint16_t* v, float* o, int n);                      // seoul.cpp:40-47
+
+
+}  // namespace orc
