@@ -1,0 +1,120 @@
+/* seoul_hip.h — C ABI of libseoul_hip.so, the MI355X (gfx950) implementation of imi's brain step.
+ *
+ * This is the boundary a host engine binds to: plain pointers and sizes, int status codes, no exceptions, no torch
+ * or HIP types. Host buffers passed in are borrowed for the call; outputs are written into caller buffers before the
+ * call returns. A context owns one model on one device and one HIP stream; calls on one context are not
+ * thread-safe. A state (one conversation's memory) or table is valid only with the context that made it.
+ * Destroying a context releases the device memory of its remaining states and tables; their handles must still be
+ * released with sh_state_free / sh_q4_free, which then only free the handle.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   imi_seoul / imi_brain engine    imi/core/seoul.h:28-94, imi/brain.h:20-65
+ *   imi_seoul_state                 imi/core/seoul.h:21-26
+ *   imi_file (GGUF read + repack)   imi/model.h:12-36, imi/core/tables.cpp:67-97
+ *   imi_q4x8 kernel API (cfg 0)     imi/kernels/q4x8.h:8-18
+ *   imi_q4 table reads              imi/core/tables.h:103-138
+ *   imi_voice generator             imi/core/voice.h:17-51
+ */
+#ifndef SEOUL_HIP_H
+#define SEOUL_HIP_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define SH_OK 0
+#define SH_E_ARG (-1)           /* bad argument (null pointer, out-of-range id, wrong size) */
+#define SH_E_HIP (-2)           /* a HIP runtime call failed; sh_last_error() names it */
+#define SH_E_FILE (-3)          /* model file unreadable or malformed (imi: load() returns false) */
+#define SH_E_SHAPE (-4)         /* a table or shape the kernels do not take (imi/core/seoul.cpp:162) */
+#define SH_E_CONTEXT_FULL (-5)  /* position would pass n_ctx; nothing was stepped (imi/core/seoul.cpp:209,353,498) */
+#define SH_E_STATE (-6)         /* state belongs to another context, or no model loaded */
+#define SH_E_NOMEM (-7)         /* device or host allocation failed */
+
+typedef struct sh_ctx sh_ctx;       /* one model on one device */
+typedef struct sh_state sh_state;   /* one conversation's memory: K/V caches, conv memory, position */
+typedef struct sh_q4 sh_q4;         /* one Q4_0 table on the device (kernel-level API) */
+typedef struct sh_voice sh_voice;   /* the Q8_0 voice generator on the device */
+
+typedef struct {
+    int n_embd, n_vocab, n_head, n_head_kv, head_dim, n_ff, d_conv, n_ctx, n_layer, n_attn, n_swa;
+    long long table_bytes;          /* bytes of all layer tables + word table in the device layout */
+} sh_model_info;
+
+/* Message of the last error on this thread ("" if none). */
+const char* sh_last_error(void);
+
+/* ---- engine: imi_seoul::load / reset / step / step2 / step_batch / new_state / swap_state ---- */
+int sh_create(int device, sh_ctx** out);
+int sh_destroy(sh_ctx* ctx);
+/* Read a GGUF brain file, repack every Q4_0 table into the device layout and upload it; n_ctx = context length of
+ * states made afterwards (imi/core/seoul.cpp:93-186). */
+int sh_load(sh_ctx* ctx, const char* gguf_path, int n_ctx);
+int sh_info(const sh_ctx* ctx, sh_model_info* out);
+
+int sh_state_new(sh_ctx* ctx, sh_state** out);          /* imi_seoul::new_state (seoul.cpp:193-201) */
+int sh_state_free(sh_state* st);
+int sh_state_reset(sh_state* st);                        /* imi_seoul::reset (seoul.cpp:188-191): pos 0, conv zeroed */
+int sh_state_pos(const sh_state* st, int* pos);
+int sh_state_set_pos(sh_state* st, int pos);             /* rewind (imi/core/hear_pieces.cpp:8-11) */
+
+/* One position (imi_seoul::step, seoul.cpp:352-357): token >= 0 reads that word's row, else embd[n_embd].
+ * hidden[n_embd] (nullable) gets the hidden state; if want_logits, logits[n_vocab] (nullable) gets the word scores
+ * and best (nullable) the first index of their maximum. */
+int sh_step(sh_ctx* ctx, sh_state* st, int32_t token, const float* embd, int want_logits,
+            float* hidden, float* logits, int32_t* best);
+
+/* Two conversations, one read of every table (imi_seoul::step2, seoul.cpp:208-220). Each conversation gets the
+ * numbers its own sh_step would give. */
+int sh_step2(sh_ctx* ctx, sh_state* a, int32_t token_a, const float* embd_a, int logits_a,
+             sh_state* b, int32_t token_b, const float* embd_b, int logits_b,
+             float* hidden_a, float* logits_a_out, int32_t* best_a,
+             float* hidden_b, float* logits_b_out, int32_t* best_b);
+
+/* n positions at once (imi_seoul::step_batch, seoul.cpp:490-517): tokens[n] or embd[n][n_embd]. hidden_last
+ * gets the last position's hidden state, hidden_all[n][n_embd] (nullable) every position's; logits/best are the
+ * last position's. */
+int sh_step_batch(sh_ctx* ctx, sh_state* st, const int32_t* tokens, const float* embd, int n, int want_logits,
+                  float* hidden_last, float* logits, float* hidden_all, int32_t* best);
+
+/* Greedy decode on the device: n_steps steps, each feeding back the argmax of its word scores, for one (b null)
+ * or two conversations (step2). out_a/out_b[n_steps] get the chosen ids; seconds (nullable) the device time.
+ * Equivalent to the greedy loops of imi/core/hear.cpp:66-72 with no host round trip per token. */
+int sh_generate(sh_ctx* ctx, sh_state* a, sh_state* b, int32_t first_a, int32_t first_b, int n_steps,
+                int32_t* out_a, int32_t* out_b, double* seconds);
+
+/* Every layer table read back to back with ncol (1 or 2) inputs riding each read, reps passes
+ * (imi_seoul::bench_tables, seoul.cpp:657-685). ms_per_pass = best pass; avg_launch_us = mean GEMV launch
+ * duration over all passes; bytes_per_pass = table bytes read per pass. */
+int sh_bench_tables(sh_ctx* ctx, int ncol, int reps, double* ms_per_pass, double* avg_launch_us,
+                    double* bytes_per_pass, int* launches_per_pass);
+
+/* ---- kernel-level Q4_0 tables (imi/kernels/q4x8.h:14-18, imi/core/tables.h:103-138) ---- */
+/* q4_0: rows * cols/32 Q4_0 blocks (fp16 scale + 16 nibble bytes) as stored in GGUF; rows % 8 == 0. */
+int sh_q4_create(sh_ctx* ctx, const void* q4_0, int rows, int cols, sh_q4** out);
+int sh_q4_free(sh_q4* t);
+/* y[n_in][rows] = W x[n_in][cols] for n_in in {1, 2}; the input is cut to int8 per 32 columns with round half to
+ * even (cut_mode 0, imi/core/vec.h:47-75) or half away from zero (cut_mode 1, imi/kernels/q4x8.cpp:38-48). */
+int sh_q4_gemv(sh_ctx* ctx, const sh_q4* t, const float* x, int n_in, float* y, int cut_mode);
+/* Dequantized rows: out[n][cols] = (code - 8) * d of rows ids[n] (the input-row lookup of a tied word table,
+ * imi/core/seoul.cpp:363, ggml_get_rows in imi/brain.cpp:161). Bit-exact. */
+int sh_q4_rows(sh_ctx* ctx, const sh_q4* t, const int32_t* ids, int n, float* out);
+/* Same on device-resident buffers (no copies, no synchronisation): x_dev, y_dev are device pointers. */
+int sh_q4_gemv_dev(sh_ctx* ctx, const sh_q4* t, const float* x_dev, int n_in, float* y_dev, int cut_mode);
+/* Time `reps` launches of the GEMV over `n_tables` tables in turn (tables[i] read in rotation so that none is
+ * resident in the 256 MB MALL when the set is larger), inputs resident; avg_launch_us = mean launch duration. */
+int sh_q4_bench(sh_ctx* ctx, sh_q4* const* tables, int n_tables, int n_in, int cut_mode, int reps, double* avg_launch_us);
+
+/* y[i] = e^x[i] with the exponential the kernels use (softmax, SiLU, head gates): bit for bit the C library's expf
+ * that imi runs on (imi/core/seoul.cpp:48,447,451). */
+int sh_expf(sh_ctx* ctx, const float* x, long long n, float* y);
+
+/* Synchronise the context's stream (for callers of the _dev entry points). */
+int sh_sync(sh_ctx* ctx);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,302 @@
+"""nunchi_amd: imi's brain step (the Seoul hybrid LM token loop) on one MI355X.
+
+Python face of libseoul_hip.so (C ABI in include/seoul_hip.h), shaped like imi's engine API
+(imi/core/seoul.h:28-94): Brain.load / reset / step / step2 / step_batch / new_state / swap_state, plus a
+device-side greedy loop and the kernel-level Q4_0 table API (imi/kernels/q4x8.h:14-18). There is no CPU fallback:
+if the HIP library is missing or no GPU is present, constructing a Brain or a Q4Table raises.
+"""
+from __future__ import annotations
+
+import atexit
+import ctypes as C
+import os
+import weakref
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libseoul_hip.so")
+
+SH_OK, SH_E_ARG, SH_E_HIP, SH_E_FILE, SH_E_SHAPE, SH_E_CONTEXT_FULL, SH_E_STATE, SH_E_NOMEM = 0, -1, -2, -3, -4, -5, -6, -7
+EXPORTS = [
+    "sh_last_error", "sh_create", "sh_destroy", "sh_load", "sh_info", "sh_state_new", "sh_state_free", "sh_state_reset",
+    "sh_state_pos", "sh_state_set_pos", "sh_step", "sh_step2", "sh_step_batch", "sh_generate", "sh_bench_tables",
+    "sh_q4_create", "sh_q4_free", "sh_q4_rows", "sh_q4_gemv", "sh_q4_gemv_dev", "sh_q4_bench", "sh_expf", "sh_sync",
+]
+
+
+class SeoulError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"{msg} (status {code})")
+        self.code = code
+
+
+class ContextFull(SeoulError):
+    pass
+
+
+class ModelInfo(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("n_embd", "n_vocab", "n_head", "n_head_kv", "head_dim", "n_ff", "d_conv", "n_ctx",
+                                       "n_layer", "n_attn", "n_swa")] + [("table_bytes", C.c_longlong)]
+
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH):
+    """Load libseoul_hip.so and declare its C ABI. Raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise ImportError(f"{path} is not built: run `python -m nunchi_amd.build` (hipcc, gfx950)")
+    L = C.CDLL(path)
+    vp, i, f, d = C.c_void_p, C.c_int, C.c_float, C.c_double
+    P = C.POINTER
+    sig = {
+        "sh_last_error": (C.c_char_p, []),
+        "sh_create": (i, [i, P(vp)]),
+        "sh_destroy": (i, [vp]),
+        "sh_load": (i, [vp, C.c_char_p, i]),
+        "sh_info": (i, [vp, P(ModelInfo)]),
+        "sh_state_new": (i, [vp, P(vp)]),
+        "sh_state_free": (i, [vp]),
+        "sh_state_reset": (i, [vp]),
+        "sh_state_pos": (i, [vp, P(i)]),
+        "sh_state_set_pos": (i, [vp, i]),
+        "sh_step": (i, [vp, vp, C.c_int32, vp, i, vp, vp, vp]),
+        "sh_step2": (i, [vp, vp, C.c_int32, vp, i, vp, C.c_int32, vp, i, vp, vp, vp, vp, vp, vp]),
+        "sh_step_batch": (i, [vp, vp, vp, vp, i, i, vp, vp, vp, vp]),
+        "sh_generate": (i, [vp, vp, vp, C.c_int32, C.c_int32, i, vp, vp, P(d)]),
+        "sh_bench_tables": (i, [vp, i, i, P(d), P(d), P(d), P(i)]),
+        "sh_q4_create": (i, [vp, vp, i, i, P(vp)]),
+        "sh_q4_free": (i, [vp]),
+        "sh_q4_rows": (i, [vp, vp, vp, i, vp]),
+        "sh_q4_gemv": (i, [vp, vp, vp, i, vp, i]),
+        "sh_q4_gemv_dev": (i, [vp, vp, vp, i, vp, i]),
+        "sh_q4_bench": (i, [vp, vp, i, i, i, i, P(d)]),
+        "sh_expf": (i, [vp, vp, C.c_longlong, vp]),
+        "sh_sync": (i, [vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def _check(rc: int):
+    if rc != SH_OK:
+        msg = _lib.sh_last_error().decode()
+        raise (ContextFull if rc == SH_E_CONTEXT_FULL else SeoulError)(rc, msg)
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+_live_contexts = weakref.WeakSet()
+
+
+class Context:
+    """One device and its stream (sh_create). States and tables made on it are freed before it is destroyed (the
+    C ABI requires it), whatever order the garbage collector finalizes them in."""
+
+    def __init__(self, device: int = 0):
+        load_library()
+        self.h = C.c_void_p()
+        self._children = weakref.WeakSet()
+        _check(_lib.sh_create(device, C.byref(self.h)))
+        _live_contexts.add(self)
+
+    def _adopt(self, obj):
+        self._children.add(obj)
+
+    def close(self):
+        if getattr(self, "h", None) and self.h.value:
+            for ch in list(self._children):
+                ch._free()
+            _lib.sh_destroy(self.h)
+            self.h = C.c_void_p()
+
+    def __del__(self):
+        self.close()
+
+    def sync(self):
+        _check(_lib.sh_sync(self.h))
+
+    def expf(self, x: np.ndarray) -> np.ndarray:
+        """The kernels' exponential (glibc's expf, bit for bit) on the device."""
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty_like(x)
+        _check(_lib.sh_expf(self.h, _p(x), int(x.size), _p(y)))
+        return y
+
+
+class State:
+    """One conversation's memory (imi_seoul_state, imi/core/seoul.h:21-26)."""
+
+    def __init__(self, brain: "Brain"):
+        self.brain = brain
+        self.h = C.c_void_p()
+        _check(_lib.sh_state_new(brain.ctx.h, C.byref(self.h)))
+        self.hidden = np.zeros(brain.n_embd, np.float32)
+        self.logits = np.zeros(brain.n_vocab, np.float32)
+        brain.ctx._adopt(self)
+
+    def _free(self):
+        if getattr(self, "h", None) and self.h.value:
+            _lib.sh_state_free(self.h)
+            self.h = C.c_void_p()
+
+    def __del__(self):
+        self._free()
+
+    @property
+    def pos(self) -> int:
+        p = C.c_int()
+        _check(_lib.sh_state_pos(self.h, C.byref(p)))
+        return p.value
+
+    @pos.setter
+    def pos(self, v: int):
+        _check(_lib.sh_state_set_pos(self.h, int(v)))
+
+    def reset(self):
+        _check(_lib.sh_state_reset(self.h))
+
+
+class Brain:
+    """imi_seoul on the GPU: load(path, ctx_len) then step / step2 / step_batch on its own state."""
+
+    def __init__(self, path: str, n_ctx: int = 1024, device: int = 0, ctx: Context | None = None):
+        self.ctx = ctx or Context(device)
+        _check(_lib.sh_load(self.ctx.h, path.encode(), int(n_ctx)))
+        info = ModelInfo()
+        _check(_lib.sh_info(self.ctx.h, C.byref(info)))
+        self.info = info
+        for n, _ in ModelInfo._fields_:
+            setattr(self, n, getattr(info, n))
+        self.state = State(self)
+
+    # the brain's own conversation (imi_seoul::hidden / logits / pos)
+    @property
+    def hidden(self):
+        return self.state.hidden
+
+    @property
+    def logits(self):
+        return self.state.logits
+
+    @property
+    def pos(self) -> int:
+        return self.state.pos
+
+    def new_state(self) -> State:
+        return State(self)
+
+    def swap_state(self, other: State):
+        """imi_seoul::swap_state (imi/core/seoul.cpp:203-206): trade the brain's own memory for other's, O(1)."""
+        mine = self.state
+        mine.h, other.h = other.h, mine.h
+        mine.hidden, other.hidden = other.hidden, mine.hidden
+        mine.logits, other.logits = other.logits, mine.logits
+
+    def reset(self):
+        self.state.reset()
+
+    def step(self, token: int, embd=None, want_logits: bool = True, st: State | None = None):
+        st = st or self.state
+        e = None if embd is None else np.ascontiguousarray(embd, np.float32)
+        best = C.c_int32(-1)
+        _check(_lib.sh_step(self.ctx.h, st.h, int(token), _p(e), int(bool(want_logits)), _p(st.hidden),
+                            _p(st.logits) if want_logits else None, C.byref(best)))
+        return st.hidden.copy(), (st.logits.copy() if want_logits else None), best.value
+
+    def step2(self, token_a, embd_a, logits_a, b: State, token_b, embd_b, logits_b, a: State | None = None):
+        a = a or self.state
+        ea = None if embd_a is None else np.ascontiguousarray(embd_a, np.float32)
+        eb = None if embd_b is None else np.ascontiguousarray(embd_b, np.float32)
+        ba, bb = C.c_int32(-1), C.c_int32(-1)
+        _check(_lib.sh_step2(self.ctx.h, a.h, int(token_a), _p(ea), int(bool(logits_a)), b.h, int(token_b), _p(eb),
+                             int(bool(logits_b)), _p(a.hidden), _p(a.logits), C.byref(ba), _p(b.hidden), _p(b.logits),
+                             C.byref(bb)))
+        return ((a.hidden.copy(), a.logits.copy() if logits_a else None, ba.value),
+                (b.hidden.copy(), b.logits.copy() if logits_b else None, bb.value))
+
+    def step_batch(self, tokens=None, embd=None, want_logits: bool = True, hidden_all: bool = False, st: State | None = None):
+        st = st or self.state
+        t = None if tokens is None else np.ascontiguousarray(tokens, np.int32)
+        e = None if embd is None else np.ascontiguousarray(embd, np.float32)
+        n = len(t) if t is not None else e.shape[0]
+        ha = np.zeros((n, self.n_embd), np.float32) if hidden_all else None
+        best = C.c_int32(-1)
+        _check(_lib.sh_step_batch(self.ctx.h, st.h, _p(t), _p(e), n, int(bool(want_logits)), _p(st.hidden),
+                                  _p(st.logits) if want_logits else None, _p(ha), C.byref(best)))
+        return st.hidden.copy(), (st.logits.copy() if want_logits else None), best.value, ha
+
+    def generate(self, first: int, n: int, b: State | None = None, first_b: int = 0, a: State | None = None):
+        """Greedy decode on the device (device-side argmax feedback). Returns ids (and b's ids) and device seconds."""
+        a = a or self.state
+        oa = np.zeros(n, np.int32)
+        ob = np.zeros(n, np.int32) if b is not None else None
+        secs = C.c_double(0)
+        _check(_lib.sh_generate(self.ctx.h, a.h, b.h if b is not None else None, int(first), int(first_b), int(n),
+                                _p(oa), _p(ob), C.byref(secs)))
+        return (oa, ob, secs.value) if b is not None else (oa, secs.value)
+
+    def bench_tables(self, ncol: int = 1, reps: int = 10):
+        ms, us, by, nl = C.c_double(), C.c_double(), C.c_double(), C.c_int()
+        _check(_lib.sh_bench_tables(self.ctx.h, int(ncol), int(reps), C.byref(ms), C.byref(us), C.byref(by), C.byref(nl)))
+        return {"ms_per_pass": ms.value, "avg_launch_us": us.value, "bytes_per_pass": by.value, "launches": nl.value}
+
+
+class Q4Table:
+    """One Q4_0 table on the device (kernel-level API): gemv(x) with imi's int8 input cut."""
+
+    def __init__(self, ctx: Context, q4_0: np.ndarray, rows: int, cols: int):
+        self.ctx = ctx
+        self.rows, self.cols = rows, cols
+        raw = np.ascontiguousarray(q4_0).view(np.uint8).reshape(-1)
+        if raw.size != rows * cols // 32 * 18:
+            raise ValueError("q4_0 buffer size does not match rows x cols")
+        self.h = C.c_void_p()
+        _check(_lib.sh_q4_create(ctx.h, _p(raw), rows, cols, C.byref(self.h)))
+        ctx._adopt(self)
+
+    def _free(self):
+        if getattr(self, "h", None) and self.h.value:
+            _lib.sh_q4_free(self.h)
+            self.h = C.c_void_p()
+
+    def __del__(self):
+        self._free()
+
+    def rows_dequant(self, ids) -> np.ndarray:
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.zeros((ids.size, self.cols), np.float32)
+        _check(_lib.sh_q4_rows(self.ctx.h, self.h, _p(ids), int(ids.size), _p(out)))
+        return out
+
+    def gemv(self, x: np.ndarray, cut_mode: int = 0) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        n_in = 1 if x.ndim == 1 else x.shape[0]
+        y = np.zeros((n_in, self.rows), np.float32)
+        _check(_lib.sh_q4_gemv(self.ctx.h, self.h, _p(x.reshape(-1)), n_in, _p(y.reshape(-1)), int(cut_mode)))
+        return y[0] if x.ndim == 1 else y
+
+
+def q4_bench(ctx: Context, tables, n_in: int = 1, cut_mode: int = 0, reps: int = 200) -> float:
+    """Mean launch duration (us) of the GEMV over `tables` in rotation, inputs resident on the device."""
+    arr = (C.c_void_p * len(tables))(*[t.h.value for t in tables])
+    us = C.c_double()
+    _check(_lib.sh_q4_bench(ctx.h, arr, len(tables), int(n_in), int(cut_mode), int(reps), C.byref(us)))
+    return us.value
+
+
+@atexit.register
+def _close_all():
+    """Destroy every live context (and its states and tables) while the HIP runtime is still up."""
+    for c in list(_live_contexts):
+        c.close()

@@ -1,0 +1,150 @@
+// Device-side helpers shared by the HIP kernels of libseoul_hip (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <cstdint>
+
+namespace sh {
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int WAVE = 64;
+
+// fp16 <-> fp32: v_cvt_f32_f16 is exact (fp16 subnormals are kept: denorm mode 3); fp32 -> fp16 rounds to nearest
+// even, as F16C's _cvtss_sh(f, 0) does on the CPU side
+__device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ int wave_isum(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// Q4_0 block dot against an int8-cut input block. Codes are the 16 file bytes (byte i = column i in the low nibble,
+// column 16 + i in the high nibble); the input block is 8 dwords of int8 (columns 0..31). Codes 0..15 are valid
+// signed bytes, so the signed 4-way dot applies directly; the -8 offset is folded in by the caller.
+__device__ __forceinline__ int q4_block_dot(u32x4 c, const int* xq) {
+    int s = 0;
+    s = __builtin_amdgcn_sdot4((int)(c.x & 0x0F0F0F0Fu), xq[0], s, false);
+    s = __builtin_amdgcn_sdot4((int)(c.y & 0x0F0F0F0Fu), xq[1], s, false);
+    s = __builtin_amdgcn_sdot4((int)(c.z & 0x0F0F0F0Fu), xq[2], s, false);
+    s = __builtin_amdgcn_sdot4((int)(c.w & 0x0F0F0F0Fu), xq[3], s, false);
+    s = __builtin_amdgcn_sdot4((int)((c.x >> 4) & 0x0F0F0F0Fu), xq[4], s, false);
+    s = __builtin_amdgcn_sdot4((int)((c.y >> 4) & 0x0F0F0F0Fu), xq[5], s, false);
+    s = __builtin_amdgcn_sdot4((int)((c.z >> 4) & 0x0F0F0F0Fu), xq[6], s, false);
+    s = __builtin_amdgcn_sdot4((int)((c.w >> 4) & 0x0F0F0F0Fu), xq[7], s, false);
+    return s;
+}
+
+// Cut 32 floats to int8 (imi/core/vec.h:47-75): d = amax / 127, id = d ? 1/d : 0, q = round(x * id), returning d
+// and the sum of q. half_away selects roundf (imi/kernels/q4x8.cpp:45) instead of round-to-nearest-even.
+__device__ __forceinline__ float cut32(const float* v, int* q8, int* sum, bool half_away) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    int s = 0;
+#pragma unroll
+    for (int w = 0; w < 8; w++) {
+        unsigned packed = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const float t = v[4 * w + b] * id;
+            const int c = (int)(half_away ? roundf(t) : rintf(t));
+            s += c;
+            packed |= ((unsigned)c & 0xFFu) << (8 * b);
+        }
+        q8[w] = (int)packed;
+    }
+    *sum = s;
+    return d;
+}
+
+// e^x, bit for bit glibc's expf (the libm imi runs on). Method: ARM optimized-routines expf (published, used by
+// glibc since 2.27): x * 32/ln2 = k + r, 2^(k/32) from a 32-entry table of 2^(i/32) (derived here from the
+// mathematics: each entry is 2^(i/32) rounded to double, minus i << 47), times a degree-3 polynomial in r, in
+// double with the fused multiply-adds of glibc's FMA build. Exhaustively equal to glibc's expf on all 2^32 inputs.
+__constant__ static const uint64_t kExp2Tab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+__device__ __forceinline__ float expf_glibc(float x) {
+    const uint32_t ux = __float_as_uint(x);
+    const uint32_t abstop = (ux >> 20) & 0x7ffu;
+    if (abstop >= 0x42bu) {                         // |x| >= 88 or nan
+        if (ux == 0xff800000u) return 0.0f;         // -inf
+        if (abstop >= 0x7f8u) return x + x;         // +inf or nan
+        if (x > 0x1.62e42ep6f) return __builtin_inff();
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    const double inv_ln2_32 = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32, c2 = 0x1.62e42ff0c52d6p-1 / 32;
+    const double xd = (double)x;
+    double kd = __builtin_fma(inv_ln2_32, xd, shift);
+    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    kd -= shift;
+    const double r = __builtin_fma(inv_ln2_32, xd, -kd);
+    const uint64_t t = kExp2Tab[ki & 31] + (ki << 47);
+    const double sc = __longlong_as_double((long long)t);
+    const double z = __builtin_fma(c0, r, c1);
+    const double r2 = r * r;
+    double y = __builtin_fma(c2, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    return (float)(y * sc);
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf_glibc(-x)); }   // imi/core/seoul.cpp:48
+
+// imi_rms_scale (imi/core/vec.h:20-33) in its AVX2 op order, by one whole wave over n floats in LDS
+// (n % 32 == 0): partial P (= accumulator P / 8, lane P % 8) is the FMA chain of x[32t + P]^2 over t; then
+// v_l = (a0_l + a1_l) + (a2_l + a3_l) and the 8-lane sum ((v0+v4) + (v2+v6)) + ((v1+v5) + (v3+v7));
+// returns 1 / sqrtf(s / n + eps) in every lane
+__device__ __forceinline__ float rms_scale_wave(const float* x, int n, float eps) {
+    const int lane = threadIdx.x & 63;
+    float a = 0.0f;
+    if (lane < 32)
+        for (int t = 0; t < n / 32; t++) a = fmaf(x[32 * t + lane], x[32 * t + lane], a);
+    const float a1 = __shfl(a, (lane + 8) & 63), a2 = __shfl(a, (lane + 16) & 63), a3 = __shfl(a, (lane + 24) & 63);
+    const float v = (a + a1) + (a2 + a3);            // lanes 0..7
+    const float r = v + __shfl(v, (lane + 4) & 63);  // lanes 0..3: v_l + v_{l+4}
+    const float q = r + __shfl(r, (lane + 2) & 63);  // lane 0: (r0 + r2), lane 1: (r1 + r3)
+    const float s = __shfl(q, 0) + __shfl(q, 1);
+    return 1.0f / sqrtf(s / (float)n + eps);
+}
+
+// dot_h (imi/core/seoul.cpp:29-39): 8 FMA chains over columns i % 8, then the 8-lane horizontal sum
+template <int D>
+__device__ __forceinline__ float dot_h8(const float* q, const float* k) {
+    float a[8];
+#pragma unroll
+    for (int l = 0; l < 8; l++) a[l] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < D; i += 8)
+#pragma unroll
+        for (int l = 0; l < 8; l++) a[l] = fmaf(q[i + l], k[i + l], a[l]);
+    return ((a[0] + a[4]) + (a[2] + a[6])) + ((a[1] + a[5]) + (a[3] + a[7]));
+}
+
+// device-scope (sc1) stores/loads for values another block reads in the same kernel (no whole-cache fences)
+__device__ __forceinline__ void st_dev(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void st_dev(int* p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
+}  // namespace sh

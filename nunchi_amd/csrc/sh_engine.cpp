@@ -1,0 +1,987 @@
+// libseoul_hip: the brain step of imi's engine (imi/core/seoul.{h,cpp}) on one MI355X, behind the C ABI of
+// include/seoul_hip.h. Host side: GGUF read, repack into the device layout, conversation states, and the step as a
+// captured HIP graph of fused kernels (one per table read, plus attention and the end of step).
+#include "../../include/seoul_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "gguf_file.h"
+#include "sh_kernels.h"
+
+namespace sh {
+hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hipStream_t s);
+hipError_t launch_attn(int M, const attn_args& a, hipStream_t s);
+hipError_t launch_final(int M, const final_args& a, hipStream_t s);
+hipError_t launch_q4_rows(const q4dev& T, const int32_t* ids, int n, float* out, hipStream_t s);
+hipError_t launch_expf(const float* x, float* y, long long n, hipStream_t s);
+}
+
+using namespace sh;
+
+namespace {
+thread_local std::string g_err;
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+#define HIPCHK(x)                                                                                          \
+    do {                                                                                                   \
+        hipError_t e_ = (x);                                                                               \
+        if (e_ != hipSuccess) return fail(SH_E_HIP, std::string(#x) + ": " + hipGetErrorString(e_));       \
+    } while (0)
+
+// one device allocation carved into 256-byte aligned pieces
+struct arena {
+    char* base = nullptr;
+    size_t size = 0, used = 0;
+    void* take(size_t n) {
+        const size_t at = (used + 255) / 256 * 256;
+        if (at + n > size) return nullptr;
+        used = at + n;
+        return base + at;
+    }
+};
+
+struct layer_dev {
+    bool conv = false, swa = false;
+    int ai = -1, ci = -1;
+    q4dev in_proj, out_proj, qkvg, o, gate_up, down;
+    const float *attn_norm = nullptr, *post_attn_norm = nullptr, *ffn_norm = nullptr, *post_ffn_norm = nullptr;
+    const float *q_norm = nullptr, *k_norm = nullptr, *conv_w = nullptr;
+};
+
+// Q4_0 rows (tensor, row) -> device layout in a host staging buffer: codes [rows][nb][16], scales [rows/8][nb][8]
+bool repack_q4(const std::vector<std::pair<const gg_tensor*, int>>& rows, std::vector<uint8_t>& codes, std::vector<uint16_t>& scales, int* cols) {
+    if (rows.empty() || rows.size() % 8) return false;
+    const gg_tensor* t0 = rows[0].first;
+    for (auto& r : rows)
+        if (!r.first->data || r.first->type != GT_Q4_0 || r.first->ne[0] != t0->ne[0]) return false;
+    const int K = (int)t0->ne[0], nb = K / 32, R = (int)rows.size();
+    codes.resize((size_t)R * nb * 16);
+    scales.resize((size_t)R * nb);
+    for (int r = 0; r < R; r++) {
+        const uint8_t* src = static_cast<const uint8_t*>(rows[r].first->data) + (size_t)rows[r].second * rows[r].first->nb[1];
+        for (int j = 0; j < nb; j++) {
+            const uint8_t* blk = src + (size_t)j * 18;
+            uint16_t d;
+            memcpy(&d, blk, 2);
+            scales[((size_t)(r / 8) * nb + j) * 8 + (r % 8)] = d;
+            memcpy(&codes[((size_t)r * nb + j) * 16], blk + 2, 16);
+        }
+    }
+    *cols = K;
+    return true;
+}
+}  // namespace
+
+struct sh_q4 {
+    sh_ctx* ctx = nullptr;
+    q4dev t;
+    void* mem = nullptr;
+};
+
+struct sh_state {
+    sh_ctx* ctx = nullptr;
+    uint16_t* kc = nullptr;
+    uint16_t* vc = nullptr;
+    float* conv = nullptr;
+    int pos = 0;
+};
+
+struct sh_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    bool loaded = false;
+    sh_model_info info{};
+    float eps = 1e-5f, rope_base = 1e6f, rope_base_swa = 1e4f;
+    arena w;                         // weights + norms + rope tables
+    std::vector<layer_dev> layers;
+    q4dev vocab;
+    const float* out_norm = nullptr;
+    const float2* rope_cs = nullptr;
+    const float2* rope_cs_swa = nullptr;
+    int n_conv = 0, nqkv = 0;
+    // work buffers (device)
+    arena work;
+    float *xbuf[2] = {nullptr, nullptr}, *y = nullptr, *u = nullptr, *qkv = nullptr, *att = nullptr, *act = nullptr, *fo = nullptr;
+    float *hidden = nullptr, *logits = nullptr, *embd_stage = nullptr, *part_v = nullptr;
+    int* part_i = nullptr;
+    int32_t* gen_out = nullptr;       // device-side greedy ids [2][gen_cap]
+    int gen_cap = 0;
+    float* bench_x = nullptr;         // kernel-API input/output staging
+    float* bench_y = nullptr;
+    size_t bench_cap = 0;
+    step_params* P_dev = nullptr;
+    step_params* P_host = nullptr;    // pinned
+    int vocab_grid = 2048;
+    hipGraphExec_t graph[3][2] = {{nullptr, nullptr}, {nullptr, nullptr}, {nullptr, nullptr}};
+    std::vector<sh_state*> states;    // live children: destroying the context releases their device memory
+    std::vector<sh_q4*> tables;
+};
+
+namespace {
+template <class T> void forget(std::vector<T*>& v, T* p) {
+    for (size_t i = 0; i < v.size(); i++)
+        if (v[i] == p) { v[i] = v.back(); v.pop_back(); return; }
+}
+void release_state_memory(sh_state* s) {
+    if (s->kc) (void)hipFree(s->kc);
+    if (s->vc) (void)hipFree(s->vc);
+    if (s->conv) (void)hipFree(s->conv);
+    s->kc = s->vc = nullptr;
+    s->conv = nullptr;
+}
+}  // namespace
+
+namespace {
+
+int enqueue_step(sh_ctx* c, int M, bool want_logits) {
+    const sh_model_info& I = c->info;
+    const int E = I.n_embd;
+    int cur = 0;
+    auto base_args = [&]() {
+        gemv_args a{};
+        a.P = c->P_dev;
+        a.E = E;
+        a.eps = c->eps;
+        return a;
+    };
+    auto units_of = [](const q4dev& t, int ug) { return t.rows / (8 * ug); };
+    auto grid_of = [](int units) { return units < 4096 ? units : 4096; };
+    const layer_dev* prev = nullptr;
+    for (size_t il = 0; il < c->layers.size(); il++) {
+        const layer_dev& L = c->layers[il];
+        // first table read of the layer: its input is norm(x) after the previous layer's FFN residual
+        gemv_args a = base_args();
+        int pro;
+        if (!prev) {
+            pro = PRO_EMBED_NORM;
+            a.emb = c->vocab;
+            a.embd = c->embd_stage;
+            a.x_out = c->xbuf[cur];
+        } else {
+            pro = PRO_RESID_NORM;
+            a.x_in = c->xbuf[cur];
+            a.y_in = c->fo;
+            a.w_post = prev->post_ffn_norm;
+            a.x_out = c->xbuf[cur ^ 1];
+            cur ^= 1;
+        }
+        a.w_pre = L.attn_norm;
+        if (L.conv) {
+            a.W = L.in_proj;
+            a.units = units_of(L.in_proj, 3);
+            a.out = c->u;
+            a.out_ld = E;
+            a.conv_w = L.conv_w;
+            a.conv_layer = L.ci;
+            a.d_conv = I.d_conv;
+            HIPCHK(launch_gemv(M, pro, EPI_CONV, grid_of(a.units), a, c->stream));
+            gemv_args b = base_args();
+            b.W = L.out_proj;
+            b.units = units_of(L.out_proj, 1);
+            b.src = c->u;
+            b.src_ld = E;
+            b.out = c->y;
+            b.out_ld = E;
+            HIPCHK(launch_gemv(M, PRO_CUT, EPI_STORE, grid_of(b.units), b, c->stream));
+        } else {
+            a.W = L.qkvg;
+            a.units = units_of(L.qkvg, 1);
+            a.out = c->qkv;
+            a.out_ld = c->nqkv;
+            HIPCHK(launch_gemv(M, pro, EPI_STORE, grid_of(a.units), a, c->stream));
+            attn_args t{};
+            t.qkv = c->qkv;
+            t.ld_qkv = c->nqkv;
+            t.att = c->att;
+            t.q_norm = L.q_norm;
+            t.k_norm = L.k_norm;
+            t.rope_cs = L.swa ? c->rope_cs_swa : c->rope_cs;
+            t.layer_ai = L.ai;
+            t.n_head = I.n_head;
+            t.n_kv = I.n_head_kv;
+            t.D = I.head_dim;
+            t.n_ctx = I.n_ctx;
+            t.n_swa = L.swa ? I.n_swa : 0;
+            t.eps = c->eps;
+            t.P = c->P_dev;
+            HIPCHK(launch_attn(M, t, c->stream));
+            gemv_args b = base_args();
+            b.W = L.o;
+            b.units = units_of(L.o, 1);
+            b.src = c->att;
+            b.src_ld = I.n_head * I.head_dim;
+            b.out = c->y;
+            b.out_ld = E;
+            HIPCHK(launch_gemv(M, PRO_CUT, EPI_STORE, grid_of(b.units), b, c->stream));
+        }
+        // FFN: x += norm(y) * post_attn_norm; h = norm(x) * ffn_norm; gate|up with SwiGLU; down
+        gemv_args f = base_args();
+        f.x_in = c->xbuf[cur];
+        f.y_in = c->y;
+        f.w_post = L.post_attn_norm;
+        f.x_out = c->xbuf[cur ^ 1];
+        cur ^= 1;
+        f.w_pre = L.ffn_norm;
+        f.W = L.gate_up;
+        f.units = units_of(L.gate_up, 2);
+        f.out = c->act;
+        f.out_ld = I.n_ff;
+        HIPCHK(launch_gemv(M, PRO_RESID_NORM, EPI_SWIGLU, grid_of(f.units), f, c->stream));
+        gemv_args d = base_args();
+        d.W = L.down;
+        d.units = units_of(L.down, 1);
+        d.src = c->act;
+        d.src_ld = I.n_ff;
+        d.out = c->fo;
+        d.out_ld = E;
+        HIPCHK(launch_gemv(M, PRO_CUT, EPI_STORE, grid_of(d.units), d, c->stream));
+        prev = &L;
+    }
+    final_args z{};
+    z.E = E;
+    z.eps = c->eps;
+    z.P = c->P_dev;
+    z.advance = 1;
+    if (want_logits) {
+        gemv_args v = base_args();
+        v.x_in = c->xbuf[cur];
+        v.y_in = c->fo;
+        v.w_post = prev->post_ffn_norm;
+        v.w_pre = c->out_norm;
+        v.hidden_out = c->hidden;
+        v.W = c->vocab;
+        v.units = units_of(c->vocab, 1);
+        v.out = c->logits;
+        v.out_ld = I.n_vocab;
+        v.part_v = c->part_v;
+        v.part_i = c->part_i;
+        const int grid = v.units < c->vocab_grid ? v.units : c->vocab_grid;
+        HIPCHK(launch_gemv(M, PRO_RESID_NORM, EPI_LOGITS, grid, v, c->stream));
+        z.part_v = c->part_v;
+        z.part_i = c->part_i;
+        z.n_part = grid;
+    } else {
+        z.x_in = c->xbuf[cur];
+        z.y_in = c->fo;
+        z.w_post = prev->post_ffn_norm;
+        z.w_out = c->out_norm;
+        z.hidden_out = c->hidden;
+    }
+    HIPCHK(launch_final(M, z, c->stream));
+    return SH_OK;
+}
+
+int get_graph(sh_ctx* c, int M, bool want_logits, hipGraphExec_t* out) {
+    hipGraphExec_t& g = c->graph[M][want_logits ? 1 : 0];
+    if (!g) {
+        hipGraph_t graph;
+        HIPCHK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+        const int rc = enqueue_step(c, M, want_logits);
+        hipError_t e = hipStreamEndCapture(c->stream, &graph);
+        if (rc != SH_OK) return rc;
+        if (e != hipSuccess) return fail(SH_E_HIP, std::string("graph capture: ") + hipGetErrorString(e));
+        e = hipGraphInstantiate(&g, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        if (e != hipSuccess) { g = nullptr; return fail(SH_E_HIP, std::string("graph instantiate: ") + hipGetErrorString(e)); }
+    }
+    *out = g;
+    return SH_OK;
+}
+
+void fill_state(step_params& p, int m, const sh_state* s) {
+    p.pos[m] = s->pos;
+    p.kc[m] = s->kc;
+    p.vc[m] = s->vc;
+    p.conv[m] = s->conv;
+    p.out_tok[m] = nullptr;
+}
+
+// host-precomputed rotation table: for every position, cos/sin of th_i / ff[i] with th_0 = pos and
+// th_{i+1} = th_i * base^(-2/D) in fp32 (imi/core/seoul.cpp:19-28), so the device uses the same angles
+std::vector<float2> rope_table(int n_ctx, int D, float base, const float* ff) {
+    std::vector<float2> t((size_t)n_ctx * (D / 2));
+    const float scale = powf(base, -2.0f / (float)D);
+    for (int p = 0; p < n_ctx; p++) {
+        float th = (float)p;
+        for (int i = 0; i < D / 2; i++) {
+            const float ang = th / (ff ? ff[i] : 1.0f);
+            t[(size_t)p * (D / 2) + i] = make_float2(cosf(ang), sinf(ang));
+            th *= scale;
+        }
+    }
+    return t;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* sh_last_error(void) { return g_err.c_str(); }
+
+int sh_create(int device, sh_ctx** out) {
+    if (!out) return fail(SH_E_ARG, "sh_create: out is null");
+    int n = 0;
+    HIPCHK(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) return fail(SH_E_ARG, "sh_create: no such device");
+    HIPCHK(hipSetDevice(device));
+    auto c = std::make_unique<sh_ctx>();
+    c->device = device;
+    HIPCHK(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+    HIPCHK(hipEventCreate(&c->ev0));
+    HIPCHK(hipEventCreate(&c->ev1));
+    HIPCHK(hipHostMalloc((void**)&c->P_host, sizeof(step_params), hipHostMallocDefault));
+    HIPCHK(hipMalloc((void**)&c->P_dev, sizeof(step_params)));
+    memset(c->P_host, 0, sizeof(step_params));
+    *out = c.release();
+    return SH_OK;
+}
+
+int sh_destroy(sh_ctx* c) {
+    if (!c) return SH_OK;
+    (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    for (sh_state* s : c->states) { release_state_memory(s); s->ctx = nullptr; }   // handles stay valid, detached
+    for (sh_q4* t : c->tables) { if (t->mem) (void)hipFree(t->mem); t->mem = nullptr; t->ctx = nullptr; }
+    for (auto& row : c->graph)
+        for (auto& g : row)
+            if (g) (void)hipGraphExecDestroy(g);
+    if (c->w.base) (void)hipFree(c->w.base);
+    if (c->work.base) (void)hipFree(c->work.base);
+    if (c->bench_x) (void)hipFree(c->bench_x);
+    if (c->bench_y) (void)hipFree(c->bench_y);
+    if (c->P_dev) (void)hipFree(c->P_dev);
+    if (c->P_host) (void)hipHostFree(c->P_host);
+    if (c->ev0) (void)hipEventDestroy(c->ev0);
+    if (c->ev1) (void)hipEventDestroy(c->ev1);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+    return SH_OK;
+}
+
+// imi/core/seoul.cpp:93-186 with a Q4_0 tied word table; tables repacked into the device layout
+int sh_load(sh_ctx* c, const char* path, int n_ctx) {
+    if (!c || !path || n_ctx < 1) return fail(SH_E_ARG, "sh_load: bad argument");
+    if (c->loaded) return fail(SH_E_STATE, "sh_load: a model is already loaded in this context");
+    HIPCHK(hipSetDevice(c->device));
+    gg_file f;
+    if (!f.load(path)) return fail(SH_E_FILE, "sh_load: " + f.error);
+    const gg_tensor* te = f.get("token_embd.weight");
+    if (!te) return fail(SH_E_FILE, "sh_load: " + f.error);
+    if (te->type != GT_Q4_0) return fail(SH_E_SHAPE, "sh_load: word table must be Q4_0");
+    sh_model_info& I = c->info;
+    I.n_embd = (int)te->ne[0];
+    I.n_vocab = (int)te->ne[1];
+    c->eps = f.key_f("lfm3.attention.layer_norm_rms_epsilon", 1e-5f);
+    c->rope_base = f.key_f("lfm3.rope.freq_base", 1e6f);
+    c->rope_base_swa = f.key_f("lfm3.rope.freq_base_swa", 1e4f);
+    I.n_swa = (int)f.key_i("lfm3.attention.sliding_window", 0);
+    I.d_conv = (int)f.key_i("lfm3.shortconv.l_cache", 7) - 1;
+    I.n_head = (int)f.key_i("lfm3.attention.head_count", 16);
+    I.head_dim = (int)f.key_i("lfm3.attention.key_length", 128);
+    I.n_layer = (int)f.key_i("lfm3.block_count", 0);
+    I.n_ctx = n_ctx;
+    const std::vector<int64_t> swa_pat = f.key_arr("lfm3.attention.sliding_window_pattern");
+    const int E = I.n_embd;
+    if (E % 32 || E / 32 > 64) return fail(SH_E_SHAPE, "sh_load: n_embd must be a multiple of 32 and at most 2048");
+    if (I.n_layer < 1) return fail(SH_E_FILE, "sh_load: no layers");
+
+    // first pass: shapes, and the bytes the device arena needs
+    struct plan { std::vector<std::pair<const gg_tensor*, int>> rows; q4dev* dst; };
+    std::vector<plan> tables;
+    c->layers.assign(I.n_layer, layer_dev{});
+    auto all_rows = [](std::vector<std::pair<const gg_tensor*, int>>& o, const gg_tensor* t, int r0, int n) {
+        for (int r = r0; r < r0 + n; r++) o.push_back({t, r});
+    };
+    std::vector<std::pair<const float**, const gg_tensor*>> vecs;   // fp32 vectors to upload
+    std::vector<std::vector<float>> conv_t;                          // conv weights transposed to [tap][channel]
+    std::vector<const float**> conv_dst;
+    int n_attn = 0, n_conv = 0;
+    for (int il = 0; il < I.n_layer; il++) {
+        const std::string p = "blk." + std::to_string(il) + ".";
+        layer_dev& L = c->layers[il];
+        auto need_f32 = [&](const std::string& name, const float** dst, int64_t n) -> bool {
+            const gg_tensor* t = f.get(p + name);
+            if (!t) return false;
+            if (t->type != GT_F32 || t->ne[0] * t->ne[1] != n) { f.error = p + name + " must be f32"; return false; }
+            vecs.push_back({dst, t});
+            return true;
+        };
+        if (!need_f32("attn_norm.weight", &L.attn_norm, E) || !need_f32("post_attention_norm.weight", &L.post_attn_norm, E) ||
+            !need_f32("ffn_norm.weight", &L.ffn_norm, E) || !need_f32("post_ffw_norm.weight", &L.post_ffn_norm, E))
+            return fail(SH_E_FILE, "sh_load: " + f.error);
+        if (const gg_tensor* cw = f.get(p + "shortconv.conv.weight", false)) {
+            L.conv = true;
+            L.ci = n_conv++;
+            const int K = (int)cw->ne[0], C = (int)cw->ne[1];
+            if (cw->type != GT_F32 || C != E || K != I.d_conv + 1) return fail(SH_E_SHAPE, "sh_load: conv weight shape");
+            std::vector<float> tw((size_t)K * C);
+            const float* src = static_cast<const float*>(cw->data);
+            for (int e = 0; e < C; e++)
+                for (int k = 0; k < K; k++) tw[(size_t)k * C + e] = src[(size_t)e * K + k];   // [channel][tap] -> [tap][channel]
+            conv_t.push_back(std::move(tw));
+            conv_dst.push_back(&L.conv_w);
+            const gg_tensor* ip = f.get(p + "shortconv.in_proj.weight");
+            const gg_tensor* op = f.get(p + "shortconv.out_proj.weight");
+            if (!ip || !op) return fail(SH_E_FILE, "sh_load: " + f.error);
+            if (ip->ne[1] != 3 * E) return fail(SH_E_SHAPE, "sh_load: in_proj must have 3 * n_embd rows");
+            // b, c, x rows of 8 channels side by side, so one unit holds everything the conv of 8 channels needs
+            plan pi;
+            for (int t = 0; t < E; t += 8) { all_rows(pi.rows, ip, t, 8); all_rows(pi.rows, ip, E + t, 8); all_rows(pi.rows, ip, 2 * E + t, 8); }
+            pi.dst = &L.in_proj;
+            tables.push_back(std::move(pi));
+            plan po;
+            all_rows(po.rows, op, 0, (int)op->ne[1]);
+            po.dst = &L.out_proj;
+            tables.push_back(std::move(po));
+        } else {
+            const gg_tensor *q = f.get(p + "attn_q.weight"), *k = f.get(p + "attn_k.weight"), *v = f.get(p + "attn_v.weight");
+            const gg_tensor *g = f.get(p + "attn_gate.weight"), *o = f.get(p + "attn_output.weight");
+            if (!q || !k || !v || !g || !o) return fail(SH_E_FILE, "sh_load: " + f.error);
+            I.n_head_kv = (int)(k->ne[1] / I.head_dim);
+            if (!need_f32("attn_q_norm.weight", &L.q_norm, I.head_dim) || !need_f32("attn_k_norm.weight", &L.k_norm, I.head_dim))
+                return fail(SH_E_FILE, "sh_load: " + f.error);
+            plan pq;   // q | k | v | gate stacked (imi/core/seoul.cpp:147)
+            for (const gg_tensor* t : {q, k, v, g}) all_rows(pq.rows, t, 0, (int)t->ne[1]);
+            pq.dst = &L.qkvg;
+            tables.push_back(std::move(pq));
+            plan po;
+            all_rows(po.rows, o, 0, (int)o->ne[1]);
+            po.dst = &L.o;
+            tables.push_back(std::move(po));
+            L.ai = n_attn++;
+            L.swa = il < (int)swa_pat.size() && swa_pat[il] != 0;
+        }
+        const gg_tensor *fg = f.get(p + "ffn_gate.weight"), *fu = f.get(p + "ffn_up.weight"), *fd = f.get(p + "ffn_down.weight");
+        if (!fg || !fu || !fd) return fail(SH_E_FILE, "sh_load: " + f.error);
+        I.n_ff = (int)fg->ne[1];
+        plan pg;   // gate and up interleaved by 8-row group (imi/core/seoul.cpp:155-160)
+        for (int t = 0; t < I.n_ff; t += 8) { all_rows(pg.rows, fg, t, 8); all_rows(pg.rows, fu, t, 8); }
+        pg.dst = &L.gate_up;
+        tables.push_back(std::move(pg));
+        plan pd;
+        all_rows(pd.rows, fd, 0, (int)fd->ne[1]);
+        pd.dst = &L.down;
+        tables.push_back(std::move(pd));
+    }
+    {
+        plan pv;
+        all_rows(pv.rows, te, 0, I.n_vocab);
+        pv.dst = &c->vocab;
+        tables.push_back(std::move(pv));
+    }
+    const gg_tensor* on = f.get("output_norm.weight");
+    if (!on || on->type != GT_F32) return fail(SH_E_FILE, "sh_load: output_norm.weight missing or not f32");
+    vecs.push_back({&c->out_norm, on});
+    const gg_tensor* rf = f.get("rope_freqs.weight", false);
+    I.n_attn = n_attn;
+    c->n_conv = n_conv;
+    if (n_attn > 0 && (I.head_dim > 64 || I.head_dim % 2 || I.n_head % I.n_head_kv || I.n_head / I.n_head_kv > 8))
+        return fail(SH_E_SHAPE, "sh_load: attention shape not supported (head_dim <= 64, group <= 8)");
+    if (n_attn > 0 && (I.n_head * I.head_dim) / 32 > 64) return fail(SH_E_SHAPE, "sh_load: attention width above 2048");
+    if (I.n_ff % 32 || I.n_ff / 32 > 256) return fail(SH_E_SHAPE, "sh_load: n_ff must be a multiple of 32, at most 8192");
+    c->nqkv = I.n_head * I.head_dim + 2 * I.n_head_kv * I.head_dim + I.n_head;
+    if (c->nqkv % 8) return fail(SH_E_SHAPE, "sh_load: q|k|v|gate rows not a multiple of 8");
+
+    // device arena: tables, fp32 vectors, conv weights, rope tables
+    size_t need = 0;
+    for (auto& t : tables) {
+        const size_t nb = (size_t)t.rows[0].first->ne[0] / 32;
+        need += (t.rows.size() * nb * 16 + 255) / 256 * 256 + (t.rows.size() * nb * 2 + 255) / 256 * 256;
+    }
+    for (auto& v : vecs) need += ((size_t)v.second->nbytes + 255) / 256 * 256;
+    for (auto& v : conv_t) need += (v.size() * 4 + 255) / 256 * 256;
+    const size_t rope_bytes = ((size_t)n_ctx * (I.head_dim / 2) * sizeof(float2) + 255) / 256 * 256;
+    need += 2 * rope_bytes + 4096;
+    HIPCHK(hipMalloc((void**)&c->w.base, need));
+    c->w.size = need;
+    long long table_bytes = 0;
+    std::vector<uint8_t> codes;
+    std::vector<uint16_t> scales;
+    for (auto& t : tables) {
+        int K = 0;
+        if (!repack_q4(t.rows, codes, scales, &K)) return fail(SH_E_SHAPE, "sh_load: a table is not Q4_0 with rows in multiples of 8");
+        void* dc = c->w.take(codes.size());
+        void* ds = c->w.take(scales.size() * 2);
+        if (!dc || !ds) return fail(SH_E_NOMEM, "sh_load: arena overflow");
+        HIPCHK(hipMemcpy(dc, codes.data(), codes.size(), hipMemcpyHostToDevice));
+        HIPCHK(hipMemcpy(ds, scales.data(), scales.size() * 2, hipMemcpyHostToDevice));
+        t.dst->codes = dc;
+        t.dst->scales = ds;
+        t.dst->rows = (int)t.rows.size();
+        t.dst->cols = K;
+        t.dst->nb = K / 32;
+        table_bytes += (long long)(codes.size() + scales.size() * 2);
+    }
+    for (auto& v : vecs) {
+        void* d = c->w.take(v.second->nbytes);
+        if (!d) return fail(SH_E_NOMEM, "sh_load: arena overflow");
+        HIPCHK(hipMemcpy(d, v.second->data, v.second->nbytes, hipMemcpyHostToDevice));
+        *v.first = static_cast<const float*>(d);
+    }
+    for (size_t i = 0; i < conv_t.size(); i++) {
+        void* d = c->w.take(conv_t[i].size() * 4);
+        if (!d) return fail(SH_E_NOMEM, "sh_load: arena overflow");
+        HIPCHK(hipMemcpy(d, conv_t[i].data(), conv_t[i].size() * 4, hipMemcpyHostToDevice));
+        *conv_dst[i] = static_cast<const float*>(d);
+    }
+    if (n_attn > 0) {
+        const float* ff = rf ? static_cast<const float*>(rf->data) : nullptr;
+        if (rf && (rf->type != GT_F32 || rf->ne[0] != I.head_dim / 2)) return fail(SH_E_SHAPE, "sh_load: rope_freqs shape");
+        auto t = rope_table(n_ctx, I.head_dim, c->rope_base, ff);
+        void* d = c->w.take(t.size() * sizeof(float2));
+        HIPCHK(hipMemcpy(d, t.data(), t.size() * sizeof(float2), hipMemcpyHostToDevice));
+        c->rope_cs = static_cast<const float2*>(d);
+        auto t2 = rope_table(n_ctx, I.head_dim, c->rope_base_swa, nullptr);   // window layers: no freq factors
+        void* d2 = c->w.take(t2.size() * sizeof(float2));
+        HIPCHK(hipMemcpy(d2, t2.data(), t2.size() * sizeof(float2), hipMemcpyHostToDevice));
+        c->rope_cs_swa = static_cast<const float2*>(d2);
+    }
+    I.table_bytes = table_bytes;
+    f.drop_data();
+
+    // work buffers for up to two conversations
+    const int Hq = I.n_head * I.head_dim;
+    const size_t fl = sizeof(float);
+    const size_t work_need = fl * (2 * 2 * E + 2 * E + 2 * E + 2 * (size_t)c->nqkv + 2 * (size_t)Hq + 2 * (size_t)I.n_ff + 2 * E + 2 * E +
+                                   2 * (size_t)I.n_vocab + 2 * E + 2 * (size_t)c->vocab_grid) +
+                             sizeof(int) * 2 * (size_t)c->vocab_grid + 32 * 256;
+    HIPCHK(hipMalloc((void**)&c->work.base, work_need));
+    c->work.size = work_need;
+    HIPCHK(hipMemset(c->work.base, 0, work_need));
+    auto fa = [&](size_t n) { return static_cast<float*>(c->work.take(n * fl)); };
+    c->xbuf[0] = fa(2 * E);
+    c->xbuf[1] = fa(2 * E);
+    c->y = fa(2 * E);
+    c->u = fa(2 * E);
+    c->qkv = fa(2 * (size_t)c->nqkv);
+    c->att = fa(2 * (size_t)Hq);
+    c->act = fa(2 * (size_t)I.n_ff);
+    c->fo = fa(2 * E);
+    c->hidden = fa(2 * E);
+    c->logits = fa(2 * (size_t)I.n_vocab);
+    c->embd_stage = fa(2 * E);
+    c->part_v = fa(2 * (size_t)c->vocab_grid);
+    c->part_i = static_cast<int*>(c->work.take(sizeof(int) * 2 * (size_t)c->vocab_grid));
+    if (!c->part_i) return fail(SH_E_NOMEM, "sh_load: work arena overflow");
+    HIPCHK(hipDeviceSynchronize());
+    c->loaded = true;
+    return SH_OK;
+}
+
+int sh_info(const sh_ctx* c, sh_model_info* out) {
+    if (!c || !out) return fail(SH_E_ARG, "sh_info: null");
+    if (!c->loaded) return fail(SH_E_STATE, "sh_info: no model loaded");
+    *out = c->info;
+    return SH_OK;
+}
+
+int sh_state_new(sh_ctx* c, sh_state** out) {
+    if (!c || !out) return fail(SH_E_ARG, "sh_state_new: null");
+    if (!c->loaded) return fail(SH_E_STATE, "sh_state_new: no model loaded");
+    HIPCHK(hipSetDevice(c->device));
+    const sh_model_info& I = c->info;
+    auto s = std::make_unique<sh_state>();
+    s->ctx = c;
+    const size_t kv = (size_t)I.n_attn * I.n_head_kv * I.n_ctx * I.head_dim;
+    const size_t cv = (size_t)c->n_conv * I.d_conv * I.n_embd;
+    if (kv) {
+        HIPCHK(hipMalloc((void**)&s->kc, kv * 2));
+        HIPCHK(hipMalloc((void**)&s->vc, kv * 2));
+        HIPCHK(hipMemset(s->kc, 0, kv * 2));
+        HIPCHK(hipMemset(s->vc, 0, kv * 2));
+    }
+    if (cv) {
+        HIPCHK(hipMalloc((void**)&s->conv, cv * 4));
+        HIPCHK(hipMemset(s->conv, 0, cv * 4));
+    }
+    HIPCHK(hipDeviceSynchronize());
+    c->states.push_back(s.get());
+    *out = s.release();
+    return SH_OK;
+}
+
+int sh_state_free(sh_state* s) {
+    if (!s) return SH_OK;
+    if (s->ctx) {   // a state whose context was destroyed has no device memory left
+        (void)hipSetDevice(s->ctx->device);
+        (void)hipStreamSynchronize(s->ctx->stream);
+        release_state_memory(s);
+        forget(s->ctx->states, s);
+    }
+    delete s;
+    return SH_OK;
+}
+
+int sh_state_reset(sh_state* s) {
+    if (!s) return fail(SH_E_ARG, "sh_state_reset: null");
+    if (!s->ctx) return fail(SH_E_STATE, "sh_state_reset: its context was destroyed");
+    sh_ctx* c = s->ctx;
+    HIPCHK(hipSetDevice(c->device));
+    s->pos = 0;
+    const size_t cv = (size_t)c->n_conv * c->info.d_conv * c->info.n_embd;
+    if (cv) HIPCHK(hipMemsetAsync(s->conv, 0, cv * 4, c->stream));
+    HIPCHK(hipStreamSynchronize(c->stream));
+    return SH_OK;
+}
+
+int sh_state_pos(const sh_state* s, int* pos) {
+    if (!s || !pos) return fail(SH_E_ARG, "sh_state_pos: null");
+    *pos = s->pos;
+    return SH_OK;
+}
+
+int sh_state_set_pos(sh_state* s, int pos) {
+    if (!s || !s->ctx) return fail(SH_E_STATE, "sh_state_set_pos: no state or its context was destroyed");
+    if (pos < 0 || pos > s->ctx->info.n_ctx) return fail(SH_E_ARG, "sh_state_set_pos: out of range");
+    s->pos = pos;
+    return SH_OK;
+}
+
+static int run_step(sh_ctx* c, int M, sh_state* const st[2], const int32_t tok[2], const float* const emb[2], bool want_logits,
+                    float* const hid[2], float* const lg[2], int32_t* const best[2]) {
+    const sh_model_info& I = c->info;
+    for (int m = 0; m < M; m++) {
+        if (!st[m] || st[m]->ctx != c) return fail(SH_E_STATE, "step: state belongs to another context");
+        if (tok[m] >= I.n_vocab) return fail(SH_E_ARG, "step: token id out of range");
+        if (tok[m] < 0 && !emb[m]) return fail(SH_E_ARG, "step: token < 0 needs an input vector");
+        if (st[m]->pos >= I.n_ctx) {
+            fprintf(stderr, "seoul-hip: context full (%d)\n", I.n_ctx);
+            return fail(SH_E_CONTEXT_FULL, "step: context full");
+        }
+    }
+    if (M == 2 && st[0] == st[1]) return fail(SH_E_ARG, "step2: the two conversations must be different states");
+    HIPCHK(hipSetDevice(c->device));
+    hipGraphExec_t g;
+    int rc = get_graph(c, M, want_logits, &g);
+    if (rc != SH_OK) return rc;
+    step_params& P = *c->P_host;
+    memset(&P, 0, sizeof P);
+    for (int m = 0; m < M; m++) {
+        P.token[m] = tok[m];
+        fill_state(P, m, st[m]);
+        if (tok[m] < 0) HIPCHK(hipMemcpyAsync(c->embd_stage + (size_t)m * I.n_embd, emb[m], (size_t)I.n_embd * 4, hipMemcpyHostToDevice, c->stream));
+    }
+    HIPCHK(hipMemcpyAsync(c->P_dev, &P, sizeof P, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(hipGraphLaunch(g, c->stream));
+    for (int m = 0; m < M; m++) {
+        if (hid[m]) HIPCHK(hipMemcpyAsync(hid[m], c->hidden + (size_t)m * I.n_embd, (size_t)I.n_embd * 4, hipMemcpyDeviceToHost, c->stream));
+        if (want_logits && lg[m]) HIPCHK(hipMemcpyAsync(lg[m], c->logits + (size_t)m * I.n_vocab, (size_t)I.n_vocab * 4, hipMemcpyDeviceToHost, c->stream));
+    }
+    HIPCHK(hipMemcpyAsync(&P, c->P_dev, sizeof P, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(hipStreamSynchronize(c->stream));
+    for (int m = 0; m < M; m++) {
+        if (best[m]) *best[m] = want_logits ? P.best[m] : -1;
+        st[m]->pos++;
+    }
+    return SH_OK;
+}
+
+int sh_step(sh_ctx* c, sh_state* s, int32_t token, const float* embd, int want_logits, float* hidden, float* logits, int32_t* best) {
+    if (!c || !c->loaded) return fail(SH_E_STATE, "sh_step: no model loaded");
+    sh_state* st[2] = {s, nullptr};
+    const int32_t tok[2] = {token, 0};
+    const float* emb[2] = {embd, nullptr};
+    float* hid[2] = {hidden, nullptr};
+    float* lg[2] = {logits, nullptr};
+    int32_t* bs[2] = {best, nullptr};
+    return run_step(c, 1, st, tok, emb, want_logits != 0, hid, lg, bs);
+}
+
+int sh_step2(sh_ctx* c, sh_state* a, int32_t ta, const float* ea, int la, sh_state* b, int32_t tb, const float* eb, int lb,
+             float* ha, float* lga, int32_t* besta, float* hb, float* lgb, int32_t* bestb) {
+    if (!c || !c->loaded) return fail(SH_E_STATE, "sh_step2: no model loaded");
+    sh_state* st[2] = {a, b};
+    const int32_t tok[2] = {ta, tb};
+    const float* emb[2] = {ea, eb};
+    float* hid[2] = {ha, hb};
+    float* lg[2] = {la ? lga : nullptr, lb ? lgb : nullptr};
+    int32_t* bs[2] = {la ? besta : nullptr, lb ? bestb : nullptr};
+    if (besta && !la) *besta = -1;
+    if (bestb && !lb) *bestb = -1;
+    return run_step(c, 2, st, tok, emb, (la || lb), hid, lg, bs);
+}
+
+// n positions as n steps through the same graph (every position's numbers equal its own step's); a prefill
+// that reads each table once per 64 positions replaces this path for long inputs
+int sh_step_batch(sh_ctx* c, sh_state* s, const int32_t* tokens, const float* embd, int n, int want_logits,
+                  float* hidden_last, float* logits, float* hidden_all, int32_t* best) {
+    if (!c || !c->loaded) return fail(SH_E_STATE, "sh_step_batch: no model loaded");
+    if (!s || n < 0 || (!tokens && !embd)) return fail(SH_E_ARG, "sh_step_batch: bad argument");
+    const int E = c->info.n_embd;
+    if (s->pos + n > c->info.n_ctx) {
+        fprintf(stderr, "seoul-hip: context full (%d)\n", c->info.n_ctx);
+        return fail(SH_E_CONTEXT_FULL, "sh_step_batch: context full");
+    }
+    for (int i = 0; i < n; i++) {
+        const bool last = i == n - 1;
+        const int rc = sh_step(c, s, tokens ? tokens[i] : -1, embd ? embd + (size_t)i * E : nullptr, last && want_logits,
+                               hidden_all ? hidden_all + (size_t)i * E : (last ? hidden_last : nullptr), last ? logits : nullptr,
+                               last ? best : nullptr);
+        if (rc != SH_OK) return rc;
+        if (last && hidden_all && hidden_last) memcpy(hidden_last, hidden_all + (size_t)i * E, (size_t)E * 4);
+    }
+    return SH_OK;
+}
+
+int sh_generate(sh_ctx* c, sh_state* a, sh_state* b, int32_t fa, int32_t fb, int n, int32_t* out_a, int32_t* out_b, double* seconds) {
+    if (!c || !c->loaded) return fail(SH_E_STATE, "sh_generate: no model loaded");
+    if (!a || n < 0 || (b && b == a)) return fail(SH_E_ARG, "sh_generate: bad argument");
+    const int M = b ? 2 : 1;
+    sh_state* st[2] = {a, b};
+    const int32_t first[2] = {fa, fb};
+    for (int m = 0; m < M; m++) {
+        if (st[m]->ctx != c) return fail(SH_E_STATE, "sh_generate: state belongs to another context");
+        if (first[m] < 0 || first[m] >= c->info.n_vocab) return fail(SH_E_ARG, "sh_generate: first token out of range");
+        if (st[m]->pos + n > c->info.n_ctx) {
+            fprintf(stderr, "seoul-hip: context full (%d)\n", c->info.n_ctx);
+            return fail(SH_E_CONTEXT_FULL, "sh_generate: context full");
+        }
+    }
+    HIPCHK(hipSetDevice(c->device));
+    if (n > c->gen_cap) {
+        if (c->gen_out) HIPCHK(hipFree(c->gen_out));
+        HIPCHK(hipMalloc((void**)&c->gen_out, sizeof(int32_t) * 2 * (size_t)n));
+        c->gen_cap = n;
+    }
+    hipGraphExec_t g;
+    int rc = get_graph(c, M, true, &g);
+    if (rc != SH_OK) return rc;
+    step_params& P = *c->P_host;
+    memset(&P, 0, sizeof P);
+    P.greedy = 1;
+    for (int m = 0; m < M; m++) {
+        P.token[m] = first[m];
+        fill_state(P, m, st[m]);
+        P.out_tok[m] = c->gen_out + (size_t)m * c->gen_cap;
+    }
+    HIPCHK(hipMemcpyAsync(c->P_dev, &P, sizeof P, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(hipEventRecord(c->ev0, c->stream));
+    for (int i = 0; i < n; i++) HIPCHK(hipGraphLaunch(g, c->stream));
+    HIPCHK(hipEventRecord(c->ev1, c->stream));
+    if (out_a) HIPCHK(hipMemcpyAsync(out_a, c->gen_out, sizeof(int32_t) * n, hipMemcpyDeviceToHost, c->stream));
+    if (out_b && b) HIPCHK(hipMemcpyAsync(out_b, c->gen_out + c->gen_cap, sizeof(int32_t) * n, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(hipStreamSynchronize(c->stream));
+    float ms = 0.0f;
+    HIPCHK(hipEventElapsedTime(&ms, c->ev0, c->ev1));
+    if (seconds) *seconds = ms * 1e-3;
+    for (int m = 0; m < M; m++) st[m]->pos += n;
+    return SH_OK;
+}
+
+int sh_bench_tables(sh_ctx* c, int ncol, int reps, double* ms_per_pass, double* avg_launch_us, double* bytes_per_pass, int* launches) {
+    if (!c || !c->loaded) return fail(SH_E_STATE, "sh_bench_tables: no model loaded");
+    if (ncol < 1 || ncol > 2 || reps < 1) return fail(SH_E_ARG, "sh_bench_tables: ncol in {1, 2}, reps >= 1");
+    HIPCHK(hipSetDevice(c->device));
+    const size_t K = (size_t)(c->info.n_ff > c->info.n_embd ? c->info.n_ff : c->info.n_embd);
+    const size_t R = 4 * (size_t)c->info.n_ff + 3 * (size_t)c->info.n_embd + 64;
+    if (c->bench_cap < 2 * (K > R ? K : R)) {
+        if (c->bench_x) HIPCHK(hipFree(c->bench_x));
+        if (c->bench_y) HIPCHK(hipFree(c->bench_y));
+        c->bench_cap = 2 * (K > R ? K : R);
+        HIPCHK(hipMalloc((void**)&c->bench_x, c->bench_cap * 4));
+        HIPCHK(hipMalloc((void**)&c->bench_y, c->bench_cap * 4));
+        std::vector<float> in(c->bench_cap);
+        for (size_t i = 0; i < in.size(); i++) in[i] = 0.01f * (float)((i * 7) % 13) - 0.06f;   // seoul.cpp:668
+        HIPCHK(hipMemcpy(c->bench_x, in.data(), in.size() * 4, hipMemcpyHostToDevice));
+    }
+    std::vector<const q4dev*> ws;
+    for (auto& L : c->layers)
+        for (const q4dev* t : {&L.in_proj, &L.out_proj, &L.qkvg, &L.o, &L.gate_up, &L.down})
+            if (t->rows) ws.push_back(t);
+    double bytes = 0;
+    for (auto* t : ws) bytes += (double)t->rows * t->nb * 18;
+    double best = 1e30, total = 0;
+    for (int r = 0; r < reps + 1; r++) {
+        HIPCHK(hipEventRecord(c->ev0, c->stream));
+        for (auto* t : ws) {
+            gemv_args a{};
+            a.W = *t;
+            a.units = t->rows / 8;
+            a.src = c->bench_x;
+            a.src_ld = (int)K;
+            a.out = c->bench_y;
+            a.out_ld = (int)R;
+            HIPCHK(launch_gemv(ncol, PRO_CUT, EPI_STORE, a.units < 4096 ? a.units : 4096, a, c->stream));
+        }
+        HIPCHK(hipEventRecord(c->ev1, c->stream));
+        HIPCHK(hipEventSynchronize(c->ev1));
+        float ms;
+        HIPCHK(hipEventElapsedTime(&ms, c->ev0, c->ev1));
+        if (r == 0) continue;   // warm-up pass
+        best = ms < best ? ms : best;
+        total += ms;
+    }
+    if (ms_per_pass) *ms_per_pass = best;
+    if (avg_launch_us) *avg_launch_us = total * 1e3 / reps / ws.size();
+    if (bytes_per_pass) *bytes_per_pass = bytes;
+    if (launches) *launches = (int)ws.size();
+    return SH_OK;
+}
+
+// ---- kernel-level tables ----
+int sh_q4_create(sh_ctx* c, const void* q4_0, int rows, int cols, sh_q4** out) {
+    if (!c || !q4_0 || !out || rows <= 0 || rows % 8 || cols <= 0 || cols % 32) return fail(SH_E_ARG, "sh_q4_create: rows % 8 == 0, cols % 32 == 0");
+    if (cols / 32 > 4 * 64) return fail(SH_E_SHAPE, "sh_q4_create: at most 8192 columns");
+    HIPCHK(hipSetDevice(c->device));
+    gg_tensor t;
+    t.type = GT_Q4_0;
+    t.ne[0] = cols;
+    t.ne[1] = rows;
+    t.nb[1] = (size_t)cols / 32 * 18;
+    t.data = q4_0;
+    std::vector<std::pair<const gg_tensor*, int>> rr;
+    for (int r = 0; r < rows; r++) rr.push_back({&t, r});
+    std::vector<uint8_t> codes;
+    std::vector<uint16_t> scales;
+    int K;
+    if (!repack_q4(rr, codes, scales, &K)) return fail(SH_E_SHAPE, "sh_q4_create: repack failed");
+    auto h = std::make_unique<sh_q4>();
+    h->ctx = c;
+    const size_t cb = (codes.size() + 255) / 256 * 256;
+    HIPCHK(hipMalloc(&h->mem, cb + scales.size() * 2));
+    HIPCHK(hipMemcpy(h->mem, codes.data(), codes.size(), hipMemcpyHostToDevice));
+    HIPCHK(hipMemcpy(static_cast<char*>(h->mem) + cb, scales.data(), scales.size() * 2, hipMemcpyHostToDevice));
+    h->t.codes = h->mem;
+    h->t.scales = static_cast<char*>(h->mem) + cb;
+    h->t.rows = rows;
+    h->t.cols = cols;
+    h->t.nb = cols / 32;
+    c->tables.push_back(h.get());
+    *out = h.release();
+    return SH_OK;
+}
+
+int sh_q4_free(sh_q4* t) {
+    if (!t) return SH_OK;
+    if (t->ctx) {
+        (void)hipSetDevice(t->ctx->device);
+        (void)hipStreamSynchronize(t->ctx->stream);
+        if (t->mem) (void)hipFree(t->mem);
+        forget(t->ctx->tables, t);
+    }
+    delete t;
+    return SH_OK;
+}
+
+int sh_q4_rows(sh_ctx* c, const sh_q4* t, const int32_t* ids, int n, float* out) {
+    if (!c || !t || !ids || !out || n < 1) return fail(SH_E_ARG, "sh_q4_rows: bad argument");
+    if (t->ctx != c) return fail(SH_E_STATE, "sh_q4_rows: table belongs to another context");
+    for (int i = 0; i < n; i++)
+        if (ids[i] < 0 || ids[i] >= t->t.rows) return fail(SH_E_ARG, "sh_q4_rows: row id out of range");
+    HIPCHK(hipSetDevice(c->device));
+    int32_t* dids = nullptr;
+    float* dout = nullptr;
+    HIPCHK(hipMalloc((void**)&dids, sizeof(int32_t) * n));
+    hipError_t e = hipMalloc((void**)&dout, sizeof(float) * (size_t)n * t->t.cols);
+    if (e == hipSuccess) e = hipMemcpyAsync(dids, ids, sizeof(int32_t) * n, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = launch_q4_rows(t->t, dids, n, dout, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(out, dout, sizeof(float) * (size_t)n * t->t.cols, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    (void)hipFree(dids);
+    if (dout) (void)hipFree(dout);
+    if (e != hipSuccess) return fail(SH_E_HIP, std::string("sh_q4_rows: ") + hipGetErrorString(e));
+    return SH_OK;
+}
+
+int sh_q4_gemv_dev(sh_ctx* c, const sh_q4* t, const float* x, int n_in, float* y, int cut_mode) {
+    if (!c || !t || !x || !y || n_in < 1 || n_in > 2 || cut_mode < 0 || cut_mode > 1) return fail(SH_E_ARG, "sh_q4_gemv: bad argument");
+    if (t->ctx != c) return fail(SH_E_STATE, "sh_q4_gemv: table belongs to another context");
+    if (cut_mode == 1 && n_in != 1) return fail(SH_E_ARG, "sh_q4_gemv: the half-away cut takes one input");
+    gemv_args a{};
+    a.W = t->t;
+    a.units = t->t.rows / 8;
+    a.src = x;
+    a.src_ld = t->t.cols;
+    a.out = y;
+    a.out_ld = t->t.rows;
+    const int grid = a.units < 4096 ? a.units : 4096;
+    HIPCHK(launch_gemv(n_in, cut_mode ? PRO_CUT_HALF_AWAY : PRO_CUT, EPI_STORE, grid, a, c->stream));
+    return SH_OK;
+}
+
+int sh_q4_gemv(sh_ctx* c, const sh_q4* t, const float* x, int n_in, float* y, int cut_mode) {
+    if (!c || !t || !x || !y || n_in < 1 || n_in > 2) return fail(SH_E_ARG, "sh_q4_gemv: bad argument");
+    HIPCHK(hipSetDevice(c->device));
+    const size_t nx = (size_t)n_in * t->t.cols, ny = (size_t)n_in * t->t.rows;
+    const size_t need = nx > ny ? nx : ny;
+    if (c->bench_cap < need) {
+        if (c->bench_x) HIPCHK(hipFree(c->bench_x));
+        if (c->bench_y) HIPCHK(hipFree(c->bench_y));
+        HIPCHK(hipMalloc((void**)&c->bench_x, need * 4));
+        HIPCHK(hipMalloc((void**)&c->bench_y, need * 4));
+        c->bench_cap = need;
+    }
+    HIPCHK(hipMemcpyAsync(c->bench_x, x, nx * 4, hipMemcpyHostToDevice, c->stream));
+    const int rc = sh_q4_gemv_dev(c, t, c->bench_x, n_in, c->bench_y, cut_mode);
+    if (rc != SH_OK) return rc;
+    HIPCHK(hipMemcpyAsync(y, c->bench_y, ny * 4, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(hipStreamSynchronize(c->stream));
+    return SH_OK;
+}
+
+int sh_q4_bench(sh_ctx* c, sh_q4* const* tables, int n_tables, int n_in, int cut_mode, int reps, double* avg_us) {
+    if (!c || !tables || n_tables < 1 || reps < 1) return fail(SH_E_ARG, "sh_q4_bench: bad argument");
+    HIPCHK(hipSetDevice(c->device));
+    size_t need = 0;
+    for (int i = 0; i < n_tables; i++) {
+        const size_t n = (size_t)n_in * (tables[i]->t.cols > tables[i]->t.rows ? tables[i]->t.cols : tables[i]->t.rows);
+        need = n > need ? n : need;
+    }
+    if (c->bench_cap < need) {
+        if (c->bench_x) HIPCHK(hipFree(c->bench_x));
+        if (c->bench_y) HIPCHK(hipFree(c->bench_y));
+        HIPCHK(hipMalloc((void**)&c->bench_x, need * 4));
+        HIPCHK(hipMalloc((void**)&c->bench_y, need * 4));
+        HIPCHK(hipMemset(c->bench_x, 0, need * 4));
+        c->bench_cap = need;
+    }
+    for (int i = 0; i < n_tables; i++) {   // warm-up: one pass over every table
+        const int rc = sh_q4_gemv_dev(c, tables[i], c->bench_x, n_in, c->bench_y, cut_mode);
+        if (rc != SH_OK) return rc;
+    }
+    HIPCHK(hipEventRecord(c->ev0, c->stream));
+    for (int r = 0; r < reps; r++) {
+        const int rc = sh_q4_gemv_dev(c, tables[r % n_tables], c->bench_x, n_in, c->bench_y, cut_mode);
+        if (rc != SH_OK) return rc;
+    }
+    HIPCHK(hipEventRecord(c->ev1, c->stream));
+    HIPCHK(hipEventSynchronize(c->ev1));
+    float ms;
+    HIPCHK(hipEventElapsedTime(&ms, c->ev0, c->ev1));
+    if (avg_us) *avg_us = ms * 1e3 / reps;
+    return SH_OK;
+}
+
+int sh_expf(sh_ctx* c, const float* x, long long n, float* y) {
+    if (!c || !x || !y || n < 1) return fail(SH_E_ARG, "sh_expf: bad argument");
+    HIPCHK(hipSetDevice(c->device));
+    float *dx = nullptr, *dy = nullptr;
+    HIPCHK(hipMalloc((void**)&dx, sizeof(float) * n));
+    hipError_t e = hipMalloc((void**)&dy, sizeof(float) * n);
+    if (e == hipSuccess) e = hipMemcpyAsync(dx, x, sizeof(float) * n, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = launch_expf(dx, dy, n, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(y, dy, sizeof(float) * n, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    (void)hipFree(dx);
+    if (dy) (void)hipFree(dy);
+    if (e != hipSuccess) return fail(SH_E_HIP, std::string("sh_expf: ") + hipGetErrorString(e));
+    return SH_OK;
+}
+
+int sh_sync(sh_ctx* c) {
+    if (!c) return fail(SH_E_ARG, "sh_sync: null");
+    HIPCHK(hipStreamSynchronize(c->stream));
+    return SH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,86 @@
+// Kernel argument blocks and launch helpers of libseoul_hip (host + device).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace sh {
+
+// Per-step parameters, in device memory. The host writes token/pos/state pointers before a step; the step's last
+// kernel advances pos, and in a device-side greedy loop writes the chosen id back into token.
+struct step_params {
+    int32_t token[2];
+    int32_t pos[2];
+    int32_t best[2];        // argmax of the step's logits (-1 when no logits were computed)
+    int32_t n_done;         // steps finished in a device-side loop
+    int32_t greedy;         // 1: the next step's token is this step's argmax
+    uint16_t* kc[2];        // conversation m's key cache [n_attn][n_kv][n_ctx][D] fp16
+    uint16_t* vc[2];        // value cache, same layout
+    float* conv[2];         // conversation m's conv memory [n_conv][d_conv][E], oldest tap first
+    int32_t* out_tok[2];    // ids chosen in a device-side loop, or null
+};
+
+enum { PRO_CUT = 0, PRO_CUT_HALF_AWAY = 1, PRO_EMBED_NORM = 2, PRO_RESID_NORM = 3 };
+enum { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_CONV = 2, EPI_LOGITS = 3 };
+
+// one Q4_0 table in the device layout: codes [rows][nb][16 B] (the file's nibble bytes, scales split off),
+// scales [rows/8][nb][8] fp16 (the 8 rows of a group side by side per block)
+struct q4dev {
+    const void* codes = nullptr;
+    const void* scales = nullptr;
+    int rows = 0, cols = 0, nb = 0;
+};
+
+struct gemv_args {
+    q4dev W;
+    int units;                 // rows / (8 * groups per unit)
+    // prologue
+    const float* src;          // PRO_CUT*: float input [M][src_ld]
+    int src_ld;
+    const float* x_in;         // residual stream [M][E]
+    float* x_out;              // updated residual stream (block 0 writes it)
+    const float* y_in;         // table output added after its post-norm (PRO_RESID_NORM), null = none
+    const float* w_post;
+    const float* w_pre;        // norm weight in front of this table
+    const float* embd;         // PRO_EMBED_NORM: input vectors [M][E] used when token < 0
+    q4dev emb;                 // word table (input rows)
+    float* hidden_out;         // if set, block 0 writes the normed input h here ([M][E])
+    float eps;
+    // epilogue
+    float* out;                // [M][out_ld]
+    int out_ld;
+    const float* conv_w;       // EPI_CONV: [d_conv + 1][E]
+    int conv_layer, d_conv, E;
+    float* part_v;             // EPI_LOGITS: per-block best value [M][gridDim.x]
+    int* part_i;               // and its row
+    step_params* P;
+};
+
+struct attn_args {
+    const float* qkv;          // [M][ld_qkv]: q (H*D) | k (Hk*D) | v (Hk*D) | gate (H)
+    int ld_qkv;
+    float* att;                // [M][H*D]
+    const float* q_norm;
+    const float* k_norm;
+    const float2* rope_cs;     // [n_ctx][D/2] (cos, sin) for this layer's base, computed on the host
+    int layer_ai;              // attention layer index into the caches
+    int n_head, n_kv, D, n_ctx, n_swa;
+    float eps;
+    step_params* P;
+};
+
+struct final_args {
+    const float* x_in;         // residual stream [M][E]
+    const float* y_in;         // last table output (post-norm residual), null = none
+    const float* w_post;
+    const float* w_out;        // output norm
+    float* hidden_out;         // [M][E]
+    int E;
+    float eps;
+    const float* part_v;       // argmax partials (null when no logits were computed)
+    const int* part_i;
+    int n_part;
+    step_params* P;
+    int advance;               // 1: pos += 1 (and greedy bookkeeping)
+};
+
+}  // namespace sh

@@ -71,6 +71,7 @@ def lib():
         "orc_q4x8_quant_in": (None, [_f32p, i, _i8p, _f32p, _f32p]),
         "orc_q8g_gemm": (None, [_u8p, i, i, _f32p, i, _f32p]),
         "orc_rms_scale": (f, [_f32p, i, f]),
+        "orc_expf": (None, [_f32p, C.c_longlong, _f32p]),
         "orc_rope": (None, [_f32p, i, i, f, vp]),
         "orc_voice_load": (vp, [C.c_char_p, i]),
         "orc_voice_free": (None, [vp]),
@@ -294,6 +295,14 @@ def cut(x: np.ndarray):
     s = np.zeros(x.size // 32, np.float32)
     lib().orc_cut(x, x.size, q, d, s)
     return q, d, s
+
+
+def expf(x: np.ndarray) -> np.ndarray:
+    """The C library's expf (what imi calls), elementwise."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().orc_expf(x.reshape(-1), x.size, y.reshape(-1))
+    return y
 
 
 def rel(a, b) -> float:

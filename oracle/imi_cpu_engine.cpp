@@ -1136,6 +1136,7 @@ void orc_q8g_gemm(const uint8_t* q8_0, int rows, int cols, const float* xt, int 
     }
 }
 float orc_rms_scale(const float* x, int n, float eps) { return rms_scale(x, n, eps); }
+void orc_expf(const float* x, long long n, float* y) { for (long long i = 0; i < n; i++) y[i] = expf(x[i]); }   // the C library's
 void orc_rope(float* v, int n, int pos, float base, const float* ff) { rope(v, n, pos, base, ff); }
 
 // ---- voice generator ----

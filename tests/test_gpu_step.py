@@ -1,0 +1,188 @@
+"""GPU parity of the brain step (C ABI: sh_step / sh_step2 / sh_step_batch / sh_generate) against the oracle.
+
+The oracle is the CPU restatement of imi's engine (imi/core/seoul.cpp). The HIP path keeps every fp32 operation of
+imi's AVX2 arithmetic in the same order (per-row GEMV chains, the AVX2 reduction orders of the norms and dot
+products, the C library's expf, the fp16 cache), so its hidden states and word scores are bit for bit the oracle's;
+the tests hold it to that, which is stricter than the north star's 1e-3 relative L2 and same greedy ids. Bitwise
+equality matters: imi cuts every table input to int8, so a one-ulp difference anywhere can flip a code and move the
+scores by ~1e-3.
+"""
+import numpy as np
+import pytest
+
+from conftest import rel
+
+pytestmark = pytest.mark.gpu
+
+def same(a, b) -> bool:
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def _prompt(n, vocab, seed):
+    return np.random.default_rng(seed).integers(0, vocab, size=n).astype(np.int32)
+
+
+def _compare_steps(path, tokens, n_ctx=256, threads=4):
+    import nunchi_amd
+    import oracle
+    g = nunchi_amd.Brain(path, n_ctx=n_ctx)
+    o = oracle.Engine(path, threads=threads, n_ctx=n_ctx)
+    for i, t in enumerate(tokens):
+        hg, lg, bg = g.step(int(t))
+        ho, lo = o.step(int(t))
+        assert same(hg, ho), f"hidden differs at position {i} (rel {rel(hg, ho):.2e})"
+        assert same(lg, lo), f"word scores differ at position {i} (rel {rel(lg, lo):.2e})"
+        assert bg == oracle.top(lo) == int(np.argmax(lg))
+
+
+def test_tiny_model_steps(tiny_model):
+    _compare_steps(tiny_model, _prompt(40, 1000, 1))
+
+
+def test_seoul_width_steps(mid_model):
+    _compare_steps(mid_model, _prompt(24, 4096, 2))
+
+
+def test_embedding_input_and_no_logits(tiny_model):
+    import nunchi_amd
+    import oracle
+    g = nunchi_amd.Brain(tiny_model, n_ctx=64)
+    o = oracle.Engine(tiny_model, threads=2, n_ctx=64)
+    rng = np.random.default_rng(4)
+    for i in range(6):
+        e = rng.standard_normal(g.n_embd).astype(np.float32)
+        want = i % 2 == 0
+        hg, lg, bg = g.step(-1, e, want_logits=want)
+        ho, lo = o.step(-1, e, want_logits=want)
+        assert same(hg, ho)
+        if want:
+            assert same(lg, lo) and bg == oracle.top(lo)
+        else:
+            assert lg is None and bg == -1
+
+
+def test_step2_equals_two_steps(tiny_model):
+    """imi/core/seoul.cpp:222-224: each conversation of step2 gets exactly its own step's numbers."""
+    import nunchi_amd
+    g = nunchi_amd.Brain(tiny_model, n_ctx=64)
+    b = g.new_state()
+    a1, b1 = g.new_state(), g.new_state()
+    ta, tb = _prompt(12, 1000, 5), _prompt(12, 1000, 6)
+    rng = np.random.default_rng(7)
+    for i in range(12):
+        eb = rng.standard_normal(g.n_embd).astype(np.float32) if i % 3 == 2 else None
+        tok_b = -1 if eb is not None else int(tb[i])
+        (ha, la, ba), (hb, lb, bb) = g.step2(int(ta[i]), None, True, b, tok_b, eb, i % 2 == 0)
+        ha1, la1, ba1 = g.step(int(ta[i]), st=a1)
+        hb1, lb1, bb1 = g.step(tok_b, eb, want_logits=i % 2 == 0, st=b1)
+        assert np.array_equal(ha, ha1) and np.array_equal(la, la1) and ba == ba1
+        assert np.array_equal(hb, hb1) and bb == bb1
+        if i % 2 == 0:
+            assert np.array_equal(lb, lb1)
+    assert g.pos == 12 and b.pos == 12
+
+
+def test_step2_matches_oracle(mid_model):
+    import nunchi_amd
+    import oracle
+    g = nunchi_amd.Brain(mid_model, n_ctx=64)
+    o = oracle.Engine(mid_model, threads=4, n_ctx=64)
+    gb, ob = g.new_state(), o.new_state()
+    ta, tb = _prompt(10, 4096, 8), _prompt(10, 4096, 9)
+    for i in range(10):
+        (ha, la, ba), (hb, lb, bb) = g.step2(int(ta[i]), None, True, gb, int(tb[i]), None, True)
+        hoa, loa, hob, lob = o.step2(int(ta[i]), None, True, ob, int(tb[i]), None, True)
+        assert same(ha, hoa) and same(hb, hob)
+        assert same(la, loa) and same(lb, lob)
+        assert ba == oracle.top(loa) and bb == oracle.top(lob)
+
+
+def test_step_batch_matches_oracle(tiny_model):
+    import nunchi_amd
+    import oracle
+    g = nunchi_amd.Brain(tiny_model, n_ctx=160)
+    o = oracle.Engine(tiny_model, threads=4, n_ctx=160)
+    toks = _prompt(70, 1000, 10)   # more than one 64-position chunk on the oracle side
+    hg, lg, bg, hall_g = g.step_batch(toks, hidden_all=True)
+    ho, lo, hall_o = o.step_batch(toks, hidden_all=True)
+    for p in range(len(toks)):
+        assert same(hall_g[p], hall_o[p]), p
+    assert same(lg, lo) and bg == oracle.top(lo)
+    assert np.array_equal(hg, hall_g[-1])
+    assert g.pos == 70
+
+
+def test_greedy_generation_matches_oracle(mid_model):
+    import nunchi_amd
+    import oracle
+    g = nunchi_amd.Brain(mid_model, n_ctx=128)
+    o = oracle.Engine(mid_model, threads=4, n_ctx=128)
+    prompt = _prompt(8, 4096, 11)
+    _, _, bg, _ = g.step_batch(prompt)
+    _, lo, _ = o.step_batch(prompt)
+    first = oracle.top(lo)
+    assert bg == first
+    ids_g, secs = g.generate(first, 48)
+    ids_o, _ = o.greedy(first, 48)
+    assert np.array_equal(ids_g, ids_o), (ids_g, ids_o)
+    assert g.pos == 8 + 48 and secs > 0
+
+
+def test_greedy_two_conversations(tiny_model):
+    import nunchi_amd
+    import oracle
+    g = nunchi_amd.Brain(tiny_model, n_ctx=96)
+    o = oracle.Engine(tiny_model, threads=4, n_ctx=96)
+    gb, ob = g.new_state(), o.new_state()
+    ia, ib, _ = g.generate(3, 40, b=gb, first_b=977)
+    oa, obb, _ = o.greedy2(ob, 3, 977, 40)
+    assert np.array_equal(ia, oa) and np.array_equal(ib, obb)
+
+
+def test_state_semantics(tiny_model):
+    """reset / rewind / swap_state / context full (imi/core/seoul.cpp:188-209, 353)."""
+    import nunchi_amd
+    g = nunchi_amd.Brain(tiny_model, n_ctx=8)
+    toks = _prompt(8, 1000, 12)
+    first = [g.step(int(t))[1] for t in toks]
+    with pytest.raises(nunchi_amd.ContextFull):
+        g.step(1)
+    assert g.pos == 8
+    g.reset()
+    assert g.pos == 0
+    again = [g.step(int(t))[1] for t in toks]
+    assert all(np.array_equal(a, b) for a, b in zip(first, again))
+    # rewind to position 4 and replay: the K/V cache is overwritten by position, conv memory must be restored by
+    # replaying from a reset, so replay from 0 with the same prefix
+    other = g.new_state()
+    g.swap_state(other)
+    assert g.pos == 0 and other.pos == 8
+    h0 = g.step(int(toks[0]))[1]
+    assert np.array_equal(h0, first[0])
+    g.swap_state(other)
+    assert g.pos == 8
+
+
+def test_full_seoul_step_and_greedy(model_dir):
+    """cfg 2: the full Seoul-shaped model, a 32-token prompt, then 256 greedy ids; every id and the final state agree."""
+    import nunchi_amd
+    import oracle
+    from nunchi_amd import synth
+    path = synth.cached("brain", synth.SEOUL, 0, model_dir)
+    g = nunchi_amd.Brain(path, n_ctx=512)
+    o = oracle.Engine(path, threads=8, n_ctx=512)
+    prompt = _prompt(32, synth.SEOUL.n_vocab, 0)
+    for t in prompt[:-1]:
+        g.step(int(t), want_logits=False)
+        o.step(int(t), want_logits=False)
+    hg, lg, bg = g.step(int(prompt[-1]))
+    ho, lo = o.step(int(prompt[-1]))
+    assert same(hg, ho) and same(lg, lo) and bg == oracle.top(lo)
+    ids_g, _ = g.generate(bg, 255)   # 256 generated ids with bg
+    ids_o, _ = o.greedy(bg, 255)
+    assert np.array_equal(ids_g, ids_o)
+    # and the state after the loop is the same: one more step gives identical scores
+    hg, lg, _ = g.step(int(ids_g[-1]))
+    ho, lo = o.step(int(ids_o[-1]))
+    assert same(hg, ho) and same(lg, lo)
