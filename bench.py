@@ -1,0 +1,189 @@
+#!/usr/bin/env python3
+"""Benchmark of the brain step on one MI355X: the Seoul-shaped greedy decode (B=1 and the two-conversation step,
+B=2), the roofline of its dominant kernel, and imi's CPU path (the oracle restatement) timed on the host cores.
+
+    python bench.py [--gpus 1] [--steps 256] [--warmup 8] [--cpu-threads N] [--no-cpu]
+
+Prints one JSON line. A step is one decode position of the Seoul-shaped model (16 layers: 10 gated short-conv blocks,
+6 GQA blocks 32/8 x 64, FFN 8192, tied Q4_0 word table 97,496 x 2048), synthetic seeded weights, a 32-token seeded
+prompt, then --steps greedy ids generated on the device (argmax fed back without host round trips), context 512.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+N_CTX = 512
+PROMPT = 32
+
+
+def _prompt(seed, vocab):
+    return np.random.default_rng(seed).integers(0, vocab, size=PROMPT).astype(np.int32)
+
+
+def gpu_decode(brain, steps, warmup, b2: bool):
+    """Greedy decode after the prompt; returns (tokens/s over the timed steps, ids, device seconds)."""
+    def prepare():
+        sa = brain.new_state()
+        sb = brain.new_state() if b2 else None
+        pa, pb = _prompt(0, brain.n_vocab), _prompt(1, brain.n_vocab)
+        for i in range(PROMPT):
+            last = i == PROMPT - 1
+            if b2:
+                (_, _, ba), (_, _, bb) = brain.step2(int(pa[i]), None, last, sb, int(pb[i]), None, last, a=sa)
+            else:
+                _, _, ba = brain.step(int(pa[i]), want_logits=last, st=sa)
+                bb = None
+        return sa, sb, ba, bb
+
+    sa, sb, ba, bb = prepare()
+    if warmup:
+        brain.generate(ba, warmup, b=sb, first_b=bb or 0, a=sa)
+    sa, sb, ba, bb = prepare()
+    t0 = time.perf_counter()
+    out = brain.generate(ba, steps, b=sb, first_b=bb or 0, a=sa)
+    wall = time.perf_counter() - t0
+    ids, dev = (out[0], out[2]) if b2 else out
+    tokens = steps * (2 if b2 else 1)
+    return tokens / wall, ids, dev, wall
+
+
+def cpu_decode(path, threads, steps, b2: bool):
+    import oracle
+    eng = oracle.Engine(path, threads=threads, n_ctx=N_CTX)
+    pa, pb = _prompt(0, eng.n_vocab), _prompt(1, eng.n_vocab)
+    if b2:
+        sb = eng.new_state()
+        for i in range(PROMPT):
+            last = i == PROMPT - 1
+            _, la, _, lb = eng.step2(int(pa[i]), None, last, sb, int(pb[i]), None, last)
+        oa, ob, secs = eng.greedy2(sb, oracle.top(la), oracle.top(lb), steps)
+        return 2 * steps / secs, oa, secs
+    for i in range(PROMPT):
+        _, lg = eng.step(int(pa[i]), want_logits=i == PROMPT - 1)
+    ids, secs = eng.greedy(oracle.top(lg), steps)
+    return steps / secs, ids, secs
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, cores in the affinity mask)")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (conversations shard across "
+              "GPUs with no exchange; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    if PROMPT + max(args.steps, args.warmup) > N_CTX:
+        print(f"bench.py: prompt + steps must fit the context of {N_CTX}", file=sys.stderr)
+        sys.exit(2)
+
+    import nunchi_amd
+    from nunchi_amd import synth
+    path = synth.cached("brain", synth.SEOUL, 0)
+    brain = nunchi_amd.Brain(path, n_ctx=N_CTX)
+
+    tok_s_b1, ids_b1, dev_b1, wall_b1 = gpu_decode(brain, args.steps, args.warmup, b2=False)
+    tok_s_b2, ids_b2, dev_b2, wall_b2 = gpu_decode(brain, args.steps, args.warmup, b2=True)
+
+    # dominant kernel: the FFN gate|up GEMV (norm prologue, SwiGLU epilogue), 16 per step, 18.9 MB of table each
+    gu = brain.bench_kernel("ffn_gate_up", n_in=1, reps=64)
+    dn = brain.bench_kernel("ffn_down", n_in=1, reps=64)
+    ws = brain.bench_kernel("word_scores", n_in=1, reps=8)
+    gu2 = brain.bench_kernel("ffn_gate_up", n_in=2, reps=64)
+    tables1 = brain.bench_tables(1, 5)
+    tables2 = brain.bench_tables(2, 5)
+
+    # cfg 0: one Q4_0 x fp32 GEMV 8192 x 2048 with imi/kernels/q4x8 semantics, 64 distinct weight copies in rotation
+    ctx = brain.ctx
+    copies = [nunchi_amd.Q4Table(ctx, synth.q4_0_random(np.random.default_rng(100 + i), 8192, 2048), 8192, 2048) for i in range(64)]
+    cfg0_us = nunchi_amd.q4_bench(ctx, copies, n_in=1, cut_mode=1, reps=640)
+    cfg0_bytes = 8192 * 64 * 18 + 2048 * 4 + 8192 * 4
+    del copies
+
+    gu_gbs = gu["bytes_per_launch"] / (gu["avg_us"] * 1e-6) / 1e9
+    # algorithmic bytes of one step: every table once (device layout = file bytes: 16 B codes + 2 B scale per 32
+    # weights) + the K and V read at the mean decode position (6 layers x 512 fp16 values per position, each)
+    mean_pos = PROMPT + args.steps / 2
+    step_bytes = brain.table_bytes + 2 * brain.n_attn * mean_pos * brain.n_head_kv * brain.head_dim * 2
+    line = {
+        "metric": "brain-step tokens/s (B=1,2) + Q4_0 GEMV HBM GB/s vs roofline, 1 MI355X",
+        "value": round(tok_s_b1, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 / tok_s_b1, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 x q4_0 -> int32 dots, fp32 epilogue",
+        "data": "synthetic (seeded random Q4_0 weights of the Seoul shape)",
+        "config": {
+            "workload": "cfg2: Seoul-shaped brain decode, 16 layers (10 short-conv k=3, 6 GQA 32/8 x 64, RoPE 1e6), FFN 8192, "
+                        "tied Q4_0 vocab 97496 x 2048, fp16 KV ctx 512; 32-token seeded prompt then greedy ids on device",
+            "batch": 1,
+            "generated_tokens": args.steps,
+            "prompt_tokens": PROMPT,
+        },
+        "b2_tokens_per_s": round(tok_s_b2, 1),
+        "b2_ms_per_step": round(2e3 / tok_s_b2, 4),
+        "device_ms_per_step": {"b1": round(dev_b1 * 1e3 / args.steps, 4), "b2": round(dev_b2 * 1e3 / args.steps, 4)},
+        "step_hbm_fraction": {"b1": round(step_bytes * tok_s_b1 / 1e9 / HBM_PEAK_GBS, 4),
+                              "b2": round(step_bytes * tok_s_b2 / 2 / 1e9 / HBM_PEAK_GBS, 4),
+                              "bytes_per_step": int(step_bytes)},
+        "roofline": {
+            "kernel": "k_gemv<1,1,PRO_RESID_NORM,EPI_SWIGLU,2> (FFN gate|up, 16384 x 2048 Q4_0)",
+            "bound": "hbm",
+            "achieved": round(gu_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_us": round(gu["avg_us"], 3),
+            "bytes_per_launch": int(gu["bytes_per_launch"]),
+        },
+        "kernels": {
+            "ffn_gate_up_b2": {"avg_us": round(gu2["avg_us"], 3), "GBs": round(gu2["bytes_per_launch"] / gu2["avg_us"] / 1e3, 1)},
+            "ffn_down": {"avg_us": round(dn["avg_us"], 3), "GBs": round(dn["bytes_per_launch"] / dn["avg_us"] / 1e3, 1)},
+            "word_scores": {"avg_us": round(ws["avg_us"], 3), "GBs": round(ws["bytes_per_launch"] / ws["avg_us"] / 1e3, 1)},
+            "layer_tables_b1": {"avg_launch_us": round(tables1["avg_launch_us"], 3), "ms_per_pass": round(tables1["ms_per_pass"], 4),
+                                "GBs": round(tables1["bytes_per_pass"] / tables1["launches"] / tables1["avg_launch_us"] / 1e3, 1)},
+            "layer_tables_b2": {"avg_launch_us": round(tables2["avg_launch_us"], 3), "ms_per_pass": round(tables2["ms_per_pass"], 4)},
+            "cfg0_gemv_8192x2048": {"avg_us": round(cfg0_us, 3), "GBs": round(cfg0_bytes / cfg0_us / 1e3, 1),
+                                    "frac": round(cfg0_bytes / cfg0_us / 1e3 / HBM_PEAK_GBS, 4)},
+        },
+    }
+    if not args.no_cpu:
+        aff = len(os.sched_getaffinity(0))
+        threads = args.cpu_threads or min(16, aff)
+        cpu_steps = min(args.steps, 256)
+        c1, cids, csecs = cpu_decode(path, threads, cpu_steps, b2=False)
+        c2, _, csecs2 = cpu_decode(path, threads, min(cpu_steps, 128), b2=True)
+        same = bool(np.array_equal(cids[:len(ids_b1)], ids_b1[:len(cids)]))
+        line["cpu_baseline"] = {
+            "value": round(c1, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"cfg2 B=1: {PROMPT}-token prompt then {cpu_steps} greedy ids ({csecs:.1f} s); B=2: step2 for "
+                      f"{min(cpu_steps, 128)} positions ({csecs2:.1f} s) = {c2:.2f} tokens/s; {threads} threads of {aff} in the "
+                      "affinity mask; oracle/ C++ restatement of imi's AVX2 engine, x86-64-v3",
+            "b2_value": round(c2, 2),
+        }
+        line["speedup_vs_cpu"] = {"b1": round(tok_s_b1 / c1, 1), "b2": round(tok_s_b2 / c2, 1)}
+        line["greedy_ids_match_cpu"] = same
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -91,6 +91,11 @@ int sh_generate(sh_ctx* ctx, sh_state* a, sh_state* b, int32_t first_a, int32_t 
 int sh_bench_tables(sh_ctx* ctx, int ncol, int reps, double* ms_per_pass, double* avg_launch_us,
                     double* bytes_per_pass, int* launches_per_pass);
 
+/* The step's own GEMV kernel for one table kind (0: FFN gate|up with norm prologue and SwiGLU epilogue, 1: FFN
+ * down, 2: word scores), launched reps times with real layer arguments rotating over the layers; avg_us = mean
+ * kernel duration (events recorded around each kernel), bytes_per_launch = table + input + output bytes. */
+int sh_bench_kernel(sh_ctx* ctx, int kind, int n_in, int reps, double* avg_us, double* bytes_per_launch);
+
 /* ---- kernel-level Q4_0 tables (imi/kernels/q4x8.h:14-18, imi/core/tables.h:103-138) ---- */
 /* q4_0: rows * cols/32 Q4_0 blocks (fp16 scale + 16 nibble bytes) as stored in GGUF; rows % 8 == 0. */
 int sh_q4_create(sh_ctx* ctx, const void* q4_0, int rows, int cols, sh_q4** out);

@@ -21,6 +21,7 @@ SH_OK, SH_E_ARG, SH_E_HIP, SH_E_FILE, SH_E_SHAPE, SH_E_CONTEXT_FULL, SH_E_STATE,
 EXPORTS = [
     "sh_last_error", "sh_create", "sh_destroy", "sh_load", "sh_info", "sh_state_new", "sh_state_free", "sh_state_reset",
     "sh_state_pos", "sh_state_set_pos", "sh_step", "sh_step2", "sh_step_batch", "sh_generate", "sh_bench_tables",
+    "sh_bench_kernel",
     "sh_q4_create", "sh_q4_free", "sh_q4_rows", "sh_q4_gemv", "sh_q4_gemv_dev", "sh_q4_bench", "sh_expf", "sh_sync",
 ]
 
@@ -69,6 +70,7 @@ def load_library(path: str = LIB_PATH):
         "sh_step_batch": (i, [vp, vp, vp, vp, i, i, vp, vp, vp, vp]),
         "sh_generate": (i, [vp, vp, vp, C.c_int32, C.c_int32, i, vp, vp, P(d)]),
         "sh_bench_tables": (i, [vp, i, i, P(d), P(d), P(d), P(i)]),
+        "sh_bench_kernel": (i, [vp, i, i, i, P(d), P(d)]),
         "sh_q4_create": (i, [vp, vp, i, i, P(vp)]),
         "sh_q4_free": (i, [vp]),
         "sh_q4_rows": (i, [vp, vp, vp, i, vp]),
@@ -250,6 +252,14 @@ class Brain:
         ms, us, by, nl = C.c_double(), C.c_double(), C.c_double(), C.c_int()
         _check(_lib.sh_bench_tables(self.ctx.h, int(ncol), int(reps), C.byref(ms), C.byref(us), C.byref(by), C.byref(nl)))
         return {"ms_per_pass": ms.value, "avg_launch_us": us.value, "bytes_per_pass": by.value, "launches": nl.value}
+
+    KERNELS = {"ffn_gate_up": 0, "ffn_down": 1, "word_scores": 2}
+
+    def bench_kernel(self, kind: str, n_in: int = 1, reps: int = 64):
+        """Mean duration (us) and bytes per launch of the step's GEMV for one table kind."""
+        us, by = C.c_double(), C.c_double()
+        _check(_lib.sh_bench_kernel(self.ctx.h, self.KERNELS[kind], int(n_in), int(reps), C.byref(us), C.byref(by)))
+        return {"avg_us": us.value, "bytes_per_launch": by.value}
 
 
 class Q4Table:

@@ -7,6 +7,7 @@
 
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -16,7 +17,7 @@
 #include "sh_kernels.h"
 
 namespace sh {
-hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hipStream_t s);
+hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hipStream_t s, hipEvent_t t0 = nullptr, hipEvent_t t1 = nullptr);
 hipError_t launch_attn(int M, const attn_args& a, hipStream_t s);
 hipError_t launch_final(int M, const final_args& a, hipStream_t s);
 hipError_t launch_q4_rows(const q4dev& T, const int32_t* ids, int n, float* out, hipStream_t s);
@@ -125,6 +126,9 @@ struct sh_ctx {
     hipGraphExec_t graph[3][2] = {{nullptr, nullptr}, {nullptr, nullptr}, {nullptr, nullptr}};
     std::vector<sh_state*> states;    // live children: destroying the context releases their device memory
     std::vector<sh_q4*> tables;
+    // the step replays a captured graph; SEOUL_HIP_GRAPHS=0 enqueues the same kernels directly (for tools that do
+    // not trace graph launches)
+    bool use_graphs = true;
 };
 
 namespace {
@@ -282,6 +286,10 @@ int enqueue_step(sh_ctx* c, int M, bool want_logits) {
 }
 
 int get_graph(sh_ctx* c, int M, bool want_logits, hipGraphExec_t* out) {
+    if (!c->use_graphs) {
+        *out = nullptr;
+        return SH_OK;
+    }
     hipGraphExec_t& g = c->graph[M][want_logits ? 1 : 0];
     if (!g) {
         hipGraph_t graph;
@@ -342,6 +350,8 @@ int sh_create(int device, sh_ctx** out) {
     HIPCHK(hipHostMalloc((void**)&c->P_host, sizeof(step_params), hipHostMallocDefault));
     HIPCHK(hipMalloc((void**)&c->P_dev, sizeof(step_params)));
     memset(c->P_host, 0, sizeof(step_params));
+    const char* g = getenv("SEOUL_HIP_GRAPHS");
+    c->use_graphs = !(g && g[0] == '0');
     *out = c.release();
     return SH_OK;
 }
@@ -672,7 +682,8 @@ static int run_step(sh_ctx* c, int M, sh_state* const st[2], const int32_t tok[2
         if (tok[m] < 0) HIPCHK(hipMemcpyAsync(c->embd_stage + (size_t)m * I.n_embd, emb[m], (size_t)I.n_embd * 4, hipMemcpyHostToDevice, c->stream));
     }
     HIPCHK(hipMemcpyAsync(c->P_dev, &P, sizeof P, hipMemcpyHostToDevice, c->stream));
-    HIPCHK(hipGraphLaunch(g, c->stream));
+    if (g) HIPCHK(hipGraphLaunch(g, c->stream));
+    else if ((rc = enqueue_step(c, M, want_logits)) != SH_OK) return rc;
     for (int m = 0; m < M; m++) {
         if (hid[m]) HIPCHK(hipMemcpyAsync(hid[m], c->hidden + (size_t)m * I.n_embd, (size_t)I.n_embd * 4, hipMemcpyDeviceToHost, c->stream));
         if (want_logits && lg[m]) HIPCHK(hipMemcpyAsync(lg[m], c->logits + (size_t)m * I.n_vocab, (size_t)I.n_vocab * 4, hipMemcpyDeviceToHost, c->stream));
@@ -766,7 +777,10 @@ int sh_generate(sh_ctx* c, sh_state* a, sh_state* b, int32_t fa, int32_t fb, int
     }
     HIPCHK(hipMemcpyAsync(c->P_dev, &P, sizeof P, hipMemcpyHostToDevice, c->stream));
     HIPCHK(hipEventRecord(c->ev0, c->stream));
-    for (int i = 0; i < n; i++) HIPCHK(hipGraphLaunch(g, c->stream));
+    for (int i = 0; i < n; i++) {
+        if (g) HIPCHK(hipGraphLaunch(g, c->stream));
+        else if ((rc = enqueue_step(c, M, true)) != SH_OK) return rc;
+    }
     HIPCHK(hipEventRecord(c->ev1, c->stream));
     if (out_a) HIPCHK(hipMemcpyAsync(out_a, c->gen_out, sizeof(int32_t) * n, hipMemcpyDeviceToHost, c->stream));
     if (out_b && b) HIPCHK(hipMemcpyAsync(out_b, c->gen_out + c->gen_cap, sizeof(int32_t) * n, hipMemcpyDeviceToHost, c->stream));
@@ -778,53 +792,170 @@ int sh_generate(sh_ctx* c, sh_state* a, sh_state* b, int32_t fa, int32_t fb, int
     return SH_OK;
 }
 
+namespace {
+// timing of individual kernel launches: event pairs recorded around each kernel (hipExtLaunchKernelGGL)
+struct launch_timer {
+    std::vector<hipEvent_t> ev;
+    int used = 0;
+    ~launch_timer() { for (auto e : ev) (void)hipEventDestroy(e); }
+    hipError_t reserve(int n) {
+        while ((int)ev.size() < 2 * n) {
+            hipEvent_t e;
+            const hipError_t r = hipEventCreate(&e);
+            if (r != hipSuccess) return r;
+            ev.push_back(e);
+        }
+        used = 0;
+        return hipSuccess;
+    }
+    hipEvent_t start() { return ev[2 * used]; }
+    hipEvent_t stop() { return ev[2 * used + 1]; }
+    void next() { used++; }
+    hipError_t total_ms(double* ms) {
+        double t = 0;
+        for (int i = 0; i < used; i++) {
+            float x;
+            const hipError_t r = hipEventElapsedTime(&x, ev[2 * i], ev[2 * i + 1]);
+            if (r != hipSuccess) return r;
+            t += x;
+        }
+        *ms = t;
+        return hipSuccess;
+    }
+};
+
+int bench_inputs(sh_ctx* c) {
+    const size_t K = (size_t)(c->info.n_ff > c->info.n_embd ? c->info.n_ff : c->info.n_embd);
+    const size_t R = 4 * (size_t)c->info.n_ff + 3 * (size_t)c->info.n_embd + 64;
+    const size_t need = 2 * (K > R ? K : R);
+    if (c->bench_cap >= need) return SH_OK;
+    if (c->bench_x) HIPCHK(hipFree(c->bench_x));
+    if (c->bench_y) HIPCHK(hipFree(c->bench_y));
+    c->bench_cap = need;
+    HIPCHK(hipMalloc((void**)&c->bench_x, c->bench_cap * 4));
+    HIPCHK(hipMalloc((void**)&c->bench_y, c->bench_cap * 4));
+    std::vector<float> in(c->bench_cap);
+    for (size_t i = 0; i < in.size(); i++) in[i] = 0.01f * (float)((i * 7) % 13) - 0.06f;   // seoul.cpp:668
+    HIPCHK(hipMemcpy(c->bench_x, in.data(), in.size() * 4, hipMemcpyHostToDevice));
+    return SH_OK;
+}
+}  // namespace
+
 int sh_bench_tables(sh_ctx* c, int ncol, int reps, double* ms_per_pass, double* avg_launch_us, double* bytes_per_pass, int* launches) {
     if (!c || !c->loaded) return fail(SH_E_STATE, "sh_bench_tables: no model loaded");
     if (ncol < 1 || ncol > 2 || reps < 1) return fail(SH_E_ARG, "sh_bench_tables: ncol in {1, 2}, reps >= 1");
     HIPCHK(hipSetDevice(c->device));
-    const size_t K = (size_t)(c->info.n_ff > c->info.n_embd ? c->info.n_ff : c->info.n_embd);
-    const size_t R = 4 * (size_t)c->info.n_ff + 3 * (size_t)c->info.n_embd + 64;
-    if (c->bench_cap < 2 * (K > R ? K : R)) {
-        if (c->bench_x) HIPCHK(hipFree(c->bench_x));
-        if (c->bench_y) HIPCHK(hipFree(c->bench_y));
-        c->bench_cap = 2 * (K > R ? K : R);
-        HIPCHK(hipMalloc((void**)&c->bench_x, c->bench_cap * 4));
-        HIPCHK(hipMalloc((void**)&c->bench_y, c->bench_cap * 4));
-        std::vector<float> in(c->bench_cap);
-        for (size_t i = 0; i < in.size(); i++) in[i] = 0.01f * (float)((i * 7) % 13) - 0.06f;   // seoul.cpp:668
-        HIPCHK(hipMemcpy(c->bench_x, in.data(), in.size() * 4, hipMemcpyHostToDevice));
-    }
+    int rc = bench_inputs(c);
+    if (rc != SH_OK) return rc;
+    const int K = c->info.n_ff > c->info.n_embd ? c->info.n_ff : c->info.n_embd;
+    const int R = 4 * c->info.n_ff + 3 * c->info.n_embd + 64;
     std::vector<const q4dev*> ws;
     for (auto& L : c->layers)
         for (const q4dev* t : {&L.in_proj, &L.out_proj, &L.qkvg, &L.o, &L.gate_up, &L.down})
             if (t->rows) ws.push_back(t);
     double bytes = 0;
     for (auto* t : ws) bytes += (double)t->rows * t->nb * 18;
-    double best = 1e30, total = 0;
+    launch_timer lt;
+    HIPCHK(lt.reserve((int)ws.size()));
+    double best = 1e30, total_launch_ms = 0;
     for (int r = 0; r < reps + 1; r++) {
+        lt.used = 0;
         HIPCHK(hipEventRecord(c->ev0, c->stream));
         for (auto* t : ws) {
             gemv_args a{};
             a.W = *t;
             a.units = t->rows / 8;
             a.src = c->bench_x;
-            a.src_ld = (int)K;
+            a.src_ld = K;
             a.out = c->bench_y;
-            a.out_ld = (int)R;
-            HIPCHK(launch_gemv(ncol, PRO_CUT, EPI_STORE, a.units < 4096 ? a.units : 4096, a, c->stream));
+            a.out_ld = R;
+            HIPCHK(launch_gemv(ncol, PRO_CUT, EPI_STORE, a.units < 4096 ? a.units : 4096, a, c->stream, lt.start(), lt.stop()));
+            lt.next();
         }
         HIPCHK(hipEventRecord(c->ev1, c->stream));
         HIPCHK(hipEventSynchronize(c->ev1));
         float ms;
         HIPCHK(hipEventElapsedTime(&ms, c->ev0, c->ev1));
+        double kms;
+        HIPCHK(lt.total_ms(&kms));
         if (r == 0) continue;   // warm-up pass
         best = ms < best ? ms : best;
-        total += ms;
+        total_launch_ms += kms;
     }
     if (ms_per_pass) *ms_per_pass = best;
-    if (avg_launch_us) *avg_launch_us = total * 1e3 / reps / ws.size();
+    if (avg_launch_us) *avg_launch_us = total_launch_ms * 1e3 / reps / ws.size();
     if (bytes_per_pass) *bytes_per_pass = bytes;
     if (launches) *launches = (int)ws.size();
+    return SH_OK;
+}
+
+// The step's own kernel for one table kind, launched with a real layer's arguments, rotating over the layers so
+// successive launches read different tables (more than the 256 MB MALL in total); each launch timed by itself.
+int sh_bench_kernel(sh_ctx* c, int kind, int M, int reps, double* avg_us, double* bytes_per_launch) {
+    if (!c || !c->loaded) return fail(SH_E_STATE, "sh_bench_kernel: no model loaded");
+    if (M < 1 || M > 2 || reps < 1 || kind < 0 || kind > 2) return fail(SH_E_ARG, "sh_bench_kernel: bad argument");
+    HIPCHK(hipSetDevice(c->device));
+    const sh_model_info& I = c->info;
+    const int E = I.n_embd;
+    launch_timer lt;
+    HIPCHK(lt.reserve(reps));
+    double bytes = 0;
+    for (int pass = 0; pass < 2; pass++) {   // pass 0 warms up (code, TLB), pass 1 is timed
+        lt.used = 0;
+        bytes = 0;
+        for (int r = 0; r < reps; r++) {
+            const layer_dev& L = c->layers[r % c->layers.size()];
+            gemv_args a{};
+            a.P = c->P_dev;
+            a.E = E;
+            a.eps = c->eps;
+            int pro, epi, grid;
+            if (kind == 0) {          // FFN gate|up with the post-norm residual, RMS norm, cut, SwiGLU epilogue
+                a.x_in = c->xbuf[0];
+                a.y_in = c->y;
+                a.w_post = L.post_attn_norm;
+                a.x_out = c->xbuf[1];
+                a.w_pre = L.ffn_norm;
+                a.W = L.gate_up;
+                a.units = L.gate_up.rows / 16;
+                a.out = c->act;
+                a.out_ld = I.n_ff;
+                pro = PRO_RESID_NORM; epi = EPI_SWIGLU;
+                bytes += (double)L.gate_up.rows * L.gate_up.nb * 18 + 4.0 * M * (2 * E + I.n_ff);
+            } else if (kind == 1) {   // FFN down, input cut in the prologue
+                a.W = L.down;
+                a.units = L.down.rows / 8;
+                a.src = c->act;
+                a.src_ld = I.n_ff;
+                a.out = c->fo;
+                a.out_ld = E;
+                pro = PRO_CUT; epi = EPI_STORE;
+                bytes += (double)L.down.rows * L.down.nb * 18 + 4.0 * M * (I.n_ff + E);
+            } else {                  // word scores over the tied table
+                a.x_in = c->xbuf[0];
+                a.y_in = c->fo;
+                a.w_post = L.post_ffn_norm;
+                a.w_pre = c->out_norm;
+                a.hidden_out = c->hidden;
+                a.W = c->vocab;
+                a.units = c->vocab.rows / 8;
+                a.out = c->logits;
+                a.out_ld = I.n_vocab;
+                a.part_v = c->part_v;
+                a.part_i = c->part_i;
+                pro = PRO_RESID_NORM; epi = EPI_LOGITS;
+                bytes += (double)c->vocab.rows * c->vocab.nb * 18 + 4.0 * M * (2 * E + I.n_vocab);
+            }
+            grid = epi == EPI_LOGITS ? (a.units < c->vocab_grid ? a.units : c->vocab_grid) : (a.units < 4096 ? a.units : 4096);
+            HIPCHK(launch_gemv(M, pro, epi, grid, a, c->stream, lt.start(), lt.stop()));
+            lt.next();
+        }
+        HIPCHK(hipStreamSynchronize(c->stream));
+    }
+    double ms;
+    HIPCHK(lt.total_ms(&ms));
+    if (avg_us) *avg_us = ms * 1e3 / reps;
+    if (bytes_per_launch) *bytes_per_launch = bytes / reps;
     return SH_OK;
 }
 

@@ -5,6 +5,8 @@
 // Arithmetic follows imi's engine (imi/core/seoul.cpp:359-488, imi/core/tables.cpp:100-198, imi/core/vec.h): the
 // input of every table is cut to int8 per 32 values, each 32-column block's integer dot is exact, and the fp32
 // epilogue per block is  float(isum) * (d * dx) - d * (8 * dx * sum(xq))  summed over blocks.
+#include <hip/hip_ext.h>
+
 #include "sh_device.h"
 #include "sh_kernels.h"
 
@@ -410,15 +412,18 @@ __global__ __launch_bounds__(64) void k_q4_rows(q4dev T, const int32_t* ids, flo
 }
 
 // ---------------------------------------------------------------- launchers
-#define SH_GEMV_CASE(M_, NBL_, PRO_, EPI_, UG_)                                                                 \
-    if (M == M_ && nbl == NBL_ && pro == PRO_ && epi == EPI_ && ug == UG_) {                                    \
-        const size_t lds = gemv_lds(M_, UG_, a.W.nb, a.E, PRO_ == PRO_EMBED_NORM || PRO_ == PRO_RESID_NORM);    \
-        if (lds > 64 * 1024) return hipErrorInvalidValue;                                                       \
-        hipLaunchKernelGGL((k_gemv<M_, NBL_, PRO_, EPI_, UG_>), dim3(grid), dim3(64), lds, s, a);               \
-        return hipGetLastError();                                                                               \
+// with t0/t1 set, the launch records them around the kernel itself (hipExtLaunchKernelGGL), which times the
+// kernel's own duration without the dispatch gap in front of it
+#define SH_GEMV_CASE(M_, NBL_, PRO_, EPI_, UG_)                                                                  \
+    if (M == M_ && nbl == NBL_ && pro == PRO_ && epi == EPI_ && ug == UG_) {                                     \
+        const size_t lds = gemv_lds(M_, UG_, a.W.nb, a.E, PRO_ == PRO_EMBED_NORM || PRO_ == PRO_RESID_NORM);     \
+        if (lds > 64 * 1024) return hipErrorInvalidValue;                                                        \
+        if (t0) hipExtLaunchKernelGGL((k_gemv<M_, NBL_, PRO_, EPI_, UG_>), dim3(grid), dim3(64), lds, s, t0, t1, 0, a); \
+        else hipLaunchKernelGGL((k_gemv<M_, NBL_, PRO_, EPI_, UG_>), dim3(grid), dim3(64), lds, s, a);           \
+        return hipGetLastError();                                                                                \
     }
 
-hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hipStream_t s) {
+hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
     const int nbl = (a.W.nb + 63) / 64;
     const int ug = epi == EPI_SWIGLU ? 2 : epi == EPI_CONV ? 3 : 1;
     SH_GEMV_CASE(1, 1, PRO_CUT, EPI_STORE, 1) SH_GEMV_CASE(2, 1, PRO_CUT, EPI_STORE, 1)
