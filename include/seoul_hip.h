@@ -116,6 +116,13 @@ int sh_q4_bench(sh_ctx* ctx, sh_q4* const* tables, int n_tables, int n_in, int c
  * that imi runs on (imi/core/seoul.cpp:48,447,451). */
 int sh_expf(sh_ctx* ctx, const float* x, long long n, float* y);
 
+/* Stage timestamps of the last launch of the persistent step kernel, for contexts created with SEOUL_HIP_TRACE=1
+ * in the environment (no counterpart in the reference: the GPU step is one launch, so this is its profile).
+ * out[grid][per_wg] (nullable, cap entries) gets wall-clock ticks: per step, one at the step's start, then four per
+ * stage (start, input arrived, table chunks done, end; 0 where a workgroup had nothing to do); ticks_per_us
+ * converts them. */
+int sh_step_trace(sh_ctx* ctx, long long* out, long long cap, int* per_wg, int* grid, double* ticks_per_us);
+
 /* Synchronise the context's stream (for callers of the _dev entry points). */
 int sh_sync(sh_ctx* ctx);
 

@@ -23,6 +23,7 @@ EXPORTS = [
     "sh_state_pos", "sh_state_set_pos", "sh_step", "sh_step2", "sh_step_batch", "sh_generate", "sh_bench_tables",
     "sh_bench_kernel",
     "sh_q4_create", "sh_q4_free", "sh_q4_rows", "sh_q4_gemv", "sh_q4_gemv_dev", "sh_q4_bench", "sh_expf", "sh_sync",
+    "sh_step_trace",
 ]
 
 
@@ -79,6 +80,7 @@ def load_library(path: str = LIB_PATH):
         "sh_q4_bench": (i, [vp, vp, i, i, i, i, P(d)]),
         "sh_expf": (i, [vp, vp, C.c_longlong, vp]),
         "sh_sync": (i, [vp]),
+        "sh_step_trace": (i, [vp, vp, C.c_longlong, P(i), P(i), P(d)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -252,6 +254,15 @@ class Brain:
         ms, us, by, nl = C.c_double(), C.c_double(), C.c_double(), C.c_int()
         _check(_lib.sh_bench_tables(self.ctx.h, int(ncol), int(reps), C.byref(ms), C.byref(us), C.byref(by), C.byref(nl)))
         return {"ms_per_pass": ms.value, "avg_launch_us": us.value, "bytes_per_pass": by.value, "launches": nl.value}
+
+    def step_trace(self):
+        """Stage timestamps (us from each workgroup's first) of the last step-kernel launch: [grid][per_wg], for
+        contexts made with SEOUL_HIP_TRACE=1."""
+        per, grid, tpu = C.c_int(), C.c_int(), C.c_double()
+        _check(_lib.sh_step_trace(self.ctx.h, None, 0, C.byref(per), C.byref(grid), C.byref(tpu)))
+        out = np.zeros((grid.value, per.value), np.int64)
+        _check(_lib.sh_step_trace(self.ctx.h, _p(out), out.size, C.byref(per), C.byref(grid), C.byref(tpu)))
+        return out, tpu.value
 
     KERNELS = {"ffn_gate_up": 0, "ffn_down": 1, "word_scores": 2}
 

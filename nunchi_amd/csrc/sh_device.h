@@ -117,11 +117,22 @@ __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf_glibc(-
 // (n % 32 == 0): partial P (= accumulator P / 8, lane P % 8) is the FMA chain of x[32t + P]^2 over t; then
 // v_l = (a0_l + a1_l) + (a2_l + a3_l) and the 8-lane sum ((v0+v4) + (v2+v6)) + ((v1+v5) + (v3+v7));
 // returns 1 / sqrtf(s / n + eps) in every lane
-__device__ __forceinline__ float rms_scale_wave(const float* x, int n, float eps) {
+template <class Ptr>
+__device__ __forceinline__ float rms_scale_wave(Ptr x, int n, float eps) {
     const int lane = threadIdx.x & 63;
     float a = 0.0f;
-    if (lane < 32)
-        for (int t = 0; t < n / 32; t++) a = fmaf(x[32 * t + lane], x[32 * t + lane], a);
+    if (lane < 32) {   // operands fetched 8 at a time: one LDS latency per 8 chain steps
+        const int nt = n / 32;
+        int t = 0;
+        for (; t + 8 <= nt; t += 8) {
+            float v[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) v[q] = x[32 * (t + q) + lane];
+#pragma unroll
+            for (int q = 0; q < 8; q++) a = fmaf(v[q], v[q], a);
+        }
+        for (; t < nt; t++) a = fmaf(x[32 * t + lane], x[32 * t + lane], a);
+    }
     const float a1 = __shfl(a, (lane + 8) & 63), a2 = __shfl(a, (lane + 16) & 63), a3 = __shfl(a, (lane + 24) & 63);
     const float v = (a + a1) + (a2 + a3);            // lanes 0..7
     const float r = v + __shfl(v, (lane + 4) & 63);  // lanes 0..3: v_l + v_{l+4}

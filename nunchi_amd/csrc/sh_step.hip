@@ -1,0 +1,889 @@
+// The persistent step kernel (gfx950, wave64): one 512-thread workgroup per compute unit, all co-resident
+// (cooperative launch), running n decode steps of imi's brain (imi/core/seoul.cpp:359-488) without returning to the
+// host.
+//
+// Work split. Every table read is split by 8-row groups across the workgroups (contiguous unit ranges, fixed for the
+// whole launch, so a workgroup always owns the same rows, conv channels and attention heads). Inside a workgroup a
+// chunk of at most 512 (group, block) pairs is computed as in the decode GEMV: phase 1, one pair per thread, loads
+// the 8 rows' 16-byte code blocks and the group's scales and forms the exact integer dots against the int8-cut
+// input; phase 2 runs imi's per-row fp32 chains over the blocks in order (imi/core/tables.cpp:127-143), the
+// acc chains and the cor chains on different waves. The arithmetic is the CPU's, op for op.
+//
+// Synchronisation. A stage's outputs are published as 8-byte records {value, tag} with device-scope stores; the
+// tag is the step's epoch. Consumers load the records with device-scope loads and wait until every tag they need
+// is current: no grid barrier, no fences, and the wait is one memory round trip after the last producer's store.
+// Buffers alternate by epoch parity, so a record is never overwritten while a slower workgroup may still read it.
+// Every wait gives up after `timeout` wall-clock ticks and raises `err`, and every workgroup then leaves.
+//
+// Prefetch. Each thread holds two register sets of one pair's weights (9 x 16 B). Before a chunk is computed, the
+// loads of this workgroup's next chunk are issued into the other set, so the stream of the next stage's weights is
+// in flight while the workgroup waits for that stage's input.
+//
+// Address spaces are explicit: weights, records, caches as global (1), LDS as local (3), the stage table as
+// constant (4). Generic (flat) accesses would count against the LDS wait counter as well and tie every LDS wait to
+// the outstanding weight prefetch.
+#include <hip/hip_runtime.h>
+
+#include "sh_device.h"
+#include "sh_step.h"
+
+namespace sh {
+namespace {
+
+typedef unsigned long long u64;
+#define GLB __attribute__((address_space(1)))
+#define LDS __attribute__((address_space(3)))
+#define CST __attribute__((address_space(4)))
+typedef const sk_stage CST& SR;
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void ll_put(u64* p, float v, unsigned tag) {
+    const u64 r = ((u64)tag << 32) | (u64)__float_as_uint(v);
+    __hip_atomic_store((u64 GLB*)p, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ u64 ll_load(const u64* p) {
+    return __hip_atomic_load((u64 GLB*)const_cast<u64*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// wait for the record at p to carry tag; false after the timeout or when another workgroup gave up
+__device__ __forceinline__ bool ll_wait(const u64* p, unsigned tag, float* v, const sk_params& P) {
+    u64 r = ll_load(p);
+    if ((unsigned)(r >> 32) != tag) {
+        const long long t0 = wall_clock64();
+        for (;;) {
+            __builtin_amdgcn_s_sleep(1);
+            r = ll_load(p);
+            if ((unsigned)(r >> 32) == tag) break;
+            if (wall_clock64() - t0 > P.timeout || __hip_atomic_load((int GLB*)P.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+                __hip_atomic_store((int GLB*)P.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                return false;
+            }
+        }
+    }
+    *v = __uint_as_float((unsigned)r);
+    return true;
+}
+
+// n_m x n_per records, value (m, i) = src[m * src_ld + i] -> dst[m * dst_ld + i]. Each thread loads up to 16 of
+// its records at once and reloads together those whose tag is not yet current, so the wait costs one memory round
+// trip after the last producer's store, not one per record.
+template <class DST>
+__device__ __forceinline__ bool ll_gather(const u64* src, int src_ld, int n_per, int n_m, unsigned tag, DST dst, int dst_ld,
+                                          const sk_params& P) {
+    constexpr int B = 8;
+    const int per_m = (n_per + SK_THREADS - 1) / SK_THREADS;   // records of one conversation per thread
+    const int n_tot = n_m * per_m;                              // this thread's record slots
+    for (int q0 = 0; q0 < n_tot; q0 += B) {
+        u64 r[B];
+        int off[B];   // record offset from src, or -1
+#pragma unroll
+        for (int q = 0; q < B; q++) {
+            const int k = q0 + q, m = k / per_m, i = (k - m * per_m) * SK_THREADS + (int)threadIdx.x;
+            off[q] = (k < n_tot && i < n_per) ? m * src_ld + i : -1;
+            r[q] = off[q] >= 0 ? ll_load(src + off[q]) : ((u64)tag << 32);
+        }
+        long long t0 = 0;
+        for (;;) {
+            bool all = true;
+#pragma unroll
+            for (int q = 0; q < B; q++) all &= (unsigned)(r[q] >> 32) == tag;
+            if (all) break;
+            if (t0 == 0) t0 = wall_clock64();
+            if (wall_clock64() - t0 > P.timeout || __hip_atomic_load((int GLB*)P.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+                __hip_atomic_store((int GLB*)P.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                return false;
+            }
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int q = 0; q < B; q++)
+                if ((unsigned)(r[q] >> 32) != tag) r[q] = ll_load(src + off[q]);
+        }
+#pragma unroll
+        for (int q = 0; q < B; q++)
+            if (off[q] >= 0) {
+                const int m = off[q] / src_ld, i = off[q] - m * src_ld;
+                dst[m * dst_ld + i] = __uint_as_float((unsigned)r[q]);
+            }
+    }
+    return true;
+}
+
+// ---------------------------------------------------------------- LDS map
+__device__ __forceinline__ char LDS* lds_base() {
+    extern __shared__ __align__(16) char smem_dyn[];
+    return (char LDS*)smem_dyn;
+}
+__device__ __forceinline__ float LDS* l_x() { return (float LDS*)(lds_base() + SK_OFF_X); }      // [2][2048]
+__device__ __forceinline__ float LDS* l_y() { return (float LDS*)(lds_base() + SK_OFF_Y); }      // [2][2048]
+__device__ __forceinline__ int LDS* l_xq() { return (int LDS*)(lds_base() + SK_OFF_XQ); }        // [2][2048] int8 x 4
+__device__ __forceinline__ float LDS* l_dx() { return (float LDS*)(lds_base() + SK_OFF_DX); }    // [2][256]
+__device__ __forceinline__ float LDS* l_s() { return (float LDS*)(lds_base() + SK_OFF_S); }      // [2][256]
+__device__ __forceinline__ f32x2 LDS* l_ops() { return (f32x2 LDS*)(lds_base() + SK_OFF_OPS); }   // [nb][C + 1]
+__device__ __forceinline__ float LDS* l_stg() { return (float LDS*)(lds_base() + SK_OFF_OPS); }  // [2][8192] staging
+__device__ __forceinline__ float LDS* l_dd() { return (float LDS*)(lds_base() + SK_OFF_DD); }    // [nb][rows + 1]
+__device__ __forceinline__ float LDS* l_cor() { return (float LDS*)(lds_base() + SK_OFF_COR); }  // [256]
+__device__ __forceinline__ float LDS* l_out() { return (float LDS*)(lds_base() + SK_OFF_OUT); }  // [256]
+__device__ __forceinline__ float LDS* l_redv() { return (float LDS*)(lds_base() + SK_OFF_RED); } // [512]
+__device__ __forceinline__ int LDS* l_redi() { return (int LDS*)(lds_base() + SK_OFF_RED + 2048); }
+__device__ __forceinline__ float LDS* l_misc() { return (float LDS*)(lds_base() + SK_OFF_MISC); } // [32]
+__device__ __forceinline__ int LDS* l_misci() { return (int LDS*)(lds_base() + SK_OFF_MISC + 128); }
+__device__ __forceinline__ float LDS* l_att() { return (float LDS*)(lds_base() + SK_OFF_OPS); }  // attention's share
+
+// ---------------------------------------------------------------- work split
+struct wg_range {
+    int u0, n, cu, nch;
+};
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4 LDS* l_rng() { return (i32x4 LDS*)(lds_base() + SK_OFF_RNG); }
+
+// this workgroup's contiguous units of stage S and their chunking (units per chunk cu, chunks nch); computed once
+// per launch into LDS, read from there afterwards
+template <int M>
+__device__ __forceinline__ wg_range compute_range(SR S, int b, int G) {
+    wg_range r;
+    const unsigned U = (unsigned)S.units;
+    r.u0 = (int)((U * (unsigned)b) / (unsigned)G);
+    r.n = (int)((U * (unsigned)(b + 1)) / (unsigned)G) - r.u0;
+    const int nb = S.W.nb > 0 ? S.W.nb : 1;
+    const int cmax = min(256, SK_OPS_BYTES / (8 * nb) - 1);
+    const int gmax = min(SK_THREADS / nb, cmax / (8 * M));
+    r.cu = max(1, gmax / max(S.ug, 1));
+    r.nch = S.kind == SK_ATTN ? 0 : (r.n + r.cu - 1) / r.cu;
+    return r;
+}
+__device__ __forceinline__ wg_range range_at(int s) {
+    const i32x4 v = l_rng()[s];
+    return wg_range{v.x, v.y, v.z, v.w};
+}
+
+__device__ __forceinline__ SR stage_at(const sk_params& P, int k) { return ((const sk_stage CST*)P.stages)[k]; }
+
+__device__ __forceinline__ bool has_gemv(const sk_params& P, SR S, int step) {
+    return S.kind == SK_GEMV || (S.kind == SK_VOCAB && step >= P.logits_from);
+}
+
+// (step, s, c) -> the next chunk this workgroup computes; false when there is none
+template <int M>
+__device__ __forceinline__ bool next_chunk(const sk_params& P, int b, int G, int& step, int& s, int& c) {
+    c++;
+    for (;;) {
+        if (s < P.n_stages) {
+            SR S = stage_at(P, s);
+            if (has_gemv(P, S, step) && c < range_at(s).nch) return true;
+        }
+        s++;
+        c = 0;
+        if (s >= P.n_stages) {
+            s = 0;
+            if (++step >= P.n_steps) return false;
+        }
+    }
+}
+
+template <int M>
+__device__ __forceinline__ void issue(const sk_params& P, int b, int G, int s, int c, u32x4 (&w)[9]) {
+    SR S = stage_at(P, s);
+    const wg_range r = range_at(s);
+    const int nu = min(r.cu, r.n - c * r.cu);
+    const int g0 = (r.u0 + c * r.cu) * S.ug, ng = nu * S.ug, nb = S.W.nb;
+    // every thread loads (threads past the chunk re-read its first pair), so the register set is written on every
+    // path and the compiler's wait counting stays exact
+    const int t = threadIdx.x < ng * nb ? threadIdx.x : 0;
+    const int gi = t / nb, j = t - gi * nb, g = g0 + gi;
+    const u32x4 GLB* codes = (const u32x4 GLB*)S.W.codes;
+#pragma unroll
+    for (int r8 = 0; r8 < 8; r8++) w[r8] = __builtin_nontemporal_load(codes + (size_t)(8 * g + r8) * nb + j);
+    w[8] = __builtin_nontemporal_load((const u32x4 GLB*)S.W.scales + (size_t)g * nb + j);
+}
+
+// stage timestamps: per step, slot 0 = step start, then per stage 4 slots: prologue start, input arrived,
+// chunks done, stage done
+__device__ __forceinline__ void trace_at(const sk_params& P, int b, int k) {
+    if (P.trace && threadIdx.x == 0 && k >= 0 && k < P.n_trace) ((long long GLB*)P.trace)[(size_t)b * P.n_trace + k] = wall_clock64();
+}
+__device__ __forceinline__ int tslot(const sk_params& P, int step, int s, int k) { return step * (1 + 4 * P.n_stages) + (s < 0 ? 0 : 1 + 4 * s + k); }
+
+// ---------------------------------------------------------------- prologues
+// h = x * sc * w_pre per 32-column block (imi_norm_mul, imi/core/vec.h:36-39), optionally written out (hid0/hid1:
+// the conversations' hidden rows, or null), then cut to int8 (imi_q8::from, imi/core/tables.cpp:100-109)
+template <int M>
+__device__ __forceinline__ void load_w_pre(const float* w_pre, int E, float (&wv)[32]) {
+    const int nbE = E / 32, t = threadIdx.x;
+    const int j = t < M * nbE ? t % nbE : 0;
+    const f32x4 GLB* w = (const f32x4 GLB*)(w_pre + 32 * j);
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+        const f32x4 a = w[q];
+        wv[4 * q] = a.x; wv[4 * q + 1] = a.y; wv[4 * q + 2] = a.z; wv[4 * q + 3] = a.w;
+    }
+}
+
+template <int M>
+__device__ __forceinline__ void norm_cut(const float (&wv)[32], int E, float* hid0, float* hid1, bool cut) {
+    const int nbE = E / 32;
+    const int t = threadIdx.x;
+    if (t < M * nbE) {
+        const int m = t / nbE, j = t - m * nbE;
+        const float sc = l_misc()[2 + m];
+        const float LDS* x = l_x() + m * 2048 + 32 * j;
+        float h[32];
+#pragma unroll
+        for (int k = 0; k < 32; k++) h[k] = x[k] * sc * wv[k];
+        float* hid = m == 0 ? hid0 : hid1;
+        if (hid) {
+            f32x4 GLB* o = (f32x4 GLB*)(hid + 32 * j);
+#pragma unroll
+            for (int k = 0; k < 8; k++) o[k] = f32x4{h[4 * k], h[4 * k + 1], h[4 * k + 2], h[4 * k + 3]};
+        }
+        if (cut) {
+            int q8[8], sum;
+            const float d = cut32(h, q8, &sum, false);
+            int LDS* xq = l_xq() + m * 2048 + 8 * j;
+#pragma unroll
+            for (int w8 = 0; w8 < 8; w8++) xq[w8] = q8[w8];
+            l_dx()[m * 256 + j] = d;
+            l_s()[m * 256 + j] = d * (float)sum;
+        }
+    }
+    __syncthreads();
+}
+
+// x += norm(y) * w_post (imi_norm_mul_add, imi/core/vec.h:41-44); then h = norm(x) * w_pre and its cut
+template <int M>
+__device__ __forceinline__ bool pro_resid(const sk_params& P, SR S, unsigned tag, int par, float* hid0, float* hid1, bool cut, int tr) {
+    const int E = P.E, t = threadIdx.x, wv = t >> 6;
+    // the post-norm weight is read before the wait, so it arrives with the input
+    float wpost[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int i = t + k * SK_THREADS;
+        wpost[k] = i < E ? ((const float GLB*)S.w_post)[i] : 0.0f;
+    }
+    const bool ok = ll_gather(S.in + (size_t)par * 2 * S.n_in, S.n_in, E, M, tag, l_y(), 2048, P);
+    if (__syncthreads_or(!ok)) return false;
+    trace_at(P, blockIdx.x, tr);
+    if (wv < M) {
+        const float sc = rms_scale_wave((const float LDS*)(l_y() + wv * 2048), E, P.eps);
+        if ((t & 63) == 0) l_misc()[wv] = sc;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < M; m++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int i = t + k * SK_THREADS;
+            if (i < E) {
+                float LDS* x = l_x() + m * 2048 + i;
+                *x = fmaf(l_y()[m * 2048 + i] * l_misc()[m], wpost[k], *x);
+            }
+        }
+    float wpre[32];   // in flight during the second norm's chain
+    load_w_pre<M>(S.w_pre, E, wpre);
+    __syncthreads();
+    if (wv < M) {
+        const float sc = rms_scale_wave((const float LDS*)(l_x() + wv * 2048), E, P.eps);
+        if ((t & 63) == 0) l_misc()[2 + wv] = sc;
+    }
+    __syncthreads();
+    norm_cut<M>(wpre, E, hid0, hid1, cut);
+    return true;
+}
+
+template <int M>
+__device__ __forceinline__ void pro_first(const sk_params& P, SR S) {
+    const int t = threadIdx.x, wv = t >> 6;
+    float wpre[32];
+    load_w_pre<M>(S.w_pre, P.E, wpre);
+    if (wv < M) {
+        const float sc = rms_scale_wave((const float LDS*)(l_x() + wv * 2048), P.E, P.eps);
+        if ((t & 63) == 0) l_misc()[2 + wv] = sc;
+    }
+    __syncthreads();
+    norm_cut<M>(wpre, P.E, nullptr, nullptr, true);
+}
+
+// the previous table's float output, cut to int8 per 32 (imi/core/vec.h:47-75)
+template <int M>
+__device__ __forceinline__ bool pro_cut(const sk_params& P, SR S, unsigned tag, int par, int tr) {
+    const int K = S.n_in, t = threadIdx.x;
+    const bool ok = ll_gather(S.in + (size_t)par * 2 * S.n_in, S.n_in, K, M, tag, l_stg(), 8192, P);
+    if (__syncthreads_or(!ok)) return false;
+    trace_at(P, blockIdx.x, tr);
+    const int nbk = K / 32;
+    for (int k = t; k < M * nbk; k += SK_THREADS) {
+        const int m = k / nbk, j = k - m * nbk;
+        float v[32];
+        const f32x4 LDS* src = (const f32x4 LDS*)(l_stg() + m * 8192 + 32 * j);
+#pragma unroll
+        for (int q = 0; q < 8; q++) { const f32x4 a = src[q]; v[4 * q] = a.x; v[4 * q + 1] = a.y; v[4 * q + 2] = a.z; v[4 * q + 3] = a.w; }
+        int q8[8], sum;
+        const float d = cut32(v, q8, &sum, false);
+        int LDS* xq = l_xq() + m * 2048 + 8 * j;
+#pragma unroll
+        for (int w8 = 0; w8 < 8; w8++) xq[w8] = q8[w8];
+        l_dx()[m * 256 + j] = d;
+        l_s()[m * 256 + j] = d * (float)sum;
+    }
+    __syncthreads();
+    return true;
+}
+
+// ---------------------------------------------------------------- GEMV chunk
+// phase 1: thread = (group gi, block j); exact integer dots of the 8 rows against each input's cut block, and the
+// chain operands {float(isum), d * dx} and d to LDS
+template <int M>
+__device__ __forceinline__ void phase1(const u32x4 (&w)[9], int ng, int nb, int rows, int C) {
+    const int t = threadIdx.x;
+    if (t < ng * nb) {
+        const int gi = t / nb, j = t - gi * nb;
+        float d[8];
+        const unsigned sw[4] = {w[8].x, w[8].y, w[8].z, w[8].w};
+#pragma unroll
+        for (int r = 0; r < 8; r++) d[r] = h2f((uint16_t)((r & 1) ? (sw[r >> 1] >> 16) : (sw[r >> 1] & 0xFFFFu)));
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            int xq[8];
+            const u32x4 LDS* xs = (const u32x4 LDS*)(l_xq() + m * 2048 + 8 * j);
+            const u32x4 a = xs[0], c = xs[1];
+            xq[0] = (int)a.x; xq[1] = (int)a.y; xq[2] = (int)a.z; xq[3] = (int)a.w;
+            xq[4] = (int)c.x; xq[5] = (int)c.y; xq[6] = (int)c.z; xq[7] = (int)c.w;
+            const float dx = l_dx()[m * 256 + j];
+            f32x2 LDS* o = l_ops() + j * (C + 1) + m * rows + 8 * gi;
+#pragma unroll
+            for (int r = 0; r < 8; r++) o[r] = f32x2{(float)q4_block_dot(w[r], xq), d[r] * dx};
+        }
+        float LDS* dd = l_dd() + j * (rows + 1) + 8 * gi;
+#pragma unroll
+        for (int r = 0; r < 8; r++) dd[r] = d[r];
+    }
+}
+
+// phase 2 (chains) and the epilogue of one chunk
+// conv taps and memory of this thread's channel, loaded before the chunk's prefetch is issued (a global load in
+// the epilogue would wait for that prefetch: loads complete in order)
+struct conv_pre {
+    float w[SK_CONV_MAX + 1], st[SK_CONV_MAX];
+};
+
+template <int M>
+__device__ __forceinline__ void conv_load(const sk_params& P, SR S, int g0, int C, int rows, conv_pre& cp) {
+    const int t = threadIdx.x;
+    if (S.epi != SKE_CONV || t >= C) return;
+    const int m = t / rows, rr = t - m * rows, k = rr % 24;
+    if (k >= 8) return;
+    const int E = P.E, dc = P.d_conv, e = 8 * (g0 / 3 + rr / 24) + k;
+    const float GLB* st = (const float GLB*)((m == 0 ? P.cv[0].conv : P.cv[M - 1].conv) + (size_t)S.conv_layer * dc * E);
+    const float GLB* cw = (const float GLB*)S.conv_w;
+#pragma unroll
+    for (int q = 0; q <= SK_CONV_MAX; q++)
+        if (q <= dc) cp.w[q] = cw[(size_t)q * E + e];
+#pragma unroll
+    for (int q = 0; q < SK_CONV_MAX; q++)
+        if (q < dc) cp.st[q] = st[(size_t)q * E + e];
+}
+
+template <int M>
+__device__ __forceinline__ void phase2_epilogue(const sk_params& P, SR S, int g0, int C, int rows, unsigned tag, int par,
+                                                float (&bv)[M], int (&bi)[M], const conv_pre& cp) {
+    const int t = threadIdx.x, nb = S.W.nb;
+    float acc = 0.0f;
+    // the chains read their operands 8 blocks at a time, so the LDS latency is paid once per 8 steps
+    if (t < C) {
+        const f32x2 LDS* o = l_ops() + t;
+        const int st = C + 1;
+        int j = 0;
+        for (; j + 8 <= nb; j += 8) {
+            f32x2 v[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) v[q] = o[(j + q) * st];
+#pragma unroll
+            for (int q = 0; q < 8; q++) acc = fmaf(v[q].x, v[q].y, acc);
+        }
+        for (; j < nb; j++) {
+            const f32x2 v = o[j * st];
+            acc = fmaf(v.x, v.y, acc);
+        }
+    } else if (t >= 256 && t < 256 + C) {
+        const int c = t - 256, m = c / rows, r = c - m * rows;
+        const float LDS* dd = l_dd() + r;
+        const float LDS* sv = l_s() + m * 256;
+        const int st = rows + 1;
+        float cor = 0.0f;
+        int j = 0;
+        for (; j + 8 <= nb; j += 8) {
+            float a[8], e[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) { a[q] = dd[(j + q) * st]; e[q] = sv[j + q]; }
+#pragma unroll
+            for (int q = 0; q < 8; q++) cor = fmaf(a[q], e[q], cor);
+        }
+        for (; j < nb; j++) cor = fmaf(dd[j * st], sv[j], cor);
+        l_cor()[c] = cor;
+    }
+    __syncthreads();
+    float outv = 0.0f;
+    if (t < C) {
+        outv = fmaf(-8.0f, l_cor()[t], acc);
+        l_out()[t] = outv;
+    }
+    __syncthreads();
+    if (t >= C) return;
+    const int m = t / rows, rr = t - m * rows;
+    u64* out = S.out ? S.out + (size_t)(par * 2 + m) * S.n_out : nullptr;
+    if (S.epi == SKE_STORE) {
+        ll_put(out + 8 * g0 + rr, outv, tag);
+    } else if (S.epi == SKE_SWIGLU) {   // (gate group, up group) of 8 FFN channels (imi/core/seoul.cpp:380-394)
+        const int k = rr & 15;
+        if (k < 8) ll_put(out + 8 * (g0 / 2 + rr / 16) + k, silu(outv) * l_out()[t + 8], tag);
+    } else if (S.epi == SKE_CONV) {     // (b, c, x) groups of 8 channels (imi/core/seoul.cpp:407-423)
+        const int k = rr % 24;
+        if (k < 8) {
+            const int E = P.E, dc = P.d_conv, e = 8 * (g0 / 3 + rr / 24) + k;
+            const float cc = l_out()[t + 8], xx = l_out()[t + 16];
+            float GLB* st = (float GLB*)((m == 0 ? P.cv[0].conv : P.cv[M - 1].conv) + (size_t)S.conv_layer * dc * E);
+            const float bx = outv * xx;
+            float wdc = cp.w[0];
+#pragma unroll
+            for (int q = 1; q <= SK_CONV_MAX; q++)
+                if (q == dc) wdc = cp.w[q];
+            float uu = outv * xx * wdc;
+#pragma unroll
+            for (int q = 0; q < SK_CONV_MAX; q++)
+                if (q < dc) uu = fmaf(cp.st[q], cp.w[q], uu);
+            uu *= cc;
+#pragma unroll
+            for (int q = 0; q + 1 < SK_CONV_MAX; q++)
+                if (q + 1 < dc) st[(size_t)q * E + e] = cp.st[q + 1];
+            st[(size_t)(dc - 1) * E + e] = bx;
+            ll_put(out + e, uu, tag);
+        }
+    } else {   // SKE_LOGITS
+        const int row = 8 * g0 + rr;
+        float* lg = m == 0 ? P.cv[0].logits : P.cv[M - 1].logits;
+        if (lg) ((float GLB*)lg)[row] = outv;
+#pragma unroll
+        for (int mm = 0; mm < M; mm++)
+            if (mm == m && (outv > bv[mm] || (outv == bv[mm] && row < bi[mm]))) { bv[mm] = outv; bi[mm] = row; }
+    }
+}
+
+// first index of the maximum over the block: each thread offers (v, i); every thread gets the winner
+__device__ __forceinline__ void block_argmax(float v, int i, float* out_v, int* out_i) {
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(v, o);
+        const int oi = __shfl_xor(i, o);
+        if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+    }
+    __syncthreads();
+    if (lane == 0) { l_redv()[wv] = v; l_redi()[wv] = i; }
+    __syncthreads();
+    v = l_redv()[0];
+    i = l_redi()[0];
+    for (int k = 1; k < SK_THREADS / 64; k++) {
+        const float ov = l_redv()[k];
+        const int oi = l_redi()[k];
+        if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+    }
+    *out_v = v;
+    *out_i = i;
+    __syncthreads();
+}
+
+// the word chosen by a step: first index of the maximum over the workgroups' partials of conversation m
+__device__ __forceinline__ bool reduce_partials(const sk_params& P, unsigned tag, int G, int m, int* best) {
+    const int par = tag & 1, t = threadIdx.x;
+    float v = -INFINITY;
+    int i = 0x7fffffff;
+    bool ok = true;
+    if (t < G) {
+        const u64* pv = P.part + (((size_t)par * 2 + m) * 2) * G;
+        u64 rv = ll_load(pv + t), ri = ll_load(pv + G + t);
+        if ((unsigned)(rv >> 32) != tag) { float x; ok = ll_wait(pv + t, tag, &x, P); rv = __float_as_uint(x); }
+        if (ok && (unsigned)(ri >> 32) != tag) { float x; ok = ll_wait(pv + G + t, tag, &x, P); ri = __float_as_uint(x); }
+        v = __uint_as_float((unsigned)rv);
+        i = (int)(unsigned)ri;
+    }
+    if (__syncthreads_or(!ok)) return false;
+    float bvv;
+    block_argmax(v, i, &bvv, best);
+    return true;
+}
+
+// ---------------------------------------------------------------- attention (imi/core/seoul.cpp:424-461)
+// workgroup (kv head g, conversation m): k = rope(norm(k) * k_norm), v to the fp16 cache at pos; per query head of
+// the group: q = rope(norm(q) * q_norm), scores = dot_h(q, K_t) / sqrt(D), softmax with the max subtracted, glibc's
+// expf and a double sum in position order, o = sum_t fma(e_t * inv, V_t, o) in order, times the sigmoid head gate
+template <int D>
+__device__ __forceinline__ bool attention(const sk_params& P, SR S, int g, int m, int pos, unsigned tag, int par) {
+    constexpr int half = D / 2;
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int grp = P.n_head / P.n_kv, Hq = P.n_head * D, kvd = P.n_kv * D, n_ctx = P.n_ctx;
+    const int s0 = (S.swa && P.n_swa > 0) ? max(0, pos - P.n_swa + 1) : 0, nk = pos - s0 + 1;
+    uint16_t GLB* kc = (uint16_t GLB*)(P.cv[m].kc + ((size_t)S.layer_ai * P.n_kv + g) * n_ctx * D);
+    uint16_t GLB* vc = (uint16_t GLB*)(P.cv[m].vc + ((size_t)S.layer_ai * P.n_kv + g) * n_ctx * D);
+    float LDS* row = l_att();                    // [grp*D | k D | v D | gates grp]
+    float LDS* q_s = row + 512;                  // [grp][D]
+    float LDS* scratch = q_s + 8 * D;            // [9][D]
+    float LDS* inv_s = scratch + 9 * D;          // [8]
+    float LDS* sc = inv_s + 8;                   // [grp][n_ctx]
+    const int n_need = grp * D + 2 * D + grp;
+    bool ok = true;
+    if (t < n_need) {
+        int idx;
+        if (t < grp * D) idx = g * grp * D + t;
+        else if (t < grp * D + D) idx = Hq + g * D + (t - grp * D);
+        else if (t < grp * D + 2 * D) idx = Hq + kvd + g * D + (t - grp * D - D);
+        else idx = Hq + 2 * kvd + g * grp + (t - grp * D - 2 * D);
+        float v;
+        ok = ll_wait(S.in + (size_t)(par * 2 + m) * S.n_in + idx, tag, &v, P);
+        row[t] = v;
+    }
+    if (__syncthreads_or(!ok)) return false;
+    const float GLB* cs = (const float GLB*)S.rope_cs + (size_t)pos * D;   // (cos, sin) pairs
+    // norm + NEOX rope of one head vector, one wave (imi/core/seoul.cpp:19-28; angles from the host's table)
+    for (int hh = wv; hh <= grp; hh += SK_THREADS / 64) {
+        const bool is_k = hh == grp;
+        const float LDS* src = is_k ? row + grp * D : row + hh * D;
+        const float GLB* w = (const float GLB*)(is_k ? S.k_norm : S.q_norm);
+        float LDS* dst = is_k ? scratch + 8 * D : q_s + hh * D;
+        float LDS* st = scratch + wv * D;
+        const float x = lane < D ? src[lane] : 0.0f;
+        if (lane < D) st[lane] = x;
+        __builtin_amdgcn_wave_barrier();
+        const float s = rms_scale_wave((const float LDS*)st, D, P.eps);
+        const float n = lane < D ? x * s * w[lane] : 0.0f;
+        const float other = __shfl(n, lane < half ? lane + half : lane - half);
+        if (lane < D) {
+            const int ci = lane < half ? lane : lane - half;
+            const float co = cs[2 * ci], si = cs[2 * ci + 1];
+            const float r = lane < half ? fmaf(n, co, -(other * si)) : fmaf(other, si, n * co);
+            dst[lane] = r;
+            if (is_k) {
+                kc[(size_t)pos * D + lane] = f2h(r);
+                vc[(size_t)pos * D + lane] = f2h(row[grp * D + D + lane]);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    __syncthreads();
+    const float scale = 1.0f / sqrtf((float)D);
+    for (int q = t; q < nk; q += SK_THREADS) {
+        const u32x4 GLB* kt = (const u32x4 GLB*)(kc + (size_t)(s0 + q) * D);
+        unsigned kw[D / 2];   // the key row as fp16 pairs, converted per use (keeps the registers low)
+#pragma unroll
+        for (int i0 = 0; i0 < D / 8; i0++) {
+            const u32x4 w4 = kt[i0];
+            kw[4 * i0] = w4.x; kw[4 * i0 + 1] = w4.y; kw[4 * i0 + 2] = w4.z; kw[4 * i0 + 3] = w4.w;
+        }
+        for (int hh = 0; hh < grp; hh++) {
+            // dot_h (imi/core/seoul.cpp:29-39): 8 FMA chains over columns i % 8, then the 8-lane horizontal sum
+            const float LDS* qh = q_s + hh * D;
+            float a[8];
+#pragma unroll
+            for (int l = 0; l < 8; l++) a[l] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < D; i += 8)
+#pragma unroll
+                for (int l = 0; l < 8; l++) a[l] = fmaf(qh[i + l], h2f((uint16_t)(kw[(i + l) >> 1] >> (16 * (l & 1)))), a[l]);
+            sc[hh * n_ctx + q] = (((a[0] + a[4]) + (a[2] + a[6])) + ((a[1] + a[5]) + (a[3] + a[7]))) * scale;
+        }
+    }
+    __syncthreads();
+    for (int hh = wv; hh < grp; hh += SK_THREADS / 64) {
+        float LDS* s = sc + hh * n_ctx;
+        float mx = -INFINITY;
+        for (int q = lane; q < nk; q += 64) mx = fmaxf(mx, s[q]);
+        mx = wave_max(mx);
+        for (int q = lane; q < nk; q += 64) s[q] = expf_glibc(s[q] - mx);
+        __builtin_amdgcn_wave_barrier();
+        if (lane == 0) {
+            double sum = 0.0;
+            int q = 0;
+            for (; q + 8 <= nk; q += 8) {
+                float v[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) v[u] = s[q + u];
+#pragma unroll
+                for (int u = 0; u < 8; u++) sum += (double)v[u];
+            }
+            for (; q < nk; q++) sum += (double)s[q];
+            inv_s[hh] = (float)(1.0 / sum);
+        }
+    }
+    __syncthreads();
+    // o = sum_t fma(e_t * inv, V_t, o): the window's value rows pass through LDS in tiles (one coalesced load per
+    // tile instead of a dependent global load per position), the chain itself stays in position order
+    float LDS* vt = sc + grp * n_ctx;
+    const int tv = min(256, ((SK_ATTN_BYTES / 4 - (int)(vt - row)) / D) & ~7);
+    const int k = t;                               // thread = (query head hh, dimension i); grp * D <= 512
+    const int hh = k / D, i = k - hh * D;
+    const bool on = k < grp * D;
+    const float inv = on ? inv_s[hh] : 0.0f;
+    const float LDS* sh = sc + (on ? hh : 0) * n_ctx;
+    float o = 0.0f;
+    for (int q0 = 0; q0 < nk; q0 += tv) {
+        const int nt = min(tv, nk - q0);
+        const u32x4 GLB* src = (const u32x4 GLB*)(vc + (size_t)(s0 + q0) * D);
+        for (int e = t; e < nt * D / 8; e += SK_THREADS) {
+            const u32x4 w4 = src[e];
+            const unsigned hw[4] = {w4.x, w4.y, w4.z, w4.w};
+            float LDS* dst = vt + 8 * e;
+#pragma unroll
+            for (int h = 0; h < 8; h++) dst[h] = h2f((uint16_t)(hw[h >> 1] >> (16 * (h & 1))));
+        }
+        __syncthreads();
+        if (on) {
+            int q = 0;
+            for (; q + 8 <= nt; q += 8) {
+                float e[8], v[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) { e[u] = sh[q0 + q + u]; v[u] = vt[(q + u) * D + i]; }
+#pragma unroll
+                for (int u = 0; u < 8; u++) o = fmaf(e[u] * inv, v[u], o);
+            }
+            for (; q < nt; q++) o = fmaf(sh[q0 + q] * inv, vt[q * D + i], o);
+        }
+        __syncthreads();
+    }
+    if (on) {
+        const float gate = 1.0f / (1.0f + expf_glibc(-row[grp * D + 2 * D + hh]));
+        u64* out = S.out + (size_t)(par * 2 + m) * S.n_out;
+        ll_put(out + (g * grp + hh) * D + i, o * gate, tag);
+    }
+    __syncthreads();
+    return true;
+}
+
+
+
+// ---------------------------------------------------------------- the walk over one workgroup's work
+// Per workgroup, a launch is a sequence of chunks with other work in between (embedding, prologues, attention,
+// the end of the word scores). `events` runs that work up to the next chunk; `chunk` issues the loads of the
+// chunk after it into the other register set and computes this one. The kernel alternates the two sets
+// explicitly, so neither is copied and the prefetch stays in flight.
+struct walk_state {
+    int step, s, c, nch;
+    bool embedded, pro_done;
+};
+
+__device__ __forceinline__ void next_stage(const sk_params& P, walk_state& W) {
+    W.s++;
+    W.c = 0;
+    W.pro_done = false;
+    if (W.s == P.n_stages) {
+        W.s = 0;
+        W.step++;
+        W.embedded = false;
+    }
+}
+
+// the step's input rows (imi/core/seoul.cpp:363-364): word-table row of the token, or the given vector
+template <int M>
+__device__ __forceinline__ bool embed(const sk_params& P, walk_state& W, int b, int G) {
+    const unsigned tag = P.epoch0 + (unsigned)W.step;
+    const int t = threadIdx.x;
+    trace_at(P, b, tslot(P, W.step, -1, 0));
+    int tok0 = 0, tok1 = 0;
+    if (P.greedy && W.step > 0) {
+        if (b == 0) {
+            tok0 = l_misci()[0];
+            tok1 = l_misci()[1];
+        } else {
+            if (!reduce_partials(P, tag - 1, G, 0, &tok0)) return false;
+            if (M == 2 && !reduce_partials(P, tag - 1, G, 1, &tok1)) return false;
+        }
+    } else if (P.greedy) {
+        tok0 = P.cv[0].first_token;
+        tok1 = P.cv[M - 1].first_token;
+    } else {
+        tok0 = ((const int GLB*)P.cv[0].tokens)[W.step];
+        tok1 = ((const int GLB*)P.cv[M - 1].tokens)[W.step];
+    }
+    if (tok0 >= P.V) tok0 = 0;   // no maximum (all scores NaN): row 0, never out of the table
+    if (tok1 >= P.V) tok1 = 0;
+    const int nbE = P.E / 32;
+    if (t < M * nbE) {
+        const int m = t / nbE, j = t - m * nbE;
+        const int tok = m == 0 ? tok0 : tok1;
+        float v[32];
+        if (tok >= 0) {
+            const u32x4 cw = ((const u32x4 GLB*)P.vocab.codes)[(size_t)tok * P.vocab.nb + j];
+            const uint16_t dh = ((const uint16_t GLB*)P.vocab.scales)[((size_t)(tok >> 3) * P.vocab.nb + j) * 8 + (tok & 7)];
+            const float d = h2f(dh);
+            const unsigned w4[4] = {cw.x, cw.y, cw.z, cw.w};
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const unsigned byte = (w4[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+                v[i] = (float)((int)(byte & 15u) - 8) * d;
+                v[16 + i] = (float)((int)(byte >> 4) - 8) * d;
+            }
+        } else {
+            const float* eb = m == 0 ? P.cv[0].embd : P.cv[M - 1].embd;
+            const f32x4 GLB* e = (const f32x4 GLB*)(eb + (size_t)W.step * P.E + 32 * j);
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const f32x4 a = e[q];
+                v[4 * q] = a.x; v[4 * q + 1] = a.y; v[4 * q + 2] = a.z; v[4 * q + 3] = a.w;
+            }
+        }
+        float LDS* x = l_x() + m * 2048 + 32 * j;
+#pragma unroll
+        for (int i = 0; i < 32; i++) x[i] = v[i];
+    }
+    __syncthreads();
+    return true;
+}
+
+// runs everything up to the next chunk; false when the launch is done (or a wait failed)
+template <int M>
+__device__ __forceinline__ bool events(const sk_params& P, walk_state& W, int b, int G, float (&bv)[M], int (&bi)[M]) {
+    for (;;) {
+        if (W.step >= P.n_steps) return false;
+        const unsigned tag = P.epoch0 + (unsigned)W.step;
+        const int par = tag & 1;
+        if (!W.embedded) {
+            if (!embed<M>(P, W, b, G)) return false;
+            W.embedded = true;
+#pragma unroll
+            for (int m = 0; m < M; m++) { bv[m] = -INFINITY; bi[m] = 0x7fffffff; }
+        }
+        SR S = stage_at(P, W.s);
+        if (!W.pro_done) {
+            trace_at(P, b, tslot(P, W.step, W.s, 0));
+            if (S.kind == SK_ATTN) {
+                if (b < P.n_kv * M) {
+                    const int g = b % P.n_kv, m = b / P.n_kv;
+                    const int pos = P.cv[m].pos + W.step;
+                    const bool ok = P.D == 64 ? attention<64>(P, S, g, m, pos, tag, par) : attention<32>(P, S, g, m, pos, tag, par);
+                    if (!ok) return false;
+                }
+                trace_at(P, b, tslot(P, W.step, W.s, 3));
+                next_stage(P, W);
+                continue;
+            }
+            float* hid0 = nullptr;
+            float* hid1 = nullptr;
+            if (S.kind == SK_VOCAB && b == 0) {
+                if (P.cv[0].hidden) hid0 = P.cv[0].hidden + (size_t)W.step * P.cv[0].hidden_stride;
+                if (M == 2 && P.cv[1].hidden) hid1 = P.cv[1].hidden + (size_t)W.step * P.cv[1].hidden_stride;
+            }
+            if (S.kind == SK_VOCAB && W.step < P.logits_from) {   // no word scores: the final norm only
+                if (b == 0 && !pro_resid<M>(P, S, tag, par, hid0, hid1, false, tslot(P, W.step, W.s, 1))) return false;
+                trace_at(P, b, tslot(P, W.step, W.s, 3));
+                next_stage(P, W);
+                continue;
+            }
+            W.nch = range_at(W.s).nch;
+            bool ok = true;
+            if (S.pro == SKP_RESID) ok = pro_resid<M>(P, S, tag, par, hid0, hid1, true, tslot(P, W.step, W.s, 1));
+            else if (S.pro == SKP_FIRST) pro_first<M>(P, S);
+            else if (W.nch > 0) ok = pro_cut<M>(P, S, tag, par, tslot(P, W.step, W.s, 1));
+            if (!ok) return false;
+            W.pro_done = true;
+        }
+        if (W.c < W.nch) return true;
+        // the stage is done
+        trace_at(P, b, tslot(P, W.step, W.s, 2));
+        if (S.epi == SKE_LOGITS) {
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                float v;
+                int i;
+                block_argmax(bv[m], bi[m], &v, &i);
+                if (threadIdx.x == 0) {
+                    u64* pv = P.part + (((size_t)par * 2 + m) * 2) * G;
+                    ll_put(pv + b, v, tag);
+                    ll_put(pv + G + b, __int_as_float(i), tag);
+                }
+            }
+            if (b == 0) {
+#pragma unroll
+                for (int m = 0; m < M; m++) {
+                    int best = 0;
+                    if (!reduce_partials(P, tag, G, m, &best)) return false;
+                    if (threadIdx.x == 0) {
+                        l_misci()[m] = best;
+                        int32_t* ids = m == 0 ? P.cv[0].ids : P.cv[M - 1].ids;
+                        if (ids) ((int GLB*)ids)[W.step] = best;
+                    }
+                }
+                __syncthreads();
+            }
+        }
+        trace_at(P, b, tslot(P, W.step, W.s, 3));
+        next_stage(P, W);
+    }
+}
+
+// chunk (step, s, c): issue the next chunk's loads into nxt, compute this one from cur
+template <int M>
+__device__ __forceinline__ void chunk(const sk_params& P, walk_state& W, int b, int G, float (&bv)[M], int (&bi)[M],
+                                      const u32x4 (&cur)[9], u32x4 (&nxt)[9]) {
+    const unsigned tag = P.epoch0 + (unsigned)W.step;
+    const int par = tag & 1;
+    SR S = stage_at(P, W.s);
+    const wg_range r = range_at(W.s);
+    const int nu = min(r.cu, r.n - W.c * r.cu);
+    const int g0 = (r.u0 + W.c * r.cu) * S.ug, ng = nu * S.ug, rows = 8 * ng, C = M * rows;
+    conv_pre cp;
+    conv_load<M>(P, S, g0, C, rows, cp);
+    // the next chunk's loads go out after this chunk's results are published: the issue cost is off the path to
+    // the publish, and the stream overlaps the wait for the next stage's input
+    int qs = W.step, qss = W.s, qc = W.c;
+    if (!next_chunk<M>(P, b, G, qs, qss, qc)) { qss = W.s; qc = W.c; }   // the last chunk: a harmless re-read
+    phase1<M>(cur, ng, S.W.nb, rows, C);
+    __syncthreads();
+    phase2_epilogue<M>(P, S, g0, C, rows, tag, par, bv, bi, cp);
+    issue<M>(P, b, G, qss, qc, nxt);
+    __syncthreads();
+    W.c++;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- the kernel
+template <int M>
+__global__ __launch_bounds__(SK_THREADS, 1) void k_step(sk_params P) {
+    const int b = blockIdx.x, G = gridDim.x;
+    walk_state W{0, 0, 0, 0, false, false};
+    float bv[M];
+    int bi[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) { bv[m] = -INFINITY; bi[m] = 0x7fffffff; }
+    for (int k = threadIdx.x; k < P.n_stages; k += SK_THREADS) {
+        const wg_range r = compute_range<M>(stage_at(P, k), b, G);
+        l_rng()[k] = i32x4{r.u0, r.n, r.cu, r.nch};
+    }
+    __syncthreads();
+    u32x4 wa[9], wb[9];
+    {
+        int st = 0, s = 0, c = -1;
+        if (next_chunk<M>(P, b, G, st, s, c)) issue<M>(P, b, G, s, c, wa);
+    }
+    for (;;) {
+        if (!events<M>(P, W, b, G, bv, bi)) break;
+        chunk<M>(P, W, b, G, bv, bi, wa, wb);
+        if (!events<M>(P, W, b, G, bv, bi)) break;
+        chunk<M>(P, W, b, G, bv, bi, wb, wa);
+    }
+}
+
+hipError_t launch_step_kernel(int M, const sk_params& p, int grid, hipStream_t s) {
+    const void* fn = M == 2 ? (const void*)k_step<2> : (const void*)k_step<1>;
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, SK_LDS_BYTES);
+    if (e != hipSuccess) return e;
+    sk_params copy = p;
+    void* args[] = {&copy};
+    return hipLaunchCooperativeKernel(fn, dim3(grid), dim3(SK_THREADS), args, SK_LDS_BYTES, s);
+}
+
+hipError_t step_kernel_occupancy(int M, int* blocks_per_cu) {
+    const void* fn = M == 2 ? (const void*)k_step<2> : (const void*)k_step<1>;
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, SK_LDS_BYTES);
+    if (e != hipSuccess) return e;
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, fn, SK_THREADS, SK_LDS_BYTES);
+}
+
+}  // namespace sh

@@ -71,5 +71,5 @@ def test_cpp_engine_api_on_gpu(tiny_model, tmp_path):
     for _ in range(7):
         _, lg = eng.step(want[-1])
         want.append(oracle.top(lg))
-    assert ids == want, (ids, want)
+    assert ids == want, (ids, want, out.stderr[-2000:])
     assert "pos 13/1" in out.stdout and "swapped pos 1/13" in out.stdout
