@@ -121,15 +121,30 @@ template <class Ptr>
 __device__ __forceinline__ float rms_scale_wave(Ptr x, int n, float eps) {
     const int lane = threadIdx.x & 63;
     float a = 0.0f;
-    if (lane < 32) {   // operands fetched 8 at a time: one LDS latency per 8 chain steps
+    if (lane < 32) {   // operands fetched 8 at a time, one batch ahead of the chain that consumes them
         const int nt = n / 32;
         int t = 0;
-        for (; t + 8 <= nt; t += 8) {
-            float v[8];
+        if (nt >= 8) {
+            float v0[8], v1[8];
 #pragma unroll
-            for (int q = 0; q < 8; q++) v[q] = x[32 * (t + q) + lane];
+            for (int q = 0; q < 8; q++) v0[q] = x[32 * q + lane];
+            for (; t + 16 <= nt; t += 16) {
 #pragma unroll
-            for (int q = 0; q < 8; q++) a = fmaf(v[q], v[q], a);
+                for (int q = 0; q < 8; q++) v1[q] = x[32 * (t + 8 + q) + lane];
+#pragma unroll
+                for (int q = 0; q < 8; q++) a = fmaf(v0[q], v0[q], a);
+                if (t + 16 + 8 <= nt) {
+#pragma unroll
+                    for (int q = 0; q < 8; q++) v0[q] = x[32 * (t + 16 + q) + lane];
+                }
+#pragma unroll
+                for (int q = 0; q < 8; q++) a = fmaf(v1[q], v1[q], a);
+            }
+            if (t + 8 <= nt) {   // one loaded batch left
+#pragma unroll
+                for (int q = 0; q < 8; q++) a = fmaf(v0[q], v0[q], a);
+                t += 8;
+            }
         }
         for (; t < nt; t++) a = fmaf(x[32 * t + lane], x[32 * t + lane], a);
     }

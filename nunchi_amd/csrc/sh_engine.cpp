@@ -475,11 +475,27 @@ int build_program(sh_ctx* c) {
         if (st.kind == SK_ATTN) continue;
         const int nb = st.W.nb;
         if (nb < 1 || nb > 256 || st.W.rows % (8 * st.ug)) return fail(SH_E_SHAPE, "step kernel: table shape");
-        int cmax = SK_OPS_BYTES / (8 * nb) - 1;
-        cmax = cmax < 256 ? cmax : 256;
-        int gmax = SK_THREADS / nb;
-        gmax = gmax < cmax / 16 ? gmax : cmax / 16;
-        if (gmax < st.ug) return fail(SH_E_SHAPE, "step kernel: a unit does not fit one chunk");
+        if (sk_gmax(nb, 2) < st.ug) return fail(SH_E_SHAPE, "step kernel: a unit does not fit one chunk");
+    }
+
+    // FFN gate|up outputs go out already cut per 32 channels when every workgroup's units (8 channels each) form
+    // whole blocks of 32 in every chunk: 10 records per 32 channels instead of 32 for the down table's input
+    for (auto& w : wires) {
+        sk_stage& prod = P[w.second];
+        sk_stage& cons = P[w.first];
+        if (prod.kind != SK_GEMV || prod.epi != SKE_SWIGLU || cons.pro != SKP_CUT) continue;
+        bool ok = prod.units % (4 * c->sk_grid) == 0;
+        for (int Mi = 1; Mi <= 2 && ok; Mi++) {
+            const int gmax = sk_gmax(prod.W.nb, Mi);
+            const int cu = gmax / prod.ug > 1 ? gmax / prod.ug : 1;
+            const int per_wg = prod.units / c->sk_grid;
+            ok = cu % 4 == 0 || per_wg <= cu;
+        }
+        if (!ok) continue;
+        prod.cut_out = 1;
+        cons.cut_in = 1;
+        out_n[w.second] = (size_t)prod.units * 8 / 32 * 10;
+        prod.n_out = (int)out_n[w.second];
     }
 
     // device memory: stage table, output records, argmax partials, error flag

@@ -28,7 +28,7 @@ constexpr int SK_OFF_XQ = SK_OFF_Y + 16384;        // int8 [2][8192] the cut inp
 constexpr int SK_OFF_DX = SK_OFF_XQ + 16384;       // float [2][256] cut scales
 constexpr int SK_OFF_S = SK_OFF_DX + 2048;         // float [2][256] d * sum(q) per block
 constexpr int SK_OFF_OPS = SK_OFF_S + 2048;        // float2 [nb][C + 1] chain operands / input staging / attention
-constexpr int SK_OPS_BYTES = 69632;
+constexpr int SK_OPS_BYTES = 70656;
 constexpr int SK_OFF_DD = SK_OFF_OPS + SK_OPS_BYTES;   // float [nb][rows + 1] weight scales
 constexpr int SK_DD_BYTES = 18432;
 constexpr int SK_OFF_COR = SK_OFF_DD + SK_DD_BYTES;    // float [256]
@@ -39,6 +39,22 @@ constexpr int SK_OFF_RNG = SK_OFF_MISC + 256;          // int4 [SK_MAX_STAGES] t
 constexpr int SK_MAX_STAGES = 128;
 constexpr int SK_LDS_BYTES = SK_OFF_RNG + 16 * SK_MAX_STAGES;
 constexpr int SK_ATTN_BYTES = SK_OPS_BYTES + SK_DD_BYTES;   // attention's share (OPS and DD are contiguous)
+
+// groups of 8 rows per chunk for a table of nb 32-column blocks and M inputs: one (group, block) pair per thread in
+// phase 1, and per row the chain operands float(isum) and d * dx ([2][M][rows][st]) and the scales d ([rows][st])
+// in LDS, st the row stride below
+__host__ __device__ inline int sk_row_stride(int nb) { return ((nb + 3) & ~3) + 4; }   // 16-byte rows, odd in 16 B
+__host__ __device__ inline int sk_gmax(int nb, int M) {
+    const int st = 4 * sk_row_stride(nb);   // bytes per row of one block-ordered array
+    int g = SK_THREADS / nb;
+    const int c1 = 256 / (8 * M);   // chains (input, row) per chunk <= 256: the epilogue's exchange buffer
+    const int c2 = (SK_DD_BYTES - 64) / (8 * st);
+    const int c3 = (SK_OPS_BYTES - 64) / (8 * 2 * M * st);   // 64 B left for the chain's read-ahead
+    g = g < c1 ? g : c1;
+    g = g < c2 ? g : c2;
+    g = g < c3 ? g : c3;
+    return g;
+}
 
 struct sk_stage {
     int kind, pro, epi;
@@ -53,6 +69,9 @@ struct sk_stage {
     const float* w_pre;               // h = norm(x) * w_pre
     const float* conv_w;              // SKE_CONV: taps [d_conv + 1][E]
     int conv_layer;
+    int cut_out;                      // SKE_SWIGLU: publish the output already cut, per 32 values 10 records
+                                      // (8 words of int8 codes, d, d * sum) instead of 32 floats
+    int cut_in;                       // SKP_CUT: the input comes in that form
     int layer_ai, swa;                // SK_ATTN
     const float* q_norm;
     const float* k_norm;

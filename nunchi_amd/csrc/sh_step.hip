@@ -118,9 +118,9 @@ __device__ __forceinline__ float LDS* l_y() { return (float LDS*)(lds_base() + S
 __device__ __forceinline__ int LDS* l_xq() { return (int LDS*)(lds_base() + SK_OFF_XQ); }        // [2][2048] int8 x 4
 __device__ __forceinline__ float LDS* l_dx() { return (float LDS*)(lds_base() + SK_OFF_DX); }    // [2][256]
 __device__ __forceinline__ float LDS* l_s() { return (float LDS*)(lds_base() + SK_OFF_S); }      // [2][256]
-__device__ __forceinline__ f32x2 LDS* l_ops() { return (f32x2 LDS*)(lds_base() + SK_OFF_OPS); }   // [nb][C + 1]
+__device__ __forceinline__ float LDS* l_pq() { return (float LDS*)(lds_base() + SK_OFF_OPS); }  // [2][M][rows][st]
 __device__ __forceinline__ float LDS* l_stg() { return (float LDS*)(lds_base() + SK_OFF_OPS); }  // [2][8192] staging
-__device__ __forceinline__ float LDS* l_dd() { return (float LDS*)(lds_base() + SK_OFF_DD); }    // [nb][rows + 1]
+__device__ __forceinline__ float LDS* l_dd() { return (float LDS*)(lds_base() + SK_OFF_DD); }    // [rows][nb + 4]
 __device__ __forceinline__ float LDS* l_cor() { return (float LDS*)(lds_base() + SK_OFF_COR); }  // [256]
 __device__ __forceinline__ float LDS* l_out() { return (float LDS*)(lds_base() + SK_OFF_OUT); }  // [256]
 __device__ __forceinline__ float LDS* l_redv() { return (float LDS*)(lds_base() + SK_OFF_RED); } // [512]
@@ -145,9 +145,7 @@ __device__ __forceinline__ wg_range compute_range(SR S, int b, int G) {
     r.u0 = (int)((U * (unsigned)b) / (unsigned)G);
     r.n = (int)((U * (unsigned)(b + 1)) / (unsigned)G) - r.u0;
     const int nb = S.W.nb > 0 ? S.W.nb : 1;
-    const int cmax = min(256, SK_OPS_BYTES / (8 * nb) - 1);
-    const int gmax = min(SK_THREADS / nb, cmax / (8 * M));
-    r.cu = max(1, gmax / max(S.ug, 1));
+    r.cu = max(1, sk_gmax(nb, M) / max(S.ug, 1));
     r.nch = S.kind == SK_ATTN ? 0 : (r.n + r.cu - 1) / r.cu;
     return r;
 }
@@ -206,106 +204,114 @@ __device__ __forceinline__ int tslot(const sk_params& P, int step, int s, int k)
 // ---------------------------------------------------------------- prologues
 // h = x * sc * w_pre per 32-column block (imi_norm_mul, imi/core/vec.h:36-39), optionally written out (hid0/hid1:
 // the conversations' hidden rows, or null), then cut to int8 (imi_q8::from, imi/core/tables.cpp:100-109)
-template <int M>
-__device__ __forceinline__ void load_w_pre(const float* w_pre, int E, float (&wv)[32]) {
-    const int nbE = E / 32, t = threadIdx.x;
-    const int j = t < M * nbE ? t % nbE : 0;
-    const f32x4 GLB* w = (const f32x4 GLB*)(w_pre + 32 * j);
+// block j of conversation m: h = x * sc * w_pre (imi_norm_mul, imi/core/vec.h:36-39), optionally written out,
+// then cut to int8 (imi_q8::from, imi/core/tables.cpp:100-109)
+__device__ __forceinline__ void norm_cut_block(int m, int j, float sc, const float (&wv)[32], float* hid, bool cut) {
+    const float LDS* x = l_x() + m * 2048 + 32 * j;
+    float h[32];
 #pragma unroll
-    for (int q = 0; q < 8; q++) {
-        const f32x4 a = w[q];
-        wv[4 * q] = a.x; wv[4 * q + 1] = a.y; wv[4 * q + 2] = a.z; wv[4 * q + 3] = a.w;
+    for (int k = 0; k < 32; k++) h[k] = x[k] * sc * wv[k];
+    if (hid) {
+        f32x4 GLB* o = (f32x4 GLB*)(hid + 32 * j);
+#pragma unroll
+        for (int k = 0; k < 8; k++) o[k] = f32x4{h[4 * k], h[4 * k + 1], h[4 * k + 2], h[4 * k + 3]};
+    }
+    if (cut) {
+        int q8[8], sum;
+        const float d = cut32(h, q8, &sum, false);
+        int LDS* xq = l_xq() + m * 2048 + 8 * j;
+#pragma unroll
+        for (int w8 = 0; w8 < 8; w8++) xq[w8] = q8[w8];
+        l_dx()[m * 256 + j] = d;
+        l_s()[m * 256 + j] = d * (float)sum;
     }
 }
 
-template <int M>
-__device__ __forceinline__ void norm_cut(const float (&wv)[32], int E, float* hid0, float* hid1, bool cut) {
-    const int nbE = E / 32;
-    const int t = threadIdx.x;
-    if (t < M * nbE) {
-        const int m = t / nbE, j = t - m * nbE;
-        const float sc = l_misc()[2 + m];
-        const float LDS* x = l_x() + m * 2048 + 32 * j;
-        float h[32];
-#pragma unroll
-        for (int k = 0; k < 32; k++) h[k] = x[k] * sc * wv[k];
-        float* hid = m == 0 ? hid0 : hid1;
-        if (hid) {
-            f32x4 GLB* o = (f32x4 GLB*)(hid + 32 * j);
-#pragma unroll
-            for (int k = 0; k < 8; k++) o[k] = f32x4{h[4 * k], h[4 * k + 1], h[4 * k + 2], h[4 * k + 3]};
-        }
-        if (cut) {
-            int q8[8], sum;
-            const float d = cut32(h, q8, &sum, false);
-            int LDS* xq = l_xq() + m * 2048 + 8 * j;
-#pragma unroll
-            for (int w8 = 0; w8 < 8; w8++) xq[w8] = q8[w8];
-            l_dx()[m * 256 + j] = d;
-            l_s()[m * 256 + j] = d * (float)sum;
-        }
-    }
-    __syncthreads();
-}
-
-// x += norm(y) * w_post (imi_norm_mul_add, imi/core/vec.h:41-44); then h = norm(x) * w_pre and its cut
+// x += norm(y) * w_post (imi_norm_mul_add, imi/core/vec.h:41-44); then h = norm(x) * w_pre and its cut. Threads
+// are split by conversation (m = t / (512 / M)); every wave computes its conversation's norm scales itself (the
+// same chain in every wave, so the same value), which saves two block barriers.
 template <int M>
 __device__ __forceinline__ bool pro_resid(const sk_params& P, SR S, unsigned tag, int par, float* hid0, float* hid1, bool cut, int tr) {
-    const int E = P.E, t = threadIdx.x, wv = t >> 6;
+    constexpr int HALF = SK_THREADS / M;
+    constexpr int PER = 2048 / HALF;   // elements of x per thread
+    const int E = P.E, t = threadIdx.x, m = t / HALF, tt = t - m * HALF;
     // the post-norm weight is read before the wait, so it arrives with the input
-    float wpost[4];
+    float wpost[PER];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int i = t + k * SK_THREADS;
+    for (int k = 0; k < PER; k++) {
+        const int i = tt + k * HALF;
         wpost[k] = i < E ? ((const float GLB*)S.w_post)[i] : 0.0f;
     }
     const bool ok = ll_gather(S.in + (size_t)par * 2 * S.n_in, S.n_in, E, M, tag, l_y(), 2048, P);
     if (__syncthreads_or(!ok)) return false;
     trace_at(P, blockIdx.x, tr);
-    if (wv < M) {
-        const float sc = rms_scale_wave((const float LDS*)(l_y() + wv * 2048), E, P.eps);
-        if ((t & 63) == 0) l_misc()[wv] = sc;
-    }
-    __syncthreads();
+    const float sc1 = rms_scale_wave((const float LDS*)(l_y() + m * 2048), E, P.eps);
 #pragma unroll
-    for (int m = 0; m < M; m++)
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int i = t + k * SK_THREADS;
-            if (i < E) {
-                float LDS* x = l_x() + m * 2048 + i;
-                *x = fmaf(l_y()[m * 2048 + i] * l_misc()[m], wpost[k], *x);
-            }
+    for (int k = 0; k < PER; k++) {
+        const int i = tt + k * HALF;
+        if (i < E) {
+            float LDS* x = l_x() + m * 2048 + i;
+            *x = fmaf(l_y()[m * 2048 + i] * sc1, wpost[k], *x);
         }
+    }
     float wpre[32];   // in flight during the second norm's chain
-    load_w_pre<M>(S.w_pre, E, wpre);
-    __syncthreads();
-    if (wv < M) {
-        const float sc = rms_scale_wave((const float LDS*)(l_x() + wv * 2048), E, P.eps);
-        if ((t & 63) == 0) l_misc()[2 + wv] = sc;
+    const int nbE = E / 32;
+    const int j = tt < nbE ? tt : 0;
+    {
+        const f32x4 GLB* w = (const f32x4 GLB*)(S.w_pre + 32 * j);
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const f32x4 a = w[q];
+            wpre[4 * q] = a.x; wpre[4 * q + 1] = a.y; wpre[4 * q + 2] = a.z; wpre[4 * q + 3] = a.w;
+        }
     }
     __syncthreads();
-    norm_cut<M>(wpre, E, hid0, hid1, cut);
+    const float sc2 = rms_scale_wave((const float LDS*)(l_x() + m * 2048), E, P.eps);
+    if (tt < nbE) norm_cut_block(m, j, sc2, wpre, m == 0 ? hid0 : hid1, cut);
+    __syncthreads();
     return true;
 }
 
 template <int M>
 __device__ __forceinline__ void pro_first(const sk_params& P, SR S) {
-    const int t = threadIdx.x, wv = t >> 6;
+    constexpr int HALF = SK_THREADS / M;
+    const int t = threadIdx.x, m = t / HALF, tt = t - m * HALF;
+    const int nbE = P.E / 32;
+    const int j = tt < nbE ? tt : 0;
     float wpre[32];
-    load_w_pre<M>(S.w_pre, P.E, wpre);
-    if (wv < M) {
-        const float sc = rms_scale_wave((const float LDS*)(l_x() + wv * 2048), P.E, P.eps);
-        if ((t & 63) == 0) l_misc()[2 + wv] = sc;
+    const f32x4 GLB* w = (const f32x4 GLB*)(S.w_pre + 32 * j);
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+        const f32x4 a = w[q];
+        wpre[4 * q] = a.x; wpre[4 * q + 1] = a.y; wpre[4 * q + 2] = a.z; wpre[4 * q + 3] = a.w;
     }
+    const float sc = rms_scale_wave((const float LDS*)(l_x() + m * 2048), P.E, P.eps);
+    if (tt < nbE) norm_cut_block(m, j, sc, wpre, nullptr, true);
     __syncthreads();
-    norm_cut<M>(wpre, P.E, nullptr, nullptr, true);
 }
 
 // the previous table's float output, cut to int8 per 32 (imi/core/vec.h:47-75)
 template <int M>
 __device__ __forceinline__ bool pro_cut(const sk_params& P, SR S, unsigned tag, int par, int tr) {
-    const int K = S.n_in, t = threadIdx.x;
+    const int t = threadIdx.x;
+    if (S.cut_in) {   // already cut by the producer: 10 records per block (8 code words, d, d * sum)
+        const int n = S.n_in;
+        const bool ok = ll_gather(S.in + (size_t)par * 2 * S.n_in, S.n_in, n, M, tag, l_stg(), 8192, P);
+        if (__syncthreads_or(!ok)) return false;
+        trace_at(P, blockIdx.x, tr);
+#pragma unroll
+        for (int m = 0; m < M; m++)
+            for (int k = t; k < n; k += SK_THREADS) {
+                const int blk = k / 10, w = k - blk * 10;
+                const float v = l_stg()[m * 8192 + k];
+                if (w < 8) l_xq()[m * 2048 + 8 * blk + w] = __float_as_int(v);
+                else if (w == 8) l_dx()[m * 256 + blk] = v;
+                else l_s()[m * 256 + blk] = v;
+            }
+        __syncthreads();
+        return true;
+    }
+    const int K = S.n_in;
     const bool ok = ll_gather(S.in + (size_t)par * 2 * S.n_in, S.n_in, K, M, tag, l_stg(), 8192, P);
     if (__syncthreads_or(!ok)) return false;
     trace_at(P, blockIdx.x, tr);
@@ -329,13 +335,14 @@ __device__ __forceinline__ bool pro_cut(const sk_params& P, SR S, unsigned tag, 
 }
 
 // ---------------------------------------------------------------- GEMV chunk
-// phase 1: thread = (group gi, block j); exact integer dots of the 8 rows against each input's cut block, and the
-// chain operands {float(isum), d * dx} and d to LDS
+// phase 1: thread = (group gi, block j); exact integer dots of the 8 rows against each input's cut block; the
+// chain operands float(isum) and d * dx to LDS row-major ([input][row][block], rows padded to st so 16-byte reads
+// by the lanes of a wave are conflict free), with the rows' scales d beside them ([row][block])
 template <int M>
-__device__ __forceinline__ void phase1(const u32x4 (&w)[9], int ng, int nb, int rows, int C) {
+__device__ __forceinline__ void phase1(const u32x4 (&w)[9], int ng, int nb, int rows) {
     const int t = threadIdx.x;
     if (t < ng * nb) {
-        const int gi = t / nb, j = t - gi * nb;
+        const int gi = t / nb, j = t - gi * nb, st = sk_row_stride(nb);
         float d[8];
         const unsigned sw[4] = {w[8].x, w[8].y, w[8].z, w[8].w};
 #pragma unroll
@@ -348,17 +355,20 @@ __device__ __forceinline__ void phase1(const u32x4 (&w)[9], int ng, int nb, int 
             xq[0] = (int)a.x; xq[1] = (int)a.y; xq[2] = (int)a.z; xq[3] = (int)a.w;
             xq[4] = (int)c.x; xq[5] = (int)c.y; xq[6] = (int)c.z; xq[7] = (int)c.w;
             const float dx = l_dx()[m * 256 + j];
-            f32x2 LDS* o = l_ops() + j * (C + 1) + m * rows + 8 * gi;
+            float LDS* op = l_pq() + (m * rows + 8 * gi) * st + j;              // float(isum)
+            float LDS* oq = l_pq() + ((M + m) * rows + 8 * gi) * st + j;        // d * dx
 #pragma unroll
-            for (int r = 0; r < 8; r++) o[r] = f32x2{(float)q4_block_dot(w[r], xq), d[r] * dx};
+            for (int r = 0; r < 8; r++) {
+                op[r * st] = (float)q4_block_dot(w[r], xq);
+                oq[r * st] = d[r] * dx;
+            }
         }
-        float LDS* dd = l_dd() + j * (rows + 1) + 8 * gi;
+        float LDS* dd = l_dd() + (8 * gi) * st + j;
 #pragma unroll
-        for (int r = 0; r < 8; r++) dd[r] = d[r];
+        for (int r = 0; r < 8; r++) dd[r * st] = d[r];
     }
 }
 
-// phase 2 (chains) and the epilogue of one chunk
 // conv taps and memory of this thread's channel, loaded before the chunk's prefetch is issued (a global load in
 // the epilogue would wait for that prefetch: loads complete in order)
 struct conv_pre {
@@ -386,44 +396,49 @@ template <int M>
 __device__ __forceinline__ void phase2_epilogue(const sk_params& P, SR S, int g0, int C, int rows, unsigned tag, int par,
                                                 float (&bv)[M], int (&bi)[M], const conv_pre& cp) {
     const int t = threadIdx.x, nb = S.W.nb;
-    float acc = 0.0f;
-    // the chains read their operands 8 blocks at a time, so the LDS latency is paid once per 8 steps
-    if (t < C) {
-        const f32x2 LDS* o = l_ops() + t;
-        const int st = C + 1;
-        int j = 0;
-        for (; j + 8 <= nb; j += 8) {
-            f32x2 v[8];
-#pragma unroll
-            for (int q = 0; q < 8; q++) v[q] = o[(j + q) * st];
-#pragma unroll
-            for (int q = 0; q < 8; q++) acc = fmaf(v[q].x, v[q].y, acc);
+    // imi's two chains per (input m, row) over the blocks in order (imi/core/tables.cpp:127-143): acc =
+    // fma(float(isum), d * dx, acc) on waves 0-3 (lane t), cor = fma(d, s, cor) on waves 4-7 (lane t - 256), so each
+    // wave issues one FMA per step; out = fma(-8, cor, acc). Operands come 4 blocks per 16-byte LDS read, in two
+    // alternating register batches of 8 blocks: the next batch's reads are in flight while the current one runs
+    // (the read-ahead past a row's end lands in padding and is not used).
+    const bool acc_lane = t < C, cor_lane = t >= 256 && t - 256 < C;
+    float chain = 0.0f;
+    if (acc_lane || cor_lane) {
+        const int c = acc_lane ? t : t - 256, m = c / rows, r = c - m * rows, st = sk_row_stride(nb);
+        const f32x4 LDS* ap = (const f32x4 LDS*)(acc_lane ? l_pq() + (m * rows + r) * st : l_dd() + r * st);
+        const f32x4 LDS* bp = (const f32x4 LDS*)(acc_lane ? l_pq() + ((M + m) * rows + r) * st : l_s() + m * 256);
+        const int n4 = nb / 4;
+        f32x4 a0 = ap[0], a1 = ap[1], b0 = bp[0], b1 = bp[1];
+        int q = 0;
+#define SK_STEP4(A4, B4)                                                                              \
+        chain = fmaf(A4.x, B4.x, chain); chain = fmaf(A4.y, B4.y, chain);                             \
+        chain = fmaf(A4.z, B4.z, chain); chain = fmaf(A4.w, B4.w, chain);
+        for (; q + 4 <= n4; q += 4) {
+            const f32x4 a2 = ap[q + 2], a3 = ap[q + 3], b2 = bp[q + 2], b3 = bp[q + 3];
+            SK_STEP4(a0, b0)
+            SK_STEP4(a1, b1)
+            a0 = ap[q + 4]; a1 = ap[q + 5]; b0 = bp[q + 4]; b1 = bp[q + 5];
+            SK_STEP4(a2, b2)
+            SK_STEP4(a3, b3)
         }
-        for (; j < nb; j++) {
-            const f32x2 v = o[j * st];
-            acc = fmaf(v.x, v.y, acc);
+        if (n4 - q >= 2) {           // the loaded batch: quads q, q + 1
+            SK_STEP4(a0, b0)
+            SK_STEP4(a1, b1)
+            q += 2;
+        } else if (n4 - q == 1) {    // the loaded quad q
+            SK_STEP4(a0, b0)
+            q += 1;
         }
-    } else if (t >= 256 && t < 256 + C) {
-        const int c = t - 256, m = c / rows, r = c - m * rows;
-        const float LDS* dd = l_dd() + r;
-        const float LDS* sv = l_s() + m * 256;
-        const int st = rows + 1;
-        float cor = 0.0f;
-        int j = 0;
-        for (; j + 8 <= nb; j += 8) {
-            float a[8], e[8];
-#pragma unroll
-            for (int q = 0; q < 8; q++) { a[q] = dd[(j + q) * st]; e[q] = sv[j + q]; }
-#pragma unroll
-            for (int q = 0; q < 8; q++) cor = fmaf(a[q], e[q], cor);
-        }
-        for (; j < nb; j++) cor = fmaf(dd[j * st], sv[j], cor);
-        l_cor()[c] = cor;
+#undef SK_STEP4
+        const float LDS* as = (const float LDS*)ap;
+        const float LDS* bs = (const float LDS*)bp;
+        for (int j = 4 * q; j < nb; j++) chain = fmaf(as[j], bs[j], chain);
+        if (cor_lane) l_cor()[c] = chain;
     }
     __syncthreads();
     float outv = 0.0f;
-    if (t < C) {
-        outv = fmaf(-8.0f, l_cor()[t], acc);
+    if (acc_lane) {
+        outv = fmaf(-8.0f, l_cor()[t], chain);
         l_out()[t] = outv;
     }
     __syncthreads();
@@ -434,7 +449,12 @@ __device__ __forceinline__ void phase2_epilogue(const sk_params& P, SR S, int g0
         ll_put(out + 8 * g0 + rr, outv, tag);
     } else if (S.epi == SKE_SWIGLU) {   // (gate group, up group) of 8 FFN channels (imi/core/seoul.cpp:380-394)
         const int k = rr & 15;
-        if (k < 8) ll_put(out + 8 * (g0 / 2 + rr / 16) + k, silu(outv) * l_out()[t + 8], tag);
+        if (k < 8) {
+            const float a = silu(outv) * l_out()[t + 8];
+            // cut_out: the chunk's channels go to LDS and are cut and published per 32 after the block barrier
+            if (S.cut_out) l_cor()[m * (rows / 2) + 8 * (rr / 16) + k] = a;
+            else ll_put(out + 8 * (g0 / 2 + rr / 16) + k, a, tag);
+        }
     } else if (S.epi == SKE_CONV) {     // (b, c, x) groups of 8 channels (imi/core/seoul.cpp:407-423)
         const int k = rr % 24;
         if (k < 8) {
@@ -833,9 +853,27 @@ __device__ __forceinline__ void chunk(const sk_params& P, walk_state& W, int b, 
     // the publish, and the stream overlaps the wait for the next stage's input
     int qs = W.step, qss = W.s, qc = W.c;
     if (!next_chunk<M>(P, b, G, qs, qss, qc)) { qss = W.s; qc = W.c; }   // the last chunk: a harmless re-read
-    phase1<M>(cur, ng, S.W.nb, rows, C);
+    phase1<M>(cur, ng, S.W.nb, rows);
     __syncthreads();
     phase2_epilogue<M>(P, S, g0, C, rows, tag, par, bv, bi, cp);
+    if (S.cut_out) {   // the chunk's rows / 2 FFN channels of each conversation, cut per 32 (imi/core/vec.h:47-75)
+        __syncthreads();
+        const int nblk = rows / 64;   // 32 channels = 4 units = 64 rows
+        if (threadIdx.x < M * nblk) {
+            const int m = threadIdx.x / nblk, k = threadIdx.x - m * nblk;
+            float v[32];
+            const float LDS* a = l_cor() + m * (rows / 2) + 32 * k;
+#pragma unroll
+            for (int i = 0; i < 32; i++) v[i] = a[i];
+            int q8[8], sum;
+            const float d = cut32(v, q8, &sum, false);
+            u64* o = S.out + (size_t)(par * 2 + m) * S.n_out + (size_t)(g0 / 8 + k) * 10;
+#pragma unroll
+            for (int w = 0; w < 8; w++) ll_put(o + w, __int_as_float(q8[w]), tag);
+            ll_put(o + 8, d, tag);
+            ll_put(o + 9, d * (float)sum, tag);
+        }
+    }
     issue<M>(P, b, G, qss, qc, nxt);
     __syncthreads();
     W.c++;
