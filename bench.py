@@ -57,21 +57,31 @@ def gpu_decode(brain, steps, warmup, b2: bool):
     return tokens / wall, ids, dev, wall
 
 
-def cpu_decode(path, threads, steps, b2: bool):
+def cpu_decode(path, threads, steps, b2: bool, runs: int = 1):
+    """imi's CPU path (the oracle restatement): `runs` conversations, each a 32-token prompt then `steps` greedy
+    ids; returns (tokens/s over the generated tokens of all runs, ids of run 0, seconds)."""
     import oracle
     eng = oracle.Engine(path, threads=threads, n_ctx=N_CTX)
-    pa, pb = _prompt(0, eng.n_vocab), _prompt(1, eng.n_vocab)
-    if b2:
-        sb = eng.new_state()
-        for i in range(PROMPT):
-            last = i == PROMPT - 1
-            _, la, _, lb = eng.step2(int(pa[i]), None, last, sb, int(pb[i]), None, last)
-        oa, ob, secs = eng.greedy2(sb, oracle.top(la), oracle.top(lb), steps)
-        return 2 * steps / secs, oa, secs
-    for i in range(PROMPT):
-        _, lg = eng.step(int(pa[i]), want_logits=i == PROMPT - 1)
-    ids, secs = eng.greedy(oracle.top(lg), steps)
-    return steps / secs, ids, secs
+    tok, secs, ids0 = 0, 0.0, None
+    for r in range(runs):
+        eng.reset()
+        pa, pb = _prompt(2 * r, eng.n_vocab), _prompt(2 * r + 1, eng.n_vocab)
+        if b2:
+            sb = eng.new_state()
+            for i in range(PROMPT):
+                last = i == PROMPT - 1
+                _, la, _, lb = eng.step2(int(pa[i]), None, last, sb, int(pb[i]), None, last)
+            oa, ob, t = eng.greedy2(sb, oracle.top(la), oracle.top(lb), steps)
+            tok += 2 * steps
+        else:
+            for i in range(PROMPT):
+                _, lg = eng.step(int(pa[i]), want_logits=i == PROMPT - 1)
+            oa, t = eng.greedy(oracle.top(lg), steps)
+            tok += steps
+        secs += t
+        if ids0 is None:
+            ids0 = oa
+    return tok / secs, ids0, secs
 
 
 def main():
@@ -81,6 +91,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, cores in the affinity mask)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-runs", type=int, default=8, help="B=1 conversations timed on the CPU (B=2: half as many pairs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (conversations shard across "
@@ -98,7 +109,7 @@ def main():
     tok_s_b1, ids_b1, dev_b1, wall_b1 = gpu_decode(brain, args.steps, args.warmup, b2=False)
     tok_s_b2, ids_b2, dev_b2, wall_b2 = gpu_decode(brain, args.steps, args.warmup, b2=True)
 
-    # dominant kernel: the FFN gate|up GEMV (norm prologue, SwiGLU epilogue), 16 per step, 18.9 MB of table each
+    # the per-table kernels (the same stages as separate launches; the step kernel's fallback path)
     gu = brain.bench_kernel("ffn_gate_up", n_in=1, reps=64)
     dn = brain.bench_kernel("ffn_down", n_in=1, reps=64)
     ws = brain.bench_kernel("word_scores", n_in=1, reps=8)
@@ -114,10 +125,14 @@ def main():
     del copies
 
     gu_gbs = gu["bytes_per_launch"] / (gu["avg_us"] * 1e-6) / 1e9
-    # algorithmic bytes of one step: every table once (device layout = file bytes: 16 B codes + 2 B scale per 32
-    # weights) + the K and V read at the mean decode position (6 layers x 512 fp16 values per position, each)
-    mean_pos = PROMPT + args.steps / 2
-    step_bytes = brain.table_bytes + 2 * brain.n_attn * mean_pos * brain.n_head_kv * brain.head_dim * 2
+    # algorithmic bytes of the greedy launch (the step kernel k_step<1>, one launch for all --steps): per step every
+    # table once (device layout = file bytes: 16 B codes + 2 B scale per 32 weights), the fp32 norm / conv vectors,
+    # and the K and V rows the step's attention reads (positions 0..pos of n_attn layers x n_kv heads x D, fp16)
+    kv_row = brain.n_attn * brain.n_head_kv * brain.head_dim * 2
+    vec_bytes = brain.vector_bytes
+    launch_bytes = sum(brain.table_bytes + vec_bytes + 2 * kv_row * (PROMPT + i + 1) for i in range(args.steps))
+    step_bytes = launch_bytes / args.steps
+    launch_gbs = launch_bytes / dev_b1 / 1e9
     line = {
         "metric": "brain-step tokens/s (B=1,2) + Q4_0 GEMV HBM GB/s vs roofline, 1 MI355X",
         "value": round(tok_s_b1, 1),
@@ -145,17 +160,18 @@ def main():
                               "b2": round(step_bytes * tok_s_b2 / 2 / 1e9 / HBM_PEAK_GBS, 4),
                               "bytes_per_step": int(step_bytes)},
         "roofline": {
-            "kernel": "k_gemv<1,1,PRO_RESID_NORM,EPI_SWIGLU,2> (FFN gate|up, 16384 x 2048 Q4_0)",
+            "kernel": f"k_step<1> (persistent step kernel: one launch, {args.steps} greedy decode steps, B=1)",
             "bound": "hbm",
-            "achieved": round(gu_gbs, 1),
+            "achieved": round(launch_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+            "frac": round(launch_gbs / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "avg_launch_us": round(gu["avg_us"], 3),
-            "bytes_per_launch": int(gu["bytes_per_launch"]),
+            "launch_us": round(dev_b1 * 1e6, 1),
+            "bytes_per_launch": int(launch_bytes),
         },
         "kernels": {
+            "ffn_gate_up_per_table": {"avg_us": round(gu["avg_us"], 3), "GBs": round(gu_gbs, 1), "frac": round(gu_gbs / HBM_PEAK_GBS, 4)},
             "ffn_gate_up_b2": {"avg_us": round(gu2["avg_us"], 3), "GBs": round(gu2["bytes_per_launch"] / gu2["avg_us"] / 1e3, 1)},
             "ffn_down": {"avg_us": round(dn["avg_us"], 3), "GBs": round(dn["bytes_per_launch"] / dn["avg_us"] / 1e3, 1)},
             "word_scores": {"avg_us": round(ws["avg_us"], 3), "GBs": round(ws["bytes_per_launch"] / ws["avg_us"] / 1e3, 1)},
@@ -170,14 +186,16 @@ def main():
         aff = len(os.sched_getaffinity(0))
         threads = args.cpu_threads or min(16, aff)
         cpu_steps = min(args.steps, 256)
-        c1, cids, csecs = cpu_decode(path, threads, cpu_steps, b2=False)
-        c2, _, csecs2 = cpu_decode(path, threads, min(cpu_steps, 128), b2=True)
+        runs1, runs2 = args.cpu_runs, max(1, args.cpu_runs // 2)
+        c1, cids, csecs = cpu_decode(path, threads, cpu_steps, b2=False, runs=runs1)
+        c2, _, csecs2 = cpu_decode(path, threads, cpu_steps, b2=True, runs=runs2)
         same = bool(np.array_equal(cids[:len(ids_b1)], ids_b1[:len(cids)]))
         line["cpu_baseline"] = {
             "value": round(c1, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"cfg2 B=1: {PROMPT}-token prompt then {cpu_steps} greedy ids ({csecs:.1f} s); B=2: step2 for "
-                      f"{min(cpu_steps, 128)} positions ({csecs2:.1f} s) = {c2:.2f} tokens/s; {threads} threads of {aff} in the "
-                      "affinity mask; oracle/ C++ restatement of imi's AVX2 engine, x86-64-v3",
+            "sample": f"cfg2 B=1: {runs1} conversations of a {PROMPT}-token seeded prompt then {cpu_steps} greedy ids "
+                      f"({csecs:.1f} s generating); B=2: {runs2} step2 pairs of {cpu_steps} positions ({csecs2:.1f} s) = "
+                      f"{c2:.2f} tokens/s; {threads} threads of {aff} in the affinity mask; oracle/ C++ restatement of "
+                      "imi's AVX2 engine, x86-64-v3",
             "b2_value": round(c2, 2),
         }
         line["speedup_vs_cpu"] = {"b1": round(tok_s_b1 / c1, 1), "b2": round(tok_s_b2 / c2, 1)}

@@ -41,6 +41,8 @@ typedef struct sh_voice sh_voice;   /* the Q8_0 voice generator on the device */
 typedef struct {
     int n_embd, n_vocab, n_head, n_head_kv, head_dim, n_ff, d_conv, n_ctx, n_layer, n_attn, n_swa;
     long long table_bytes;          /* bytes of all layer tables + word table in the device layout */
+    long long vector_bytes;         /* bytes a step reads besides the tables and K/V: fp32 norm weights and conv
+                                       taps, plus the conv memory read and written */
 } sh_model_info;
 
 /* Message of the last error on this thread ("" if none). */

@@ -39,7 +39,7 @@ class ContextFull(SeoulError):
 
 class ModelInfo(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("n_embd", "n_vocab", "n_head", "n_head_kv", "head_dim", "n_ff", "d_conv", "n_ctx",
-                                       "n_layer", "n_attn", "n_swa")] + [("table_bytes", C.c_longlong)]
+                                       "n_layer", "n_attn", "n_swa")] + [("table_bytes", C.c_longlong), ("vector_bytes", C.c_longlong)]
 
 
 _lib = None

@@ -758,6 +758,15 @@ int sh_load(sh_ctx* c, const char* path, int n_ctx) {
         c->rope_cs_swa = static_cast<const float2*>(d2);
     }
     I.table_bytes = table_bytes;
+    {
+        long long vb = 4LL * E;   // output norm
+        for (const layer_dev& L : c->layers) {
+            vb += 4LL * 4 * E;   // attn, post-attention, ffn, post-ffn norms
+            if (L.conv) vb += 4LL * (I.d_conv + 1) * E + 2 * 4LL * I.d_conv * E;   // taps, memory read + written
+            else vb += 4LL * 2 * I.head_dim;                                        // q and k norms
+        }
+        I.vector_bytes = vb;
+    }
     f.drop_data();
 
     // work buffers for up to two conversations
