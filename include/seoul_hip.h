@@ -125,6 +125,30 @@ int sh_expf(sh_ctx* ctx, const float* x, long long n, float* y);
  * converts them. */
 int sh_step_trace(sh_ctx* ctx, long long* out, long long cap, int* per_wg, int* grid, double* ticks_per_us);
 
+/* ---- voice generator: imi_voice::load / begin_frame / pass / feedback (imi/core/voice.h:17-51) ---- */
+typedef struct {
+    int n_embd, n_vocab, n_cb, n_in, n_head, n_head_kv, head_dim, n_ff, n_layer;
+    long long table_bytes;          /* bytes of every 8-bit table in the device layout (layers, score tables,
+                                       input projection) */
+    long long feedback_bytes;       /* bytes of the feedback rows (Q8_0 as stored) */
+} sh_voice_shape;
+
+/* Read a GGUF voice generator ("a.gen.code." tensors, Q8_0 tables) onto `device` (imi/core/voice.cpp:27-88). The
+ * generator has its own stream; it takes 2 to 12 codebooks and head_dim 32 or 64. */
+int sh_voice_load(int device, const char* gguf_path, sh_voice** out);
+int sh_voice_free(sh_voice* v);                                   /* imi_voice::~imi_voice (voice.cpp:208-212) */
+int sh_voice_info(const sh_voice* v, sh_voice_shape* out);
+/* The frame's input projection from the brain's hidden state hidden[n_in] (voice.cpp:99-111). */
+int sh_voice_begin_frame(sh_voice* v, const float* hidden);
+/* The frame's projected input, [n_cb][n_embd] (imi_voice::base, voice.h:30). */
+int sh_voice_base(sh_voice* v, float* out);
+/* One masked pass (voice.cpp:113-206): codes[n_cb], < 0 = still masked; out[n_need][n_vocab] gets the scores of
+ * codebooks need[0..n_need) (0 <= n_need <= n_cb). */
+int sh_voice_pass(sh_voice* v, const int32_t* codes, const int32_t* need, int n_need, float* out);
+/* The brain's next input after a frame: the sum, codebook by codebook, of the chosen codes' feedback rows,
+ * out[n_in] (voice.cpp:90-97). codes[n_cb] must all be chosen (0 <= code < n_vocab). */
+int sh_voice_feedback(sh_voice* v, const int32_t* codes, float* out);
+
 /* Synchronise the context's stream (for callers of the _dev entry points). */
 int sh_sync(sh_ctx* ctx);
 

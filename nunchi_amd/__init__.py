@@ -24,6 +24,8 @@ EXPORTS = [
     "sh_bench_kernel",
     "sh_q4_create", "sh_q4_free", "sh_q4_rows", "sh_q4_gemv", "sh_q4_gemv_dev", "sh_q4_bench", "sh_expf", "sh_sync",
     "sh_step_trace",
+    "sh_voice_load", "sh_voice_free", "sh_voice_info", "sh_voice_begin_frame", "sh_voice_base", "sh_voice_pass",
+    "sh_voice_feedback",
 ]
 
 
@@ -40,6 +42,11 @@ class ContextFull(SeoulError):
 class ModelInfo(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("n_embd", "n_vocab", "n_head", "n_head_kv", "head_dim", "n_ff", "d_conv", "n_ctx",
                                        "n_layer", "n_attn", "n_swa")] + [("table_bytes", C.c_longlong), ("vector_bytes", C.c_longlong)]
+
+
+class VoiceShape(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("n_embd", "n_vocab", "n_cb", "n_in", "n_head", "n_head_kv", "head_dim", "n_ff",
+                                       "n_layer")] + [("table_bytes", C.c_longlong), ("feedback_bytes", C.c_longlong)]
 
 
 _lib = None
@@ -81,6 +88,13 @@ def load_library(path: str = LIB_PATH):
         "sh_expf": (i, [vp, vp, C.c_longlong, vp]),
         "sh_sync": (i, [vp]),
         "sh_step_trace": (i, [vp, vp, C.c_longlong, P(i), P(i), P(d)]),
+        "sh_voice_load": (i, [i, C.c_char_p, P(vp)]),
+        "sh_voice_free": (i, [vp]),
+        "sh_voice_info": (i, [vp, P(VoiceShape)]),
+        "sh_voice_begin_frame": (i, [vp, vp]),
+        "sh_voice_base": (i, [vp, vp]),
+        "sh_voice_pass": (i, [vp, vp, vp, i, vp]),
+        "sh_voice_feedback": (i, [vp, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -316,8 +330,64 @@ def q4_bench(ctx: Context, tables, n_in: int = 1, cut_mode: int = 0, reps: int =
     return us.value
 
 
+_live_voices = weakref.WeakSet()
+
+
+class Voice:
+    """The Q8_0 voice generator on the device, shaped like imi_voice (imi/core/voice.h:17-51): begin_frame(hidden)
+    once per frame, pass_(codes, need) per masked pass, feedback(codes) for the brain's next input."""
+
+    def __init__(self, path: str, device: int = 0):
+        load_library()
+        self.h = C.c_void_p()
+        _check(_lib.sh_voice_load(int(device), path.encode(), C.byref(self.h)))
+        _live_voices.add(self)
+        sh = VoiceShape()
+        _check(_lib.sh_voice_info(self.h, C.byref(sh)))
+        for n, _ in VoiceShape._fields_:
+            setattr(self, n, getattr(sh, n))
+
+    def close(self):
+        if getattr(self, "h", None) and self.h.value:
+            _lib.sh_voice_free(self.h)
+            self.h = C.c_void_p()
+
+    def __del__(self):
+        self.close()
+
+    def begin_frame(self, hidden):
+        hidden = np.ascontiguousarray(hidden, np.float32)
+        if hidden.size != self.n_in:
+            raise ValueError("hidden must have n_in values")
+        _check(_lib.sh_voice_begin_frame(self.h, _p(hidden)))
+
+    def base(self) -> np.ndarray:
+        out = np.zeros(self.n_cb * self.n_embd, np.float32)
+        _check(_lib.sh_voice_base(self.h, _p(out)))
+        return out
+
+    def pass_(self, codes, need) -> np.ndarray:
+        codes = np.ascontiguousarray(codes, np.int32)
+        need = np.ascontiguousarray(need, np.int32)
+        if codes.size != self.n_cb:
+            raise ValueError("codes must have n_cb entries")
+        out = np.zeros((need.size, self.n_vocab), np.float32)
+        _check(_lib.sh_voice_pass(self.h, _p(codes), _p(need), int(need.size), _p(out)))
+        return out
+
+    def feedback(self, codes) -> np.ndarray:
+        codes = np.ascontiguousarray(codes, np.int32)
+        if codes.size != self.n_cb:
+            raise ValueError("codes must have n_cb entries")
+        out = np.zeros(self.n_in, np.float32)
+        _check(_lib.sh_voice_feedback(self.h, _p(codes), _p(out)))
+        return out
+
+
 @atexit.register
 def _close_all():
-    """Destroy every live context (and its states and tables) while the HIP runtime is still up."""
+    """Destroy every live context (and its states and tables) and voice generator while the HIP runtime is up."""
+    for v in list(_live_voices):
+        v.close()
     for c in list(_live_contexts):
         c.close()

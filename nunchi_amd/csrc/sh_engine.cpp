@@ -85,6 +85,10 @@ bool repack_q4(const std::vector<std::pair<const gg_tensor*, int>>& rows, std::v
 }
 }  // namespace
 
+namespace sh {
+int set_error(int code, const std::string& msg) { return fail(code, msg); }   // for the other host files
+}
+
 struct sh_q4 {
     sh_ctx* ctx = nullptr;
     q4dev t;

@@ -1,0 +1,378 @@
+// Kernels of the Q8_0 voice generator (imi/core/voice.cpp:90-206) for gfx950.
+//
+// A pass is: code embeddings + the frame's base (one kernel), then per layer the qkvg table with the ln1 norm folded
+// into its input staging, bidirectional attention over the P positions (one workgroup per query head), the o table
+// adding into the residual stream, the gate|up table with the ln2 norm in front and SiLU(gate) * up behind, the down
+// table adding into the residual stream; then the word scores of the needed codebooks with the output and head
+// norms folded into their input staging. Every operation order is the CPU path's, so results agree bit for bit.
+#include "sh_device.h"
+#include "sh_voice.h"
+
+namespace sh {
+namespace {
+
+constexpr int VX_NJ = 32;    // 32-column blocks per staged chunk of the input (1024 columns)
+constexpr int VX_SS = 33;    // row stride of the per-block partial sums in LDS (odd: conflict-free column reads)
+
+__host__ __device__ constexpr int vx_pp(int P) { return (P + 3) & ~3; }          // positions padded to float4
+__host__ __device__ constexpr int vx_xj(int P) { return 32 * vx_pp(P) + 4; }     // floats per staged block
+
+// rms scale of each position's input row (imi/core/vec.h:20-33), one wave per row
+template <int P>
+__device__ __forceinline__ void position_scales(const vtab_args& a, float* scl) {
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int p = w; p < P; p += VX_THREADS / 64) {
+        const float s = rms_scale_wave(a.src + (size_t)p * a.src_ld, a.W.cols, a.eps);
+        if (lane == 0) scl[p] = s;
+    }
+}
+
+// columns [1024 q, 1024 q + 32 nbc) of the P positions, k-major: xs[block][column in block][position]
+// (imi/core/voice.cpp:157-166: the transposed input, normed first when the table follows a norm)
+template <int P, int PRO>
+__device__ __forceinline__ void stage_chunk(float* xs, const vtab_args& a, int q, int nbc, const float* scl) {
+    constexpr int PP = vx_pp(P), XJ = vx_xj(P);
+    const int n = 32 * nbc, c0 = q * 32 * VX_NJ;
+    for (int p = 0; p < P; p++) {
+        const float* row = a.src + (size_t)p * a.src_ld + c0;
+        for (int k = threadIdx.x; k < n; k += VX_THREADS) {
+            float v = row[k];
+            if (PRO == VP_NORM) v = v * scl[p] * a.norm_w[c0 + k];
+            xs[(k >> 5) * XJ + (k & 31) * PP + p] = v;
+        }
+    }
+}
+
+// results of the workgroup's NR rows (from group g0 on): thread t holds row t / P, position t % P
+template <int P, int EPI, int NR>
+__device__ __forceinline__ void table_epilogue(const vtab_args& a, int g0, float acc, float* ev) {
+    const int t = threadIdx.x, frow = t / P, fc = t - frow * P;
+    if (EPI == VE_SWIGLU) {   // groups g0 (gate rows) and g0 + 1 (up rows): out[p][4 g0 + r] (voice.cpp:150-156)
+        static_assert(EPI != VE_SWIGLU || NR == 16, "gate and up groups side by side");
+        if (t < 16 * P) ev[t] = acc;
+        __syncthreads();
+        if (t < 8 * P) a.out[(size_t)fc * a.out_ld + 4 * g0 + frow] = silu(ev[t]) * ev[8 * P + t];
+    } else {
+        const int row = 8 * g0 + frow;
+        if (t < NR * P && row < a.W.rows) {
+            float* o = a.out + (size_t)fc * a.out_ld + row;
+            *o = EPI == VE_RESID ? *o + acc : acc;   // x[i] += y[i] (voice.cpp:188,196)
+        }
+    }
+}
+
+// generic order (imi/core/tables.cpp:391-401): thread (row r of the group, block j) forms s = sum fma(w, x, s) over
+// the block's 32 columns for every position; then thread (row, position) folds acc = fma(d, s, acc) block by block
+template <int P, int PRO, int EPI>
+__global__ __launch_bounds__(VX_THREADS) void k_vtab_gen(vtab_args a) {
+    constexpr int R = EPI == VE_SWIGLU ? 2 : 1;   // row groups per workgroup
+    constexpr int PP = vx_pp(P), XJ = vx_xj(P);
+    static_assert(8 * R * P <= VX_THREADS, "one folding thread per (row, position)");
+    __shared__ __attribute__((aligned(16))) float xs[VX_NJ * XJ];
+    __shared__ float ss[8 * R * P * VX_SS];
+    __shared__ float ds[8 * R * VX_SS];
+    __shared__ float scl[VX_MAX_P];
+    __shared__ float ev[16 * VX_MAX_P];
+    const int t = threadIdx.x, r8 = t & 7, jl = t >> 3;
+    const int nb = a.W.nb, g0 = blockIdx.x * R;
+    if (PRO == VP_NORM) {
+        position_scales<P>(a, scl);
+        __syncthreads();
+    }
+    float acc = 0.0f;
+    for (int q = 0; q * VX_NJ < nb; q++) {
+        const int nbc = min(VX_NJ, nb - q * VX_NJ), j = q * VX_NJ + jl;
+        if (q) __syncthreads();   // the previous chunk's fold has read ss and ds
+        stage_chunk<P, PRO>(xs, a, q, nbc, scl);
+        u32x4 w[R][2];
+        if (jl < nbc) {
+#pragma unroll
+            for (int g = 0; g < R; g++) {
+                const size_t blk = ((size_t)(g0 + g) * nb + j) * 8 + r8;
+                const u32x4* cp = reinterpret_cast<const u32x4*>(a.W.codes + blk * 32);
+                w[g][0] = cp[0];
+                w[g][1] = cp[1];
+                ds[(8 * g + r8) * VX_SS + jl] = h2f(a.W.scales[blk]);
+            }
+        }
+        __syncthreads();
+        if (jl < nbc) {
+            float s[R][P];
+#pragma unroll
+            for (int g = 0; g < R; g++)
+#pragma unroll
+                for (int c = 0; c < P; c++) s[g][c] = 0.0f;
+            const float* xb = xs + jl * XJ;
+#pragma unroll 4
+            for (int kk = 0; kk < 32; kk++) {
+                float xv[PP];
+#pragma unroll
+                for (int c4 = 0; c4 < PP / 4; c4++) {
+                    const f32x4 v = *reinterpret_cast<const f32x4*>(xb + kk * PP + 4 * c4);
+                    xv[4 * c4] = v.x; xv[4 * c4 + 1] = v.y; xv[4 * c4 + 2] = v.z; xv[4 * c4 + 3] = v.w;
+                }
+#pragma unroll
+                for (int g = 0; g < R; g++) {
+                    const u32x4 h = w[g][kk >> 4];
+                    const unsigned word = (kk & 12) == 0 ? h.x : (kk & 12) == 4 ? h.y : (kk & 12) == 8 ? h.z : h.w;
+                    const float wf = (float)(int)(signed char)(word >> (8 * (kk & 3)));
+#pragma unroll
+                    for (int c = 0; c < P; c++) s[g][c] = fmaf(wf, xv[c], s[g][c]);
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < R; g++)
+#pragma unroll
+                for (int c = 0; c < P; c++) ss[((8 * g + r8) * P + c) * VX_SS + jl] = s[g][c];
+        }
+        __syncthreads();
+        if (t < 8 * R * P) {
+            const float* sp = ss + t * VX_SS;
+            const float* dp = ds + (t / P) * VX_SS;
+            for (int i = 0; i < nbc; i++) acc = fmaf(dp[i], sp[i], acc);
+        }
+    }
+    table_epilogue<P, EPI, 8 * R>(a, g0, acc, ev);
+}
+
+// scaled order (imi/core/tables.cpp:324-365, P = 12 or 6): thread (row, position) runs one chain over all columns
+// of fma(float(w) * d, x, acc); two row groups per workgroup
+template <int P, int PRO, int EPI>
+__global__ __launch_bounds__(VX_THREADS) void k_vtab_scaled(vtab_args a) {
+    constexpr int PP = vx_pp(P), XJ = vx_xj(P);
+    static_assert(16 * P <= VX_THREADS, "one thread per (row, position)");
+    __shared__ __attribute__((aligned(16))) float xs[VX_NJ * XJ];
+    __shared__ float scl[VX_MAX_P];
+    __shared__ float ev[16 * VX_MAX_P];
+    const int t = threadIdx.x, rl = t / P, c = t - rl * P;
+    const int nb = a.W.nb, g0 = blockIdx.x * 2, g = g0 + (rl >> 3), r8 = rl & 7;
+    const bool live = t < 16 * P && 8 * g < a.W.rows_pad;
+    if (PRO == VP_NORM) {
+        position_scales<P>(a, scl);
+        __syncthreads();
+    }
+    float acc = 0.0f;
+    for (int q = 0; q * VX_NJ < nb; q++) {
+        const int nbc = min(VX_NJ, nb - q * VX_NJ);
+        if (q) __syncthreads();
+        stage_chunk<P, PRO>(xs, a, q, nbc, scl);
+        __syncthreads();
+        if (live) {
+            for (int jl = 0; jl < nbc; jl++) {
+                const size_t blk = ((size_t)g * nb + q * VX_NJ + jl) * 8 + r8;
+                const float d = h2f(a.W.scales[blk]);
+                const u32x4* cp = reinterpret_cast<const u32x4*>(a.W.codes + blk * 32);
+                const u32x4 h0 = cp[0], h1 = cp[1];
+                const unsigned wd[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+                const float* xb = xs + jl * XJ + c;
+#pragma unroll
+                for (int kk = 0; kk < 32; kk++) {
+                    const float wv = (float)(int)(signed char)(wd[kk >> 2] >> (8 * (kk & 3))) * d;
+                    acc = fmaf(wv, xb[kk * PP], acc);
+                }
+            }
+        }
+    }
+    table_epilogue<P, EPI, 16>(a, g0, acc, ev);
+}
+
+// single-input order (imi/core/tables.cpp:366-382): 4 threads per row, thread o runs the chain over columns
+// k % 4 == o of fma(float(w), d * x, a_o); the row's result is (a0 + a1) + (a2 + a3)
+template <int HEAD>
+__global__ __launch_bounds__(VX_THREADS) void k_vone(vone_args a, int cols) {
+    __shared__ float xs[4096];
+    const int nrb = (a.rows + 63) / 64, set = blockIdx.x / nrb, rb = blockIdx.x - set * nrb;
+    int cb = 0;
+    const float* src = a.src;
+    if (HEAD) {   // the needed codebook's position: out_norm, then its head_norm (voice.cpp:199-203)
+        if (set >= *a.n_need) return;
+        cb = a.need[set];
+        src = a.src + (size_t)cb * cols;
+        const float s1 = rms_scale_wave(src, cols, a.eps);
+        for (int k = threadIdx.x; k < cols; k += VX_THREADS) xs[k] = src[k] * s1 * a.out_norm[k];
+        __syncthreads();
+        const float s2 = rms_scale_wave(static_cast<const float*>(xs), cols, a.eps);
+        __syncthreads();
+        const float* hn = a.head_norm + (size_t)cb * cols;
+        for (int k = threadIdx.x; k < cols; k += VX_THREADS) xs[k] = xs[k] * s2 * hn[k];
+    } else {
+        for (int k = threadIdx.x; k < cols; k += VX_THREADS) xs[k] = src[k];
+    }
+    __syncthreads();
+    const q8dev W = a.tabs[cb];
+    const int o = threadIdx.x & 3, row = rb * 64 + (threadIdx.x >> 2);
+    float acc = 0.0f;
+    if (row < W.rows_pad) {
+        const int g = row >> 3, r8 = row & 7, nb = W.nb;
+        for (int j = 0; j < nb; j++) {
+            const size_t blk = ((size_t)g * nb + j) * 8 + r8;
+            const float d = h2f(W.scales[blk]);
+            const u32x4* cp = reinterpret_cast<const u32x4*>(W.codes + blk * 32);
+            const u32x4 h0 = cp[0], h1 = cp[1];
+            const unsigned wd[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+            const float* xb = xs + 32 * j + o;
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const float wf = (float)(int)(signed char)(wd[q] >> (8 * o));
+                acc = fmaf(wf, d * xb[4 * q], acc);
+            }
+        }
+    }
+    const float pair = acc + __shfl_xor(acc, 1);    // a0 + a1 (o = 0), a2 + a3 (o = 2)
+    const float other = __shfl_xor(pair, 2);
+    const float total = (o & 2) ? other + pair : pair + other;
+    if (o == 0 && row < a.rows) a.out[(size_t)set * a.rows + row] = a.bias ? total + a.bias[row] : total;
+}
+
+// one query head per workgroup over the P positions (imi/core/voice.cpp:159-180): q/k rows rms-normed and rotated
+// by position, scores fma-chained over the head width, softmax with a float sum, sigmoid head gate
+__global__ __launch_bounds__(VX_THREADS) void k_vattn(vattn_args a) {
+    __shared__ float qq[VX_MAX_P][VX_MAX_D], kk[VX_MAX_P][VX_MAX_D];
+    __shared__ float sc[VX_MAX_P][VX_MAX_P + 1];
+    __shared__ float sm[VX_MAX_P], gt[VX_MAX_P];
+    const int P = a.P, D = a.D, hh = blockIdx.x, kv = hh / (a.n_head / a.n_kv);
+    const int Hq = a.n_head * D, Hk = a.n_kv * D, t = threadIdx.x;
+    for (int i = t; i < P * D; i += VX_THREADS) {
+        const int p = i / D, e = i - p * D;
+        const float* r = a.qkv + (size_t)p * a.n_qkv;
+        qq[p][e] = r[hh * D + e];
+        kk[p][e] = r[Hq + kv * D + e];
+    }
+    __syncthreads();
+    const int w = t >> 6, lane = t & 63, half = D / 2;
+    for (int ri = w; ri < 2 * P; ri += VX_THREADS / 64) {
+        const int p = ri < P ? ri : ri - P;
+        float* v = ri < P ? kk[p] : qq[p];
+        const float* nw = ri < P ? a.k_norm : a.q_norm;
+        const float s = rms_scale_wave(static_cast<const float*>(v), D, a.eps);
+        if (lane < half) {
+            const float x0 = v[lane] * s * nw[lane], x1 = v[lane + half] * s * nw[lane + half];
+            const float2 cs = a.rope_cs[p * half + lane];
+            v[lane] = fmaf(x0, cs.x, -(x1 * cs.y));
+            v[lane + half] = fmaf(x0, cs.y, x1 * cs.x);
+        }
+    }
+    __syncthreads();
+    if (t < P * P) {
+        const int p = t / P, u = t - p * P;
+        float s = 0.0f;
+        for (int i = 0; i < D; i++) s = fmaf(qq[p][i], kk[u][i], s);
+        sc[p][u] = s * a.scale;
+    }
+    __syncthreads();
+    if (t < P) {
+        float mx = -__builtin_inff();
+        for (int u = 0; u < P; u++) mx = mx < sc[t][u] ? sc[t][u] : mx;   // std::max(mx, sc)
+        float sum = 0.0f;
+        for (int u = 0; u < P; u++) {
+            const float e = expf_glibc(sc[t][u] - mx);
+            sc[t][u] = e;
+            sum += e;
+        }
+        sm[t] = sum;
+        gt[t] = 1.0f / (1.0f + expf_glibc(-a.qkv[(size_t)t * a.n_qkv + Hq + 2 * Hk + hh]));
+    }
+    __syncthreads();
+    for (int i = t; i < P * D; i += VX_THREADS) {
+        const int p = i / D, e = i - p * D;
+        const float* vcol = a.qkv + Hq + Hk + kv * D + e;
+        float acc = 0.0f;
+        for (int u = 0; u < P; u++) acc = fmaf(sc[p][u], vcol[(size_t)u * a.n_qkv], acc);
+        a.att[(size_t)p * Hq + hh * D + e] = acc / sm[p] * gt[p];
+    }
+}
+
+// pass input: position p's code row of codebook p (dequantized d * q), or mask_embd, plus the frame's base
+// (imi/core/voice.cpp:122-127)
+__global__ __launch_bounds__(VX_THREADS) void k_vembed(vembed_args a) {
+    const int i = blockIdx.x * VX_THREADS + threadIdx.x;
+    if (i >= a.P * a.E) return;
+    const int p = i / a.E, e = i - p * a.E, code = a.codes[p];
+    float v;
+    if (code >= 0) {
+        const q8dev T = a.tabs[p];
+        const size_t blk = ((size_t)(code >> 3) * T.nb + (e >> 5)) * 8 + (code & 7);
+        v = h2f(T.scales[blk]) * (float)T.codes[blk * 32 + (e & 31)];
+    } else {
+        v = a.mask[e];
+    }
+    a.x[i] = v + a.base[i];
+}
+
+// the brain's next input: the sum over codebooks, in order, of the chosen codes' feedback rows (voice.cpp:90-97)
+__global__ __launch_bounds__(VX_THREADS) void k_vfeed(vfeed_args a) {
+    const int i = blockIdx.x * VX_THREADS + threadIdx.x;
+    if (i >= a.n_in) return;
+    float o = 0.0f;
+    for (int c = 0; c < a.n_cb; c++) {
+        const uint8_t* blk = a.rows + (size_t)(a.codes[c] + c * a.n_vocab) * a.row_bytes + (size_t)(i >> 5) * 34;
+        const float d = h2f(*reinterpret_cast<const uint16_t*>(blk));
+        const float v = d * (float)(signed char)blk[2 + (i & 31)];
+        o = o + v;
+    }
+    a.out[i] = o;
+}
+
+template <int P, int PRO, int EPI>
+hipError_t launch_vtab_p(const vtab_args& a, hipStream_t s) {
+    if constexpr (P == 6 || P == 12)
+        hipLaunchKernelGGL((k_vtab_scaled<P, PRO, EPI>), dim3(a.units), dim3(VX_THREADS), 0, s, a);
+    else
+        hipLaunchKernelGGL((k_vtab_gen<P, PRO, EPI>), dim3(a.units), dim3(VX_THREADS), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int P>
+hipError_t launch_vtab_kind(int pro, int epi, const vtab_args& a, hipStream_t s) {
+    if (pro == VP_NORM && epi == VE_STORE) return launch_vtab_p<P, VP_NORM, VE_STORE>(a, s);
+    if (pro == VP_PLAIN && epi == VE_RESID) return launch_vtab_p<P, VP_PLAIN, VE_RESID>(a, s);
+    if (pro == VP_NORM && epi == VE_SWIGLU) return launch_vtab_p<P, VP_NORM, VE_SWIGLU>(a, s);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t launch_vtab(int P, int pro, int epi, const vtab_args& a, hipStream_t s) {
+    switch (P) {
+        case 2: return launch_vtab_kind<2>(pro, epi, a, s);
+        case 3: return launch_vtab_kind<3>(pro, epi, a, s);
+        case 4: return launch_vtab_kind<4>(pro, epi, a, s);
+        case 5: return launch_vtab_kind<5>(pro, epi, a, s);
+        case 6: return launch_vtab_kind<6>(pro, epi, a, s);
+        case 7: return launch_vtab_kind<7>(pro, epi, a, s);
+        case 8: return launch_vtab_kind<8>(pro, epi, a, s);
+        case 9: return launch_vtab_kind<9>(pro, epi, a, s);
+        case 10: return launch_vtab_kind<10>(pro, epi, a, s);
+        case 11: return launch_vtab_kind<11>(pro, epi, a, s);
+        case 12: return launch_vtab_kind<12>(pro, epi, a, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_vone(const vone_args& a, int n_sets, int cols, hipStream_t s) {
+    if (cols > 4096 || cols % 32) return hipErrorInvalidValue;
+    const int grid = n_sets * ((a.rows + 63) / 64);
+    if (a.head)
+        hipLaunchKernelGGL(k_vone<1>, dim3(grid), dim3(VX_THREADS), 0, s, a, cols);
+    else
+        hipLaunchKernelGGL(k_vone<0>, dim3(grid), dim3(VX_THREADS), 0, s, a, cols);
+    return hipGetLastError();
+}
+
+hipError_t launch_vattn(const vattn_args& a, hipStream_t s) {
+    if (a.P > VX_MAX_P || a.D > VX_MAX_D || a.D % 32) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_vattn, dim3(a.n_head), dim3(VX_THREADS), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_vembed(const vembed_args& a, hipStream_t s) {
+    hipLaunchKernelGGL(k_vembed, dim3((a.P * a.E + VX_THREADS - 1) / VX_THREADS), dim3(VX_THREADS), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_vfeed(const vfeed_args& a, hipStream_t s) {
+    hipLaunchKernelGGL(k_vfeed, dim3((a.n_in + VX_THREADS - 1) / VX_THREADS), dim3(VX_THREADS), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace sh

@@ -1,0 +1,117 @@
+"""GPU parity of the Q8_0 voice generator (C ABI: sh_voice_*) against the oracle's imi_voice restatement
+(imi/core/voice.cpp:90-206).
+
+The HIP path keeps each fp32 operation order of imi_q8g_group (the generic order for most codebook counts, the
+scaled order for 6 and 12, the single-input order for the input projection and the word scores), of the norms,
+the position rope, the attention softmax and SiLU, so the frame base, every score of every pass and the feedback row
+sum equal the oracle's bit for bit. Each test plays frames the way imi's talk loop does (imi/core/talk.cpp:127-187):
+begin_frame from a brain hidden state, masked passes that each score a few codebooks and fix their codes (here the
+first index of the maximum, in place of sampling), then the feedback row sum.
+"""
+import numpy as np
+import pytest
+
+from conftest import rel
+
+pytestmark = pytest.mark.gpu
+
+
+def same(a, b) -> bool:
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def _shape(**kw):
+    from nunchi_amd import synth
+    base = dict(n_embd=256, n_layer=2, n_head=4, n_head_kv=2, head_dim=64, n_ff=512, n_vocab=256, n_cb=8, n_in=256)
+    base.update(kw)
+    return synth.VoiceShape(**base)
+
+
+def _play(path, seed, schedule, n_frames=2, threads=4):
+    import nunchi_amd
+    import oracle
+    g = nunchi_amd.Voice(path)
+    o = oracle.Voice(path, threads=threads)
+    assert (g.n_embd, g.n_vocab, g.n_cb, g.n_in, g.n_head, g.n_head_kv, g.head_dim, g.n_ff, g.n_layer) == \
+        (o.n_embd, o.n_vocab, o.n_cb, o.n_in, o.n_head, o.n_head_kv, o.head_dim, o.n_ff, o.n_layer)
+    rng = np.random.default_rng(seed)
+    for f in range(n_frames):
+        h = rng.standard_normal(g.n_in).astype(np.float32)
+        g.begin_frame(h)
+        o.begin_frame(h)
+        assert same(g.base(), o.base()), f"frame {f}: base differs (rel {rel(g.base(), o.base()):.2e})"
+        codes = np.full(g.n_cb, -1, np.int32)
+        start = 0
+        for n in schedule:
+            need = np.arange(start, start + n, dtype=np.int32)
+            sg = g.pass_(codes, need)
+            so = o.pass_(codes, need)
+            assert np.isfinite(sg).all()
+            assert same(sg, so), f"frame {f}, codebooks {need.tolist()}: scores differ (rel {rel(sg, so):.2e})"
+            codes[need] = np.argmax(so, axis=1)
+            start += n
+        fg = g.feedback(codes)
+        fo = o.feedback(codes)
+        assert same(fg, fo), f"frame {f}: feedback differs (rel {rel(fg, fo):.2e})"
+    return g, o
+
+
+def test_tiny_voice_frames(tiny_voice):
+    """8 codebooks: the generic order; passes of 4 + 4 codebooks."""
+    _play(tiny_voice, 1, (4, 4))
+
+
+@pytest.mark.parametrize("n_cb,schedule", [(12, (6, 6)), (6, (3, 3)), (5, (2, 3)), (2, (1, 1))])
+def test_codebook_counts(model_dir, n_cb, schedule):
+    """12 and 6 codebooks take the scaled order (imi's 12-codebook talk schedule is {6, 6}); 5 and 2 the generic one."""
+    from nunchi_amd import synth
+    path = synth.cached("voice", _shape(n_cb=n_cb), 3, model_dir)
+    _play(path, n_cb, schedule, n_frames=1)
+
+
+def test_narrow_heads_and_odd_groups(model_dir):
+    """head_dim 32, 4 query heads per kv head, widths that are not powers of two, an odd number of qkvg row groups."""
+    from nunchi_amd import synth
+    path = synth.cached("voice", _shape(n_head=8, n_head_kv=2, head_dim=32, n_ff=288, n_embd=192, n_in=96), 5, model_dir)
+    _play(path, 5, (3, 5), n_frames=1)
+
+
+def test_wide_inputs(model_dir):
+    """n_ff > 1024 and an input projection wider than one staged chunk: several input chunks per table."""
+    from nunchi_amd import synth
+    path = synth.cached("voice", _shape(n_ff=2112, n_in=2048, n_embd=320, n_vocab=96), 6, model_dir)
+    _play(path, 6, (8,), n_frames=1)
+
+
+def test_pass_arguments(tiny_voice):
+    """No codebooks needed: nothing is scored; a codebook twice: the same scores twice; bad codes are refused."""
+    import nunchi_amd
+    import oracle
+    g = nunchi_amd.Voice(tiny_voice)
+    o = oracle.Voice(tiny_voice, threads=2)
+    h = np.random.default_rng(0).standard_normal(g.n_in).astype(np.float32)
+    g.begin_frame(h)
+    o.begin_frame(h)
+    codes = np.full(g.n_cb, -1, np.int32)
+    assert g.pass_(codes, []).shape == (0, g.n_vocab)
+    sg = g.pass_(codes, [2, 2, 7])
+    assert same(sg, o.pass_(codes, [2, 2, 7])) and same(sg[0], sg[1])
+    bad = codes.copy()
+    bad[1] = g.n_vocab
+    with pytest.raises(nunchi_amd.SeoulError):
+        g.pass_(bad, [0])
+    with pytest.raises(nunchi_amd.SeoulError):
+        g.pass_(codes, [g.n_cb])
+    with pytest.raises(nunchi_amd.SeoulError):
+        g.feedback(codes)   # masked codes have no feedback row
+    # the generator still works after refused calls
+    assert same(g.pass_(codes, [0]), o.pass_(codes, [0]))
+
+
+def test_full_voice_frame(model_dir):
+    """The live voice frame's generator (6 layers, hidden 1024, FFN 4096, 8 codebooks x 2048 codes, 16/4 heads x
+    64), passes of 4 + 4 codebooks."""
+    from nunchi_amd import synth
+    path = synth.cached("voice", synth.VOICE, 1, model_dir)
+    _play(path, 11, (4, 4), n_frames=1, threads=8)
