@@ -84,6 +84,79 @@ def cpu_decode(path, threads, steps, b2: bool, runs: int = 1):
     return tok / secs, ids0, secs
 
 
+VOICE_CTX = 4096      # slot A's KV context in the voice frame
+A_POS = 2048          # slot A's position when the timed frames start
+SCHEDULE = ((0, 1, 2, 3), (4, 5, 6, 7))   # masked passes of a frame: codebooks scored (and fixed) by each
+
+
+def play_frames(step2, voice, tok_a, fb, frames):
+    """Voice frames as imi's talk loop runs them (imi/core/talk.cpp:127-187) with slot A riding along
+    (imi/core/flow.cpp:118): step2 (A: text step with scores, B: the voice brain step fed the last feedback row sum),
+    begin_frame from B's hidden state, the masked passes (each fixes its codebooks' codes; the first index of the
+    maximum stands in for sampling), then the feedback row sum. Returns per-frame seconds, the step2 and generator
+    shares, the codes of every frame and slot A's ids."""
+    tot, br, vo, codes_all, ids = [], [], [], [], []
+    for _ in range(frames):
+        t0 = time.perf_counter()
+        tok_a, hb = step2(tok_a, fb)
+        t1 = time.perf_counter()
+        voice.begin_frame(hb)
+        codes = np.full(voice.n_cb, -1, np.int32)
+        for need in SCHEDULE:
+            sc = voice.pass_(codes, need)
+            codes[list(need)] = np.argmax(sc, axis=1)
+        fb = voice.feedback(codes)
+        t2 = time.perf_counter()
+        tot.append(t2 - t0)
+        br.append(t1 - t0)
+        vo.append(t2 - t1)
+        codes_all.append(codes)
+        ids.append(tok_a)
+    return np.array(tot), np.array(br), np.array(vo), np.array(codes_all), ids, tok_a, fb
+
+
+def gpu_voice_frames(brain_path, voice_path, frames, warmup):
+    import nunchi_amd
+    brain = nunchi_amd.Brain(brain_path, n_ctx=VOICE_CTX)
+    voice = nunchi_amd.Voice(voice_path)
+    sa, sb = brain.new_state(), brain.new_state()
+    pa = _prompt(2, brain.n_vocab)
+    for i in range(PROMPT):
+        _, _, ba = brain.step(int(pa[i]), want_logits=i == PROMPT - 1, st=sa)
+    ids, _ = brain.generate(ba, A_POS - PROMPT, a=sa)
+
+    def step2(tok, fb):
+        (_, _, best), (hb, _, _) = brain.step2(tok, None, True, sb, -1, fb, False, a=sa)
+        return best, hb
+
+    fb = voice.feedback(np.zeros(voice.n_cb, np.int32))
+    ref = play_frames(step2, voice, int(ids[-1]), fb, frames + warmup)
+    # the timed frames are the frames after the warmup ones, in the same run (states keep advancing)
+    out = tuple(x[warmup:] for x in ref[:4]) + (ref[4][warmup:],)
+    info = {"table_bytes": voice.table_bytes, "n_cb": voice.n_cb}
+    voice.close()
+    brain.ctx.close()
+    return out, ref, info
+
+
+def cpu_voice_frames(brain_path, voice_path, threads, frames):
+    import oracle
+    eng = oracle.Engine(brain_path, threads=threads, n_ctx=VOICE_CTX)
+    voice = oracle.Voice(voice_path, threads=threads)
+    pa = _prompt(2, eng.n_vocab)
+    for i in range(PROMPT):
+        _, lg = eng.step(int(pa[i]), want_logits=i == PROMPT - 1)
+    ids, _ = eng.greedy(oracle.top(lg), A_POS - PROMPT)
+    st = eng.new_state()
+
+    def step2(tok, fb):
+        _, la, hb, _ = eng.step2(tok, None, True, st, -1, fb, False)
+        return oracle.top(la), hb
+
+    fb = voice.feedback(np.zeros(voice.n_cb, np.int32))
+    return play_frames(step2, voice, int(ids[-1]), fb, frames)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -92,6 +165,8 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, cores in the affinity mask)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=8, help="B=1 conversations timed on the CPU (B=2: half as many pairs)")
+    ap.add_argument("--voice-frames", type=int, default=64, help="timed voice frames (cfg 4); 0 = skip")
+    ap.add_argument("--cpu-voice-frames", type=int, default=8)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (conversations shard across "
@@ -182,6 +257,23 @@ def main():
                                     "frac": round(cfg0_bytes / cfg0_us / 1e3 / HBM_PEAK_GBS, 4)},
         },
     }
+    if args.voice_frames:
+        vpath = synth.cached("voice", synth.VOICE, 1)
+        (ft, fbr, fvo, fcodes, fids), fref, vinfo = gpu_voice_frames(path, vpath, args.voice_frames, 4)
+        line["voice_frame"] = {
+            "workload": "cfg4: step2 of the cfg2 model (slot A: text step with scores at KV context 4096, from position "
+                        f"{A_POS}; slot B: voice brain step fed the feedback row sum), then the Q8_0 generator "
+                        "(6 layers, hidden 1024, FFN 4096, 16/4 heads x 64, 8 codebooks x 2048) in passes of 4 + 4 "
+                        "codebooks, then the feedback row sum; host argmax in place of sampling",
+            "frames": int(len(ft)),
+            "p50_ms": round(float(np.percentile(ft, 50)) * 1e3, 3),
+            "p99_ms": round(float(np.percentile(ft, 99)) * 1e3, 3),
+            "mean_ms": round(float(ft.mean()) * 1e3, 3),
+            "step2_p50_ms": round(float(np.percentile(fbr, 50)) * 1e3, 3),
+            "generator_p50_ms": round(float(np.percentile(fvo, 50)) * 1e3, 3),
+            "generator_table_bytes": int(vinfo["table_bytes"]),
+            "budget_ms": 80.0,
+        }
     if not args.no_cpu:
         aff = len(os.sched_getaffinity(0))
         threads = args.cpu_threads or min(16, aff)
@@ -200,6 +292,18 @@ def main():
         }
         line["speedup_vs_cpu"] = {"b1": round(tok_s_b1 / c1, 1), "b2": round(tok_s_b2 / c2, 1)}
         line["greedy_ids_match_cpu"] = same
+        if args.voice_frames and args.cpu_voice_frames:
+            ct, cbr, cvo, ccodes, cids, _, _ = cpu_voice_frames(path, vpath, threads, args.cpu_voice_frames)
+            n = len(ct)
+            line["voice_frame"]["cpu"] = {
+                "p50_ms": round(float(np.percentile(ct, 50)) * 1e3, 2),
+                "step2_p50_ms": round(float(np.percentile(cbr, 50)) * 1e3, 2),
+                "generator_p50_ms": round(float(np.percentile(cvo, 50)) * 1e3, 2),
+                "frames": n, "cores": threads, "kind": "port",
+                "sample": f"the first {n} frames of the same run on the oracle (C++ restatement of imi's engine and voice "
+                          "generator; its 8-codebook pass tables take imi's scalar generic order)",
+            }
+            line["voice_frame"]["codes_match_cpu"] = bool(np.array_equal(ccodes, fref[3][:n]) and cids == fref[4][:n])
     print(json.dumps(line), flush=True)
 
 

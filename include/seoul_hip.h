@@ -77,7 +77,8 @@ int sh_step2(sh_ctx* ctx, sh_state* a, int32_t token_a, const float* embd_a, int
 
 /* n positions at once (imi_seoul::step_batch, seoul.cpp:490-517): tokens[n] or embd[n][n_embd]. hidden_last
  * gets the last position's hidden state, hidden_all[n][n_embd] (nullable) every position's; logits/best are the
- * last position's. */
+ * last position's. For n >= 2 the positions go through each table together on the int8 matrix cores (the
+ * prefill); every number equals n single steps. The whole batch must fit the context, else nothing is stepped. */
 int sh_step_batch(sh_ctx* ctx, sh_state* st, const int32_t* tokens, const float* embd, int n, int want_logits,
                   float* hidden_last, float* logits, float* hidden_all, int32_t* best);
 
@@ -105,6 +106,10 @@ int sh_q4_free(sh_q4* t);
 /* y[n_in][rows] = W x[n_in][cols] for n_in in {1, 2}; the input is cut to int8 per 32 columns with round half to
  * even (cut_mode 0, imi/core/vec.h:47-75) or half away from zero (cut_mode 1, imi/kernels/q4x8.cpp:38-48). */
 int sh_q4_gemv(sh_ctx* ctx, const sh_q4* t, const float* x, int n_in, float* y, int cut_mode);
+/* y[n][rows] = W x[n][cols] for 1 <= n <= 512 inputs through the prefill's int8 matrix-core product: each input cut
+ * to int8 per 32 columns (round half to even), each 32-column block's integer sum exact, then imi's per-row chains
+ * over the blocks (imi_q4_group_batch, imi/core/tables.cpp:419-454); bit for bit sh_q4_gemv per input. */
+int sh_q4_gemm(sh_ctx* ctx, const sh_q4* t, const float* x, int n, float* y);
 /* Dequantized rows: out[n][cols] = (code - 8) * d of rows ids[n] (the input-row lookup of a tied word table,
  * imi/core/seoul.cpp:363, ggml_get_rows in imi/brain.cpp:161). Bit-exact. */
 int sh_q4_rows(sh_ctx* ctx, const sh_q4* t, const int32_t* ids, int n, float* out);

@@ -22,7 +22,7 @@ EXPORTS = [
     "sh_last_error", "sh_create", "sh_destroy", "sh_load", "sh_info", "sh_state_new", "sh_state_free", "sh_state_reset",
     "sh_state_pos", "sh_state_set_pos", "sh_step", "sh_step2", "sh_step_batch", "sh_generate", "sh_bench_tables",
     "sh_bench_kernel",
-    "sh_q4_create", "sh_q4_free", "sh_q4_rows", "sh_q4_gemv", "sh_q4_gemv_dev", "sh_q4_bench", "sh_expf", "sh_sync",
+    "sh_q4_create", "sh_q4_free", "sh_q4_rows", "sh_q4_gemv", "sh_q4_gemm", "sh_q4_gemv_dev", "sh_q4_bench", "sh_expf", "sh_sync",
     "sh_step_trace",
     "sh_voice_load", "sh_voice_free", "sh_voice_info", "sh_voice_begin_frame", "sh_voice_base", "sh_voice_pass",
     "sh_voice_feedback",
@@ -84,6 +84,7 @@ def load_library(path: str = LIB_PATH):
         "sh_q4_rows": (i, [vp, vp, vp, i, vp]),
         "sh_q4_gemv": (i, [vp, vp, vp, i, vp, i]),
         "sh_q4_gemv_dev": (i, [vp, vp, vp, i, vp, i]),
+        "sh_q4_gemm": (i, [vp, vp, vp, i, vp]),
         "sh_q4_bench": (i, [vp, vp, i, i, i, i, P(d)]),
         "sh_expf": (i, [vp, vp, C.c_longlong, vp]),
         "sh_sync": (i, [vp]),
@@ -320,6 +321,14 @@ class Q4Table:
         y = np.zeros((n_in, self.rows), np.float32)
         _check(_lib.sh_q4_gemv(self.ctx.h, self.h, _p(x.reshape(-1)), n_in, _p(y.reshape(-1)), int(cut_mode)))
         return y[0] if x.ndim == 1 else y
+
+
+    def gemm(self, x: np.ndarray) -> np.ndarray:
+        """n inputs through the prefill's matrix-core product (imi_q4_group_batch arithmetic)."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, self.cols)
+        y = np.zeros((x.shape[0], self.rows), np.float32)
+        _check(_lib.sh_q4_gemm(self.ctx.h, self.h, _p(x), int(x.shape[0]), _p(y)))
+        return y
 
 
 def q4_bench(ctx: Context, tables, n_in: int = 1, cut_mode: int = 0, reps: int = 200) -> float:

@@ -16,16 +16,7 @@
 #include <vector>
 
 #include "gguf_file.h"
-#include "sh_kernels.h"
-#include "sh_step.h"
-
-namespace sh {
-hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hipStream_t s, hipEvent_t t0 = nullptr, hipEvent_t t1 = nullptr);
-hipError_t launch_attn(int M, const attn_args& a, hipStream_t s);
-hipError_t launch_final(int M, const final_args& a, hipStream_t s);
-hipError_t launch_q4_rows(const q4dev& T, const int32_t* ids, int n, float* out, hipStream_t s);
-hipError_t launch_expf(const float* x, float* y, long long n, hipStream_t s);
-}
+#include "sh_ctx.h"
 
 using namespace sh;
 
@@ -40,26 +31,6 @@ int fail(int code, const std::string& msg) {
         hipError_t e_ = (x);                                                                               \
         if (e_ != hipSuccess) return fail(SH_E_HIP, std::string(#x) + ": " + hipGetErrorString(e_));       \
     } while (0)
-
-// one device allocation carved into 256-byte aligned pieces
-struct arena {
-    char* base = nullptr;
-    size_t size = 0, used = 0;
-    void* take(size_t n) {
-        const size_t at = (used + 255) / 256 * 256;
-        if (at + n > size) return nullptr;
-        used = at + n;
-        return base + at;
-    }
-};
-
-struct layer_dev {
-    bool conv = false, swa = false;
-    int ai = -1, ci = -1;
-    q4dev in_proj, out_proj, qkvg, o, gate_up, down;
-    const float *attn_norm = nullptr, *post_attn_norm = nullptr, *ffn_norm = nullptr, *post_ffn_norm = nullptr;
-    const float *q_norm = nullptr, *k_norm = nullptr, *conv_w = nullptr;
-};
 
 // Q4_0 rows (tensor, row) -> device layout in a host staging buffer: codes [rows][nb][16], scales [rows/8][nb][8]
 bool repack_q4(const std::vector<std::pair<const gg_tensor*, int>>& rows, std::vector<uint8_t>& codes, std::vector<uint16_t>& scales, int* cols) {
@@ -88,75 +59,6 @@ bool repack_q4(const std::vector<std::pair<const gg_tensor*, int>>& rows, std::v
 namespace sh {
 int set_error(int code, const std::string& msg) { return fail(code, msg); }   // for the other host files
 }
-
-struct sh_q4 {
-    sh_ctx* ctx = nullptr;
-    q4dev t;
-    void* mem = nullptr;
-};
-
-struct sh_state {
-    sh_ctx* ctx = nullptr;
-    uint16_t* kc = nullptr;
-    uint16_t* vc = nullptr;
-    float* conv = nullptr;
-    int pos = 0;
-};
-
-struct sh_ctx {
-    int device = 0;
-    hipStream_t stream = nullptr;
-    hipEvent_t ev0 = nullptr, ev1 = nullptr;
-    bool loaded = false;
-    sh_model_info info{};
-    float eps = 1e-5f, rope_base = 1e6f, rope_base_swa = 1e4f;
-    arena w;                         // weights + norms + rope tables
-    std::vector<layer_dev> layers;
-    q4dev vocab;
-    const float* out_norm = nullptr;
-    const float2* rope_cs = nullptr;
-    const float2* rope_cs_swa = nullptr;
-    int n_conv = 0, nqkv = 0;
-    // work buffers (device)
-    arena work;
-    float *xbuf[2] = {nullptr, nullptr}, *y = nullptr, *u = nullptr, *qkv = nullptr, *att = nullptr, *act = nullptr, *fo = nullptr;
-    float *hidden = nullptr, *logits = nullptr, *embd_stage = nullptr, *part_v = nullptr;
-    int* part_i = nullptr;
-    int32_t* gen_out = nullptr;       // device-side greedy ids [2][gen_cap]
-    int gen_cap = 0;
-    float* bench_x = nullptr;         // kernel-API input/output staging
-    float* bench_y = nullptr;
-    size_t bench_cap = 0;
-    step_params* P_dev = nullptr;
-    step_params* P_host = nullptr;    // pinned
-    int vocab_grid = 2048;
-    hipGraphExec_t graph[3][2] = {{nullptr, nullptr}, {nullptr, nullptr}, {nullptr, nullptr}};
-    std::vector<sh_state*> states;    // live children: destroying the context releases their device memory
-    std::vector<sh_q4*> tables;
-    // the step replays a captured graph; SEOUL_HIP_GRAPHS=0 enqueues the same kernels directly (for tools that do
-    // not trace graph launches)
-    bool use_graphs = true;
-    // persistent step kernel: its program, tagged record buffers and per-launch staging
-    bool use_persistent = true;       // SEOUL_HIP_STEP=kernels selects the graph of per-table kernels
-    std::vector<sk_stage> sk_host;
-    sk_stage* sk_dev = nullptr;
-    char* sk_mem = nullptr;
-    unsigned long long* sk_part = nullptr;
-    int* sk_err = nullptr;
-    int sk_grid = 0;
-    long long sk_timeout = 0;
-    double ticks_per_us = 100.0;
-    unsigned epoch = 1;
-    int io_cap = 0;
-    int32_t* io_tok = nullptr;        // [2][io_cap]
-    float* io_embd = nullptr;         // [2][io_cap][E]
-    int32_t* io_ids = nullptr;        // [2][io_cap]
-    float* io_hidden = nullptr;       // [2][io_cap][E]
-    bool want_trace = false;
-    long long* trace = nullptr;
-    long long trace_cap = 0;
-    int trace_per_wg = 0;
-};
 
 namespace {
 template <class T> void forget(std::vector<T*>& v, T* p) {
@@ -551,6 +453,8 @@ int sh_create(int device, sh_ctx** out) {
     c->use_graphs = !(g && g[0] == '0');
     const char* sp = getenv("SEOUL_HIP_STEP");
     c->use_persistent = !(sp && strcmp(sp, "kernels") == 0);
+    const char* pf = getenv("SEOUL_HIP_PREFILL");
+    c->use_prefill = !(pf && strcmp(pf, "0") == 0);
     const char* tr = getenv("SEOUL_HIP_TRACE");
     c->want_trace = tr && tr[0] == '1';
     *out = c.release();
@@ -568,6 +472,7 @@ int sh_destroy(sh_ctx* c) {
             if (g) (void)hipGraphExecDestroy(g);
     if (c->w.base) (void)hipFree(c->w.base);
     if (c->work.base) (void)hipFree(c->work.base);
+    if (c->pf_mem) (void)hipFree(c->pf_mem);
     if (c->bench_x) (void)hipFree(c->bench_x);
     if (c->bench_y) (void)hipFree(c->bench_y);
     if (c->P_dev) (void)hipFree(c->P_dev);
@@ -1120,6 +1025,8 @@ int sh_step_batch(sh_ctx* c, sh_state* s, const int32_t* tokens, const float* em
     if (!c || !c->loaded) return fail(SH_E_STATE, "sh_step_batch: no model loaded");
     if (!s || n < 0 || (!tokens && !embd)) return fail(SH_E_ARG, "sh_step_batch: bad argument");
     const int E = c->info.n_embd;
+    if (s->ctx != c) return fail(SH_E_STATE, "sh_step_batch: state belongs to another context");
+    if (c->use_prefill && n >= 2) return run_prefill(c, s, tokens, embd, n, want_logits != 0, hidden_last, logits, hidden_all, best);
     if (c->use_persistent) {
         sh_state* st[2] = {s, nullptr};
         launch_io io;

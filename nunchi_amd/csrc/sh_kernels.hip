@@ -438,6 +438,7 @@ hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hi
     SH_GEMV_CASE(1, 1, PRO_RESID_NORM, EPI_CONV, 3) SH_GEMV_CASE(2, 1, PRO_RESID_NORM, EPI_CONV, 3)
     SH_GEMV_CASE(1, 1, PRO_RESID_NORM, EPI_SWIGLU, 2) SH_GEMV_CASE(2, 1, PRO_RESID_NORM, EPI_SWIGLU, 2)
     SH_GEMV_CASE(1, 1, PRO_RESID_NORM, EPI_LOGITS, 1) SH_GEMV_CASE(2, 1, PRO_RESID_NORM, EPI_LOGITS, 1)
+    SH_GEMV_CASE(1, 1, PRO_CUT, EPI_LOGITS, 1)
     return hipErrorInvalidValue;
 }
 

@@ -1,0 +1,430 @@
+// Prefill kernels (imi_seoul::step_batch / run_batch, imi/core/seoul.cpp:490-655) for gfx950.
+//
+// Per layer: the table products run on the int8 matrix cores, everything between them (norms, cuts, the short conv,
+// attention) as per-position kernels. Every fp32 operation is the one imi's CPU path does for that position, in the
+// same order, so hidden states and word scores equal n single steps bit for bit.
+#include "sh_device.h"
+#include "sh_prefill.h"
+
+namespace sh {
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void load32(const float* p, float* v) {
+    const f32x4* q = reinterpret_cast<const f32x4*>(p);
+#pragma unroll
+    for (int k = 0; k < 8; k++) { const f32x4 t = q[k]; v[4 * k] = t.x; v[4 * k + 1] = t.y; v[4 * k + 2] = t.z; v[4 * k + 3] = t.w; }
+}
+
+// cut 32 floats (imi/core/vec.h:47-75, round half to even) into block j of position p of a block-major cut
+__device__ __forceinline__ void cut_store(const pf_cut& c, int n, int j, int p, const float* v) {
+    int q8[8], sum;
+    const float d = cut32(v, q8, &sum, false);
+    u32x4* qp = reinterpret_cast<u32x4*>(c.q + ((size_t)j * n + p) * 32);
+    qp[0] = u32x4{(unsigned)q8[0], (unsigned)q8[1], (unsigned)q8[2], (unsigned)q8[3]};
+    qp[1] = u32x4{(unsigned)q8[4], (unsigned)q8[5], (unsigned)q8[6], (unsigned)q8[7]};
+    c.d[(size_t)j * n + p] = d;
+    c.s[(size_t)j * n + p] = d * (float)sum;
+}
+
+// ---------------------------------------------------------------- per-position norms
+// PFR_FIRST: x = the word's dequantized row ((code - 8) * d) or the given embedding row (imi/core/seoul.cpp:363-364);
+// PFR_RESID: x = fma(y * rms(y), w_post, x) (imi/core/vec.h:41-44); then h = x * rms(x) * w_pre, cut or stored
+template <int MODE>
+__global__ __launch_bounds__(256) void k_pf_rows(pf_rows_args a) {
+    __shared__ __attribute__((aligned(16))) float xs[2048];
+    __shared__ __attribute__((aligned(16))) float hs[2048];
+    __shared__ float red[2];
+    const int p = blockIdx.x, tid = threadIdx.x, E = a.E, nb = E / 32;
+    float* xr = a.x + (size_t)p * E;
+    if (MODE == PFR_FIRST) {
+        const int tok = a.tokens ? a.tokens[p] : -1;
+        if (tok >= 0) {
+            for (int j = tid; j < nb; j += 256) {
+                const u32x4 c = reinterpret_cast<const u32x4*>(a.vocab.codes)[(size_t)tok * nb + j];
+                const float d = h2f(reinterpret_cast<const uint16_t*>(a.vocab.scales)[((size_t)(tok >> 3) * nb + j) * 8 + (tok & 7)]);
+                const unsigned w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const unsigned byte = (w[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+                    xs[32 * j + i] = (float)((int)(byte & 15u) - 8) * d;
+                    xs[32 * j + 16 + i] = (float)((int)(byte >> 4) - 8) * d;
+                }
+            }
+        } else {
+            for (int i = tid; i < E; i += 256) xs[i] = a.embd[(size_t)p * E + i];
+        }
+        __syncthreads();
+        for (int i = tid; i < E; i += 256) xr[i] = xs[i];
+    } else {
+        const float* yr = a.y + (size_t)p * E;
+        for (int i = tid; i < E; i += 256) hs[i] = yr[i];
+        __syncthreads();
+        if (tid < 64) {
+            const float s = rms_scale_wave(static_cast<const float*>(hs), E, a.eps);
+            if (tid == 0) red[0] = s;
+        }
+        __syncthreads();
+        const float sc1 = red[0];
+        for (int i = tid; i < E; i += 256) {
+            const float v = fmaf(hs[i] * sc1, a.w_post[i], xr[i]);
+            xs[i] = v;
+            xr[i] = v;
+        }
+        __syncthreads();
+    }
+    if (tid < 64) {
+        const float s = rms_scale_wave(static_cast<const float*>(xs), E, a.eps);
+        if (tid == 0) red[1] = s;
+    }
+    __syncthreads();
+    const float sc2 = red[1];
+    for (int i = tid; i < E; i += 256) {
+        const float h = xs[i] * sc2 * a.w_pre[i];
+        hs[i] = h;
+        if (a.hidden) a.hidden[(size_t)p * E + i] = h;
+    }
+    if (!a.cut.q) return;
+    __syncthreads();
+    for (int j = tid; j < nb; j += 256) cut_store(a.cut, a.n, j, p, hs + 32 * j);
+}
+
+// ---------------------------------------------------------------- cut of n rows
+__global__ __launch_bounds__(256) void k_pf_cut(pf_cutk_args a) {
+    const int nb = a.K / 32, idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= a.n * nb) return;
+    const int j = idx / a.n, p = idx - j * a.n;
+    float v[32];
+    load32(a.src + (size_t)p * a.ld + 32 * j, v);
+    cut_store(a.cut, a.n, j, p, v);
+}
+
+// ---------------------------------------------------------------- table products on the matrix cores
+// Workgroup tile 64 rows x 64 positions, wave tile 32 x 32 (2 x 2 products of 16 x 16 per 32-column block).
+// v_mfma_i32_16x16x32_i8 operands: lane l holds row / position l % 16, columns 8 (l / 16) .. + 7 of the block;
+// the result's lane l holds rows 4 (l / 16) + i (i < 4) at position l % 16. The weight codes enter as they are
+// stored (0..15), the input as its int8 cut, so each product is imi's integer block sum exactly; then per (row,
+// position), block by block in order: acc = fma(float(isum), d * dx, acc), cor = fma(d, s, cor), and at the end
+// out = fma(-8, cor, acc) (imi/core/tables.cpp:419-454, the batch kernel imi's prefill uses).
+template <int EPI>
+__global__ __launch_bounds__(256) void k_pf_gemm(pf_gemm_args a) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int li = lane & 15, lq = lane >> 4;
+    const int rows = a.W.rows, n = a.n, nb = a.W.nb;
+    const int rbase = blockIdx.x * 64 + (w & 1) * 32, pbase = blockIdx.y * 64 + (w >> 1) * 32;
+    if (rbase >= rows || pbase >= n) return;   // whole waves; no barriers below
+    const uint8_t* codes = static_cast<const uint8_t*>(a.W.codes);
+    const uint16_t* scales = static_cast<const uint16_t*>(a.W.scales);
+    const uint8_t* ap[2];
+    const uint16_t* dp[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++) {
+        const int r = min(rbase + 16 * mt + li, rows - 1);              // operand row (clamped: results dropped)
+        ap[mt] = codes + (size_t)r * nb * 16 + (lq & 1) * 8;            // bytes 0-7 or 8-15 of the row's block
+        const int rd = min(rbase + 16 * mt + 4 * lq, rows - 4);         // first of the 4 result rows
+        dp[mt] = scales + (size_t)(rd >> 3) * nb * 8 + (rd & 7);
+    }
+    const int shift = (lq >> 1) * 4;   // columns 0-15: low nibbles, 16-31: high nibbles
+    int pp[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++) pp[nt] = min(pbase + 16 * nt + li, n - 1);
+
+    float acc[2][2][4], cor[2][2][4];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) { acc[mt][nt][i] = 0.0f; cor[mt][nt][i] = 0.0f; }
+
+    // operands of block j, fetched one block ahead
+    uint2 ra[2], rs[2];
+    long rb[2];
+    float fx[2], fs[2];
+    auto fetch = [&](int j) {
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++) {
+            ra[mt] = *reinterpret_cast<const uint2*>(ap[mt] + (size_t)j * 16);
+            rs[mt] = *reinterpret_cast<const uint2*>(dp[mt] + (size_t)j * 8);
+        }
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++) {
+            const size_t o = (size_t)j * n + pp[nt];
+            rb[nt] = *reinterpret_cast<const long*>(a.in.q + o * 32 + lq * 8);
+            fx[nt] = a.in.d[o];
+            fs[nt] = a.in.s[o];
+        }
+    };
+    fetch(0);
+    for (int j = 0; j < nb; j++) {
+        const uint2 ca[2] = {ra[0], ra[1]}, cs[2] = {rs[0], rs[1]};
+        const long cb[2] = {rb[0], rb[1]};
+        const float cx[2] = {fx[0], fx[1]}, cz[2] = {fs[0], fs[1]};
+        if (j + 1 < nb) fetch(j + 1);
+        i32x4 isum[2][2];
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++) {
+            const unsigned lo = (ca[mt].x >> shift) & 0x0F0F0F0Fu, hi = (ca[mt].y >> shift) & 0x0F0F0F0Fu;
+            const long av = (long)((unsigned long)lo | ((unsigned long)hi << 32));
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++)
+                isum[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, cb[nt], i32x4{0, 0, 0, 0}, 0, 0, 0);
+        }
+#pragma unroll
+        for (int mt = 0; mt < 2; mt++) {
+            const float dd[4] = {h2f((uint16_t)(cs[mt].x & 0xFFFFu)), h2f((uint16_t)(cs[mt].x >> 16)),
+                                 h2f((uint16_t)(cs[mt].y & 0xFFFFu)), h2f((uint16_t)(cs[mt].y >> 16))};
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    acc[mt][nt][i] = fmaf((float)isum[mt][nt][i], dd[i] * cx[nt], acc[mt][nt][i]);
+                    cor[mt][nt][i] = fmaf(dd[i], cz[nt], cor[mt][nt][i]);
+                }
+        }
+    }
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++) {
+            const int p = pbase + 16 * nt + li, r0 = rbase + 16 * mt + 4 * lq;
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = fmaf(-8.0f, cor[mt][nt][i], acc[mt][nt][i]);
+            if (EPI == EPI_SWIGLU) {
+                // rows 0-7 of the 16-row tile are a gate group, rows 8-15 the matching up group (lanes + 32)
+                float up[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) up[i] = __shfl_xor(v[i], 32);
+                if (lq < 2 && p < n) {
+                    float* o = a.out + (size_t)p * a.out_ld + (rbase + 16 * mt) / 2 + 4 * lq;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) o[i] = silu(v[i]) * up[i];
+                }
+            } else if (p < n) {
+                float* o = a.out + (size_t)p * a.out_ld + r0;
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (r0 + i < rows) o[i] = v[i];
+            }
+        }
+}
+
+// ---------------------------------------------------------------- gated short conv along positions
+// thread (position p, 32 channels): u = c * (b x w_d + taps), the taps being the b x values of the d_conv positions
+// before p (from this batch, or the conversation's conv memory before it), fma-chained oldest first
+// (imi/core/seoul.cpp:562-577); then the cut of the 32 outputs
+__global__ __launch_bounds__(256) void k_pf_conv(pf_conv_args a) {
+    const int nbk = a.E / 32, idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= a.n * nbk) return;
+    const int t = idx / a.n, p = idx - t * a.n, E = a.E, dc = a.d_conv;
+    const size_t ld = 3 * (size_t)E;
+    float u[32];
+    for (int c = 0; c < 32; c++) {
+        const int e = 32 * t + c, ub = 96 * t + 24 * (c >> 3) + (c & 7);
+        const float* r = a.bcx + (size_t)p * ld + ub;
+        const float bx = r[0] * r[16];
+        float s = bx * a.w[(size_t)dc * E + e];
+        for (int tt = 0; tt < dc; tt++) {
+            const int q = p - dc + tt;
+            float st;
+            if (q >= 0) {
+                const float* rq = a.bcx + (size_t)q * ld + ub;
+                st = rq[0] * rq[16];
+            } else {
+                st = a.state[(size_t)(p + tt) * E + e];
+            }
+            s = fmaf(st, a.w[(size_t)tt * E + e], s);
+        }
+        u[c] = s * r[8];
+    }
+    cut_store(a.cut, a.n, t, p, u);
+}
+
+// the conv memory after the batch: its last d_conv b x values (older memory where the batch is shorter)
+__global__ __launch_bounds__(256) void k_pf_conv_state(pf_conv_args a) {
+    const int e = blockIdx.x * 256 + threadIdx.x;
+    if (e >= a.E) return;
+    const int ub = 24 * (e >> 3) + (e & 7), dc = a.d_conv, E = a.E;
+    for (int tt = 0; tt < dc; tt++) {   // increasing tt reads only taps not yet rewritten
+        const int q = a.n - dc + tt;
+        float v;
+        if (q >= 0) {
+            const float* rq = a.bcx + (size_t)q * 3 * E + ub;
+            v = rq[0] * rq[16];
+        } else {
+            v = a.state[(size_t)(tt + a.n) * E + e];
+        }
+        a.state[(size_t)tt * E + e] = v;
+    }
+}
+
+// ---------------------------------------------------------------- attention
+// keys and values of the batch into the fp16 cache: k = rope(norm(k) * k_norm) at the position (imi/core/seoul.cpp:
+// 590-601); one wave per (position, kv head)
+__global__ __launch_bounds__(64) void k_pf_kv(pf_attn_args a) {
+    __shared__ float st[64];
+    const int p = blockIdx.x, g = blockIdx.y, lane = threadIdx.x, D = a.D, half = D / 2;
+    const int at = a.pos0 + p, Hq = a.n_head * D, kvd = a.n_kv * D;
+    const float* row = a.qkv + (size_t)p * a.ld;
+    const float x = lane < D ? row[Hq + g * D + lane] : 0.0f;
+    st[lane] = x;
+    __builtin_amdgcn_wave_barrier();
+    const float s = rms_scale_wave(static_cast<const float*>(st), D, a.eps);
+    const float nv = lane < D ? x * s * a.k_norm[lane] : 0.0f;
+    const float other = __shfl(nv, lane < half ? lane + half : lane - half);
+    if (lane < D) {
+        const float2 cs = a.rope_cs[(size_t)at * half + (lane < half ? lane : lane - half)];
+        const float kd = lane < half ? fmaf(nv, cs.x, -(other * cs.y)) : fmaf(other, cs.y, nv * cs.x);
+        a.kc[((size_t)g * a.n_ctx + at) * D + lane] = f2h(kd);
+        a.vc[((size_t)g * a.n_ctx + at) * D + lane] = f2h(row[Hq + kvd + g * D + lane]);
+    }
+}
+
+// workgroup per (position, kv head), its query heads together (imi/core/seoul.cpp:602-621): q = rope(norm(q) *
+// q_norm); score_t = dot_h(q, K_t) / sqrt(D) over the causal window; softmax with the max subtracted, glibc's expf and
+// a double sum in position order; o = sum_t fma(e_t * inv, V_t, o) in order; times the sigmoid head gate; the
+// output rows cut per 32 channels for the o table
+template <int D>
+__global__ __launch_bounds__(256) void k_pf_attn(pf_attn_args a) {
+    extern __shared__ float lds[];
+    const int p = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    constexpr int half = D / 2;
+    const int Hq = a.n_head * D, kvd = a.n_kv * D, grp = a.n_head / a.n_kv;
+    const int at = a.pos0 + p;
+    const int s0 = a.n_swa > 0 ? max(0, at - a.n_swa + 1) : 0, nk = at - s0 + 1, nks = a.pos0 + a.n;
+    const uint16_t* kc = a.kc + (size_t)g * a.n_ctx * D;
+    const uint16_t* vc = a.vc + (size_t)g * a.n_ctx * D;
+    const float* row = a.qkv + (size_t)p * a.ld;
+    float* q_s = lds;                      // [grp][D]
+    float* o_s = q_s + grp * D;            // [grp][D]
+    float* scratch = o_s + grp * D;        // [4][D]
+    float* inv_s = scratch + 4 * D;        // [8]
+    float* sc = inv_s + 8;                 // [grp][nks]
+    const float2* cs = a.rope_cs + (size_t)at * half;
+
+    for (int hh = wv; hh < grp; hh += 4) {
+        float* stg = scratch + wv * D;
+        const float* src = row + (g * grp + hh) * D;
+        const float x = lane < D ? src[lane] : 0.0f;
+        if (lane < D) stg[lane] = x;
+        __builtin_amdgcn_wave_barrier();
+        const float s = rms_scale_wave(static_cast<const float*>(stg), D, a.eps);
+        const float nv = lane < D ? x * s * a.q_norm[lane] : 0.0f;
+        const float other = __shfl(nv, lane < half ? lane + half : lane - half);
+        if (lane < D) {
+            const float2 t = cs[lane < half ? lane : lane - half];
+            q_s[hh * D + lane] = lane < half ? fmaf(nv, t.x, -(other * t.y)) : fmaf(other, t.y, nv * t.x);
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    __syncthreads();
+
+    const float scale = 1.0f / sqrtf((float)D);
+    for (int t = tid; t < nk; t += 256) {
+        const uint16_t* kt = kc + (size_t)(s0 + t) * D;
+        float kf[D];
+#pragma unroll
+        for (int i0 = 0; i0 < D; i0 += 8) {
+            const u32x4 kw = *reinterpret_cast<const u32x4*>(kt + i0);
+            const unsigned w4[4] = {kw.x, kw.y, kw.z, kw.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) kf[i0 + e] = h2f((uint16_t)((w4[e >> 1] >> (16 * (e & 1))) & 0xFFFFu));
+        }
+        for (int hh = 0; hh < grp; hh++) sc[(size_t)hh * nks + t] = dot_h8<D>(q_s + hh * D, kf) * scale;
+    }
+    __syncthreads();
+    for (int hh = wv; hh < grp; hh += 4) {
+        float* s = sc + (size_t)hh * nks;
+        float mx = -INFINITY;
+        for (int t = lane; t < nk; t += 64) mx = fmaxf(mx, s[t]);
+        mx = wave_max(mx);
+        for (int t = lane; t < nk; t += 64) s[t] = expf_glibc(s[t] - mx);
+        __builtin_amdgcn_wave_barrier();
+        if (lane == 0) {   // double sum in position order, as imi's loop
+            double sum = 0.0;
+            for (int t = 0; t < nk; t++) sum += (double)s[t];
+            inv_s[hh] = (float)(1.0 / sum);
+        }
+    }
+    __syncthreads();
+    for (int k = tid; k < grp * D; k += 256) {
+        const int hh = k / D, i = k - hh * D;
+        const float* s = sc + (size_t)hh * nks;
+        const float inv = inv_s[hh];
+        float o = 0.0f;
+        for (int t = 0; t < nk; t++) o = fmaf(s[t] * inv, h2f(vc[(size_t)(s0 + t) * D + i]), o);
+        const int h = g * grp + hh;
+        const float gate = 1.0f / (1.0f + expf_glibc(-row[Hq + 2 * kvd + h]));
+        o_s[k] = o * gate;
+    }
+    __syncthreads();
+    const int nblk = grp * D / 32, cb0 = g * nblk;
+    if (tid < nblk) cut_store(a.cut, a.n, cb0 + tid, p, o_s + 32 * tid);
+}
+
+}  // namespace
+
+hipError_t launch_pf_rows(int mode, const pf_rows_args& a, hipStream_t s) {
+    if (a.E % 32 || a.E > 2048 || a.n < 1) return hipErrorInvalidValue;
+    if (mode == PFR_FIRST)
+        hipLaunchKernelGGL(k_pf_rows<PFR_FIRST>, dim3(a.n), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(k_pf_rows<PFR_RESID>, dim3(a.n), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_pf_gemm(int epi, const pf_gemm_args& a, hipStream_t s) {
+    if (a.n < 1 || a.W.rows % 8 || (epi == EPI_SWIGLU && a.W.rows % 16)) return hipErrorInvalidValue;
+    const dim3 grid((a.W.rows + 63) / 64, (a.n + 63) / 64);
+    if (epi == EPI_SWIGLU)
+        hipLaunchKernelGGL(k_pf_gemm<EPI_SWIGLU>, grid, dim3(256), 0, s, a);
+    else if (epi == EPI_STORE)
+        hipLaunchKernelGGL(k_pf_gemm<EPI_STORE>, grid, dim3(256), 0, s, a);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_pf_cut(const pf_cutk_args& a, hipStream_t s) {
+    if (a.K % 32 || a.n < 1) return hipErrorInvalidValue;
+    const int total = a.n * (a.K / 32);
+    hipLaunchKernelGGL(k_pf_cut, dim3((total + 255) / 256), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_pf_conv(const pf_conv_args& a, hipStream_t s) {
+    if (a.E % 32 || a.n < 1 || a.d_conv < 1) return hipErrorInvalidValue;
+    const int total = a.n * (a.E / 32);
+    hipLaunchKernelGGL(k_pf_conv, dim3((total + 255) / 256), dim3(256), 0, s, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_pf_conv_state, dim3((a.E + 255) / 256), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_pf_kv(const pf_attn_args& a, hipStream_t s) {
+    if (a.D > 64 || a.D % 32 || a.n < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_pf_kv, dim3(a.n, a.n_kv), dim3(64), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_pf_attn(const pf_attn_args& a, hipStream_t s) {
+    const int grp = a.n_head / a.n_kv;
+    const size_t lds = sizeof(float) * ((size_t)2 * grp * a.D + 4 * (size_t)a.D + 8 + (size_t)grp * (a.pos0 + a.n));
+    if (lds > 160 * 1024 || a.n < 1) return hipErrorInvalidValue;
+    const void* fn = a.D == 64 ? (const void*)k_pf_attn<64> : a.D == 32 ? (const void*)k_pf_attn<32> : nullptr;
+    if (!fn) return hipErrorInvalidValue;
+    if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    if (a.D == 64)
+        hipLaunchKernelGGL(k_pf_attn<64>, dim3(a.n, a.n_kv), dim3(256), lds, s, a);
+    else
+        hipLaunchKernelGGL(k_pf_attn<32>, dim3(a.n, a.n_kv), dim3(256), lds, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace sh
