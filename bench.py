@@ -157,6 +157,41 @@ def cpu_voice_frames(brain_path, voice_path, threads, frames):
     return play_frames(step2, voice, int(ids[-1]), fb, frames)
 
 
+HEAR_EMB, HEAR_TOK = 384, 64   # the hearing window: audio-encoder rows, then words
+
+
+def hearing_inputs(vocab):
+    rng = np.random.default_rng(12)
+    emb = rng.standard_normal((HEAR_EMB + HEAR_TOK, 2048)).astype(np.float32)
+    toks = np.full(HEAR_EMB + HEAR_TOK, -1, np.int32)
+    toks[HEAR_EMB:] = np.random.default_rng(13).integers(0, vocab, size=HEAR_TOK)
+    return toks, emb
+
+
+def gpu_prefill(brain, reps):
+    """The hearing window as one causal prefill (step_batch) on a fresh conversation; returns the wall seconds of
+    each rep (inputs copied from the host inside the call), the last scores and the chosen id."""
+    toks, emb = hearing_inputs(brain.n_vocab)
+    st = brain.new_state()
+    times = []
+    for r in range(reps + 1):
+        st.reset()
+        t0 = time.perf_counter()
+        _, lg, best, _ = brain.step_batch(toks, emb, want_logits=True, st=st)
+        if r:
+            times.append(time.perf_counter() - t0)
+    return np.array(times), lg, best
+
+
+def cpu_prefill(path, threads):
+    import oracle
+    toks, emb = hearing_inputs(97496)
+    eng = oracle.Engine(path, threads=threads, n_ctx=N_CTX)
+    t0 = time.perf_counter()
+    _, lg, _ = eng.step_batch(toks, emb, want_logits=True)
+    return time.perf_counter() - t0, lg
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -166,6 +201,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=8, help="B=1 conversations timed on the CPU (B=2: half as many pairs)")
     ap.add_argument("--voice-frames", type=int, default=64, help="timed voice frames (cfg 4); 0 = skip")
+    ap.add_argument("--prefill-reps", type=int, default=10, help="timed hearing-window prefills (cfg 3); 0 = skip")
     ap.add_argument("--cpu-voice-frames", type=int, default=8)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -257,6 +293,23 @@ def main():
                                     "frac": round(cfg0_bytes / cfg0_us / 1e3 / HBM_PEAK_GBS, 4)},
         },
     }
+    if args.prefill_reps:
+        pt, plg, pbest = gpu_prefill(brain, args.prefill_reps)
+        n_pf = HEAR_EMB + HEAR_TOK
+        # integer ops of the layer tables (2 per weight per position) and of the last position's word scores
+        layer_weights = (brain.table_bytes - brain.n_vocab * brain.n_embd * 18 // 32) * 32 // 18
+        ops = 2 * n_pf * layer_weights + 2 * brain.n_vocab * brain.n_embd
+        line["prefill"] = {
+            "workload": f"cfg3: hearing window, {HEAR_EMB} fp32 embedding rows ~N(0,1) then {HEAR_TOK} seeded words, one "
+                        "causal prefill of the cfg2 model (KV written), last-position word scores",
+            "positions": n_pf,
+            "best_ms": round(float(pt.min()) * 1e3, 3),
+            "p50_ms": round(float(np.percentile(pt, 50)) * 1e3, 3),
+            "positions_per_s": round(n_pf / float(np.percentile(pt, 50)), 1),
+            "int8_tops": round(ops / float(np.percentile(pt, 50)) / 1e12, 2),
+            "int8_peak_tops": 5000.0,
+            "reps": int(len(pt)),
+        }
     if args.voice_frames:
         vpath = synth.cached("voice", synth.VOICE, 1)
         (ft, fbr, fvo, fcodes, fids), fref, vinfo = gpu_voice_frames(path, vpath, args.voice_frames, 4)
@@ -292,6 +345,12 @@ def main():
         }
         line["speedup_vs_cpu"] = {"b1": round(tok_s_b1 / c1, 1), "b2": round(tok_s_b2 / c2, 1)}
         line["greedy_ids_match_cpu"] = same
+        if args.prefill_reps:
+            csec, clg = cpu_prefill(path, threads)
+            line["prefill"]["cpu"] = {"ms": round(csec * 1e3, 1), "cores": threads, "kind": "port",
+                                      "sample": "one hearing-window prefill on the oracle (imi's step_batch restated)"}
+            line["prefill"]["speedup_vs_cpu"] = round(csec / float(np.percentile(pt, 50)), 1)
+            line["prefill"]["scores_match_cpu"] = bool(np.array_equal(clg.view(np.uint32), plg.view(np.uint32)))
         if args.voice_frames and args.cpu_voice_frames:
             ct, cbr, cvo, ccodes, cids, _, _ = cpu_voice_frames(path, vpath, threads, args.cpu_voice_frames)
             n = len(ct)

@@ -1,9 +1,10 @@
-// seoul_gpu.hpp — imi's engine API (imi/core/seoul.h:19-94, imi/brain.h:20-65) over libseoul_hip's C ABI.
+// seoul_gpu.hpp — imi's engine API (imi/core/seoul.h:19-94, imi/brain.h:20-65) and voice generator API
+// (imi/core/voice.h:17-51) over libseoul_hip's C ABI.
 //
 // Drop-in for the CPU engine: the same members and signatures, so imi's callers (greedy loops, the voice frame,
 // step2 riding) compile unchanged after
 //     #include "seoul_gpu.hpp"
-//     using seoul_hip::imi_seoul; using seoul_hip::imi_seoul_state;
+//     using seoul_hip::imi_seoul; using seoul_hip::imi_seoul_state; using seoul_hip::imi_voice;
 // and link -lseoul_hip. Header-only C++17; no HIP or torch types. The thread arguments of load() are accepted and
 // ignored (the device has no thread team). Errors follow imi: load() returns false and prints; a full context
 // prints "context full" and returns without stepping (imi/core/seoul.cpp:209,353,498).
@@ -147,6 +148,55 @@ private:
     }
     bool report(const char* what) const {
         fprintf(stderr, "seoul-hip: %s: %s\n", what, sh_last_error());
+        return false;
+    }
+};
+
+// imi_voice (imi/core/voice.h:17-51) over the same C ABI: the Q8_0 voice generator on the device. `base` is the
+// frame's projected input, refreshed by begin_frame as in imi.
+struct imi_voice {
+    int n_embd = 0, n_vocab = 0, n_cb = 0, n_in = 0, n_head = 0, n_head_kv = 0, head_dim = 0, n_ff = 0;
+    float eps = 1e-5f, rope_theta = 1e6f;
+    int n_threads = 4;
+    std::vector<float> base;   // [n_cb][n_embd]
+
+    imi_voice() = default;
+    imi_voice(const imi_voice&) = delete;
+    imi_voice& operator=(const imi_voice&) = delete;
+    ~imi_voice() {
+        if (v) sh_voice_free(v);
+    }
+
+    // imi/core/voice.cpp:27-88; `threads` and `shared` (CPU thread team) are ignored on the device
+    bool load(const std::string& path, int threads, void* shared = nullptr, int device = 0) {
+        (void)shared;
+        n_threads = threads;
+        if (sh_voice_load(device, path.c_str(), &v) != SH_OK) return report("load");
+        sh_voice_shape I{};
+        sh_voice_info(v, &I);
+        n_embd = I.n_embd; n_vocab = I.n_vocab; n_cb = I.n_cb; n_in = I.n_in; n_head = I.n_head;
+        n_head_kv = I.n_head_kv; head_dim = I.head_dim; n_ff = I.n_ff;
+        base.assign((size_t)n_cb * n_embd, 0.0f);
+        return true;
+    }
+    void begin_frame(const float* h) {   // voice.cpp:99-111
+        if (sh_voice_begin_frame(v, h) != SH_OK || sh_voice_base(v, base.data()) != SH_OK) report("begin_frame");
+    }
+    // the brain's next input after a frame: the sum of the codes' feedback rows, n_in wide (voice.cpp:90-97)
+    void feedback(const int32_t* codes, float* out) const {
+        if (sh_voice_feedback(v, codes, out) != SH_OK) report("feedback");
+    }
+    // codes[i] < 0 = still masked; scores of the codebooks in `need`, [need.size()][n_vocab] (voice.cpp:113-117)
+    void pass(const int32_t* codes, const std::vector<int>& need, std::vector<float>& out) {
+        out.resize(need.size() * (size_t)n_vocab);
+        std::vector<int32_t> nd(need.begin(), need.end());
+        if (sh_voice_pass(v, codes, nd.data(), (int)nd.size(), out.data()) != SH_OK) report("pass");
+    }
+
+private:
+    sh_voice* v = nullptr;
+    bool report(const char* what) const {
+        fprintf(stderr, "seoul-hip: voice %s: %s\n", what, sh_last_error());
         return false;
     }
 };

@@ -52,16 +52,16 @@ def test_gpu_reproduces_golden(tiny_model):
 
 
 @pytest.mark.gpu
-def test_cpp_engine_api_on_gpu(tiny_model, tmp_path):
+def test_cpp_engine_api_on_gpu(tiny_model, tiny_voice, tmp_path):
     """imi's API (include/seoul_gpu.hpp) compiled with g++ against libseoul_hip.so, driving the GPU like imi's callers;
-    its greedy ids equal the oracle's."""
+    its greedy ids and one voice frame's codes equal the oracle's."""
     import subprocess
     exe = str(tmp_path / "seoul_gpu_check")
     lib_dir = os.path.join(ROOT, "nunchi_amd")
     r = subprocess.run(["g++", "-std=c++17", "-O1", "-I", os.path.join(ROOT, "include"), os.path.join(ROOT, "tests", "cpp", "seoul_gpu_check.cpp"),
                         "-L", lib_dir, "-lseoul_hip", f"-Wl,-rpath,{lib_dir}", "-o", exe], capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
-    out = subprocess.run([exe, tiny_model], capture_output=True, text=True, timeout=120)
+    out = subprocess.run([exe, tiny_model, tiny_voice], capture_output=True, text=True, timeout=120)
     assert out.returncode == 0, out.stderr
     ids = [int(v) for v in out.stdout.split("\n")[0].split(":")[1].split()]
     eng = oracle.Engine(tiny_model, threads=2, n_ctx=128)
@@ -73,3 +73,14 @@ def test_cpp_engine_api_on_gpu(tiny_model, tmp_path):
         want.append(oracle.top(lg))
     assert ids == want, (ids, want, out.stderr[-2000:])
     assert "pos 13/1" in out.stdout and "swapped pos 1/13" in out.stdout
+    # the voice frame: same hidden-like input, passes of half the codebooks each, first maximum
+    v = oracle.Voice(tiny_voice, threads=2)
+    h = ((np.arange(v.n_in) % 17 - 8) * 0.125).astype(np.float32)
+    v.begin_frame(h)
+    codes = np.full(v.n_cb, -1, np.int32)
+    half = v.n_cb // 2
+    for need in (list(range(half)), list(range(half, v.n_cb))):
+        sc = v.pass_(codes, need)
+        codes[need] = [oracle.top(r) for r in sc]
+    got = [int(c) for c in out.stdout.split("codes:")[1].split("\n")[0].split()]
+    assert got == codes.tolist(), (got, codes.tolist())
