@@ -368,7 +368,8 @@ int build_program(sh_ctx* c) {
     // shape limits of the kernel
     if (P.size() > (size_t)SK_MAX_STAGES) return fail(SH_E_SHAPE, "step kernel: too many stages");
     const int grp = I.n_attn ? I.n_head / I.n_head_kv : 1;
-    if (E > 2048 || I.n_ff > 8192 || Hq > 8192) return fail(SH_E_SHAPE, "step kernel: widths above 2048 (hidden) / 8192");
+    if ((E != 256 && E != 512 && E != 1024 && E != 2048) || I.n_ff > 8192 || Hq > 8192)
+        return fail(SH_E_SHAPE, "step kernel: hidden width 256, 512, 1024 or 2048, others up to 8192");
     if (c->n_conv && (I.d_conv < 1 || I.d_conv > SK_CONV_MAX)) return fail(SH_E_SHAPE, "step kernel: conv memory of 1..7 taps");
     if (I.n_attn) {
         if (I.head_dim != 64 && I.head_dim != 32) return fail(SH_E_SHAPE, "step kernel: head_dim must be 32 or 64");
@@ -702,9 +703,10 @@ int sh_load(sh_ctx* c, const char* path, int n_ctx) {
     c->part_v = fa(2 * (size_t)c->vocab_grid);
     c->part_i = static_cast<int*>(c->work.take(sizeof(int) * 2 * (size_t)c->vocab_grid));
     if (!c->part_i) return fail(SH_E_NOMEM, "sh_load: work arena overflow");
-    if (c->use_persistent) {
+    if (c->use_persistent) {   // shapes the step kernel does not take run on the per-table kernels
         const int rc = build_program(c);
-        if (rc != SH_OK) return rc;
+        if (rc == SH_E_SHAPE) c->use_persistent = false;
+        else if (rc != SH_OK) return rc;
     }
     HIPCHK(hipDeviceSynchronize());
     c->loaded = true;

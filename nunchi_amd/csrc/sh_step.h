@@ -22,9 +22,13 @@ constexpr int SK_THREADS = 512;
 constexpr int SK_CONV_MAX = 7;                     // conv memory taps (d_conv) the kernel takes
 
 // LDS map of the step kernel (bytes)
-constexpr int SK_OFF_X = 0;                        // float [2][2048] residual stream, private to the workgroup
-constexpr int SK_OFF_Y = SK_OFF_X + 16384;         // float [2][2048] table output feeding a norm
-constexpr int SK_OFF_XQ = SK_OFF_Y + 16384;        // int8 [2][8192] the cut input
+// x and y hold E <= 2048 values per conversation transposed: value i at (i % 32) * SK_XT_LD + i / 32, so lane P of
+// a norm's AVX2-order chain (the squares of values P, P + 32, P + 64, ...) reads its operands 4 at a time
+constexpr int SK_XT_LD = 68;                       // row stride (floats): 64 + 4 keeps 16-byte reads conflict free
+constexpr int SK_XT_M = 32 * SK_XT_LD;             // floats per conversation
+constexpr int SK_OFF_X = 0;                        // float [2][32][68] residual stream, private to the workgroup
+constexpr int SK_OFF_Y = SK_OFF_X + 8 * SK_XT_M;   // float [2][32][68] table output feeding a norm
+constexpr int SK_OFF_XQ = SK_OFF_Y + 8 * SK_XT_M;  // int8 [2][8192] the cut input
 constexpr int SK_OFF_DX = SK_OFF_XQ + 16384;       // float [2][256] cut scales
 constexpr int SK_OFF_S = SK_OFF_DX + 2048;         // float [2][256] d * sum(q) per block
 constexpr int SK_OFF_OPS = SK_OFF_S + 2048;        // float2 [nb][C + 1] chain operands / input staging / attention

@@ -113,8 +113,8 @@ __device__ __forceinline__ char LDS* lds_base() {
     extern __shared__ __align__(16) char smem_dyn[];
     return (char LDS*)smem_dyn;
 }
-__device__ __forceinline__ float LDS* l_x() { return (float LDS*)(lds_base() + SK_OFF_X); }      // [2][2048]
-__device__ __forceinline__ float LDS* l_y() { return (float LDS*)(lds_base() + SK_OFF_Y); }      // [2][2048]
+__device__ __forceinline__ float LDS* l_x() { return (float LDS*)(lds_base() + SK_OFF_X); }      // [2][32][68]
+__device__ __forceinline__ float LDS* l_y() { return (float LDS*)(lds_base() + SK_OFF_Y); }      // [2][32][68]
 __device__ __forceinline__ int LDS* l_xq() { return (int LDS*)(lds_base() + SK_OFF_XQ); }        // [2][2048] int8 x 4
 __device__ __forceinline__ float LDS* l_dx() { return (float LDS*)(lds_base() + SK_OFF_DX); }    // [2][256]
 __device__ __forceinline__ float LDS* l_s() { return (float LDS*)(lds_base() + SK_OFF_S); }      // [2][256]
@@ -201,73 +201,173 @@ __device__ __forceinline__ void trace_at(const sk_params& P, int b, int k) {
 }
 __device__ __forceinline__ int tslot(const sk_params& P, int step, int s, int k) { return step * (1 + 4 * P.n_stages) + (s < 0 ? 0 : 1 + 4 * s + k); }
 
-// ---------------------------------------------------------------- prologues
-// h = x * sc * w_pre per 32-column block (imi_norm_mul, imi/core/vec.h:36-39), optionally written out (hid0/hid1:
-// the conversations' hidden rows, or null), then cut to int8 (imi_q8::from, imi/core/tables.cpp:100-109)
-// block j of conversation m: h = x * sc * w_pre (imi_norm_mul, imi/core/vec.h:36-39), optionally written out,
-// then cut to int8 (imi_q8::from, imi/core/tables.cpp:100-109)
-__device__ __forceinline__ void norm_cut_block(int m, int j, float sc, const float (&wv)[32], float* hid, bool cut) {
-    const float LDS* x = l_x() + m * 2048 + 32 * j;
-    float h[32];
+// ---------------------------------------------------------------- transposed x / y
+__device__ __forceinline__ int xt_at(int i) { return (i & 31) * SK_XT_LD + (i >> 5); }
+
+// gather destination in the transposed layout: index m * 2048 + i -> conversation m's value i
+struct xt_dst {
+    float LDS* base;
+    __device__ __forceinline__ float LDS& operator[](int k) const { return base[(k >> 11) * SK_XT_M + xt_at(k & 2047)]; }
+};
+
+// cross-lane moves on the VALU (DPP), no LDS round trip: lane i gets lane i ^ 1, i ^ 2 (within a quad), 7 - i
+// (within 8 lanes), 15 - i (within 16 lanes)
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+template <int CTRL>
+__device__ __forceinline__ int dppi(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true); }
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_MIRROR8 = 0x141, DPP_MIRROR16 = 0x140;
+
+// imi_rms_scale (imi/core/vec.h:20-33) of n = 128 NQ values held transposed. imi's order: 32 FMA chains, chain P
+// over the squares of values P, P + 32, P + 64, ...; then v_P = (a_P + a_{P+8}) + (a_{P+16} + a_{P+24}) for P < 8 and
+// ((v0 + v4) + (v2 + v6)) + ((v1 + v5) + (v3 + v7)). Lane L < 32 runs chain P(L) = 8 b0 + 16 b1 + 4 b2 + 2 b3 + b4
+// (b_k = bit k of L), so the tree's levels pair lanes L ^ 1, ^ 2, then 8-lane and 16-lane mirrors, then 0 and 16:
+// each level is one DPP add (fp addition is commutative, so the pair order does not matter, only the tree).
+// Every lane gets 1 / sqrtf(s / n + eps).
+template <int NQ>
+__device__ __forceinline__ float rms_scale_T(const float LDS* xt, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int row = 8 * (lane & 1) + 16 * ((lane >> 1) & 1) + 4 * ((lane >> 2) & 1) + 2 * ((lane >> 3) & 1) + ((lane >> 4) & 1);
+    const f32x4 LDS* r = (const f32x4 LDS*)(xt + row * SK_XT_LD);
+    constexpr int B = NQ < 4 ? NQ : 4;   // quads per batch; the next batch is read while this one runs
+    float a = 0.0f;
+    f32x4 cur[B], nxt[B];
 #pragma unroll
-    for (int k = 0; k < 32; k++) h[k] = x[k] * sc * wv[k];
-    if (hid) {
-        f32x4 GLB* o = (f32x4 GLB*)(hid + 32 * j);
+    for (int k = 0; k < B; k++) cur[k] = r[k];
 #pragma unroll
-        for (int k = 0; k < 8; k++) o[k] = f32x4{h[4 * k], h[4 * k + 1], h[4 * k + 2], h[4 * k + 3]};
+    for (int q = 0; q < NQ; q += B) {
+        if (q + B < NQ) {
+#pragma unroll
+            for (int k = 0; k < B; k++) nxt[k] = r[q + B + k];
+        }
+#pragma unroll
+        for (int k = 0; k < B; k++) {
+            a = fmaf(cur[k].x, cur[k].x, a);
+            a = fmaf(cur[k].y, cur[k].y, a);
+            a = fmaf(cur[k].z, cur[k].z, a);
+            a = fmaf(cur[k].w, cur[k].w, a);
+        }
+        if (q + B < NQ) {
+#pragma unroll
+            for (int k = 0; k < B; k++) cur[k] = nxt[k];
+        }
     }
-    if (cut) {
-        int q8[8], sum;
-        const float d = cut32(h, q8, &sum, false);
-        int LDS* xq = l_xq() + m * 2048 + 8 * j;
+    float x = a;   // lanes 32..63 ran the same chains; only lanes 0..31 are read below
+    x = x + dppf<DPP_XOR1>(x);
+    x = x + dppf<DPP_XOR2>(x);
+    x = x + dppf<DPP_MIRROR8>(x);
+    x = x + dppf<DPP_MIRROR16>(x);
+    const float s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0)) +
+                    __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+    return 1.0f / sqrtf(s / (float)(128 * NQ) + eps);
+}
+
+__device__ __forceinline__ float rms_T(const float LDS* xt, int n, float eps) {
+    switch (n) {
+        case 256: return rms_scale_T<2>(xt, eps);
+        case 512: return rms_scale_T<4>(xt, eps);
+        case 1024: return rms_scale_T<8>(xt, eps);
+        default: return rms_scale_T<16>(xt, eps);
+    }
+}
+
+// a quarter (values 4s .. 4s+3) of 32-value block j of conversation m cut to int8 (imi/core/vec.h:47-75) by the 8
+// consecutive lanes s = 0..7 of the block: amax and the code sum are reduced across them (max and integer sums do
+// not depend on order); lane s writes code word s; lane 0 the scale d and d * sum
+__device__ __forceinline__ void cut_quad(const float (&h)[4], int m, int j, int s) {
+    float amax = fmaxf(fmaxf(fabsf(h[0]), fabsf(h[1])), fmaxf(fabsf(h[2]), fabsf(h[3])));
+    amax = fmaxf(amax, dppf<DPP_XOR1>(amax));
+    amax = fmaxf(amax, dppf<DPP_XOR2>(amax));
+    amax = fmaxf(amax, dppf<DPP_MIRROR8>(amax));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    int sum = 0;
+    unsigned packed = 0;
 #pragma unroll
-        for (int w8 = 0; w8 < 8; w8++) xq[w8] = q8[w8];
+    for (int k = 0; k < 4; k++) {
+        const int c = (int)rintf(h[k] * id);
+        sum += c;
+        packed |= ((unsigned)c & 0xFFu) << (8 * k);
+    }
+    sum += dppi<DPP_XOR1>(sum);
+    sum += dppi<DPP_XOR2>(sum);
+    sum += dppi<DPP_MIRROR8>(sum);
+    l_xq()[m * 2048 + 8 * j + s] = (int)packed;
+    if (s == 0) {
         l_dx()[m * 256 + j] = d;
         l_s()[m * 256 + j] = d * (float)sum;
     }
 }
 
+// ---------------------------------------------------------------- prologues
+// values 4s .. 4s+3 of block j of conversation m: h = x * sc * w_pre (imi_norm_mul, imi/core/vec.h:36-39), optionally
+// written out (hid: the conversation's hidden row), then cut with the block's other 7 lanes (imi_q8::from,
+// imi/core/tables.cpp:100-109)
+__device__ __forceinline__ void norm_cut_quad(int m, int j, int s, float sc, const f32x4& w, float* hid, bool cut) {
+    const float LDS* xc = l_x() + m * SK_XT_M + (4 * s) * SK_XT_LD + j;
+    float h[4];
+    h[0] = xc[0] * sc * w.x;
+    h[1] = xc[SK_XT_LD] * sc * w.y;
+    h[2] = xc[2 * SK_XT_LD] * sc * w.z;
+    h[3] = xc[3 * SK_XT_LD] * sc * w.w;
+    if (hid) *(f32x4 GLB*)(hid + 32 * j + 4 * s) = f32x4{h[0], h[1], h[2], h[3]};
+    if (cut) cut_quad(h, m, j, s);
+}
+
 // x += norm(y) * w_post (imi_norm_mul_add, imi/core/vec.h:41-44); then h = norm(x) * w_pre and its cut. Threads
 // are split by conversation (m = t / (512 / M)); every wave computes its conversation's norm scales itself (the
-// same chain in every wave, so the same value), which saves two block barriers.
+// same chain in every wave, so the same value), which saves two block barriers. The x update runs over 4-value
+// row pieces of the transposed layout, the norm and cut over (block, quarter) pairs, E / 4 of each per conversation.
 template <int M>
 __device__ __forceinline__ bool pro_resid(const sk_params& P, SR S, unsigned tag, int par, float* hid0, float* hid1, bool cut, int tr) {
     constexpr int HALF = SK_THREADS / M;
-    constexpr int PER = 2048 / HALF;   // elements of x per thread
-    const int E = P.E, t = threadIdx.x, m = t / HALF, tt = t - m * HALF;
+    constexpr int QPT = 512 / HALF;   // pieces (and pairs) per thread at E = 2048
+    const int E = P.E, t = threadIdx.x, m = t / HALF, tt = t - m * HALF, nqr = E / 128, npc = E / 4;
     // the post-norm weight is read before the wait, so it arrives with the input
-    float wpost[PER];
+    float wpost[QPT][4];
 #pragma unroll
-    for (int k = 0; k < PER; k++) {
-        const int i = tt + k * HALF;
-        wpost[k] = i < E ? ((const float GLB*)S.w_post)[i] : 0.0f;
+    for (int k = 0; k < QPT; k++) {
+        const int q = tt + k * HALF;
+        if (q < npc) {
+            const int pr = q / nqr, t0 = 4 * (q - pr * nqr);
+#pragma unroll
+            for (int e = 0; e < 4; e++) wpost[k][e] = ((const float GLB*)S.w_post)[32 * (t0 + e) + pr];
+        }
     }
-    const bool ok = ll_gather(S.in + (size_t)par * 2 * S.n_in, S.n_in, E, M, tag, l_y(), 2048, P);
+    const bool ok = ll_gather(S.in + (size_t)par * 2 * S.n_in, S.n_in, E, M, tag, xt_dst{l_y()}, 2048, P);
     if (__syncthreads_or(!ok)) return false;
     trace_at(P, blockIdx.x, tr);
-    const float sc1 = rms_scale_wave((const float LDS*)(l_y() + m * 2048), E, P.eps);
+    const float sc1 = rms_T(l_y() + m * SK_XT_M, E, P.eps);
 #pragma unroll
-    for (int k = 0; k < PER; k++) {
-        const int i = tt + k * HALF;
-        if (i < E) {
-            float LDS* x = l_x() + m * 2048 + i;
-            *x = fmaf(l_y()[m * 2048 + i] * sc1, wpost[k], *x);
+    for (int k = 0; k < QPT; k++) {
+        const int q = tt + k * HALF;
+        if (q < npc) {
+            const int pr = q / nqr, t0 = 4 * (q - pr * nqr);
+            const f32x4 y4 = *(const f32x4 LDS*)(l_y() + m * SK_XT_M + pr * SK_XT_LD + t0);
+            f32x4 LDS* xp = (f32x4 LDS*)(l_x() + m * SK_XT_M + pr * SK_XT_LD + t0);
+            f32x4 x4 = *xp;
+            x4.x = fmaf(y4.x * sc1, wpost[k][0], x4.x);
+            x4.y = fmaf(y4.y * sc1, wpost[k][1], x4.y);
+            x4.z = fmaf(y4.z * sc1, wpost[k][2], x4.z);
+            x4.w = fmaf(y4.w * sc1, wpost[k][3], x4.w);
+            *xp = x4;
         }
     }
-    float wpre[32];   // in flight during the second norm's chain
-    const int nbE = E / 32;
-    const int j = tt < nbE ? tt : 0;
-    {
-        const f32x4 GLB* w = (const f32x4 GLB*)(S.w_pre + 32 * j);
+    f32x4 wpre[QPT];   // in flight during the second norm's chain
 #pragma unroll
-        for (int q = 0; q < 8; q++) {
-            const f32x4 a = w[q];
-            wpre[4 * q] = a.x; wpre[4 * q + 1] = a.y; wpre[4 * q + 2] = a.z; wpre[4 * q + 3] = a.w;
-        }
+    for (int k = 0; k < QPT; k++) {
+        const int q = tt + k * HALF;
+        wpre[k] = q < npc ? *(const f32x4 GLB*)(S.w_pre + 4 * q) : f32x4{0, 0, 0, 0};   // block q / 8, quarter q % 8
     }
     __syncthreads();
-    const float sc2 = rms_scale_wave((const float LDS*)(l_x() + m * 2048), E, P.eps);
-    if (tt < nbE) norm_cut_block(m, j, sc2, wpre, m == 0 ? hid0 : hid1, cut);
+    const float sc2 = rms_T(l_x() + m * SK_XT_M, E, P.eps);
+#pragma unroll
+    for (int k = 0; k < QPT; k++) {
+        const int q = tt + k * HALF;
+        if (q < npc) norm_cut_quad(m, q >> 3, q & 7, sc2, wpre[k], m == 0 ? hid0 : hid1, cut);
+    }
     __syncthreads();
     return true;
 }
@@ -275,18 +375,20 @@ __device__ __forceinline__ bool pro_resid(const sk_params& P, SR S, unsigned tag
 template <int M>
 __device__ __forceinline__ void pro_first(const sk_params& P, SR S) {
     constexpr int HALF = SK_THREADS / M;
-    const int t = threadIdx.x, m = t / HALF, tt = t - m * HALF;
-    const int nbE = P.E / 32;
-    const int j = tt < nbE ? tt : 0;
-    float wpre[32];
-    const f32x4 GLB* w = (const f32x4 GLB*)(S.w_pre + 32 * j);
+    constexpr int QPT = 512 / HALF;
+    const int E = P.E, t = threadIdx.x, m = t / HALF, tt = t - m * HALF, npc = E / 4;
+    f32x4 wpre[QPT];
 #pragma unroll
-    for (int q = 0; q < 8; q++) {
-        const f32x4 a = w[q];
-        wpre[4 * q] = a.x; wpre[4 * q + 1] = a.y; wpre[4 * q + 2] = a.z; wpre[4 * q + 3] = a.w;
+    for (int k = 0; k < QPT; k++) {
+        const int q = tt + k * HALF;
+        wpre[k] = q < npc ? *(const f32x4 GLB*)(S.w_pre + 4 * q) : f32x4{0, 0, 0, 0};
     }
-    const float sc = rms_scale_wave((const float LDS*)(l_x() + m * 2048), P.E, P.eps);
-    if (tt < nbE) norm_cut_block(m, j, sc, wpre, nullptr, true);
+    const float sc = rms_T(l_x() + m * SK_XT_M, E, P.eps);
+#pragma unroll
+    for (int k = 0; k < QPT; k++) {
+        const int q = tt + k * HALF;
+        if (q < npc) norm_cut_quad(m, q >> 3, q & 7, sc, wpre[k], nullptr, true);
+    }
     __syncthreads();
 }
 
@@ -315,20 +417,12 @@ __device__ __forceinline__ bool pro_cut(const sk_params& P, SR S, unsigned tag, 
     const bool ok = ll_gather(S.in + (size_t)par * 2 * S.n_in, S.n_in, K, M, tag, l_stg(), 8192, P);
     if (__syncthreads_or(!ok)) return false;
     trace_at(P, blockIdx.x, tr);
-    const int nbk = K / 32;
-    for (int k = t; k < M * nbk; k += SK_THREADS) {
-        const int m = k / nbk, j = k - m * nbk;
-        float v[32];
-        const f32x4 LDS* src = (const f32x4 LDS*)(l_stg() + m * 8192 + 32 * j);
-#pragma unroll
-        for (int q = 0; q < 8; q++) { const f32x4 a = src[q]; v[4 * q] = a.x; v[4 * q + 1] = a.y; v[4 * q + 2] = a.z; v[4 * q + 3] = a.w; }
-        int q8[8], sum;
-        const float d = cut32(v, q8, &sum, false);
-        int LDS* xq = l_xq() + m * 2048 + 8 * j;
-#pragma unroll
-        for (int w8 = 0; w8 < 8; w8++) xq[w8] = q8[w8];
-        l_dx()[m * 256 + j] = d;
-        l_s()[m * 256 + j] = d * (float)sum;
+    const int npc = K / 4;   // (block, quarter) pairs per conversation; 8 consecutive lanes per block
+    for (int k = t; k < M * npc; k += SK_THREADS) {
+        const int m = k / npc, q = k - m * npc;
+        const f32x4 a = *(const f32x4 LDS*)(l_stg() + m * 8192 + 4 * q);
+        const float h[4] = {a.x, a.y, a.z, a.w};
+        cut_quad(h, m, q >> 3, q & 7);
     }
     __syncthreads();
     return true;
@@ -748,9 +842,9 @@ __device__ __forceinline__ bool embed(const sk_params& P, walk_state& W, int b, 
                 v[4 * q] = a.x; v[4 * q + 1] = a.y; v[4 * q + 2] = a.z; v[4 * q + 3] = a.w;
             }
         }
-        float LDS* x = l_x() + m * 2048 + 32 * j;
+        float LDS* x = l_x() + m * SK_XT_M + j;   // values 32 j + i at row i, column j
 #pragma unroll
-        for (int i = 0; i < 32; i++) x[i] = v[i];
+        for (int i = 0; i < 32; i++) x[i * SK_XT_LD] = v[i];
     }
     __syncthreads();
     return true;
