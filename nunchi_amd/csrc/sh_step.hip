@@ -492,9 +492,8 @@ __device__ __forceinline__ void phase2_epilogue(const sk_params& P, SR S, int g0
     const int t = threadIdx.x, nb = S.W.nb;
     // imi's two chains per (input m, row) over the blocks in order (imi/core/tables.cpp:127-143): acc =
     // fma(float(isum), d * dx, acc) on waves 0-3 (lane t), cor = fma(d, s, cor) on waves 4-7 (lane t - 256), so each
-    // wave issues one FMA per step; out = fma(-8, cor, acc). Operands come 4 blocks per 16-byte LDS read, in two
-    // alternating register batches of 8 blocks: the next batch's reads are in flight while the current one runs
-    // (the read-ahead past a row's end lands in padding and is not used).
+    // wave issues one FMA per step; out = fma(-8, cor, acc). Operands come 4 blocks per 16-byte LDS read, with the
+    // reads of the next 28 blocks in flight while the chain runs.
     const bool acc_lane = t < C, cor_lane = t >= 256 && t - 256 < C;
     float chain = 0.0f;
     if (acc_lane || cor_lane) {
@@ -502,31 +501,27 @@ __device__ __forceinline__ void phase2_epilogue(const sk_params& P, SR S, int g0
         const f32x4 LDS* ap = (const f32x4 LDS*)(acc_lane ? l_pq() + (m * rows + r) * st : l_dd() + r * st);
         const f32x4 LDS* bp = (const f32x4 LDS*)(acc_lane ? l_pq() + ((M + m) * rows + r) * st : l_s() + m * 256);
         const int n4 = nb / 4;
-        f32x4 a0 = ap[0], a1 = ap[1], b0 = bp[0], b1 = bp[1];
-        int q = 0;
 #define SK_STEP4(A4, B4)                                                                              \
         chain = fmaf(A4.x, B4.x, chain); chain = fmaf(A4.y, B4.y, chain);                             \
         chain = fmaf(A4.z, B4.z, chain); chain = fmaf(A4.w, B4.w, chain);
-        for (; q + 4 <= n4; q += 4) {
-            const f32x4 a2 = ap[q + 2], a3 = ap[q + 3], b2 = bp[q + 2], b3 = bp[q + 3];
-            SK_STEP4(a0, b0)
-            SK_STEP4(a1, b1)
-            a0 = ap[q + 4]; a1 = ap[q + 5]; b0 = bp[q + 4]; b1 = bp[q + 5];
-            SK_STEP4(a2, b2)
-            SK_STEP4(a3, b3)
-        }
-        if (n4 - q >= 2) {           // the loaded batch: quads q, q + 1
-            SK_STEP4(a0, b0)
-            SK_STEP4(a1, b1)
-            q += 2;
-        } else if (n4 - q == 1) {    // the loaded quad q
-            SK_STEP4(a0, b0)
-            q += 1;
+        if ((n4 & 15) == 0) {   // per 64 blocks: the reads of the next 7 quads (28 blocks) in flight ahead
+            for (int q0 = 0; q0 < n4; q0 += 16) {
+                f32x4 qa[16], qb[16];
+#pragma unroll
+                for (int k = 0; k < 6; k++) { qa[k] = ap[q0 + k]; qb[k] = bp[q0 + k]; }
+#pragma unroll
+                for (int k = 0; k < 16; k++) {
+                    if (k + 6 < 16) { qa[k + 6] = ap[q0 + k + 6]; qb[k + 6] = bp[q0 + k + 6]; }
+                    __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the chain
+                    SK_STEP4(qa[k], qb[k])
+                }
+            }
+        } else {
+            const float LDS* as = (const float LDS*)ap;
+            const float LDS* bs = (const float LDS*)bp;
+            for (int j = 0; j < nb; j++) chain = fmaf(as[j], bs[j], chain);
         }
 #undef SK_STEP4
-        const float LDS* as = (const float LDS*)ap;
-        const float LDS* bs = (const float LDS*)bp;
-        for (int j = 4 * q; j < nb; j++) chain = fmaf(as[j], bs[j], chain);
         if (cor_lane) l_cor()[c] = chain;
     }
     __syncthreads();
