@@ -41,7 +41,9 @@ constexpr int SK_OFF_RED = SK_OFF_OUT + 1024;          // float [512] + int [512
 constexpr int SK_OFF_MISC = SK_OFF_RED + 4096;         // small scalars
 constexpr int SK_OFF_RNG = SK_OFF_MISC + 256;          // int4 [SK_MAX_STAGES] this workgroup's unit range per stage
 constexpr int SK_MAX_STAGES = 128;
-constexpr int SK_LDS_BYTES = SK_OFF_RNG + 16 * SK_MAX_STAGES;
+constexpr int SK_OFF_CL = SK_OFF_RNG + 16 * SK_MAX_STAGES;   // int [SK_MAX_CHUNKS + 1] this workgroup's chunks of a step
+constexpr int SK_MAX_CHUNKS = 511;
+constexpr int SK_LDS_BYTES = SK_OFF_CL + 4 * (SK_MAX_CHUNKS + 1);
 constexpr int SK_ATTN_BYTES = SK_OPS_BYTES + SK_DD_BYTES;   // attention's share (OPS and DD are contiguous)
 
 // groups of 8 rows per chunk for a table of nb 32-column blocks and M inputs: one (group, block) pair per thread in

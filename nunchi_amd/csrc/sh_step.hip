@@ -156,26 +156,42 @@ __device__ __forceinline__ wg_range range_at(int s) {
 
 __device__ __forceinline__ SR stage_at(const sk_params& P, int k) { return ((const sk_stage CST*)P.stages)[k]; }
 
-__device__ __forceinline__ bool has_gemv(const sk_params& P, SR S, int step) {
-    return S.kind == SK_GEMV || (S.kind == SK_VOCAB && step >= P.logits_from);
+// the workgroup's chunks of one step in walk order, built once per launch: entry = stage | chunk << 8 | vocab << 16;
+// word 0 holds the count
+__device__ __forceinline__ int LDS* l_cl() { return (int LDS*)(lds_base() + SK_OFF_CL); }
+constexpr int SK_CL_VOCAB = 1 << 16;
+
+template <int M>
+__device__ __forceinline__ void build_chunk_list(const sk_params& P) {
+    if (threadIdx.x != 0) return;
+    int n = 0;
+    for (int s = 0; s < P.n_stages; s++) {
+        SR S = stage_at(P, s);
+        if (S.kind == SK_ATTN) continue;
+        const int nch = range_at(s).nch;
+        for (int c = 0; c < nch && n < SK_MAX_CHUNKS; c++) l_cl()[1 + n++] = s | (c << 8) | (S.kind == SK_VOCAB ? SK_CL_VOCAB : 0);
+    }
+    l_cl()[0] = n;
 }
 
-// (step, s, c) -> the next chunk this workgroup computes; false when there is none
-template <int M>
-__device__ __forceinline__ bool next_chunk(const sk_params& P, int b, int G, int& step, int& s, int& c) {
-    c++;
-    for (;;) {
-        if (s < P.n_stages) {
-            SR S = stage_at(P, s);
-            if (has_gemv(P, S, step) && c < range_at(s).nch) return true;
+// chunk list entry ci of step `step` -> the next chunk this workgroup computes (the word scores only from
+// logits_from on); false when there is none
+__device__ __forceinline__ bool next_chunk(const sk_params& P, int& step, int& ci, int& s, int& c) {
+    const int n = l_cl()[0];
+    int k = ci + 1;
+    for (int guard = 0; guard < 2 * SK_MAX_CHUNKS + 4; guard++) {
+        if (k >= n) {
+            k = 0;
+            if (++step >= P.n_steps || n == 0) return false;
         }
-        s++;
-        c = 0;
-        if (s >= P.n_stages) {
-            s = 0;
-            if (++step >= P.n_steps) return false;
-        }
+        const int e = l_cl()[1 + k];
+        if ((e & SK_CL_VOCAB) && step < P.logits_from) { k = n; continue; }
+        ci = k;
+        s = e & 0xFF;
+        c = (e >> 8) & 0xFF;
+        return true;
     }
+    return false;
 }
 
 template <int M>
@@ -775,6 +791,7 @@ __device__ __forceinline__ bool attention(const sk_params& P, SR S, int g, int m
 struct walk_state {
     int step, s, c, nch;
     bool embedded, pro_done;
+    int ci;   // chunk list index of the next chunk computed
 };
 
 __device__ __forceinline__ void next_stage(const sk_params& P, walk_state& W) {
@@ -940,8 +957,9 @@ __device__ __forceinline__ void chunk(const sk_params& P, walk_state& W, int b, 
     conv_load<M>(P, S, g0, C, rows, cp);
     // the next chunk's loads go out after this chunk's results are published: the issue cost is off the path to
     // the publish, and the stream overlaps the wait for the next stage's input
-    int qs = W.step, qss = W.s, qc = W.c;
-    if (!next_chunk<M>(P, b, G, qs, qss, qc)) { qss = W.s; qc = W.c; }   // the last chunk: a harmless re-read
+    int qs = W.step, qci = W.ci, qss = W.s, qc = W.c;
+    if (!next_chunk(P, qs, qci, qss, qc)) { qss = W.s; qc = W.c; }   // the last chunk: a harmless re-read
+    W.ci = qci;
     phase1<M>(cur, ng, S.W.nb, rows);
     __syncthreads();
     phase2_epilogue<M>(P, S, g0, C, rows, tag, par, bv, bi, cp);
@@ -974,7 +992,7 @@ __device__ __forceinline__ void chunk(const sk_params& P, walk_state& W, int b, 
 template <int M>
 __global__ __launch_bounds__(SK_THREADS, 1) void k_step(sk_params P) {
     const int b = blockIdx.x, G = gridDim.x;
-    walk_state W{0, 0, 0, 0, false, false};
+    walk_state W{0, 0, 0, 0, false, false, -1};
     float bv[M];
     int bi[M];
 #pragma unroll
@@ -984,10 +1002,12 @@ __global__ __launch_bounds__(SK_THREADS, 1) void k_step(sk_params P) {
         l_rng()[k] = i32x4{r.u0, r.n, r.cu, r.nch};
     }
     __syncthreads();
+    build_chunk_list<M>(P);
+    __syncthreads();
     u32x4 wa[9], wb[9];
     {
         int st = 0, s = 0, c = -1;
-        if (next_chunk<M>(P, b, G, st, s, c)) issue<M>(P, b, G, s, c, wa);
+        if (next_chunk(P, st, W.ci, s, c)) issue<M>(P, b, G, s, c, wa);
     }
     for (;;) {
         if (!events<M>(P, W, b, G, bv, bi)) break;
