@@ -507,13 +507,15 @@ __device__ __forceinline__ void phase2_epilogue(const sk_params& P, SR S, int g0
                                                 float (&bv)[M], int (&bi)[M], const conv_pre& cp) {
     const int t = threadIdx.x, nb = S.W.nb;
     // imi's two chains per (input m, row) over the blocks in order (imi/core/tables.cpp:127-143): acc =
-    // fma(float(isum), d * dx, acc) on waves 0-3 (lane t), cor = fma(d, s, cor) on waves 4-7 (lane t - 256), so each
-    // wave issues one FMA per step; out = fma(-8, cor, acc). Operands come 4 blocks per 16-byte LDS read, with the
-    // reads of the next 28 blocks in flight while the chain runs.
-    const bool acc_lane = t < C, cor_lane = t >= 256 && t - 256 < C;
+    // fma(float(isum), d * dx, acc) and cor = fma(d, s, cor), each wave issuing one FMA per step; out = fma(-8, cor,
+    // acc). Chain c's acc runs on lane 128 (c / 64) + c % 64 and its cor 64 lanes further, so the two waves of a
+    // 128-lane pair sit on different SIMDs and the two chains of a row do not share one SIMD's issue slots. Operands
+    // come 4 blocks per 16-byte LDS read, with the reads of the next 24 blocks in flight while the chain runs.
+    const int cw = t >> 6, cc = 64 * (cw >> 1) + (t & 63);
+    const bool acc_lane = (cw & 1) == 0 && cc < C, cor_lane = (cw & 1) == 1 && cc < C;
     float chain = 0.0f;
     if (acc_lane || cor_lane) {
-        const int c = acc_lane ? t : t - 256, m = c / rows, r = c - m * rows, st = sk_row_stride(nb);
+        const int c = cc, m = c / rows, r = c - m * rows, st = sk_row_stride(nb);
         const f32x4 LDS* ap = (const f32x4 LDS*)(acc_lane ? l_pq() + (m * rows + r) * st : l_dd() + r * st);
         const f32x4 LDS* bp = (const f32x4 LDS*)(acc_lane ? l_pq() + ((M + m) * rows + r) * st : l_s() + m * 256);
         const int n4 = nb / 4;
@@ -541,12 +543,9 @@ __device__ __forceinline__ void phase2_epilogue(const sk_params& P, SR S, int g0
         if (cor_lane) l_cor()[c] = chain;
     }
     __syncthreads();
-    float outv = 0.0f;
-    if (acc_lane) {
-        outv = fmaf(-8.0f, l_cor()[t], chain);
-        l_out()[t] = outv;
-    }
+    if (acc_lane) l_out()[cc] = fmaf(-8.0f, l_cor()[cc], chain);
     __syncthreads();
+    const float outv = t < C ? l_out()[t] : 0.0f;
     if (t >= C) return;
     const int m = t / rows, rr = t - m * rows;
     u64* out = S.out ? S.out + (size_t)(par * 2 + m) * S.n_out : nullptr;
