@@ -235,6 +235,105 @@ __global__ __launch_bounds__(64) void k_gemv(gemv_args a) {
     }
 }
 
+// ---------------------------------------------------------------- Q4_0 GEMV with the input cut (decode tables,
+// kernel-level API): one workgroup per 8-row group, one wave per 64-block slice of the rows (nb <= 256).
+// Each thread owns one block j: its weight loads (8 rows x 16 B codes + the group's 8 scales) go out first, then it
+// cuts input block j itself (codes stay in registers), forms the 8 exact integer dots, and writes the chain operands
+// float(isum), d * dx and d to LDS row-major. Then wave 0 runs the 16 M chains of imi's per-row epilogue over the
+// blocks in order (imi/core/tables.cpp:127-143): lane (m, r) acc = fma(float(isum), d * dx, acc), lane 8 M + (m, r)
+// cor = fma(d, s, cor) (the same instruction stream for both, operands through per-lane row pointers), four blocks
+// per 16-byte LDS read with later reads in flight; out = fma(-8, cor, acc), or acc - cor with q4x8's corr
+// (imi/kernels/q4x8.cpp:51-77).
+template <int M, bool HALF>
+__global__ __launch_bounds__(256) void k_gemv_cut(gemv_args a) {
+    extern __shared__ __align__(16) float lds[];
+    const int nb = a.W.nb, st = ((nb + 3) & ~3) + 4;   // row stride: 16-byte rows, odd in 16-byte units
+    const int t = threadIdx.x, lane = t & 63, j = t, g = blockIdx.x;
+    float* l_op = lds;                         // [M][8][st] float(isum)
+    float* l_oq = l_op + M * 8 * st;           // [M][8][st] d * dx
+    float* l_dd = l_oq + M * 8 * st;           // [8][st] d
+    float* l_s = l_dd + 8 * st;                // [M][st] s = d * sum (q4x8: 8 * d * sum)
+    const bool on = j < nb;
+    u32x4 c[8], s8 = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int r = 0; r < 8; r++) c[r] = u32x4{0u, 0u, 0u, 0u};
+    if (on) {
+        const u32x4* codes = (const u32x4*)a.W.codes + (size_t)8 * g * nb + j;
+#pragma unroll
+        for (int r = 0; r < 8; r++) c[r] = __builtin_nontemporal_load(codes + (size_t)r * nb);
+        s8 = __builtin_nontemporal_load((const u32x4*)a.W.scales + (size_t)g * nb + j);
+    }
+    int xq[M][8];
+    float dxv[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        dxv[m] = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 8; w++) xq[m][w] = 0;
+        if (on) {
+            float v[32];
+            load32(a.src + (size_t)m * a.src_ld + 32 * j, v);
+            int sum;
+            const float d = cut32(v, xq[m], &sum, HALF);
+            dxv[m] = d;
+            l_s[m * st + j] = HALF ? 8.0f * d * (float)sum : d * (float)sum;
+        }
+    }
+    if (on) {
+        const unsigned sw[4] = {s8.x, s8.y, s8.z, s8.w};
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+            const float d = h2f((uint16_t)((r & 1) ? (sw[r >> 1] >> 16) : (sw[r >> 1] & 0xFFFFu)));
+            l_dd[r * st + j] = d;
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                l_op[(m * 8 + r) * st + j] = (float)q4_block_dot(c[r], xq[m]);
+                l_oq[(m * 8 + r) * st + j] = d * dxv[m];
+            }
+        }
+    }
+    __syncthreads();
+    if (t >= 64) return;
+    const bool acc_lane = lane < 8 * M, cor_lane = lane >= 8 * M && lane < 16 * M;
+    float chain = 0.0f;
+    if (acc_lane || cor_lane) {
+        const int k = acc_lane ? lane : lane - 8 * M, m = k >> 3, r = k & 7;
+        const f32x4* ap = (const f32x4*)(acc_lane ? l_op + (m * 8 + r) * st : l_dd + r * st);
+        const f32x4* bp = (const f32x4*)(acc_lane ? l_oq + (m * 8 + r) * st : l_s + m * st);
+        const int n4 = nb / 4;
+        if ((nb & 63) == 0) {   // per 64 blocks: the reads of the next 6 quads in flight ahead of the chain
+            for (int q0 = 0; q0 < n4; q0 += 16) {
+                f32x4 qa[16], qb[16];
+#pragma unroll
+                for (int q = 0; q < 6; q++) { qa[q] = ap[q0 + q]; qb[q] = bp[q0 + q]; }
+#pragma unroll
+                for (int q = 0; q < 16; q++) {
+                    if (q + 6 < 16) { qa[q + 6] = ap[q0 + q + 6]; qb[q + 6] = bp[q0 + q + 6]; }
+                    __builtin_amdgcn_sched_barrier(0);
+                    chain = fmaf(qa[q].x, qb[q].x, chain);
+                    chain = fmaf(qa[q].y, qb[q].y, chain);
+                    chain = fmaf(qa[q].z, qb[q].z, chain);
+                    chain = fmaf(qa[q].w, qb[q].w, chain);
+                }
+            }
+        } else {
+            const float* as = (const float*)ap;
+            const float* bs = (const float*)bp;
+            for (int q = 0; q < nb; q++) chain = fmaf(as[q], bs[q], chain);
+        }
+    }
+    const float cor = __shfl(chain, (lane + 8 * M) & 63);
+    if (acc_lane) {
+        const int m = lane >> 3, r = lane & 7;
+        a.out[(size_t)m * a.out_ld + 8 * g + r] = HALF ? chain - cor : fmaf(-8.0f, cor, chain);
+    }
+}
+
+static size_t gemv_cut_lds(int M, int nb) {
+    const size_t st = (size_t)(((nb + 3) & ~3) + 4);
+    return sizeof(float) * st * ((size_t)2 * M * 8 + 8 + M);
+}
+
 // dynamic LDS bytes of a k_gemv instantiation
 static size_t gemv_lds(int M, int UG, int nb, int E, bool norm) {
     const int R = 8 * UG;
@@ -426,6 +525,17 @@ __global__ __launch_bounds__(64) void k_q4_rows(q4dev T, const int32_t* ids, flo
 hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
     const int nbl = (a.W.nb + 63) / 64;
     const int ug = epi == EPI_SWIGLU ? 2 : epi == EPI_CONV ? 3 : 1;
+    // the plain tables (input cut, rows stored): one workgroup per 8-row group, the grid is the group count
+    if (epi == EPI_STORE && (pro == PRO_CUT || pro == PRO_CUT_HALF_AWAY) && a.W.nb <= 256 && a.W.rows % 8 == 0 &&
+        (M == 1 || (M == 2 && pro == PRO_CUT))) {
+        const void* fn = M == 2 ? (const void*)k_gemv_cut<2, false>
+                       : pro == PRO_CUT ? (const void*)k_gemv_cut<1, false> : (const void*)k_gemv_cut<1, true>;
+        void* args[] = {const_cast<gemv_args*>(&a)};
+        const dim3 gr(a.W.rows / 8), bl(64 * nbl);
+        const size_t lds = gemv_cut_lds(M, a.W.nb);
+        if (t0) return hipExtLaunchKernel(fn, gr, bl, args, lds, s, t0, t1, 0);
+        return hipLaunchKernel(fn, gr, bl, args, lds, s);
+    }
     SH_GEMV_CASE(1, 1, PRO_CUT, EPI_STORE, 1) SH_GEMV_CASE(2, 1, PRO_CUT, EPI_STORE, 1)
     SH_GEMV_CASE(1, 2, PRO_CUT, EPI_STORE, 1) SH_GEMV_CASE(2, 2, PRO_CUT, EPI_STORE, 1)
     SH_GEMV_CASE(1, 3, PRO_CUT, EPI_STORE, 1) SH_GEMV_CASE(2, 3, PRO_CUT, EPI_STORE, 1)
