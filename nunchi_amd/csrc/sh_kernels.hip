@@ -236,59 +236,103 @@ __global__ __launch_bounds__(64) void k_gemv(gemv_args a) {
 }
 
 // ---------------------------------------------------------------- Q4_0 GEMV with the input cut (decode tables,
-// kernel-level API): one workgroup per 8-row group, one wave per 64-block slice of the rows (nb <= 256).
-// Each thread owns one block j: its weight loads (8 rows x 16 B codes + the group's 8 scales) go out first, then it
-// cuts input block j itself (codes stay in registers), forms the 8 exact integer dots, and writes the chain operands
-// float(isum), d * dx and d to LDS row-major. Then wave 0 runs the 16 M chains of imi's per-row epilogue over the
-// blocks in order (imi/core/tables.cpp:127-143): lane (m, r) acc = fma(float(isum), d * dx, acc), lane 8 M + (m, r)
-// cor = fma(d, s, cor) (the same instruction stream for both, operands through per-lane row pointers), four blocks
-// per 16-byte LDS read with later reads in flight; out = fma(-8, cor, acc), or acc - cor with q4x8's corr
-// (imi/kernels/q4x8.cpp:51-77).
-template <int M, bool HALF>
+// kernel-level API): one 256-thread workgroup per 8-row group, NB = 64, 128 or 256 blocks per row. Every step is
+// spread over the whole workgroup, so its critical path is short:
+//  - loads: each thread first loads its share of the input (32 / TPB values of one block, TPB = 256 / NB threads
+//    per block), then the codes of its RPT = NB / 32 rows of one block and the group's 8 scales of that block;
+//  - cut (imi_cut32, imi/core/vec.h:47-75): the TPB threads of a block reduce amax and the code sum across lanes
+//    (max and integer sums do not depend on order); codes, d and s to LDS; it waits only for the input loads;
+//  - dots: thread (row subset, block) forms its rows' exact integer dots and writes the chain operands float(isum),
+//    d * dx and d to LDS row-major;
+//  - chains (imi/core/tables.cpp:127-143): wave 0, lane (m, r) acc = fma(float(isum), d * dx, acc), lane 8 M + (m, r)
+//    cor = fma(d, s, cor), the same instruction stream for both (operands through per-lane row pointers), four
+//    blocks per 16-byte LDS read with later reads in flight; out = fma(-8, cor, acc), or acc - cor with q4x8's
+//    corr = 8 d sum (imi/kernels/q4x8.cpp:45-77).
+template <int M, bool HALF, int NB>
 __global__ __launch_bounds__(256) void k_gemv_cut(gemv_args a) {
+    constexpr int TPB = 256 / NB, VPT = 32 / TPB, RPT = NB / 32, ST = NB + 4;
     extern __shared__ __align__(16) float lds[];
-    const int nb = a.W.nb, st = ((nb + 3) & ~3) + 4;   // row stride: 16-byte rows, odd in 16-byte units
-    const int t = threadIdx.x, lane = t & 63, j = t, g = blockIdx.x;
-    float* l_op = lds;                         // [M][8][st] float(isum)
-    float* l_oq = l_op + M * 8 * st;           // [M][8][st] d * dx
-    float* l_dd = l_oq + M * 8 * st;           // [8][st] d
-    float* l_s = l_dd + 8 * st;                // [M][st] s = d * sum (q4x8: 8 * d * sum)
-    const bool on = j < nb;
-    u32x4 c[8], s8 = u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int r = 0; r < 8; r++) c[r] = u32x4{0u, 0u, 0u, 0u};
-    if (on) {
-        const u32x4* codes = (const u32x4*)a.W.codes + (size_t)8 * g * nb + j;
-#pragma unroll
-        for (int r = 0; r < 8; r++) c[r] = __builtin_nontemporal_load(codes + (size_t)r * nb);
-        s8 = __builtin_nontemporal_load((const u32x4*)a.W.scales + (size_t)g * nb + j);
-    }
-    int xq[M][8];
-    float dxv[M];
+    int* l_xq = (int*)lds;                      // [M][NB][8] int8 codes of the cut input, 4 per word
+    float* l_dx = lds + M * NB * 8;             // [M][NB]
+    float* l_s = l_dx + M * NB;                 // [M][ST] s = d * sum (q4x8: 8 * d * sum)
+    float* l_op = l_s + M * ST;                 // [M][8][ST] float(isum)
+    float* l_oq = l_op + M * 8 * ST;            // [M][8][ST] d * dx
+    float* l_dd = l_oq + M * 8 * ST;            // [8][ST] d
+    const int t = threadIdx.x, lane = t & 63, g = blockIdx.x;
+    // input share first: block jc, values part * VPT .. + VPT - 1
+    const int jc = t / TPB, part = t - jc * TPB;
+    f32x4 xin[M][VPT / 4];
 #pragma unroll
     for (int m = 0; m < M; m++) {
-        dxv[m] = 0.0f;
+        const f32x4* src = (const f32x4*)(a.src + (size_t)m * a.src_ld + 32 * jc + VPT * part);
 #pragma unroll
-        for (int w = 0; w < 8; w++) xq[m][w] = 0;
-        if (on) {
-            float v[32];
-            load32(a.src + (size_t)m * a.src_ld + 32 * j, v);
-            int sum;
-            const float d = cut32(v, xq[m], &sum, HALF);
-            dxv[m] = d;
-            l_s[m * st + j] = HALF ? 8.0f * d * (float)sum : d * (float)sum;
+        for (int k = 0; k < VPT / 4; k++) xin[m][k] = src[k];
+    }
+    // then the weights: rows sub * RPT .. + RPT - 1 of block jw
+    const int jw = t % NB, sub = t / NB;
+    u32x4 c[RPT];
+    const u32x4* codes = (const u32x4*)a.W.codes + (size_t)(8 * g + sub * RPT) * NB + jw;
+#pragma unroll
+    for (int k = 0; k < RPT; k++) c[k] = __builtin_nontemporal_load(codes + (size_t)k * NB);
+    const u32x4 s8 = __builtin_nontemporal_load((const u32x4*)a.W.scales + (size_t)g * NB + jw);
+    // the cut of block jc by its TPB threads
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        float v[VPT];
+#pragma unroll
+        for (int k = 0; k < VPT / 4; k++) {
+            v[4 * k] = xin[m][k].x; v[4 * k + 1] = xin[m][k].y; v[4 * k + 2] = xin[m][k].z; v[4 * k + 3] = xin[m][k].w;
+        }
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < VPT; i++) amax = fmaxf(amax, fabsf(v[i]));
+        if (TPB >= 2) amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(amax), 0xB1, 0xF, 0xF, true)));
+        if (TPB >= 4) amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(amax), 0x4E, 0xF, 0xF, true)));
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        int sum = 0;
+#pragma unroll
+        for (int w = 0; w < VPT / 4; w++) {
+            unsigned packed = 0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float q = v[4 * w + k] * id;
+                const int cq = (int)(HALF ? roundf(q) : rintf(q));
+                sum += cq;
+                packed |= ((unsigned)cq & 0xFFu) << (8 * k);
+            }
+            l_xq[(m * NB + jc) * 8 + part * (VPT / 4) + w] = (int)packed;
+        }
+        if (TPB >= 2) sum += __builtin_amdgcn_update_dpp(0, sum, 0xB1, 0xF, 0xF, true);
+        if (TPB >= 4) sum += __builtin_amdgcn_update_dpp(0, sum, 0x4E, 0xF, 0xF, true);
+        if (part == 0) {
+            l_dx[m * NB + jc] = d;
+            l_s[m * ST + jc] = HALF ? 8.0f * d * (float)sum : d * (float)sum;
         }
     }
-    if (on) {
+    __syncthreads();
+    // exact dots of rows sub * RPT .. against block jw
+    {
         const unsigned sw[4] = {s8.x, s8.y, s8.z, s8.w};
+        float d[RPT];
 #pragma unroll
-        for (int r = 0; r < 8; r++) {
-            const float d = h2f((uint16_t)((r & 1) ? (sw[r >> 1] >> 16) : (sw[r >> 1] & 0xFFFFu)));
-            l_dd[r * st + j] = d;
+        for (int k = 0; k < RPT; k++) {
+            const int r = sub * RPT + k;
+            const unsigned word = RPT == 8 ? sw[k >> 1] : (r >> 1) == 0 ? sw[0] : (r >> 1) == 1 ? sw[1] : (r >> 1) == 2 ? sw[2] : sw[3];
+            d[k] = h2f((uint16_t)((r & 1) ? (word >> 16) : (word & 0xFFFFu)));
+            l_dd[r * ST + jw] = d[k];
+        }
 #pragma unroll
-            for (int m = 0; m < M; m++) {
-                l_op[(m * 8 + r) * st + j] = (float)q4_block_dot(c[r], xq[m]);
-                l_oq[(m * 8 + r) * st + j] = d * dxv[m];
+        for (int m = 0; m < M; m++) {
+            const u32x4* xs = (const u32x4*)(l_xq + (m * NB + jw) * 8);
+            const u32x4 x0 = xs[0], x1 = xs[1];
+            const int xq[8] = {(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+            const float dx = l_dx[m * NB + jw];
+#pragma unroll
+            for (int k = 0; k < RPT; k++) {
+                const int r = sub * RPT + k;
+                l_op[(m * 8 + r) * ST + jw] = (float)q4_block_dot(c[k], xq);
+                l_oq[(m * 8 + r) * ST + jw] = d[k] * dx;
             }
         }
     }
@@ -298,28 +342,21 @@ __global__ __launch_bounds__(256) void k_gemv_cut(gemv_args a) {
     float chain = 0.0f;
     if (acc_lane || cor_lane) {
         const int k = acc_lane ? lane : lane - 8 * M, m = k >> 3, r = k & 7;
-        const f32x4* ap = (const f32x4*)(acc_lane ? l_op + (m * 8 + r) * st : l_dd + r * st);
-        const f32x4* bp = (const f32x4*)(acc_lane ? l_oq + (m * 8 + r) * st : l_s + m * st);
-        const int n4 = nb / 4;
-        if ((nb & 63) == 0) {   // per 64 blocks: the reads of the next 6 quads in flight ahead of the chain
-            for (int q0 = 0; q0 < n4; q0 += 16) {
-                f32x4 qa[16], qb[16];
+        const f32x4* ap = (const f32x4*)(acc_lane ? l_op + (m * 8 + r) * ST : l_dd + r * ST);
+        const f32x4* bp = (const f32x4*)(acc_lane ? l_oq + (m * 8 + r) * ST : l_s + m * ST);
+        for (int q0 = 0; q0 < NB / 4; q0 += 16) {   // per 64 blocks: the reads of the next 6 quads in flight
+            f32x4 qa[16], qb[16];
 #pragma unroll
-                for (int q = 0; q < 6; q++) { qa[q] = ap[q0 + q]; qb[q] = bp[q0 + q]; }
+            for (int q = 0; q < 6; q++) { qa[q] = ap[q0 + q]; qb[q] = bp[q0 + q]; }
 #pragma unroll
-                for (int q = 0; q < 16; q++) {
-                    if (q + 6 < 16) { qa[q + 6] = ap[q0 + q + 6]; qb[q + 6] = bp[q0 + q + 6]; }
-                    __builtin_amdgcn_sched_barrier(0);
-                    chain = fmaf(qa[q].x, qb[q].x, chain);
-                    chain = fmaf(qa[q].y, qb[q].y, chain);
-                    chain = fmaf(qa[q].z, qb[q].z, chain);
-                    chain = fmaf(qa[q].w, qb[q].w, chain);
-                }
+            for (int q = 0; q < 16; q++) {
+                if (q + 6 < 16) { qa[q + 6] = ap[q0 + q + 6]; qb[q + 6] = bp[q0 + q + 6]; }
+                __builtin_amdgcn_sched_barrier(0);
+                chain = fmaf(qa[q].x, qb[q].x, chain);
+                chain = fmaf(qa[q].y, qb[q].y, chain);
+                chain = fmaf(qa[q].z, qb[q].z, chain);
+                chain = fmaf(qa[q].w, qb[q].w, chain);
             }
-        } else {
-            const float* as = (const float*)ap;
-            const float* bs = (const float*)bp;
-            for (int q = 0; q < nb; q++) chain = fmaf(as[q], bs[q], chain);
         }
     }
     const float cor = __shfl(chain, (lane + 8 * M) & 63);
@@ -330,8 +367,8 @@ __global__ __launch_bounds__(256) void k_gemv_cut(gemv_args a) {
 }
 
 static size_t gemv_cut_lds(int M, int nb) {
-    const size_t st = (size_t)(((nb + 3) & ~3) + 4);
-    return sizeof(float) * st * ((size_t)2 * M * 8 + 8 + M);
+    const size_t st = (size_t)nb + 4;
+    return sizeof(float) * ((size_t)M * nb * 8 + (size_t)M * nb + (size_t)M * st + (size_t)2 * M * 8 * st + 8 * st);
 }
 
 // dynamic LDS bytes of a k_gemv instantiation
@@ -526,13 +563,19 @@ hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hi
     const int nbl = (a.W.nb + 63) / 64;
     const int ug = epi == EPI_SWIGLU ? 2 : epi == EPI_CONV ? 3 : 1;
     // the plain tables (input cut, rows stored): one workgroup per 8-row group, the grid is the group count
-    if (epi == EPI_STORE && (pro == PRO_CUT || pro == PRO_CUT_HALF_AWAY) && a.W.nb <= 256 && a.W.rows % 8 == 0 &&
-        (M == 1 || (M == 2 && pro == PRO_CUT))) {
-        const void* fn = M == 2 ? (const void*)k_gemv_cut<2, false>
-                       : pro == PRO_CUT ? (const void*)k_gemv_cut<1, false> : (const void*)k_gemv_cut<1, true>;
+    const int nb = a.W.nb;
+    if (epi == EPI_STORE && (pro == PRO_CUT || pro == PRO_CUT_HALF_AWAY) && (nb == 64 || nb == 128 || nb == 256) &&
+        a.W.rows % 8 == 0 && (M == 1 || (M == 2 && pro == PRO_CUT))) {
+        const bool half = pro == PRO_CUT_HALF_AWAY;
+        const void* fn = nullptr;
+#define SH_CUT_FN(M_, H_, NB_) if (M == M_ && half == H_ && nb == NB_) fn = (const void*)k_gemv_cut<M_, H_, NB_>;
+        SH_CUT_FN(1, false, 64) SH_CUT_FN(1, false, 128) SH_CUT_FN(1, false, 256)
+        SH_CUT_FN(1, true, 64) SH_CUT_FN(1, true, 128) SH_CUT_FN(1, true, 256)
+        SH_CUT_FN(2, false, 64) SH_CUT_FN(2, false, 128) SH_CUT_FN(2, false, 256)
+#undef SH_CUT_FN
         void* args[] = {const_cast<gemv_args*>(&a)};
-        const dim3 gr(a.W.rows / 8), bl(64 * nbl);
-        const size_t lds = gemv_cut_lds(M, a.W.nb);
+        const dim3 gr(a.W.rows / 8), bl(256);
+        const size_t lds = gemv_cut_lds(M, nb);
         if (t0) return hipExtLaunchKernel(fn, gr, bl, args, lds, s, t0, t1, 0);
         return hipLaunchKernel(fn, gr, bl, args, lds, s);
     }
