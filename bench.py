@@ -231,7 +231,8 @@ def main():
     # cfg 0: one Q4_0 x fp32 GEMV 8192 x 2048 with imi/kernels/q4x8 semantics, 64 distinct weight copies in rotation
     ctx = brain.ctx
     copies = [nunchi_amd.Q4Table(ctx, synth.q4_0_random(np.random.default_rng(100 + i), 8192, 2048), 8192, 2048) for i in range(64)]
-    cfg0_us = nunchi_amd.q4_bench(ctx, copies, n_in=1, cut_mode=1, reps=640)
+    cfg0_us = nunchi_amd.q4_bench(ctx, copies, n_in=1, cut_mode=1, reps=640)           # per call, back to back
+    cfg0_kernel_us = nunchi_amd.q4_bench_kernel(ctx, copies, n_in=1, cut_mode=1, reps=256)   # the kernel itself
     cfg0_bytes = 8192 * 64 * 18 + 2048 * 4 + 8192 * 4
     del copies
 
@@ -290,7 +291,10 @@ def main():
                                 "GBs": round(tables1["bytes_per_pass"] / tables1["launches"] / tables1["avg_launch_us"] / 1e3, 1)},
             "layer_tables_b2": {"avg_launch_us": round(tables2["avg_launch_us"], 3), "ms_per_pass": round(tables2["ms_per_pass"], 4)},
             "cfg0_gemv_8192x2048": {"avg_us": round(cfg0_us, 3), "GBs": round(cfg0_bytes / cfg0_us / 1e3, 1),
-                                    "frac": round(cfg0_bytes / cfg0_us / 1e3 / HBM_PEAK_GBS, 4)},
+                                    "frac": round(cfg0_bytes / cfg0_us / 1e3 / HBM_PEAK_GBS, 4),
+                                    "kernel_us": round(cfg0_kernel_us, 3),
+                                    "kernel_GBs": round(cfg0_bytes / cfg0_kernel_us / 1e3, 1),
+                                    "kernel_frac": round(cfg0_bytes / cfg0_kernel_us / 1e3 / HBM_PEAK_GBS, 4)},
         },
     }
     if args.prefill_reps:

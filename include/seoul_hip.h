@@ -118,6 +118,9 @@ int sh_q4_gemv_dev(sh_ctx* ctx, const sh_q4* t, const float* x_dev, int n_in, fl
 /* Time `reps` launches of the GEMV over `n_tables` tables in turn (tables[i] read in rotation so that none is
  * resident in the 256 MB MALL when the set is larger), inputs resident; avg_launch_us = mean launch duration. */
 int sh_q4_bench(sh_ctx* ctx, sh_q4* const* tables, int n_tables, int n_in, int cut_mode, int reps, double* avg_launch_us);
+/* The kernel's own duration: each launch timed alone by events recorded around the kernel (no dispatch gap in
+ * front of it), averaged over `reps`; after sh_q4_bench on the same tables (which sizes the device input/output). */
+int sh_q4_bench_kernel(sh_ctx* ctx, sh_q4* const* tables, int n_tables, int n_in, int cut_mode, int reps, double* avg_kernel_us);
 
 /* y[i] = e^x[i] with the exponential the kernels use (softmax, SiLU, head gates): bit for bit the C library's expf
  * that imi runs on (imi/core/seoul.cpp:48,447,451). */

@@ -198,7 +198,7 @@ int enqueue_step(sh_ctx* c, int M, bool want_logits) {
         v.out_ld = I.n_vocab;
         v.part_v = c->part_v;
         v.part_i = c->part_i;
-        const int grid = v.units < c->vocab_grid ? v.units : c->vocab_grid;
+        const int grid = gemv_logits_grid(M, PRO_RESID_NORM, v, c->vocab_grid);
         HIPCHK(launch_gemv(M, PRO_RESID_NORM, EPI_LOGITS, grid, v, c->stream));
         z.part_v = c->part_v;
         z.part_i = c->part_i;
@@ -1275,7 +1275,7 @@ int sh_bench_kernel(sh_ctx* c, int kind, int M, int reps, double* avg_us, double
                 pro = PRO_RESID_NORM; epi = EPI_LOGITS;
                 bytes += (double)c->vocab.rows * c->vocab.nb * 18 + 4.0 * M * (2 * E + I.n_vocab);
             }
-            grid = epi == EPI_LOGITS ? (a.units < c->vocab_grid ? a.units : c->vocab_grid) : (a.units < 4096 ? a.units : 4096);
+            grid = epi == EPI_LOGITS ? gemv_logits_grid(M, pro, a, c->vocab_grid) : (a.units < 4096 ? a.units : 4096);
             HIPCHK(launch_gemv(M, pro, epi, grid, a, c->stream, lt.start(), lt.stop()));
             lt.next();
         }
@@ -1353,7 +1353,9 @@ int sh_q4_rows(sh_ctx* c, const sh_q4* t, const int32_t* ids, int n, float* out)
     return SH_OK;
 }
 
-int sh_q4_gemv_dev(sh_ctx* c, const sh_q4* t, const float* x, int n_in, float* y, int cut_mode) {
+namespace {
+// the kernel-level GEMV launch; with t0/t1 the launch records them around the kernel itself
+int q4_gemv_launch(sh_ctx* c, const sh_q4* t, const float* x, int n_in, float* y, int cut_mode, hipEvent_t t0, hipEvent_t t1) {
     if (!c || !t || !x || !y || n_in < 1 || n_in > 2 || cut_mode < 0 || cut_mode > 1) return fail(SH_E_ARG, "sh_q4_gemv: bad argument");
     if (t->ctx != c) return fail(SH_E_STATE, "sh_q4_gemv: table belongs to another context");
     if (cut_mode == 1 && n_in != 1) return fail(SH_E_ARG, "sh_q4_gemv: the half-away cut takes one input");
@@ -1365,8 +1367,13 @@ int sh_q4_gemv_dev(sh_ctx* c, const sh_q4* t, const float* x, int n_in, float* y
     a.out = y;
     a.out_ld = t->t.rows;
     const int grid = a.units < 4096 ? a.units : 4096;
-    HIPCHK(launch_gemv(n_in, cut_mode ? PRO_CUT_HALF_AWAY : PRO_CUT, EPI_STORE, grid, a, c->stream));
+    HIPCHK(launch_gemv(n_in, cut_mode ? PRO_CUT_HALF_AWAY : PRO_CUT, EPI_STORE, grid, a, c->stream, t0, t1));
     return SH_OK;
+}
+}  // namespace
+
+int sh_q4_gemv_dev(sh_ctx* c, const sh_q4* t, const float* x, int n_in, float* y, int cut_mode) {
+    return q4_gemv_launch(c, t, x, n_in, y, cut_mode, nullptr, nullptr);
 }
 
 int sh_q4_gemv(sh_ctx* c, const sh_q4* t, const float* x, int n_in, float* y, int cut_mode) {
@@ -1419,6 +1426,25 @@ int sh_q4_bench(sh_ctx* c, sh_q4* const* tables, int n_tables, int n_in, int cut
     float ms;
     HIPCHK(hipEventElapsedTime(&ms, c->ev0, c->ev1));
     if (avg_us) *avg_us = ms * 1e3 / reps;
+    return SH_OK;
+}
+
+int sh_q4_bench_kernel(sh_ctx* c, sh_q4* const* tables, int n_tables, int n_in, int cut_mode, int reps, double* avg_us) {
+    if (!c || !tables || n_tables < 1 || reps < 1) return fail(SH_E_ARG, "sh_q4_bench_kernel: bad argument");
+    HIPCHK(hipSetDevice(c->device));
+    double total_ms = 0.0;
+    for (int r = -n_tables; r < reps; r++) {   // the first pass over the tables is a warm-up
+        sh_q4* t = tables[(r + n_tables) % n_tables];
+        const size_t need = (size_t)n_in * (t->t.cols > t->t.rows ? t->t.cols : t->t.rows);
+        if (c->bench_cap < need) return fail(SH_E_STATE, "sh_q4_bench_kernel: run sh_q4_bench on these tables first");
+        const int rc = q4_gemv_launch(c, t, c->bench_x, n_in, c->bench_y, cut_mode, c->ev0, c->ev1);
+        if (rc != SH_OK) return rc;
+        HIPCHK(hipEventSynchronize(c->ev1));
+        float ms;
+        HIPCHK(hipEventElapsedTime(&ms, c->ev0, c->ev1));
+        if (r >= 0) total_ms += ms;
+    }
+    if (avg_us) *avg_us = total_ms * 1e3 / reps;
     return SH_OK;
 }
 

@@ -53,6 +53,7 @@ struct gemv_args {
     float* part_v;             // EPI_LOGITS: per-block best value [M][gridDim.x]
     int* part_i;               // and its row
     step_params* P;
+    int upw;                   // k_gemv_norm: units per workgroup (chunk), 0 = pick
 };
 
 struct attn_args {

@@ -371,6 +371,265 @@ static size_t gemv_cut_lds(int M, int nb) {
     return sizeof(float) * ((size_t)M * nb * 8 + (size_t)M * nb + (size_t)M * st + (size_t)2 * M * 8 * st + 8 * st);
 }
 
+// ---------------------------------------------------------------- Q4_0 GEMV behind the post-norm residual
+// (x += norm(y) * w_post; h = norm(x) * w_pre; imi/core/seoul.cpp:462-475, imi/core/vec.h:20-44), 512 threads per
+// workgroup, a chunk of upw units (UG groups of 8 rows each) per workgroup and step of its loop:
+//  - the prologue's input vectors are requested first, then the first chunk's weights;
+//  - prologue: the E-value vectors are read once per workgroup, one wave per conversation runs imi's AVX2-order norm
+//    chains over them in LDS (rms_scale_wave), every thread updates and normalises its 4 values, and the 8 threads of
+//    each 32-value block cut it to int8 (imi_cut32, imi/core/vec.h:47-75: amax and code sums reduced across lanes);
+//  - dots: thread (row subset, group, block) forms the exact integer dots of its rows, chain operands to LDS;
+//    the next chunk's weights are requested as soon as these registers are free;
+//  - chains: acc on threads 0.., cor on threads 256.. (other SIMDs), imi's per-row order
+//    (imi/core/tables.cpp:127-143); epilogue: rows stored, SwiGLU of (gate, up) groups (imi/core/seoul.cpp:380-394),
+//    the gated short conv of (b, c, x) groups (:407-423) or word scores with the workgroup's first maximum.
+template <int M, int EPI, int UG>
+__global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
+    extern __shared__ __align__(16) float lds[];
+    const int E = a.E, nb = a.W.nb, st = ((nb + 3) & ~3) + 4;
+    const int upw = a.upw, G = upw * UG, R = 8 * G, C = M * R;
+    const int t = threadIdx.x, nq = E / 4;
+    float* l_v = lds;                              // [M][E] the norm input (y, then x)
+    int* l_xq = (int*)(l_v + M * E);               // [M][nb][8] codes of the cut input
+    float* l_dx = (float*)(l_xq + M * nb * 8);     // [M][nb]
+    float* l_s = l_dx + M * nb;                    // [M][st]
+    float* l_op = l_s + M * st;                    // [M][R][st] float(isum)
+    float* l_oq = l_op + M * R * st;               // [M][R][st] d * dx
+    float* l_dd = l_oq + M * R * st;               // [R][st] d
+    float* l_cor = l_dd + R * st;                  // [C]
+    float* l_out = l_cor + C;                      // [C]
+    float* l_sc = l_out + C;                       // [16] norm scales, reduction scratch
+    int* l_si = (int*)(l_sc + 16);                 // [16]
+
+    const int gtot = a.W.rows / 8, nchunk = (a.units + upw - 1) / upw;
+    // this thread's share of a chunk's weights: rows sub * rpt .. + rpt - 1 of group gi, block jw
+    const int np = G * nb, rpt = np <= 64 ? 1 : np <= 128 ? 2 : np <= 256 ? 4 : 8;
+    const bool wt = t < np * (8 / rpt);
+    const int sub = t / np, pr = t - sub * np, gi = pr / nb, jw = pr - gi * nb;
+    u32x4 w[9];
+    // all 9 loads are issued on every path (rows past this thread's share and absent groups re-read a row it owns,
+    // which the caches serve), so the compiler counts them exactly and the prologue waits only for its own inputs
+    auto load_chunk = [&](int k) {
+        const int g = min(k * G + (wt ? gi : 0), gtot - 1), s0 = wt ? sub * rpt : 0;
+        const u32x4* cp = (const u32x4*)a.W.codes + (size_t)(8 * g + s0) * nb + jw;
+#pragma unroll
+        for (int r = 0; r < 8; r++) w[r] = __builtin_nontemporal_load(cp + (size_t)(r < rpt ? r : 0) * nb);
+        w[8] = __builtin_nontemporal_load((const u32x4*)a.W.scales + (size_t)g * nb + jw);
+    };
+    // ---- prologue: its inputs are requested first (a wave's loads complete in order, so the norm work can start
+    // while the weights that follow are still streaming in) ----
+    // (every load on every path: threads past the E / 4 quads re-read the last one, and a workgroup past the last
+    // chunk loads that chunk, so the compiler's wait counts stay exact)
+    f32x4 xv[M], yv[M];
+    const int tq = t < nq ? t : nq - 1;
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        xv[m] = ((const f32x4*)(a.x_in + (size_t)m * E))[tq];
+        yv[m] = ((const f32x4*)(a.y_in + (size_t)m * E))[tq];
+    }
+    const f32x4 wp = ((const f32x4*)a.w_post)[tq], wq = ((const f32x4*)a.w_pre)[tq];
+    int k = blockIdx.x;
+    load_chunk(k < nchunk ? k : nchunk - 1);
+    {   // x += norm(y) * w_post (imi_norm_mul_add)
+        if (t < nq)
+#pragma unroll
+            for (int m = 0; m < M; m++) ((f32x4*)(l_v + m * E))[t] = yv[m];
+        __syncthreads();
+        if ((t >> 6) < M) {
+            const float sc = rms_scale_wave(l_v + (t >> 6) * E, E, a.eps);
+            if ((t & 63) == 0) l_sc[t >> 6] = sc;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const float sc = l_sc[m];
+            xv[m].x = fmaf(yv[m].x * sc, wp.x, xv[m].x);
+            xv[m].y = fmaf(yv[m].y * sc, wp.y, xv[m].y);
+            xv[m].z = fmaf(yv[m].z * sc, wp.z, xv[m].z);
+            xv[m].w = fmaf(yv[m].w * sc, wp.w, xv[m].w);
+        }
+        __syncthreads();
+    }
+    if (t < nq)
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            ((f32x4*)(l_v + m * E))[t] = xv[m];
+            if (blockIdx.x == 0 && a.x_out) ((f32x4*)(a.x_out + (size_t)m * E))[t] = xv[m];
+        }
+    __syncthreads();
+    if ((t >> 6) < M) {   // h = norm(x) * w_pre (imi_norm_mul)
+        const float sc = rms_scale_wave(l_v + (t >> 6) * E, E, a.eps);
+        if ((t & 63) == 0) l_sc[4 + (t >> 6)] = sc;
+    }
+    __syncthreads();
+    if (t < nq) {
+        const int j = t >> 3, q = t & 7;   // block j, values 4q .. 4q+3 (8 consecutive lanes per block)
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const float sc = l_sc[4 + m];
+            float h[4] = {xv[m].x * sc * wq.x, xv[m].y * sc * wq.y, xv[m].z * sc * wq.z, xv[m].w * sc * wq.w};
+            if (a.hidden_out && blockIdx.x == 0) ((f32x4*)(a.hidden_out + (size_t)m * E))[t] = f32x4{h[0], h[1], h[2], h[3]};
+            float amax = fmaxf(fmaxf(fabsf(h[0]), fabsf(h[1])), fmaxf(fabsf(h[2]), fabsf(h[3])));
+            amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(amax), 0xB1, 0xF, 0xF, true)));
+            amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(amax), 0x4E, 0xF, 0xF, true)));
+            amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(amax), 0x141, 0xF, 0xF, true)));
+            const float d = amax / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            int sum = 0;
+            unsigned packed = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int cq = (int)rintf(h[i] * id);
+                sum += cq;
+                packed |= ((unsigned)cq & 0xFFu) << (8 * i);
+            }
+            sum += __builtin_amdgcn_update_dpp(0, sum, 0xB1, 0xF, 0xF, true);
+            sum += __builtin_amdgcn_update_dpp(0, sum, 0x4E, 0xF, 0xF, true);
+            sum += __builtin_amdgcn_update_dpp(0, sum, 0x141, 0xF, 0xF, true);
+            l_xq[(m * nb + j) * 8 + q] = (int)packed;
+            if (q == 0) {
+                l_dx[m * nb + j] = d;
+                l_s[m * st + j] = d * (float)sum;
+            }
+        }
+    }
+    __syncthreads();
+
+    float best_v[M];
+    int best_i[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) { best_v[m] = -INFINITY; best_i[m] = 0x7fffffff; }
+    for (; k < nchunk; k += gridDim.x) {
+        const int u0 = k * upw, g0 = k * G, gv = min(G, gtot - g0);   // groups of this chunk that exist
+        // ---- dots: exact integer sums of this thread's rows, chain operands to LDS ----
+        if (wt && gi < gv) {
+            const unsigned sw[4] = {w[8].x, w[8].y, w[8].z, w[8].w};
+            float d[8];
+#pragma unroll
+            for (int r = 0; r < 8; r++) {
+                const int rr = (sub * rpt + r) & 7;
+                const unsigned word = (rr >> 1) == 0 ? sw[0] : (rr >> 1) == 1 ? sw[1] : (rr >> 1) == 2 ? sw[2] : sw[3];
+                d[r] = h2f((uint16_t)((rr & 1) ? (word >> 16) : (word & 0xFFFFu)));
+            }
+            const int r0 = 8 * gi + sub * rpt;
+#pragma unroll
+            for (int r = 0; r < 8; r++)
+                if (r < rpt) l_dd[(r0 + r) * st + jw] = d[r];
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                const u32x4* xs = (const u32x4*)(l_xq + (m * nb + jw) * 8);
+                const u32x4 x0 = xs[0], x1 = xs[1];
+                const int xq[8] = {(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+                const float dx = l_dx[m * nb + jw];
+#pragma unroll
+                for (int r = 0; r < 8; r++)
+                    if (r < rpt) {
+                        l_op[(m * R + r0 + r) * st + jw] = (float)q4_block_dot(w[r], xq);
+                        l_oq[(m * R + r0 + r) * st + jw] = d[r] * dx;
+                    }
+            }
+        }
+        __syncthreads();
+        if (k + (int)gridDim.x < nchunk) load_chunk(k + gridDim.x);   // in flight during the chains
+        // ---- chains ----
+        const bool acc_lane = t < C, cor_lane = t >= 256 && t - 256 < C;
+        float chain = 0.0f;
+        const int c = acc_lane ? t : t - 256;
+        if ((acc_lane || cor_lane) && (c % R) < 8 * gv) {
+            const int m = c / R, r = c - m * R;
+            const f32x4* ap = (const f32x4*)(acc_lane ? l_op + (m * R + r) * st : l_dd + r * st);
+            const f32x4* bp = (const f32x4*)(acc_lane ? l_oq + (m * R + r) * st : l_s + m * st);
+            if ((nb & 63) == 0) {
+                for (int q0 = 0; q0 < nb / 4; q0 += 16) {
+                    f32x4 qa[16], qb[16];
+#pragma unroll
+                    for (int q = 0; q < 6; q++) { qa[q] = ap[q0 + q]; qb[q] = bp[q0 + q]; }
+#pragma unroll
+                    for (int q = 0; q < 16; q++) {
+                        if (q + 6 < 16) { qa[q + 6] = ap[q0 + q + 6]; qb[q + 6] = bp[q0 + q + 6]; }
+                        __builtin_amdgcn_sched_barrier(0);
+                        chain = fmaf(qa[q].x, qb[q].x, chain);
+                        chain = fmaf(qa[q].y, qb[q].y, chain);
+                        chain = fmaf(qa[q].z, qb[q].z, chain);
+                        chain = fmaf(qa[q].w, qb[q].w, chain);
+                    }
+                }
+            } else {
+                const float* as = (const float*)ap;
+                const float* bs = (const float*)bp;
+                for (int q = 0; q < nb; q++) chain = fmaf(as[q], bs[q], chain);
+            }
+            if (cor_lane) l_cor[c] = chain;
+        }
+        __syncthreads();
+        if (acc_lane) l_out[c] = fmaf(-8.0f, l_cor[c], chain);
+        __syncthreads();
+        // ---- epilogue: thread c < C holds row r of the chunk for input m ----
+        if (t < C) {
+            const int m = t / R, r = t - m * R;
+            const float v = l_out[t];
+            if (r < 8 * gv) {
+                if (EPI == EPI_STORE) {
+                    a.out[(size_t)m * a.out_ld + 8 * g0 + r] = v;
+                } else if (EPI == EPI_SWIGLU) {   // unit = (gate group, up group) of 8 channels
+                    const int ui = r >> 4, i = r & 15;
+                    if (i < 8) a.out[(size_t)m * a.out_ld + 8 * (u0 + ui) + i] = silu(v) * l_out[t + 8];
+                } else if (EPI == EPI_CONV) {     // unit = (b, c, x) groups of 8 channels
+                    const int ui = r / 24, i = r - 24 * ui;
+                    if (i < 8) {
+                        const int e = 8 * (u0 + ui) + i, dc = a.d_conv;
+                        const float cc = l_out[t + 8], xx = l_out[t + 16];
+                        float* stt = a.P->conv[m] + (size_t)a.conv_layer * dc * E;
+                        const float bx = v * xx;
+                        float uu = v * xx * a.conv_w[(size_t)dc * E + e];
+                        for (int q = 0; q < dc; q++) uu = fmaf(stt[(size_t)q * E + e], a.conv_w[(size_t)q * E + e], uu);
+                        uu *= cc;
+                        for (int q = 0; q + 1 < dc; q++) stt[(size_t)q * E + e] = stt[(size_t)(q + 1) * E + e];
+                        stt[(size_t)(dc - 1) * E + e] = bx;
+                        a.out[(size_t)m * a.out_ld + e] = uu;
+                    }
+                } else {   // EPI_LOGITS
+                    const int row = 8 * g0 + r;
+                    if (a.out) a.out[(size_t)m * a.out_ld + row] = v;
+#pragma unroll
+                    for (int mm = 0; mm < M; mm++)
+                        if (mm == m && (v > best_v[mm] || (v == best_v[mm] && row < best_i[mm]))) { best_v[mm] = v; best_i[mm] = row; }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (EPI == EPI_LOGITS) {   // the workgroup's first maximum per input
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            float v = best_v[m];
+            int i = best_i[m];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const float ov = __shfl_xor(v, o);
+                const int oi = __shfl_xor(i, o);
+                if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+            }
+            if ((t & 63) == 0) { l_sc[8 + (t >> 6)] = v; l_si[8 + (t >> 6)] = i; }
+            __syncthreads();
+            if (t == 0) {
+                float bv = l_sc[8];
+                int bi = l_si[8];
+                for (int q = 1; q < 8; q++)
+                    if (l_sc[8 + q] > bv || (l_sc[8 + q] == bv && l_si[8 + q] < bi)) { bv = l_sc[8 + q]; bi = l_si[8 + q]; }
+                a.part_v[m * gridDim.x + blockIdx.x] = bv;
+                a.part_i[m * gridDim.x + blockIdx.x] = bi;
+            }
+            __syncthreads();
+        }
+    }
+}
+
+static size_t gemv_norm_lds(int M, int E, int nb, int G) {
+    const size_t st = (size_t)(((nb + 3) & ~3) + 4), R = 8 * (size_t)G, C = M * R;
+    return sizeof(float) * ((size_t)M * E + (size_t)M * nb * 8 + (size_t)M * nb + M * st + 2 * M * R * st + R * st + 2 * C + 32);
+}
+
 // dynamic LDS bytes of a k_gemv instantiation
 static size_t gemv_lds(int M, int UG, int nb, int E, bool norm) {
     const int R = 8 * UG;
@@ -462,6 +721,157 @@ __global__ __launch_bounds__(256) void k_attn(attn_args a) {
         const int h = g * grp + hh;
         const float gate = 1.0f / (1.0f + expf_glibc(-row[Hq + 2 * kvd + h]));
         a.att[(size_t)m * Hq + h * D + i] = o * gate;
+    }
+}
+
+// ---------------------------------------------------------------- GQA decode attention, one query head per block
+// Block (query head h, conversation m), 256 threads, imi/core/seoul.cpp:433-453 in the CPU's op order. The key rows
+// of the first 256 positions and the first tile of value rows are requested before anything else (they are the
+// cache rows of earlier steps); then q = rope(norm(q) * q_norm) (wave 0) and this position's k = rope(norm(k) *
+// k_norm) and v (wave 1; the first head of each kv group writes them to the fp16 cache, the group's other heads use
+// their own copy, which is the same number); score_t = dot_h(q, K_t) / sqrt(D), thread per position; softmax with the
+// max subtracted, glibc's expf and a double sum in position order; o = sum_t fma(e_t * inv, V_t, o) in order over t
+// by lane i of wave 0, value rows through LDS in tiles; times the sigmoid head gate.
+template <int D>
+__global__ __launch_bounds__(256) void k_attn_head(attn_args a) {
+    constexpr int TV = 256, half = D / 2, KW = D / 8;   // positions per value tile, 16-byte words per row
+    extern __shared__ __align__(16) float lds[];
+    const int h = blockIdx.x, m = blockIdx.y, t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int grp = a.n_head / a.n_kv, g = h / grp, hh = h - g * grp;
+    const int Hq = a.n_head * D, kvd = a.n_kv * D;
+    const int pos = a.P->pos[m];
+    const int s0 = a.n_swa > 0 ? max(0, pos - a.n_swa + 1) : 0, nk = pos - s0 + 1;
+    uint16_t* kc = a.P->kc[m] + ((size_t)a.layer_ai * a.n_kv + g) * a.n_ctx * D;
+    uint16_t* vc = a.P->vc[m] + ((size_t)a.layer_ai * a.n_kv + g) * a.n_ctx * D;
+    const float* row = a.qkv + (size_t)m * a.ld_qkv;
+    float* q_s = lds;                              // [D]
+    float* k_s = q_s + D;                          // [D] this position's key as the cache holds it
+    float* red = k_s + D;                          // [32]
+    float* stg = red + 32;                         // [2][D] norm staging of waves 0 and 1
+    float* sc = stg + 2 * D;                       // [n_ctx] scores, then e_t
+    u32x4* vt = (u32x4*)(sc + ((a.n_ctx + 3) & ~3));   // [TV][KW] fp16 value rows
+    const float2* cs = a.rope_cs + (size_t)pos * half;
+
+    // ---- requests first: key row of position s0 + t (t < nk - 1), value tile 0 (positions before pos) ----
+    const int kp = s0 + min(t, max(nk - 2, 0));
+    u32x4 kw[KW];
+#pragma unroll
+    for (int i = 0; i < KW; i++) kw[i] = ((const u32x4*)(kc + (size_t)kp * D))[i];
+    const int nv0 = min(TV, nk - 1) * KW;          // words of tile 0 before pos
+    constexpr int VPT = TV * KW / 256;             // words per thread
+    u32x4 vw[VPT];
+#pragma unroll
+    for (int q = 0; q < VPT; q++) {
+        const int e = min(t + 256 * q, max(nv0 - 1, 0));
+        vw[q] = ((const u32x4*)(vc + (size_t)s0 * D))[e];
+    }
+    // ---- q (wave 0) and this position's k, v (wave 1): norm + NEOX rope (imi/core/seoul.cpp:19-28) ----
+    if (wv < 2) {
+        const bool is_k = wv == 1;
+        const float* src = is_k ? row + Hq + g * D : row + h * D;
+        const float* w = is_k ? a.k_norm : a.q_norm;
+        float* st = stg + wv * D;
+        const float x = lane < D ? src[lane] : 0.0f;
+        if (lane < D) st[lane] = x;
+        __builtin_amdgcn_wave_barrier();
+        const float s = rms_scale_wave(st, D, a.eps);
+        const float n = lane < D ? x * s * w[lane] : 0.0f;
+        const float other = __shfl(n, lane < half ? lane + half : lane - half);
+        if (lane < D) {
+            const float2 cz = cs[lane < half ? lane : lane - half];
+            const float r = lane < half ? fmaf(n, cz.x, -(other * cz.y)) : fmaf(other, cz.y, n * cz.x);
+            if (is_k) {
+                const uint16_t kh = f2h(r), vh = f2h(row[Hq + kvd + g * D + lane]);
+                k_s[lane] = h2f(kh);
+                if (nk <= TV) ((uint16_t*)vt)[(nk - 1) * D + lane] = vh;   // tile 0 holds this position
+                if (hh == 0) {
+                    kc[(size_t)pos * D + lane] = kh;
+                    vc[(size_t)pos * D + lane] = vh;
+                }
+            } else {
+                q_s[lane] = r;
+            }
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < VPT; q++) {
+        const int e = t + 256 * q;
+        if (e < nv0) vt[e] = vw[q];
+    }
+    __syncthreads();
+    // ---- scores ----
+    const float scale = 1.0f / sqrtf((float)D);
+    for (int p = t; p < nk; p += 256) {
+        float kf[D];
+        if (p == nk - 1) {
+#pragma unroll
+            for (int i = 0; i < D; i++) kf[i] = k_s[i];
+        } else {
+            if (p != t) {
+#pragma unroll
+                for (int i = 0; i < KW; i++) kw[i] = ((const u32x4*)(kc + (size_t)(s0 + p) * D))[i];
+            }
+#pragma unroll
+            for (int i = 0; i < KW; i++) {
+                const unsigned w4[4] = {kw[i].x, kw[i].y, kw[i].z, kw[i].w};
+#pragma unroll
+                for (int e = 0; e < 8; e++) kf[8 * i + e] = h2f((uint16_t)((w4[e >> 1] >> (16 * (e & 1))) & 0xFFFFu));
+            }
+        }
+        sc[p] = dot_h8<D>(q_s, kf) * scale;
+    }
+    __syncthreads();
+    // ---- softmax: max, e_t = expf(s_t - max), double sum in position order ----
+    float mx = -INFINITY;
+    for (int p = t; p < nk; p += 256) mx = fmaxf(mx, sc[p]);
+    mx = wave_max(mx);
+    if (lane == 0) red[wv] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int p = t; p < nk; p += 256) sc[p] = expf_glibc(sc[p] - mx);
+    __syncthreads();
+    if (t == 0) {
+        double sum = 0.0;
+        int p = 0;
+        for (; p + 8 <= nk; p += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = sc[p + u];
+#pragma unroll
+            for (int u = 0; u < 8; u++) sum += (double)v[u];
+        }
+        for (; p < nk; p++) sum += (double)sc[p];
+        red[8] = (float)(1.0 / sum);
+    }
+    __syncthreads();
+    // ---- o = sum_t fma(e_t * inv, V_t, o), lane i of wave 0, value rows through LDS in tiles of TV ----
+    const float inv = red[8];
+    float o = 0.0f;
+    const uint16_t* vh = (const uint16_t*)vt;
+    for (int q0 = 0; q0 < nk; q0 += TV) {
+        const int nt = min(TV, nk - q0);
+        if (q0 > 0) {   // tile 0 is in LDS already
+            __syncthreads();
+            const int nv = (q0 + nt == nk ? nt - 1 : nt) * KW;   // pos's row comes from this position's v
+            for (int e = t; e < nv; e += 256) vt[e] = ((const u32x4*)(vc + (size_t)(s0 + q0) * D))[e];
+            if (q0 + nt == nk && t < D) ((uint16_t*)vt)[(nt - 1) * D + t] = f2h(row[Hq + kvd + g * D + t]);
+            __syncthreads();
+        }
+        if (t < D) {
+            int p = 0;
+            for (; p + 8 <= nt; p += 8) {
+                float e[8], v[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) { e[u] = sc[q0 + p + u]; v[u] = h2f(vh[(p + u) * D + t]); }
+#pragma unroll
+                for (int u = 0; u < 8; u++) o = fmaf(e[u] * inv, v[u], o);
+            }
+            for (; p < nt; p++) o = fmaf(sc[q0 + p] * inv, h2f(vh[p * D + t]), o);
+        }
+    }
+    if (t < D) {
+        const float gate = 1.0f / (1.0f + expf_glibc(-row[Hq + 2 * kvd + h]));
+        a.att[(size_t)m * Hq + h * D + t] = o * gate;
     }
 }
 
@@ -559,9 +969,44 @@ __global__ __launch_bounds__(64) void k_q4_rows(q4dev T, const int32_t* ids, flo
         return hipGetLastError();                                                                                \
     }
 
+// tables behind the post-norm residual that k_gemv_norm takes (E a multiple of 128 up to 2048, the table's input E)
+static bool norm_kernel_takes(int M, int pro, const gemv_args& a, int ug) {
+    return pro == PRO_RESID_NORM && (M == 1 || M == 2) && a.E % 128 == 0 && a.E <= 2048 && a.W.nb * 32 == a.E &&
+           a.W.cols == a.E && a.x_in && a.y_in && a.w_post && a.W.rows % (8 * ug) == 0;
+}
+
+int gemv_logits_grid(int M, int pro, const gemv_args& a, int max_grid) {
+    if (norm_kernel_takes(M, pro, a, 1)) return 256;   // k_gemv_norm: one workgroup per compute unit, chunks looped
+    return a.units < max_grid ? a.units : max_grid;
+}
+
 hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
     const int nbl = (a.W.nb + 63) / 64;
     const int ug = epi == EPI_SWIGLU ? 2 : epi == EPI_CONV ? 3 : 1;
+    if (norm_kernel_takes(M, pro, a, ug)) {
+        gemv_args b = a;
+        // units per chunk: 8 groups for the word scores (looped), else enough that one round of workgroups (one
+        // per compute unit: the register use allows one 512-thread workgroup per unit) covers the table
+        const int cap = 8 / ug, want = (a.units + 255) / 256;
+        b.upw = epi == EPI_LOGITS ? 8 : (want < 1 ? 1 : want > cap ? cap : want);
+        const int nchunk = (a.units + b.upw - 1) / b.upw;
+        const void* fn = nullptr;
+#define SH_NORM_FN(M_, EPI_, UG_) if (M == M_ && epi == EPI_) fn = (const void*)k_gemv_norm<M_, EPI_, UG_>;
+        SH_NORM_FN(1, EPI_STORE, 1) SH_NORM_FN(1, EPI_SWIGLU, 2) SH_NORM_FN(1, EPI_CONV, 3) SH_NORM_FN(1, EPI_LOGITS, 1)
+        SH_NORM_FN(2, EPI_STORE, 1) SH_NORM_FN(2, EPI_SWIGLU, 2) SH_NORM_FN(2, EPI_CONV, 3) SH_NORM_FN(2, EPI_LOGITS, 1)
+#undef SH_NORM_FN
+        if (!fn) return hipErrorInvalidValue;
+        const size_t lds = gemv_norm_lds(M, a.E, a.W.nb, b.upw * ug);
+        if (lds > 160 * 1024) return hipErrorInvalidValue;
+        if (lds > 64 * 1024) {
+            const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+        }
+        void* args[] = {&b};
+        const dim3 gr(epi == EPI_LOGITS ? grid : nchunk), bl(512);
+        if (t0) return hipExtLaunchKernel(fn, gr, bl, args, lds, s, t0, t1, 0);
+        return hipLaunchKernel(fn, gr, bl, args, lds, s);
+    }
     // the plain tables (input cut, rows stored): one workgroup per 8-row group, the grid is the group count
     const int nb = a.W.nb;
     if (epi == EPI_STORE && (pro == PRO_CUT || pro == PRO_CUT_HALF_AWAY) && (nb == 64 || nb == 128 || nb == 256) &&
@@ -604,6 +1049,19 @@ hipError_t launch_attn(int M, const attn_args& a, hipStream_t s) {
     const int grp = a.n_head / a.n_kv;
     const size_t lds = sizeof(float) * ((size_t)grp * a.D + (size_t)grp * a.n_ctx + 5 * (size_t)a.D + (size_t)grp);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
+    {   // one block per query head
+        const size_t lds2 = sizeof(float) * (4 * (size_t)a.D + 32 + (((size_t)a.n_ctx + 3) & ~(size_t)3)) + (size_t)256 * a.D * 2;
+        const void* fh = a.D == 64 ? (const void*)k_attn_head<64> : a.D == 32 ? (const void*)k_attn_head<32> : nullptr;
+        if (fh && lds2 <= 160 * 1024) {
+            if (lds2 > 64 * 1024) {
+                const hipError_t e = hipFuncSetAttribute(fh, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
+                if (e != hipSuccess) return e;
+            }
+            attn_args b = a;
+            void* args[] = {&b};
+            return hipLaunchKernel(fh, dim3(a.n_head, M), dim3(256), args, lds2, s);
+        }
+    }
     const void* fn = a.D == 64 ? (const void*)k_attn<64> : a.D == 32 ? (const void*)k_attn<32> : nullptr;
     if (!fn) return hipErrorInvalidValue;
     if (lds > 64 * 1024) {

@@ -14,6 +14,17 @@ from conftest import rel
 
 pytestmark = pytest.mark.gpu
 
+@pytest.fixture(params=["persistent", "kernels"])
+def step_path(request, monkeypatch):
+    """Both device paths of a step: the persistent step kernel and the per-table kernels (SEOUL_HIP_STEP=kernels,
+    also the path taken when a cooperative launch is refused); contexts read the choice when they are made."""
+    if request.param == "kernels":
+        monkeypatch.setenv("SEOUL_HIP_STEP", "kernels")
+    else:
+        monkeypatch.delenv("SEOUL_HIP_STEP", raising=False)
+    return request.param
+
+
 def same(a, b) -> bool:
     a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
     return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
@@ -36,15 +47,15 @@ def _compare_steps(path, tokens, n_ctx=256, threads=4):
         assert bg == oracle.top(lo) == int(np.argmax(lg))
 
 
-def test_tiny_model_steps(tiny_model):
+def test_tiny_model_steps(tiny_model, step_path):
     _compare_steps(tiny_model, _prompt(40, 1000, 1))
 
 
-def test_seoul_width_steps(mid_model):
+def test_seoul_width_steps(mid_model, step_path):
     _compare_steps(mid_model, _prompt(24, 4096, 2))
 
 
-def test_embedding_input_and_no_logits(tiny_model):
+def test_embedding_input_and_no_logits(tiny_model, step_path):
     import nunchi_amd
     import oracle
     g = nunchi_amd.Brain(tiny_model, n_ctx=64)
@@ -62,7 +73,7 @@ def test_embedding_input_and_no_logits(tiny_model):
             assert lg is None and bg == -1
 
 
-def test_step2_equals_two_steps(tiny_model):
+def test_step2_equals_two_steps(tiny_model, step_path):
     """imi/core/seoul.cpp:222-224: each conversation of step2 gets exactly its own step's numbers."""
     import nunchi_amd
     g = nunchi_amd.Brain(tiny_model, n_ctx=64)
@@ -83,7 +94,7 @@ def test_step2_equals_two_steps(tiny_model):
     assert g.pos == 12 and b.pos == 12
 
 
-def test_step2_matches_oracle(mid_model):
+def test_step2_matches_oracle(mid_model, step_path):
     import nunchi_amd
     import oracle
     g = nunchi_amd.Brain(mid_model, n_ctx=64)
@@ -113,7 +124,7 @@ def test_step_batch_matches_oracle(tiny_model):
     assert g.pos == 70
 
 
-def test_greedy_generation_matches_oracle(mid_model):
+def test_greedy_generation_matches_oracle(mid_model, step_path):
     import nunchi_amd
     import oracle
     g = nunchi_amd.Brain(mid_model, n_ctx=128)
@@ -129,7 +140,7 @@ def test_greedy_generation_matches_oracle(mid_model):
     assert g.pos == 8 + 48 and secs > 0
 
 
-def test_greedy_two_conversations(tiny_model):
+def test_greedy_two_conversations(tiny_model, step_path):
     import nunchi_amd
     import oracle
     g = nunchi_amd.Brain(tiny_model, n_ctx=96)
@@ -164,7 +175,7 @@ def test_state_semantics(tiny_model):
     assert g.pos == 8
 
 
-def test_full_seoul_step_and_greedy(model_dir):
+def test_full_seoul_step_and_greedy(model_dir, step_path):
     """cfg 2: the full Seoul-shaped model, a 32-token prompt, then 256 greedy ids; every id and the final state agree."""
     import nunchi_amd
     import oracle
