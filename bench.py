@@ -237,14 +237,13 @@ def main():
     del copies
 
     gu_gbs = gu["bytes_per_launch"] / (gu["avg_us"] * 1e-6) / 1e9
-    # algorithmic bytes of the greedy launch (the step kernel k_step<1>, one launch for all --steps): per step every
-    # table once (device layout = file bytes: 16 B codes + 2 B scale per 32 weights), the fp32 norm / conv vectors,
-    # and the K and V rows the step's attention reads (positions 0..pos of n_attn layers x n_kv heads x D, fp16)
+    # algorithmic bytes of a decode step: every table once (device layout = file bytes: 16 B codes + 2 B scale per
+    # 32 weights), the fp32 norm / conv vectors, and the K and V rows the step's attention reads (positions 0..pos of
+    # n_attn layers x n_kv heads x D, fp16), averaged over the generated positions
     kv_row = brain.n_attn * brain.n_head_kv * brain.head_dim * 2
     vec_bytes = brain.vector_bytes
-    launch_bytes = sum(brain.table_bytes + vec_bytes + 2 * kv_row * (PROMPT + i + 1) for i in range(args.steps))
-    step_bytes = launch_bytes / args.steps
-    launch_gbs = launch_bytes / dev_b1 / 1e9
+    gen_bytes = sum(brain.table_bytes + vec_bytes + 2 * kv_row * (PROMPT + i + 1) for i in range(args.steps))
+    step_bytes = gen_bytes / args.steps
     line = {
         "metric": "brain-step tokens/s (B=1,2) + Q4_0 GEMV HBM GB/s vs roofline, 1 MI355X",
         "value": round(tok_s_b1, 1),
@@ -271,16 +270,19 @@ def main():
         "step_hbm_fraction": {"b1": round(step_bytes * tok_s_b1 / 1e9 / HBM_PEAK_GBS, 4),
                               "b2": round(step_bytes * tok_s_b2 / 2 / 1e9 / HBM_PEAK_GBS, 4),
                               "bytes_per_step": int(step_bytes)},
+        # the dominant kernel of the step: FFN gate|up (16 launches per step, the largest share of its time), each
+        # launch timed alone with HIP events on the context's stream, rotating over the 16 layers' tables
         "roofline": {
-            "kernel": f"k_step<1> (persistent step kernel: one launch, {args.steps} greedy decode steps, B=1)",
+            "kernel": "k_gemv_norm<1, EPI_SWIGLU, 2> (FFN gate|up 16384 x 2048 Q4_0 with the post-norm residual, RMS "
+                      "norm, int8 cut and SwiGLU fused; B=1)",
             "bound": "hbm",
-            "achieved": round(launch_gbs, 1),
+            "achieved": round(gu_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(launch_gbs / HBM_PEAK_GBS, 4),
+            "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "launch_us": round(dev_b1 * 1e6, 1),
-            "bytes_per_launch": int(launch_bytes),
+            "launch_us": round(gu["avg_us"], 3),
+            "bytes_per_launch": int(gu["bytes_per_launch"]),
         },
         "kernels": {
             "ffn_gate_up_per_table": {"avg_us": round(gu["avg_us"], 3), "GBs": round(gu_gbs, 1), "frac": round(gu_gbs / HBM_PEAK_GBS, 4)},

@@ -102,7 +102,7 @@ struct sh_ctx {
     // not trace graph launches)
     bool use_graphs = true;
     // persistent step kernel: its program, tagged record buffers and per-launch staging
-    bool use_persistent = true;       // SEOUL_HIP_STEP=kernels selects the graph of per-table kernels
+    bool use_persistent = false;      // SEOUL_HIP_STEP=persistent selects the persistent step kernel
     std::vector<sk_stage> sk_host;
     sk_stage* sk_dev = nullptr;
     char* sk_mem = nullptr;

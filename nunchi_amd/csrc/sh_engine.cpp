@@ -1,8 +1,8 @@
 // libseoul_hip: the brain step of imi's engine (imi/core/seoul.{h,cpp}) on one MI355X, behind the C ABI of
 // include/seoul_hip.h. Host side: GGUF read, repack into the device layout, conversation states, and the step as
-// one cooperative launch of the persistent step kernel (sh_step.hip) running every stage of n steps. The same
-// stages also exist as separate fused kernels (one per table read, plus attention and the end of step), replayed
-// from a captured HIP graph when SEOUL_HIP_STEP=kernels; the per-table kernel API and benchmarks use those.
+// a captured HIP graph of fused kernels (one per table read, with the norms, cuts and epilogues folded in, plus
+// attention and the end of step; sh_kernels.hip). SEOUL_HIP_STEP=persistent runs the same stages instead as one
+// cooperative launch of the persistent step kernel (sh_step.hip) covering every stage of n steps.
 #include "../../include/seoul_hip.h"
 
 #include <hip/hip_runtime.h>
@@ -453,7 +453,7 @@ int sh_create(int device, sh_ctx** out) {
     const char* g = getenv("SEOUL_HIP_GRAPHS");
     c->use_graphs = !(g && g[0] == '0');
     const char* sp = getenv("SEOUL_HIP_STEP");
-    c->use_persistent = !(sp && strcmp(sp, "kernels") == 0);
+    c->use_persistent = sp && strcmp(sp, "persistent") == 0;
     const char* pf = getenv("SEOUL_HIP_PREFILL");
     c->use_prefill = !(pf && strcmp(pf, "0") == 0);
     const char* tr = getenv("SEOUL_HIP_TRACE");

@@ -14,12 +14,12 @@ from conftest import rel
 
 pytestmark = pytest.mark.gpu
 
-@pytest.fixture(params=["persistent", "kernels"])
+@pytest.fixture(params=["kernels", "persistent"])
 def step_path(request, monkeypatch):
-    """Both device paths of a step: the persistent step kernel and the per-table kernels (SEOUL_HIP_STEP=kernels,
-    also the path taken when a cooperative launch is refused); contexts read the choice when they are made."""
-    if request.param == "kernels":
-        monkeypatch.setenv("SEOUL_HIP_STEP", "kernels")
+    """Both device paths of a step: the graph of per-table kernels (the default) and the persistent step kernel
+    (SEOUL_HIP_STEP=persistent); contexts read the choice when they are made."""
+    if request.param == "persistent":
+        monkeypatch.setenv("SEOUL_HIP_STEP", "persistent")
     else:
         monkeypatch.delenv("SEOUL_HIP_STEP", raising=False)
     return request.param
