@@ -36,16 +36,18 @@ __device__ __forceinline__ int wave_isum(int v) {
 // column 16 + i in the high nibble); the input block is 8 dwords of int8 (columns 0..31). Codes 0..15 are valid
 // signed bytes, so the signed 4-way dot applies directly; the -8 offset is folded in by the caller.
 __device__ __forceinline__ int q4_block_dot(u32x4 c, const int* xq) {
-    int s = 0;
+    // two independent accumulators (low and high nibbles): integer sums, so the split changes nothing but the
+    // dependency depth
+    int s = 0, u = 0;
     s = __builtin_amdgcn_sdot4((int)(c.x & 0x0F0F0F0Fu), xq[0], s, false);
+    u = __builtin_amdgcn_sdot4((int)((c.x >> 4) & 0x0F0F0F0Fu), xq[4], u, false);
     s = __builtin_amdgcn_sdot4((int)(c.y & 0x0F0F0F0Fu), xq[1], s, false);
+    u = __builtin_amdgcn_sdot4((int)((c.y >> 4) & 0x0F0F0F0Fu), xq[5], u, false);
     s = __builtin_amdgcn_sdot4((int)(c.z & 0x0F0F0F0Fu), xq[2], s, false);
+    u = __builtin_amdgcn_sdot4((int)((c.z >> 4) & 0x0F0F0F0Fu), xq[6], u, false);
     s = __builtin_amdgcn_sdot4((int)(c.w & 0x0F0F0F0Fu), xq[3], s, false);
-    s = __builtin_amdgcn_sdot4((int)((c.x >> 4) & 0x0F0F0F0Fu), xq[4], s, false);
-    s = __builtin_amdgcn_sdot4((int)((c.y >> 4) & 0x0F0F0F0Fu), xq[5], s, false);
-    s = __builtin_amdgcn_sdot4((int)((c.z >> 4) & 0x0F0F0F0Fu), xq[6], s, false);
-    s = __builtin_amdgcn_sdot4((int)((c.w >> 4) & 0x0F0F0F0Fu), xq[7], s, false);
-    return s;
+    u = __builtin_amdgcn_sdot4((int)((c.w >> 4) & 0x0F0F0F0Fu), xq[7], u, false);
+    return s + u;
 }
 
 // Cut 32 floats to int8 (imi/core/vec.h:47-75): d = amax / 127, id = d ? 1/d : 0, q = round(x * id), returning d
@@ -86,7 +88,10 @@ __constant__ static const uint64_t kExp2Tab[32] = {
     0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
     0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
-__device__ __forceinline__ float expf_glibc(float x) {
+// tab: the 32-entry table (kExp2Tab, or a copy of it in LDS, which a kernel fills once so that the lookup is not a
+// memory round trip)
+template <class TabPtr>
+__device__ __forceinline__ float expf_glibc_t(float x, TabPtr tab) {
     const uint32_t ux = __float_as_uint(x);
     const uint32_t abstop = (ux >> 20) & 0x7ffu;
     if (abstop >= 0x42bu) {                         // |x| >= 88 or nan
@@ -102,7 +107,7 @@ __device__ __forceinline__ float expf_glibc(float x) {
     const uint64_t ki = (uint64_t)__double_as_longlong(kd);
     kd -= shift;
     const double r = __builtin_fma(inv_ln2_32, xd, -kd);
-    const uint64_t t = kExp2Tab[ki & 31] + (ki << 47);
+    const uint64_t t = tab[ki & 31] + (ki << 47);
     const double sc = __longlong_as_double((long long)t);
     const double z = __builtin_fma(c0, r, c1);
     const double r2 = r * r;
@@ -111,7 +116,11 @@ __device__ __forceinline__ float expf_glibc(float x) {
     return (float)(y * sc);
 }
 
+__device__ __forceinline__ float expf_glibc(float x) { return expf_glibc_t(x, kExp2Tab); }
+
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf_glibc(-x)); }   // imi/core/seoul.cpp:48
+template <class TabPtr>
+__device__ __forceinline__ float silu_t(float x, TabPtr tab) { return x / (1.0f + expf_glibc_t(-x, tab)); }
 
 // imi_rms_scale (imi/core/vec.h:20-33) in its AVX2 op order, by one whole wave over n floats in LDS
 // (n % 32 == 0): partial P (= accumulator P / 8, lane P % 8) is the FMA chain of x[32t + P]^2 over t; then
@@ -154,6 +163,67 @@ __device__ __forceinline__ float rms_scale_wave(Ptr x, int n, float eps) {
     const float q = r + __shfl(r, (lane + 2) & 63);  // lane 0: (r0 + r2), lane 1: (r1 + r3)
     const float s = __shfl(q, 0) + __shfl(q, 1);
     return 1.0f / sqrtf(s / (float)n + eps);
+}
+
+// cross-lane moves on the VALU (DPP), no LDS round trip: lane i gets lane i ^ 1, i ^ 2 (within a quad), 7 - i
+// (within 8 lanes), 15 - i (within 16 lanes)
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+template <int CTRL>
+__device__ __forceinline__ int dppi(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true); }
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_MIRROR8 = 0x141, DPP_MIRROR16 = 0x140;
+
+// imi_rms_scale (imi/core/vec.h:20-33) of n = 128 NQ values held transposed (value i at row i % 32, column i / 32,
+// rows LD floats apart; 16-byte aligned rows), by one wave. imi's order: 32 FMA chains, chain P
+// over the squares of values P, P + 32, P + 64, ...; then v_P = (a_P + a_{P+8}) + (a_{P+16} + a_{P+24}) for P < 8 and
+// ((v0 + v4) + (v2 + v6)) + ((v1 + v5) + (v3 + v7)). Lane L < 32 runs chain P(L) = 8 b0 + 16 b1 + 4 b2 + 2 b3 + b4
+// (b_k = bit k of L), so the tree's levels pair lanes L ^ 1, ^ 2, then 8-lane and 16-lane mirrors, then 0 and 16:
+// each level is one DPP add (fp addition is commutative, so the pair order does not matter, only the tree).
+// Every lane gets 1 / sqrtf(s / n + eps).
+template <class P> struct quad_of;   // float pointer -> f32x4 pointer in the same address space
+template <> struct quad_of<const float*> { typedef const f32x4* type; };
+template <> struct quad_of<const float __attribute__((address_space(3)))*> {
+    typedef const f32x4 __attribute__((address_space(3)))* type;
+};
+
+template <int NQ, int LD, class Ptr>
+__device__ __forceinline__ float rms_scale_xt(Ptr xt, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int row = 8 * (lane & 1) + 16 * ((lane >> 1) & 1) + 4 * ((lane >> 2) & 1) + 2 * ((lane >> 3) & 1) + ((lane >> 4) & 1);
+    const auto r = (typename quad_of<Ptr>::type)(xt + row * LD);
+    constexpr int B = NQ < 8 ? NQ : 8;   // quads per batch; the next batch is read while this one runs
+    float a = 0.0f;
+    f32x4 cur[B], nxt[B];
+#pragma unroll
+    for (int k = 0; k < B; k++) cur[k] = r[k];
+#pragma unroll
+    for (int q = 0; q < NQ; q += B) {
+        if (q + B < NQ) {
+#pragma unroll
+            for (int k = 0; k < B; k++) nxt[k] = r[q + B + k];
+        }
+#pragma unroll
+        for (int k = 0; k < B; k++) {
+            a = fmaf(cur[k].x, cur[k].x, a);
+            a = fmaf(cur[k].y, cur[k].y, a);
+            a = fmaf(cur[k].z, cur[k].z, a);
+            a = fmaf(cur[k].w, cur[k].w, a);
+        }
+        if (q + B < NQ) {
+#pragma unroll
+            for (int k = 0; k < B; k++) cur[k] = nxt[k];
+        }
+    }
+    float x = a;   // lanes 32..63 ran the same chains; only lanes 0..31 are read below
+    x = x + dppf<DPP_XOR1>(x);
+    x = x + dppf<DPP_XOR2>(x);
+    x = x + dppf<DPP_MIRROR8>(x);
+    x = x + dppf<DPP_MIRROR16>(x);
+    const float s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0)) +
+                    __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+    return 1.0f / sqrtf(s / (float)(128 * NQ) + eps);
 }
 
 // dot_h (imi/core/seoul.cpp:29-39): 8 FMA chains over columns i % 8, then the 8-lane horizontal sum

@@ -376,21 +376,43 @@ static size_t gemv_cut_lds(int M, int nb) {
 // workgroup, a chunk of upw units (UG groups of 8 rows each) per workgroup and step of its loop:
 //  - the prologue's input vectors are requested first, then the first chunk's weights;
 //  - prologue: the E-value vectors are read once per workgroup, one wave per conversation runs imi's AVX2-order norm
-//    chains over them in LDS (rms_scale_wave), every thread updates and normalises its 4 values, and the 8 threads of
+//    chains over them in LDS (held transposed, 16-byte reads: rms_scale_xt), every thread updates and normalises its
+//    4 values, and the 8 threads of
 //    each 32-value block cut it to int8 (imi_cut32, imi/core/vec.h:47-75: amax and code sums reduced across lanes);
 //  - dots: thread (row subset, group, block) forms the exact integer dots of its rows, chain operands to LDS;
 //    the next chunk's weights are requested as soon as these registers are free;
 //  - chains: acc on threads 0.., cor on threads 256.. (other SIMDs), imi's per-row order
 //    (imi/core/tables.cpp:127-143); epilogue: rows stored, SwiGLU of (gate, up) groups (imi/core/seoul.cpp:380-394),
 //    the gated short conv of (b, c, x) groups (:407-423) or word scores with the workgroup's first maximum.
+constexpr int XLD = 68;   // row stride of a transposed E <= 2048 vector: value i at (i % 32) * XLD + i / 32
+
+// imi's norm scale of E = 256 .. 2048 values held transposed (rms_scale_xt), by one wave
+__device__ __forceinline__ float rms_xt(const float* xt, int E, float eps) {
+    switch (E) {
+        case 256: return rms_scale_xt<2, XLD>(xt, eps);
+        case 512: return rms_scale_xt<4, XLD>(xt, eps);
+        case 1024: return rms_scale_xt<8, XLD>(xt, eps);
+        default: return rms_scale_xt<16, XLD>(xt, eps);
+    }
+}
+
+// thread t's values 4t .. 4t+3 into the transposed layout: rows 4 (t % 8) + k of column t / 8
+__device__ __forceinline__ void put_xt(float* xt, int t, const f32x4& v) {
+    float* p = xt + (4 * (t & 7)) * XLD + (t >> 3);
+    p[0] = v.x;
+    p[XLD] = v.y;
+    p[2 * XLD] = v.z;
+    p[3 * XLD] = v.w;
+}
+
 template <int M, int EPI, int UG>
 __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
     extern __shared__ __align__(16) float lds[];
     const int E = a.E, nb = a.W.nb, st = ((nb + 3) & ~3) + 4;
     const int upw = a.upw, G = upw * UG, R = 8 * G, C = M * R;
     const int t = threadIdx.x, nq = E / 4;
-    float* l_v = lds;                              // [M][E] the norm input (y, then x)
-    int* l_xq = (int*)(l_v + M * E);               // [M][nb][8] codes of the cut input
+    float* l_v = lds;                              // [M][32][XLD] the norm input (y, then x), transposed
+    int* l_xq = (int*)(l_v + M * 32 * XLD);        // [M][nb][8] codes of the cut input
     float* l_dx = (float*)(l_xq + M * nb * 8);     // [M][nb]
     float* l_s = l_dx + M * nb;                    // [M][st]
     float* l_op = l_s + M * st;                    // [M][R][st] float(isum)
@@ -400,6 +422,7 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
     float* l_out = l_cor + C;                      // [C]
     float* l_sc = l_out + C;                       // [16] norm scales, reduction scratch
     int* l_si = (int*)(l_sc + 16);                 // [16]
+    uint64_t* l_exp = (uint64_t*)(l_si + 16);      // [32] the exponential's table (SwiGLU)
 
     const int gtot = a.W.rows / 8, nchunk = (a.units + upw - 1) / upw;
     // this thread's share of a chunk's weights: rows sub * rpt .. + rpt - 1 of group gi, block jw
@@ -428,15 +451,30 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
         yv[m] = ((const f32x4*)(a.y_in + (size_t)m * E))[tq];
     }
     const f32x4 wp = ((const f32x4*)a.w_post)[tq], wq = ((const f32x4*)a.w_pre)[tq];
+    const uint64_t etab = kExp2Tab[t & 31];   // (SwiGLU) copied to LDS once the dots have waited for the weights
     int k = blockIdx.x;
     load_chunk(k < nchunk ? k : nchunk - 1);
+    // the conv epilogue's taps and memory of this thread's channel (one chunk per workgroup), after the weights
+    constexpr int CMAX = 8;
+    float cw[CMAX + 1], cst[CMAX];
+    if (EPI == EPI_CONV) {
+        const int m = t / R, r = t - m * R, ui = r / 24, i = r - 24 * ui, dc = a.d_conv;
+        const bool mine = t < C && i < 8 && k < nchunk;
+        const int e = mine ? 8 * (k * upw + ui) + i : 0;
+        const float* stt = a.P->conv[mine ? m : 0] + (size_t)a.conv_layer * dc * E;
+#pragma unroll
+        for (int q = 0; q <= CMAX; q++) cw[q] = q <= dc ? a.conv_w[(size_t)q * E + e] : 0.0f;
+#pragma unroll
+        for (int q = 0; q < CMAX; q++) cst[q] = q < dc ? stt[(size_t)q * E + e] : 0.0f;
+    }
+
     {   // x += norm(y) * w_post (imi_norm_mul_add)
         if (t < nq)
 #pragma unroll
-            for (int m = 0; m < M; m++) ((f32x4*)(l_v + m * E))[t] = yv[m];
+            for (int m = 0; m < M; m++) put_xt(l_v + m * 32 * XLD, t, yv[m]);
         __syncthreads();
         if ((t >> 6) < M) {
-            const float sc = rms_scale_wave(l_v + (t >> 6) * E, E, a.eps);
+            const float sc = rms_xt(l_v + (t >> 6) * 32 * XLD, E, a.eps);
             if ((t & 63) == 0) l_sc[t >> 6] = sc;
         }
         __syncthreads();
@@ -453,12 +491,12 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
     if (t < nq)
 #pragma unroll
         for (int m = 0; m < M; m++) {
-            ((f32x4*)(l_v + m * E))[t] = xv[m];
+            put_xt(l_v + m * 32 * XLD, t, xv[m]);
             if (blockIdx.x == 0 && a.x_out) ((f32x4*)(a.x_out + (size_t)m * E))[t] = xv[m];
         }
     __syncthreads();
     if ((t >> 6) < M) {   // h = norm(x) * w_pre (imi_norm_mul)
-        const float sc = rms_scale_wave(l_v + (t >> 6) * E, E, a.eps);
+        const float sc = rms_xt(l_v + (t >> 6) * 32 * XLD, E, a.eps);
         if ((t & 63) == 0) l_sc[4 + (t >> 6)] = sc;
     }
     __syncthreads();
@@ -529,6 +567,7 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
                     }
             }
         }
+        if (EPI == EPI_SWIGLU && t < 32) l_exp[t] = etab;
         __syncthreads();
         if (k + (int)gridDim.x < nchunk) load_chunk(k + gridDim.x);   // in flight during the chains
         // ---- chains ----
@@ -573,7 +612,7 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
                     a.out[(size_t)m * a.out_ld + 8 * g0 + r] = v;
                 } else if (EPI == EPI_SWIGLU) {   // unit = (gate group, up group) of 8 channels
                     const int ui = r >> 4, i = r & 15;
-                    if (i < 8) a.out[(size_t)m * a.out_ld + 8 * (u0 + ui) + i] = silu(v) * l_out[t + 8];
+                    if (i < 8) a.out[(size_t)m * a.out_ld + 8 * (u0 + ui) + i] = silu_t(v, (const uint64_t*)l_exp) * l_out[t + 8];
                 } else if (EPI == EPI_CONV) {     // unit = (b, c, x) groups of 8 channels
                     const int ui = r / 24, i = r - 24 * ui;
                     if (i < 8) {
@@ -581,10 +620,18 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
                         const float cc = l_out[t + 8], xx = l_out[t + 16];
                         float* stt = a.P->conv[m] + (size_t)a.conv_layer * dc * E;
                         const float bx = v * xx;
-                        float uu = v * xx * a.conv_w[(size_t)dc * E + e];
-                        for (int q = 0; q < dc; q++) uu = fmaf(stt[(size_t)q * E + e], a.conv_w[(size_t)q * E + e], uu);
+                        float wdc = cw[0];
+#pragma unroll
+                        for (int q = 1; q <= CMAX; q++)
+                            if (q == dc) wdc = cw[q];
+                        float uu = v * xx * wdc;
+#pragma unroll
+                        for (int q = 0; q < CMAX; q++)
+                            if (q < dc) uu = fmaf(cst[q], cw[q], uu);
                         uu *= cc;
-                        for (int q = 0; q + 1 < dc; q++) stt[(size_t)q * E + e] = stt[(size_t)(q + 1) * E + e];
+#pragma unroll
+                        for (int q = 0; q + 1 < CMAX; q++)
+                            if (q + 1 < dc) stt[(size_t)q * E + e] = cst[q + 1];
                         stt[(size_t)(dc - 1) * E + e] = bx;
                         a.out[(size_t)m * a.out_ld + e] = uu;
                     }
@@ -627,7 +674,8 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
 
 static size_t gemv_norm_lds(int M, int E, int nb, int G) {
     const size_t st = (size_t)(((nb + 3) & ~3) + 4), R = 8 * (size_t)G, C = M * R;
-    return sizeof(float) * ((size_t)M * E + (size_t)M * nb * 8 + (size_t)M * nb + M * st + 2 * M * R * st + R * st + 2 * C + 32);
+    (void)E;
+    return sizeof(float) * ((size_t)M * 32 * XLD + (size_t)M * nb * 8 + (size_t)M * nb + M * st + 2 * M * R * st + R * st + 2 * C + 32 + 64);
 }
 
 // dynamic LDS bytes of a k_gemv instantiation
@@ -983,7 +1031,7 @@ int gemv_logits_grid(int M, int pro, const gemv_args& a, int max_grid) {
 hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
     const int nbl = (a.W.nb + 63) / 64;
     const int ug = epi == EPI_SWIGLU ? 2 : epi == EPI_CONV ? 3 : 1;
-    if (norm_kernel_takes(M, pro, a, ug)) {
+    if (norm_kernel_takes(M, pro, a, ug) && (epi != EPI_CONV || a.d_conv <= 8)) {
         gemv_args b = a;
         // units per chunk: 8 groups for the word scores (looped), else enough that one round of workgroups (one
         // per compute unit: the register use allows one 512-thread workgroup per unit) covers the table

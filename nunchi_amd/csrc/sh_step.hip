@@ -226,59 +226,8 @@ struct xt_dst {
     __device__ __forceinline__ float LDS& operator[](int k) const { return base[(k >> 11) * SK_XT_M + xt_at(k & 2047)]; }
 };
 
-// cross-lane moves on the VALU (DPP), no LDS round trip: lane i gets lane i ^ 1, i ^ 2 (within a quad), 7 - i
-// (within 8 lanes), 15 - i (within 16 lanes)
-template <int CTRL>
-__device__ __forceinline__ float dppf(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
-}
-template <int CTRL>
-__device__ __forceinline__ int dppi(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true); }
-constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_MIRROR8 = 0x141, DPP_MIRROR16 = 0x140;
-
-// imi_rms_scale (imi/core/vec.h:20-33) of n = 128 NQ values held transposed. imi's order: 32 FMA chains, chain P
-// over the squares of values P, P + 32, P + 64, ...; then v_P = (a_P + a_{P+8}) + (a_{P+16} + a_{P+24}) for P < 8 and
-// ((v0 + v4) + (v2 + v6)) + ((v1 + v5) + (v3 + v7)). Lane L < 32 runs chain P(L) = 8 b0 + 16 b1 + 4 b2 + 2 b3 + b4
-// (b_k = bit k of L), so the tree's levels pair lanes L ^ 1, ^ 2, then 8-lane and 16-lane mirrors, then 0 and 16:
-// each level is one DPP add (fp addition is commutative, so the pair order does not matter, only the tree).
-// Every lane gets 1 / sqrtf(s / n + eps).
 template <int NQ>
-__device__ __forceinline__ float rms_scale_T(const float LDS* xt, float eps) {
-    const int lane = threadIdx.x & 63;
-    const int row = 8 * (lane & 1) + 16 * ((lane >> 1) & 1) + 4 * ((lane >> 2) & 1) + 2 * ((lane >> 3) & 1) + ((lane >> 4) & 1);
-    const f32x4 LDS* r = (const f32x4 LDS*)(xt + row * SK_XT_LD);
-    constexpr int B = NQ < 4 ? NQ : 4;   // quads per batch; the next batch is read while this one runs
-    float a = 0.0f;
-    f32x4 cur[B], nxt[B];
-#pragma unroll
-    for (int k = 0; k < B; k++) cur[k] = r[k];
-#pragma unroll
-    for (int q = 0; q < NQ; q += B) {
-        if (q + B < NQ) {
-#pragma unroll
-            for (int k = 0; k < B; k++) nxt[k] = r[q + B + k];
-        }
-#pragma unroll
-        for (int k = 0; k < B; k++) {
-            a = fmaf(cur[k].x, cur[k].x, a);
-            a = fmaf(cur[k].y, cur[k].y, a);
-            a = fmaf(cur[k].z, cur[k].z, a);
-            a = fmaf(cur[k].w, cur[k].w, a);
-        }
-        if (q + B < NQ) {
-#pragma unroll
-            for (int k = 0; k < B; k++) cur[k] = nxt[k];
-        }
-    }
-    float x = a;   // lanes 32..63 ran the same chains; only lanes 0..31 are read below
-    x = x + dppf<DPP_XOR1>(x);
-    x = x + dppf<DPP_XOR2>(x);
-    x = x + dppf<DPP_MIRROR8>(x);
-    x = x + dppf<DPP_MIRROR16>(x);
-    const float s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0)) +
-                    __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
-    return 1.0f / sqrtf(s / (float)(128 * NQ) + eps);
-}
+__device__ __forceinline__ float rms_scale_T(const float LDS* xt, float eps) { return rms_scale_xt<NQ, SK_XT_LD>(xt, eps); }
 
 __device__ __forceinline__ float rms_T(const float LDS* xt, int n, float eps) {
     switch (n) {
