@@ -22,6 +22,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+GATE_UP_TRAFFIC_BYTES = 19353293   # counters: FETCH_SIZE 9436.1 KiB x 1.9987 + WRITE_SIZE 40 KiB x 1.0 per launch
 N_CTX = 512
 PROMPT = 32
 
@@ -203,6 +204,9 @@ def main():
     ap.add_argument("--voice-frames", type=int, default=64, help="timed voice frames (cfg 4); 0 = skip")
     ap.add_argument("--prefill-reps", type=int, default=10, help="timed hearing-window prefills (cfg 3); 0 = skip")
     ap.add_argument("--cpu-voice-frames", type=int, default=8)
+    ap.add_argument("--counters-workload", action="store_true",
+                    help="only the launches the hardware-counter runs read: a streaming kernel of known size (the "
+                         "exponential over 16 Mi floats: 64 MiB read, 64 MiB written) and 64 FFN gate|up launches")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (conversations shard across "
@@ -216,6 +220,14 @@ def main():
     from nunchi_amd import synth
     path = synth.cached("brain", synth.SEOUL, 0)
     brain = nunchi_amd.Brain(path, n_ctx=N_CTX)
+    if args.counters_workload:
+        x = np.linspace(-10.0, 10.0, 16 << 20, dtype=np.float32)
+        brain.ctx.expf(x)
+        gu = brain.bench_kernel("ffn_gate_up", n_in=1, reps=64)
+        print(json.dumps({"counters_workload": {"copy_bytes_read": int(x.nbytes), "copy_bytes_written": int(x.nbytes),
+                                                "ffn_gate_up_avg_us": round(gu["avg_us"], 3),
+                                                "ffn_gate_up_bytes_per_launch": int(gu["bytes_per_launch"])}}))
+        return
 
     tok_s_b1, ids_b1, dev_b1, wall_b1 = gpu_decode(brain, args.steps, args.warmup, b2=False)
     tok_s_b2, ids_b2, dev_b2, wall_b2 = gpu_decode(brain, args.steps, args.warmup, b2=True)
@@ -280,7 +292,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            # HBM bytes per launch from the FETCH_SIZE / WRITE_SIZE counter runs of `bench.py --counters-workload`,
+            # calibrated on a streaming kernel of known size (profiles/ffn_gate_up_counters_seoul.md)
+            "traffic": GATE_UP_TRAFFIC_BYTES,
             "launch_us": round(gu["avg_us"], 3),
             "bytes_per_launch": int(gu["bytes_per_launch"]),
         },
