@@ -773,46 +773,106 @@ __global__ __launch_bounds__(256) void k_attn(attn_args a) {
 }
 
 // ---------------------------------------------------------------- GQA decode attention, one query head per block
-// Block (query head h, conversation m), 256 threads, imi/core/seoul.cpp:433-453 in the CPU's op order. The key rows
-// of the first 256 positions and the first tile of value rows are requested before anything else (they are the
-// cache rows of earlier steps); then q = rope(norm(q) * q_norm) (wave 0) and this position's k = rope(norm(k) *
-// k_norm) and v (wave 1; the first head of each kv group writes them to the fp16 cache, the group's other heads use
-// their own copy, which is the same number); score_t = dot_h(q, K_t) / sqrt(D), thread per position; softmax with the
-// max subtracted, glibc's expf and a double sum in position order; o = sum_t fma(e_t * inv, V_t, o) in order over t
-// by lane i of wave 0, value rows through LDS in tiles; times the sigmoid head gate.
+// Block (query head h, conversation m), 512 threads, imi/core/seoul.cpp:433-453 in the CPU's op order.
+//  - requests first: each thread's first two key rows (cache rows of earlier steps) and, on waves 4-7, the first
+//    value tile;
+//  - q = rope(norm(q) * q_norm) (wave 0); this position's k = rope(norm(k) * k_norm) and v (wave 1; the first head
+//    of each kv group writes them to the fp16 cache, the group's other heads use their own copy, the same number);
+//  - score_t = dot_h(q, K_t) / sqrt(D), thread per position, the next key row requested before the current dot;
+//  - softmax: max, e_t = glibc expf(s_t - max), and the double sum of e_t in position order. When every e_t is a
+//    multiple of 2^(B - 51), B = floor(log2(sum)), every partial sum in any order is exact (a multiple of that unit
+//    below 2^(B + 2) has at most 53 significant bits), so the in-order double sum equals the block's tree sum; else
+//    thread 0 adds in position order;
+//  - a_t = e_t * inv; o = fma(a_t, V_t, o) in order over t by lane i of wave 0 (one chain per dimension). Waves
+//    4-7 stage value tiles of 256 positions into LDS transposed (dimension-major, 16-byte slots XOR-swizzled so that
+//    both the staging writes and the chain's 8-position reads are free of bank conflicts), double-buffered: tile
+//    j + 1 is written and tile j + 2 requested while wave 0 runs tile j;
+//  - times the sigmoid head gate.
+namespace attn_detail {
+constexpr int NT = 512, TV = 256;   // threads, positions per value tile
+__device__ __forceinline__ int vswz(int d) { return (2 * (d >> 3) + 4 * (d & 7) + ((d & 7) >> 2)) & 15; }
+// lowest set bit exponent of a positive float (e = 0 gives a large value)
+__device__ __forceinline__ int low_bit_exp(float e) {
+    const unsigned b = __float_as_uint(e), ex = b >> 23, mt = b & 0x7FFFFFu;
+    if (b == 0) return 1 << 20;
+    return ex == 0 ? -149 + __builtin_ctz(mt) : (int)ex - 150 + __builtin_ctz(mt | 0x800000u);
+}
+}  // namespace attn_detail
+
 template <int D>
-__global__ __launch_bounds__(256) void k_attn_head(attn_args a) {
-    constexpr int TV = 256, half = D / 2, KW = D / 8;   // positions per value tile, 16-byte words per row
+__global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
+    using namespace attn_detail;
+    constexpr int half = D / 2, KW = D / 8;        // 16-byte words per cache row
+    constexpr int NL = (TV / 8) * KW;              // loader threads: one 8-position x 8-dimension block each
     extern __shared__ __align__(16) float lds[];
     const int h = blockIdx.x, m = blockIdx.y, t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int grp = a.n_head / a.n_kv, g = h / grp, hh = h - g * grp;
     const int Hq = a.n_head * D, kvd = a.n_kv * D;
     const int pos = a.P->pos[m];
     const int s0 = a.n_swa > 0 ? max(0, pos - a.n_swa + 1) : 0, nk = pos - s0 + 1;
+    const int ntile = (nk + TV - 1) / TV;
     uint16_t* kc = a.P->kc[m] + ((size_t)a.layer_ai * a.n_kv + g) * a.n_ctx * D;
     uint16_t* vc = a.P->vc[m] + ((size_t)a.layer_ai * a.n_kv + g) * a.n_ctx * D;
     const float* row = a.qkv + (size_t)m * a.ld_qkv;
     float* q_s = lds;                              // [D]
     float* k_s = q_s + D;                          // [D] this position's key as the cache holds it
     float* red = k_s + D;                          // [32]
-    float* stg = red + 32;                         // [2][D] norm staging of waves 0 and 1
-    float* sc = stg + 2 * D;                       // [n_ctx] scores, then e_t
-    u32x4* vt = (u32x4*)(sc + ((a.n_ctx + 3) & ~3));   // [TV][KW] fp16 value rows
+    double* red_d = (double*)(red + 32);           // [8]
+    int* red_i = (int*)(red_d + 8);                // [8]
+    float* stg = (float*)(red_i + 8);              // [2][D] norm staging of waves 0 and 1
+    float* sc = stg + 2 * D;                       // [n_ctx] scores, then e_t, then a_t
+    uint16_t* vT = (uint16_t*)(sc + ((a.n_ctx + 3) & ~3));   // [2][D][TV] fp16 value tiles, dimension-major
     const float2* cs = a.rope_cs + (size_t)pos * half;
+    const int last = max(nk - 2, 0);               // last cache row written by an earlier step
 
-    // ---- requests first: key row of position s0 + t (t < nk - 1), value tile 0 (positions before pos) ----
-    const int kp = s0 + min(t, max(nk - 2, 0));
-    u32x4 kw[KW];
+    // ---- requests first ----
+    u32x4 ka[KW], kb[KW];
+    {
+        const int p0 = min(t, last), p1 = min(t + NT, last);
 #pragma unroll
-    for (int i = 0; i < KW; i++) kw[i] = ((const u32x4*)(kc + (size_t)kp * D))[i];
-    const int nv0 = min(TV, nk - 1) * KW;          // words of tile 0 before pos
-    constexpr int VPT = TV * KW / 256;             // words per thread
-    u32x4 vw[VPT];
+        for (int i = 0; i < KW; i++) ka[i] = ((const u32x4*)(kc + (size_t)(s0 + p0) * D))[i];
 #pragma unroll
-    for (int q = 0; q < VPT; q++) {
-        const int e = min(t + 256 * q, max(nv0 - 1, 0));
-        vw[q] = ((const u32x4*)(vc + (size_t)s0 * D))[e];
+        for (int i = 0; i < KW; i++) kb[i] = ((const u32x4*)(kc + (size_t)(s0 + p1) * D))[i];
     }
+    // value staging: loader lt = t - 256 holds positions 8 * pb .. + 7 of a tile, dimensions 8 * kq .. + 7
+    const int lt = t - 256, kq = lt & (KW - 1), pb = lt / KW;
+    const bool loader = lt >= 0 && lt < NL;
+    u32x4 vw[8];
+    f32x4 vn0, vn1;                                // this position's v, dimensions 8 * kq .. + 7
+    auto load_tile = [&](int j) {
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+            const int p = min(j * TV + 8 * pb + r, last);
+            vw[r] = ((const u32x4*)(vc + (size_t)(s0 + p) * D))[kq];
+        }
+    };
+    auto store_tile = [&](int j) {   // (this position's row replaced by its v)
+        uint16_t* dst = vT + (size_t)(j & 1) * D * TV;
+        const int rl = nk - 1 - (j * TV + 8 * pb);
+        if (rl >= 0 && rl < 8) {
+            const float f[8] = {vn0.x, vn0.y, vn0.z, vn0.w, vn1.x, vn1.y, vn1.z, vn1.w};
+            unsigned wd[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) wd[e] = (unsigned)f2h(f[2 * e]) | ((unsigned)f2h(f[2 * e + 1]) << 16);
+#pragma unroll
+            for (int r = 0; r < 8; r++)
+                if (r == rl) vw[r] = u32x4{wd[0], wd[1], wd[2], wd[3]};
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const unsigned sel = (e & 1) ? 0x07060302u : 0x05040100u;
+            unsigned o4[4];
+#pragma unroll
+            for (int r = 0; r < 8; r += 2) {
+                const unsigned lo = e >> 1 == 0 ? vw[r].x : e >> 1 == 1 ? vw[r].y : e >> 1 == 2 ? vw[r].z : vw[r].w;
+                const unsigned hi = e >> 1 == 0 ? vw[r + 1].x : e >> 1 == 1 ? vw[r + 1].y : e >> 1 == 2 ? vw[r + 1].z : vw[r + 1].w;
+                o4[r >> 1] = __builtin_amdgcn_perm(hi, lo, sel);
+            }
+            const int d = 8 * kq + e;
+            *(u32x4*)(dst + (size_t)d * TV + 8 * (pb ^ vswz(d))) = u32x4{o4[0], o4[1], o4[2], o4[3]};
+        }
+    };
+
     // ---- q (wave 0) and this position's k, v (wave 1): norm + NEOX rope (imi/core/seoul.cpp:19-28) ----
     if (wv < 2) {
         const bool is_k = wv == 1;
@@ -829,98 +889,142 @@ __global__ __launch_bounds__(256) void k_attn_head(attn_args a) {
             const float2 cz = cs[lane < half ? lane : lane - half];
             const float r = lane < half ? fmaf(n, cz.x, -(other * cz.y)) : fmaf(other, cz.y, n * cz.x);
             if (is_k) {
-                const uint16_t kh = f2h(r), vh = f2h(row[Hq + kvd + g * D + lane]);
+                const uint16_t kh = f2h(r);
                 k_s[lane] = h2f(kh);
-                if (nk <= TV) ((uint16_t*)vt)[(nk - 1) * D + lane] = vh;   // tile 0 holds this position
                 if (hh == 0) {
                     kc[(size_t)pos * D + lane] = kh;
-                    vc[(size_t)pos * D + lane] = vh;
+                    vc[(size_t)pos * D + lane] = f2h(row[Hq + kvd + g * D + lane]);
                 }
             } else {
                 q_s[lane] = r;
             }
         }
     }
-#pragma unroll
-    for (int q = 0; q < VPT; q++) {
-        const int e = t + 256 * q;
-        if (e < nv0) vt[e] = vw[q];
-    }
     __syncthreads();
     // ---- scores ----
     const float scale = 1.0f / sqrtf((float)D);
-    for (int p = t; p < nk; p += 256) {
+    for (int p = t; p < nk; p += NT) {
+        u32x4 kn[KW];
+        const int pn = min(p + 2 * NT, last);
+#pragma unroll
+        for (int i = 0; i < KW; i++) kn[i] = ((const u32x4*)(kc + (size_t)(s0 + pn) * D))[i];
         float kf[D];
         if (p == nk - 1) {
 #pragma unroll
             for (int i = 0; i < D; i++) kf[i] = k_s[i];
         } else {
-            if (p != t) {
-#pragma unroll
-                for (int i = 0; i < KW; i++) kw[i] = ((const u32x4*)(kc + (size_t)(s0 + p) * D))[i];
-            }
 #pragma unroll
             for (int i = 0; i < KW; i++) {
-                const unsigned w4[4] = {kw[i].x, kw[i].y, kw[i].z, kw[i].w};
+                const unsigned w4[4] = {ka[i].x, ka[i].y, ka[i].z, ka[i].w};
 #pragma unroll
                 for (int e = 0; e < 8; e++) kf[8 * i + e] = h2f((uint16_t)((w4[e >> 1] >> (16 * (e & 1))) & 0xFFFFu));
             }
         }
         sc[p] = dot_h8<D>(q_s, kf) * scale;
+#pragma unroll
+        for (int i = 0; i < KW; i++) { ka[i] = kb[i]; kb[i] = kn[i]; }
+    }
+    if (loader) {   // tile 0 requested (to LDS once the softmax is done)
+        load_tile(0);
+        vn0 = ((const f32x4*)(row + Hq + kvd + g * D))[2 * kq];
+        vn1 = ((const f32x4*)(row + Hq + kvd + g * D))[2 * kq + 1];
     }
     __syncthreads();
-    // ---- softmax: max, e_t = expf(s_t - max), double sum in position order ----
+    // ---- softmax ----
     float mx = -INFINITY;
-    for (int p = t; p < nk; p += 256) mx = fmaxf(mx, sc[p]);
+    for (int p = t; p < nk; p += NT) mx = fmaxf(mx, sc[p]);
     mx = wave_max(mx);
     if (lane == 0) red[wv] = mx;
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int p = t; p < nk; p += 256) sc[p] = expf_glibc(sc[p] - mx);
+    mx = red[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; w++) mx = fmaxf(mx, red[w]);
+    double part = 0.0;
+    int lowb = 1 << 20;
+    for (int p = t; p < nk; p += NT) {
+        const float e = expf_glibc(sc[p] - mx);
+        sc[p] = e;
+        part += (double)e;
+        lowb = min(lowb, low_bit_exp(e));
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        part += __shfl_xor(part, o);
+        lowb = min(lowb, __shfl_xor(lowb, o));
+    }
+    if (lane == 0) { red_d[wv] = part; red_i[wv] = lowb; }
     __syncthreads();
     if (t == 0) {
-        double sum = 0.0;
-        int p = 0;
-        for (; p + 8 <= nk; p += 8) {
-            float v[8];
+        double tot = 0.0;
+        int lb = 1 << 20;
 #pragma unroll
-            for (int u = 0; u < 8; u++) v[u] = sc[p + u];
+        for (int w = 0; w < NT / 64; w++) { tot += red_d[w]; lb = min(lb, red_i[w]); }
+        int ex;
+        (void)frexp(tot, &ex);   // tot = f * 2^ex, f in [0.5, 1): floor(log2(tot)) = ex - 1
+        if (lb < ex - 1 - 51) {  // some e_t below the exact unit: add in position order
+            double sum = 0.0;
+            int p = 0;
+            for (; p + 8 <= nk; p += 8) {
+                float v[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) sum += (double)v[u];
+                for (int u = 0; u < 8; u++) v[u] = sc[p + u];
+#pragma unroll
+                for (int u = 0; u < 8; u++) sum += (double)v[u];
+            }
+            for (; p < nk; p++) sum += (double)sc[p];
+            tot = sum;
         }
-        for (; p < nk; p++) sum += (double)sc[p];
-        red[8] = (float)(1.0 / sum);
+        red[8] = (float)(1.0 / tot);
     }
     __syncthreads();
-    // ---- o = sum_t fma(e_t * inv, V_t, o), lane i of wave 0, value rows through LDS in tiles of TV ----
-    const float inv = red[8];
+    {
+        const float inv = red[8];
+        for (int p = t; p < nk; p += NT) sc[p] = sc[p] * inv;
+    }
+    if (loader) {   // tile 0 to LDS, tile 1 requested
+        store_tile(0);
+        if (ntile > 1) load_tile(1);
+    }
+    __syncthreads();
+    // ---- o = sum_t fma(a_t, V_t, o), lane i of wave 0; tiles double-buffered through LDS ----
     float o = 0.0f;
-    const uint16_t* vh = (const uint16_t*)vt;
-    for (int q0 = 0; q0 < nk; q0 += TV) {
-        const int nt = min(TV, nk - q0);
-        if (q0 > 0) {   // tile 0 is in LDS already
-            __syncthreads();
-            const int nv = (q0 + nt == nk ? nt - 1 : nt) * KW;   // pos's row comes from this position's v
-            for (int e = t; e < nv; e += 256) vt[e] = ((const u32x4*)(vc + (size_t)(s0 + q0) * D))[e];
-            if (q0 + nt == nk && t < D) ((uint16_t*)vt)[(nt - 1) * D + t] = f2h(row[Hq + kvd + g * D + t]);
-            __syncthreads();
-        }
-        if (t < D) {
+    for (int j = 0; j < ntile; j++) {
+        if (wv == 0 && lane < D) {
+            const int q0 = j * TV, nt = min(TV, nk - q0), fz = vswz(lane);
+            const uint16_t* vr = vT + (size_t)(j & 1) * D * TV + (size_t)lane * TV;
+            const float* ar = sc + q0;
             int p = 0;
             for (; p + 8 <= nt; p += 8) {
-                float e[8], v[8];
+                const u32x4 w = *(const u32x4*)(vr + 8 * ((p >> 3) ^ fz));
+                const f32x4 a0 = *(const f32x4*)(ar + p), a1 = *(const f32x4*)(ar + p + 4);
+                const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+                const unsigned ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-                for (int u = 0; u < 8; u++) { e[u] = sc[q0 + p + u]; v[u] = h2f(vh[(p + u) * D + t]); }
-#pragma unroll
-                for (int u = 0; u < 8; u++) o = fmaf(e[u] * inv, v[u], o);
+                for (int u = 0; u < 8; u++) o = fmaf(av[u], h2f((uint16_t)((ws[u >> 1] >> (16 * (u & 1))) & 0xFFFFu)), o);
             }
-            for (; p < nt; p++) o = fmaf(sc[q0 + p] * inv, h2f(vh[p * D + t]), o);
+            if (p < nt) {
+                const u32x4 w = *(const u32x4*)(vr + 8 * ((p >> 3) ^ fz));
+                const unsigned ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    if (p + u < nt) o = fmaf(ar[p + u], h2f((uint16_t)((ws[u >> 1] >> (16 * (u & 1))) & 0xFFFFu)), o);
+            }
         }
+        if (loader && j + 1 < ntile) {
+            store_tile(j + 1);
+            if (j + 2 < ntile) load_tile(j + 2);
+        }
+        __syncthreads();
     }
-    if (t < D) {
+    if (wv == 0 && lane < D) {
         const float gate = 1.0f / (1.0f + expf_glibc(-row[Hq + 2 * kvd + h]));
-        a.att[(size_t)m * Hq + h * D + t] = o * gate;
+        a.att[(size_t)m * Hq + h * D + lane] = o * gate;
     }
+}
+
+static size_t attn_head_lds(int D, int n_ctx) {
+    return sizeof(float) * (4 * (size_t)D + 32 + 16 + 8 + (((size_t)n_ctx + 3) & ~(size_t)3)) +
+           2 * (size_t)D * attn_detail::TV * sizeof(uint16_t);
 }
 
 // ---------------------------------------------------------------- end of step
@@ -1098,7 +1202,7 @@ hipError_t launch_attn(int M, const attn_args& a, hipStream_t s) {
     const size_t lds = sizeof(float) * ((size_t)grp * a.D + (size_t)grp * a.n_ctx + 5 * (size_t)a.D + (size_t)grp);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     {   // one block per query head
-        const size_t lds2 = sizeof(float) * (4 * (size_t)a.D + 32 + (((size_t)a.n_ctx + 3) & ~(size_t)3)) + (size_t)256 * a.D * 2;
+        const size_t lds2 = attn_head_lds(a.D, a.n_ctx);
         const void* fh = a.D == 64 ? (const void*)k_attn_head<64> : a.D == 32 ? (const void*)k_attn_head<32> : nullptr;
         if (fh && lds2 <= 160 * 1024) {
             if (lds2 > 64 * 1024) {
@@ -1107,7 +1211,7 @@ hipError_t launch_attn(int M, const attn_args& a, hipStream_t s) {
             }
             attn_args b = a;
             void* args[] = {&b};
-            return hipLaunchKernel(fh, dim3(a.n_head, M), dim3(256), args, lds2, s);
+            return hipLaunchKernel(fh, dim3(a.n_head, M), dim3(attn_detail::NT), args, lds2, s);
         }
     }
     const void* fn = a.D == 64 ? (const void*)k_attn<64> : a.D == 32 ? (const void*)k_attn<32> : nullptr;

@@ -34,6 +34,7 @@ class BrainShape:
     conv_kernel: int = 3                          # lfm3.shortconv.l_cache (d_conv = kernel - 1 taps of memory)
     rope_base: float = 1e6
     eps: float = 1e-5
+    qk_norm_scale: float = 1.0                    # > 1 sharpens attention (scores grow with its square)
 
 
 SEOUL = BrainShape()
@@ -121,8 +122,8 @@ def write_brain(path: str, shape: BrainShape = SEOUL, seed: int = 0) -> str:
             q4(p + "attn_v.weight", s.n_head_kv * D, E)
             q4(p + "attn_gate.weight", s.n_head, E)
             q4(p + "attn_output.weight", E, s.n_head * D)
-            f32(p + "attn_q_norm.weight", _norm_w(_rng(seed, p + "q_norm"), D), (D,))
-            f32(p + "attn_k_norm.weight", _norm_w(_rng(seed, p + "k_norm"), D), (D,))
+            f32(p + "attn_q_norm.weight", s.qk_norm_scale * _norm_w(_rng(seed, p + "q_norm"), D), (D,))
+            f32(p + "attn_k_norm.weight", s.qk_norm_scale * _norm_w(_rng(seed, p + "k_norm"), D), (D,))
         else:
             K = s.conv_kernel
             cw = (0.3 * _rng(seed, p + "conv").standard_normal((E, K))).astype(np.float32)   # [channel][tap]

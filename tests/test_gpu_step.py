@@ -151,6 +151,49 @@ def test_greedy_two_conversations(tiny_model, step_path):
     assert np.array_equal(ia, oa) and np.array_equal(ib, obb)
 
 
+def _long_greedy(path, vocab, n_ctx, n_gen, seed):
+    """Prompt, n_gen greedy ids on the device and on the oracle, then one more step compared bit for bit."""
+    import nunchi_amd
+    import oracle
+    g = nunchi_amd.Brain(path, n_ctx=n_ctx)
+    o = oracle.Engine(path, threads=8, n_ctx=n_ctx)
+    prompt = _prompt(8, vocab, seed)
+    for t in prompt[:-1]:
+        g.step(int(t), want_logits=False)
+        o.step(int(t), want_logits=False)
+    hg, lg, bg = g.step(int(prompt[-1]))
+    ho, lo = o.step(int(prompt[-1]))
+    assert same(hg, ho) and same(lg, lo) and bg == oracle.top(lo)
+    ids_g, _ = g.generate(bg, n_gen)
+    ids_o, _ = o.greedy(bg, n_gen)
+    assert np.array_equal(ids_g, ids_o), int(np.argmax(ids_g != ids_o))
+    hg, lg, _ = g.step(int(ids_g[-1]))
+    ho, lo = o.step(int(ids_o[-1]))
+    assert same(hg, ho) and same(lg, lo)
+
+
+def test_long_context_attention(mid_model, step_path):
+    """Head width 64 over 1,200 positions: several value tiles and key rows per thread in the decode attention."""
+    _long_greedy(mid_model, 4096, 1280, 1200, 13)
+
+
+def test_long_context_attention_narrow_heads(tiny_model, step_path):
+    """Head width 32 over 600 positions."""
+    _long_greedy(tiny_model, 1000, 640, 600, 14)
+
+
+@pytest.mark.parametrize("shape", ["tiny", "mid"])
+def test_sharp_attention_in_order_sum(model_dir, shape, step_path):
+    """q/k norm weights scaled by 6: scores spread over hundreds and most e_t = expf(s_t - max) fall far below the
+    double sum's last bit, so the sum has rounding steps and the kernel adds it in position order (its exact-sum
+    shortcut does not apply); the default models take the shortcut."""
+    from nunchi_amd import synth
+    base = synth.TINY if shape == "tiny" else synth.BrainShape(n_layer=4, attn_layers=(1, 3), n_vocab=4096)
+    sharp = synth.BrainShape(**{**base.__dict__, "qk_norm_scale": 6.0})
+    path = synth.cached("brain", sharp, 15, model_dir)
+    _long_greedy(path, sharp.n_vocab, 640, 560, 16)
+
+
 def test_state_semantics(tiny_model):
     """reset / rewind / swap_state / context full (imi/core/seoul.cpp:188-209, 353)."""
     import nunchi_amd
