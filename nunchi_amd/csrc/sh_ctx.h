@@ -20,6 +20,10 @@ hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hi
 // workgroups of a word-score launch (the argmax partials k_final reduces), at most max_grid
 int gemv_logits_grid(int M, int pro, const gemv_args& a, int max_grid);
 hipError_t launch_attn(int M, const attn_args& a, hipStream_t s);
+// word scores over a Q6_K table (a.W6): prologue from x_in/y_in/w_post/w_pre (or src, already normed), logits to
+// a.out when set, per-workgroup first maxima to part_v / part_i [M][grid]
+constexpr int SH_Q6K_GRID = 256;   // k_scores_q6k workgroups: one per compute unit, each looping over tiles
+hipError_t launch_scores_q6k(int M, int grid, const gemv_args& a, hipStream_t s, hipEvent_t t0 = nullptr, hipEvent_t t1 = nullptr);
 hipError_t launch_final(int M, const final_args& a, hipStream_t s);
 hipError_t launch_q4_rows(const q4dev& T, const int32_t* ids, int n, float* out, hipStream_t s);
 hipError_t launch_expf(const float* x, float* y, long long n, hipStream_t s);
@@ -51,6 +55,7 @@ struct layer_dev {
 using sh::arena;
 using sh::layer_dev;
 using sh::q4dev;
+using sh::q6dev;
 using sh::sk_stage;
 using sh::step_params;
 
@@ -77,7 +82,8 @@ struct sh_ctx {
     float eps = 1e-5f, rope_base = 1e6f, rope_base_swa = 1e4f;
     arena w;                         // weights + norms + rope tables
     std::vector<layer_dev> layers;
-    q4dev vocab;
+    q4dev vocab;                     // tied word table when it is Q4_0
+    q6dev vocab6;                    // tied word table when it is Q6_K (imi's own format)
     const float* out_norm = nullptr;
     const float2* rope_cs = nullptr;
     const float2* rope_cs_swa = nullptr;

@@ -35,6 +35,33 @@ __device__ __forceinline__ int wave_isum(int v) {
 // Q4_0 block dot against an int8-cut input block. Codes are the 16 file bytes (byte i = column i in the low nibble,
 // column 16 + i in the high nibble); the input block is 8 dwords of int8 (columns 0..31). Codes 0..15 are valid
 // signed bytes, so the signed 4-way dot applies directly; the -8 offset is folded in by the caller.
+// Q6_K word table in its tiled device layout (codes: 13 16-byte words per unit, word-major within tiles of 64 units;
+// d: fp16 per unit), values 32 j .. 32 j + 31 of a row: block i = j / 8 and 32-value chunk c = j % 8 = 4 h + k of it;
+// value l = (low nibble of ql[64 h + 32 (k & 1) + l] for k < 2, high nibble for k >= 2) | (bits 2k, 2k+1 of
+// qh[32 h + l]) << 4, and y = (d * scale[8 h + 2 k + l / 16]) * (value - 32) (imi/core/tables.cpp:216-233)
+__device__ __forceinline__ void q6k_dequant32(const u32x4* codes, const uint16_t* dv, int nbk, int row, int j, float* v) {
+    const int i = j >> 3, c = j & 7, h = c >> 2, k = c & 3;
+    const size_t u = (size_t)row * nbk + i;
+    const u32x4* base = codes + (u >> 6) * 13 * 64 + (u & 63);
+    const int wl = 4 * h + 2 * (k & 1), wh = 8 + 2 * h;
+    const u32x4 l0 = base[(size_t)wl * 64], l1 = base[(size_t)(wl + 1) * 64];
+    const u32x4 q0 = base[(size_t)wh * 64], q1 = base[(size_t)(wh + 1) * 64];
+    const u32x4 sw = base[12 * 64];
+    const float d = h2f(dv[u]);
+    const unsigned lw[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+    const unsigned hw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    const unsigned scw[4] = {sw.x, sw.y, sw.z, sw.w};
+    const int s0 = 8 * h + 2 * k;
+    const float ds0 = d * (float)(int8_t)((scw[s0 >> 2] >> (8 * (s0 & 3))) & 0xFFu);
+    const float ds1 = d * (float)(int8_t)((scw[(s0 + 1) >> 2] >> (8 * ((s0 + 1) & 3))) & 0xFFu);
+#pragma unroll
+    for (int l = 0; l < 32; l++) {
+        const unsigned lb = (lw[l >> 2] >> (8 * (l & 3))) & 0xFFu, hb = (hw[l >> 2] >> (8 * (l & 3))) & 0xFFu;
+        const int q = (int)(((k < 2 ? lb : lb >> 4) & 15u) | (((hb >> (2 * k)) & 3u) << 4));
+        v[l] = (l < 16 ? ds0 : ds1) * (float)(q - 32);
+    }
+}
+
 __device__ __forceinline__ int q4_block_dot(u32x4 c, const int* xq) {
     // two independent accumulators (low and high nibbles): integer sums, so the split changes nothing but the
     // dependency depth

@@ -54,6 +54,24 @@ bool repack_q4(const std::vector<std::pair<const gg_tensor*, int>>& rows, std::v
     *cols = K;
     return true;
 }
+// Q6_K rows -> the tiled device layout (q6dev): unit u = row * nbk + block; word w (16 bytes: 0-7 ql, 8-11 qh, 12 the
+// scales) of unit u at [(u / 64) * 13 + w][u % 64]; d per unit. Units are padded to whole tiles with zeros.
+void repack_q6k(const gg_tensor* t, std::vector<uint8_t>& codes, std::vector<uint16_t>& d) {
+    const int nbk = (int)t->ne[0] / 256, rows = (int)t->ne[1];
+    const size_t nunit = (size_t)rows * nbk, ntile = (nunit + 63) / 64;
+    codes.assign(ntile * 13 * 64 * 16, 0);
+    d.assign(ntile * 64, 0);
+    for (size_t u = 0; u < nunit; u++) {
+        const uint8_t* blk = static_cast<const uint8_t*>(t->data) + (u / nbk) * t->nb[1] + (u % nbk) * 210;
+        uint8_t* base = &codes[(u / 64) * 13 * 64 * 16 + (u % 64) * 16];
+        for (int w = 0; w < 13; w++) memcpy(base + (size_t)w * 64 * 16, blk + 16 * w, 16);   // ql | qh | scales
+        memcpy(&d[u], blk + 208, 2);
+    }
+}
+size_t q6k_device_bytes(const gg_tensor* t) {
+    const size_t ntile = ((size_t)t->ne[1] * (t->ne[0] / 256) + 63) / 64;
+    return (ntile * 13 * 64 * 16 + 255) / 256 * 256 + (ntile * 64 * 2 + 255) / 256 * 256;
+}
 }  // namespace
 
 namespace sh {
@@ -98,6 +116,7 @@ int enqueue_step(sh_ctx* c, int M, bool want_logits) {
         if (!prev) {
             pro = PRO_EMBED_NORM;
             a.emb = c->vocab;
+            a.emb6 = c->vocab6;
             a.embd = c->embd_stage;
             a.x_out = c->xbuf[cur];
         } else {
@@ -193,13 +212,15 @@ int enqueue_step(sh_ctx* c, int M, bool want_logits) {
         v.w_pre = c->out_norm;
         v.hidden_out = c->hidden;
         v.W = c->vocab;
+        v.W6 = c->vocab6;
         v.units = units_of(c->vocab, 1);
         v.out = c->logits;
         v.out_ld = I.n_vocab;
         v.part_v = c->part_v;
         v.part_i = c->part_i;
-        const int grid = gemv_logits_grid(M, PRO_RESID_NORM, v, c->vocab_grid);
-        HIPCHK(launch_gemv(M, PRO_RESID_NORM, EPI_LOGITS, grid, v, c->stream));
+        const int grid = c->vocab6.codes ? SH_Q6K_GRID : gemv_logits_grid(M, PRO_RESID_NORM, v, c->vocab_grid);
+        if (c->vocab6.codes) HIPCHK(launch_scores_q6k(M, grid, v, c->stream));
+        else HIPCHK(launch_gemv(M, PRO_RESID_NORM, EPI_LOGITS, grid, v, c->stream));
         z.part_v = c->part_v;
         z.part_i = c->part_i;
         z.n_part = grid;
@@ -263,6 +284,7 @@ std::vector<float2> rope_table(int n_ctx, int D, float base, const float* ff) {
 // The persistent kernel's program: the stages of one step in order, each with its own tagged output buffer
 // [2 parity][2 conversations][n_out] (zeroed: tag 0 is never a step's epoch).
 int build_program(sh_ctx* c) {
+    if (c->vocab6.codes) return fail(SH_E_SHAPE, "step kernel: the word table is Q6_K");   // per-table kernels run it
     const sh_model_info& I = c->info;
     const int E = I.n_embd, Hq = I.n_head * I.head_dim;
     int dev_cus = 0;
@@ -489,7 +511,7 @@ int sh_destroy(sh_ctx* c) {
     return SH_OK;
 }
 
-// imi/core/seoul.cpp:93-186 with a Q4_0 tied word table; tables repacked into the device layout
+// imi/core/seoul.cpp:93-186; the tied word table is Q6_K (imi's format) or Q4_0; tables repacked into the device layout
 int sh_load(sh_ctx* c, const char* path, int n_ctx) {
     if (!c || !path || n_ctx < 1) return fail(SH_E_ARG, "sh_load: bad argument");
     if (c->loaded) return fail(SH_E_STATE, "sh_load: a model is already loaded in this context");
@@ -498,10 +520,13 @@ int sh_load(sh_ctx* c, const char* path, int n_ctx) {
     if (!f.load(path)) return fail(SH_E_FILE, "sh_load: " + f.error);
     const gg_tensor* te = f.get("token_embd.weight");
     if (!te) return fail(SH_E_FILE, "sh_load: " + f.error);
-    if (te->type != GT_Q4_0) return fail(SH_E_SHAPE, "sh_load: word table must be Q4_0");
+    if (te->type != GT_Q4_0 && te->type != GT_Q6_K) return fail(SH_E_SHAPE, "sh_load: word table must be Q6_K or Q4_0");
+    const bool q6 = te->type == GT_Q6_K;
     sh_model_info& I = c->info;
     I.n_embd = (int)te->ne[0];
     I.n_vocab = (int)te->ne[1];
+    if (q6 && I.n_embd != 256 && I.n_embd != 512 && I.n_embd != 1024 && I.n_embd != 2048)
+        return fail(SH_E_SHAPE, "sh_load: a Q6_K word table needs n_embd 256, 512, 1024 or 2048");
     c->eps = f.key_f("lfm3.attention.layer_norm_rms_epsilon", 1e-5f);
     c->rope_base = f.key_f("lfm3.rope.freq_base", 1e6f);
     c->rope_base_swa = f.key_f("lfm3.rope.freq_base_swa", 1e4f);
@@ -594,7 +619,7 @@ int sh_load(sh_ctx* c, const char* path, int n_ctx) {
         pd.dst = &L.down;
         tables.push_back(std::move(pd));
     }
-    {
+    if (!q6) {
         plan pv;
         all_rows(pv.rows, te, 0, I.n_vocab);
         pv.dst = &c->vocab;
@@ -619,6 +644,7 @@ int sh_load(sh_ctx* c, const char* path, int n_ctx) {
         const size_t nb = (size_t)t.rows[0].first->ne[0] / 32;
         need += (t.rows.size() * nb * 16 + 255) / 256 * 256 + (t.rows.size() * nb * 2 + 255) / 256 * 256;
     }
+    if (q6) need += q6k_device_bytes(te);
     for (auto& v : vecs) need += ((size_t)v.second->nbytes + 255) / 256 * 256;
     for (auto& v : conv_t) need += (v.size() * 4 + 255) / 256 * 256;
     const size_t rope_bytes = ((size_t)n_ctx * (I.head_dim / 2) * sizeof(float2) + 255) / 256 * 256;
@@ -642,6 +668,20 @@ int sh_load(sh_ctx* c, const char* path, int n_ctx) {
         t.dst->cols = K;
         t.dst->nb = K / 32;
         table_bytes += (long long)(codes.size() + scales.size() * 2);
+    }
+    if (q6) {
+        repack_q6k(te, codes, scales);
+        void* dc = c->w.take(codes.size());
+        void* dd = c->w.take(scales.size() * 2);
+        if (!dc || !dd) return fail(SH_E_NOMEM, "sh_load: arena overflow");
+        HIPCHK(hipMemcpy(dc, codes.data(), codes.size(), hipMemcpyHostToDevice));
+        HIPCHK(hipMemcpy(dd, scales.data(), scales.size() * 2, hipMemcpyHostToDevice));
+        c->vocab6.codes = dc;
+        c->vocab6.d = static_cast<const uint16_t*>(dd);
+        c->vocab6.rows = I.n_vocab;
+        c->vocab6.cols = E;
+        c->vocab6.nbk = E / 256;
+        table_bytes += (long long)I.n_vocab * (E / 256) * 210;
     }
     for (auto& v : vecs) {
         void* d = c->w.take(v.second->nbytes);
@@ -1267,13 +1307,20 @@ int sh_bench_kernel(sh_ctx* c, int kind, int M, int reps, double* avg_us, double
                 a.w_pre = c->out_norm;
                 a.hidden_out = c->hidden;
                 a.W = c->vocab;
+                a.W6 = c->vocab6;
                 a.units = c->vocab.rows / 8;
                 a.out = c->logits;
                 a.out_ld = I.n_vocab;
                 a.part_v = c->part_v;
                 a.part_i = c->part_i;
                 pro = PRO_RESID_NORM; epi = EPI_LOGITS;
-                bytes += (double)c->vocab.rows * c->vocab.nb * 18 + 4.0 * M * (2 * E + I.n_vocab);
+                bytes += c->vocab6.codes ? (double)I.n_vocab * (E / 256) * 210 + 4.0 * M * (2 * E + I.n_vocab)
+                                         : (double)c->vocab.rows * c->vocab.nb * 18 + 4.0 * M * (2 * E + I.n_vocab);
+            }
+            if (kind == 2 && c->vocab6.codes) {
+                HIPCHK(launch_scores_q6k(M, SH_Q6K_GRID, a, c->stream, lt.start(), lt.stop()));
+                lt.next();
+                continue;
             }
             grid = epi == EPI_LOGITS ? gemv_logits_grid(M, pro, a, c->vocab_grid) : (a.units < 4096 ? a.units : 4096);
             HIPCHK(launch_gemv(M, pro, epi, grid, a, c->stream, lt.start(), lt.stop()));

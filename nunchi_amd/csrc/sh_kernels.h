@@ -30,6 +30,16 @@ struct q4dev {
     int rows = 0, cols = 0, nb = 0;
 };
 
+// Q6_K word table (imi/core/tables.cpp:63, 215-287), 210-byte blocks of 256 values, one unit = (row, block).
+// Codes: units in tiles of 64; tile t holds 13 16-byte words per unit, word-major: word w of unit u at
+// [(u / 64) * 13 + w][u % 64] (words 0-7 ql, 8-11 qh, 12 the 16 int8 scales), so a wave reading one word of 64
+// consecutive units reads 1 KB contiguously. d: fp16 per unit. Units past rows * nbk are zero.
+struct q6dev {
+    const void* codes = nullptr;
+    const uint16_t* d = nullptr;
+    int rows = 0, cols = 0, nbk = 0;   // nbk = cols / 256 blocks per row
+};
+
 struct gemv_args {
     q4dev W;
     int units;                 // rows / (8 * groups per unit)
@@ -43,6 +53,7 @@ struct gemv_args {
     const float* w_pre;        // norm weight in front of this table
     const float* embd;         // PRO_EMBED_NORM: input vectors [M][E] used when token < 0
     q4dev emb;                 // word table (input rows)
+    q6dev emb6;                // the word table when it is Q6_K (then emb is empty)
     float* hidden_out;         // if set, block 0 writes the normed input h here ([M][E])
     float eps;
     // epilogue
@@ -54,6 +65,7 @@ struct gemv_args {
     int* part_i;               // and its row
     step_params* P;
     int upw;                   // k_gemv_norm: units per workgroup (chunk), 0 = pick
+    q6dev W6;                  // k_scores_q6k: the Q6_K word table
 };
 
 struct attn_args {

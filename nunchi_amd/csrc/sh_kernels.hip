@@ -93,7 +93,8 @@ __global__ __launch_bounds__(64) void k_gemv(gemv_args a) {
             if (PRO == PRO_EMBED_NORM) {
                 const int tok = a.P->token[m];
                 if (on) {
-                    if (tok >= 0) q4_dequant_block(a.emb, tok, lane, xv);
+                    if (tok >= 0 && a.emb6.codes) q6k_dequant32((const u32x4*)a.emb6.codes, a.emb6.d, a.emb6.nbk, tok, lane, xv);
+                    else if (tok >= 0) q4_dequant_block(a.emb, tok, lane, xv);
                     else load32(a.embd + (size_t)m * E + 32 * lane, xv);
                 }
             } else {
@@ -678,6 +679,228 @@ static size_t gemv_norm_lds(int M, int E, int nb, int G) {
     return sizeof(float) * ((size_t)M * 32 * XLD + (size_t)M * nb * 8 + (size_t)M * nb + M * st + 2 * M * R * st + R * st + 2 * C + 32 + 64);
 }
 
+// ---------------------------------------------------------------- word scores over a Q6_K table
+// imi/core/seoul.cpp:479-487: the hidden state cut per 256 values (imi_q8k::from, imi/core/tables.cpp:200-213) and
+// each row scored by imi_q6k_row (tables.cpp:235-277) in its AVX2 op order. 512 threads.
+//  - prologue (workgroup): h = norm(x + norm(y) * w_post) * w_pre with k_gemv_norm's norm order (block 0 writes x and
+//    h), or h = src when a.src is set; thread t holds values 4t .. 4t+3, so wave b holds 256-value block b: amax by
+//    wave reduction, codes rint(h / d) (half-even, as lrintf), code sums per 16 values over 4 lanes; codes, d and the
+//    sums go to LDS;
+//  - main loop (wave-local): a wave takes tiles of 64 units (64 / nbk rows x nbk blocks), lane = unit, and requests
+//    the next tile's 13 words before the current tile's math. A lane forms its block's eight int32 AVX2 lanes: lane L
+//    takes values 4L .. 4L+3 of each 32-value chunk (h, k) as one sdot4 of 6-bit values (nibble | 2 high bits) and
+//    codes, times the chunk's scale for its register half (8h + 2k + L / 4), minus 32 (sc[2L] bsum[2L] +
+//    sc[2L+1] bsum[2L+1]); exact. Their floats and dd = d * X.d go to LDS; 8 lanes per row then run the chains
+//    acc_L = fma(dd_i, lane_iL, acc_L) over the row's blocks in order and the 256-bit horizontal sum
+//    ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7)) by xor-shuffles 4, 2, 1 (each add commutes);
+//  - the first maximum per input over the workgroup's rows goes to part_v / part_i for k_final.
+namespace q6k_detail {
+constexpr int XS = 68;   // LDS dwords per 256-code block (64 + 4, so the 8 blocks a wave reads sit in distinct banks)
+constexpr int NW = 13;   // 16-byte words per unit
+}  // namespace q6k_detail
+
+template <int M>
+__global__ __launch_bounds__(512) void k_scores_q6k(gemv_args a) {
+    using namespace q6k_detail;
+    extern __shared__ __align__(16) float lds[];
+    constexpr int LNS = 9 * M + 1;                         // floats per unit in the lane buffer (odd stride)
+    const int E = a.E, nbk = E / 256, t = threadIdx.x, lane = t & 63, wv = t >> 6, nq = E / 4;
+    float* l_v = lds;                                      // [M][32][XLD] transposed norm input
+    int* l_xq = (int*)(l_v + M * 32 * XLD);                // [M][nbk][XS] codes, 4 per dword
+    float* l_xd = (float*)(l_xq + M * nbk * XS);           // [M][nbk]
+    int* l_bs = (int*)(l_xd + M * nbk);                    // [M][nbk][16]
+    float* l_sc = (float*)(l_bs + M * nbk * 16);           // [16] norm scales, reduction scratch
+    int* l_si = (int*)(l_sc + 16);                         // [16]
+    float* l_ln = (float*)(l_si + 16) + wv * 64 * LNS;     // this wave's [64][LNS]: lanes of m, then dd of m
+
+    const int rows = a.W6.rows, nunit = rows * nbk, ntile = (nunit + 63) / 64;
+    const u32x4* codes = (const u32x4*)a.W6.codes;
+    int tile = blockIdx.x * 8 + wv;
+    const int tstep = gridDim.x * 8;
+    u32x4 w[NW];
+    auto load_tile = [&](int tl) {   // (a wave past the last tile re-reads the last one)
+        const u32x4* b = codes + (size_t)min(tl, ntile - 1) * NW * 64 + lane;
+#pragma unroll
+        for (int q = 0; q < NW; q++) w[q] = __builtin_nontemporal_load(b + q * 64);
+    };
+    load_tile(tile);
+    float dw = h2f(a.W6.d[(size_t)min(tile, ntile - 1) * 64 + lane]);
+
+    // ---- prologue ----
+    const int tq = t < nq ? t : nq - 1;
+    f32x4 hv[M];
+    if (a.src) {
+#pragma unroll
+        for (int m = 0; m < M; m++) hv[m] = ((const f32x4*)(a.src + (size_t)m * a.src_ld))[tq];
+    } else {
+        f32x4 xv[M], yv[M];
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            xv[m] = ((const f32x4*)(a.x_in + (size_t)m * E))[tq];
+            yv[m] = a.y_in ? ((const f32x4*)(a.y_in + (size_t)m * E))[tq] : f32x4{0, 0, 0, 0};
+        }
+        const f32x4 wq = ((const f32x4*)a.w_pre)[tq];
+        if (a.y_in) {   // x += norm(y) * w_post (imi_norm_mul_add)
+            const f32x4 wp = ((const f32x4*)a.w_post)[tq];
+            if (t < nq)
+#pragma unroll
+                for (int m = 0; m < M; m++) put_xt(l_v + m * 32 * XLD, t, yv[m]);
+            __syncthreads();
+            if ((t >> 6) < M) {
+                const float sc = rms_xt(l_v + (t >> 6) * 32 * XLD, E, a.eps);
+                if ((t & 63) == 0) l_sc[t >> 6] = sc;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                const float sc = l_sc[m];
+                xv[m].x = fmaf(yv[m].x * sc, wp.x, xv[m].x);
+                xv[m].y = fmaf(yv[m].y * sc, wp.y, xv[m].y);
+                xv[m].z = fmaf(yv[m].z * sc, wp.z, xv[m].z);
+                xv[m].w = fmaf(yv[m].w * sc, wp.w, xv[m].w);
+            }
+            __syncthreads();
+        }
+        if (t < nq)
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                put_xt(l_v + m * 32 * XLD, t, xv[m]);
+                if (blockIdx.x == 0 && a.x_out) ((f32x4*)(a.x_out + (size_t)m * E))[t] = xv[m];
+            }
+        __syncthreads();
+        if ((t >> 6) < M) {   // h = norm(x) * w_pre (imi_norm_mul)
+            const float sc = rms_xt(l_v + (t >> 6) * 32 * XLD, E, a.eps);
+            if ((t & 63) == 0) l_sc[4 + (t >> 6)] = sc;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const float sc = l_sc[4 + m];
+            hv[m] = f32x4{xv[m].x * sc * wq.x, xv[m].y * sc * wq.y, xv[m].z * sc * wq.z, xv[m].w * sc * wq.w};
+            if (a.hidden_out && blockIdx.x == 0 && t < nq) ((f32x4*)(a.hidden_out + (size_t)m * E))[t] = hv[m];
+        }
+    }
+    if (t < nq) {   // cut per 256 values: block wv, values 4 lane .. 4 lane + 3
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const float h[4] = {hv[m].x, hv[m].y, hv[m].z, hv[m].w};
+            const float amax = wave_max(fmaxf(fmaxf(fabsf(h[0]), fabsf(h[1])), fmaxf(fabsf(h[2]), fabsf(h[3]))));
+            const float d = amax / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
+            int sum = 0;
+            unsigned packed = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int c = (int)rintf(h[i] * id);
+                sum += c;
+                packed |= ((unsigned)c & 0xFFu) << (8 * i);
+            }
+            sum += __builtin_amdgcn_update_dpp(0, sum, 0xB1, 0xF, 0xF, true);   // lanes xor 1
+            sum += __builtin_amdgcn_update_dpp(0, sum, 0x4E, 0xF, 0xF, true);   // lanes xor 2
+            l_xq[(m * nbk + wv) * XS + lane] = (int)packed;
+            if ((lane & 3) == 0) l_bs[(m * nbk + wv) * 16 + (lane >> 2)] = sum;
+            if (lane == 0) l_xd[m * nbk + wv] = d;
+        }
+    }
+    __syncthreads();
+
+    // ---- main loop ----
+    const int bi = lane % nbk, rpt = 64 / nbk;              // this lane's block within its row; rows per tile
+    float best_v[M];
+    int best_i[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) { best_v[m] = -INFINITY; best_i[m] = 0x7fffffff; }
+    for (; tile < ntile; tile += tstep) {
+        u32x4 c[NW];
+#pragma unroll
+        for (int q = 0; q < NW; q++) c[q] = w[q];
+        const float d = dw;
+        load_tile(tile + tstep);
+        dw = h2f(a.W6.d[(size_t)min(tile + tstep, ntile - 1) * 64 + lane]);
+        unsigned ql[32], qh[16];
+#pragma unroll
+        for (int q = 0; q < 8; q++) { ql[4 * q] = c[q].x; ql[4 * q + 1] = c[q].y; ql[4 * q + 2] = c[q].z; ql[4 * q + 3] = c[q].w; }
+#pragma unroll
+        for (int q = 0; q < 4; q++) { qh[4 * q] = c[8 + q].x; qh[4 * q + 1] = c[8 + q].y; qh[4 * q + 2] = c[8 + q].z; qh[4 * q + 3] = c[8 + q].w; }
+        const unsigned scw[4] = {c[12].x, c[12].y, c[12].z, c[12].w};
+        int sc[16];
+#pragma unroll
+        for (int s = 0; s < 16; s++) sc[s] = (int)(int8_t)((scw[s >> 2] >> (8 * (s & 3))) & 0xFFu);
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const int* xb = l_xq + (m * nbk + bi) * XS;
+            const int* bs = l_bs + (m * nbk + bi) * 16;
+            int isum[8];
+#pragma unroll
+            for (int L = 0; L < 8; L++) isum[L] = -32 * (sc[2 * L] * bs[2 * L] + sc[2 * L + 1] * bs[2 * L + 1]);
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const u32x4 x0 = *(const u32x4*)(xb + 32 * hh + 8 * k), x1 = *(const u32x4*)(xb + 32 * hh + 8 * k + 4);
+                    const unsigned xw[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                    for (int L = 0; L < 8; L++) {
+                        const unsigned lo = ql[16 * hh + 8 * (k & 1) + L], hi = qh[8 * hh + L];
+                        const unsigned q = ((k < 2 ? lo : lo >> 4) & 0x0F0F0F0Fu) | (((hi >> (2 * k)) & 0x03030303u) << 4);
+                        isum[L] += sc[8 * hh + 2 * k + (L >> 2)] * __builtin_amdgcn_sdot4((int)q, (int)xw[L], 0, false);
+                    }
+                }
+            float* ln = l_ln + lane * LNS + 9 * m;
+#pragma unroll
+            for (int L = 0; L < 8; L++) ln[L] = (float)isum[L];
+            ln[8] = d * l_xd[m * nbk + bi];
+        }
+        __builtin_amdgcn_wave_barrier();
+        for (int ci = lane; ci < rpt * 8; ci += 64) {
+            const int r = ci >> 3, L = ci & 7, row = tile * rpt + r;
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                float acc = 0.0f;
+                for (int i = 0; i < nbk; i++) {
+                    const float* ln = l_ln + (r * nbk + i) * LNS + 9 * m;
+                    acc = fmaf(ln[8], ln[L], acc);
+                }
+                acc += __shfl_xor(acc, 4);
+                acc += __shfl_xor(acc, 2);
+                acc += __shfl_xor(acc, 1);
+                if (L == 0 && row < rows) {
+                    if (a.out) a.out[(size_t)m * a.out_ld + row] = acc;
+                    if (acc > best_v[m] || (acc == best_v[m] && row < best_i[m])) { best_v[m] = acc; best_i[m] = row; }
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    // ---- the workgroup's first maximum per input ----
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        float v = best_v[m];
+        int i = best_i[m];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(v, o);
+            const int oi = __shfl_xor(i, o);
+            if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+        }
+        if (lane == 0) { l_sc[8 + wv] = v; l_si[8 + wv] = i; }
+        __syncthreads();
+        if (t == 0) {
+            float bv = l_sc[8];
+            int bj = l_si[8];
+            for (int q = 1; q < 8; q++)
+                if (l_sc[8 + q] > bv || (l_sc[8 + q] == bv && l_si[8 + q] < bj)) { bv = l_sc[8 + q]; bj = l_si[8 + q]; }
+            a.part_v[m * gridDim.x + blockIdx.x] = bv;
+            a.part_i[m * gridDim.x + blockIdx.x] = bj;
+        }
+        __syncthreads();
+    }
+}
+
+static size_t scores_q6k_lds(int M, int E) {
+    const size_t nbk = (size_t)E / 256;
+    return sizeof(float) * ((size_t)M * 32 * XLD + (size_t)M * nbk * (q6k_detail::XS + 1 + 16) + 32 + 8 * 64 * (9 * (size_t)M + 1));
+}
+
 // dynamic LDS bytes of a k_gemv instantiation
 static size_t gemv_lds(int M, int UG, int nb, int E, bool norm) {
     const int R = 8 * UG;
@@ -1123,13 +1346,29 @@ __global__ __launch_bounds__(64) void k_q4_rows(q4dev T, const int32_t* ids, flo
 
 // tables behind the post-norm residual that k_gemv_norm takes (E a multiple of 128 up to 2048, the table's input E)
 static bool norm_kernel_takes(int M, int pro, const gemv_args& a, int ug) {
-    return pro == PRO_RESID_NORM && (M == 1 || M == 2) && a.E % 128 == 0 && a.E <= 2048 && a.W.nb * 32 == a.E &&
+    return pro == PRO_RESID_NORM && (M == 1 || M == 2) && (a.E == 256 || a.E == 512 || a.E == 1024 || a.E == 2048) && a.W.nb * 32 == a.E &&
            a.W.cols == a.E && a.x_in && a.y_in && a.w_post && a.W.rows % (8 * ug) == 0;
 }
 
 int gemv_logits_grid(int M, int pro, const gemv_args& a, int max_grid) {
     if (norm_kernel_takes(M, pro, a, 1)) return 256;   // k_gemv_norm: one workgroup per compute unit, chunks looped
     return a.units < max_grid ? a.units : max_grid;
+}
+
+hipError_t launch_scores_q6k(int M, int grid, const gemv_args& a, hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
+    const bool e_ok = a.E == 256 || a.E == 512 || a.E == 1024 || a.E == 2048;
+    if ((M != 1 && M != 2) || !e_ok || !a.W6.codes || a.W6.cols != a.E || a.W6.nbk * 256 != a.E || grid < 1 || !a.part_v ||
+        !a.part_i || (!a.src && (!a.x_in || !a.w_pre || (a.y_in && !a.w_post))))
+        return hipErrorInvalidValue;
+    const void* fn = M == 2 ? (const void*)k_scores_q6k<2> : (const void*)k_scores_q6k<1>;
+    const size_t lds = scores_q6k_lds(M, a.E);
+    if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    gemv_args b = a;
+    void* args[] = {&b};
+    return hipExtLaunchKernel(fn, dim3(grid), dim3(512), args, lds, s, t0, t1, 0);
 }
 
 hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hipStream_t s, hipEvent_t t0, hipEvent_t t1) {

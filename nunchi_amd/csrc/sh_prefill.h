@@ -30,6 +30,7 @@ struct pf_rows_args {
     const int32_t* tokens;  // PFR_FIRST: [n] device, or null (every row from embd)
     const float* embd;      // PFR_FIRST: [n][E] rows of positions whose token < 0
     q4dev vocab;            // PFR_FIRST: the tied word table (input rows)
+    q6dev vocab6;           // PFR_FIRST: the word table when it is Q6_K (then vocab is empty)
     float* x;               // [n][E] residual stream (written by PFR_FIRST, updated by PFR_RESID)
     const float* y;         // PFR_RESID: [n][E] the table output the post-norm applies to
     const float* w_post;

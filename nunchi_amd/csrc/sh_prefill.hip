@@ -29,7 +29,8 @@ __device__ __forceinline__ void cut_store(const pf_cut& c, int n, int j, int p, 
 }
 
 // ---------------------------------------------------------------- per-position norms
-// PFR_FIRST: x = the word's dequantized row ((code - 8) * d) or the given embedding row (imi/core/seoul.cpp:363-364);
+// PFR_FIRST: x = the word's dequantized row (Q4_0: (code - 8) * d; Q6_K: imi_q6k_dequant_row) or the given embedding
+// row (imi/core/seoul.cpp:363-364);
 // PFR_RESID: x = fma(y * rms(y), w_post, x) (imi/core/vec.h:41-44); then h = x * rms(x) * w_pre, cut or stored
 template <int MODE>
 __global__ __launch_bounds__(256) void k_pf_rows(pf_rows_args a) {
@@ -40,7 +41,9 @@ __global__ __launch_bounds__(256) void k_pf_rows(pf_rows_args a) {
     float* xr = a.x + (size_t)p * E;
     if (MODE == PFR_FIRST) {
         const int tok = a.tokens ? a.tokens[p] : -1;
-        if (tok >= 0) {
+        if (tok >= 0 && a.vocab6.codes) {
+            for (int j = tid; j < nb; j += 256) q6k_dequant32((const u32x4*)a.vocab6.codes, a.vocab6.d, a.vocab6.nbk, tok, j, xs + 32 * j);
+        } else if (tok >= 0) {
             for (int j = tid; j < nb; j += 256) {
                 const u32x4 c = reinterpret_cast<const u32x4*>(a.vocab.codes)[(size_t)tok * nb + j];
                 const float d = h2f(reinterpret_cast<const uint16_t*>(a.vocab.scales)[((size_t)(tok >> 3) * nb + j) * 8 + (tok & 7)]);

@@ -59,6 +59,7 @@ int enqueue_chunk(sh_ctx* c, sh_state* st, int m, bool have_tokens, bool have_em
     r.tokens = have_tokens ? c->pf_tok : nullptr;
     r.embd = have_embd ? c->pf_emb : nullptr;
     r.vocab = c->vocab;
+    r.vocab6 = c->vocab6;
     r.x = c->pf_x;
     r.w_pre = c->layers[0].attn_norm;
     r.cut = cut;
@@ -182,8 +183,10 @@ int run_prefill(sh_ctx* c, sh_state* st, const int32_t* tokens, const float* emb
         v.E = E;
         v.eps = c->eps;
         v.P = c->P_dev;
-        const int grid = v.units < c->vocab_grid ? v.units : c->vocab_grid;
-        PCHK(launch_gemv(1, PRO_CUT, EPI_LOGITS, grid, v, c->stream));
+        v.W6 = c->vocab6;
+        const int grid = c->vocab6.codes ? SH_Q6K_GRID : v.units < c->vocab_grid ? v.units : c->vocab_grid;
+        if (c->vocab6.codes) PCHK(launch_scores_q6k(1, grid, v, c->stream));   // src: the last hidden row, normed
+        else PCHK(launch_gemv(1, PRO_CUT, EPI_LOGITS, grid, v, c->stream));
         final_args z{};
         z.E = E;
         z.eps = c->eps;

@@ -12,7 +12,7 @@ from dataclasses import dataclass, field
 import numpy as np
 
 GGUF_MAGIC = 0x46554747  # "GGUF" little-endian
-T_F32, T_F16, T_Q4_0, T_Q8_0 = 0, 1, 2, 8
+T_F32, T_F16, T_Q4_0, T_Q8_0, T_Q6_K = 0, 1, 2, 8, 14
 
 # value types of GGUF key/value pairs
 V_U8, V_I8, V_U16, V_I16, V_U32, V_I32, V_F32, V_BOOL, V_STR, V_ARR, V_U64, V_I64, V_F64 = range(13)
@@ -21,6 +21,8 @@ _SCALAR = {V_U8: "<B", V_I8: "<b", V_U16: "<H", V_I16: "<h", V_U32: "<I", V_I32:
 
 Q4_0_BLOCK = np.dtype([("d", "<f2"), ("qs", "u1", 16)])   # 18 bytes per 32 weights
 Q8_0_BLOCK = np.dtype([("d", "<f2"), ("qs", "i1", 32)])   # 34 bytes per 32 weights
+# 210 bytes per 256 weights: low 4 bits, high 2 bits, 16 int8 scales (one per 16 values), fp16 d
+Q6_K_BLOCK = np.dtype([("ql", "u1", 128), ("qh", "u1", 64), ("scales", "i1", 16), ("d", "<f2")])
 
 
 def row_bytes(gtype: int, ne0: int) -> int:
@@ -32,6 +34,8 @@ def row_bytes(gtype: int, ne0: int) -> int:
         return ne0 // 32 * 18
     if gtype == T_Q8_0:
         return ne0 // 32 * 34
+    if gtype == T_Q6_K:
+        return ne0 // 256 * 210
     raise ValueError(f"unsupported ggml type {gtype}")
 
 

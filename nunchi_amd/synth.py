@@ -18,7 +18,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from .gguf import GGUFWriter, Q4_0_BLOCK, Q8_0_BLOCK, T_F32, T_Q4_0, T_Q8_0
+from .gguf import GGUFWriter, Q4_0_BLOCK, Q6_K_BLOCK, Q8_0_BLOCK, T_F32, T_Q4_0, T_Q6_K, T_Q8_0
 
 
 @dataclass
@@ -35,6 +35,7 @@ class BrainShape:
     rope_base: float = 1e6
     eps: float = 1e-5
     qk_norm_scale: float = 1.0                    # > 1 sharpens attention (scores grow with its square)
+    vocab_type: str = "q4_0"                      # tied word table: "q4_0", or "q6_k" (imi's own format)
 
 
 SEOUL = BrainShape()
@@ -77,6 +78,18 @@ def q4_0_random(rng: np.random.Generator, rows: int, cols: int) -> np.ndarray:
     return blk
 
 
+def q6_k_random(rng: np.random.Generator, rows: int, cols: int) -> np.ndarray:
+    """[rows][cols/256] Q6_K blocks: random ql/qh bytes (uniform 6-bit values 0..63), int8 scales uniform in
+    [-64, 63], d = fp16(|N(0, 0.02)| / 1024), so values d * scale * (q - 32) are of the Q4_0 tables' size."""
+    nb = rows * (cols // 256)
+    blk = np.empty(nb, dtype=Q6_K_BLOCK)
+    blk["ql"] = np.frombuffer(rng.bytes(nb * 128), dtype=np.uint8).reshape(nb, 128)
+    blk["qh"] = np.frombuffer(rng.bytes(nb * 64), dtype=np.uint8).reshape(nb, 64)
+    blk["scales"] = rng.integers(-64, 64, size=(nb, 16), dtype=np.int8)
+    blk["d"] = (np.abs(rng.standard_normal(nb, dtype=np.float32) * np.float32(0.02)) / np.float32(1024)).astype(np.float16)
+    return blk
+
+
 def q8_0_random(rng: np.random.Generator, rows: int, cols: int) -> np.ndarray:
     nb = rows * (cols // 32)
     blk = np.empty(nb, dtype=Q8_0_BLOCK)
@@ -110,7 +123,10 @@ def write_brain(path: str, shape: BrainShape = SEOUL, seed: int = 0) -> str:
     def f32(name, arr, ne):
         w.add_tensor(name, T_F32, ne, np.ascontiguousarray(arr, dtype=np.float32))
 
-    q4("token_embd.weight", s.n_vocab, E)
+    if s.vocab_type == "q6_k":
+        w.add_tensor("token_embd.weight", T_Q6_K, (E, s.n_vocab), q6_k_random(_rng(seed, "token_embd.weight"), s.n_vocab, E))
+    else:
+        q4("token_embd.weight", s.n_vocab, E)
     f32("output_norm.weight", _norm_w(_rng(seed, "output_norm.weight"), E), (E,))
     for il in range(s.n_layer):
         p = f"blk.{il}."

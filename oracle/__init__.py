@@ -55,6 +55,9 @@ def lib():
         "orc_engine_cache": (None, [vp, i, _u16p, _u16p]),
         "orc_engine_conv_state": (None, [vp, i, _f32p]),
         "orc_h2f": (f, [C.c_uint16]),
+        "orc_q8k_from": (None, [_f32p, i, _i8p, _f32p, C.POINTER(C.c_int16)]),
+        "orc_q6k_dequant_row": (None, [_u8p, i, _f32p]),
+        "orc_q6k_rows": (None, [_u8p, i, i, _f32p, _f32p, vp]),
         "orc_f2h": (C.c_uint16, [f]),
         "orc_cut32": (f, [_f32p, _i8p, C.POINTER(C.c_int)]),
         "orc_cut": (None, [_f32p, i, _i8p, _f32p, _f32p]),
@@ -295,6 +298,36 @@ def cut(x: np.ndarray):
     s = np.zeros(x.size // 32, np.float32)
     lib().orc_cut(x, x.size, q, d, s)
     return q, d, s
+
+
+def q8k(x: np.ndarray):
+    """imi_q8k::from (imi/core/tables.cpp:200-213): codes, d per 256, code sums per 16."""
+    x = np.ascontiguousarray(x, np.float32)
+    q = np.zeros(x.size, np.int8)
+    d = np.zeros(x.size // 256, np.float32)
+    bs = np.zeros(x.size // 16, np.int16)
+    lib().orc_q8k_from(x, x.size, q, d, bs.ctypes.data_as(C.POINTER(C.c_int16)))
+    return q, d, bs
+
+
+def q6k_dequant(row: np.ndarray, n_embd: int) -> np.ndarray:
+    """imi_q6k_dequant_row of one row of n_embd / 256 blocks (bytes)."""
+    row = np.ascontiguousarray(row, np.uint8)
+    y = np.zeros(n_embd, np.float32)
+    lib().orc_q6k_dequant_row(row, n_embd // 256, y)
+    return y
+
+
+def q6k_rows(rows: np.ndarray, x: np.ndarray, lanes: bool = False):
+    """imi_q6k_row for every row of a [n_rows][nblocks * 210] byte table against x cut by q8k; with lanes, also the
+    [n_rows][nblocks][8] int32 lane sums."""
+    rows = np.ascontiguousarray(rows, np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    n_rows, nb = rows.shape[0], x.size // 256
+    out = np.zeros(n_rows, np.float32)
+    ln = np.zeros((n_rows, nb, 8), np.int32) if lanes else None
+    lib().orc_q6k_rows(rows, n_rows, nb, x, out, _ptr(ln))
+    return (out, ln) if lanes else out
 
 
 def expf(x: np.ndarray) -> np.ndarray:

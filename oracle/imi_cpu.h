@@ -99,6 +99,19 @@ bool q8g_build(q8gtab& t, const std::vector<const uint8_t*>& rows, int cols);
 void q8g_group(const q8gtab& W, const float* xt, int C, int g, float* out);     // xt [cols][C] -> out [C][8]
 void q8_0_dequant_row(const uint8_t* row, float* y, int cols);
 
+// ---- Q6_K word table (imi/core/tables.cpp:200-287): 210-byte blocks of 256 values {ql[128], qh[64], scales[16], d} ----
+struct q8kin {                                             // imi_q8k: the hidden state cut to int8 per 256 values
+    int n = 0;
+    std::vector<int8_t> q;
+    std::vector<float> d;                                  // per 256: amax / 127
+    std::vector<int16_t> bsums;                            // per 16 values: sum of their codes
+    void from(const float* x, int n);                      // tables.cpp:200-213
+};
+int   q6k_at(const uint8_t* blk, int e);                   // value e (0..255) of a block, 0..63 (tables.cpp:215-233)
+void  q6k_dequant_row(const uint8_t* row, float* y, int nblocks);                    // tables.cpp:216-233
+void  q6k_lane_sums(const uint8_t* blk, const q8kin& X, int i, int32_t out[8]);      // block i's 8 int32 AVX2 lanes
+float q6k_row(const uint8_t* row, const q8kin& X, int nblocks);                      // tables.cpp:235-277
+
 // ---- small vector math (imi/core/vec.h:20-44) ----
 float rms_scale(const float* x, int n, float eps);
 void  norm_mul(const float* x, const float* w, float* o, int n, float eps);

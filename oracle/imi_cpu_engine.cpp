@@ -200,6 +200,7 @@ struct engine {
     gfile f;
     std::vector<layer> layers;
     q4tab vocab;                     // tied Q4_0 word table in the 8-row layout (word scores)
+    bool vocab_q6k = false;          // the word table is Q6_K (imi's own format): read as stored, rows of 210-byte blocks
     const gtensor* tok = nullptr;    // tied word table as stored (input rows)
     const float *out_norm = nullptr, *rope_freqs = nullptr;
     int n_embd = 0, n_vocab = 0, n_head = 0, n_head_kv = 0, head_dim = 0, n_ff = 0, d_conv = 0, n_swa = 0, n_ctx = 0;
@@ -207,7 +208,7 @@ struct engine {
     state own;
     team tm;
     int n_threads = 1;
-    struct per_thread { std::vector<float> x, h, t, u, x2; q8in qi, qi2; };
+    struct per_thread { std::vector<float> x, h, t, u, x2; q8in qi, qi2; q8kin qk; };
     std::vector<per_thread> per;
     std::vector<float> bcx, qkv, att, y, act, fo, bcx2, qkv2, att2, y2, act2, fo2;
     std::unique_ptr<std::atomic<int>[]> ctr;
@@ -218,6 +219,7 @@ struct engine {
 
     bool load(const std::string& path, int threads, int ctx_len);
     void embed(int32_t token, const float* embd, float* x) const;
+    void word_scores(per_thread& T, const float* hid, float* lg, std::atomic<int>& k);
     void reset_counters() { for (int i = 0; i < n_ctr; i++) ctr[i].store(0, std::memory_order_relaxed); }
     void step(int32_t token, const float* embd, bool want_logits);
     void step2(int32_t ta, const float* ea, bool la, state& b, int32_t tb, const float* eb, bool lb);
@@ -231,11 +233,14 @@ struct engine {
 
 static const float* f32(const gtensor* t) { return t ? (const float*)t->data : nullptr; }
 
-// imi/core/seoul.cpp:93-186, with the word table taken as Q4_0 (its rows repacked like any layer table)
+// imi/core/seoul.cpp:93-186. The word table is Q6_K as imi requires (seoul.cpp:96), or Q4_0 (its rows repacked like
+// any layer table and scored with the layer tables' kernel)
 bool engine::load(const std::string& path, int threads, int ctx_len) {
     if (!f.open(path)) return false;
     tok = f.get("token_embd.weight");
-    if (!tok || tok->type != T_Q4_0) { fprintf(stderr, "oracle: word table must be Q4_0\n"); return false; }
+    if (!tok || (tok->type != T_Q4_0 && tok->type != T_Q6_K)) { fprintf(stderr, "oracle: word table must be Q6_K or Q4_0\n"); return false; }
+    vocab_q6k = tok->type == T_Q6_K;
+    if (vocab_q6k && tok->ne[0] % 256) { fprintf(stderr, "oracle: Q6_K word table needs n_embd %% 256 == 0\n"); return false; }
     n_embd = (int)tok->ne[0]; n_vocab = (int)tok->ne[1];
     out_norm = f32(f.get("output_norm.weight"));
     rope_freqs = f32(f.get("rope_freqs.weight"));
@@ -301,7 +306,7 @@ bool engine::load(const std::string& path, int threads, int ctx_len) {
         ok &= whole(L.down, {need(p + "ffn_down.weight")});
         if (!ok) { fprintf(stderr, "oracle: layer %d has a table the kernels do not read\n", il); return false; }
     }
-    if (!whole(vocab, {tok})) return false;
+    if (!vocab_q6k && !whole(vocab, {tok})) return false;
     n_ctx = ctx_len;
     const int kvd = n_head_kv * head_dim;
     own.k_cache.assign(n_attn, std::vector<uint16_t>((size_t)n_ctx * kvd));
@@ -325,9 +330,12 @@ bool engine::load(const std::string& path, int threads, int ctx_len) {
     return true;
 }
 
-// input row: Q4_0 word -> (code - 8) * d (ggml's dequantize_row_q4_0 semantics), or a given vector
+// input row: Q6_K word -> imi_q6k_dequant_row (seoul.cpp:363); Q4_0 word -> (code - 8) * d (ggml's
+// dequantize_row_q4_0 semantics); or a given vector
 void engine::embed(int32_t token, const float* embd, float* x) const {
-    if (token >= 0) {
+    if (token >= 0 && vocab_q6k) {
+        q6k_dequant_row(tok->data + (size_t)token * tok->row_bytes, x, n_embd / 256);
+    } else if (token >= 0) {
         const uint8_t* row = tok->data + (size_t)token * tok->row_bytes;
         for (int j = 0; j < n_embd / 32; j++) {
             uint16_t dh; memcpy(&dh, row + 18 * j, 2);
@@ -341,6 +349,22 @@ void engine::embed(int32_t token, const float* embd, float* x) const {
     } else {
         memcpy(x, embd, (size_t)n_embd * sizeof(float));
     }
+}
+
+// word scores of one hidden state, rows taken from the shared counter k: Q6_K rows against the hidden state cut per
+// 256 (seoul.cpp:479-487, chunks of 64 rows), or Q4_0 groups against it cut per 32
+void engine::word_scores(per_thread& T, const float* hid, float* lg, std::atomic<int>& k) {
+    if (vocab_q6k) {
+        T.qk.from(hid, n_embd);
+        const int nb = n_embd / 256, chunk = 64;
+        for (int r = k.fetch_add(chunk, std::memory_order_relaxed); r < n_vocab; r = k.fetch_add(chunk, std::memory_order_relaxed))
+            for (int i = r; i < std::min(n_vocab, r + chunk); i++) lg[i] = q6k_row(tok->data + (size_t)i * tok->row_bytes, T.qk, nb);
+        return;
+    }
+    T.qi.from(hid, n_embd);
+    const int ng = vocab.rows / 8;
+    for (int g = k.fetch_add(4, std::memory_order_relaxed); g < ng; g = k.fetch_add(4, std::memory_order_relaxed))
+        for (int gg = g; gg < std::min(ng, g + 4); gg++) q4_group(vocab, T.qi, gg, lg + 8 * gg);
 }
 
 state engine::new_state() const {   // imi/core/seoul.cpp:193-201
@@ -461,10 +485,7 @@ void engine::run(int tid, int32_t token, const float* embd, bool want_logits) {
     float* hid = T.h.data();
     norm_mul(x, out_norm, hid, E, eps);
     if (tid == 0) memcpy(own.hidden.data(), hid, (size_t)E * sizeof(float));
-    if (want_logits) {   // word scores: the hidden state cut to int8 per 32, times the Q4_0 word table
-        T.qi.from(hid, E);
-        table(vocab, own.logits.data());
-    }
+    if (want_logits) word_scores(T, hid, own.logits.data(), ctr[c++]);
 }
 
 void engine::step2(int32_t ta, const float* ea, bool la, state& b, int32_t tb, const float* eb, bool lb) {   // seoul.cpp:208-220
@@ -559,14 +580,7 @@ void engine::run2(int tid, state& B, const int32_t tk[2], const float* const em[
         float* hid = T.h.data();
         norm_mul(x[s], out_norm, hid, E, eps);
         if (tid == 0) memcpy(ss[s]->hidden.data(), hid, (size_t)E * sizeof(float));
-        if (want[s]) {
-            qi[s]->from(hid, E);
-            std::atomic<int>& k = ctr[c++];
-            const int ng = vocab.rows / 8;
-            float* lg = ss[s]->logits.data();
-            for (int g = k.fetch_add(4, std::memory_order_relaxed); g < ng; g = k.fetch_add(4, std::memory_order_relaxed))
-                for (int gg = g; gg < std::min(ng, g + 4); gg++) q4_group(vocab, *qi[s], gg, lg + 8 * gg);
-        }
+        if (want[s]) word_scores(T, hid, ss[s]->logits.data(), ctr[c++]);
     }
 }
 
@@ -588,13 +602,7 @@ void engine::step_batch(const int32_t* tokens, const float* embd, int n, bool wa
     }
     if (want_logits) {
         reset_counters();
-        tm.run([&](int tid) {
-            per_thread& T = per[tid];
-            T.qi.from(own.hidden.data(), n_embd);
-            const int ng = vocab.rows / 8;
-            for (int g = ctr[0].fetch_add(4); g < ng; g = ctr[0].fetch_add(4))
-                for (int gg = g; gg < std::min(ng, g + 4); gg++) q4_group(vocab, T.qi, gg, own.logits.data() + 8 * gg);
-        });
+        tm.run([&](int tid) { word_scores(per[tid], own.hidden.data(), own.logits.data(), ctr[0]); });
     }
 }
 
@@ -1026,6 +1034,25 @@ void orc_engine_conv_state(void* h, int il, float* out) {
 
 // ---- kernel-level entry points ----
 float orc_h2f(uint16_t h) { return h2f(h); }
+// Q6_K word table pieces: x [n] -> codes, d [n/256], bsums [n/16]; rows of nblocks 210-byte blocks
+void orc_q8k_from(const float* x, int n, int8_t* q, float* d, int16_t* bsums) {
+    q8kin X;
+    X.from(x, n);
+    memcpy(q, X.q.data(), (size_t)n);
+    memcpy(d, X.d.data(), sizeof(float) * (size_t)(n / 256));
+    memcpy(bsums, X.bsums.data(), sizeof(int16_t) * (size_t)(n / 16));
+}
+void orc_q6k_dequant_row(const uint8_t* row, int nblocks, float* y) { q6k_dequant_row(row, y, nblocks); }
+void orc_q6k_rows(const uint8_t* rows, int n_rows, int nblocks, const float* x, float* out, int32_t* lanes) {
+    q8kin X;
+    X.from(x, 256 * nblocks);
+    for (int r = 0; r < n_rows; r++) {
+        const uint8_t* row = rows + (size_t)r * 210 * nblocks;
+        out[r] = q6k_row(row, X, nblocks);
+        if (lanes)
+            for (int i = 0; i < nblocks; i++) q6k_lane_sums(row + 210 * (size_t)i, X, i, lanes + ((size_t)r * nblocks + i) * 8);
+    }
+}
 uint16_t orc_f2h(float f) { return f2h(f); }
 float orc_cut32(const float* x, int8_t* q, int* sum) { return cut32(x, q, sum); }
 void orc_cut(const float* x, int n, int8_t* q, float* d, float* s) {

@@ -296,6 +296,81 @@ void q8_0_dequant_row(const uint8_t* row, float* y, int cols) {   // tables.cpp:
         for (int i = 0; i < 32; i++) y[32 * j + i] = d * (float)qs[i];
     }
 }
+// ---- Q6_K word table ----
+// imi/core/tables.cpp:200-213: per 256 values amax, d = amax / 127, codes lrintf(v / d) (half-even), and the code sum
+// of every 16 values as int16
+void q8kin::from(const float* x, int nn) {
+    n = nn;
+    const int nbk = n / 256;
+    q.resize(n); d.resize(nbk); bsums.resize((size_t)nbk * 16);
+    for (int j = 0; j < nbk; j++) {
+        const float* v = x + 256 * j;
+        float amax = 0.0f;
+        for (int i = 0; i < 256; i++) amax = std::max(amax, fabsf(v[i]));
+        d[j] = amax / 127.0f;
+        const float id = d[j] != 0.0f ? 1.0f / d[j] : 0.0f;
+        int8_t* c = &q[256 * j];
+        for (int s = 0; s < 16; s++) {
+            int t = 0;
+            for (int i = 16 * s; i < 16 * s + 16; i++) t += (c[i] = (int8_t)lrintf(v[i] * id));
+            bsums[16 * j + s] = (int16_t)t;
+        }
+    }
+}
+// value e of a Q6_K block: e = 128 h + 32 k + l; low 4 bits from ql[64 h + 32 (k & 1) + l] (low nibble for k < 2,
+// high nibble for k >= 2), high 2 bits from bits 2k, 2k+1 of qh[32 h + l] (imi/core/tables.cpp:219-230)
+int q6k_at(const uint8_t* blk, int e) {
+    const int h = e >> 7, k = (e >> 5) & 3, l = e & 31;
+    const uint8_t lo = blk[64 * h + 32 * (k & 1) + l], hi = blk[128 + 32 * h + l];
+    return ((k < 2 ? lo : lo >> 4) & 15) | (((hi >> (2 * k)) & 3) << 4);
+}
+static float blk_d(const uint8_t* blk) { uint16_t dh; memcpy(&dh, blk + 208, 2); return h2f(dh); }
+// y = d * scale[e / 16] * (value - 32), the two products in that order (imi/core/tables.cpp:216-233)
+void q6k_dequant_row(const uint8_t* row, float* y, int nblocks) {
+    for (int i = 0; i < nblocks; i++) {
+        const uint8_t* b = row + 210 * (size_t)i;
+        const float d = blk_d(b);
+        const int8_t* sc = (const int8_t*)(b + 192);
+        for (int e = 0; e < 256; e++) y[256 * i + e] = d * (float)sc[e >> 4] * (float)(q6k_at(b, e) - 32);
+    }
+}
+// imi/core/tables.cpp:246-270, lane by lane. Per 128-value half h and 32-value chunk k, maddubs pairs bytes and madd
+// pairs those, so int32 lane l takes values 4l .. 4l+3 of the chunk, weighted by the chunk's scale for its half of
+// the register (lanes 0-3: scale 8h + 2k, lanes 4-7: 8h + 2k + 1); corr lane l = sc[2l] bsums[2l] + sc[2l+1]
+// bsums[2l+1], and each lane ends as sum - 32 corr. Integer, exact.
+void q6k_lane_sums(const uint8_t* blk, const q8kin& X, int i, int32_t out[8]) {
+    const int8_t* sc = (const int8_t*)(blk + 192);
+    const int8_t* xq = &X.q[256 * (size_t)i];
+    const int16_t* bs = &X.bsums[16 * (size_t)i];
+    for (int l = 0; l < 8; l++) {
+        int32_t s = 0;
+        for (int h = 0; h < 2; h++)
+            for (int k = 0; k < 4; k++) {
+                int32_t p = 0;
+                for (int u = 0; u < 4; u++) {
+                    const int e = 128 * h + 32 * k + 4 * l + u;
+                    p += q6k_at(blk, e) * xq[e];
+                }
+                s += p * sc[8 * h + 2 * k + (l >> 2)];
+            }
+        const int32_t corr = sc[2 * l] * bs[2 * l] + sc[2 * l + 1] * bs[2 * l + 1];
+        out[l] = s - 32 * corr;
+    }
+}
+// imi/core/tables.cpp:271-276: acc_l = fma(d * X.d[i], float(lane_l), acc_l) over blocks; then the 256-bit
+// horizontal sum ((a0 + a4) + (a2 + a6)) + ((a1 + a5) + (a3 + a7))
+float q6k_row(const uint8_t* row, const q8kin& X, int nblocks) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int i = 0; i < nblocks; i++) {
+        const uint8_t* b = row + 210 * (size_t)i;
+        int32_t lane[8];
+        q6k_lane_sums(b, X, i, lane);
+        const float dd = blk_d(b) * X.d[i];
+        for (int l = 0; l < 8; l++) acc[l] = fmaf(dd, (float)lane[l], acc[l]);
+    }
+    return ((acc[0] + acc[4]) + (acc[2] + acc[6])) + ((acc[1] + acc[5]) + (acc[3] + acc[7]));
+}
+
 bool q8g_build(q8gtab& t, const std::vector<const uint8_t*>& rows, int cols) {
     if (rows.empty() || cols % 32) return false;
     t.rows = (int)rows.size(); t.rows_pad = (t.rows + 7) / 8 * 8; t.cols = cols; t.nb = cols / 32;

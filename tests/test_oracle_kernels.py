@@ -168,3 +168,126 @@ def test_rms_scale_and_rope_float64():
         x0, x1 = v[:D // 2].astype(np.float64), v[D // 2:].astype(np.float64)
         want = np.concatenate([x0 * c - x1 * s, x0 * s + x1 * c])
         assert np.abs(r - want).max() <= 2e-5 * max(1.0, pos / 64)
+
+
+# ---- Q6_K word table (imi/core/tables.cpp:200-287) ----
+
+def _q6k_blocks(n, rng):
+    from nunchi_amd.gguf import Q6_K_BLOCK
+    b = np.zeros(n, Q6_K_BLOCK)
+    b["ql"] = rng.integers(0, 256, (n, 128), dtype=np.uint8)
+    b["qh"] = rng.integers(0, 256, (n, 64), dtype=np.uint8)
+    b["scales"] = rng.integers(-128, 128, (n, 16), dtype=np.int8)
+    b["d"] = (rng.standard_normal(n) * 1e-3).astype(np.float16)
+    return b
+
+
+def _q6k_values(b):
+    """[n][256] 6-bit values by the GGML Q6_K layout: per 128-value half n and l < 32, the four values l, l+32,
+    l+64, l+96 take ql[l] low, ql[l+32] low, ql[l] high, ql[l+32] high nibbles and bit pairs 0, 2, 4, 6 of qh[l]."""
+    ql, qh = b["ql"].astype(np.int32), b["qh"].astype(np.int32)
+    out = np.zeros((len(b), 256), np.int32)
+    for h in range(2):
+        lo, hi = ql[:, 64 * h:64 * h + 64], qh[:, 32 * h:32 * h + 32]
+        base = 128 * h
+        out[:, base:base + 32] = (lo[:, :32] & 15) | ((hi & 3) << 4)
+        out[:, base + 32:base + 64] = (lo[:, 32:] & 15) | (((hi >> 2) & 3) << 4)
+        out[:, base + 64:base + 96] = (lo[:, :32] >> 4) | (((hi >> 4) & 3) << 4)
+        out[:, base + 96:base + 128] = (lo[:, 32:] >> 4) | (((hi >> 6) & 3) << 4)
+    return out
+
+
+def test_q6k_dequant_closed_form():
+    """imi_q6k_dequant_row: y = (d * scale[e / 16]) * (value - 32) in fp32, values decoded from the format; scale
+    edge cases (+-128/127, 0) and fp16 d edge cases (0, subnormal, max, negative)."""
+    r = np.random.default_rng(61)
+    b = _q6k_blocks(64, r)
+    b["scales"][0] = np.array([-128, 127, 0, 1, -1] + [64] * 11, np.int8)
+    b["d"][:6] = np.array([0.0, 6e-8, 65504.0, -2.0, 1.0, -0.0], np.float16)
+    q = _q6k_values(b)
+    d = b["d"].astype(np.float32)[:, None]
+    sc = np.repeat(b["scales"].astype(np.float32), 16, axis=1)
+    want = (d * sc) * (q - 32).astype(np.float32)
+    row = b.view(np.uint8).reshape(4, -1)          # 4 rows of 16 blocks (n_embd 4096)
+    got = np.concatenate([oracle.q6k_dequant(row[i], 4096) for i in range(4)]).reshape(64, 256)
+    assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
+
+
+def test_q8k_cut_brute_force():
+    """imi_q8k::from: per 256 values d = amax / 127 (fp32 division), id = d ? 1 / d : 0, codes rint(x * id)
+    half-even, int16 code sums per 16; with an all-zero block and exact ties."""
+    r = np.random.default_rng(62)
+    x = (r.standard_normal(2048) * 3).astype(np.float32)
+    x[256:512] = 0.0
+    x[512] = 127.0
+    x[513:520] = np.array([0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5], np.float32)   # d = 1 exactly: ties
+    q, d, bs = oracle.q8k(x)
+    xb = x.reshape(8, 256)
+    amax = np.abs(xb).max(axis=1).astype(np.float32)
+    dd = (amax / np.float32(127)).astype(np.float32)
+    idv = np.where(dd != 0, np.float32(1) / np.where(dd != 0, dd, 1), 0).astype(np.float32)
+    wq = np.rint((xb * idv[:, None]).astype(np.float32)).astype(np.int32)
+    assert np.array_equal(d.view(np.uint32), dd.view(np.uint32))
+    assert np.array_equal(q.reshape(8, 256).astype(np.int32), wq)
+    assert np.array_equal(bs.astype(np.int32), wq.reshape(128, 16).sum(axis=1))
+    assert list(q[513:520]) == [0, 2, 2, 0, -2, -2, 126]
+
+
+def _avx2_lanes(blk, xq, bsums):
+    """The int32 lanes of imi_q6k_row's AVX2 body (imi/core/tables.cpp:246-270), emulated instruction by instruction
+    on 32-byte registers: 16-bit shifts and byte masks build the 6-bit values, maddubs (u8 x s8 pairs -> s16,
+    saturating), a per-128-bit-lane byte shuffle broadcasts the scales, madd (s16 pairs -> s32), then - 32 * corr."""
+    ql, qh = blk["ql"], blk["qh"]
+    sc = blk["scales"].astype(np.int16)
+
+    def srli16(v, n):
+        return (v.view(np.uint16) >> n).astype(np.uint16).view(np.uint8)
+
+    def slli16(v, n):
+        return (v.view(np.uint16) << n).astype(np.uint16).view(np.uint8)
+
+    def maddubs(a, b):
+        p = a.astype(np.int32) * b.astype(np.int32)
+        return np.clip(p[0::2] + p[1::2], -32768, 32767).astype(np.int16)
+
+    def madd(a, b):
+        p = a.astype(np.int32) * b.astype(np.int32)
+        return (p[0::2] + p[1::2]).astype(np.int32)
+
+    isum = np.zeros(8, np.int64)
+    for n in range(2):
+        a, a2, h = ql[64 * n:64 * n + 32], ql[64 * n + 32:64 * n + 64], qh[32 * n:32 * n + 32]
+        q = [(a & 15) | (slli16(h, 4) & 0x30), (a2 & 15) | (slli16(h, 2) & 0x30),
+             (srli16(a, 4) & 15) | (h & 0x30), (srli16(a2, 4) & 15) | (srli16(h, 2) & 0x30)]
+        s8 = sc[8 * n:8 * n + 8]
+        s2 = np.concatenate([s8, s8]).view(np.uint8)           # 32 bytes, both 128-bit lanes hold the 8 scales
+        for k in range(4):
+            ctl = np.array([2 * (2 * k) + (i & 1) for i in range(16)] + [2 * (2 * k + 1) + (i & 1) for i in range(16)])
+            sh = np.concatenate([s2[:16][ctl[:16]], s2[16:][ctl[16:]]]).view(np.int16)
+            p = maddubs(q[k], xq[128 * n + 32 * k:128 * n + 32 * k + 32])
+            isum += madd(p, sh)
+    corr = madd(sc, bsums)
+    return (isum - 32 * corr.astype(np.int64)).astype(np.int32)
+
+
+def test_q6k_lanes_and_row():
+    """imi_q6k_row: the oracle's 8 int32 lanes per block equal an instruction-level emulation of the AVX2 body, and
+    their total equals the closed form sum_e (value_e - 32) * scale_e * x_e exactly; the row result is
+    sum_i d_i * X.d_i * lanes in float64 to 1e-5 relative."""
+    r = np.random.default_rng(63)
+    nb, n_rows = 8, 24
+    b = _q6k_blocks(n_rows * nb, r)
+    x = (r.standard_normal(256 * nb) * 2).astype(np.float32)
+    out, lanes = oracle.q6k_rows(b.view(np.uint8).reshape(n_rows, -1), x, lanes=True)
+    q, d, bs = oracle.q8k(x)
+    vals = _q6k_values(b).reshape(n_rows, nb, 256) - 32
+    sc = np.repeat(b["scales"].astype(np.int64), 16, axis=1).reshape(n_rows, nb, 256)
+    xq = q.astype(np.int64).reshape(nb, 256)
+    assert np.array_equal(lanes.sum(axis=2).astype(np.int64), (vals * sc * xq[None]).sum(axis=2))
+    for rr in range(0, n_rows, 5):
+        for i in range(nb):
+            blk = b[rr * nb + i]
+            assert np.array_equal(lanes[rr, i], _avx2_lanes(blk, q[256 * i:256 * i + 256], bs[16 * i:16 * i + 16]))
+    dd = b["d"].astype(np.float64).reshape(n_rows, nb) * d.astype(np.float64)[None]
+    want = (dd * lanes.sum(axis=2)).sum(axis=1)
+    assert np.allclose(out, want, rtol=1e-5, atol=1e-6 * np.abs(want).max())
