@@ -239,6 +239,12 @@ def main():
     gu2 = brain.bench_kernel("ffn_gate_up", n_in=2, reps=64)
     tables1 = brain.bench_tables(1, 5)
     tables2 = brain.bench_tables(2, 5)
+    # imi's own word-table format: the same vocab shape as Q6_K (one layer in front, only the scores are timed)
+    q6_shape = synth.BrainShape(n_layer=1, attn_layers=(), n_vocab=synth.SEOUL.n_vocab, vocab_type="q6_k")
+    q6_brain = nunchi_amd.Brain(synth.cached("brain", q6_shape, 0), n_ctx=64)
+    ws6 = q6_brain.bench_kernel("word_scores", n_in=1, reps=8)
+    ws6_2 = q6_brain.bench_kernel("word_scores", n_in=2, reps=8)
+    del q6_brain
 
     # cfg 0: one Q4_0 x fp32 GEMV 8192 x 2048 with imi/kernels/q4x8 semantics, 64 distinct weight copies in rotation
     ctx = brain.ctx
@@ -302,7 +308,10 @@ def main():
             "ffn_gate_up_per_table": {"avg_us": round(gu["avg_us"], 3), "GBs": round(gu_gbs, 1), "frac": round(gu_gbs / HBM_PEAK_GBS, 4)},
             "ffn_gate_up_b2": {"avg_us": round(gu2["avg_us"], 3), "GBs": round(gu2["bytes_per_launch"] / gu2["avg_us"] / 1e3, 1)},
             "ffn_down": {"avg_us": round(dn["avg_us"], 3), "GBs": round(dn["bytes_per_launch"] / dn["avg_us"] / 1e3, 1)},
+            # (back-to-back launches of one table: it fits the 256 MB MALL, so these read faster than a decode step's)
             "word_scores": {"avg_us": round(ws["avg_us"], 3), "GBs": round(ws["bytes_per_launch"] / ws["avg_us"] / 1e3, 1)},
+            "word_scores_q6k_97496x2048": {"avg_us": round(ws6["avg_us"], 3), "GBs": round(ws6["bytes_per_launch"] / ws6["avg_us"] / 1e3, 1),
+                                           "b2_avg_us": round(ws6_2["avg_us"], 3), "bytes_per_launch": int(ws6["bytes_per_launch"])},
             "layer_tables_b1": {"avg_launch_us": round(tables1["avg_launch_us"], 3), "ms_per_pass": round(tables1["ms_per_pass"], 4),
                                 "GBs": round(tables1["bytes_per_pass"] / tables1["launches"] / tables1["avg_launch_us"] / 1e3, 1)},
             "layer_tables_b2": {"avg_launch_us": round(tables2["avg_launch_us"], 3), "ms_per_pass": round(tables2["ms_per_pass"], 4)},
