@@ -36,6 +36,10 @@ class BrainShape:
     eps: float = 1e-5
     qk_norm_scale: float = 1.0                    # > 1 sharpens attention (scores grow with its square)
     vocab_type: str = "q4_0"                      # tied word table: "q4_0", or "q6_k" (imi's own format)
+    rope_freqs: bool = False                      # write rope_freqs.weight (angle divisors, head_dim / 2 of them)
+    sliding_window: int = 0                       # window of the layers in swa_layers (0: none)
+    swa_layers: tuple = ()                        # attention layers with the window and the swa RoPE base
+    rope_base_swa: float = 1e4
 
 
 SEOUL = BrainShape()
@@ -113,7 +117,10 @@ def write_brain(path: str, shape: BrainShape = SEOUL, seed: int = 0) -> str:
     w.add_u32("lfm3.attention.key_length", D)
     w.add_f32("lfm3.attention.layer_norm_rms_epsilon", s.eps)
     w.add_f32("lfm3.rope.freq_base", s.rope_base)
-    w.add_u32("lfm3.attention.sliding_window", 0)
+    w.add_u32("lfm3.attention.sliding_window", s.sliding_window)
+    if s.swa_layers:
+        w.add_bool_array("lfm3.attention.sliding_window_pattern", [il in s.swa_layers for il in range(s.n_layer)])
+        w.add_f32("lfm3.rope.freq_base_swa", s.rope_base_swa)
     w.add_u32("lfm3.shortconv.l_cache", s.conv_kernel)
     w.add_u32("lfm3.feed_forward_length", s.n_ff)
 
@@ -128,6 +135,9 @@ def write_brain(path: str, shape: BrainShape = SEOUL, seed: int = 0) -> str:
     else:
         q4("token_embd.weight", s.n_vocab, E)
     f32("output_norm.weight", _norm_w(_rng(seed, "output_norm.weight"), E), (E,))
+    if s.rope_freqs:
+        ff = (1.0 + 3.0 * _rng(seed, "rope_freqs.weight").random(D // 2)).astype(np.float32)
+        f32("rope_freqs.weight", ff, (D // 2,))
     for il in range(s.n_layer):
         p = f"blk.{il}."
         for n in ("attn_norm", "post_attention_norm", "ffn_norm", "post_ffw_norm"):

@@ -1,0 +1,85 @@
+"""GPU parity on model features the real Seoul files use beyond BASELINE's synthetic shape (imi/core/seoul.cpp:99-114,
+136-142, 288-295, 428-431): rope_freqs angle divisors, sliding-window attention layers (window, pattern and their
+own RoPE base, no divisors), and a 7-tap short conv (6 positions of conv memory). Every hidden state and score is
+compared bit for bit with the oracle, on single steps past the window, step2, device-side greedy ids and a prefill
+longer than the window, on both device step paths.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def same(a, b) -> bool:
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.fixture(params=["kernels", "persistent"])
+def step_path(request, monkeypatch):
+    if request.param == "persistent":
+        monkeypatch.setenv("SEOUL_HIP_STEP", "persistent")
+    else:
+        monkeypatch.delenv("SEOUL_HIP_STEP", raising=False)
+    return request.param
+
+
+@pytest.fixture(scope="module", params=["tiny", "mid"])
+def feat_model(request, model_dir):
+    from nunchi_amd import synth
+    base = synth.TINY if request.param == "tiny" else synth.BrainShape(n_layer=4, attn_layers=(1, 3), n_vocab=4096)
+    shape = synth.BrainShape(**{**base.__dict__, "n_layer": 5, "attn_layers": (1, 2, 4), "conv_kernel": 7,
+                                "rope_freqs": True, "sliding_window": 16, "swa_layers": (1, 4)})
+    return synth.cached("brain", shape, 31, model_dir), shape
+
+
+def _prompt(n, vocab, seed):
+    return np.random.default_rng(seed).integers(0, vocab, size=n).astype(np.int32)
+
+
+def test_features_steps_and_greedy(feat_model, step_path):
+    import nunchi_amd
+    import oracle
+    path, shape = feat_model
+    g = nunchi_amd.Brain(path, n_ctx=128)
+    o = oracle.Engine(path, threads=4, n_ctx=128)
+    for i, t in enumerate(_prompt(40, shape.n_vocab, 32)):   # past the 16-position window
+        hg, lg, bg = g.step(int(t))
+        ho, lo = o.step(int(t))
+        assert same(hg, ho) and same(lg, lo), i
+    ids_g, _ = g.generate(bg, 48)
+    ids_o, _ = o.greedy(bg, 48)
+    assert np.array_equal(ids_g, ids_o)
+
+
+def test_features_step2(feat_model, step_path):
+    import nunchi_amd
+    import oracle
+    path, shape = feat_model
+    g = nunchi_amd.Brain(path, n_ctx=64)
+    o = oracle.Engine(path, threads=4, n_ctx=64)
+    gb, ob = g.new_state(), o.new_state()
+    ta, tb = _prompt(24, shape.n_vocab, 33), _prompt(24, shape.n_vocab, 34)
+    for i in range(24):
+        (ha, la, _), (hb, lb, _) = g.step2(int(ta[i]), None, True, gb, int(tb[i]), None, i % 3 == 0)
+        hoa, loa, hob, lob = o.step2(int(ta[i]), None, True, ob, int(tb[i]), None, i % 3 == 0)
+        assert same(ha, hoa) and same(hb, hob) and same(la, loa), i
+        if i % 3 == 0:
+            assert same(lb, lob), i
+
+
+def test_features_prefill(feat_model):
+    import nunchi_amd
+    import oracle
+    path, shape = feat_model
+    g = nunchi_amd.Brain(path, n_ctx=160)
+    o = oracle.Engine(path, threads=4, n_ctx=160)
+    toks = _prompt(70, shape.n_vocab, 35)
+    hg, lg, bg, hall_g = g.step_batch(toks, hidden_all=True)
+    ho, lo, hall_o = o.step_batch(toks, hidden_all=True)
+    for p in range(len(toks)):
+        assert same(hall_g[p], hall_o[p]), p
+    assert same(lg, lo) and bg == oracle.top(lo)
+    hg, lg, _ = g.step(7)   # and a step after it reads the prefill's caches and conv memory
+    ho, lo = o.step(7)
+    assert same(hg, ho) and same(lg, lo)
