@@ -284,7 +284,9 @@ std::vector<float2> rope_table(int n_ctx, int D, float base, const float* ff) {
 // The persistent kernel's program: the stages of one step in order, each with its own tagged output buffer
 // [2 parity][2 conversations][n_out] (zeroed: tag 0 is never a step's epoch).
 int build_program(sh_ctx* c) {
-    if (c->vocab6.codes) return fail(SH_E_SHAPE, "step kernel: the word table is Q6_K");   // per-table kernels run it
+    // shapes the step kernel does not read run on the per-table kernels
+    if (c->vocab6.codes) return fail(SH_E_SHAPE, "step kernel: the word table is Q6_K");
+    if (c->info.n_attn > 0 && c->info.head_dim != 32 && c->info.head_dim != 64) return fail(SH_E_SHAPE, "step kernel: head_dim 32 or 64");
     const sh_model_info& I = c->info;
     const int E = I.n_embd, Hq = I.n_head * I.head_dim;
     int dev_cus = 0;
@@ -631,8 +633,8 @@ int sh_load(sh_ctx* c, const char* path, int n_ctx) {
     const gg_tensor* rf = f.get("rope_freqs.weight", false);
     I.n_attn = n_attn;
     c->n_conv = n_conv;
-    if (n_attn > 0 && (I.head_dim > 64 || I.head_dim % 2 || I.n_head % I.n_head_kv || I.n_head / I.n_head_kv > 8))
-        return fail(SH_E_SHAPE, "sh_load: attention shape not supported (head_dim <= 64, group <= 8)");
+    if (n_attn > 0 && ((I.head_dim != 32 && I.head_dim != 64 && I.head_dim != 128) || I.n_head % I.n_head_kv || I.n_head / I.n_head_kv > 8))
+        return fail(SH_E_SHAPE, "sh_load: attention shape not supported (head_dim 32, 64 or 128, group <= 8)");
     if (n_attn > 0 && (I.n_head * I.head_dim) / 32 > 64) return fail(SH_E_SHAPE, "sh_load: attention width above 2048");
     if (I.n_ff % 32 || I.n_ff / 32 > 256) return fail(SH_E_SHAPE, "sh_load: n_ff must be a multiple of 32, at most 8192");
     c->nqkv = I.n_head * I.head_dim + 2 * I.n_head_kv * I.head_dim + I.n_head;

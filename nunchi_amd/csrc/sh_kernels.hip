@@ -1012,7 +1012,8 @@ __global__ __launch_bounds__(256) void k_attn(attn_args a) {
 //    j + 1 is written and tile j + 2 requested while wave 0 runs tile j;
 //  - times the sigmoid head gate.
 namespace attn_detail {
-constexpr int NT = 512, TV = 256;   // threads, positions per value tile
+constexpr int NT = 512;                                        // threads
+template <int D> constexpr int tile_positions() { return D > 64 ? 128 : 256; }   // value tile: 32 KB of fp16 at D 64 / 128
 __device__ __forceinline__ int vswz(int d) { return (2 * (d >> 3) + 4 * (d & 7) + ((d & 7) >> 2)) & 15; }
 // lowest set bit exponent of a positive float (e = 0 gives a large value)
 __device__ __forceinline__ int low_bit_exp(float e) {
@@ -1025,8 +1026,12 @@ __device__ __forceinline__ int low_bit_exp(float e) {
 template <int D>
 __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
     using namespace attn_detail;
+    constexpr int TV = tile_positions<D>();
     constexpr int half = D / 2, KW = D / 8;        // 16-byte words per cache row
+    constexpr int DPL = (D + 63) / 64;             // dimensions per lane in the per-head wave work (lane + 64 c)
+    constexpr bool AHEAD2 = D <= 64;               // key rows requested two passes ahead (one at D 128: registers)
     constexpr int NL = (TV / 8) * KW;              // loader threads: one 8-position x 8-dimension block each
+    static_assert(NL <= 256 && TV / 8 <= 32, "value staging layout");
     extern __shared__ __align__(16) float lds[];
     const int h = blockIdx.x, m = blockIdx.y, t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int grp = a.n_head / a.n_kv, g = h / grp, hh = h - g * grp;
@@ -1049,13 +1054,14 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
     const int last = max(nk - 2, 0);               // last cache row written by an earlier step
 
     // ---- requests first ----
-    u32x4 ka[KW], kb[KW];
+    u32x4 ka[KW], kb[AHEAD2 ? KW : 1];
     {
         const int p0 = min(t, last), p1 = min(t + NT, last);
 #pragma unroll
         for (int i = 0; i < KW; i++) ka[i] = ((const u32x4*)(kc + (size_t)(s0 + p0) * D))[i];
+        if (AHEAD2)
 #pragma unroll
-        for (int i = 0; i < KW; i++) kb[i] = ((const u32x4*)(kc + (size_t)(s0 + p1) * D))[i];
+            for (int i = 0; i < KW; i++) kb[AHEAD2 ? i : 0] = ((const u32x4*)(kc + (size_t)(s0 + p1) * D))[i];
     }
     // value staging: loader lt = t - 256 holds positions 8 * pb .. + 7 of a tile, dimensions 8 * kq .. + 7
     const int lt = t - 256, kq = lt & (KW - 1), pb = lt / KW;
@@ -1097,29 +1103,40 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
     };
 
     // ---- q (wave 0) and this position's k, v (wave 1): norm + NEOX rope (imi/core/seoul.cpp:19-28) ----
-    if (wv < 2) {
+    if (wv < 2) {   // lane holds dimensions lane + 64 c; at D 128 a rope pair (i, i + 64) sits in one lane
         const bool is_k = wv == 1;
         const float* src = is_k ? row + Hq + g * D : row + h * D;
         const float* w = is_k ? a.k_norm : a.q_norm;
         float* st = stg + wv * D;
-        const float x = lane < D ? src[lane] : 0.0f;
-        if (lane < D) st[lane] = x;
+        float x[DPL], n[DPL];
+#pragma unroll
+        for (int c = 0; c < DPL; c++) {
+            const int e = lane + 64 * c;
+            x[c] = e < D ? src[e] : 0.0f;
+            if (e < D) st[e] = x[c];
+        }
         __builtin_amdgcn_wave_barrier();
         const float s = rms_scale_wave(st, D, a.eps);
-        const float n = lane < D ? x * s * w[lane] : 0.0f;
-        const float other = __shfl(n, lane < half ? lane + half : lane - half);
-        if (lane < D) {
-            const float2 cz = cs[lane < half ? lane : lane - half];
-            const float r = lane < half ? fmaf(n, cz.x, -(other * cz.y)) : fmaf(other, cz.y, n * cz.x);
-            if (is_k) {
-                const uint16_t kh = f2h(r);
-                k_s[lane] = h2f(kh);
-                if (hh == 0) {
-                    kc[(size_t)pos * D + lane] = kh;
-                    vc[(size_t)pos * D + lane] = f2h(row[Hq + kvd + g * D + lane]);
+#pragma unroll
+        for (int c = 0; c < DPL; c++) n[c] = lane + 64 * c < D ? x[c] * s * w[lane + 64 * c] : 0.0f;
+        const float sh = __shfl(n[0], lane < half ? lane + half : lane - half);
+#pragma unroll
+        for (int c = 0; c < DPL; c++) {
+            const int e = lane + 64 * c;
+            if (e < D) {
+                const float other = DPL == 2 ? n[c ^ 1] : sh;
+                const float2 cz = cs[e < half ? e : e - half];
+                const float r = e < half ? fmaf(n[c], cz.x, -(other * cz.y)) : fmaf(other, cz.y, n[c] * cz.x);
+                if (is_k) {
+                    const uint16_t kh = f2h(r);
+                    k_s[e] = h2f(kh);
+                    if (hh == 0) {
+                        kc[(size_t)pos * D + e] = kh;
+                        vc[(size_t)pos * D + e] = f2h(row[Hq + kvd + g * D + e]);
+                    }
+                } else {
+                    q_s[e] = r;
                 }
-            } else {
-                q_s[lane] = r;
             }
         }
     }
@@ -1127,6 +1144,33 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
     // ---- scores ----
     const float scale = 1.0f / sqrtf((float)D);
     for (int p = t; p < nk; p += NT) {
+        if (!AHEAD2 && p != t) {   // D 128: this pass's row requested here (no prefetch registers to spare)
+#pragma unroll
+            for (int i = 0; i < KW; i++) ka[i] = ((const u32x4*)(kc + (size_t)(s0 + min(p, last)) * D))[i];
+        }
+        if (!AHEAD2) {   // dot_h's 8 chains over columns i % 8, a word (8 columns) at a time
+            float acc[8];
+#pragma unroll
+            for (int l = 0; l < 8; l++) acc[l] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < KW; i++) {
+                const f32x4 qa = *(const f32x4*)(q_s + 8 * i), qb = *(const f32x4*)(q_s + 8 * i + 4);
+                const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+                float kv[8];
+                if (p == nk - 1) {
+                    const f32x4 ka4 = *(const f32x4*)(k_s + 8 * i), kb4 = *(const f32x4*)(k_s + 8 * i + 4);
+                    kv[0] = ka4.x; kv[1] = ka4.y; kv[2] = ka4.z; kv[3] = ka4.w; kv[4] = kb4.x; kv[5] = kb4.y; kv[6] = kb4.z; kv[7] = kb4.w;
+                } else {
+                    const unsigned w4[4] = {ka[i].x, ka[i].y, ka[i].z, ka[i].w};
+#pragma unroll
+                    for (int e = 0; e < 8; e++) kv[e] = h2f((uint16_t)((w4[e >> 1] >> (16 * (e & 1))) & 0xFFFFu));
+                }
+#pragma unroll
+                for (int l = 0; l < 8; l++) acc[l] = fmaf(qv[l], kv[l], acc[l]);
+            }
+            sc[p] = (((acc[0] + acc[4]) + (acc[2] + acc[6])) + ((acc[1] + acc[5]) + (acc[3] + acc[7]))) * scale;
+            continue;
+        }
         u32x4 kn[KW];
         const int pn = min(p + 2 * NT, last);
 #pragma unroll
@@ -1145,7 +1189,7 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
         }
         sc[p] = dot_h8<D>(q_s, kf) * scale;
 #pragma unroll
-        for (int i = 0; i < KW; i++) { ka[i] = kb[i]; kb[i] = kn[i]; }
+        for (int i = 0; i < KW; i++) { ka[i] = kb[AHEAD2 ? i : 0]; kb[AHEAD2 ? i : 0] = kn[i]; }
     }
     if (loader) {   // tile 0 requested (to LDS once the softmax is done)
         load_tile(0);
@@ -1210,27 +1254,41 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
     }
     __syncthreads();
     // ---- o = sum_t fma(a_t, V_t, o), lane i of wave 0; tiles double-buffered through LDS ----
-    float o = 0.0f;
+    float o[DPL];
+#pragma unroll
+    for (int c = 0; c < DPL; c++) o[c] = 0.0f;
     for (int j = 0; j < ntile; j++) {
-        if (wv == 0 && lane < D) {
-            const int q0 = j * TV, nt = min(TV, nk - q0), fz = vswz(lane);
-            const uint16_t* vr = vT + (size_t)(j & 1) * D * TV + (size_t)lane * TV;
+        if (wv == 0 && lane < D) {   // dimension lane + 64 c's chain (two independent chains per lane at D 128)
+            const int q0 = j * TV, nt = min(TV, nk - q0);
             const float* ar = sc + q0;
+            int fz[DPL];
+            const uint16_t* vr[DPL];
+#pragma unroll
+            for (int c = 0; c < DPL; c++) {
+                fz[c] = vswz(lane + 64 * c);
+                vr[c] = vT + (size_t)(j & 1) * D * TV + (size_t)(lane + 64 * c) * TV;
+            }
             int p = 0;
             for (; p + 8 <= nt; p += 8) {
-                const u32x4 w = *(const u32x4*)(vr + 8 * ((p >> 3) ^ fz));
                 const f32x4 a0 = *(const f32x4*)(ar + p), a1 = *(const f32x4*)(ar + p + 4);
                 const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-                const unsigned ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-                for (int u = 0; u < 8; u++) o = fmaf(av[u], h2f((uint16_t)((ws[u >> 1] >> (16 * (u & 1))) & 0xFFFFu)), o);
+                for (int c = 0; c < DPL; c++) {
+                    const u32x4 w = *(const u32x4*)(vr[c] + 8 * ((p >> 3) ^ fz[c]));
+                    const unsigned ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int u = 0; u < 8; u++) o[c] = fmaf(av[u], h2f((uint16_t)((ws[u >> 1] >> (16 * (u & 1))) & 0xFFFFu)), o[c]);
+                }
             }
             if (p < nt) {
-                const u32x4 w = *(const u32x4*)(vr + 8 * ((p >> 3) ^ fz));
-                const unsigned ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-                for (int u = 0; u < 8; u++)
-                    if (p + u < nt) o = fmaf(ar[p + u], h2f((uint16_t)((ws[u >> 1] >> (16 * (u & 1))) & 0xFFFFu)), o);
+                for (int c = 0; c < DPL; c++) {
+                    const u32x4 w = *(const u32x4*)(vr[c] + 8 * ((p >> 3) ^ fz[c]));
+                    const unsigned ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int u = 0; u < 8; u++)
+                        if (p + u < nt) o[c] = fmaf(ar[p + u], h2f((uint16_t)((ws[u >> 1] >> (16 * (u & 1))) & 0xFFFFu)), o[c]);
+                }
             }
         }
         if (loader && j + 1 < ntile) {
@@ -1241,13 +1299,15 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
     }
     if (wv == 0 && lane < D) {
         const float gate = 1.0f / (1.0f + expf_glibc(-row[Hq + 2 * kvd + h]));
-        a.att[(size_t)m * Hq + h * D + lane] = o * gate;
+#pragma unroll
+        for (int c = 0; c < DPL; c++)
+            if (lane + 64 * c < D) a.att[(size_t)m * Hq + h * D + lane + 64 * c] = o[c] * gate;
     }
 }
 
 static size_t attn_head_lds(int D, int n_ctx) {
-    return sizeof(float) * (4 * (size_t)D + 32 + 16 + 8 + (((size_t)n_ctx + 3) & ~(size_t)3)) +
-           2 * (size_t)D * attn_detail::TV * sizeof(uint16_t);
+    const size_t tv = D > 64 ? attn_detail::tile_positions<128>() : attn_detail::tile_positions<64>();
+    return sizeof(float) * (4 * (size_t)D + 32 + 16 + 8 + (((size_t)n_ctx + 3) & ~(size_t)3)) + 2 * (size_t)D * tv * sizeof(uint16_t);
 }
 
 // ---------------------------------------------------------------- end of step
@@ -1442,7 +1502,8 @@ hipError_t launch_attn(int M, const attn_args& a, hipStream_t s) {
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     {   // one block per query head
         const size_t lds2 = attn_head_lds(a.D, a.n_ctx);
-        const void* fh = a.D == 64 ? (const void*)k_attn_head<64> : a.D == 32 ? (const void*)k_attn_head<32> : nullptr;
+        const void* fh = a.D == 128 ? (const void*)k_attn_head<128> : a.D == 64 ? (const void*)k_attn_head<64>
+                       : a.D == 32 ? (const void*)k_attn_head<32> : nullptr;
         if (fh && lds2 <= 160 * 1024) {
             if (lds2 > 64 * 1024) {
                 const hipError_t e = hipFuncSetAttribute(fh, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);

@@ -267,21 +267,20 @@ __global__ __launch_bounds__(256) void k_pf_conv_state(pf_conv_args a) {
 // keys and values of the batch into the fp16 cache: k = rope(norm(k) * k_norm) at the position (imi/core/seoul.cpp:
 // 590-601); one wave per (position, kv head)
 __global__ __launch_bounds__(64) void k_pf_kv(pf_attn_args a) {
-    __shared__ float st[64];
-    const int p = blockIdx.x, g = blockIdx.y, lane = threadIdx.x, D = a.D, half = D / 2;
+    __shared__ float st[128];
+    const int p = blockIdx.x, g = blockIdx.y, lane = threadIdx.x, D = a.D;
     const int at = a.pos0 + p, Hq = a.n_head * D, kvd = a.n_kv * D;
     const float* row = a.qkv + (size_t)p * a.ld;
-    const float x = lane < D ? row[Hq + g * D + lane] : 0.0f;
-    st[lane] = x;
-    __builtin_amdgcn_wave_barrier();
-    const float s = rms_scale_wave(static_cast<const float*>(st), D, a.eps);
-    const float nv = lane < D ? x * s * a.k_norm[lane] : 0.0f;
-    const float other = __shfl(nv, lane < half ? lane + half : lane - half);
-    if (lane < D) {
-        const float2 cs = a.rope_cs[(size_t)at * half + (lane < half ? lane : lane - half)];
-        const float kd = lane < half ? fmaf(nv, cs.x, -(other * cs.y)) : fmaf(other, cs.y, nv * cs.x);
-        a.kc[((size_t)g * a.n_ctx + at) * D + lane] = f2h(kd);
-        a.vc[((size_t)g * a.n_ctx + at) * D + lane] = f2h(row[Hq + kvd + g * D + lane]);
+    float kd[2];
+    const float2* cs = a.rope_cs + (size_t)at * (D / 2);
+    if (D > 64) head_norm_rope<2>(row + Hq + g * D, a.k_norm, (float*)st, cs, D, a.eps, kd);
+    else head_norm_rope<1>(row + Hq + g * D, a.k_norm, (float*)st, cs, D, a.eps, kd);
+    for (int c = 0; c < 2; c++) {
+        const int e = lane + 64 * c;
+        if (e < D) {
+            a.kc[((size_t)g * a.n_ctx + at) * D + e] = f2h(kd[c]);
+            a.vc[((size_t)g * a.n_ctx + at) * D + e] = f2h(row[Hq + kvd + g * D + e]);
+        }
     }
 }
 
@@ -307,20 +306,13 @@ __global__ __launch_bounds__(256) void k_pf_attn(pf_attn_args a) {
     float* sc = inv_s + 8;                 // [grp][nks]
     const float2* cs = a.rope_cs + (size_t)at * half;
 
+    constexpr int DPL = (D + 63) / 64;
     for (int hh = wv; hh < grp; hh += 4) {
-        float* stg = scratch + wv * D;
-        const float* src = row + (g * grp + hh) * D;
-        const float x = lane < D ? src[lane] : 0.0f;
-        if (lane < D) stg[lane] = x;
-        __builtin_amdgcn_wave_barrier();
-        const float s = rms_scale_wave(static_cast<const float*>(stg), D, a.eps);
-        const float nv = lane < D ? x * s * a.q_norm[lane] : 0.0f;
-        const float other = __shfl(nv, lane < half ? lane + half : lane - half);
-        if (lane < D) {
-            const float2 t = cs[lane < half ? lane : lane - half];
-            q_s[hh * D + lane] = lane < half ? fmaf(nv, t.x, -(other * t.y)) : fmaf(other, t.y, nv * t.x);
-        }
-        __builtin_amdgcn_wave_barrier();
+        float r[DPL];
+        head_norm_rope<DPL>(row + (g * grp + hh) * D, a.q_norm, scratch + wv * D, cs, D, a.eps, r);
+#pragma unroll
+        for (int c = 0; c < DPL; c++)
+            if (lane + 64 * c < D) q_s[hh * D + lane + 64 * c] = r[c];
     }
     __syncthreads();
 
@@ -408,7 +400,7 @@ hipError_t launch_pf_conv(const pf_conv_args& a, hipStream_t s) {
 }
 
 hipError_t launch_pf_kv(const pf_attn_args& a, hipStream_t s) {
-    if (a.D > 64 || a.D % 32 || a.n < 1) return hipErrorInvalidValue;
+    if (a.D > 128 || a.D % 32 || a.n < 1) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_pf_kv, dim3(a.n, a.n_kv), dim3(64), 0, s, a);
     return hipGetLastError();
 }
@@ -417,17 +409,16 @@ hipError_t launch_pf_attn(const pf_attn_args& a, hipStream_t s) {
     const int grp = a.n_head / a.n_kv;
     const size_t lds = sizeof(float) * ((size_t)2 * grp * a.D + 4 * (size_t)a.D + 8 + (size_t)grp * (a.pos0 + a.n));
     if (lds > 160 * 1024 || a.n < 1) return hipErrorInvalidValue;
-    const void* fn = a.D == 64 ? (const void*)k_pf_attn<64> : a.D == 32 ? (const void*)k_pf_attn<32> : nullptr;
+    const void* fn = a.D == 128 ? (const void*)k_pf_attn<128> : a.D == 64 ? (const void*)k_pf_attn<64>
+                   : a.D == 32 ? (const void*)k_pf_attn<32> : nullptr;
     if (!fn) return hipErrorInvalidValue;
     if (lds > 64 * 1024) {
         const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
     }
-    if (a.D == 64)
-        hipLaunchKernelGGL(k_pf_attn<64>, dim3(a.n, a.n_kv), dim3(256), lds, s, a);
-    else
-        hipLaunchKernelGGL(k_pf_attn<32>, dim3(a.n, a.n_kv), dim3(256), lds, s, a);
-    return hipGetLastError();
+    pf_attn_args b = a;
+    void* args[] = {&b};
+    return hipLaunchKernel(fn, dim3(a.n, a.n_kv), dim3(256), args, lds, s);
 }
 
 }  // namespace sh

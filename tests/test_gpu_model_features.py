@@ -83,3 +83,55 @@ def test_features_prefill(feat_model):
     hg, lg, _ = g.step(7)   # and a step after it reads the prefill's caches and conv memory
     ho, lo = o.step(7)
     assert same(hg, ho) and same(lg, lo)
+
+
+@pytest.fixture(scope="module", params=["tiny", "mid"])
+def wide_head_model(request, model_dir):
+    """head_dim 128 (the reference loader's default key_length): 8/2 heads at width 1024, 16/4 heads at 2048 (the
+    q|k|v|gate rows stay a multiple of 8, as imi's table build requires)."""
+    from nunchi_amd import synth
+    if request.param == "tiny":
+        shape = synth.BrainShape(**{**synth.TINY.__dict__, "n_embd": 1024, "n_head": 8, "n_head_kv": 2, "head_dim": 128,
+                                    "n_ff": 1024})
+    else:
+        shape = synth.BrainShape(n_layer=4, attn_layers=(1, 3), n_head=16, n_head_kv=4, head_dim=128, n_vocab=4096)
+    return synth.cached("brain", shape, 36, model_dir), shape
+
+
+def test_head_dim_128_long_context(wide_head_model, step_path):
+    """Single steps, then 600 device-side greedy ids (several value tiles, key rows past one pass of the block),
+    then one more step compared bit for bit."""
+    import nunchi_amd
+    import oracle
+    path, shape = wide_head_model
+    g = nunchi_amd.Brain(path, n_ctx=640)
+    o = oracle.Engine(path, threads=8, n_ctx=640)
+    for i, t in enumerate(_prompt(8, shape.n_vocab, 37)):
+        hg, lg, bg = g.step(int(t))
+        ho, lo = o.step(int(t))
+        assert same(hg, ho) and same(lg, lo), i
+    ids_g, _ = g.generate(bg, 600)
+    ids_o, _ = o.greedy(bg, 600)
+    assert np.array_equal(ids_g, ids_o), int(np.argmax(ids_g != ids_o))
+    hg, lg, _ = g.step(int(ids_g[-1]))
+    ho, lo = o.step(int(ids_o[-1]))
+    assert same(hg, ho) and same(lg, lo)
+
+
+def test_head_dim_128_step2_and_prefill(wide_head_model):
+    import nunchi_amd
+    import oracle
+    path, shape = wide_head_model
+    g = nunchi_amd.Brain(path, n_ctx=160)
+    o = oracle.Engine(path, threads=4, n_ctx=160)
+    toks = _prompt(70, shape.n_vocab, 38)
+    hg, lg, bg, hall_g = g.step_batch(toks, hidden_all=True)
+    ho, lo, hall_o = o.step_batch(toks, hidden_all=True)
+    for p in range(len(toks)):
+        assert same(hall_g[p], hall_o[p]), p
+    assert same(lg, lo) and bg == oracle.top(lo)
+    gb, ob = g.new_state(), o.new_state()
+    for i in range(8):
+        (ha, la, _), (hb, lb, _) = g.step2(int(toks[i]), None, True, gb, int(toks[-1 - i]), None, True)
+        hoa, loa, hob, lob = o.step2(int(toks[i]), None, True, ob, int(toks[-1 - i]), None, True)
+        assert same(ha, hoa) and same(hb, hob) and same(la, loa) and same(lb, lob), i
