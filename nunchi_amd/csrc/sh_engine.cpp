@@ -32,23 +32,29 @@ int fail(int code, const std::string& msg) {
         if (e_ != hipSuccess) return fail(SH_E_HIP, std::string(#x) + ": " + hipGetErrorString(e_));       \
     } while (0)
 
-// Q4_0 rows (tensor, row) -> device layout in a host staging buffer: codes [rows][nb][16], scales [rows/8][nb][8]
-bool repack_q4(const std::vector<std::pair<const gg_tensor*, int>>& rows, std::vector<uint8_t>& codes, std::vector<uint16_t>& scales, int* cols) {
+// Q4_0 / Q4_1 rows (tensor, row) -> device layout in a host staging buffer: codes [rows][nb][16], scales and (Q4_1)
+// block minima [rows/8][nb][8]. A table's rows are all Q4_0 or all Q4_1 (imi/core/tables.cpp:70-72).
+bool repack_q4(const std::vector<std::pair<const gg_tensor*, int>>& rows, std::vector<uint8_t>& codes, std::vector<uint16_t>& scales,
+               std::vector<uint16_t>& mins, int* cols) {
     if (rows.empty() || rows.size() % 8) return false;
     const gg_tensor* t0 = rows[0].first;
+    if (t0->type != GT_Q4_0 && t0->type != GT_Q4_1) return false;
     for (auto& r : rows)
-        if (!r.first->data || r.first->type != GT_Q4_0 || r.first->ne[0] != t0->ne[0]) return false;
+        if (!r.first->data || r.first->type != t0->type || r.first->ne[0] != t0->ne[0]) return false;
+    const bool q41 = t0->type == GT_Q4_1;
+    const size_t bb = q41 ? 20 : 18;   // block: fp16 d, (Q4_1: fp16 m,) 16 bytes of nibbles
     const int K = (int)t0->ne[0], nb = K / 32, R = (int)rows.size();
     codes.resize((size_t)R * nb * 16);
     scales.resize((size_t)R * nb);
+    mins.assign(q41 ? (size_t)R * nb : 0, 0);
     for (int r = 0; r < R; r++) {
         const uint8_t* src = static_cast<const uint8_t*>(rows[r].first->data) + (size_t)rows[r].second * rows[r].first->nb[1];
         for (int j = 0; j < nb; j++) {
-            const uint8_t* blk = src + (size_t)j * 18;
-            uint16_t d;
-            memcpy(&d, blk, 2);
-            scales[((size_t)(r / 8) * nb + j) * 8 + (r % 8)] = d;
-            memcpy(&codes[((size_t)r * nb + j) * 16], blk + 2, 16);
+            const uint8_t* blk = src + (size_t)j * bb;
+            const size_t so = ((size_t)(r / 8) * nb + j) * 8 + (r % 8);
+            memcpy(&scales[so], blk, 2);
+            if (q41) memcpy(&mins[so], blk + 2, 2);
+            memcpy(&codes[((size_t)r * nb + j) * 16], blk + bb - 16, 16);
         }
     }
     *cols = K;
@@ -287,6 +293,9 @@ int build_program(sh_ctx* c) {
     // shapes the step kernel does not read run on the per-table kernels
     if (c->vocab6.codes) return fail(SH_E_SHAPE, "step kernel: the word table is Q6_K");
     if (c->info.n_attn > 0 && c->info.head_dim != 32 && c->info.head_dim != 64) return fail(SH_E_SHAPE, "step kernel: head_dim 32 or 64");
+    for (const layer_dev& L : c->layers)
+        for (const q4dev* t : {&L.in_proj, &L.out_proj, &L.qkvg, &L.o, &L.gate_up, &L.down})
+            if (t->mins) return fail(SH_E_SHAPE, "step kernel: Q4_1 tables");
     const sh_model_info& I = c->info;
     const int E = I.n_embd, Hq = I.n_head * I.head_dim;
     int dev_cus = 0;
@@ -644,7 +653,7 @@ int sh_load(sh_ctx* c, const char* path, int n_ctx) {
     size_t need = 0;
     for (auto& t : tables) {
         const size_t nb = (size_t)t.rows[0].first->ne[0] / 32;
-        need += (t.rows.size() * nb * 16 + 255) / 256 * 256 + (t.rows.size() * nb * 2 + 255) / 256 * 256;
+        need += (t.rows.size() * nb * 16 + 255) / 256 * 256 + 2 * ((t.rows.size() * nb * 2 + 255) / 256 * 256);   // + Q4_1 minima
     }
     if (q6) need += q6k_device_bytes(te);
     for (auto& v : vecs) need += ((size_t)v.second->nbytes + 255) / 256 * 256;
@@ -655,21 +664,25 @@ int sh_load(sh_ctx* c, const char* path, int n_ctx) {
     c->w.size = need;
     long long table_bytes = 0;
     std::vector<uint8_t> codes;
-    std::vector<uint16_t> scales;
+    std::vector<uint16_t> scales, mins;
     for (auto& t : tables) {
         int K = 0;
-        if (!repack_q4(t.rows, codes, scales, &K)) return fail(SH_E_SHAPE, "sh_load: a table is not Q4_0 with rows in multiples of 8");
+        if (!repack_q4(t.rows, codes, scales, mins, &K))
+            return fail(SH_E_SHAPE, "sh_load: a table is not all Q4_0 or all Q4_1 with rows in multiples of 8");
         void* dc = c->w.take(codes.size());
         void* ds = c->w.take(scales.size() * 2);
-        if (!dc || !ds) return fail(SH_E_NOMEM, "sh_load: arena overflow");
+        void* dm = mins.empty() ? nullptr : c->w.take(mins.size() * 2);
+        if (!dc || !ds || (!mins.empty() && !dm)) return fail(SH_E_NOMEM, "sh_load: arena overflow");
         HIPCHK(hipMemcpy(dc, codes.data(), codes.size(), hipMemcpyHostToDevice));
         HIPCHK(hipMemcpy(ds, scales.data(), scales.size() * 2, hipMemcpyHostToDevice));
+        if (dm) HIPCHK(hipMemcpy(dm, mins.data(), mins.size() * 2, hipMemcpyHostToDevice));
         t.dst->codes = dc;
         t.dst->scales = ds;
+        t.dst->mins = dm;
         t.dst->rows = (int)t.rows.size();
         t.dst->cols = K;
         t.dst->nb = K / 32;
-        table_bytes += (long long)(codes.size() + scales.size() * 2);
+        table_bytes += (long long)(codes.size() + scales.size() * 2 + mins.size() * 2);
     }
     if (q6) {
         repack_q6k(te, codes, scales);
@@ -1351,9 +1364,9 @@ int sh_q4_create(sh_ctx* c, const void* q4_0, int rows, int cols, sh_q4** out) {
     std::vector<std::pair<const gg_tensor*, int>> rr;
     for (int r = 0; r < rows; r++) rr.push_back({&t, r});
     std::vector<uint8_t> codes;
-    std::vector<uint16_t> scales;
+    std::vector<uint16_t> scales, mins;
     int K;
-    if (!repack_q4(rr, codes, scales, &K)) return fail(SH_E_SHAPE, "sh_q4_create: repack failed");
+    if (!repack_q4(rr, codes, scales, mins, &K)) return fail(SH_E_SHAPE, "sh_q4_create: repack failed");
     auto h = std::make_unique<sh_q4>();
     h->ctx = c;
     const size_t cb = (codes.size() + 255) / 256 * 256;

@@ -27,6 +27,7 @@ enum { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_CONV = 2, EPI_LOGITS = 3 };
 struct q4dev {
     const void* codes = nullptr;
     const void* scales = nullptr;
+    const void* mins = nullptr;    // Q4_1 tables: fp16 block minima, laid out as scales; null for Q4_0
     int rows = 0, cols = 0, nb = 0;
 };
 

@@ -38,6 +38,12 @@ __device__ __forceinline__ void q4_dequant_block(const q4dev& T, int row, int bl
     }
 }
 
+// half r (0..7) of a 16-byte word of 8 fp16 values, as float
+__device__ __forceinline__ float half_of(const u32x4& w, int r) {
+    const unsigned word = (r >> 1) == 0 ? w.x : (r >> 1) == 1 ? w.y : (r >> 1) == 2 ? w.z : w.w;
+    return h2f((uint16_t)((r & 1) ? (word >> 16) : (word & 0xFFFFu)));
+}
+
 // ---------------------------------------------------------------- Q4_0 GEMV
 // One wave per block; a unit is UG groups of 8 rows (R rows).
 // Phase 1, lanes over input blocks: lane j owns blocks j, j + 64, ... (< nb); it cuts them itself (int8 codes stay in
@@ -47,6 +53,8 @@ __device__ __forceinline__ void q4_dequant_block(const q4dev& T, int row, int bl
 // (imi/core/tables.cpp:127-143): acc = fma(float(isum), d * dx, acc), cor = fma(d, s, cor), out = acc - 8 cor
 // (q4x8, imi/kernels/q4x8.cpp:51-77: cor = fma(d, corr, cor), out = acc - cor) -- the same fp32 operations in the
 // same order as the CPU, so the outputs are the CPU's bit for bit.
+template <int PRO> constexpr bool norm_staging() { return PRO == PRO_EMBED_NORM || PRO == PRO_RESID_NORM; }
+
 template <int M, int NBL, int PRO, int EPI, int UG>
 __global__ __launch_bounds__(64) void k_gemv(gemv_args a) {
     constexpr int R = 8 * UG;
@@ -60,6 +68,8 @@ __global__ __launch_bounds__(64) void k_gemv(gemv_args a) {
     float* l_dx = l_d + (size_t)nb * LDD;          // [M][nb]
     float* l_s = l_dx + (size_t)M * nb;            // [M][nb]
     float* l_x = l_s + (size_t)M * nb;             // [E] staging for the norms
+    float* l_m = l_x + (norm_staging<PRO>() ? a.E : 0);   // [nb][LDD] Q4_1 block minima (a.W.mins set)
+    const bool hm = a.W.mins != nullptr;
     int xq[M][NBL][8];
 
     // ---- prologue: the input of this table, cut to int8 per 32 ----
@@ -150,7 +160,7 @@ __global__ __launch_bounds__(64) void k_gemv(gemv_args a) {
 #pragma unroll
         for (int gi = 0; gi < UG; gi++) {
             const int g = u * UG + gi;
-            u32x4 c[8][NBL], s8[NBL];
+            u32x4 c[8][NBL], s8[NBL], m8[NBL];
 #pragma unroll
             for (int b = 0; b < NBL; b++) {
                 const int blk = lane + 64 * b;
@@ -158,6 +168,8 @@ __global__ __launch_bounds__(64) void k_gemv(gemv_args a) {
 #pragma unroll
                     for (int r = 0; r < 8; r++) c[r][b] = __builtin_nontemporal_load(codes + (size_t)(8 * g + r) * nb + blk);
                     s8[b] = __builtin_nontemporal_load(scales + (size_t)g * nb + blk);
+                    // (issued on every path, so the compiler's wait counts stay exact; Q4_0 re-reads the scales)
+                    m8[b] = __builtin_nontemporal_load((const u32x4*)(hm ? a.W.mins : a.W.scales) + (size_t)g * nb + blk);
                 }
             }
 #pragma unroll
@@ -168,6 +180,7 @@ __global__ __launch_bounds__(64) void k_gemv(gemv_args a) {
                     for (int r = 0; r < 8; r++) {
                         const unsigned sw = (r < 2) ? s8[b].x : (r < 4) ? s8[b].y : (r < 6) ? s8[b].z : s8[b].w;
                         l_d[blk * LDD + gi * 8 + r] = h2f((uint16_t)((r & 1) ? (sw >> 16) : (sw & 0xFFFFu)));
+                        if (hm) l_m[blk * LDD + gi * 8 + r] = half_of(m8[b], r);
 #pragma unroll
                         for (int m = 0; m < M; m++) l_isum[blk * LDI + m * R + gi * 8 + r] = q4_block_dot(c[r][b], xq[m][b]);
                     }
@@ -186,9 +199,9 @@ __global__ __launch_bounds__(64) void k_gemv(gemv_args a) {
             for (int j = 0; j < nb; j++) {
                 const float d = l_d[j * LDD + k];
                 acc = fmaf((float)l_isum[j * LDI + lane], d * dx[j], acc);
-                cor = fmaf(d, sv[j], cor);
+                cor = fmaf(hm ? l_m[j * LDD + k] : d, sv[j], cor);   // Q4_1: the block minimum
             }
-            outv = PRO == PRO_CUT_HALF_AWAY ? acc - cor : fmaf(-8.0f, cor, acc);
+            outv = PRO == PRO_CUT_HALF_AWAY ? acc - cor : hm ? acc + cor : fmaf(-8.0f, cor, acc);
         }
         __syncthreads();
         // ---- epilogue: lane (m, k) holds row k of the unit for input m ----
@@ -249,7 +262,9 @@ __global__ __launch_bounds__(64) void k_gemv(gemv_args a) {
 //    cor = fma(d, s, cor), the same instruction stream for both (operands through per-lane row pointers), four
 //    blocks per 16-byte LDS read with later reads in flight; out = fma(-8, cor, acc), or acc - cor with q4x8's
 //    corr = 8 d sum (imi/kernels/q4x8.cpp:45-77).
-template <int M, bool HALF, int NB>
+// HM: the table is Q4_1 (imi/core/tables.cpp:127-143 with HAS_M): the correction chain takes the block minimum m in
+// place of d and the row ends as acc + cor
+template <int M, bool HALF, int NB, bool HM = false>
 __global__ __launch_bounds__(256) void k_gemv_cut(gemv_args a) {
     constexpr int TPB = 256 / NB, VPT = 32 / TPB, RPT = NB / 32, ST = NB + 4;
     extern __shared__ __align__(16) float lds[];
@@ -276,6 +291,8 @@ __global__ __launch_bounds__(256) void k_gemv_cut(gemv_args a) {
 #pragma unroll
     for (int k = 0; k < RPT; k++) c[k] = __builtin_nontemporal_load(codes + (size_t)k * NB);
     const u32x4 s8 = __builtin_nontemporal_load((const u32x4*)a.W.scales + (size_t)g * NB + jw);
+    u32x4 m8 = s8;
+    if (HM) m8 = __builtin_nontemporal_load((const u32x4*)a.W.mins + (size_t)g * NB + jw);
     // the cut of block jc by its TPB threads
 #pragma unroll
     for (int m = 0; m < M; m++) {
@@ -321,7 +338,7 @@ __global__ __launch_bounds__(256) void k_gemv_cut(gemv_args a) {
             const int r = sub * RPT + k;
             const unsigned word = RPT == 8 ? sw[k >> 1] : (r >> 1) == 0 ? sw[0] : (r >> 1) == 1 ? sw[1] : (r >> 1) == 2 ? sw[2] : sw[3];
             d[k] = h2f((uint16_t)((r & 1) ? (word >> 16) : (word & 0xFFFFu)));
-            l_dd[r * ST + jw] = d[k];
+            l_dd[r * ST + jw] = HM ? half_of(m8, r) : d[k];
         }
 #pragma unroll
         for (int m = 0; m < M; m++) {
@@ -363,7 +380,7 @@ __global__ __launch_bounds__(256) void k_gemv_cut(gemv_args a) {
     const float cor = __shfl(chain, (lane + 8 * M) & 63);
     if (acc_lane) {
         const int m = lane >> 3, r = lane & 7;
-        a.out[(size_t)m * a.out_ld + 8 * g + r] = HALF ? chain - cor : fmaf(-8.0f, cor, chain);
+        a.out[(size_t)m * a.out_ld + 8 * g + r] = HALF ? chain - cor : HM ? chain + cor : fmaf(-8.0f, cor, chain);
     }
 }
 
@@ -406,7 +423,7 @@ __device__ __forceinline__ void put_xt(float* xt, int t, const f32x4& v) {
     p[3 * XLD] = v.w;
 }
 
-template <int M, int EPI, int UG>
+template <int M, int EPI, int UG, bool HM = false>   // HM: Q4_1 table, as k_gemv_cut
 __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
     extern __shared__ __align__(16) float lds[];
     const int E = a.E, nb = a.W.nb, st = ((nb + 3) & ~3) + 4;
@@ -430,15 +447,17 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
     const int np = G * nb, rpt = np <= 64 ? 1 : np <= 128 ? 2 : np <= 256 ? 4 : 8;
     const bool wt = t < np * (8 / rpt);
     const int sub = t / np, pr = t - sub * np, gi = pr / nb, jw = pr - gi * nb;
-    u32x4 w[9];
-    // all 9 loads are issued on every path (rows past this thread's share and absent groups re-read a row it owns,
-    // which the caches serve), so the compiler counts them exactly and the prologue waits only for its own inputs
+    u32x4 w[HM ? 10 : 9];
+    // all 9 (Q4_1: 10) loads are issued on every path (rows past this thread's share and absent groups re-read a row
+    // it owns, which the caches serve), so the compiler counts them exactly and the prologue waits only for its own
+    // inputs
     auto load_chunk = [&](int k) {
         const int g = min(k * G + (wt ? gi : 0), gtot - 1), s0 = wt ? sub * rpt : 0;
         const u32x4* cp = (const u32x4*)a.W.codes + (size_t)(8 * g + s0) * nb + jw;
 #pragma unroll
         for (int r = 0; r < 8; r++) w[r] = __builtin_nontemporal_load(cp + (size_t)(r < rpt ? r : 0) * nb);
         w[8] = __builtin_nontemporal_load((const u32x4*)a.W.scales + (size_t)g * nb + jw);
+        if (HM) w[HM ? 9 : 8] = __builtin_nontemporal_load((const u32x4*)a.W.mins + (size_t)g * nb + jw);
     };
     // ---- prologue: its inputs are requested first (a wave's loads complete in order, so the norm work can start
     // while the weights that follow are still streaming in) ----
@@ -553,7 +572,7 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
             const int r0 = 8 * gi + sub * rpt;
 #pragma unroll
             for (int r = 0; r < 8; r++)
-                if (r < rpt) l_dd[(r0 + r) * st + jw] = d[r];
+                if (r < rpt) l_dd[(r0 + r) * st + jw] = HM ? half_of(w[HM ? 9 : 8], (sub * rpt + r) & 7) : d[r];
 #pragma unroll
             for (int m = 0; m < M; m++) {
                 const u32x4* xs = (const u32x4*)(l_xq + (m * nb + jw) * 8);
@@ -602,7 +621,7 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
             if (cor_lane) l_cor[c] = chain;
         }
         __syncthreads();
-        if (acc_lane) l_out[c] = fmaf(-8.0f, l_cor[c], chain);
+        if (acc_lane) l_out[c] = HM ? chain + l_cor[c] : fmaf(-8.0f, l_cor[c], chain);
         __syncthreads();
         // ---- epilogue: thread c < C holds row r of the chunk for input m ----
         if (t < C) {
@@ -904,7 +923,7 @@ static size_t scores_q6k_lds(int M, int E) {
 // dynamic LDS bytes of a k_gemv instantiation
 static size_t gemv_lds(int M, int UG, int nb, int E, bool norm) {
     const int R = 8 * UG;
-    return sizeof(float) * ((size_t)nb * (M * R + 1) + (size_t)nb * (R + 1) + 2 * (size_t)M * nb + (norm ? (size_t)E : 0));
+    return sizeof(float) * ((size_t)nb * (M * R + 1) + 2 * (size_t)nb * (R + 1) + 2 * (size_t)M * nb + (norm ? (size_t)E : 0));
 }
 
 // ---------------------------------------------------------------- GQA decode attention
@@ -1442,7 +1461,8 @@ hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hi
         b.upw = epi == EPI_LOGITS ? 8 : (want < 1 ? 1 : want > cap ? cap : want);
         const int nchunk = (a.units + b.upw - 1) / b.upw;
         const void* fn = nullptr;
-#define SH_NORM_FN(M_, EPI_, UG_) if (M == M_ && epi == EPI_) fn = (const void*)k_gemv_norm<M_, EPI_, UG_>;
+        const bool hm = a.W.mins != nullptr;
+#define SH_NORM_FN(M_, EPI_, UG_) if (M == M_ && epi == EPI_) fn = hm ? (const void*)k_gemv_norm<M_, EPI_, UG_, true> : (const void*)k_gemv_norm<M_, EPI_, UG_>;
         SH_NORM_FN(1, EPI_STORE, 1) SH_NORM_FN(1, EPI_SWIGLU, 2) SH_NORM_FN(1, EPI_CONV, 3) SH_NORM_FN(1, EPI_LOGITS, 1)
         SH_NORM_FN(2, EPI_STORE, 1) SH_NORM_FN(2, EPI_SWIGLU, 2) SH_NORM_FN(2, EPI_CONV, 3) SH_NORM_FN(2, EPI_LOGITS, 1)
 #undef SH_NORM_FN
@@ -1462,13 +1482,20 @@ hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hi
     const int nb = a.W.nb;
     if (epi == EPI_STORE && (pro == PRO_CUT || pro == PRO_CUT_HALF_AWAY) && (nb == 64 || nb == 128 || nb == 256) &&
         a.W.rows % 8 == 0 && (M == 1 || (M == 2 && pro == PRO_CUT))) {
-        const bool half = pro == PRO_CUT_HALF_AWAY;
+        const bool half = pro == PRO_CUT_HALF_AWAY, hm = a.W.mins != nullptr;
+        if (half && hm) return hipErrorInvalidValue;   // q4x8's cut is for Q4_0 tables only
         const void* fn = nullptr;
 #define SH_CUT_FN(M_, H_, NB_) if (M == M_ && half == H_ && nb == NB_) fn = (const void*)k_gemv_cut<M_, H_, NB_>;
-        SH_CUT_FN(1, false, 64) SH_CUT_FN(1, false, 128) SH_CUT_FN(1, false, 256)
-        SH_CUT_FN(1, true, 64) SH_CUT_FN(1, true, 128) SH_CUT_FN(1, true, 256)
-        SH_CUT_FN(2, false, 64) SH_CUT_FN(2, false, 128) SH_CUT_FN(2, false, 256)
+#define SH_CUT_FN1(M_, NB_) if (M == M_ && nb == NB_) fn = (const void*)k_gemv_cut<M_, false, NB_, true>;
+        if (hm) {
+            SH_CUT_FN1(1, 64) SH_CUT_FN1(1, 128) SH_CUT_FN1(1, 256) SH_CUT_FN1(2, 64) SH_CUT_FN1(2, 128) SH_CUT_FN1(2, 256)
+        } else {
+            SH_CUT_FN(1, false, 64) SH_CUT_FN(1, false, 128) SH_CUT_FN(1, false, 256)
+            SH_CUT_FN(1, true, 64) SH_CUT_FN(1, true, 128) SH_CUT_FN(1, true, 256)
+            SH_CUT_FN(2, false, 64) SH_CUT_FN(2, false, 128) SH_CUT_FN(2, false, 256)
+        }
 #undef SH_CUT_FN
+#undef SH_CUT_FN1
         void* args[] = {const_cast<gemv_args*>(&a)};
         const dim3 gr(a.W.rows / 8), bl(256);
         const size_t lds = gemv_cut_lds(M, nb);

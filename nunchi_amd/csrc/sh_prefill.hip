@@ -109,8 +109,9 @@ __global__ __launch_bounds__(256) void k_pf_cut(pf_cutk_args a) {
 // the result's lane l holds rows 4 (l / 16) + i (i < 4) at position l % 16. The weight codes enter as they are
 // stored (0..15), the input as its int8 cut, so each product is imi's integer block sum exactly; then per (row,
 // position), block by block in order: acc = fma(float(isum), d * dx, acc), cor = fma(d, s, cor), and at the end
-// out = fma(-8, cor, acc) (imi/core/tables.cpp:419-454, the batch kernel imi's prefill uses).
-template <int EPI>
+// out = fma(-8, cor, acc) (imi/core/tables.cpp:419-454, the batch kernel imi's prefill uses); Q4_1 tables take the
+// block minimum m in the cor chain and end as acc + cor.
+template <int EPI, bool HM>
 __global__ __launch_bounds__(256) void k_pf_gemm(pf_gemm_args a) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int li = lane & 15, lq = lane >> 4;
@@ -119,14 +120,17 @@ __global__ __launch_bounds__(256) void k_pf_gemm(pf_gemm_args a) {
     if (rbase >= rows || pbase >= n) return;   // whole waves; no barriers below
     const uint8_t* codes = static_cast<const uint8_t*>(a.W.codes);
     const uint16_t* scales = static_cast<const uint16_t*>(a.W.scales);
+    const uint16_t* mins = static_cast<const uint16_t*>(a.W.mins);
     const uint8_t* ap[2];
     const uint16_t* dp[2];
+    const uint16_t* mp[2];
 #pragma unroll
     for (int mt = 0; mt < 2; mt++) {
         const int r = min(rbase + 16 * mt + li, rows - 1);              // operand row (clamped: results dropped)
         ap[mt] = codes + (size_t)r * nb * 16 + (lq & 1) * 8;            // bytes 0-7 or 8-15 of the row's block
         const int rd = min(rbase + 16 * mt + 4 * lq, rows - 4);         // first of the 4 result rows
         dp[mt] = scales + (size_t)(rd >> 3) * nb * 8 + (rd & 7);
+        mp[mt] = HM ? mins + (size_t)(rd >> 3) * nb * 8 + (rd & 7) : dp[mt];
     }
     const int shift = (lq >> 1) * 4;   // columns 0-15: low nibbles, 16-31: high nibbles
     int pp[2];
@@ -142,7 +146,7 @@ __global__ __launch_bounds__(256) void k_pf_gemm(pf_gemm_args a) {
             for (int i = 0; i < 4; i++) { acc[mt][nt][i] = 0.0f; cor[mt][nt][i] = 0.0f; }
 
     // operands of block j, fetched one block ahead
-    uint2 ra[2], rs[2];
+    uint2 ra[2], rs[2], rm[2];
     long rb[2];
     float fx[2], fs[2];
     auto fetch = [&](int j) {
@@ -150,6 +154,7 @@ __global__ __launch_bounds__(256) void k_pf_gemm(pf_gemm_args a) {
         for (int mt = 0; mt < 2; mt++) {
             ra[mt] = *reinterpret_cast<const uint2*>(ap[mt] + (size_t)j * 16);
             rs[mt] = *reinterpret_cast<const uint2*>(dp[mt] + (size_t)j * 8);
+            if (HM) rm[mt] = *reinterpret_cast<const uint2*>(mp[mt] + (size_t)j * 8);
         }
 #pragma unroll
         for (int nt = 0; nt < 2; nt++) {
@@ -161,7 +166,7 @@ __global__ __launch_bounds__(256) void k_pf_gemm(pf_gemm_args a) {
     };
     fetch(0);
     for (int j = 0; j < nb; j++) {
-        const uint2 ca[2] = {ra[0], ra[1]}, cs[2] = {rs[0], rs[1]};
+        const uint2 ca[2] = {ra[0], ra[1]}, cs[2] = {rs[0], rs[1]}, cm[2] = {HM ? rm[0] : rs[0], HM ? rm[1] : rs[1]};
         const long cb[2] = {rb[0], rb[1]};
         const float cx[2] = {fx[0], fx[1]}, cz[2] = {fs[0], fs[1]};
         if (j + 1 < nb) fetch(j + 1);
@@ -178,12 +183,14 @@ __global__ __launch_bounds__(256) void k_pf_gemm(pf_gemm_args a) {
         for (int mt = 0; mt < 2; mt++) {
             const float dd[4] = {h2f((uint16_t)(cs[mt].x & 0xFFFFu)), h2f((uint16_t)(cs[mt].x >> 16)),
                                  h2f((uint16_t)(cs[mt].y & 0xFFFFu)), h2f((uint16_t)(cs[mt].y >> 16))};
+            const float mm[4] = {h2f((uint16_t)(cm[mt].x & 0xFFFFu)), h2f((uint16_t)(cm[mt].x >> 16)),
+                                 h2f((uint16_t)(cm[mt].y & 0xFFFFu)), h2f((uint16_t)(cm[mt].y >> 16))};
 #pragma unroll
             for (int nt = 0; nt < 2; nt++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     acc[mt][nt][i] = fmaf((float)isum[mt][nt][i], dd[i] * cx[nt], acc[mt][nt][i]);
-                    cor[mt][nt][i] = fmaf(dd[i], cz[nt], cor[mt][nt][i]);
+                    cor[mt][nt][i] = fmaf(mm[i], cz[nt], cor[mt][nt][i]);
                 }
         }
     }
@@ -194,7 +201,7 @@ __global__ __launch_bounds__(256) void k_pf_gemm(pf_gemm_args a) {
             const int p = pbase + 16 * nt + li, r0 = rbase + 16 * mt + 4 * lq;
             float v[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) v[i] = fmaf(-8.0f, cor[mt][nt][i], acc[mt][nt][i]);
+            for (int i = 0; i < 4; i++) v[i] = HM ? acc[mt][nt][i] + cor[mt][nt][i] : fmaf(-8.0f, cor[mt][nt][i], acc[mt][nt][i]);
             if (EPI == EPI_SWIGLU) {
                 // rows 0-7 of the 16-row tile are a gate group, rows 8-15 the matching up group (lanes + 32)
                 float up[4];
@@ -373,10 +380,15 @@ hipError_t launch_pf_rows(int mode, const pf_rows_args& a, hipStream_t s) {
 hipError_t launch_pf_gemm(int epi, const pf_gemm_args& a, hipStream_t s) {
     if (a.n < 1 || a.W.rows % 8 || (epi == EPI_SWIGLU && a.W.rows % 16)) return hipErrorInvalidValue;
     const dim3 grid((a.W.rows + 63) / 64, (a.n + 63) / 64);
-    if (epi == EPI_SWIGLU)
-        hipLaunchKernelGGL(k_pf_gemm<EPI_SWIGLU>, grid, dim3(256), 0, s, a);
+    const bool hm = a.W.mins != nullptr;   // Q4_1 table
+    if (epi == EPI_SWIGLU && hm)
+        hipLaunchKernelGGL((k_pf_gemm<EPI_SWIGLU, true>), grid, dim3(256), 0, s, a);
+    else if (epi == EPI_SWIGLU)
+        hipLaunchKernelGGL((k_pf_gemm<EPI_SWIGLU, false>), grid, dim3(256), 0, s, a);
+    else if (epi == EPI_STORE && hm)
+        hipLaunchKernelGGL((k_pf_gemm<EPI_STORE, true>), grid, dim3(256), 0, s, a);
     else if (epi == EPI_STORE)
-        hipLaunchKernelGGL(k_pf_gemm<EPI_STORE>, grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((k_pf_gemm<EPI_STORE, false>), grid, dim3(256), 0, s, a);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

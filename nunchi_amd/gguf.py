@@ -12,7 +12,7 @@ from dataclasses import dataclass, field
 import numpy as np
 
 GGUF_MAGIC = 0x46554747  # "GGUF" little-endian
-T_F32, T_F16, T_Q4_0, T_Q8_0, T_Q6_K = 0, 1, 2, 8, 14
+T_F32, T_F16, T_Q4_0, T_Q4_1, T_Q8_0, T_Q6_K = 0, 1, 2, 3, 8, 14
 
 # value types of GGUF key/value pairs
 V_U8, V_I8, V_U16, V_I16, V_U32, V_I32, V_F32, V_BOOL, V_STR, V_ARR, V_U64, V_I64, V_F64 = range(13)
@@ -20,6 +20,7 @@ _SCALAR = {V_U8: "<B", V_I8: "<b", V_U16: "<H", V_I16: "<h", V_U32: "<I", V_I32:
            V_U64: "<Q", V_I64: "<q", V_F64: "<d"}
 
 Q4_0_BLOCK = np.dtype([("d", "<f2"), ("qs", "u1", 16)])   # 18 bytes per 32 weights
+Q4_1_BLOCK = np.dtype([("d", "<f2"), ("m", "<f2"), ("qs", "u1", 16)])   # 20 bytes: weight = code * d + m
 Q8_0_BLOCK = np.dtype([("d", "<f2"), ("qs", "i1", 32)])   # 34 bytes per 32 weights
 # 210 bytes per 256 weights: low 4 bits, high 2 bits, 16 int8 scales (one per 16 values), fp16 d
 Q6_K_BLOCK = np.dtype([("ql", "u1", 128), ("qh", "u1", 64), ("scales", "i1", 16), ("d", "<f2")])
@@ -32,6 +33,8 @@ def row_bytes(gtype: int, ne0: int) -> int:
         return 2 * ne0
     if gtype == T_Q4_0:
         return ne0 // 32 * 18
+    if gtype == T_Q4_1:
+        return ne0 // 32 * 20
     if gtype == T_Q8_0:
         return ne0 // 32 * 34
     if gtype == T_Q6_K:

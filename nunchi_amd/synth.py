@@ -18,7 +18,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from .gguf import GGUFWriter, Q4_0_BLOCK, Q6_K_BLOCK, Q8_0_BLOCK, T_F32, T_Q4_0, T_Q6_K, T_Q8_0
+from .gguf import GGUFWriter, Q4_0_BLOCK, Q4_1_BLOCK, Q6_K_BLOCK, Q8_0_BLOCK, T_F32, T_Q4_0, T_Q4_1, T_Q6_K, T_Q8_0
 
 
 @dataclass
@@ -40,6 +40,7 @@ class BrainShape:
     sliding_window: int = 0                       # window of the layers in swa_layers (0: none)
     swa_layers: tuple = ()                        # attention layers with the window and the swa RoPE base
     rope_base_swa: float = 1e4
+    layer_type: str = "q4_0"                      # layer tables: "q4_0", or "q4_1" (code * d + m)
 
 
 SEOUL = BrainShape()
@@ -78,6 +79,18 @@ def q4_0_random(rng: np.random.Generator, rows: int, cols: int) -> np.ndarray:
     nb = rows * (cols // 32)
     blk = np.empty(nb, dtype=Q4_0_BLOCK)
     blk["d"] = (np.abs(rng.standard_normal(nb, dtype=np.float32) * np.float32(0.02)) / np.float32(8)).astype(np.float16)
+    blk["qs"] = np.frombuffer(rng.bytes(nb * 16), dtype=np.uint8).reshape(nb, 16)
+    return blk
+
+
+def q4_1_random(rng: np.random.Generator, rows: int, cols: int) -> np.ndarray:
+    """[rows][cols/32] Q4_1 blocks: d = fp16(|N(0,0.02)|/8), m = fp16(-(8 + N(0,1)) d) (near Q4_0's centring),
+    16 random bytes of codes."""
+    nb = rows * (cols // 32)
+    blk = np.empty(nb, dtype=Q4_1_BLOCK)
+    d = (np.abs(rng.standard_normal(nb, dtype=np.float32) * np.float32(0.02)) / np.float32(8)).astype(np.float16)
+    blk["d"] = d
+    blk["m"] = (-(np.float32(8) + rng.standard_normal(nb, dtype=np.float32)) * d.astype(np.float32)).astype(np.float16)
     blk["qs"] = np.frombuffer(rng.bytes(nb * 16), dtype=np.uint8).reshape(nb, 16)
     return blk
 
@@ -125,7 +138,10 @@ def write_brain(path: str, shape: BrainShape = SEOUL, seed: int = 0) -> str:
     w.add_u32("lfm3.feed_forward_length", s.n_ff)
 
     def q4(name, rows, cols):
-        w.add_tensor(name, T_Q4_0, (cols, rows), q4_0_random(_rng(seed, name), rows, cols))
+        if s.layer_type == "q4_1" and name != "token_embd.weight":
+            w.add_tensor(name, T_Q4_1, (cols, rows), q4_1_random(_rng(seed, name), rows, cols))
+        else:
+            w.add_tensor(name, T_Q4_0, (cols, rows), q4_0_random(_rng(seed, name), rows, cols))
 
     def f32(name, arr, ne):
         w.add_tensor(name, T_F32, ne, np.ascontiguousarray(arr, dtype=np.float32))

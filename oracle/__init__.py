@@ -62,7 +62,7 @@ def lib():
         "orc_cut32": (f, [_f32p, _i8p, C.POINTER(C.c_int)]),
         "orc_cut": (None, [_f32p, i, _i8p, _f32p, _f32p]),
         "orc_q4_layout": (None, [_u8p, i, i, _u8p, _u16p]),
-        "orc_q4_create": (vp, [_u8p, i, i, i]),
+        "orc_q4_create": (vp, [_u8p, i, i, i, i]),
         "orc_q4_free": (None, [vp]),
         "orc_q4_gemv": (d, [vp, _f32p, i, _f32p, i, i]),
         "orc_q4_gemv_batch": (None, [vp, _f32p, i, _f32p]),
@@ -197,12 +197,12 @@ class State:
 
 
 class Q4Table:
-    """A Q4_0 matrix in imi's 8-row layout with imi's GEMV (cut + group / group2 / group_batch)."""
+    """A Q4_0 (or, with q4_1, Q4_1) matrix in imi's 8-row layout with imi's GEMV (cut + group / group2 / group_batch)."""
 
-    def __init__(self, q4_0: np.ndarray, rows: int, cols: int, threads: int = 1):
+    def __init__(self, q4_0: np.ndarray, rows: int, cols: int, threads: int = 1, q4_1: bool = False):
         self.raw = np.ascontiguousarray(q4_0).view(np.uint8).reshape(-1)
         self.rows, self.cols = rows, cols
-        self.h = lib().orc_q4_create(self.raw, rows, cols, threads)
+        self.h = lib().orc_q4_create(self.raw, rows, cols, threads, int(q4_1))
 
     def __del__(self):
         if getattr(self, "h", None):

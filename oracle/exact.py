@@ -9,7 +9,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from nunchi_amd.gguf import GGUFFile, Q4_0_BLOCK, Q8_0_BLOCK, T_F16, T_F32, T_Q4_0, T_Q8_0
+from nunchi_amd.gguf import GGUFFile, Q4_0_BLOCK, Q4_1_BLOCK, Q8_0_BLOCK, T_F16, T_F32, T_Q4_0, T_Q4_1, T_Q8_0
 
 
 def dequant_q4_0(raw: np.ndarray, rows: int, cols: int) -> np.ndarray:
@@ -18,6 +18,14 @@ def dequant_q4_0(raw: np.ndarray, rows: int, cols: int) -> np.ndarray:
     qs = b["qs"].astype(np.int64)
     codes = np.concatenate([qs & 15, qs >> 4], axis=-1) - 8              # [rows][nb][32]
     return (codes * b["d"].astype(np.float64)[..., None]).reshape(rows, cols)
+
+
+def dequant_q4_1(raw: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """Q4_1: weight i of a block = code_i * d + m, codes 0..15 as in Q4_0 (imi/core/tables.cpp:62, 138-142)."""
+    b = np.frombuffer(np.ascontiguousarray(raw).tobytes(), dtype=Q4_1_BLOCK).reshape(rows, cols // 32)
+    qs = b["qs"].astype(np.int64)
+    codes = np.concatenate([qs & 15, qs >> 4], axis=-1)
+    return (codes * b["d"].astype(np.float64)[..., None] + b["m"].astype(np.float64)[..., None]).reshape(rows, cols)
 
 
 def dequant_q8_0(raw: np.ndarray, rows: int, cols: int) -> np.ndarray:
@@ -42,6 +50,8 @@ class Weights:
         cols, rows = t.ne[0], t.rows
         if t.gtype == T_Q4_0:
             w = dequant_q4_0(t.data, rows, cols)
+        elif t.gtype == T_Q4_1:
+            w = dequant_q4_1(t.data, rows, cols)
         elif t.gtype == T_Q8_0:
             w = dequant_q8_0(t.data, rows, cols)
         elif t.gtype == T_F32:

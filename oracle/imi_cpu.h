@@ -48,11 +48,14 @@ struct gfile {
 // low nibble, 16+4t..16+4t+3 high nibble), then fp16 scales [group][block][8]
 struct q4tab {
     int rows = 0, cols = 0, nb = 0;
+    bool has_m = false;            // Q4_1: weight = code * d + m (imi/core/tables.cpp:62,78-83)
     std::vector<uint8_t> codes;    // [rows/8][nb][128]
     std::vector<uint16_t> d;       // [rows/8][nb][8]
+    std::vector<uint16_t> m;       // [rows/8][nb][8] (Q4_1 only)
 };
-// rows given as pointers to Q4_0 rows (nb blocks of 18 B each); rows.size() % 8 == 0
-bool q4_build(q4tab& t, const std::vector<const uint8_t*>& rows, int cols);
+// rows given as pointers to Q4_0 rows (nb blocks of 18 B: d, 16 B of nibbles) or, with q4_1, Q4_1 rows (20 B: d, m,
+// 16 B of nibbles); rows.size() % 8 == 0
+bool q4_build(q4tab& t, const std::vector<const uint8_t*>& rows, int cols, bool q4_1 = false);
 int  q4_code_at(const uint8_t* blk128, int r, int k);   // imi/core/tables.cpp:167-169
 
 // ---- activation cut to int8 per 32 (imi/core/vec.h:47-75) ----

@@ -263,10 +263,14 @@ bool engine::load(const std::string& path, int threads, int ctx_len) {
         if (!t) { fprintf(stderr, "oracle: missing tensor %s\n", n.c_str()); }
         return t;
     };
+    // a table's stacked parts are all Q4_0 or all Q4_1 (imi/core/tables.cpp:70-72)
     auto whole = [&](q4tab& dst, std::vector<const gtensor*> parts) {
         std::vector<const uint8_t*> o;
-        for (auto* p : parts) { if (!p || p->type != T_Q4_0) return false; rows_of(o, p, 0, (int)p->ne[1]); }
-        return q4_build(dst, o, (int)parts[0]->ne[0]);
+        for (auto* p : parts) {
+            if (!p || (p->type != T_Q4_0 && p->type != T_Q4_1) || p->type != parts[0]->type) return false;
+            rows_of(o, p, 0, (int)p->ne[1]);
+        }
+        return q4_build(dst, o, (int)parts[0]->ne[0], parts[0]->type == T_Q4_1);
     };
     int n_attn = 0;
     layers.resize(n_layer);
@@ -302,7 +306,8 @@ bool engine::load(const std::string& path, int threads, int ctx_len) {
         n_ff = (int)fg->ne[1];
         std::vector<const uint8_t*> o;   // gate and up interleaved by 8-row group (seoul.cpp:155-160)
         for (int t = 0; t < n_ff; t += 8) { rows_of(o, fg, t, 8); rows_of(o, fu, t, 8); }
-        ok &= q4_build(L.gate_up, o, (int)fg->ne[0]);
+        ok &= (fg->type == T_Q4_0 || fg->type == T_Q4_1) && fu->type == fg->type &&
+              q4_build(L.gate_up, o, (int)fg->ne[0], fg->type == T_Q4_1);
         ok &= whole(L.down, {need(p + "ffn_down.weight")});
         if (!ok) { fprintf(stderr, "oracle: layer %d has a table the kernels do not read\n", il); return false; }
     }
@@ -1067,11 +1072,12 @@ void orc_q4_layout(const uint8_t* q4_0, int rows, int cols, uint8_t* codes, uint
     memcpy(codes, t.codes.data(), t.codes.size()); memcpy(d, t.d.data(), t.d.size() * 2);
 }
 struct q4h { q4tab t; team tm; };
-void* orc_q4_create(const uint8_t* q4_0, int rows, int cols, int threads) {
+// q4_1: the rows are Q4_1 (20-byte blocks)
+void* orc_q4_create(const uint8_t* q4, int rows, int cols, int threads, int q4_1) {
     auto* h = new q4h;
     std::vector<const uint8_t*> rr(rows);
-    for (int r = 0; r < rows; r++) rr[r] = q4_0 + (size_t)r * (cols / 32) * 18;
-    if (!q4_build(h->t, rr, cols)) { delete h; return nullptr; }
+    for (int r = 0; r < rows; r++) rr[r] = q4 + (size_t)r * (cols / 32) * (q4_1 ? 20 : 18);
+    if (!q4_build(h->t, rr, cols, q4_1 != 0)) { delete h; return nullptr; }
     h->tm.start(threads);
     return h;
 }

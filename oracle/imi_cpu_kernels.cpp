@@ -37,20 +37,22 @@ float h2f(uint16_t h) {
 uint16_t f2h(float f) { return (uint16_t)_cvtss_sh(f, 0); }
 
 // ---- 8-row 4-bit layout (imi/core/tables.cpp:67-97) ----
-bool q4_build(q4tab& t, const std::vector<const uint8_t*>& rows, int cols) {
+bool q4_build(q4tab& t, const std::vector<const uint8_t*>& rows, int cols, bool q4_1) {
     if (rows.empty() || rows.size() % 8 || cols % 32) return false;
-    t.rows = (int)rows.size(); t.cols = cols; t.nb = cols / 32;
-    const size_t ng = t.rows / 8;
+    t.rows = (int)rows.size(); t.cols = cols; t.nb = cols / 32; t.has_m = q4_1;
+    const size_t ng = t.rows / 8, bb = q4_1 ? 20 : 18;
     t.codes.assign(ng * t.nb * 128, 0);
     t.d.assign(ng * t.nb * 8, 0);
+    t.m.assign(q4_1 ? ng * t.nb * 8 : 0, 0);
     for (size_t g = 0; g < ng; g++)
         for (int j = 0; j < t.nb; j++) {
             uint8_t* c = &t.codes[(g * t.nb + j) * 128];
             for (int r = 0; r < 8; r++) {
-                const uint8_t* blk = rows[8 * g + r] + (size_t)j * 18;   // Q4_0 block: fp16 d, 16 B of nibbles
+                const uint8_t* blk = rows[8 * g + r] + (size_t)j * bb;   // fp16 d, (Q4_1: fp16 m,) 16 B of nibbles
                 uint16_t d; memcpy(&d, blk, 2);
                 t.d[(g * t.nb + j) * 8 + r] = d;
-                const uint8_t* qs = blk + 2;
+                if (q4_1) memcpy(&t.m[(g * t.nb + j) * 8 + r], blk + 2, 2);
+                const uint8_t* qs = blk + (q4_1 ? 4 : 2);
                 // file byte i holds column i (low nibble) and column 16+i (high nibble); ours keeps the byte and
                 // moves it to chunk i/4, position 4r + i%4
                 for (int i = 0; i < 16; i++) c[32 * (i / 4) + 4 * r + (i % 4)] = qs[i];
@@ -131,6 +133,14 @@ static inline __m256i block8(const uint8_t* c, const int8_t* xq) {
 }
 
 // imi/core/tables.cpp:127-143 (Q4_0): acc = fma(float(sum), d*dx, acc); cor = fma(d, s, cor); out = acc - 8*cor
+// the correction chain's per-row factor: d for Q4_0 (out = acc - 8 cor), m for Q4_1 (out = acc + cor)
+// (imi/core/tables.cpp:127-143)
+static inline __m256 cor_factor(const q4tab& W, const uint16_t* dp, size_t g, int j, __m256 d8) {
+    return W.has_m ? _mm256_cvtph_ps(_mm_loadu_si128((const __m128i*)(W.m.data() + (g * W.nb + j) * 8))) : d8;
+}
+static inline __m256 q4_finish(const q4tab& W, __m256 acc, __m256 cor) {
+    return W.has_m ? _mm256_add_ps(acc, cor) : _mm256_fnmadd_ps(_mm256_set1_ps(8.0f), cor, acc);
+}
 void q4_group(const q4tab& W, const q8in& X, int g, float* out) {
     const uint8_t* w = W.codes.data() + (size_t)g * W.nb * 128;
     const uint16_t* dp = W.d.data() + (size_t)g * W.nb * 8;
@@ -139,9 +149,9 @@ void q4_group(const q4tab& W, const q8in& X, int g, float* out) {
         const __m256i s = block8(w + (size_t)j * 128, &X.q[32 * j]);
         const __m256 d8 = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i*)(dp + 8 * j)));
         acc = _mm256_fmadd_ps(_mm256_cvtepi32_ps(s), _mm256_mul_ps(d8, _mm256_set1_ps(X.d[j])), acc);
-        cor = _mm256_fmadd_ps(d8, _mm256_set1_ps(X.s[j]), cor);
+        cor = _mm256_fmadd_ps(cor_factor(W, dp, g, j, d8), _mm256_set1_ps(X.s[j]), cor);
     }
-    _mm256_storeu_ps(out, _mm256_fnmadd_ps(_mm256_set1_ps(8.0f), cor, acc));
+    _mm256_storeu_ps(out, q4_finish(W, acc, cor));
 }
 // imi/core/tables.cpp:145-163: one code load, two inputs, each accumulated exactly as q4_group
 void q4_group2(const q4tab& W, const q8in& X, const q8in& X2, int g, float* out, float* out2) {
@@ -154,11 +164,12 @@ void q4_group2(const q4tab& W, const q8in& X, const q8in& X2, int g, float* out,
         const __m256 d8 = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i*)(dp + 8 * j)));
         a0 = _mm256_fmadd_ps(_mm256_cvtepi32_ps(s0), _mm256_mul_ps(d8, _mm256_set1_ps(X.d[j])), a0);
         a1 = _mm256_fmadd_ps(_mm256_cvtepi32_ps(s1), _mm256_mul_ps(d8, _mm256_set1_ps(X2.d[j])), a1);
-        c0 = _mm256_fmadd_ps(d8, _mm256_set1_ps(X.s[j]), c0);
-        c1 = _mm256_fmadd_ps(d8, _mm256_set1_ps(X2.s[j]), c1);
+        const __m256 mm = cor_factor(W, dp, g, j, d8);
+        c0 = _mm256_fmadd_ps(mm, _mm256_set1_ps(X.s[j]), c0);
+        c1 = _mm256_fmadd_ps(mm, _mm256_set1_ps(X2.s[j]), c1);
     }
-    _mm256_storeu_ps(out, _mm256_fnmadd_ps(_mm256_set1_ps(8.0f), c0, a0));
-    _mm256_storeu_ps(out2, _mm256_fnmadd_ps(_mm256_set1_ps(8.0f), c1, a1));
+    _mm256_storeu_ps(out, q4_finish(W, a0, c0));
+    _mm256_storeu_ps(out2, q4_finish(W, a1, c1));
 }
 // imi/core/tables.cpp:419-454: codes unpacked once per block, then every input
 void q4_group_batch(const q4tab& W, const q8b& X, int g, float* out) {
@@ -176,6 +187,7 @@ void q4_group_batch(const q4tab& W, const q8b& X, int g, float* out) {
             hi[t] = _mm256_and_si256(_mm256_srli_epi16(v, 4), nib);
         }
         const __m256 d8 = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i*)(dp + 8 * j)));
+        const __m256 m8 = cor_factor(W, dp, g, j, d8);
         const int8_t* xq = X.q.data() + (size_t)j * n * 32;
         const float* xd = X.d.data() + (size_t)j * n;
         const float* xs = X.s.data() + (size_t)j * n;
@@ -191,10 +203,10 @@ void q4_group_batch(const q4tab& W, const q8b& X, int g, float* out) {
             }
             const __m256i s = _mm256_madd_epi16(a, ones);
             acc[c] = _mm256_fmadd_ps(_mm256_cvtepi32_ps(s), _mm256_mul_ps(d8, _mm256_set1_ps(xd[c])), acc[c]);
-            cor[c] = _mm256_fmadd_ps(d8, _mm256_set1_ps(xs[c]), cor[c]);
+            cor[c] = _mm256_fmadd_ps(m8, _mm256_set1_ps(xs[c]), cor[c]);
         }
     }
-    for (int c = 0; c < n; c++) _mm256_storeu_ps(out + 8 * c, _mm256_fnmadd_ps(_mm256_set1_ps(8.0f), cor[c], acc[c]));
+    for (int c = 0; c < n; c++) _mm256_storeu_ps(out + 8 * c, q4_finish(W, acc[c], cor[c]));
 }
 // the same arithmetic one row at a time in plain C (pins the AVX2 lane bookkeeping above)
 void q4_group_scalar(const q4tab& W, const q8in& X, int g, float* out) {
@@ -205,10 +217,11 @@ void q4_group_scalar(const q4tab& W, const q8in& X, int g, float* out) {
             int s = 0;
             for (int k = 0; k < 32; k++) s += q4_code_at(c, r, k) * X.q[32 * j + k];
             const float dd = h2f(W.d[((size_t)g * W.nb + j) * 8 + r]);
+            const float mm = W.has_m ? h2f(W.m[((size_t)g * W.nb + j) * 8 + r]) : dd;
             acc = fmaf((float)s, dd * X.d[j], acc);
-            cor = fmaf(dd, X.s[j], cor);
+            cor = fmaf(mm, X.s[j], cor);
         }
-        out[r] = fmaf(-8.0f, cor, acc);
+        out[r] = W.has_m ? acc + cor : fmaf(-8.0f, cor, acc);
     }
 }
 void q4_block_sums(const q4tab& W, const q8in& X, int g, int32_t* sums) {

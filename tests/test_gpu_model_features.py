@@ -135,3 +135,46 @@ def test_head_dim_128_step2_and_prefill(wide_head_model):
         (ha, la, _), (hb, lb, _) = g.step2(int(toks[i]), None, True, gb, int(toks[-1 - i]), None, True)
         hoa, loa, hob, lob = o.step2(int(toks[i]), None, True, ob, int(toks[-1 - i]), None, True)
         assert same(ha, hoa) and same(hb, hob) and same(la, loa) and same(lb, lob), i
+
+
+@pytest.fixture(scope="module", params=["tiny", "mid"])
+def q4_1_model(request, model_dir):
+    """Every layer table Q4_1 (weight = code * d + m; imi/core/tables.cpp:62, 78-83, 127-143 with HAS_M)."""
+    from nunchi_amd import synth
+    base = synth.TINY if request.param == "tiny" else synth.BrainShape(n_layer=4, attn_layers=(1, 3), n_vocab=4096)
+    shape = synth.BrainShape(**{**base.__dict__, "layer_type": "q4_1"})
+    return synth.cached("brain", shape, 42, model_dir), shape
+
+
+def test_q4_1_tables_steps_greedy(q4_1_model, step_path):
+    import nunchi_amd
+    import oracle
+    path, shape = q4_1_model
+    g = nunchi_amd.Brain(path, n_ctx=96)
+    o = oracle.Engine(path, threads=4, n_ctx=96)
+    for i, t in enumerate(_prompt(10, shape.n_vocab, 43)):
+        hg, lg, bg = g.step(int(t))
+        ho, lo = o.step(int(t))
+        assert same(hg, ho) and same(lg, lo), i
+    ids_g, _ = g.generate(bg, 48)
+    ids_o, _ = o.greedy(bg, 48)
+    assert np.array_equal(ids_g, ids_o)
+
+
+def test_q4_1_tables_step2_and_prefill(q4_1_model):
+    import nunchi_amd
+    import oracle
+    path, shape = q4_1_model
+    g = nunchi_amd.Brain(path, n_ctx=160)
+    o = oracle.Engine(path, threads=4, n_ctx=160)
+    toks = _prompt(70, shape.n_vocab, 44)
+    hg, lg, bg, hall_g = g.step_batch(toks, hidden_all=True)
+    ho, lo, hall_o = o.step_batch(toks, hidden_all=True)
+    for p in range(len(toks)):
+        assert same(hall_g[p], hall_o[p]), p
+    assert same(lg, lo) and bg == oracle.top(lo)
+    gb, ob = g.new_state(), o.new_state()
+    for i in range(6):
+        (ha, la, _), (hb, lb, _) = g.step2(int(toks[i]), None, True, gb, int(toks[-1 - i]), None, True)
+        hoa, loa, hob, lob = o.step2(int(toks[i]), None, True, ob, int(toks[-1 - i]), None, True)
+        assert same(ha, hoa) and same(hb, hob) and same(la, loa) and same(lb, lob), i

@@ -111,3 +111,19 @@ def test_reset_and_context_full(tiny_model):
     e.reset()
     again = [e.step(t)[1] for t in (1, 2, 3, 4)]
     assert all(_same(x, y) for x, y in zip(first, again))
+
+
+def test_engine_q4_1_tables_vs_float64_truth(model_dir):
+    """Every layer table Q4_1: the restatement against the float64 model with the cuts applied. (Over longer runs an
+    int8 code eventually lands on the other side of a rounding boundary in one of the two arithmetics and the
+    positions after it differ at the cut's own scale, ~1e-3, for Q4_0 and Q4_1 models alike; these five positions
+    have no such flip, and a wrong m term would show at the first.)"""
+    from nunchi_amd import synth
+    shape = synth.BrainShape(**{**synth.TINY.__dict__, "layer_type": "q4_1"})
+    path = synth.cached("brain", shape, 41, model_dir)
+    toks = [5, 17, 300, 999, 0]
+    hid_c, lg_c = exact.brain(path, tokens=toks, cut=True)
+    e = oracle.Engine(path, threads=3, n_ctx=32)
+    for i, t in enumerate(toks):
+        h, lg = e.step(t)
+        assert rel(h, hid_c[i]) < 5e-6 and rel(lg, lg_c[i]) < 5e-6

@@ -291,3 +291,27 @@ def test_q6k_lanes_and_row():
     dd = b["d"].astype(np.float64).reshape(n_rows, nb) * d.astype(np.float64)[None]
     want = (dd * lanes.sum(axis=2)).sum(axis=1)
     assert np.allclose(out, want, rtol=1e-5, atol=1e-6 * np.abs(want).max())
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 512), (24, 2048)])
+def test_q4_1_gemv_float64_and_scalar_and_two_inputs(rows, cols):
+    """Q4_1 tables (imi/core/tables.cpp:127-143 with HAS_M): cor = fma(m, s, cor) and out = acc + cor. The AVX2
+    kernel equals the plain per-row chain, group2 equals two groups, group_batch equals n groups, and the result
+    equals sum over blocks of (code * d + m) . (q * dx) in float64."""
+    from nunchi_amd import synth
+    from oracle.exact import cut_dequant, dequant_q4_1
+    blk = synth.q4_1_random(np.random.default_rng(5 * rows + cols), rows, cols)
+    x = rng.standard_normal((2, cols)).astype(np.float32)
+    t = oracle.Q4Table(blk, rows, cols, threads=3, q4_1=True)
+    y0, _ = t.gemv(x[0])
+    ys, _ = t.gemv(x[0], scalar=True)
+    assert np.array_equal(y0, ys)
+    y2, _ = t.gemv(x)
+    assert np.array_equal(y2[0], y0) and np.array_equal(y2[1], t.gemv(x[1])[0])
+    assert np.array_equal(t.gemv_batch(x), y2)
+    ref = dequant_q4_1(blk, rows, cols) @ cut_dequant(x[0])
+    assert np.abs(y0 - ref).max() <= 1e-5 * np.sqrt((ref ** 2).mean())
+    # a Q4_0 reading of the same codes would differ: the m term is what the restatement adds
+    q0 = np.zeros(blk.shape, dtype=[("d", "<f2"), ("qs", "u1", 16)])
+    q0["d"], q0["qs"] = blk["d"], blk["qs"]
+    assert not np.allclose(oracle.Q4Table(q0, rows, cols).gemv(x[0])[0], y0)
