@@ -221,6 +221,152 @@ __global__ __launch_bounds__(256) void k_pf_gemm(pf_gemm_args a) {
         }
 }
 
+// LDS-staged form of the same product (taken when nb is a multiple of KC): per workgroup the operands of KC blocks
+// (64 rows of codes, their scales and, for Q4_1, minima; 64 positions of input codes and their (d, s)) are fetched
+// with wide coalesced loads into registers while the waves run the previous KC blocks from LDS, then stored to the
+// other half of a double buffer. The per-(row, position) arithmetic and its order are k_pf_gemm's.
+template <int EPI, bool HM, int KC>
+__global__ __launch_bounds__(256, KC == 4 ? 3 : 2) void k_pf_gemm_lds(pf_gemm_args a) {
+    __shared__ u32x4 sA[2][KC][64];         // row r's 16 code bytes of block j
+    __shared__ u32x4 sB[2][KC][64][2];      // position p's 32 input codes of block j
+    __shared__ __align__(16) uint16_t sD[2][KC][64];
+    __shared__ __align__(16) uint16_t sM[2][KC][HM ? 64 : 8];
+    __shared__ float2 sX[2][KC][64];        // (d, s) of position p's block j
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6, li = lane & 15, lq = lane >> 4;
+    const int rows = a.W.rows, n = a.n, nb = a.W.nb, nch = nb / KC, ng = rows / 8;
+    const int r0 = blockIdx.x * 64, p0 = blockIdx.y * 64, rl = (w & 1) * 32, pl = (w >> 1) * 32;
+    constexpr int NA = 64 * KC / 256, NBQ = 64 * KC * 2 / 256, NX = 64 * KC / 256;   // staging words per thread
+    const u32x4* codes = (const u32x4*)a.W.codes;
+    const u32x4* inq = (const u32x4*)a.in.q;
+    u32x4 ga[NA], gb[NBQ], gd = u32x4{0, 0, 0, 0}, gm = u32x4{0, 0, 0, 0};
+    float gxd[NX], gxs[NX];
+    auto fetch = [&](int c) {   // (rows and positions past the table / batch are clamped: their results are dropped)
+        const int j0 = c * KC;
+#pragma unroll
+        for (int q = 0; q < NA; q++) {
+            const int idx = t + 256 * q, row = idx / KC, jb = idx % KC;
+            ga[q] = codes[(size_t)min(r0 + row, rows - 1) * nb + j0 + jb];
+        }
+#pragma unroll
+        for (int q = 0; q < NBQ; q++) {
+            const int idx = t + 256 * q, jb = idx / 128, rem = idx % 128;
+            gb[q] = inq[((size_t)(j0 + jb) * n + min(p0 + (rem >> 1), n - 1)) * 2 + (rem & 1)];
+        }
+        if (t < 8 * KC) {
+            const int g = t / KC, jb = t % KC, gg = min(r0 / 8 + g, ng - 1);
+            gd = ((const u32x4*)a.W.scales)[(size_t)gg * nb + j0 + jb];
+            if (HM) gm = ((const u32x4*)a.W.mins)[(size_t)gg * nb + j0 + jb];
+        }
+#pragma unroll
+        for (int q = 0; q < NX; q++) {
+            const int idx = t + 256 * q, jb = idx / 64, pp = min(p0 + idx % 64, n - 1);
+            gxd[q] = a.in.d[(size_t)(j0 + jb) * n + pp];
+            gxs[q] = a.in.s[(size_t)(j0 + jb) * n + pp];
+        }
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int q = 0; q < NA; q++) {
+            const int idx = t + 256 * q;
+            sA[buf][idx % KC][idx / KC] = ga[q];
+        }
+#pragma unroll
+        for (int q = 0; q < NBQ; q++) {
+            const int idx = t + 256 * q, rem = idx % 128;
+            sB[buf][idx / 128][rem >> 1][rem & 1] = gb[q];
+        }
+        if (t < 8 * KC) {
+            const int g = t / KC, jb = t % KC;
+            *(u32x4*)&sD[buf][jb][8 * g] = gd;
+            if (HM) *(u32x4*)&sM[buf][jb][HM ? 8 * g : 0] = gm;
+        }
+#pragma unroll
+        for (int q = 0; q < NX; q++) {
+            const int idx = t + 256 * q;
+            sX[buf][idx / 64][idx % 64] = float2{gxd[q], gxs[q]};
+        }
+    };
+
+    float acc[2][2][4], cor[2][2][4];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) { acc[mt][nt][i] = 0.0f; cor[mt][nt][i] = 0.0f; }
+    const int shift = (lq >> 1) * 4;   // columns 0-15: low nibbles, 16-31: high nibbles
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    for (int c = 0; c < nch; c++) {
+        const int buf = c & 1;
+        if (c + 1 < nch) fetch(c + 1);
+#pragma unroll 2
+        for (int jb = 0; jb < KC; jb++) {
+            i32x4 isum[2][2];
+            long cb[2];
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++) cb[nt] = ((const long*)&sB[buf][jb][pl + 16 * nt + li][0])[lq];
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) {
+                const uint2 ca = ((const uint2*)&sA[buf][jb][rl + 16 * mt + li])[lq & 1];
+                const unsigned lo = (ca.x >> shift) & 0x0F0F0F0Fu, hi = (ca.y >> shift) & 0x0F0F0F0Fu;
+                const long av = (long)((unsigned long)lo | ((unsigned long)hi << 32));
+#pragma unroll
+                for (int nt = 0; nt < 2; nt++)
+                    isum[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, cb[nt], i32x4{0, 0, 0, 0}, 0, 0, 0);
+            }
+            float2 xz[2];
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++) xz[nt] = sX[buf][jb][pl + 16 * nt + li];
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++) {
+                const uint2 cs = *(const uint2*)&sD[buf][jb][rl + 16 * mt + 4 * lq];
+                const uint2 cm = HM ? *(const uint2*)&sM[buf][jb][HM ? rl + 16 * mt + 4 * lq : 0] : cs;
+                const float dd[4] = {h2f((uint16_t)(cs.x & 0xFFFFu)), h2f((uint16_t)(cs.x >> 16)),
+                                     h2f((uint16_t)(cs.y & 0xFFFFu)), h2f((uint16_t)(cs.y >> 16))};
+                const float mm[4] = {h2f((uint16_t)(cm.x & 0xFFFFu)), h2f((uint16_t)(cm.x >> 16)),
+                                     h2f((uint16_t)(cm.y & 0xFFFFu)), h2f((uint16_t)(cm.y >> 16))};
+#pragma unroll
+                for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        acc[mt][nt][i] = fmaf((float)isum[mt][nt][i], dd[i] * xz[nt].x, acc[mt][nt][i]);
+                        cor[mt][nt][i] = fmaf(mm[i], xz[nt].y, cor[mt][nt][i]);
+                    }
+            }
+        }
+        if (c + 1 < nch) stash(buf ^ 1);
+        __syncthreads();
+    }
+    const int rbase = r0 + rl, pbase = p0 + pl;
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++) {
+            const int p = pbase + 16 * nt + li, rr0 = rbase + 16 * mt + 4 * lq;
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = HM ? acc[mt][nt][i] + cor[mt][nt][i] : fmaf(-8.0f, cor[mt][nt][i], acc[mt][nt][i]);
+            if (EPI == EPI_SWIGLU) {
+                // rows 0-7 of the 16-row tile are a gate group, rows 8-15 the matching up group (lanes + 32)
+                float up[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) up[i] = __shfl_xor(v[i], 32);
+                if (lq < 2 && p < n && rbase + 16 * mt < rows) {
+                    float* o = a.out + (size_t)p * a.out_ld + (rbase + 16 * mt) / 2 + 4 * lq;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) o[i] = silu(v[i]) * up[i];
+                }
+            } else if (p < n) {
+                float* o = a.out + (size_t)p * a.out_ld + rr0;
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (rr0 + i < rows) o[i] = v[i];
+            }
+        }
+}
+
 // ---------------------------------------------------------------- gated short conv along positions
 // thread (position p, 32 channels): u = c * (b x w_d + taps), the taps being the b x values of the d_conv positions
 // before p (from this batch, or the conversation's conv memory before it), fma-chained oldest first
@@ -377,10 +523,27 @@ hipError_t launch_pf_rows(int mode, const pf_rows_args& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+#ifndef PF_KC
+#define PF_KC 8   // blocks staged per step of the LDS-staged product
+#endif
+// SEOUL_HIP_PF_PLAIN=1 keeps the products on the unstaged kernel (a comparison switch)
+static bool getenv_pf_plain() {
+    static const int v = [] { const char* e = getenv("SEOUL_HIP_PF_PLAIN"); return e && e[0] == '1' ? 1 : 0; }();
+    return v != 0;
+}
+
 hipError_t launch_pf_gemm(int epi, const pf_gemm_args& a, hipStream_t s) {
     if (a.n < 1 || a.W.rows % 8 || (epi == EPI_SWIGLU && a.W.rows % 16)) return hipErrorInvalidValue;
     const dim3 grid((a.W.rows + 63) / 64, (a.n + 63) / 64);
     const bool hm = a.W.mins != nullptr;   // Q4_1 table
+    if (a.W.nb % PF_KC == 0 && !getenv_pf_plain()) {
+        if (epi == EPI_SWIGLU && hm) hipLaunchKernelGGL((k_pf_gemm_lds<EPI_SWIGLU, true, PF_KC>), grid, dim3(256), 0, s, a);
+        else if (epi == EPI_SWIGLU) hipLaunchKernelGGL((k_pf_gemm_lds<EPI_SWIGLU, false, PF_KC>), grid, dim3(256), 0, s, a);
+        else if (epi == EPI_STORE && hm) hipLaunchKernelGGL((k_pf_gemm_lds<EPI_STORE, true, PF_KC>), grid, dim3(256), 0, s, a);
+        else if (epi == EPI_STORE) hipLaunchKernelGGL((k_pf_gemm_lds<EPI_STORE, false, PF_KC>), grid, dim3(256), 0, s, a);
+        else return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
     if (epi == EPI_SWIGLU && hm)
         hipLaunchKernelGGL((k_pf_gemm<EPI_SWIGLU, true>), grid, dim3(256), 0, s, a);
     else if (epi == EPI_SWIGLU)
