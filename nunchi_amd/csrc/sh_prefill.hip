@@ -227,8 +227,8 @@ __global__ __launch_bounds__(256) void k_pf_gemm(pf_gemm_args a) {
 // other half of a double buffer. The per-(row, position) arithmetic and its order are k_pf_gemm's.
 template <int EPI, bool HM, int KC>
 __global__ __launch_bounds__(256, KC == 4 ? 3 : 2) void k_pf_gemm_lds(pf_gemm_args a) {
-    __shared__ u32x4 sA[2][KC][64];         // row r's 16 code bytes of block j
-    __shared__ u32x4 sB[2][KC][64][2];      // position p's 32 input codes of block j
+    __shared__ u32x4 sA[2][64][KC + 1];     // row r's 16 code bytes of block j (row stride padded: no bank conflicts)
+    __shared__ u32x4 sB[2][KC][64][2];      // position p's 32 input codes of block j, 16-byte halves swapped when p & 8
     __shared__ __align__(16) uint16_t sD[2][KC][64];
     __shared__ __align__(16) uint16_t sM[2][KC][HM ? 64 : 8];
     __shared__ float2 sX[2][KC][64];        // (d, s) of position p's block j
@@ -236,44 +236,55 @@ __global__ __launch_bounds__(256, KC == 4 ? 3 : 2) void k_pf_gemm_lds(pf_gemm_ar
     const int rows = a.W.rows, n = a.n, nb = a.W.nb, nch = nb / KC, ng = rows / 8;
     const int r0 = blockIdx.x * 64, p0 = blockIdx.y * 64, rl = (w & 1) * 32, pl = (w >> 1) * 32;
     constexpr int NA = 64 * KC / 256, NBQ = 64 * KC * 2 / 256, NX = 64 * KC / 256;   // staging words per thread
-    const u32x4* codes = (const u32x4*)a.W.codes;
-    const u32x4* inq = (const u32x4*)a.in.q;
+    // this thread's staging sources, chunk 0 (rows and positions past the table / batch are clamped: their results
+    // are dropped); chunk c adds c * KC blocks
+    const u32x4* pa[NA];
+    const u32x4* pb[NBQ];
+    const float* px[NX];
+#pragma unroll
+    for (int q = 0; q < NA; q++) {
+        const int idx = t + 256 * q;
+        pa[q] = (const u32x4*)a.W.codes + (size_t)min(r0 + idx / KC, rows - 1) * nb + idx % KC;
+    }
+#pragma unroll
+    for (int q = 0; q < NBQ; q++) {
+        const int idx = t + 256 * q, rem = idx % 128;
+        pb[q] = (const u32x4*)a.in.q + ((size_t)(idx / 128) * n + min(p0 + (rem >> 1), n - 1)) * 2 + (rem & 1);
+    }
+#pragma unroll
+    for (int q = 0; q < NX; q++) {
+        const int idx = t + 256 * q;
+        px[q] = a.in.d + (size_t)(idx / 64) * n + min(p0 + idx % 64, n - 1);
+    }
+    const size_t pdo = (size_t)min(r0 / 8 + t / KC, ng - 1) * nb + t % KC, sdo = a.in.s - a.in.d;
     u32x4 ga[NA], gb[NBQ], gd = u32x4{0, 0, 0, 0}, gm = u32x4{0, 0, 0, 0};
     float gxd[NX], gxs[NX];
-    auto fetch = [&](int c) {   // (rows and positions past the table / batch are clamped: their results are dropped)
+    auto fetch = [&](int c) {
         const int j0 = c * KC;
 #pragma unroll
-        for (int q = 0; q < NA; q++) {
-            const int idx = t + 256 * q, row = idx / KC, jb = idx % KC;
-            ga[q] = codes[(size_t)min(r0 + row, rows - 1) * nb + j0 + jb];
-        }
+        for (int q = 0; q < NA; q++) ga[q] = pa[q][j0];
 #pragma unroll
-        for (int q = 0; q < NBQ; q++) {
-            const int idx = t + 256 * q, jb = idx / 128, rem = idx % 128;
-            gb[q] = inq[((size_t)(j0 + jb) * n + min(p0 + (rem >> 1), n - 1)) * 2 + (rem & 1)];
-        }
+        for (int q = 0; q < NBQ; q++) gb[q] = pb[q][(size_t)j0 * n * 2];
         if (t < 8 * KC) {
-            const int g = t / KC, jb = t % KC, gg = min(r0 / 8 + g, ng - 1);
-            gd = ((const u32x4*)a.W.scales)[(size_t)gg * nb + j0 + jb];
-            if (HM) gm = ((const u32x4*)a.W.mins)[(size_t)gg * nb + j0 + jb];
+            gd = ((const u32x4*)a.W.scales)[pdo + j0];
+            if (HM) gm = ((const u32x4*)a.W.mins)[pdo + j0];
         }
 #pragma unroll
         for (int q = 0; q < NX; q++) {
-            const int idx = t + 256 * q, jb = idx / 64, pp = min(p0 + idx % 64, n - 1);
-            gxd[q] = a.in.d[(size_t)(j0 + jb) * n + pp];
-            gxs[q] = a.in.s[(size_t)(j0 + jb) * n + pp];
+            gxd[q] = px[q][(size_t)j0 * n];
+            gxs[q] = px[q][(size_t)j0 * n + sdo];
         }
     };
     auto stash = [&](int buf) {
 #pragma unroll
         for (int q = 0; q < NA; q++) {
             const int idx = t + 256 * q;
-            sA[buf][idx % KC][idx / KC] = ga[q];
+            sA[buf][idx / KC][idx % KC] = ga[q];
         }
 #pragma unroll
         for (int q = 0; q < NBQ; q++) {
             const int idx = t + 256 * q, rem = idx % 128;
-            sB[buf][idx / 128][rem >> 1][rem & 1] = gb[q];
+            sB[buf][idx / 128][rem >> 1][(rem & 1) ^ ((rem >> 4) & 1)] = gb[q];
         }
         if (t < 8 * KC) {
             const int g = t / KC, jb = t % KC;
@@ -306,10 +317,11 @@ __global__ __launch_bounds__(256, KC == 4 ? 3 : 2) void k_pf_gemm_lds(pf_gemm_ar
             i32x4 isum[2][2];
             long cb[2];
 #pragma unroll
-            for (int nt = 0; nt < 2; nt++) cb[nt] = ((const long*)&sB[buf][jb][pl + 16 * nt + li][0])[lq];
+            for (int nt = 0; nt < 2; nt++)   // (li & 8: the halves were swapped, which spreads the reads over the banks)
+                cb[nt] = ((const long*)&sB[buf][jb][pl + 16 * nt + li][0])[lq ^ ((li >> 3) << 1)];
 #pragma unroll
             for (int mt = 0; mt < 2; mt++) {
-                const uint2 ca = ((const uint2*)&sA[buf][jb][rl + 16 * mt + li])[lq & 1];
+                const uint2 ca = ((const uint2*)&sA[buf][rl + 16 * mt + li][jb])[lq & 1];
                 const unsigned lo = (ca.x >> shift) & 0x0F0F0F0Fu, hi = (ca.y >> shift) & 0x0F0F0F0Fu;
                 const long av = (long)((unsigned long)lo | ((unsigned long)hi << 32));
 #pragma unroll
