@@ -453,6 +453,13 @@ __global__ __launch_bounds__(64) void k_pf_kv(pf_attn_args a) {
 // q_norm); score_t = dot_h(q, K_t) / sqrt(D) over the causal window; softmax with the max subtracted, glibc's expf and
 // a double sum in position order; o = sum_t fma(e_t * inv, V_t, o) in order; times the sigmoid head gate; the
 // output rows cut per 32 channels for the o table
+// lowest set bit exponent of a positive float (0 gives a large value)
+__device__ __forceinline__ int low_bit_exp(float e) {
+    const unsigned b = __float_as_uint(e), ex = b >> 23, mt = b & 0x7FFFFFu;
+    if (b == 0) return 1 << 20;
+    return ex == 0 ? -149 + __builtin_ctz(mt) : (int)ex - 150 + __builtin_ctz(mt | 0x800000u);
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void k_pf_attn(pf_attn_args a) {
     extern __shared__ float lds[];
@@ -495,29 +502,76 @@ __global__ __launch_bounds__(256) void k_pf_attn(pf_attn_args a) {
         for (int hh = 0; hh < grp; hh++) sc[(size_t)hh * nks + t] = dot_h8<D>(q_s + hh * D, kf) * scale;
     }
     __syncthreads();
+    // softmax per head (wave hh): max, e_t = glibc expf(s_t - max), the double sum of e_t in position order (its
+    // exact-sum shortcut: when every e_t is a multiple of 2^(B - 51), B = floor(log2 sum), any order gives the same
+    // double, so the wave's tree sum is used; otherwise lane 0 adds in order), then a_t = e_t * inv in place
     for (int hh = wv; hh < grp; hh += 4) {
         float* s = sc + (size_t)hh * nks;
         float mx = -INFINITY;
         for (int t = lane; t < nk; t += 64) mx = fmaxf(mx, s[t]);
         mx = wave_max(mx);
-        for (int t = lane; t < nk; t += 64) s[t] = expf_glibc(s[t] - mx);
-        __builtin_amdgcn_wave_barrier();
-        if (lane == 0) {   // double sum in position order, as imi's loop
-            double sum = 0.0;
-            for (int t = 0; t < nk; t++) sum += (double)s[t];
-            inv_s[hh] = (float)(1.0 / sum);
+        double part = 0.0;
+        int lowb = 1 << 20;
+        for (int t = lane; t < nk; t += 64) {
+            const float e = expf_glibc(s[t] - mx);
+            s[t] = e;
+            part += (double)e;
+            lowb = min(lowb, low_bit_exp(e));
         }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            part += __shfl_xor(part, o);
+            lowb = min(lowb, __shfl_xor(lowb, o));
+        }
+        __builtin_amdgcn_wave_barrier();
+        float inv = 0.0f;
+        if (lane == 0) {
+            int ex;
+            (void)frexp(part, &ex);
+            if (lowb < ex - 1 - 51) {   // some e_t below the exact unit: add in position order, as imi's loop
+                double sum = 0.0;
+                for (int t = 0; t < nk; t++) sum += (double)s[t];
+                part = sum;
+            }
+            inv = (float)(1.0 / part);
+        }
+        inv = __shfl(inv, 0);
+        for (int t = lane; t < nk; t += 64) s[t] = s[t] * inv;
     }
     __syncthreads();
-    for (int k = tid; k < grp * D; k += 256) {
-        const int hh = k / D, i = k - hh * D;
-        const float* s = sc + (size_t)hh * nks;
-        const float inv = inv_s[hh];
-        float o = 0.0f;
-        for (int t = 0; t < nk; t++) o = fmaf(s[t] * inv, h2f(vc[(size_t)(s0 + t) * D + i]), o);
-        const int h = g * grp + hh;
-        const float gate = 1.0f / (1.0f + expf_glibc(-row[Hq + 2 * kvd + h]));
-        o_s[k] = o * gate;
+    // o = sum_t fma(a_t, V_t, o) in position order, thread per (head, dimension); value rows staged through LDS in
+    // tiles of TP positions, shared by the group's heads
+    constexpr int TP = 32, TW = TP * D / 8;   // positions per tile, 16-byte words per tile
+    u32x4* vt = (u32x4*)(sc + (size_t)grp * ((nks + 3) & ~3));
+    const uint16_t* vh = (const uint16_t*)vt;
+    const int nitem = grp * D;                // (head, dimension) items, at most 4 per thread
+    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int q0 = 0; q0 < nk; q0 += TP) {
+        const int nt = min(TP, nk - q0);
+        __syncthreads();
+        for (int w = tid; w < nt * (D / 8); w += 256) vt[w] = ((const u32x4*)(vc + (size_t)(s0 + q0) * D))[w];
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int k = tid + 256 * c;
+            if (k < nitem) {
+                const int hh = k / D, i = k - hh * D;
+                const float* av = sc + (size_t)hh * nks + q0;
+                float acc = o[c];
+                for (int t = 0; t < nt; t++) acc = fmaf(av[t], h2f(vh[t * D + i]), acc);
+                o[c] = acc;
+            }
+        }
+    }
+    (void)TW;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int k = tid + 256 * c;
+        if (k < nitem) {
+            const int hh = k / D, h = g * grp + hh;
+            const float gate = 1.0f / (1.0f + expf_glibc(-row[Hq + 2 * kvd + h]));
+            o_s[k] = o[c] * gate;
+        }
     }
     __syncthreads();
     const int nblk = grp * D / 32, cb0 = g * nblk;
@@ -594,7 +648,8 @@ hipError_t launch_pf_kv(const pf_attn_args& a, hipStream_t s) {
 
 hipError_t launch_pf_attn(const pf_attn_args& a, hipStream_t s) {
     const int grp = a.n_head / a.n_kv;
-    const size_t lds = sizeof(float) * ((size_t)2 * grp * a.D + 4 * (size_t)a.D + 8 + (size_t)grp * (a.pos0 + a.n));
+    const size_t lds = sizeof(float) * ((size_t)2 * grp * a.D + 4 * (size_t)a.D + 8 + (size_t)grp * ((a.pos0 + a.n + 3) & ~3)) +
+                       32 * (size_t)a.D * sizeof(uint16_t);   // + one value tile of 32 positions
     if (lds > 160 * 1024 || a.n < 1) return hipErrorInvalidValue;
     const void* fn = a.D == 128 ? (const void*)k_pf_attn<128> : a.D == 64 ? (const void*)k_pf_attn<64>
                    : a.D == 32 ? (const void*)k_pf_attn<32> : nullptr;

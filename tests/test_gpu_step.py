@@ -240,3 +240,22 @@ def test_full_seoul_step_and_greedy(model_dir, step_path):
     hg, lg, _ = g.step(int(ids_g[-1]))
     ho, lo = o.step(int(ids_o[-1]))
     assert same(hg, ho) and same(lg, lo)
+
+
+@pytest.mark.parametrize("shape", ["tiny", "mid"])
+def test_sharp_attention_prefill(model_dir, shape):
+    """The prefill's softmax on the sharp model (q/k norm weights x 6): in-order double sums, bit for bit."""
+    import nunchi_amd
+    import oracle
+    from nunchi_amd import synth
+    base = synth.TINY if shape == "tiny" else synth.BrainShape(n_layer=4, attn_layers=(1, 3), n_vocab=4096)
+    sharp = synth.BrainShape(**{**base.__dict__, "qk_norm_scale": 6.0})
+    path = synth.cached("brain", sharp, 15, model_dir)
+    g = nunchi_amd.Brain(path, n_ctx=320)
+    o = oracle.Engine(path, threads=8, n_ctx=320)
+    toks = _prompt(300, sharp.n_vocab, 17)
+    hg, lg, bg, hall_g = g.step_batch(toks, hidden_all=True)
+    ho, lo, hall_o = o.step_batch(toks, hidden_all=True)
+    for p in range(len(toks)):
+        assert same(hall_g[p], hall_o[p]), p
+    assert same(lg, lo) and bg == oracle.top(lo)
