@@ -380,20 +380,21 @@ __global__ __launch_bounds__(256, KC == 4 ? 3 : 2) void k_pf_gemm_lds(pf_gemm_ar
 }
 
 // ---------------------------------------------------------------- gated short conv along positions
-// thread (position p, 32 channels): u = c * (b x w_d + taps), the taps being the b x values of the d_conv positions
+// thread per (position p, channel e): u = c * (b x w_d + taps), the taps being the b x values of the d_conv positions
 // before p (from this batch, or the conversation's conv memory before it), fma-chained oldest first
-// (imi/core/seoul.cpp:562-577); then the cut of the 32 outputs
-__global__ __launch_bounds__(256) void k_pf_conv(pf_conv_args a) {
-    const int nbk = a.E / 32, idx = blockIdx.x * 256 + threadIdx.x;
-    if (idx >= a.n * nbk) return;
-    const int t = idx / a.n, p = idx - t * a.n, E = a.E, dc = a.d_conv;
+// (imi/core/seoul.cpp:562-577); then the cut of each 32 outputs: the 32 channels of a cut block are 32 lanes, which
+// reduce amax and the code sum across lanes (imi_cut32's values; the max and the integer sum do not depend on order)
+__global__ __launch_bounds__(256) void k_pf_conv_lanes(pf_conv_args a) {
+    const int E = a.E, dc = a.d_conv, gid = blockIdx.x * 256 + threadIdx.x;
+    const bool on = gid < a.n * E;
+    const int p = on ? gid / E : 0, e = on ? gid - p * E : 0, t = e >> 5, c = e & 31;
     const size_t ld = 3 * (size_t)E;
-    float u[32];
-    for (int c = 0; c < 32; c++) {
-        const int e = 32 * t + c, ub = 96 * t + 24 * (c >> 3) + (c & 7);
-        const float* r = a.bcx + (size_t)p * ld + ub;
+    const int ub = 96 * t + 24 * (c >> 3) + (c & 7);
+    const float* r = a.bcx + (size_t)p * ld + ub;
+    float u = 0.0f;
+    if (on) {
         const float bx = r[0] * r[16];
-        float s = bx * a.w[(size_t)dc * E + e];
+        float sv = bx * a.w[(size_t)dc * E + e];
         for (int tt = 0; tt < dc; tt++) {
             const int q = p - dc + tt;
             float st;
@@ -403,11 +404,25 @@ __global__ __launch_bounds__(256) void k_pf_conv(pf_conv_args a) {
             } else {
                 st = a.state[(size_t)(p + tt) * E + e];
             }
-            s = fmaf(st, a.w[(size_t)tt * E + e], s);
+            sv = fmaf(st, a.w[(size_t)tt * E + e], sv);
         }
-        u[c] = s * r[8];
+        u = sv * r[8];
     }
-    cut_store(a.cut, a.n, t, p, u);
+    float amax = fabsf(u);
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    const float d = amax / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
+    const int q = (int)rintf(u * id);
+    int sum = q;
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+    if (on) {
+        a.cut.q[((size_t)t * a.n + p) * 32 + c] = (int8_t)q;
+        if (c == 0) {
+            a.cut.d[(size_t)t * a.n + p] = d;
+            a.cut.s[(size_t)t * a.n + p] = d * (float)sum;
+        }
+    }
 }
 
 // the conv memory after the batch: its last d_conv b x values (older memory where the batch is shorter)
@@ -632,8 +647,8 @@ hipError_t launch_pf_cut(const pf_cutk_args& a, hipStream_t s) {
 
 hipError_t launch_pf_conv(const pf_conv_args& a, hipStream_t s) {
     if (a.E % 32 || a.n < 1 || a.d_conv < 1) return hipErrorInvalidValue;
-    const int total = a.n * (a.E / 32);
-    hipLaunchKernelGGL(k_pf_conv, dim3((total + 255) / 256), dim3(256), 0, s, a);
+    const long long total = (long long)a.n * a.E;   // a thread per (position, channel)
+    hipLaunchKernelGGL(k_pf_conv_lanes, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_pf_conv_state, dim3((a.E + 255) / 256), dim3(256), 0, s, a);
