@@ -1048,7 +1048,8 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
     constexpr int TV = tile_positions<D>();
     constexpr int half = D / 2, KW = D / 8;        // 16-byte words per cache row
     constexpr int DPL = (D + 63) / 64;             // dimensions per lane in the per-head wave work (lane + 64 c)
-    constexpr bool AHEAD2 = D <= 64;               // key rows requested two passes ahead (one at D 128: registers)
+    constexpr bool AHEAD2 = false;                 // key rows two passes ahead (registers: the value tile comes first)
+    constexpr bool EARLY_V = D <= 64;              // value tile 0 requested at the start (D 128: after the scores)
     constexpr int NL = (TV / 8) * KW;              // loader threads: one 8-position x 8-dimension block each
     static_assert(NL <= 256 && TV / 8 <= 32, "value staging layout");
     extern __shared__ __align__(16) float lds[];
@@ -1121,6 +1122,11 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
         }
     };
 
+    if (EARLY_V && loader) {   // tile 0 requested with the key rows (cache rows of earlier steps)
+        load_tile(0);
+        vn0 = ((const f32x4*)(row + Hq + kvd + g * D))[2 * kq];
+        vn1 = ((const f32x4*)(row + Hq + kvd + g * D))[2 * kq + 1];
+    }
     // ---- q (wave 0) and this position's k, v (wave 1): norm + NEOX rope (imi/core/seoul.cpp:19-28) ----
     if (wv < 2) {   // lane holds dimensions lane + 64 c; at D 128 a rope pair (i, i + 64) sits in one lane
         const bool is_k = wv == 1;
@@ -1163,11 +1169,11 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
     // ---- scores ----
     const float scale = 1.0f / sqrtf((float)D);
     for (int p = t; p < nk; p += NT) {
-        if (!AHEAD2 && p != t) {   // D 128: this pass's row requested here (no prefetch registers to spare)
+        if (D > 64 && p != t) {   // D 128: this pass's row requested here (no prefetch registers to spare)
 #pragma unroll
             for (int i = 0; i < KW; i++) ka[i] = ((const u32x4*)(kc + (size_t)(s0 + min(p, last)) * D))[i];
         }
-        if (!AHEAD2) {   // dot_h's 8 chains over columns i % 8, a word (8 columns) at a time
+        if (D > 64) {   // dot_h's 8 chains over columns i % 8, a word (8 columns) at a time
             float acc[8];
 #pragma unroll
             for (int l = 0; l < 8; l++) acc[l] = 0.0f;
@@ -1191,7 +1197,7 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
             continue;
         }
         u32x4 kn[KW];
-        const int pn = min(p + 2 * NT, last);
+        const int pn = min(p + (AHEAD2 ? 2 : 1) * NT, last);
 #pragma unroll
         for (int i = 0; i < KW; i++) kn[i] = ((const u32x4*)(kc + (size_t)(s0 + pn) * D))[i];
         float kf[D];
@@ -1207,10 +1213,15 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
             }
         }
         sc[p] = dot_h8<D>(q_s, kf) * scale;
+        if (AHEAD2) {
 #pragma unroll
-        for (int i = 0; i < KW; i++) { ka[i] = kb[AHEAD2 ? i : 0]; kb[AHEAD2 ? i : 0] = kn[i]; }
+            for (int i = 0; i < KW; i++) { ka[i] = kb[AHEAD2 ? i : 0]; kb[AHEAD2 ? i : 0] = kn[i]; }
+        } else {
+#pragma unroll
+            for (int i = 0; i < KW; i++) ka[i] = kn[i];
+        }
     }
-    if (loader) {   // tile 0 requested (to LDS once the softmax is done)
+    if (!EARLY_V && loader) {   // tile 0 requested (to LDS once the softmax is done)
         load_tile(0);
         vn0 = ((const f32x4*)(row + Hq + kvd + g * D))[2 * kq];
         vn1 = ((const f32x4*)(row + Hq + kvd + g * D))[2 * kq + 1];
