@@ -423,7 +423,42 @@ __device__ __forceinline__ void put_xt(float* xt, int t, const f32x4& v) {
     p[3 * XLD] = v.w;
 }
 
-template <int M, int EPI, int UG, bool HM = false>   // HM: Q4_1 table, as k_gemv_cut
+// values 4t .. 4t+3 of conversation m's input row: the word's dequantized row (Q4_0: (code - 8) * d; Q6_K:
+// (d * scale) * (value - 32), imi/core/tables.cpp:216-233) or the given vector (imi/core/seoul.cpp:363-364)
+__device__ __forceinline__ f32x4 embed_quad(const gemv_args& a, int m, int t, int E) {
+    const int tok = a.P->token[m];
+    if (tok < 0) return ((const f32x4*)(a.embd + (size_t)m * E))[t];
+    float v[4];
+    if (a.emb6.codes) {
+        const int e = 4 * t, i = e >> 8, p = e & 255, h = p >> 7, k = (p >> 5) & 3, l = p & 31, sx = p >> 4;
+        const size_t u = (size_t)tok * a.emb6.nbk + i;
+        const unsigned* base = (const unsigned*)((const u32x4*)a.emb6.codes + (u >> 6) * 13 * 64 + (u & 63));
+        const int dq = 16 * h + 8 * (k & 1) + (l >> 2), dh = 8 * h + (l >> 2);   // ql / qh dwords
+        const unsigned ql = base[(dq >> 2) * 256 + (dq & 3)], qh = base[(8 + (dh >> 2)) * 256 + (dh & 3)];
+        const unsigned sw = base[12 * 256 + (sx >> 2)];
+        const float ds = h2f(a.emb6.d[u]) * (float)(int8_t)((sw >> (8 * (sx & 3))) & 0xFFu);
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const unsigned lo = (ql >> (8 * b)) & 0xFFu, hi = (qh >> (8 * b)) & 0xFFu;
+            const int q = (int)(((k < 2 ? lo : lo >> 4) & 15u) | (((hi >> (2 * k)) & 3u) << 4));
+            v[b] = ds * (float)(q - 32);
+        }
+    } else {
+        const int nb = a.emb.nb, j = t >> 3, q = t & 7;
+        const u32x4 c = ((const u32x4*)a.emb.codes)[(size_t)tok * nb + j];
+        const unsigned word = (q & 3) == 0 ? c.x : (q & 3) == 1 ? c.y : (q & 3) == 2 ? c.z : c.w;
+        const float d = h2f(((const uint16_t*)a.emb.scales)[((size_t)(tok >> 3) * nb + j) * 8 + (tok & 7)]);
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const unsigned byte = (word >> (8 * b)) & 0xFFu;
+            v[b] = (float)((int)(q < 4 ? byte & 15u : byte >> 4) - 8) * d;
+        }
+    }
+    return f32x4{v[0], v[1], v[2], v[3]};
+}
+
+// HM: Q4_1 table, as k_gemv_cut. EMB: the layer-0 form, whose input is the embedding row (no residual to add)
+template <int M, int EPI, int UG, bool HM = false, bool EMB = false>
 __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
     extern __shared__ __align__(16) float lds[];
     const int E = a.E, nb = a.W.nb, st = ((nb + 3) & ~3) + 4;
@@ -467,10 +502,15 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
     const int tq = t < nq ? t : nq - 1;
 #pragma unroll
     for (int m = 0; m < M; m++) {
-        xv[m] = ((const f32x4*)(a.x_in + (size_t)m * E))[tq];
-        yv[m] = ((const f32x4*)(a.y_in + (size_t)m * E))[tq];
+        if (EMB) {
+            xv[m] = embed_quad(a, m, tq, E);
+            yv[m] = xv[m];
+        } else {
+            xv[m] = ((const f32x4*)(a.x_in + (size_t)m * E))[tq];
+            yv[m] = ((const f32x4*)(a.y_in + (size_t)m * E))[tq];
+        }
     }
-    const f32x4 wp = ((const f32x4*)a.w_post)[tq], wq = ((const f32x4*)a.w_pre)[tq];
+    const f32x4 wp = EMB ? f32x4{0, 0, 0, 0} : ((const f32x4*)a.w_post)[tq], wq = ((const f32x4*)a.w_pre)[tq];
     const uint64_t etab = kExp2Tab[t & 31];   // (SwiGLU) copied to LDS once the dots have waited for the weights
     int k = blockIdx.x;
     load_chunk(k < nchunk ? k : nchunk - 1);
@@ -488,7 +528,7 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
         for (int q = 0; q < CMAX; q++) cst[q] = q < dc ? stt[(size_t)q * E + e] : 0.0f;
     }
 
-    {   // x += norm(y) * w_post (imi_norm_mul_add)
+    if (!EMB) {   // x += norm(y) * w_post (imi_norm_mul_add)
         if (t < nq)
 #pragma unroll
             for (int m = 0; m < M; m++) put_xt(l_v + m * 32 * XLD, t, yv[m]);
@@ -1436,8 +1476,10 @@ __global__ __launch_bounds__(64) void k_q4_rows(q4dev T, const int32_t* ids, flo
 
 // tables behind the post-norm residual that k_gemv_norm takes (E a multiple of 128 up to 2048, the table's input E)
 static bool norm_kernel_takes(int M, int pro, const gemv_args& a, int ug) {
-    return pro == PRO_RESID_NORM && (M == 1 || M == 2) && (a.E == 256 || a.E == 512 || a.E == 1024 || a.E == 2048) && a.W.nb * 32 == a.E &&
-           a.W.cols == a.E && a.x_in && a.y_in && a.w_post && a.W.rows % (8 * ug) == 0;
+    const bool resid = pro == PRO_RESID_NORM && a.x_in && a.y_in && a.w_post;
+    const bool embed = pro == PRO_EMBED_NORM && (a.emb.codes || a.emb6.codes) && a.embd;
+    return (resid || embed) && (M == 1 || M == 2) && (a.E == 256 || a.E == 512 || a.E == 1024 || a.E == 2048) && a.W.nb * 32 == a.E &&
+           a.W.cols == a.E && a.W.rows % (8 * ug) == 0;
 }
 
 int gemv_logits_grid(int M, int pro, const gemv_args& a, int max_grid) {
@@ -1473,10 +1515,17 @@ hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hi
         const int nchunk = (a.units + b.upw - 1) / b.upw;
         const void* fn = nullptr;
         const bool hm = a.W.mins != nullptr;
+        if (pro == PRO_EMBED_NORM) {   // layer 0: the embedding row in the prologue
+            if (epi != EPI_STORE && epi != EPI_CONV) return hipErrorInvalidValue;
+#define SH_EMB_FN(M_, EPI_, UG_) if (M == M_ && epi == EPI_) fn = hm ? (const void*)k_gemv_norm<M_, EPI_, UG_, true, true> : (const void*)k_gemv_norm<M_, EPI_, UG_, false, true>;
+            SH_EMB_FN(1, EPI_STORE, 1) SH_EMB_FN(1, EPI_CONV, 3) SH_EMB_FN(2, EPI_STORE, 1) SH_EMB_FN(2, EPI_CONV, 3)
+#undef SH_EMB_FN
+        } else {
 #define SH_NORM_FN(M_, EPI_, UG_) if (M == M_ && epi == EPI_) fn = hm ? (const void*)k_gemv_norm<M_, EPI_, UG_, true> : (const void*)k_gemv_norm<M_, EPI_, UG_>;
-        SH_NORM_FN(1, EPI_STORE, 1) SH_NORM_FN(1, EPI_SWIGLU, 2) SH_NORM_FN(1, EPI_CONV, 3) SH_NORM_FN(1, EPI_LOGITS, 1)
-        SH_NORM_FN(2, EPI_STORE, 1) SH_NORM_FN(2, EPI_SWIGLU, 2) SH_NORM_FN(2, EPI_CONV, 3) SH_NORM_FN(2, EPI_LOGITS, 1)
+            SH_NORM_FN(1, EPI_STORE, 1) SH_NORM_FN(1, EPI_SWIGLU, 2) SH_NORM_FN(1, EPI_CONV, 3) SH_NORM_FN(1, EPI_LOGITS, 1)
+            SH_NORM_FN(2, EPI_STORE, 1) SH_NORM_FN(2, EPI_SWIGLU, 2) SH_NORM_FN(2, EPI_CONV, 3) SH_NORM_FN(2, EPI_LOGITS, 1)
 #undef SH_NORM_FN
+        }
         if (!fn) return hipErrorInvalidValue;
         const size_t lds = gemv_norm_lds(M, a.E, a.W.nb, b.upw * ug);
         if (lds > 160 * 1024) return hipErrorInvalidValue;
