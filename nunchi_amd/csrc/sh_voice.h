@@ -39,6 +39,8 @@ struct vtab_args {
     float* out;             // VE_STORE: out[p][row]; VE_RESID: out[p][row] += acc; VE_SWIGLU: out[p][4 g + r]
     int out_ld;
     int units;              // workgroups: row groups per workgroup = 1 (2 for VE_SWIGLU: gate group, up group)
+    float* part;            // generic order, VE_STORE/VE_RESID, nb > 32: [units][8 P][nb] scratch of per-block sums
+                            // that splits the table over its 1024-column chunks (null: one workgroup per group)
 };
 
 // one table times a single input vector: the input projection (per frame) and the word scores (per pass)

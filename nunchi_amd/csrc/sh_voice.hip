@@ -29,16 +29,28 @@ __device__ __forceinline__ void position_scales(const vtab_args& a, float* scl) 
 
 // columns [1024 q, 1024 q + 32 nbc) of the P positions, k-major: xs[block][column in block][position]
 // (imi/core/voice.cpp:157-166: the transposed input, normed first when the table follows a norm)
+// Thread t stages columns 4t..4t+3 of every position: all P 16-byte loads are in flight before the first LDS store
+// (src rows and norm_w are 16-byte aligned, src_ld a multiple of 4: the launcher checks).
 template <int P, int PRO>
 __device__ __forceinline__ void stage_chunk(float* xs, const vtab_args& a, int q, int nbc, const float* scl) {
     constexpr int PP = vx_pp(P), XJ = vx_xj(P);
-    const int n = 32 * nbc, c0 = q * 32 * VX_NJ;
+    static_assert(4 * VX_THREADS == 32 * VX_NJ, "one float4 of each position per thread");
+    const int n = 32 * nbc, c0 = q * 32 * VX_NJ, k = 4 * threadIdx.x;
+    if (k >= n) return;
+    f32x4 v[P];
+#pragma unroll
+    for (int p = 0; p < P; p++) v[p] = *reinterpret_cast<const f32x4*>(a.src + (size_t)p * a.src_ld + c0 + k);
+    f32x4 nw{};
+    if (PRO == VP_NORM) nw = *reinterpret_cast<const f32x4*>(a.norm_w + c0 + k);
+    float* dst = xs + (k >> 5) * XJ + (k & 31) * PP;
+#pragma unroll
     for (int p = 0; p < P; p++) {
-        const float* row = a.src + (size_t)p * a.src_ld + c0;
-        for (int k = threadIdx.x; k < n; k += VX_THREADS) {
-            float v = row[k];
-            if (PRO == VP_NORM) v = v * scl[p] * a.norm_w[c0 + k];
-            xs[(k >> 5) * XJ + (k & 31) * PP + p] = v;
+        float e[4] = {v[p].x, v[p].y, v[p].z, v[p].w};
+        const float w4[4] = {nw.x, nw.y, nw.z, nw.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            if (PRO == VP_NORM) e[i] = e[i] * scl[p] * w4[i];
+            dst[i * PP + p] = e[i];
         }
     }
 }
@@ -57,6 +69,34 @@ __device__ __forceinline__ void table_epilogue(const vtab_args& a, int g0, float
         if (t < NR * P && row < a.W.rows) {
             float* o = a.out + (size_t)fc * a.out_ld + row;
             *o = EPI == VE_RESID ? *o + acc : acc;   // x[i] += y[i] (voice.cpp:188,196)
+        }
+    }
+}
+
+// s[g][c] = sum over the block's 32 columns k of fma(w[g][k], x[k][c], s) in column order, for the R row groups'
+// codes w (two 16-byte words each) and the staged block xb (column k, position c at xb[k * PP + c])
+template <int P, int R>
+__device__ __forceinline__ void block_sums(const float* xb, const u32x4 (&w)[R][2], float (&s)[R][P]) {
+    constexpr int PP = vx_pp(P);
+#pragma unroll
+    for (int g = 0; g < R; g++)
+#pragma unroll
+        for (int c = 0; c < P; c++) s[g][c] = 0.0f;
+#pragma unroll 4
+    for (int kk = 0; kk < 32; kk++) {
+        float xv[PP];
+#pragma unroll
+        for (int c4 = 0; c4 < PP / 4; c4++) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(xb + kk * PP + 4 * c4);
+            xv[4 * c4] = v.x; xv[4 * c4 + 1] = v.y; xv[4 * c4 + 2] = v.z; xv[4 * c4 + 3] = v.w;
+        }
+#pragma unroll
+        for (int g = 0; g < R; g++) {
+            const u32x4 h = w[g][kk >> 4];
+            const unsigned word = (kk & 12) == 0 ? h.x : (kk & 12) == 4 ? h.y : (kk & 12) == 8 ? h.z : h.w;
+            const float wf = (float)(int)(signed char)(word >> (8 * (kk & 3)));
+#pragma unroll
+            for (int c = 0; c < P; c++) s[g][c] = fmaf(wf, xv[c], s[g][c]);
         }
     }
 }
@@ -82,44 +122,28 @@ __global__ __launch_bounds__(VX_THREADS) void k_vtab_gen(vtab_args a) {
     float acc = 0.0f;
     for (int q = 0; q * VX_NJ < nb; q++) {
         const int nbc = min(VX_NJ, nb - q * VX_NJ), j = q * VX_NJ + jl;
-        if (q) __syncthreads();   // the previous chunk's fold has read ss and ds
-        stage_chunk<P, PRO>(xs, a, q, nbc, scl);
         u32x4 w[R][2];
-        if (jl < nbc) {
+        uint16_t dh[R];
+        if (jl < nbc) {   // codes and scales first: their loads overlap the input staging
 #pragma unroll
             for (int g = 0; g < R; g++) {
                 const size_t blk = ((size_t)(g0 + g) * nb + j) * 8 + r8;
                 const u32x4* cp = reinterpret_cast<const u32x4*>(a.W.codes + blk * 32);
                 w[g][0] = cp[0];
                 w[g][1] = cp[1];
-                ds[(8 * g + r8) * VX_SS + jl] = h2f(a.W.scales[blk]);
+                dh[g] = a.W.scales[blk];
             }
+        }
+        if (q) __syncthreads();   // the previous chunk's fold has read ss and ds
+        stage_chunk<P, PRO>(xs, a, q, nbc, scl);
+        if (jl < nbc) {
+#pragma unroll
+            for (int g = 0; g < R; g++) ds[(8 * g + r8) * VX_SS + jl] = h2f(dh[g]);
         }
         __syncthreads();
         if (jl < nbc) {
             float s[R][P];
-#pragma unroll
-            for (int g = 0; g < R; g++)
-#pragma unroll
-                for (int c = 0; c < P; c++) s[g][c] = 0.0f;
-            const float* xb = xs + jl * XJ;
-#pragma unroll 4
-            for (int kk = 0; kk < 32; kk++) {
-                float xv[PP];
-#pragma unroll
-                for (int c4 = 0; c4 < PP / 4; c4++) {
-                    const f32x4 v = *reinterpret_cast<const f32x4*>(xb + kk * PP + 4 * c4);
-                    xv[4 * c4] = v.x; xv[4 * c4 + 1] = v.y; xv[4 * c4 + 2] = v.z; xv[4 * c4 + 3] = v.w;
-                }
-#pragma unroll
-                for (int g = 0; g < R; g++) {
-                    const u32x4 h = w[g][kk >> 4];
-                    const unsigned word = (kk & 12) == 0 ? h.x : (kk & 12) == 4 ? h.y : (kk & 12) == 8 ? h.z : h.w;
-                    const float wf = (float)(int)(signed char)(word >> (8 * (kk & 3)));
-#pragma unroll
-                    for (int c = 0; c < P; c++) s[g][c] = fmaf(wf, xv[c], s[g][c]);
-                }
-            }
+            block_sums<P, R>(xs + jl * XJ, w, s);
 #pragma unroll
             for (int g = 0; g < R; g++)
 #pragma unroll
@@ -133,6 +157,84 @@ __global__ __launch_bounds__(VX_THREADS) void k_vtab_gen(vtab_args a) {
         }
     }
     table_epilogue<P, EPI, 8 * R>(a, g0, acc, ev);
+}
+
+// the generic order split over the input's 1024-column chunks, for tables wider than one chunk (the down table):
+// workgroup (group g, chunk q) forms its blocks' sums s as k_vtab_gen does and stores them to
+// part[g][8 P][nb] (row r8 * P + position c); k_vtab_fold then runs each (row, position)'s chain
+// acc = fma(d, s, acc) over all blocks in order, so the results are k_vtab_gen's. Spreading the chunks over
+// workgroups keeps the chip busy where one workgroup per group would walk the chunks one after another.
+template <int P, int PRO>
+__global__ __launch_bounds__(VX_THREADS) void k_vtab_part(vtab_args a) {
+    constexpr int XJ = vx_xj(P);
+    static_assert(8 * VX_NJ == VX_THREADS, "thread (row, block) of a chunk");
+    __shared__ __attribute__((aligned(16))) float xs[VX_NJ * XJ];
+    __shared__ float ss[8 * P * VX_SS];
+    __shared__ float scl[VX_MAX_P];
+    const int t = threadIdx.x, r8 = t & 7, jl = t >> 3;
+    const int nb = a.W.nb, g = blockIdx.x, q = blockIdx.y;
+    const int nbc = min(VX_NJ, nb - q * VX_NJ);
+    u32x4 w[1][2];
+    if (jl < nbc) {
+        const size_t blk = ((size_t)g * nb + q * VX_NJ + jl) * 8 + r8;
+        const u32x4* cp = reinterpret_cast<const u32x4*>(a.W.codes + blk * 32);
+        w[0][0] = cp[0];
+        w[0][1] = cp[1];
+    }
+    if (PRO == VP_NORM) {
+        position_scales<P>(a, scl);
+        __syncthreads();
+    }
+    stage_chunk<P, PRO>(xs, a, q, nbc, scl);
+    __syncthreads();
+    if (jl < nbc) {
+        float s[1][P];
+        block_sums<P, 1>(xs + jl * XJ, w, s);
+#pragma unroll
+        for (int c = 0; c < P; c++) ss[(r8 * P + c) * VX_SS + jl] = s[0][c];
+    }
+    __syncthreads();
+    float* dst = a.part + (size_t)g * 8 * P * nb + q * VX_NJ;
+    for (int i = t; i < 8 * P * VX_NJ; i += VX_THREADS) {
+        const int row = i / VX_NJ, k = i - row * VX_NJ;
+        if (k < nbc) dst[(size_t)row * nb + k] = ss[row * VX_SS + k];
+    }
+}
+
+template <int P, int EPI>
+__global__ __launch_bounds__(VX_THREADS) void k_vtab_fold(vtab_args a) {
+    __shared__ float ss[8 * P * VX_SS];
+    __shared__ float ds[8 * VX_SS];
+    __shared__ float ev[16 * VX_MAX_P];
+    static_assert(VX_THREADS == 8 * VX_NJ, "thread (row, block) loads a chunk's scale");
+    const int t = threadIdx.x, nb = a.W.nb, g0 = blockIdx.x, nq = (nb + VX_NJ - 1) / VX_NJ;
+    const int k = t & (VX_NJ - 1), rw = t / VX_NJ;   // block k of rows rw, rw + 8, ... of the chunk; scale row rw
+    const float* src = a.part + (size_t)g0 * 8 * P * nb;
+    float v[P];
+    uint16_t dh = 0;
+    auto load = [&](int q) {   // chunk q into registers
+        const bool in = q * VX_NJ + k < nb;
+#pragma unroll
+        for (int u = 0; u < P; u++) v[u] = in ? src[(size_t)(rw + 8 * u) * nb + q * VX_NJ + k] : 0.0f;
+        if (in) dh = a.W.scales[((size_t)g0 * nb + q * VX_NJ + k) * 8 + rw];
+    };
+    load(0);
+    float acc = 0.0f;
+    for (int q = 0; q < nq; q++) {
+        const int nbc = min(VX_NJ, nb - q * VX_NJ);
+        if (q) __syncthreads();   // the previous chunk's fold has read ss and ds
+#pragma unroll
+        for (int u = 0; u < P; u++) ss[(rw + 8 * u) * VX_SS + k] = v[u];
+        ds[rw * VX_SS + k] = h2f(dh);
+        __syncthreads();
+        if (q + 1 < nq) load(q + 1);
+        if (t < 8 * P) {
+            const float* sp = ss + t * VX_SS;
+            const float* dp = ds + (t / P) * VX_SS;
+            for (int i = 0; i < nbc; i++) acc = fmaf(dp[i], sp[i], acc);
+        }
+    }
+    table_epilogue<P, EPI, 8>(a, g0, acc, ev);
 }
 
 // scaled order (imi/core/tables.cpp:324-365, P = 12 or 6): thread (row, position) runs one chain over all columns
@@ -317,8 +419,17 @@ template <int P, int PRO, int EPI>
 hipError_t launch_vtab_p(const vtab_args& a, hipStream_t s) {
     if constexpr (P == 6 || P == 12)
         hipLaunchKernelGGL((k_vtab_scaled<P, PRO, EPI>), dim3(a.units), dim3(VX_THREADS), 0, s, a);
-    else
+    else {
+        if constexpr (EPI != VE_SWIGLU) {
+            if (a.part && a.W.nb > VX_NJ) {
+                hipLaunchKernelGGL((k_vtab_part<P, PRO>), dim3(a.units, (a.W.nb + VX_NJ - 1) / VX_NJ),
+                                   dim3(VX_THREADS), 0, s, a);
+                hipLaunchKernelGGL((k_vtab_fold<P, EPI>), dim3(a.units), dim3(VX_THREADS), 0, s, a);
+                return hipGetLastError();
+            }
+        }
         hipLaunchKernelGGL((k_vtab_gen<P, PRO, EPI>), dim3(a.units), dim3(VX_THREADS), 0, s, a);
+    }
     return hipGetLastError();
 }
 
@@ -333,6 +444,10 @@ hipError_t launch_vtab_kind(int pro, int epi, const vtab_args& a, hipStream_t s)
 }  // namespace
 
 hipError_t launch_vtab(int P, int pro, int epi, const vtab_args& a, hipStream_t s) {
+    // the input staging reads 16-byte words of every position's row and of the norm weights
+    if (a.src_ld % 4 || reinterpret_cast<uintptr_t>(a.src) % 16 ||
+        (pro == VP_NORM && reinterpret_cast<uintptr_t>(a.norm_w) % 16))
+        return hipErrorInvalidValue;
     switch (P) {
         case 2: return launch_vtab_kind<2>(pro, epi, a, s);
         case 3: return launch_vtab_kind<3>(pro, epi, a, s);

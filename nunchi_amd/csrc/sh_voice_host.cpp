@@ -69,6 +69,7 @@ struct sh_voice {
     const float2* rope_cs = nullptr;
     float *x = nullptr, *qkv = nullptr, *att = nullptr, *act = nullptr, *base = nullptr, *hid = nullptr;
     float *out = nullptr, *fb = nullptr;
+    float* part = nullptr;             // per-block sums of the o and down tables split over column chunks
     pass_in* in_dev = nullptr;
     pass_in* in_host = nullptr;        // pinned
     bool use_graph = true;
@@ -99,7 +100,7 @@ int enqueue_pass(sh_voice* v) {
         VCHK(launch_vattn(aa, v->stream));
         t = vtab_args{};
         t.eps = v->eps;
-        t.W = L.o; t.src = v->att; t.src_ld = Hq; t.out = v->x; t.out_ld = E;
+        t.W = L.o; t.src = v->att; t.src_ld = Hq; t.out = v->x; t.out_ld = E; t.part = v->part;
         t.units = units_of(P, L.o);
         VCHK(launch_vtab(P, VP_PLAIN, VE_RESID, t, v->stream));
         t = vtab_args{};
@@ -109,7 +110,7 @@ int enqueue_pass(sh_voice* v) {
         VCHK(launch_vtab(P, VP_NORM, VE_SWIGLU, t, v->stream));
         t = vtab_args{};
         t.eps = v->eps;
-        t.W = L.down; t.src = v->act; t.src_ld = I.n_ff; t.out = v->x; t.out_ld = E;
+        t.W = L.down; t.src = v->act; t.src_ld = I.n_ff; t.out = v->x; t.out_ld = E; t.part = v->part;
         t.units = units_of(P, L.down);
         VCHK(launch_vtab(P, VP_PLAIN, VE_RESID, t, v->stream));
     }
@@ -257,6 +258,8 @@ int sh_voice_load(int device, const char* path, sh_voice** out) {
     room((size_t)P * (D / 2) * sizeof(float2));
     const size_t wide = (size_t)P * std::max({E, Hq, I.n_ff, v->n_qkv, I.n_vocab});
     for (int i = 0; i < 5; i++) room(wide * 4);   // x, qkv, att, act, out
+    const size_t part_floats = (size_t)(E + 7) / 8 * 8 * P * (std::max(Hq, I.n_ff) / 32);
+    room(part_floats * 4);
     room((size_t)P * E * 4 + I.n_in * 4 * 2);
     room(sizeof(pass_in));
     hipError_t e = hipStreamCreateWithFlags(&v->stream, hipStreamNonBlocking);
@@ -326,6 +329,7 @@ int sh_voice_load(int device, const char* path, sh_voice** out) {
     v->att = reinterpret_cast<float*>(take(wide * 4));
     v->act = reinterpret_cast<float*>(take(wide * 4));
     v->out = reinterpret_cast<float*>(take(wide * 4));
+    v->part = reinterpret_cast<float*>(take(part_floats * 4));
     v->base = reinterpret_cast<float*>(take((size_t)P * E * 4 + I.n_in * 4 * 2));
     v->hid = v->base + (size_t)P * E;
     v->fb = v->hid + I.n_in;

@@ -84,6 +84,15 @@ def test_wide_inputs(model_dir):
     _play(path, 6, (8,), n_frames=1)
 
 
+def test_wide_tables_split(model_dir):
+    """o and down tables over several 1024-column chunks (attention width 1280, n_ff 3104: the last chunk ragged),
+    5 codebooks: the per-chunk block sums are folded by a second kernel in the same block order."""
+    from nunchi_amd import synth
+    path = synth.cached("voice", _shape(n_cb=5, n_head=20, n_head_kv=4, n_ff=3104, n_embd=288, n_vocab=80), 8,
+                        model_dir)
+    _play(path, 8, (2, 3), n_frames=1)
+
+
 def test_pass_arguments(tiny_voice):
     """No codebooks needed: nothing is scored; a codebook twice: the same scores twice; bad codes are refused."""
     import nunchi_amd
