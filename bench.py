@@ -87,25 +87,35 @@ def cpu_decode(path, threads, steps, b2: bool, runs: int = 1):
 
 VOICE_CTX = 4096      # slot A's KV context in the voice frame
 A_POS = 2048          # slot A's position when the timed frames start
-SCHEDULE = ((0, 1, 2, 3), (4, 5, 6, 7))   # masked passes of a frame: codebooks scored (and fixed) by each
+SCHEDULE = (4, 4)     # masked passes of a frame: codebooks scored (and fixed) by each, in a shuffled order
+TEMP, REP, REP_WIN = 0.4, 1.2, 64   # imi's sampling settings (imi/core/talk.cpp:131-133)
 
 
-def play_frames(step2, voice, tok_a, fb, frames):
+def play_frames(step2, voice, tok_a, fb, frames, pick):
     """Voice frames as imi's talk loop runs them (imi/core/talk.cpp:127-187) with slot A riding along
     (imi/core/flow.cpp:118): step2 (A: text step with scores, B: the voice brain step fed the last feedback row sum),
-    begin_frame from B's hidden state, the masked passes (each fixes its codebooks' codes; the first index of the
-    maximum stands in for sampling), then the feedback row sum. Returns per-frame seconds, the step2 and generator
-    shares, the codes of every frame and slot A's ids."""
+    begin_frame from B's hidden state, the masked passes over a shuffled codebook order (each samples its
+    codebooks' codes with temperature 0.4 and repeat penalty 1.2 over the last 64 frames: `pick`), then the feedback
+    row sum. The shuffles and uniform draws come from one seeded generator (numpy's, in place of imi's mt19937), so
+    two runs with the same scores pick the same codes; an end-of-audio pick does not end the run. Returns
+    per-frame seconds, the step2 and generator shares, the codes of every frame and slot A's ids."""
     tot, br, vo, codes_all, ids = [], [], [], [], []
+    rng = np.random.default_rng(7)
     for _ in range(frames):
+        order = rng.permutation(voice.n_cb).astype(np.int32)
+        u = rng.uniform(size=voice.n_cb)
+        window = np.array(codes_all[-REP_WIN:], np.int32).reshape(-1, voice.n_cb)
         t0 = time.perf_counter()
         tok_a, hb = step2(tok_a, fb)
         t1 = time.perf_counter()
         voice.begin_frame(hb)
         codes = np.full(voice.n_cb, -1, np.int32)
-        for need in SCHEDULE:
+        k = 0
+        for n in SCHEDULE:
+            need = order[k:k + n]
             sc = voice.pass_(codes, need)
-            codes[list(need)] = np.argmax(sc, axis=1)
+            codes[need] = pick(voice, sc, need, window, u[k:k + n])
+            k += n
         fb = voice.feedback(codes)
         t2 = time.perf_counter()
         tot.append(t2 - t0)
@@ -131,7 +141,8 @@ def gpu_voice_frames(brain_path, voice_path, frames, warmup):
         return best, hb
 
     fb = voice.feedback(np.zeros(voice.n_cb, np.int32))
-    ref = play_frames(step2, voice, int(ids[-1]), fb, frames + warmup)
+    ref = play_frames(step2, voice, int(ids[-1]), fb, frames + warmup,
+                      lambda v, sc, need, win, u: v.sample(win, u, TEMP, REP)[0])
     # the timed frames are the frames after the warmup ones, in the same run (states keep advancing)
     out = tuple(x[warmup:] for x in ref[:4]) + (ref[4][warmup:],)
     info = {"table_bytes": voice.table_bytes, "n_cb": voice.n_cb}
@@ -155,7 +166,8 @@ def cpu_voice_frames(brain_path, voice_path, threads, frames):
         return oracle.top(la), hb
 
     fb = voice.feedback(np.zeros(voice.n_cb, np.int32))
-    return play_frames(step2, voice, int(ids[-1]), fb, frames)
+    return play_frames(step2, voice, int(ids[-1]), fb, frames,
+                       lambda v, sc, need, win, u: oracle.voice_sample(sc, need, win, u, TEMP, REP)[0])
 
 
 HEAR_EMB, HEAR_TOK = 384, 64   # the hearing window: audio-encoder rows, then words
@@ -346,7 +358,8 @@ def main():
             "workload": "cfg4: step2 of the cfg2 model (slot A: text step with scores at KV context 4096, from position "
                         f"{A_POS}; slot B: voice brain step fed the feedback row sum), then the Q8_0 generator "
                         "(6 layers, hidden 1024, FFN 4096, 16/4 heads x 64, 8 codebooks x 2048) in passes of 4 + 4 "
-                        "codebooks, then the feedback row sum; host argmax in place of sampling",
+                        "codebooks in a shuffled order, each followed by sampling on the device (temperature 0.4, "
+                        "repeat penalty 1.2 over the last 64 frames), then the feedback row sum",
             "frames": int(len(ft)),
             "p50_ms": round(float(np.percentile(ft, 50)) * 1e3, 3),
             "p99_ms": round(float(np.percentile(ft, 99)) * 1e3, 3),

@@ -156,6 +156,18 @@ int sh_voice_pass(sh_voice* v, const int32_t* codes, const int32_t* need, int n_
 /* The brain's next input after a frame: the sum, codebook by codebook, of the chosen codes' feedback rows,
  * out[n_in] (voice.cpp:90-97). codes[n_cb] must all be chosen (0 <= code < n_vocab). */
 int sh_voice_feedback(sh_voice* v, const int32_t* codes, float* out);
+/* Temperature sampling with a repeat penalty of the codebooks the last sh_voice_pass scored, on the device
+ * (imi_talker::next, imi/core/talk.cpp:147-164). For score row j (codebook need[j] of that pass): every distinct
+ * code c the codebook took in hist (n_frames rows of n_cb codes, oldest first, as imi's last min(frames, rep_win)
+ * frames; codes outside [0, n_vocab) are skipped) is penalised once, l = l > 0 ? l / rep : l * rep; then
+ * p[v] = exp((double)(l[v] - max l) / temp), sum = the sum of p in code order, keep[j] = 1 - p[n_vocab - 1] / sum
+ * (the chance that this pick is not end-of-audio), and picks[j] = the first v at which r = u[j] * sum minus
+ * p[0], p[1], ... p[v] in double reaches <= 0 (n_vocab - 1 if none). u[j] in [0, 1) is the caller's uniform draw
+ * for pick j (imi draws std::uniform_real_distribution<double>(0, 1) from its std::mt19937, pick by pick, after
+ * the frame's shuffle). The penalised scores stay in the device score rows. 0 <= n_frames <= 256,
+ * n_vocab <= 4096, temp > 0, rep > 0. */
+int sh_voice_sample(sh_voice* v, const int32_t* hist, int n_frames, const double* u, float temp, float rep,
+                    int32_t* picks, double* keep);
 
 /* Synchronise the context's stream (for callers of the _dev entry points). */
 int sh_sync(sh_ctx* ctx);

@@ -25,7 +25,7 @@ EXPORTS = [
     "sh_q4_create", "sh_q4_free", "sh_q4_rows", "sh_q4_gemv", "sh_q4_gemm", "sh_q4_gemv_dev", "sh_q4_bench", "sh_q4_bench_kernel", "sh_expf", "sh_sync",
     "sh_step_trace",
     "sh_voice_load", "sh_voice_free", "sh_voice_info", "sh_voice_begin_frame", "sh_voice_base", "sh_voice_pass",
-    "sh_voice_feedback",
+    "sh_voice_feedback", "sh_voice_sample",
 ]
 
 
@@ -97,6 +97,7 @@ def load_library(path: str = LIB_PATH):
         "sh_voice_base": (i, [vp, vp]),
         "sh_voice_pass": (i, [vp, vp, vp, i, vp]),
         "sh_voice_feedback": (i, [vp, vp, vp]),
+        "sh_voice_sample": (i, [vp, vp, i, vp, f, f, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -391,6 +392,7 @@ class Voice:
             raise ValueError("codes must have n_cb entries")
         out = np.zeros((need.size, self.n_vocab), np.float32)
         _check(_lib.sh_voice_pass(self.h, _p(codes), _p(need), int(need.size), _p(out)))
+        self._scored = int(need.size)
         return out
 
     def feedback(self, codes) -> np.ndarray:
@@ -398,8 +400,24 @@ class Voice:
         if codes.size != self.n_cb:
             raise ValueError("codes must have n_cb entries")
         out = np.zeros(self.n_in, np.float32)
+        self._scored = -1
         _check(_lib.sh_voice_feedback(self.h, _p(codes), _p(out)))
         return out
+
+    def sample(self, hist, u, temp: float = 0.4, rep: float = 1.2):
+        """Temperature sampling with a repeat penalty of the codebooks the last pass_ scored, on the device
+        (imi_talker::next, imi/core/talk.cpp:147-164): hist [n_frames][n_cb] codes of the previous frames (oldest
+        first; imi passes its last min(frames, rep_win = 64)), u [n_need] uniform draws in [0, 1), one per pick.
+        Returns (picks [n_need] int32, keep [n_need] float64: 1 - p[end-of-audio] / sum)."""
+        hist = np.ascontiguousarray(np.asarray(hist, np.int32).reshape(-1, self.n_cb))
+        u = np.ascontiguousarray(u, np.float64)
+        if u.size != getattr(self, "_scored", -1):
+            raise ValueError("u must hold one draw per codebook the last pass scored")
+        picks = np.zeros(max(u.size, 1), np.int32)
+        keep = np.zeros(max(u.size, 1), np.float64)
+        _check(_lib.sh_voice_sample(self.h, _p(hist), hist.shape[0], _p(u), float(temp), float(rep), _p(picks),
+                                    _p(keep)))
+        return picks[:u.size], keep[:u.size]
 
 
 @atexit.register

@@ -87,7 +87,25 @@ struct vfeed_args {
     float* out;             // [n_in]
 };
 
+constexpr int VS_MAX_HIST = 256;   // history frames the repeat penalty may look back over
+constexpr int VS_MAX_V = 4096;     // codes per codebook the sampler takes (its row lives in LDS)
+
+// temperature sampling with a repeat penalty of one pass's scored codebooks (imi/core/talk.cpp:147-164)
+struct vsample_args {
+    float* scores;          // [n_need][V] the pass's scores; the penalised rows are written back
+    int V, n_cb;
+    const int32_t* need;    // device [n_need]: codebook of score row j
+    const int32_t* n_need;  // device scalar
+    const int32_t* hist;    // device [n_frames][n_cb] codes of the previous frames, oldest first
+    int n_frames;
+    const double* u;        // device [n_need] uniform draws in [0, 1)
+    float temp, rep;
+    int32_t* picks;         // device [n_need]
+    double* keep;           // device [n_need] 1 - p[V - 1] / sum
+};
+
 hipError_t launch_vtab(int P, int pro, int epi, const vtab_args& a, hipStream_t s);
+hipError_t launch_vsample(const vsample_args& a, int max_need, hipStream_t s);
 hipError_t launch_vone(const vone_args& a, int n_sets, int cols, hipStream_t s);
 hipError_t launch_vattn(const vattn_args& a, hipStream_t s);
 hipError_t launch_vembed(const vembed_args& a, hipStream_t s);

@@ -415,6 +415,68 @@ __global__ __launch_bounds__(VX_THREADS) void k_vfeed(vfeed_args a) {
     a.out[i] = o;
 }
 
+// One workgroup per scored codebook j (imi_talker::next, imi/core/talk.cpp:147-164). The row is read into LDS;
+// thread 0 applies the repeat penalty once per distinct code of the history window (oldest frame first), the
+// maximum is reduced across the workgroup (exact), p[v] = exp((double)(l[v] - max) / temp) is formed in parallel,
+// and thread 0 then runs imi's two in-order loops in double: the sum, and r = u * sum minus p[0], p[1], ... until
+// r <= 0, which names the pick.
+__global__ __launch_bounds__(256) void k_vsample(vsample_args a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char vs_lds[];
+    double* ps = reinterpret_cast<double*>(vs_lds);                 // [V]
+    float* lf = reinterpret_cast<float*>(ps + a.V);                 // [V]
+    int* hc = reinterpret_cast<int*>(lf + a.V);                     // [n_frames]
+    unsigned char* seen = reinterpret_cast<unsigned char*>(hc + VS_MAX_HIST);   // [V]
+    __shared__ float wmax[4];
+    const int j = blockIdx.x, t = threadIdx.x, V = a.V;
+    if (j >= *a.n_need) return;
+    const int cb = a.need[j];
+    float* l = a.scores + (size_t)j * V;
+    for (int v = t; v < V; v += 256) {
+        lf[v] = l[v];
+        seen[v] = 0;
+    }
+    for (int f = t; f < a.n_frames; f += 256) hc[f] = a.hist[(size_t)f * a.n_cb + cb];
+    __syncthreads();
+    if (t == 0) {
+        for (int f = 0; f < a.n_frames; f++) {
+            const int c = hc[f];
+            if (c >= 0 && c < V && !seen[c]) {
+                seen[c] = 1;
+                lf[c] = lf[c] > 0 ? lf[c] / a.rep : lf[c] * a.rep;
+            }
+        }
+    }
+    __syncthreads();
+    float m = -INFINITY;
+    for (int v = t; v < V; v += 256) m = fmaxf(m, lf[v]);
+    m = wave_max(m);
+    if ((t & 63) == 0) wmax[t >> 6] = m;
+    __syncthreads();
+    const float lmax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const double temp = a.temp;
+    for (int v = t; v < V; v += 256) {
+        ps[v] = exp((double)(lf[v] - lmax) / temp);
+        l[v] = lf[v];
+    }
+    __syncthreads();
+    if (t == 0) {
+        double sum = 0;
+#pragma unroll 8
+        for (int v = 0; v < V; v++) sum += ps[v];
+        double r = a.u[j] * sum;
+        int pick = V - 1;
+        for (int v = 0; v < V; v++) {
+            r -= ps[v];
+            if (r <= 0) {
+                pick = v;
+                break;
+            }
+        }
+        a.picks[j] = pick;
+        a.keep[j] = 1.0 - ps[V - 1] / sum;
+    }
+}
+
 template <int P, int PRO, int EPI>
 hipError_t launch_vtab_p(const vtab_args& a, hipStream_t s) {
     if constexpr (P == 6 || P == 12)
@@ -442,6 +504,13 @@ hipError_t launch_vtab_kind(int pro, int epi, const vtab_args& a, hipStream_t s)
 }
 
 }  // namespace
+
+hipError_t launch_vsample(const vsample_args& a, int max_need, hipStream_t s) {
+    if (a.V < 1 || a.V > VS_MAX_V || a.n_frames < 0 || a.n_frames > VS_MAX_HIST || max_need < 1) return hipErrorInvalidValue;
+    const size_t lds = (size_t)a.V * 8 + (size_t)a.V * 4 + VS_MAX_HIST * 4 + ((a.V + 15) & ~15);
+    hipLaunchKernelGGL(k_vsample, dim3(max_need), dim3(256), lds, s, a);
+    return hipGetLastError();
+}
 
 hipError_t launch_vtab(int P, int pro, int epi, const vtab_args& a, hipStream_t s) {
     // the input staging reads 16-byte words of every position's row and of the norm weights

@@ -7,6 +7,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstddef>
 #include <cstdlib>
 #include <cstring>
 #include <string>
@@ -52,6 +53,13 @@ struct pass_in {               // one host -> device copy per pass
     int32_t codes[VX_MAX_P];
     int32_t need[VX_MAX_P];
 };
+
+struct sample_io {             // the sampler's inputs (host -> device) and outputs (device -> host)
+    double u[VX_MAX_P];
+    double keep[VX_MAX_P];
+    int32_t picks[VX_MAX_P];
+    int32_t hist[VS_MAX_HIST * VX_MAX_P];   // only the frames given are copied
+};
 }  // namespace
 
 struct sh_voice {
@@ -72,6 +80,9 @@ struct sh_voice {
     float* part = nullptr;             // per-block sums of the o and down tables split over column chunks
     pass_in* in_dev = nullptr;
     pass_in* in_host = nullptr;        // pinned
+    sample_io* smp_dev = nullptr;
+    sample_io* smp_host = nullptr;     // pinned
+    int last_need = -1;                // codebooks the last pass scored (-1: no pass since the frame began)
     bool use_graph = true;
     hipGraphExec_t graph = nullptr;
 };
@@ -126,6 +137,7 @@ void release(sh_voice* v) {
     if (v->graph) (void)hipGraphExecDestroy(v->graph);
     if (v->mem) (void)hipFree(v->mem);
     if (v->in_host) (void)hipHostFree(v->in_host);
+    if (v->smp_host) (void)hipHostFree(v->smp_host);
     if (v->stream) (void)hipStreamDestroy(v->stream);
     delete v;
 }
@@ -262,9 +274,11 @@ int sh_voice_load(int device, const char* path, sh_voice** out) {
     room(part_floats * 4);
     room((size_t)P * E * 4 + I.n_in * 4 * 2);
     room(sizeof(pass_in));
+    room(sizeof(sample_io));
     hipError_t e = hipStreamCreateWithFlags(&v->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipMalloc(&v->mem, need);
     if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&v->in_host), sizeof(pass_in), hipHostMallocDefault);
+    if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&v->smp_host), sizeof(sample_io), hipHostMallocDefault);
     if (e != hipSuccess) {
         release(v);
         return set_error(SH_E_NOMEM, std::string("sh_voice_load: device allocation: ") + hipGetErrorString(e));
@@ -334,6 +348,7 @@ int sh_voice_load(int device, const char* path, sh_voice** out) {
     v->hid = v->base + (size_t)P * E;
     v->fb = v->hid + I.n_in;
     v->in_dev = reinterpret_cast<pass_in*>(take(sizeof(pass_in)));
+    v->smp_dev = reinterpret_cast<sample_io*>(take(sizeof(sample_io)));
     if (used > need) {   // the carving above must follow the sizing pass piece by piece
         release(v);
         return set_error(SH_E_NOMEM, "sh_voice_load: internal layout error");
@@ -398,6 +413,7 @@ int sh_voice_pass(sh_voice* v, const int32_t* codes, const int32_t* need, int n_
     for (int j = 0; j < n_need; j++)
         if (need[j] < 0 || need[j] >= P) return set_error(SH_E_ARG, "sh_voice_pass: codebook out of range");
     VCHK(hipSetDevice(v->device));
+    v->last_need = -1;
     pass_in& in = *v->in_host;
     in.n_need = n_need;
     for (int i = 0; i < VX_MAX_P; i++) {
@@ -424,6 +440,43 @@ int sh_voice_pass(sh_voice* v, const int32_t* codes, const int32_t* need, int n_
     }
     if (n_need) VCHK(hipMemcpyAsync(out, v->out, (size_t)n_need * v->info.n_vocab * 4, hipMemcpyDeviceToHost, v->stream));
     VCHK(hipStreamSynchronize(v->stream));
+    v->last_need = n_need;
+    return SH_OK;
+}
+
+int sh_voice_sample(sh_voice* v, const int32_t* hist, int n_frames, const double* u, float temp, float rep,
+                    int32_t* picks, double* keep) {
+    if (!v || n_frames < 0 || n_frames > VS_MAX_HIST || (n_frames && !hist))
+        return set_error(SH_E_ARG, "sh_voice_sample: bad argument (0 <= n_frames <= 256)");
+    if (v->last_need < 0) return set_error(SH_E_ARG, "sh_voice_sample: no pass has scored codebooks yet");
+    const int n = v->last_need;
+    if (n && (!u || !picks || !keep)) return set_error(SH_E_ARG, "sh_voice_sample: bad argument");
+    if (!(temp > 0.0f) || !(rep > 0.0f)) return set_error(SH_E_ARG, "sh_voice_sample: temp and rep must be > 0");
+    if (v->info.n_vocab > VS_MAX_V) return set_error(SH_E_SHAPE, "sh_voice_sample: more than 4096 codes per codebook");
+    for (int j = 0; j < n; j++)
+        if (!(u[j] >= 0.0 && u[j] < 1.0)) return set_error(SH_E_ARG, "sh_voice_sample: u must lie in [0, 1)");
+    if (!n) return SH_OK;
+    VCHK(hipSetDevice(v->device));
+    sample_io& io = *v->smp_host;
+    const int P = v->info.n_cb;
+    for (int j = 0; j < n; j++) io.u[j] = u[j];
+    memcpy(io.hist, hist, (size_t)n_frames * P * sizeof(int32_t));
+    const size_t in_bytes = offsetof(sample_io, hist) + (size_t)n_frames * P * sizeof(int32_t);
+    VCHK(hipMemcpyAsync(v->smp_dev, &io, in_bytes, hipMemcpyHostToDevice, v->stream));
+    vsample_args a{};
+    a.scores = v->out; a.V = v->info.n_vocab; a.n_cb = P;
+    a.need = v->in_dev->need; a.n_need = &v->in_dev->n_need;
+    a.hist = v->smp_dev->hist; a.n_frames = n_frames;
+    a.u = v->smp_dev->u; a.temp = temp; a.rep = rep;
+    a.picks = v->smp_dev->picks; a.keep = v->smp_dev->keep;
+    VCHK(launch_vsample(a, n, v->stream));
+    VCHK(hipMemcpyAsync(&io.keep, &v->smp_dev->keep, offsetof(sample_io, hist) - offsetof(sample_io, keep),
+                        hipMemcpyDeviceToHost, v->stream));
+    VCHK(hipStreamSynchronize(v->stream));
+    for (int j = 0; j < n; j++) {
+        picks[j] = io.picks[j];
+        keep[j] = io.keep[j];
+    }
     return SH_OK;
 }
 
@@ -436,6 +489,7 @@ int sh_voice_feedback(sh_voice* v, const int32_t* codes, float* out) {
     pass_in& in = *v->in_host;
     for (int i = 0; i < VX_MAX_P; i++) in.codes[i] = i < P ? codes[i] : 0;
     in.n_need = 0;
+    v->last_need = -1;   // the device copy of the pass's need list is overwritten: nothing left to sample
     VCHK(hipMemcpyAsync(v->in_dev, &in, sizeof(pass_in), hipMemcpyHostToDevice, v->stream));
     vfeed_args a{v->feed_rows, v->feed_row_bytes, v->info.n_in, v->info.n_vocab, P, v->in_dev->codes, v->fb};
     VCHK(launch_vfeed(a, v->stream));

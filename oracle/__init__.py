@@ -83,6 +83,8 @@ def lib():
         "orc_voice_base": (None, [vp, _f32p]),
         "orc_voice_pass": (None, [vp, _i32p, _i32p, i, _f32p]),
         "orc_voice_feedback": (None, [vp, _i32p, _f32p]),
+        "orc_voice_sample": (None, [_f32p, i, i, _i32p, _i32p, i, i, C.POINTER(C.c_double), f, f, _i32p,
+                                    C.POINTER(C.c_double)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -289,6 +291,24 @@ class Voice:
         out = np.zeros(self.n_in, np.float32)
         lib().orc_voice_feedback(self.h, np.ascontiguousarray(codes, np.int32), out)
         return out
+
+
+def voice_sample(scores, cbs, hist, u, temp=0.4, rep=1.2):
+    """imi_talker::next's picks (imi/core/talk.cpp:147-164) of score rows scores[j] (codebook cbs[j]) given the
+    history window hist [n_frames][n_cb] (oldest first) and one uniform draw u[j] per pick. Returns (picks,
+    keep = 1 - p[eos] / sum, the penalised scores)."""
+    l = np.array(scores, np.float32, order="C", copy=True)
+    n, V = l.shape
+    hist = np.ascontiguousarray(hist, np.int32)
+    n_cb = hist.shape[1] if hist.ndim == 2 and hist.size else 1
+    n_frames = hist.shape[0] if hist.size else 0
+    u = np.ascontiguousarray(u, np.float64)
+    picks = np.zeros(max(n, 1), np.int32)
+    keep = np.zeros(max(n, 1), np.float64)
+    lib().orc_voice_sample(l, n, V, np.ascontiguousarray(cbs, np.int32), hist.reshape(-1) if hist.size else
+                           np.zeros(1, np.int32), n_frames, n_cb, u.ctypes.data_as(C.POINTER(C.c_double)),
+                           float(temp), float(rep), picks, keep.ctypes.data_as(C.POINTER(C.c_double)))
+    return picks[:n], keep[:n], l
 
 
 def cut(x: np.ndarray):

@@ -1192,4 +1192,32 @@ void orc_voice_pass(void* h, const int32_t* codes, const int32_t* need, int n_ne
 }
 void orc_voice_feedback(void* h, const int32_t* codes, float* out) { ((voice*)h)->feedback(codes, out); }
 
+// imi_talker::next's pick of one codebook (imi/core/talk.cpp:147-164) for each score row j of a pass: the repeat
+// penalty over the history window (each distinct code once), then temperature probabilities in double, their sum
+// in code order, keep = 1 - p[eos] / sum, and the pick by subtracting p in code order from r = u * sum. The
+// uniform draw u[j] replaces imi's std::uniform_real_distribution<double>(0, 1)(rng); rows are penalised in place.
+void orc_voice_sample(float* scores, int n, int V, const int32_t* cbs, const int32_t* hist, int n_frames, int n_cb,
+                      const double* u, float temp, float rep, int32_t* picks, double* keep) {
+    const int eos = V - 1;
+    std::vector<char> seen(V);
+    std::vector<double> p(V);
+    for (int j = 0; j < n; j++) {
+        float* l = scores + (size_t)j * V;
+        const int cb = cbs[j];
+        std::fill(seen.begin(), seen.end(), 0);
+        for (int f = 0; f < n_frames; f++) {
+            const int c = hist[(size_t)f * n_cb + cb];
+            if (c >= 0 && c < V && !seen[c]) { seen[c] = 1; l[c] = l[c] > 0 ? l[c] / rep : l[c] * rep; }
+        }
+        const float lmax = *std::max_element(l, l + V);
+        double sum = 0;
+        for (int v = 0; v < V; v++) { p[v] = std::exp((double)(l[v] - lmax) / temp); sum += p[v]; }
+        keep[j] = 1.0 - p[eos] / sum;
+        double r = u[j] * sum;
+        int pick = V - 1;
+        for (int v = 0; v < V; v++) { r -= p[v]; if (r <= 0) { pick = v; break; } }
+        picks[j] = pick;
+    }
+}
+
 }  // extern "C"

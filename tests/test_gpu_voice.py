@@ -124,3 +124,37 @@ def test_full_voice_frame(model_dir):
     from nunchi_amd import synth
     path = synth.cached("voice", synth.VOICE, 1, model_dir)
     _play(path, 11, (4, 4), n_frames=1, threads=8)
+
+
+def test_device_sampling(tiny_voice):
+    """sh_voice_sample against the oracle's pick (imi/core/talk.cpp:147-164) on the same pass scores, in a talk loop:
+    a shuffled codebook order per frame, passes of 4 + 4, the repeat-penalty window of the last 64 frames (seeded
+    with 70 frames of codes that repeat and hold -1), temperatures 0.4 and 1.5, rep 1.2. Picks are equal; keep
+    (1 - p[end-of-audio] / sum) agrees within 1e-12 (the device's double exp and the C library's may differ in the
+    last place)."""
+    import nunchi_amd
+    import oracle
+    g = nunchi_amd.Voice(tiny_voice)
+    rng = np.random.default_rng(21)
+    hist = [rng.integers(-1, 12, g.n_cb).astype(np.int32) for _ in range(70)]
+    for f in range(6):
+        temp = 0.4 if f % 2 == 0 else 1.5
+        order = rng.permutation(g.n_cb).astype(np.int32)
+        codes = np.full(g.n_cb, -1, np.int32)
+        g.begin_frame(rng.standard_normal(g.n_in).astype(np.float32))
+        window = np.array(hist[-64:], np.int32)
+        for k in (0, 4):
+            need = order[k:k + 4]
+            sg = g.pass_(codes, need)
+            u = rng.uniform(size=4)
+            picks, keep = g.sample(window, u, temp, 1.2)
+            po, ko, _ = oracle.voice_sample(sg, need, window, u, temp, 1.2)
+            assert np.array_equal(picks, po), f"frame {f}, codebooks {need.tolist()}: {picks} vs {po}"
+            assert np.all(np.abs(keep - ko) <= 1e-12), f"frame {f}: keep {keep} vs {ko}"
+            codes[need] = picks
+        hist.append(codes.copy())
+    # the draws must lie in [0, 1)
+    g.pass_(codes, [0, 1])
+    with pytest.raises(nunchi_amd.SeoulError):
+        g.sample(np.zeros((0, g.n_cb), np.int32), [0.5, 1.0])
+    assert g.sample(np.zeros((0, g.n_cb), np.int32), [0.0, 0.0])[0].tolist() == [0, 0]
