@@ -192,6 +192,14 @@ struct imi_voice {
         std::vector<int32_t> nd(need.begin(), need.end());
         if (sh_voice_pass(v, codes, nd.data(), (int)nd.size(), out.data()) != SH_OK) report("pass");
     }
+    // imi_talker::next's picks for the codebooks the last pass scored (imi/core/talk.cpp:147-164), on the device:
+    // hist = the last n_frames frames of codes (n_cb each), u = one uniform draw in [0, 1) per pick, drawn by the
+    // caller from its generator; keep[j] = 1 - p[end-of-audio] / sum. The scores `pass` returned are not changed.
+    bool sample(const int32_t* hist, int n_frames, const double* u, float temp, float rep, int32_t* picks,
+                double* keep) {
+        if (sh_voice_sample(v, hist, n_frames, u, temp, rep, picks, keep) != SH_OK) return report("sample");
+        return true;
+    }
 
 private:
     sh_voice* v = nullptr;
