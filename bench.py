@@ -95,8 +95,8 @@ def play_frames(step2, voice, tok_a, fb, frames, pick):
     """Voice frames as imi's talk loop runs them (imi/core/talk.cpp:127-187) with slot A riding along
     (imi/core/flow.cpp:118): step2 (A: text step with scores, B: the voice brain step fed the last feedback row sum),
     begin_frame from B's hidden state, the masked passes over a shuffled codebook order (each samples its
-    codebooks' codes with temperature 0.4 and repeat penalty 1.2 over the last 64 frames: `pick`), then the feedback
-    row sum. The shuffles and uniform draws come from one seeded generator (numpy's, in place of imi's mt19937), so
+    codebooks' codes with temperature 0.4 and repeat penalty 1.2 over the last 64 frames: `pick` runs the pass
+    and the sampling), then the feedback row sum. The shuffles and uniform draws come from one seeded generator (numpy's, in place of imi's mt19937), so
     two runs with the same scores pick the same codes; an end-of-audio pick does not end the run. Returns
     per-frame seconds, the step2 and generator shares, the codes of every frame and slot A's ids."""
     tot, br, vo, codes_all, ids = [], [], [], [], []
@@ -113,8 +113,7 @@ def play_frames(step2, voice, tok_a, fb, frames, pick):
         k = 0
         for n in SCHEDULE:
             need = order[k:k + n]
-            sc = voice.pass_(codes, need)
-            codes[need] = pick(voice, sc, need, window, u[k:k + n])
+            codes[need] = pick(voice, codes, need, window, u[k:k + n])
             k += n
         fb = voice.feedback(codes)
         t2 = time.perf_counter()
@@ -142,7 +141,8 @@ def gpu_voice_frames(brain_path, voice_path, frames, warmup):
 
     fb = voice.feedback(np.zeros(voice.n_cb, np.int32))
     ref = play_frames(step2, voice, int(ids[-1]), fb, frames + warmup,
-                      lambda v, sc, need, win, u: v.sample(win, u, TEMP, REP)[0])
+                      lambda v, codes, need, win, u: (v.pass_(codes, need, scores=False),
+                                                      v.sample(win, u, TEMP, REP)[0])[1])
     # the timed frames are the frames after the warmup ones, in the same run (states keep advancing)
     out = tuple(x[warmup:] for x in ref[:4]) + (ref[4][warmup:],)
     info = {"table_bytes": voice.table_bytes, "n_cb": voice.n_cb}
@@ -167,7 +167,8 @@ def cpu_voice_frames(brain_path, voice_path, threads, frames):
 
     fb = voice.feedback(np.zeros(voice.n_cb, np.int32))
     return play_frames(step2, voice, int(ids[-1]), fb, frames,
-                       lambda v, sc, need, win, u: oracle.voice_sample(sc, need, win, u, TEMP, REP)[0])
+                       lambda v, codes, need, win, u: oracle.voice_sample(v.pass_(codes, need), need, win, u, TEMP,
+                                                                          REP)[0])
 
 
 HEAR_EMB, HEAR_TOK = 384, 64   # the hearing window: audio-encoder rows, then words

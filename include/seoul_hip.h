@@ -151,7 +151,8 @@ int sh_voice_begin_frame(sh_voice* v, const float* hidden);
 /* The frame's projected input, [n_cb][n_embd] (imi_voice::base, voice.h:30). */
 int sh_voice_base(sh_voice* v, float* out);
 /* One masked pass (voice.cpp:113-206): codes[n_cb], < 0 = still masked; out[n_need][n_vocab] gets the scores of
- * codebooks need[0..n_need) (0 <= n_need <= n_cb). */
+ * codebooks need[0..n_need) (0 <= n_need <= n_cb). out may be NULL: the scores then stay on the device for
+ * sh_voice_sample and the call returns without waiting for the pass (its errors show at the next call that waits). */
 int sh_voice_pass(sh_voice* v, const int32_t* codes, const int32_t* need, int n_need, float* out);
 /* The brain's next input after a frame: the sum, codebook by codebook, of the chosen codes' feedback rows,
  * out[n_in] (voice.cpp:90-97). codes[n_cb] must all be chosen (0 <= code < n_vocab). */

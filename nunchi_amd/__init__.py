@@ -385,12 +385,14 @@ class Voice:
         _check(_lib.sh_voice_base(self.h, _p(out)))
         return out
 
-    def pass_(self, codes, need) -> np.ndarray:
+    def pass_(self, codes, need, scores: bool = True):
+        """One masked pass; returns the scores [len(need)][n_vocab], or None with scores=False (they stay on the
+        device for sample(), and the call does not wait for the pass)."""
         codes = np.ascontiguousarray(codes, np.int32)
         need = np.ascontiguousarray(need, np.int32)
         if codes.size != self.n_cb:
             raise ValueError("codes must have n_cb entries")
-        out = np.zeros((need.size, self.n_vocab), np.float32)
+        out = np.zeros((need.size, self.n_vocab), np.float32) if scores else None
         _check(_lib.sh_voice_pass(self.h, _p(codes), _p(need), int(need.size), _p(out)))
         self._scored = int(need.size)
         return out

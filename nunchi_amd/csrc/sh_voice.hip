@@ -115,16 +115,12 @@ __global__ __launch_bounds__(VX_THREADS) void k_vtab_gen(vtab_args a) {
     __shared__ float ev[16 * VX_MAX_P];
     const int t = threadIdx.x, r8 = t & 7, jl = t >> 3;
     const int nb = a.W.nb, g0 = blockIdx.x * R;
-    if (PRO == VP_NORM) {
-        position_scales<P>(a, scl);
-        __syncthreads();
-    }
     float acc = 0.0f;
     for (int q = 0; q * VX_NJ < nb; q++) {
         const int nbc = min(VX_NJ, nb - q * VX_NJ), j = q * VX_NJ + jl;
         u32x4 w[R][2];
         uint16_t dh[R];
-        if (jl < nbc) {   // codes and scales first: their loads overlap the input staging
+        if (jl < nbc) {   // codes and scales first: their loads overlap the norm scales and the input staging
 #pragma unroll
             for (int g = 0; g < R; g++) {
                 const size_t blk = ((size_t)(g0 + g) * nb + j) * 8 + r8;
@@ -133,6 +129,10 @@ __global__ __launch_bounds__(VX_THREADS) void k_vtab_gen(vtab_args a) {
                 w[g][1] = cp[1];
                 dh[g] = a.W.scales[blk];
             }
+        }
+        if (PRO == VP_NORM && q == 0) {
+            position_scales<P>(a, scl);
+            __syncthreads();
         }
         if (q) __syncthreads();   // the previous chunk's fold has read ss and ds
         stage_chunk<P, PRO>(xs, a, q, nbc, scl);

@@ -405,7 +405,7 @@ int sh_voice_base(sh_voice* v, float* out) {
 }
 
 int sh_voice_pass(sh_voice* v, const int32_t* codes, const int32_t* need, int n_need, float* out) {
-    if (!v || !codes || n_need < 0 || n_need > v->info.n_cb || (n_need && (!need || !out)))
+    if (!v || !codes || n_need < 0 || n_need > v->info.n_cb || (n_need && !need))
         return set_error(SH_E_ARG, "sh_voice_pass: bad argument (0 <= n_need <= n_cb)");
     const int P = v->info.n_cb;
     for (int i = 0; i < P; i++)
@@ -438,8 +438,10 @@ int sh_voice_pass(sh_voice* v, const int32_t* codes, const int32_t* need, int n_
         const int rc = enqueue_pass(v);
         if (rc != SH_OK) return rc;
     }
-    if (n_need) VCHK(hipMemcpyAsync(out, v->out, (size_t)n_need * v->info.n_vocab * 4, hipMemcpyDeviceToHost, v->stream));
-    VCHK(hipStreamSynchronize(v->stream));
+    if (out) {
+        if (n_need) VCHK(hipMemcpyAsync(out, v->out, (size_t)n_need * v->info.n_vocab * 4, hipMemcpyDeviceToHost, v->stream));
+        VCHK(hipStreamSynchronize(v->stream));
+    }
     v->last_need = n_need;
     return SH_OK;
 }

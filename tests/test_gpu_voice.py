@@ -146,6 +146,8 @@ def test_device_sampling(tiny_voice):
         for k in (0, 4):
             need = order[k:k + 4]
             sg = g.pass_(codes, need)
+            if k:   # the same pass again, its scores left on the device and not waited for
+                assert g.pass_(codes, need, scores=False) is None
             u = rng.uniform(size=4)
             picks, keep = g.sample(window, u, temp, 1.2)
             po, ko, _ = oracle.voice_sample(sg, need, window, u, temp, 1.2)
