@@ -415,17 +415,19 @@ __global__ __launch_bounds__(VX_THREADS) void k_vfeed(vfeed_args a) {
     a.out[i] = o;
 }
 
-// One workgroup per scored codebook j (imi_talker::next, imi/core/talk.cpp:147-164). The row is read into LDS;
-// thread 0 applies the repeat penalty once per distinct code of the history window (oldest frame first), the
-// maximum is reduced across the workgroup (exact), p[v] = exp((double)(l[v] - max) / temp) is formed in parallel,
-// and thread 0 then runs imi's two in-order loops in double: the sum, and r = u * sum minus p[0], p[1], ... until
-// r <= 0, which names the pick.
+// One workgroup per scored codebook j (imi_talker::next, imi/core/talk.cpp:147-164). The row is read into LDS; the
+// repeat penalty goes once to each distinct code of the history window: every frame offers its index to first[c]
+// (an LDS minimum), and the frame that holds the minimum applies the penalty. The maximum is reduced across the
+// workgroup (exact in any order), p[v] = exp((double)(l[v] - max) / temp) is formed in parallel, and thread 0 then
+// runs imi's two in-order loops in double: the sum, and r = u * sum minus p[0], p[1], ... until r <= 0, which names
+// the pick. Thread 0 takes p 16 values at a time: the LDS reads overlap, and the pick loop tests a block at once.
 __global__ __launch_bounds__(256) void k_vsample(vsample_args a) {
+    constexpr int VB = 16;
     extern __shared__ __attribute__((aligned(16))) unsigned char vs_lds[];
     double* ps = reinterpret_cast<double*>(vs_lds);                 // [V]
+    int* first = reinterpret_cast<int*>(vs_lds);                    // [V], in ps's room until p is formed
     float* lf = reinterpret_cast<float*>(ps + a.V);                 // [V]
-    int* hc = reinterpret_cast<int*>(lf + a.V);                     // [n_frames]
-    unsigned char* seen = reinterpret_cast<unsigned char*>(hc + VS_MAX_HIST);   // [V]
+    int* hc = reinterpret_cast<int*>(lf + a.V);                     // [VS_MAX_HIST]
     __shared__ float wmax[4];
     const int j = blockIdx.x, t = threadIdx.x, V = a.V;
     if (j >= *a.n_need) return;
@@ -433,18 +435,18 @@ __global__ __launch_bounds__(256) void k_vsample(vsample_args a) {
     float* l = a.scores + (size_t)j * V;
     for (int v = t; v < V; v += 256) {
         lf[v] = l[v];
-        seen[v] = 0;
+        first[v] = VS_MAX_HIST;
     }
     for (int f = t; f < a.n_frames; f += 256) hc[f] = a.hist[(size_t)f * a.n_cb + cb];
     __syncthreads();
-    if (t == 0) {
-        for (int f = 0; f < a.n_frames; f++) {
-            const int c = hc[f];
-            if (c >= 0 && c < V && !seen[c]) {
-                seen[c] = 1;
-                lf[c] = lf[c] > 0 ? lf[c] / a.rep : lf[c] * a.rep;
-            }
-        }
+    for (int f = t; f < a.n_frames; f += 256) {
+        const int c = hc[f];
+        if (c >= 0 && c < V) atomicMin(&first[c], f);
+    }
+    __syncthreads();
+    for (int f = t; f < a.n_frames; f += 256) {
+        const int c = hc[f];
+        if (c >= 0 && c < V && first[c] == f) lf[c] = lf[c] > 0 ? lf[c] / a.rep : lf[c] * a.rep;
     }
     __syncthreads();
     float m = -INFINITY;
@@ -460,18 +462,39 @@ __global__ __launch_bounds__(256) void k_vsample(vsample_args a) {
     }
     __syncthreads();
     if (t == 0) {
+        const int VF = V & ~(VB - 1);   // whole blocks of VB codes; the rest one by one
         double sum = 0;
-#pragma unroll 8
-        for (int v = 0; v < V; v++) sum += ps[v];
-        double r = a.u[j] * sum;
-        int pick = V - 1;
-        for (int v = 0; v < V; v++) {
-            r -= ps[v];
-            if (r <= 0) {
-                pick = v;
-                break;
-            }
+        for (int v0 = 0; v0 < VF; v0 += VB) {
+            double b[VB];
+#pragma unroll
+            for (int i = 0; i < VB; i++) b[i] = ps[v0 + i];
+#pragma unroll
+            for (int i = 0; i < VB; i++) sum += b[i];
         }
+        for (int v = VF; v < V; v++) sum += ps[v];
+        double r = a.u[j] * sum;
+        int pick = -1;
+        // per block: the VB subtractions in order (no branch), then the first partial r <= 0 among them; the
+        // subtractions past that one change nothing, as imi stops there
+        for (int v0 = 0; v0 < VF && pick < 0; v0 += VB) {
+            double b[VB], rr[VB];
+#pragma unroll
+            for (int i = 0; i < VB; i++) b[i] = ps[v0 + i];
+#pragma unroll
+            for (int i = 0; i < VB; i++) {
+                r -= b[i];
+                rr[i] = r;
+            }
+            int hit = VB;
+#pragma unroll
+            for (int i = VB - 1; i >= 0; i--) hit = rr[i] <= 0 ? i : hit;
+            if (hit < VB) pick = v0 + hit;
+        }
+        for (int v = VF; v < V && pick < 0; v++) {
+            r -= ps[v];
+            if (r <= 0) pick = v;
+        }
+        if (pick < 0) pick = V - 1;
         a.picks[j] = pick;
         a.keep[j] = 1.0 - ps[V - 1] / sum;
     }
@@ -507,7 +530,7 @@ hipError_t launch_vtab_kind(int pro, int epi, const vtab_args& a, hipStream_t s)
 
 hipError_t launch_vsample(const vsample_args& a, int max_need, hipStream_t s) {
     if (a.V < 1 || a.V > VS_MAX_V || a.n_frames < 0 || a.n_frames > VS_MAX_HIST || max_need < 1) return hipErrorInvalidValue;
-    const size_t lds = (size_t)a.V * 8 + (size_t)a.V * 4 + VS_MAX_HIST * 4 + ((a.V + 15) & ~15);
+    const size_t lds = (size_t)a.V * 8 + (size_t)a.V * 4 + VS_MAX_HIST * 4;
     hipLaunchKernelGGL(k_vsample, dim3(max_need), dim3(256), lds, s, a);
     return hipGetLastError();
 }

@@ -160,3 +160,24 @@ def test_device_sampling(tiny_voice):
     with pytest.raises(nunchi_amd.SeoulError):
         g.sample(np.zeros((0, g.n_cb), np.int32), [0.5, 1.0])
     assert g.sample(np.zeros((0, g.n_cb), np.int32), [0.0, 0.0])[0].tolist() == [0, 0]
+
+
+def test_device_sampling_ragged_vocab(model_dir):
+    """90 codes per codebook (not a multiple of the sampler's 16-code blocks): draws near 1 land in the last,
+    partial block; picks equal the oracle's."""
+    import nunchi_amd
+    import oracle
+    from nunchi_amd import synth
+    path = synth.cached("voice", _shape(n_vocab=90), 9, model_dir)
+    g = nunchi_amd.Voice(path)
+    rng = np.random.default_rng(9)
+    codes = np.full(g.n_cb, -1, np.int32)
+    g.begin_frame(rng.standard_normal(g.n_in).astype(np.float32))
+    hist = rng.integers(0, 90, (5, g.n_cb)).astype(np.int32)
+    for u in ([0.999999, 0.99, 0.5, 0.0], [1.0 - 2.0 ** -30, 0.75, 0.25, 0.9999]):
+        need = np.arange(4, dtype=np.int32)
+        sg = g.pass_(codes, need)
+        picks, keep = g.sample(hist, u, 3.0, 1.2)
+        po, ko, _ = oracle.voice_sample(sg, need, hist, u, 3.0, 1.2)
+        assert np.array_equal(picks, po), f"{picks} vs {po}"
+        assert np.all(np.abs(keep - ko) <= 1e-12)
