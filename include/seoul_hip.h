@@ -55,6 +55,12 @@ int sh_destroy(sh_ctx* ctx);
  * states made afterwards (imi/core/seoul.cpp:93-186). */
 int sh_load(sh_ctx* ctx, const char* gguf_path, int n_ctx);
 int sh_info(const sh_ctx* ctx, sh_model_info* out);
+/* Check a GGUF brain file on the host, without a device: its keys, and every table's type, rows and columns against
+ * what the kernels take (the same kv head count and FFN width in every layer), and that the attention kernels hold
+ * n_ctx positions at its head shape. sh_load runs the same check before it uploads anything (imi's load reads the
+ * same keys and tensors, imi/core/seoul.cpp:93-162, and returns false on a file it cannot use). out (nullable) gets
+ * the shape; table_bytes and vector_bytes are left 0. Returns SH_OK, SH_E_FILE or SH_E_SHAPE. */
+int sh_check_model(const char* gguf_path, int n_ctx, sh_model_info* out);
 
 int sh_state_new(sh_ctx* ctx, sh_state** out);          /* imi_seoul::new_state (seoul.cpp:193-201) */
 int sh_state_free(sh_state* st);
@@ -126,13 +132,6 @@ int sh_q4_bench_kernel(sh_ctx* ctx, sh_q4* const* tables, int n_tables, int n_in
  * that imi runs on (imi/core/seoul.cpp:48,447,451). */
 int sh_expf(sh_ctx* ctx, const float* x, long long n, float* y);
 
-/* Stage timestamps of the last launch of the persistent step kernel, for contexts created with SEOUL_HIP_TRACE=1
- * in the environment (no counterpart in the reference: the GPU step is one launch, so this is its profile).
- * out[grid][per_wg] (nullable, cap entries) gets wall-clock ticks: per step, one at the step's start, then four per
- * stage (start, input arrived, table chunks done, end; 0 where a workgroup had nothing to do); ticks_per_us
- * converts them. */
-int sh_step_trace(sh_ctx* ctx, long long* out, long long cap, int* per_wg, int* grid, double* ticks_per_us);
-
 /* ---- voice generator: imi_voice::load / begin_frame / pass / feedback (imi/core/voice.h:17-51) ---- */
 typedef struct {
     int n_embd, n_vocab, n_cb, n_in, n_head, n_head_kv, head_dim, n_ff, n_layer;
@@ -165,7 +164,8 @@ int sh_voice_feedback(sh_voice* v, const int32_t* codes, float* out);
  * (the chance that this pick is not end-of-audio), and picks[j] = the first v at which r = u[j] * sum minus
  * p[0], p[1], ... p[v] in double reaches <= 0 (n_vocab - 1 if none). u[j] in [0, 1) is the caller's uniform draw
  * for pick j (imi draws std::uniform_real_distribution<double>(0, 1) from its std::mt19937, pick by pick, after
- * the frame's shuffle). The penalised scores stay in the device score rows. 0 <= n_frames <= 256,
+ * the frame's shuffle). The penalised scores stay in the device score rows, so a pass is sampled once: a second
+ * call before the next sh_voice_pass fails with SH_E_ARG. 0 <= n_frames <= 256,
  * n_vocab <= 4096, temp > 0, rep > 0. */
 int sh_voice_sample(sh_voice* v, const int32_t* hist, int n_frames, const double* u, float temp, float rep,
                     int32_t* picks, double* keep);

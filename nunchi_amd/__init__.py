@@ -19,11 +19,10 @@ LIB_PATH = os.path.join(HERE, "libseoul_hip.so")
 
 SH_OK, SH_E_ARG, SH_E_HIP, SH_E_FILE, SH_E_SHAPE, SH_E_CONTEXT_FULL, SH_E_STATE, SH_E_NOMEM = 0, -1, -2, -3, -4, -5, -6, -7
 EXPORTS = [
-    "sh_last_error", "sh_create", "sh_destroy", "sh_load", "sh_info", "sh_state_new", "sh_state_free", "sh_state_reset",
+    "sh_last_error", "sh_create", "sh_destroy", "sh_load", "sh_info", "sh_check_model", "sh_state_new", "sh_state_free", "sh_state_reset",
     "sh_state_pos", "sh_state_set_pos", "sh_step", "sh_step2", "sh_step_batch", "sh_generate", "sh_bench_tables",
     "sh_bench_kernel",
     "sh_q4_create", "sh_q4_free", "sh_q4_rows", "sh_q4_gemv", "sh_q4_gemm", "sh_q4_gemv_dev", "sh_q4_bench", "sh_q4_bench_kernel", "sh_expf", "sh_sync",
-    "sh_step_trace",
     "sh_voice_load", "sh_voice_free", "sh_voice_info", "sh_voice_begin_frame", "sh_voice_base", "sh_voice_pass",
     "sh_voice_feedback", "sh_voice_sample",
 ]
@@ -68,6 +67,7 @@ def load_library(path: str = LIB_PATH):
         "sh_destroy": (i, [vp]),
         "sh_load": (i, [vp, C.c_char_p, i]),
         "sh_info": (i, [vp, P(ModelInfo)]),
+        "sh_check_model": (i, [C.c_char_p, i, P(ModelInfo)]),
         "sh_state_new": (i, [vp, P(vp)]),
         "sh_state_free": (i, [vp]),
         "sh_state_reset": (i, [vp]),
@@ -89,7 +89,6 @@ def load_library(path: str = LIB_PATH):
         "sh_q4_bench_kernel": (i, [vp, vp, i, i, i, i, P(d)]),
         "sh_expf": (i, [vp, vp, C.c_longlong, vp]),
         "sh_sync": (i, [vp]),
-        "sh_step_trace": (i, [vp, vp, C.c_longlong, P(i), P(i), P(d)]),
         "sh_voice_load": (i, [i, C.c_char_p, P(vp)]),
         "sh_voice_free": (i, [vp]),
         "sh_voice_info": (i, [vp, P(VoiceShape)]),
@@ -115,6 +114,15 @@ def _check(rc: int):
 
 def _p(a):
     return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def check_model(path: str, n_ctx: int = 1024) -> ModelInfo:
+    """sh_check_model: the file's keys and table shapes against what the kernels take, on the host (no device).
+    Raises SeoulError (status SH_E_SHAPE or SH_E_FILE) naming the first problem."""
+    L = load_library()
+    info = ModelInfo()
+    _check(L.sh_check_model(path.encode(), int(n_ctx), C.byref(info)))
+    return info
 
 
 _live_contexts = weakref.WeakSet()
@@ -271,17 +279,6 @@ class Brain:
         ms, us, by, nl = C.c_double(), C.c_double(), C.c_double(), C.c_int()
         _check(_lib.sh_bench_tables(self.ctx.h, int(ncol), int(reps), C.byref(ms), C.byref(us), C.byref(by), C.byref(nl)))
         return {"ms_per_pass": ms.value, "avg_launch_us": us.value, "bytes_per_pass": by.value, "launches": nl.value}
-
-    def step_trace(self):
-        """Stage timestamps (us from each workgroup's first) of the last step-kernel launch: [grid][per_wg], for
-        contexts made with SEOUL_HIP_TRACE=1."""
-        per, grid, tpu = C.c_int(), C.c_int(), C.c_double()
-        _check(_lib.sh_step_trace(self.ctx.h, None, 0, C.byref(per), C.byref(grid), C.byref(tpu)))
-        out = np.zeros((grid.value, per.value), np.int64)
-        _check(_lib.sh_step_trace(self.ctx.h, _p(out), out.size, C.byref(per), C.byref(grid), C.byref(tpu)))
-        return out, tpu.value
-
-    KERNELS = {"ffn_gate_up": 0, "ffn_down": 1, "word_scores": 2}
 
     def bench_kernel(self, kind: str, n_in: int = 1, reps: int = 64):
         """Mean duration (us) and bytes per launch of the step's GEMV for one table kind."""

@@ -9,7 +9,6 @@
 
 #include "../../include/seoul_hip.h"
 #include "sh_kernels.h"
-#include "sh_step.h"
 
 namespace sh {
 int set_error(int code, const std::string& msg);   // sets the thread's last error; returns code
@@ -27,6 +26,9 @@ hipError_t launch_scores_q6k(int M, int grid, const gemv_args& a, hipStream_t s,
 hipError_t launch_final(int M, const final_args& a, hipStream_t s);
 hipError_t launch_q4_rows(const q4dev& T, const int32_t* ids, int n, float* out, hipStream_t s);
 hipError_t launch_expf(const float* x, float* y, long long n, hipStream_t s);
+// the longest contexts the decode and prefill attention kernels hold (their score rows live in LDS)
+int attn_max_ctx(int grp, int D);
+int pf_attn_max_ctx(int grp, int D);
 }
 
 namespace sh {
@@ -56,7 +58,6 @@ using sh::arena;
 using sh::layer_dev;
 using sh::q4dev;
 using sh::q6dev;
-using sh::sk_stage;
 using sh::step_params;
 
 struct sh_q4 {
@@ -107,22 +108,6 @@ struct sh_ctx {
     // the step replays a captured graph; SEOUL_HIP_GRAPHS=0 enqueues the same kernels directly (for tools that do
     // not trace graph launches)
     bool use_graphs = true;
-    // persistent step kernel: its program, tagged record buffers and per-launch staging
-    bool use_persistent = false;      // SEOUL_HIP_STEP=persistent selects the persistent step kernel
-    std::vector<sk_stage> sk_host;
-    sk_stage* sk_dev = nullptr;
-    char* sk_mem = nullptr;
-    unsigned long long* sk_part = nullptr;
-    int* sk_err = nullptr;
-    int sk_grid = 0;
-    long long sk_timeout = 0;
-    double ticks_per_us = 100.0;
-    unsigned epoch = 1;
-    int io_cap = 0;
-    int32_t* io_tok = nullptr;        // [2][io_cap]
-    float* io_embd = nullptr;         // [2][io_cap][E]
-    int32_t* io_ids = nullptr;        // [2][io_cap]
-    float* io_hidden = nullptr;       // [2][io_cap][E]
     // prefill work buffers (PF_MAX_N positions, made on first use)
     char* pf_mem = nullptr;
     float *pf_x = nullptr, *pf_y = nullptr, *pf_big = nullptr, *pf_act = nullptr, *pf_hid = nullptr;
@@ -130,9 +115,5 @@ struct sh_ctx {
     float *pf_d = nullptr, *pf_s = nullptr, *pf_emb = nullptr;
     int32_t* pf_tok = nullptr;
     bool use_prefill = true;          // SEOUL_HIP_PREFILL=0: step_batch runs n single steps instead
-    bool want_trace = false;
-    long long* trace = nullptr;
-    long long trace_cap = 0;
-    int trace_per_wg = 0;
 };
 

@@ -1,8 +1,7 @@
 // libseoul_hip: the brain step of imi's engine (imi/core/seoul.{h,cpp}) on one MI355X, behind the C ABI of
 // include/seoul_hip.h. Host side: GGUF read, repack into the device layout, conversation states, and the step as
 // a captured HIP graph of fused kernels (one per table read, with the norms, cuts and epilogues folded in, plus
-// attention and the end of step; sh_kernels.hip). SEOUL_HIP_STEP=persistent runs the same stages instead as one
-// cooperative launch of the persistent step kernel (sh_step.hip) covering every stage of n steps.
+// attention and the end of step; sh_kernels.hip).
 #include "../../include/seoul_hip.h"
 
 #include <hip/hip_runtime.h>
@@ -34,6 +33,34 @@ int fail(int code, const std::string& msg) {
 
 // Q4_0 / Q4_1 rows (tensor, row) -> device layout in a host staging buffer: codes [rows][nb][16], scales and (Q4_1)
 // block minima [rows/8][nb][8]. A table's rows are all Q4_0 or all Q4_1 (imi/core/tables.cpp:70-72).
+// Replace a grow-on-demand device buffer: the new block is allocated before the old one is freed, so a failed
+// allocation leaves the buffer (and the capacity the caller keeps for it) as they were.
+hipError_t regrow(void** p, size_t bytes) {
+    void* q = nullptr;
+    const hipError_t e = hipMalloc(&q, bytes);
+    if (e != hipSuccess) return e;
+    if (*p) (void)hipFree(*p);
+    *p = q;
+    return hipSuccess;
+}
+
+// both staging buffers of the kernel-level API, or neither
+hipError_t regrow2(float** x, float** y, size_t n_floats) {
+    void* nx = nullptr;
+    void* ny = nullptr;
+    hipError_t e = hipMalloc(&nx, n_floats * 4);
+    if (e == hipSuccess) e = hipMalloc(&ny, n_floats * 4);
+    if (e != hipSuccess) {
+        if (nx) (void)hipFree(nx);
+        return e;
+    }
+    if (*x) (void)hipFree(*x);
+    if (*y) (void)hipFree(*y);
+    *x = static_cast<float*>(nx);
+    *y = static_cast<float*>(ny);
+    return hipSuccess;
+}
+
 bool repack_q4(const std::vector<std::pair<const gg_tensor*, int>>& rows, std::vector<uint8_t>& codes, std::vector<uint16_t>& scales,
                std::vector<uint16_t>& mins, int* cols) {
     if (rows.empty() || rows.size() % 8) return false;
@@ -230,6 +257,8 @@ int enqueue_step(sh_ctx* c, int M, bool want_logits) {
         z.part_v = c->part_v;
         z.part_i = c->part_i;
         z.n_part = grid;
+        z.logits = c->logits;
+        z.ld_logits = I.n_vocab;
     } else {
         z.x_in = c->xbuf[cur];
         z.y_in = c->fo;
@@ -287,182 +316,110 @@ std::vector<float2> rope_table(int n_ctx, int D, float base, const float* ff) {
 }
 
 
-// The persistent kernel's program: the stages of one step in order, each with its own tagged output buffer
-// [2 parity][2 conversations][n_out] (zeroed: tag 0 is never a step's epoch).
-int build_program(sh_ctx* c) {
-    // shapes the step kernel does not read run on the per-table kernels
-    if (c->vocab6.codes) return fail(SH_E_SHAPE, "step kernel: the word table is Q6_K");
-    if (c->info.n_attn > 0 && c->info.head_dim != 32 && c->info.head_dim != 64) return fail(SH_E_SHAPE, "step kernel: head_dim 32 or 64");
-    for (const layer_dev& L : c->layers)
-        for (const q4dev* t : {&L.in_proj, &L.out_proj, &L.qkvg, &L.o, &L.gate_up, &L.down})
-            if (t->mins) return fail(SH_E_SHAPE, "step kernel: Q4_1 tables");
-    const sh_model_info& I = c->info;
-    const int E = I.n_embd, Hq = I.n_head * I.head_dim;
-    int dev_cus = 0;
-    HIPCHK(hipDeviceGetAttribute(&dev_cus, hipDeviceAttributeMultiprocessorCount, c->device));
-    int per_cu = 0;
-    HIPCHK(step_kernel_occupancy(2, &per_cu));
-    if (per_cu < 1) return fail(SH_E_SHAPE, "step kernel: one workgroup per compute unit does not fit");
-    HIPCHK(step_kernel_occupancy(1, &per_cu));
-    if (per_cu < 1) return fail(SH_E_SHAPE, "step kernel: one workgroup per compute unit does not fit");
-    // every workgroup owns at least one unit of every table read, so each one publishes in every GEMV stage: then
-    // no workgroup can fall two steps behind another, which is what the two record buffers per stage rely on
-    int grid = dev_cus < SK_THREADS ? dev_cus : SK_THREADS;
-    auto min_units = [&](const q4dev& W, int ug) { const int u = W.rows / (8 * ug); if (u < grid) grid = u; };
-    for (const layer_dev& L : c->layers) {
-        if (L.conv) { min_units(L.in_proj, 3); min_units(L.out_proj, 1); }
-        else { min_units(L.qkvg, 1); min_units(L.o, 1); }
-        min_units(L.gate_up, 2);
-        min_units(L.down, 1);
-    }
-    min_units(c->vocab, 1);
-    if (grid < 1) return fail(SH_E_SHAPE, "step kernel: a table has no whole unit");
-    c->sk_grid = grid;
-    int rate_khz = 0;
-    HIPCHK(hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, c->device));
-    if (rate_khz <= 0) rate_khz = 100000;
-    c->ticks_per_us = rate_khz / 1000.0;
-    c->sk_timeout = 2LL * rate_khz * 1000;   // a wait longer than 2 s means the launch is broken
+// The keys and tensor shapes of a brain file (imi/core/seoul.cpp:93-142 reads the same keys and tensors), checked
+// against what the kernels take before anything is uploaded: every table's type, rows and columns, the same kv head
+// count and FFN width in every layer, and a context the attention kernels can hold (their score rows live in LDS).
+// Fills I (n_ctx included) and the float keys. Host only.
+struct model_keys {
+    float eps = 1e-5f, rope_base = 1e6f, rope_base_swa = 1e4f;
+};
 
-    std::vector<sk_stage> P;
-    std::vector<size_t> out_n;   // records per conversation of each stage's output
-    auto add = [&](sk_stage st, int n_out) {
-        st.n_out = n_out;
-        P.push_back(st);
-        out_n.push_back((size_t)n_out);
-        return (int)P.size() - 1;
+int check_model(gg_file& f, int n_ctx, sh_model_info& I, model_keys& K) {
+    const gg_tensor* te = f.get("token_embd.weight");
+    if (!te) return fail(SH_E_FILE, "sh_load: " + f.error);
+    if (te->type != GT_Q4_0 && te->type != GT_Q6_K) return fail(SH_E_SHAPE, "sh_load: word table must be Q6_K or Q4_0");
+    I = sh_model_info{};
+    I.n_embd = (int)te->ne[0];
+    I.n_vocab = (int)te->ne[1];
+    const int E = I.n_embd;
+    if (E < 32 || E % 32 || E / 32 > 64) return fail(SH_E_SHAPE, "sh_load: n_embd must be a multiple of 32 and at most 2048");
+    if (I.n_vocab < 1) return fail(SH_E_SHAPE, "sh_load: empty word table");
+    if (te->type == GT_Q6_K && E != 256 && E != 512 && E != 1024 && E != 2048)
+        return fail(SH_E_SHAPE, "sh_load: a Q6_K word table needs n_embd 256, 512, 1024 or 2048");
+    K.eps = f.key_f("lfm3.attention.layer_norm_rms_epsilon", 1e-5f);
+    K.rope_base = f.key_f("lfm3.rope.freq_base", 1e6f);
+    K.rope_base_swa = f.key_f("lfm3.rope.freq_base_swa", 1e4f);
+    I.n_swa = (int)f.key_i("lfm3.attention.sliding_window", 0);
+    I.d_conv = (int)f.key_i("lfm3.shortconv.l_cache", 7) - 1;
+    I.n_head = (int)f.key_i("lfm3.attention.head_count", 16);
+    I.head_dim = (int)f.key_i("lfm3.attention.key_length", 128);
+    I.n_layer = (int)f.key_i("lfm3.block_count", 0);
+    I.n_ctx = n_ctx;
+    if (I.n_layer < 1) return fail(SH_E_FILE, "sh_load: no layers");
+    if (I.n_swa < 0) return fail(SH_E_SHAPE, "sh_load: negative sliding window");
+    auto table = [&](const gg_tensor* t, int64_t rows, int64_t cols, const std::string& what) -> int {
+        if (t->type != GT_Q4_0 && t->type != GT_Q4_1) return fail(SH_E_SHAPE, "sh_load: " + what + " must be Q4_0 or Q4_1");
+        if (t->ne[1] != rows || t->ne[0] != cols || t->ne[2] != 1 || t->ne[3] != 1)
+            return fail(SH_E_SHAPE, "sh_load: " + what + " is " + std::to_string(t->ne[1]) + " x " + std::to_string(t->ne[0]) +
+                                        ", the kernels need " + std::to_string(rows) + " x " + std::to_string(cols));
+        return SH_OK;
     };
-    auto gemv = [&](const q4dev& W, int ug, int pro, int epi) {
-        sk_stage st{};
-        st.kind = SK_GEMV;
-        st.pro = pro;
-        st.epi = epi;
-        st.W = W;
-        st.ug = ug;
-        st.units = W.rows / (8 * ug);
-        return st;
-    };
-    // inputs are wired after the buffers exist: (stage, producer stage)
-    std::vector<std::pair<int, int>> wires;
-    int prev_down = -1;
-    const layer_dev* prev = nullptr;
-    for (size_t il = 0; il < c->layers.size(); il++) {
-        const layer_dev& L = c->layers[il];
-        const int pro0 = prev ? SKP_RESID : SKP_FIRST;
-        int s1;
-        if (L.conv) {
-            sk_stage a = gemv(L.in_proj, 3, pro0, SKE_CONV);
-            a.conv_w = L.conv_w;
-            a.conv_layer = L.ci;
-            a.w_post = prev ? prev->post_ffn_norm : nullptr;
-            a.w_pre = L.attn_norm;
-            s1 = add(a, E);
-            if (prev) wires.push_back({s1, prev_down});
-            sk_stage b = gemv(L.out_proj, 1, SKP_CUT, SKE_STORE);
-            const int s2 = add(b, E);
-            wires.push_back({s2, s1});
-            s1 = s2;
+    int n_kv = -1, n_ff = -1, n_attn = 0;
+    const int D = I.head_dim, Hq = I.n_head * D;
+    for (int il = 0; il < I.n_layer; il++) {
+        const std::string p = "blk." + std::to_string(il) + ".";
+        int rc = SH_OK;
+        if (const gg_tensor* cw = f.get(p + "shortconv.conv.weight", false)) {
+            if (I.d_conv < 1 || I.d_conv > 8) return fail(SH_E_SHAPE, "sh_load: conv kernel must be 2 to 9 taps");
+            if (cw->type != GT_F32 || cw->ne[1] != E || cw->ne[0] != I.d_conv + 1) return fail(SH_E_SHAPE, "sh_load: conv weight shape");
+            const gg_tensor* ip = f.get(p + "shortconv.in_proj.weight");
+            const gg_tensor* op = f.get(p + "shortconv.out_proj.weight");
+            if (!ip || !op) return fail(SH_E_FILE, "sh_load: " + f.error);
+            if ((rc = table(ip, 3LL * E, E, p + "shortconv.in_proj")) != SH_OK) return rc;
+            if ((rc = table(op, E, E, p + "shortconv.out_proj")) != SH_OK) return rc;
         } else {
-            sk_stage a = gemv(L.qkvg, 1, pro0, SKE_STORE);
-            a.w_post = prev ? prev->post_ffn_norm : nullptr;
-            a.w_pre = L.attn_norm;
-            const int sq = add(a, c->nqkv);
-            if (prev) wires.push_back({sq, prev_down});
-            sk_stage t{};
-            t.kind = SK_ATTN;
-            t.layer_ai = L.ai;
-            t.swa = L.swa ? 1 : 0;
-            t.q_norm = L.q_norm;
-            t.k_norm = L.k_norm;
-            t.rope_cs = L.swa ? c->rope_cs_swa : c->rope_cs;
-            const int sa = add(t, Hq);
-            wires.push_back({sa, sq});
-            sk_stage o = gemv(L.o, 1, SKP_CUT, SKE_STORE);
-            s1 = add(o, E);
-            wires.push_back({s1, sa});
+            const gg_tensor *q = f.get(p + "attn_q.weight"), *k = f.get(p + "attn_k.weight"), *v = f.get(p + "attn_v.weight");
+            const gg_tensor *g = f.get(p + "attn_gate.weight"), *o = f.get(p + "attn_output.weight");
+            if (!q || !k || !v || !g || !o) return fail(SH_E_FILE, "sh_load: " + f.error);
+            if (D != 32 && D != 64 && D != 128) return fail(SH_E_SHAPE, "sh_load: head_dim must be 32, 64 or 128");
+            if (I.n_head < 1 || Hq / 32 > 64) return fail(SH_E_SHAPE, "sh_load: attention width must be 32 to 2048");
+            const int kv = k->ne[1] % D == 0 ? (int)(k->ne[1] / D) : 0;
+            if (kv < 1 || I.n_head % kv || I.n_head / kv > 8)
+                return fail(SH_E_SHAPE, "sh_load: " + p + "attn_k rows must be a multiple of head_dim giving 1 to 8 query heads per kv head");
+            if (n_kv >= 0 && kv != n_kv) return fail(SH_E_SHAPE, "sh_load: kv head count differs between layers");
+            n_kv = kv;
+            if ((rc = table(q, Hq, E, p + "attn_q")) != SH_OK || (rc = table(k, (int64_t)kv * D, E, p + "attn_k")) != SH_OK ||
+                (rc = table(v, (int64_t)kv * D, E, p + "attn_v")) != SH_OK || (rc = table(g, I.n_head, E, p + "attn_gate")) != SH_OK ||
+                (rc = table(o, E, Hq, p + "attn_output")) != SH_OK)
+                return rc;
+            for (const char* nm : {"attn_q_norm.weight", "attn_k_norm.weight"}) {
+                const gg_tensor* t = f.get(p + nm);
+                if (!t) return fail(SH_E_FILE, "sh_load: " + f.error);
+                if (t->type != GT_F32 || t->ne[0] * t->ne[1] != D) return fail(SH_E_SHAPE, "sh_load: " + p + nm + " must be f32 [head_dim]");
+            }
+            n_attn++;
         }
-        sk_stage f = gemv(L.gate_up, 2, SKP_RESID, SKE_SWIGLU);
-        f.w_post = L.post_attn_norm;
-        f.w_pre = L.ffn_norm;
-        const int sf = add(f, I.n_ff);
-        wires.push_back({sf, s1});
-        sk_stage d = gemv(L.down, 1, SKP_CUT, SKE_STORE);
-        prev_down = add(d, E);
-        wires.push_back({prev_down, sf});
-        prev = &L;
-    }
-    sk_stage v = gemv(c->vocab, 1, SKP_RESID, SKE_LOGITS);
-    v.kind = SK_VOCAB;
-    v.w_post = prev->post_ffn_norm;
-    v.w_pre = c->out_norm;
-    const int sv = add(v, 0);
-    wires.push_back({sv, prev_down});
-
-    // shape limits of the kernel
-    if (P.size() > (size_t)SK_MAX_STAGES) return fail(SH_E_SHAPE, "step kernel: too many stages");
-    const int grp = I.n_attn ? I.n_head / I.n_head_kv : 1;
-    if ((E != 256 && E != 512 && E != 1024 && E != 2048) || I.n_ff > 8192 || Hq > 8192)
-        return fail(SH_E_SHAPE, "step kernel: hidden width 256, 512, 1024 or 2048, others up to 8192");
-    if (c->n_conv && (I.d_conv < 1 || I.d_conv > SK_CONV_MAX)) return fail(SH_E_SHAPE, "step kernel: conv memory of 1..7 taps");
-    if (I.n_attn) {
-        if (I.head_dim != 64 && I.head_dim != 32) return fail(SH_E_SHAPE, "step kernel: head_dim must be 32 or 64");
-        if (grp * I.head_dim + 2 * I.head_dim + grp > SK_THREADS) return fail(SH_E_SHAPE, "step kernel: attention group too wide");
-        if ((512 + 17 * (size_t)I.head_dim + 8 + (size_t)grp * I.n_ctx + 8 * (size_t)I.head_dim) * 4 > (size_t)SK_ATTN_BYTES)
-            return fail(SH_E_SHAPE, "step kernel: context too long for the attention scores in LDS");
-        if (I.n_head_kv * 2 > c->sk_grid) return fail(SH_E_SHAPE, "step kernel: more kv heads than workgroups");
-    }
-    for (const sk_stage& st : P) {
-        if (st.kind == SK_ATTN) continue;
-        const int nb = st.W.nb;
-        if (nb < 1 || nb > 256 || st.W.rows % (8 * st.ug)) return fail(SH_E_SHAPE, "step kernel: table shape");
-        if (sk_gmax(nb, 2) < st.ug) return fail(SH_E_SHAPE, "step kernel: a unit does not fit one chunk");
-    }
-
-    // FFN gate|up outputs go out already cut per 32 channels when every workgroup's units (8 channels each) form
-    // whole blocks of 32 in every chunk: 10 records per 32 channels instead of 32 for the down table's input
-    for (auto& w : wires) {
-        sk_stage& prod = P[w.second];
-        sk_stage& cons = P[w.first];
-        if (prod.kind != SK_GEMV || prod.epi != SKE_SWIGLU || cons.pro != SKP_CUT) continue;
-        bool ok = prod.units % (4 * c->sk_grid) == 0;
-        for (int Mi = 1; Mi <= 2 && ok; Mi++) {
-            const int gmax = sk_gmax(prod.W.nb, Mi);
-            const int cu = gmax / prod.ug > 1 ? gmax / prod.ug : 1;
-            const int per_wg = prod.units / c->sk_grid;
-            ok = cu % 4 == 0 || per_wg <= cu;
+        for (const char* nm : {"attn_norm.weight", "post_attention_norm.weight", "ffn_norm.weight", "post_ffw_norm.weight"}) {
+            const gg_tensor* t = f.get(p + nm);
+            if (!t) return fail(SH_E_FILE, "sh_load: " + f.error);
+            if (t->type != GT_F32 || t->ne[0] * t->ne[1] != E) return fail(SH_E_SHAPE, "sh_load: " + p + nm + " must be f32 [n_embd]");
         }
-        if (!ok) continue;
-        prod.cut_out = 1;
-        cons.cut_in = 1;
-        out_n[w.second] = (size_t)prod.units * 8 / 32 * 10;
-        prod.n_out = (int)out_n[w.second];
+        const gg_tensor *fg = f.get(p + "ffn_gate.weight"), *fu = f.get(p + "ffn_up.weight"), *fd = f.get(p + "ffn_down.weight");
+        if (!fg || !fu || !fd) return fail(SH_E_FILE, "sh_load: " + f.error);
+        const int ff = (int)fg->ne[1];
+        if (ff < 32 || ff % 32 || ff / 32 > 256) return fail(SH_E_SHAPE, "sh_load: n_ff must be a multiple of 32, at most 8192");
+        if (n_ff >= 0 && ff != n_ff) return fail(SH_E_SHAPE, "sh_load: FFN width differs between layers");
+        n_ff = ff;
+        if ((rc = table(fg, ff, E, p + "ffn_gate")) != SH_OK || (rc = table(fu, ff, E, p + "ffn_up")) != SH_OK ||
+            (rc = table(fd, E, ff, p + "ffn_down")) != SH_OK)
+            return rc;
     }
-
-    // device memory: stage table, output records, argmax partials, error flag
-    size_t rec = 0;
-    for (size_t n : out_n) rec += 4 * n;
-    const size_t part = 8 * (size_t)c->sk_grid;
-    const size_t bytes = 8 * (rec + part) + 256;
-    HIPCHK(hipMalloc((void**)&c->sk_mem, bytes));
-    HIPCHK(hipMemset(c->sk_mem, 0, bytes));
-    unsigned long long* base = reinterpret_cast<unsigned long long*>(c->sk_mem);
-    size_t at = 0;
-    for (size_t i = 0; i < P.size(); i++) {
-        P[i].out = out_n[i] ? base + at : nullptr;
-        at += 4 * out_n[i];
+    const gg_tensor* on = f.get("output_norm.weight");
+    if (!on || on->type != GT_F32 || on->ne[0] * on->ne[1] != E) return fail(SH_E_FILE, "sh_load: output_norm.weight missing or not f32 [n_embd]");
+    if (const gg_tensor* rf = f.get("rope_freqs.weight", false))
+        if (rf->type != GT_F32 || rf->ne[0] != D / 2) return fail(SH_E_SHAPE, "sh_load: rope_freqs shape");
+    I.n_attn = n_attn;
+    I.n_head_kv = n_kv > 0 ? n_kv : 0;
+    I.n_ff = n_ff;
+    if (n_attn > 0) {
+        const int grp = I.n_head / I.n_head_kv, lim = std::min(attn_max_ctx(grp, D), pf_attn_max_ctx(grp, D));
+        if (n_ctx > lim)
+            return fail(SH_E_SHAPE, "sh_load: n_ctx " + std::to_string(n_ctx) + " is above the " + std::to_string(lim) +
+                                        " positions the attention kernels hold at this head shape");
     }
-    c->sk_part = base + at;
-    at += part;
-    c->sk_err = reinterpret_cast<int*>(base + at);
-    for (auto& w : wires) {
-        P[w.first].in = P[w.second].out;
-        P[w.first].n_in = P[w.second].n_out;
-    }
-    HIPCHK(hipMalloc((void**)&c->sk_dev, sizeof(sk_stage) * P.size()));
-    HIPCHK(hipMemcpy(c->sk_dev, P.data(), sizeof(sk_stage) * P.size(), hipMemcpyHostToDevice));
-    c->sk_host = std::move(P);
     return SH_OK;
 }
+
 }  // namespace
 
 extern "C" {
@@ -485,12 +442,8 @@ int sh_create(int device, sh_ctx** out) {
     memset(c->P_host, 0, sizeof(step_params));
     const char* g = getenv("SEOUL_HIP_GRAPHS");
     c->use_graphs = !(g && g[0] == '0');
-    const char* sp = getenv("SEOUL_HIP_STEP");
-    c->use_persistent = sp && strcmp(sp, "persistent") == 0;
     const char* pf = getenv("SEOUL_HIP_PREFILL");
     c->use_prefill = !(pf && strcmp(pf, "0") == 0);
-    const char* tr = getenv("SEOUL_HIP_TRACE");
-    c->want_trace = tr && tr[0] == '1';
     *out = c.release();
     return SH_OK;
 }
@@ -511,15 +464,23 @@ int sh_destroy(sh_ctx* c) {
     if (c->bench_y) (void)hipFree(c->bench_y);
     if (c->P_dev) (void)hipFree(c->P_dev);
     if (c->P_host) (void)hipHostFree(c->P_host);
-    for (void* p : {(void*)c->sk_dev, (void*)c->sk_mem, (void*)c->io_tok, (void*)c->io_embd, (void*)c->io_ids, (void*)c->io_hidden,
-                    (void*)c->trace})
-        if (p) (void)hipFree(p);
     if (c->gen_out) (void)hipFree(c->gen_out);
     if (c->ev0) (void)hipEventDestroy(c->ev0);
     if (c->ev1) (void)hipEventDestroy(c->ev1);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
     return SH_OK;
+}
+
+int sh_check_model(const char* path, int n_ctx, sh_model_info* out) {
+    if (!path || n_ctx < 1) return fail(SH_E_ARG, "sh_check_model: bad argument");
+    gg_file f;
+    if (!f.load(path)) return fail(SH_E_FILE, "sh_load: " + f.error);
+    sh_model_info I;
+    model_keys K;
+    const int rc = check_model(f, n_ctx, I, K);
+    if (rc == SH_OK && out) *out = I;
+    return rc;
 }
 
 // imi/core/seoul.cpp:93-186; the tied word table is Q6_K (imi's format) or Q4_0; tables repacked into the device layout
@@ -529,28 +490,17 @@ int sh_load(sh_ctx* c, const char* path, int n_ctx) {
     HIPCHK(hipSetDevice(c->device));
     gg_file f;
     if (!f.load(path)) return fail(SH_E_FILE, "sh_load: " + f.error);
-    const gg_tensor* te = f.get("token_embd.weight");
-    if (!te) return fail(SH_E_FILE, "sh_load: " + f.error);
-    if (te->type != GT_Q4_0 && te->type != GT_Q6_K) return fail(SH_E_SHAPE, "sh_load: word table must be Q6_K or Q4_0");
-    const bool q6 = te->type == GT_Q6_K;
     sh_model_info& I = c->info;
-    I.n_embd = (int)te->ne[0];
-    I.n_vocab = (int)te->ne[1];
-    if (q6 && I.n_embd != 256 && I.n_embd != 512 && I.n_embd != 1024 && I.n_embd != 2048)
-        return fail(SH_E_SHAPE, "sh_load: a Q6_K word table needs n_embd 256, 512, 1024 or 2048");
-    c->eps = f.key_f("lfm3.attention.layer_norm_rms_epsilon", 1e-5f);
-    c->rope_base = f.key_f("lfm3.rope.freq_base", 1e6f);
-    c->rope_base_swa = f.key_f("lfm3.rope.freq_base_swa", 1e4f);
-    I.n_swa = (int)f.key_i("lfm3.attention.sliding_window", 0);
-    I.d_conv = (int)f.key_i("lfm3.shortconv.l_cache", 7) - 1;
-    I.n_head = (int)f.key_i("lfm3.attention.head_count", 16);
-    I.head_dim = (int)f.key_i("lfm3.attention.key_length", 128);
-    I.n_layer = (int)f.key_i("lfm3.block_count", 0);
-    I.n_ctx = n_ctx;
+    model_keys K;
+    const int rc = check_model(f, n_ctx, I, K);
+    if (rc != SH_OK) return rc;
+    const gg_tensor* te = f.get("token_embd.weight");
+    const bool q6 = te->type == GT_Q6_K;
+    c->eps = K.eps;
+    c->rope_base = K.rope_base;
+    c->rope_base_swa = K.rope_base_swa;
     const std::vector<int64_t> swa_pat = f.key_arr("lfm3.attention.sliding_window_pattern");
     const int E = I.n_embd;
-    if (E % 32 || E / 32 > 64) return fail(SH_E_SHAPE, "sh_load: n_embd must be a multiple of 32 and at most 2048");
-    if (I.n_layer < 1) return fail(SH_E_FILE, "sh_load: no layers");
 
     // first pass: shapes, and the bytes the device arena needs
     struct plan { std::vector<std::pair<const gg_tensor*, int>> rows; q4dev* dst; };
@@ -758,11 +708,6 @@ int sh_load(sh_ctx* c, const char* path, int n_ctx) {
     c->part_v = fa(2 * (size_t)c->vocab_grid);
     c->part_i = static_cast<int*>(c->work.take(sizeof(int) * 2 * (size_t)c->vocab_grid));
     if (!c->part_i) return fail(SH_E_NOMEM, "sh_load: work arena overflow");
-    if (c->use_persistent) {   // shapes the step kernel does not take run on the per-table kernels
-        const int rc = build_program(c);
-        if (rc == SH_E_SHAPE) c->use_persistent = false;
-        else if (rc != SH_OK) return rc;
-    }
     HIPCHK(hipDeviceSynchronize());
     c->loaded = true;
     return SH_OK;
@@ -878,160 +823,8 @@ static int run_step(sh_ctx* c, int M, sh_state* const st[2], const int32_t tok[2
 }
 
 
-// One launch of the persistent step kernel over n steps of M conversations.
-struct launch_io {
-    bool greedy = false;
-    int32_t first[2] = {0, 0};                    // greedy: tokens of step 0
-    const int32_t* tokens[2] = {nullptr, nullptr};  // host [n]; null = every step takes its embd row
-    const float* embd[2] = {nullptr, nullptr};     // host [n][E] (rows of steps whose token < 0)
-    int logits_from = 0;                           // steps >= this compute word scores
-    float* hidden_last[2] = {nullptr, nullptr};    // host [E]
-    float* hidden_all = nullptr;                   // host [n][E] (M = 1)
-    float* logits[2] = {nullptr, nullptr};         // host [V]: the last step's word scores
-    int32_t* ids[2] = {nullptr, nullptr};          // host [n]: argmax of each step with word scores
-    double* seconds = nullptr;
-};
-
-constexpr int SK_FALLBACK = -1000;   // internal: the persistent kernel could not be launched, nothing was stepped
-
-static int run_persistent(sh_ctx* c, int M, sh_state* const st[2], int n, const launch_io& io) {
-    const sh_model_info& I = c->info;
-    const int E = I.n_embd;
-    for (int m = 0; m < M; m++) {
-        if (!st[m] || st[m]->ctx != c) return fail(SH_E_STATE, "step: state belongs to another context");
-        if (st[m]->pos + n > I.n_ctx) {
-            fprintf(stderr, "seoul-hip: context full (%d)\n", I.n_ctx);
-            return fail(SH_E_CONTEXT_FULL, "step: context full");
-        }
-        for (int i = 0; i < n; i++) {
-            const int32_t tk = io.greedy ? (i == 0 ? io.first[m] : 0) : (io.tokens[m] ? io.tokens[m][i] : -1);
-            if (tk >= I.n_vocab) return fail(SH_E_ARG, "step: token id out of range");
-            if (tk < 0 && !io.embd[m]) return fail(SH_E_ARG, "step: token < 0 needs an input vector");
-        }
-    }
-    if (M == 2 && st[0] == st[1]) return fail(SH_E_ARG, "step2: the two conversations must be different states");
-    if (n == 0) return SH_OK;
-    HIPCHK(hipSetDevice(c->device));
-    if (n > c->io_cap) {
-        for (void* p : {(void*)c->io_tok, (void*)c->io_embd, (void*)c->io_ids, (void*)c->io_hidden})
-            if (p) HIPCHK(hipFree(p));
-        c->io_cap = n;
-        HIPCHK(hipMalloc((void**)&c->io_tok, sizeof(int32_t) * 2 * (size_t)n));
-        HIPCHK(hipMalloc((void**)&c->io_embd, sizeof(float) * 2 * (size_t)n * E));
-        HIPCHK(hipMalloc((void**)&c->io_ids, sizeof(int32_t) * 2 * (size_t)n));
-        HIPCHK(hipMalloc((void**)&c->io_hidden, sizeof(float) * 2 * (size_t)n * E));
-    }
-    const int G = c->sk_grid;
-    const int per_wg = n * (4 * (int)c->sk_host.size() + 1);
-    if (c->want_trace && (long long)G * per_wg > c->trace_cap) {
-        if (c->trace) HIPCHK(hipFree(c->trace));
-        c->trace_cap = (long long)G * per_wg;
-        HIPCHK(hipMalloc((void**)&c->trace, sizeof(long long) * c->trace_cap));
-    }
-    sk_params p{};
-    p.stages = c->sk_dev;
-    p.n_stages = (int)c->sk_host.size();
-    p.E = E;
-    p.n_head = I.n_head;
-    p.n_kv = I.n_head_kv;
-    p.D = I.head_dim;
-    p.n_ctx = I.n_ctx;
-    p.n_swa = I.n_swa;
-    p.d_conv = I.d_conv;
-    p.V = I.n_vocab;
-    p.eps = c->eps;
-    p.vocab = c->vocab;
-    p.n_steps = n;
-    p.logits_from = io.logits_from;
-    p.greedy = io.greedy ? 1 : 0;
-    p.epoch0 = c->epoch;
-    p.part = c->sk_part;
-    p.err = c->sk_err;
-    p.timeout = c->sk_timeout;
-    p.trace = c->want_trace ? c->trace : nullptr;
-    p.n_trace = per_wg;
-    const bool with_logits = io.logits_from < n;
-    for (int m = 0; m < M; m++) {
-        sk_conv& v = p.cv[m];
-        v.kc = st[m]->kc;
-        v.vc = st[m]->vc;
-        v.conv = st[m]->conv;
-        v.pos = st[m]->pos;
-        v.first_token = io.first[m];
-        int32_t* tok = c->io_tok + (size_t)m * c->io_cap;
-        float* emb = c->io_embd + (size_t)m * c->io_cap * E;
-        if (!io.greedy) {
-            std::vector<int32_t> t(n, -1);
-            if (io.tokens[m]) memcpy(t.data(), io.tokens[m], sizeof(int32_t) * n);
-            HIPCHK(hipMemcpyAsync(tok, t.data(), sizeof(int32_t) * n, hipMemcpyHostToDevice, c->stream));
-            HIPCHK(hipStreamSynchronize(c->stream));   // t is a stack vector
-            v.tokens = tok;
-        }
-        if (io.embd[m]) HIPCHK(hipMemcpyAsync(emb, io.embd[m], sizeof(float) * (size_t)n * E, hipMemcpyHostToDevice, c->stream));
-        else if (io.greedy && io.first[m] < 0) return fail(SH_E_ARG, "generate: first token < 0 needs an input vector");
-        v.embd = emb;
-        v.ids = c->io_ids + (size_t)m * c->io_cap;
-        v.hidden = c->io_hidden + (size_t)m * c->io_cap * E;
-        v.hidden_stride = io.hidden_all ? E : 0;
-        v.logits = (with_logits && io.logits[m]) ? c->logits + (size_t)m * I.n_vocab : nullptr;
-    }
-    if (p.trace) HIPCHK(hipMemsetAsync(c->trace, 0, sizeof(long long) * (size_t)G * per_wg, c->stream));
-    HIPCHK(hipEventRecord(c->ev0, c->stream));
-    const hipError_t le = launch_step_kernel(M, p, G, c->stream);
-    if (le != hipSuccess) {
-        // a cooperative launch is refused while the device is shared in ways that cannot guarantee every
-        // workgroup a compute unit (e.g. another process holds a context): this context then runs the same
-        // stages as separate kernels
-        (void)hipGetLastError();
-        (void)hipStreamSynchronize(c->stream);
-        fprintf(stderr, "seoul-hip: persistent step kernel unavailable (%s); using per-table kernels\n", hipGetErrorString(le));
-        c->use_persistent = false;
-        return SK_FALLBACK;
-    }
-    HIPCHK(hipEventRecord(c->ev1, c->stream));
-    int err = 0;
-    HIPCHK(hipMemcpyAsync(&err, c->sk_err, sizeof(int), hipMemcpyDeviceToHost, c->stream));
-    HIPCHK(hipStreamSynchronize(c->stream));
-    c->epoch += (unsigned)n;
-    if (c->want_trace) c->trace_per_wg = per_wg;
-    if (err) {
-        HIPCHK(hipMemset(c->sk_err, 0, sizeof(int)));
-        return fail(SH_E_HIP, "step kernel: a stage input did not arrive within the time limit");
-    }
-    float ms = 0.0f;
-    HIPCHK(hipEventElapsedTime(&ms, c->ev0, c->ev1));
-    if (io.seconds) *io.seconds = ms * 1e-3;
-    for (int m = 0; m < M; m++) {
-        const sk_conv& v = p.cv[m];
-        if (io.ids[m]) HIPCHK(hipMemcpyAsync(io.ids[m], v.ids, sizeof(int32_t) * n, hipMemcpyDeviceToHost, c->stream));
-        if (io.hidden_all && m == 0) HIPCHK(hipMemcpyAsync(io.hidden_all, v.hidden, sizeof(float) * (size_t)n * E, hipMemcpyDeviceToHost, c->stream));
-        if (io.hidden_last[m]) {
-            const float* src = v.hidden + (io.hidden_all ? (size_t)(n - 1) * E : 0);
-            HIPCHK(hipMemcpyAsync(io.hidden_last[m], src, sizeof(float) * E, hipMemcpyDeviceToHost, c->stream));
-        }
-        if (v.logits) HIPCHK(hipMemcpyAsync(io.logits[m], v.logits, sizeof(float) * I.n_vocab, hipMemcpyDeviceToHost, c->stream));
-    }
-    HIPCHK(hipStreamSynchronize(c->stream));
-    for (int m = 0; m < M; m++) st[m]->pos += n;
-    return SH_OK;
-}
-
 int sh_step(sh_ctx* c, sh_state* s, int32_t token, const float* embd, int want_logits, float* hidden, float* logits, int32_t* best) {
     if (!c || !c->loaded) return fail(SH_E_STATE, "sh_step: no model loaded");
-    if (c->use_persistent) {
-        if (!s) return fail(SH_E_ARG, "sh_step: null state");
-        sh_state* st[2] = {s, nullptr};
-        launch_io io;
-        io.tokens[0] = &token;
-        io.embd[0] = token < 0 ? embd : nullptr;
-        io.logits_from = want_logits ? 0 : 1;
-        io.hidden_last[0] = hidden;
-        io.logits[0] = logits;
-        io.ids[0] = want_logits ? best : nullptr;
-        if (best && !want_logits) *best = -1;
-        const int rc = run_persistent(c, 1, st, 1, io);
-        if (rc != SK_FALLBACK) return rc;
-    }
     sh_state* st[2] = {s, nullptr};
     const int32_t tok[2] = {token, 0};
     const float* emb[2] = {embd, nullptr};
@@ -1044,26 +837,6 @@ int sh_step(sh_ctx* c, sh_state* s, int32_t token, const float* embd, int want_l
 int sh_step2(sh_ctx* c, sh_state* a, int32_t ta, const float* ea, int la, sh_state* b, int32_t tb, const float* eb, int lb,
              float* ha, float* lga, int32_t* besta, float* hb, float* lgb, int32_t* bestb) {
     if (!c || !c->loaded) return fail(SH_E_STATE, "sh_step2: no model loaded");
-    if (c->use_persistent) {
-        if (!a || !b) return fail(SH_E_ARG, "sh_step2: null state");
-        sh_state* st[2] = {a, b};
-        launch_io io;
-        io.tokens[0] = &ta;
-        io.tokens[1] = &tb;
-        io.embd[0] = ta < 0 ? ea : nullptr;
-        io.embd[1] = tb < 0 ? eb : nullptr;
-        io.logits_from = (la || lb) ? 0 : 1;
-        io.hidden_last[0] = ha;
-        io.hidden_last[1] = hb;
-        io.logits[0] = la ? lga : nullptr;
-        io.logits[1] = lb ? lgb : nullptr;
-        io.ids[0] = la ? besta : nullptr;
-        io.ids[1] = lb ? bestb : nullptr;
-        if (besta && !la) *besta = -1;
-        if (bestb && !lb) *bestb = -1;
-        const int rc = run_persistent(c, 2, st, 1, io);
-        if (rc != SK_FALLBACK) return rc;
-    }
     sh_state* st[2] = {a, b};
     const int32_t tok[2] = {ta, tb};
     const float* emb[2] = {ea, eb};
@@ -1084,23 +857,6 @@ int sh_step_batch(sh_ctx* c, sh_state* s, const int32_t* tokens, const float* em
     const int E = c->info.n_embd;
     if (s->ctx != c) return fail(SH_E_STATE, "sh_step_batch: state belongs to another context");
     if (c->use_prefill && n >= 2) return run_prefill(c, s, tokens, embd, n, want_logits != 0, hidden_last, logits, hidden_all, best);
-    if (c->use_persistent) {
-        sh_state* st[2] = {s, nullptr};
-        launch_io io;
-        io.tokens[0] = tokens;
-        io.embd[0] = embd;
-        io.logits_from = want_logits ? n - 1 : n;
-        io.hidden_last[0] = hidden_last;
-        io.hidden_all = hidden_all;
-        io.logits[0] = logits;
-        std::vector<int32_t> ids(n > 0 ? n : 1, -1);
-        io.ids[0] = ids.data();
-        const int rc = run_persistent(c, 1, st, n, io);
-        if (rc != SK_FALLBACK) {
-            if (rc == SH_OK && best) *best = (want_logits && n > 0) ? ids[n - 1] : -1;
-            return rc;
-        }
-    }
     if (s->pos + n > c->info.n_ctx) {
         fprintf(stderr, "seoul-hip: context full (%d)\n", c->info.n_ctx);
         return fail(SH_E_CONTEXT_FULL, "sh_step_batch: context full");
@@ -1130,22 +886,9 @@ int sh_generate(sh_ctx* c, sh_state* a, sh_state* b, int32_t fa, int32_t fb, int
             return fail(SH_E_CONTEXT_FULL, "sh_generate: context full");
         }
     }
-    if (c->use_persistent) {
-        launch_io io;
-        io.greedy = true;
-        io.first[0] = fa;
-        io.first[1] = fb;
-        io.logits_from = 0;
-        io.ids[0] = out_a;
-        io.ids[1] = b ? out_b : nullptr;
-        io.seconds = seconds;
-        const int rc = run_persistent(c, M, st, n, io);
-        if (rc != SK_FALLBACK) return rc;
-    }
     HIPCHK(hipSetDevice(c->device));
     if (n > c->gen_cap) {
-        if (c->gen_out) HIPCHK(hipFree(c->gen_out));
-        HIPCHK(hipMalloc((void**)&c->gen_out, sizeof(int32_t) * 2 * (size_t)n));
+        HIPCHK(regrow((void**)&c->gen_out, sizeof(int32_t) * 2 * (size_t)n));
         c->gen_cap = n;
     }
     hipGraphExec_t g;
@@ -1213,11 +956,8 @@ int bench_inputs(sh_ctx* c) {
     const size_t R = 4 * (size_t)c->info.n_ff + 3 * (size_t)c->info.n_embd + 64;
     const size_t need = 2 * (K > R ? K : R);
     if (c->bench_cap >= need) return SH_OK;
-    if (c->bench_x) HIPCHK(hipFree(c->bench_x));
-    if (c->bench_y) HIPCHK(hipFree(c->bench_y));
+    HIPCHK(regrow2(&c->bench_x, &c->bench_y, need));
     c->bench_cap = need;
-    HIPCHK(hipMalloc((void**)&c->bench_x, c->bench_cap * 4));
-    HIPCHK(hipMalloc((void**)&c->bench_y, c->bench_cap * 4));
     std::vector<float> in(c->bench_cap);
     for (size_t i = 0; i < in.size(); i++) in[i] = 0.01f * (float)((i * 7) % 13) - 0.06f;   // seoul.cpp:668
     HIPCHK(hipMemcpy(c->bench_x, in.data(), in.size() * 4, hipMemcpyHostToDevice));
@@ -1444,10 +1184,7 @@ int sh_q4_gemv(sh_ctx* c, const sh_q4* t, const float* x, int n_in, float* y, in
     const size_t nx = (size_t)n_in * t->t.cols, ny = (size_t)n_in * t->t.rows;
     const size_t need = nx > ny ? nx : ny;
     if (c->bench_cap < need) {
-        if (c->bench_x) HIPCHK(hipFree(c->bench_x));
-        if (c->bench_y) HIPCHK(hipFree(c->bench_y));
-        HIPCHK(hipMalloc((void**)&c->bench_x, need * 4));
-        HIPCHK(hipMalloc((void**)&c->bench_y, need * 4));
+        HIPCHK(regrow2(&c->bench_x, &c->bench_y, need));
         c->bench_cap = need;
     }
     HIPCHK(hipMemcpyAsync(c->bench_x, x, nx * 4, hipMemcpyHostToDevice, c->stream));
@@ -1467,10 +1204,7 @@ int sh_q4_bench(sh_ctx* c, sh_q4* const* tables, int n_tables, int n_in, int cut
         need = n > need ? n : need;
     }
     if (c->bench_cap < need) {
-        if (c->bench_x) HIPCHK(hipFree(c->bench_x));
-        if (c->bench_y) HIPCHK(hipFree(c->bench_y));
-        HIPCHK(hipMalloc((void**)&c->bench_x, need * 4));
-        HIPCHK(hipMalloc((void**)&c->bench_y, need * 4));
+        HIPCHK(regrow2(&c->bench_x, &c->bench_y, need));
         HIPCHK(hipMemset(c->bench_x, 0, need * 4));
         c->bench_cap = need;
     }
@@ -1523,20 +1257,6 @@ int sh_expf(sh_ctx* c, const float* x, long long n, float* y) {
     (void)hipFree(dx);
     if (dy) (void)hipFree(dy);
     if (e != hipSuccess) return fail(SH_E_HIP, std::string("sh_expf: ") + hipGetErrorString(e));
-    return SH_OK;
-}
-
-int sh_step_trace(sh_ctx* c, long long* out, long long cap, int* per_wg, int* grid, double* ticks_per_us) {
-    if (!c || !per_wg || !grid) return fail(SH_E_ARG, "sh_step_trace: null");
-    if (!c->want_trace || !c->trace || !c->trace_per_wg) return fail(SH_E_STATE, "sh_step_trace: no traced launch (SEOUL_HIP_TRACE=1)");
-    const long long n = (long long)c->sk_grid * c->trace_per_wg;
-    *per_wg = c->trace_per_wg;
-    *grid = c->sk_grid;
-    if (ticks_per_us) *ticks_per_us = c->ticks_per_us;
-    if (out) {
-        if (cap < n) return fail(SH_E_ARG, "sh_step_trace: buffer too small");
-        HIPCHK(hipMemcpy(out, c->trace, sizeof(long long) * n, hipMemcpyDeviceToHost));
-    }
     return SH_OK;
 }
 

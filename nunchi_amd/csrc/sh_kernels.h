@@ -93,6 +93,8 @@ struct final_args {
     const float* part_v;       // argmax partials (null when no logits were computed)
     const int* part_i;
     int n_part;
+    const float* logits;       // the word scores [M][ld_logits] the partials were taken over (row 0 is read)
+    int ld_logits;
     step_params* P;
     int advance;               // 1: pos += 1 (and greedy bookkeeping)
 };

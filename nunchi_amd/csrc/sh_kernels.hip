@@ -1380,6 +1380,19 @@ static size_t attn_head_lds(int D, int n_ctx) {
     return sizeof(float) * (4 * (size_t)D + 32 + 16 + 8 + (((size_t)n_ctx + 3) & ~(size_t)3)) + 2 * (size_t)D * tv * sizeof(uint16_t);
 }
 
+// the longest context the decode attention holds: its score row (one float per position) and two value tiles share
+// the workgroup's 160 KB of LDS
+int attn_max_ctx(int grp, int D) {
+    (void)grp;
+    int lo = 0, hi = 1 << 20;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) / 2;
+        if (attn_head_lds(D, mid) <= 160 * 1024) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
 // ---------------------------------------------------------------- end of step
 // Hidden state when no word scores were computed (x += norm(y) * w_post; hidden = norm(x) * w_out, in the CPU's
 // op order), argmax over the word-score partials (first index of the maximum), position advance and the
@@ -1431,7 +1444,11 @@ __global__ __launch_bounds__(256) void k_final(final_args a) {
                 }
                 __syncthreads();
             }
+            // imi's loop (imi/core/hear.cpp:67-68): best = 0, then v replaces it only if logits[v] > logits[best].
+            // The partials give the first maximum over the scores that are not NaN; imi keeps 0 when score 0 is NaN
+            // (nothing compares greater than it) and when every score is NaN (the partials then hold no row)
             best = red_i[0];
+            if (best < 0 || best >= a.ld_logits || (a.logits && isnan(a.logits[(size_t)m * a.ld_logits]))) best = 0;
             __syncthreads();
         }
         if (tid == 0) {

@@ -661,10 +661,26 @@ hipError_t launch_pf_kv(const pf_attn_args& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// LDS of the prefill attention over `ctx` key positions: the group's query rows, staging, one score row per query
+// head of the group and one value tile of 32 positions
+static size_t pf_attn_lds(int grp, int D, int ctx) {
+    return sizeof(float) * ((size_t)2 * grp * D + 4 * (size_t)D + 8 + (size_t)grp * (((size_t)ctx + 3) & ~(size_t)3)) +
+           32 * (size_t)D * sizeof(uint16_t);
+}
+
+int pf_attn_max_ctx(int grp, int D) {
+    int lo = 0, hi = 1 << 20;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) / 2;
+        if (pf_attn_lds(grp, D, mid) <= 160 * 1024) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
 hipError_t launch_pf_attn(const pf_attn_args& a, hipStream_t s) {
     const int grp = a.n_head / a.n_kv;
-    const size_t lds = sizeof(float) * ((size_t)2 * grp * a.D + 4 * (size_t)a.D + 8 + (size_t)grp * ((a.pos0 + a.n + 3) & ~3)) +
-                       32 * (size_t)a.D * sizeof(uint16_t);   // + one value tile of 32 positions
+    const size_t lds = pf_attn_lds(grp, a.D, a.pos0 + a.n);
     if (lds > 160 * 1024 || a.n < 1) return hipErrorInvalidValue;
     const void* fn = a.D == 128 ? (const void*)k_pf_attn<128> : a.D == 64 ? (const void*)k_pf_attn<64>
                    : a.D == 32 ? (const void*)k_pf_attn<32> : nullptr;

@@ -193,6 +193,8 @@ int run_prefill(sh_ctx* c, sh_state* st, const int32_t* tokens, const float* emb
         z.part_v = c->part_v;
         z.part_i = c->part_i;
         z.n_part = grid;
+        z.logits = c->logits;
+        z.ld_logits = I.n_vocab;
         z.P = c->P_dev;
         z.advance = 0;
         PCHK(launch_final(1, z, c->stream));

@@ -479,6 +479,7 @@ int sh_voice_sample(sh_voice* v, const int32_t* hist, int n_frames, const double
         picks[j] = io.picks[j];
         keep[j] = io.keep[j];
     }
+    v->last_need = -1;   // the score rows now hold penalised scores: a pass is sampled once
     return SH_OK;
 }
 

@@ -366,5 +366,10 @@ def rel(a, b) -> float:
 
 
 def top(a) -> int:
-    """imi/core/seoul_check.cpp:15: first index of the maximum."""
-    return int(np.argmax(np.asarray(a)))
+    """imi's greedy pick (imi/core/hear.cpp:67-68, imi/core/seoul_check.cpp:15): best = 0, and score v replaces it
+    only if logits[v] > logits[best]. That is the first index of the maximum; a NaN score never wins, and a NaN at
+    index 0 is never beaten (nothing compares greater than it), so the pick is then 0."""
+    a = np.asarray(a)
+    if a.size == 0 or np.isnan(a[0]):
+        return 0
+    return int(np.argmax(np.where(np.isnan(a), -np.inf, a)))

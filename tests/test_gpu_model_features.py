@@ -2,7 +2,7 @@
 136-142, 288-295, 428-431): rope_freqs angle divisors, sliding-window attention layers (window, pattern and their
 own RoPE base, no divisors), and a 7-tap short conv (6 positions of conv memory). Every hidden state and score is
 compared bit for bit with the oracle, on single steps past the window, step2, device-side greedy ids and a prefill
-longer than the window, on both device step paths.
+longer than the window, through the graph of per-table kernels.
 """
 import numpy as np
 import pytest
@@ -13,15 +13,6 @@ pytestmark = pytest.mark.gpu
 def same(a, b) -> bool:
     a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
     return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
-
-
-@pytest.fixture(params=["kernels", "persistent"])
-def step_path(request, monkeypatch):
-    if request.param == "persistent":
-        monkeypatch.setenv("SEOUL_HIP_STEP", "persistent")
-    else:
-        monkeypatch.delenv("SEOUL_HIP_STEP", raising=False)
-    return request.param
 
 
 @pytest.fixture(scope="module", params=["tiny", "mid"])
@@ -37,7 +28,7 @@ def _prompt(n, vocab, seed):
     return np.random.default_rng(seed).integers(0, vocab, size=n).astype(np.int32)
 
 
-def test_features_steps_and_greedy(feat_model, step_path):
+def test_features_steps_and_greedy(feat_model):
     import nunchi_amd
     import oracle
     path, shape = feat_model
@@ -52,7 +43,7 @@ def test_features_steps_and_greedy(feat_model, step_path):
     assert np.array_equal(ids_g, ids_o)
 
 
-def test_features_step2(feat_model, step_path):
+def test_features_step2(feat_model):
     import nunchi_amd
     import oracle
     path, shape = feat_model
@@ -98,7 +89,7 @@ def wide_head_model(request, model_dir):
     return synth.cached("brain", shape, 36, model_dir), shape
 
 
-def test_head_dim_128_long_context(wide_head_model, step_path):
+def test_head_dim_128_long_context(wide_head_model):
     """Single steps, then 600 device-side greedy ids (several value tiles, key rows past one pass of the block),
     then one more step compared bit for bit."""
     import nunchi_amd
@@ -146,7 +137,7 @@ def q4_1_model(request, model_dir):
     return synth.cached("brain", shape, 42, model_dir), shape
 
 
-def test_q4_1_tables_steps_greedy(q4_1_model, step_path):
+def test_q4_1_tables_steps_greedy(q4_1_model):
     import nunchi_amd
     import oracle
     path, shape = q4_1_model

@@ -76,21 +76,3 @@ def test_q6k_prefill(q6_model):
     for p in range(len(toks)):
         assert same(hall_g[p], hall_o[p]), p
     assert same(lg, lo) and bg == oracle.top(lo)
-
-
-def test_q6k_persistent_request_runs_per_table(q6_model, monkeypatch):
-    """SEOUL_HIP_STEP=persistent with a Q6_K word table: the step kernel does not read Q6_K, so the context runs the
-    per-table kernels, with the same numbers."""
-    import nunchi_amd
-    import oracle
-    monkeypatch.setenv("SEOUL_HIP_STEP", "persistent")
-    path, shape = q6_model
-    g = nunchi_amd.Brain(path, n_ctx=64)
-    o = oracle.Engine(path, threads=4, n_ctx=64)
-    for t in _prompt(4, shape.n_vocab, 27):
-        hg, lg, _ = g.step(int(t))
-        ho, lo = o.step(int(t))
-        assert same(hg, ho) and same(lg, lo)
-    ids_g, _ = g.generate(3, 16)
-    ids_o, _ = o.greedy(3, 16)
-    assert np.array_equal(ids_g, ids_o)

@@ -14,17 +14,6 @@ from conftest import rel
 
 pytestmark = pytest.mark.gpu
 
-@pytest.fixture(params=["kernels", "persistent"])
-def step_path(request, monkeypatch):
-    """Both device paths of a step: the graph of per-table kernels (the default) and the persistent step kernel
-    (SEOUL_HIP_STEP=persistent); contexts read the choice when they are made."""
-    if request.param == "persistent":
-        monkeypatch.setenv("SEOUL_HIP_STEP", "persistent")
-    else:
-        monkeypatch.delenv("SEOUL_HIP_STEP", raising=False)
-    return request.param
-
-
 def same(a, b) -> bool:
     a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
     return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
@@ -47,15 +36,15 @@ def _compare_steps(path, tokens, n_ctx=256, threads=4):
         assert bg == oracle.top(lo) == int(np.argmax(lg))
 
 
-def test_tiny_model_steps(tiny_model, step_path):
+def test_tiny_model_steps(tiny_model):
     _compare_steps(tiny_model, _prompt(40, 1000, 1))
 
 
-def test_seoul_width_steps(mid_model, step_path):
+def test_seoul_width_steps(mid_model):
     _compare_steps(mid_model, _prompt(24, 4096, 2))
 
 
-def test_embedding_input_and_no_logits(tiny_model, step_path):
+def test_embedding_input_and_no_logits(tiny_model):
     import nunchi_amd
     import oracle
     g = nunchi_amd.Brain(tiny_model, n_ctx=64)
@@ -73,7 +62,7 @@ def test_embedding_input_and_no_logits(tiny_model, step_path):
             assert lg is None and bg == -1
 
 
-def test_step2_equals_two_steps(tiny_model, step_path):
+def test_step2_equals_two_steps(tiny_model):
     """imi/core/seoul.cpp:222-224: each conversation of step2 gets exactly its own step's numbers."""
     import nunchi_amd
     g = nunchi_amd.Brain(tiny_model, n_ctx=64)
@@ -94,7 +83,7 @@ def test_step2_equals_two_steps(tiny_model, step_path):
     assert g.pos == 12 and b.pos == 12
 
 
-def test_step2_matches_oracle(mid_model, step_path):
+def test_step2_matches_oracle(mid_model):
     import nunchi_amd
     import oracle
     g = nunchi_amd.Brain(mid_model, n_ctx=64)
@@ -124,7 +113,7 @@ def test_step_batch_matches_oracle(tiny_model):
     assert g.pos == 70
 
 
-def test_greedy_generation_matches_oracle(mid_model, step_path):
+def test_greedy_generation_matches_oracle(mid_model):
     import nunchi_amd
     import oracle
     g = nunchi_amd.Brain(mid_model, n_ctx=128)
@@ -140,7 +129,7 @@ def test_greedy_generation_matches_oracle(mid_model, step_path):
     assert g.pos == 8 + 48 and secs > 0
 
 
-def test_greedy_two_conversations(tiny_model, step_path):
+def test_greedy_two_conversations(tiny_model):
     import nunchi_amd
     import oracle
     g = nunchi_amd.Brain(tiny_model, n_ctx=96)
@@ -172,18 +161,18 @@ def _long_greedy(path, vocab, n_ctx, n_gen, seed):
     assert same(hg, ho) and same(lg, lo)
 
 
-def test_long_context_attention(mid_model, step_path):
+def test_long_context_attention(mid_model):
     """Head width 64 over 1,200 positions: several value tiles and key rows per thread in the decode attention."""
     _long_greedy(mid_model, 4096, 1280, 1200, 13)
 
 
-def test_long_context_attention_narrow_heads(tiny_model, step_path):
+def test_long_context_attention_narrow_heads(tiny_model):
     """Head width 32 over 600 positions."""
     _long_greedy(tiny_model, 1000, 640, 600, 14)
 
 
 @pytest.mark.parametrize("shape", ["tiny", "mid"])
-def test_sharp_attention_in_order_sum(model_dir, shape, step_path):
+def test_sharp_attention_in_order_sum(model_dir, shape):
     """q/k norm weights scaled by 6: scores spread over hundreds and most e_t = expf(s_t - max) fall far below the
     double sum's last bit, so the sum has rounding steps and the kernel adds it in position order (its exact-sum
     shortcut does not apply); the default models take the shortcut."""
@@ -218,7 +207,7 @@ def test_state_semantics(tiny_model):
     assert g.pos == 8
 
 
-def test_full_seoul_step_and_greedy(model_dir, step_path):
+def test_full_seoul_step_and_greedy(model_dir):
     """cfg 2: the full Seoul-shaped model, a 32-token prompt, then 256 greedy ids; every id and the final state agree."""
     import nunchi_amd
     import oracle
@@ -259,3 +248,92 @@ def test_sharp_attention_prefill(model_dir, shape):
     for p in range(len(toks)):
         assert same(hall_g[p], hall_o[p]), p
     assert same(lg, lo) and bg == oracle.top(lo)
+
+
+def test_full_seoul_two_conversations_greedy(model_dir):
+    """cfg 2 at B=2: the full Seoul-shaped model, two seeded 32-token prompts through step2 (one weight read for
+    both conversations, imi/core/seoul.cpp:208-350), then 256 greedy ids each from the device loop; every id of both
+    conversations agrees with the oracle's greedy2, and so do the scores of one more step2."""
+    import nunchi_amd
+    import oracle
+    from nunchi_amd import synth
+    path = synth.cached("brain", synth.SEOUL, 0, model_dir)
+    g = nunchi_amd.Brain(path, n_ctx=512)
+    o = oracle.Engine(path, threads=8, n_ctx=512)
+    pa, pb = _prompt(32, synth.SEOUL.n_vocab, 0), _prompt(32, synth.SEOUL.n_vocab, 1)
+    gb, ob = g.new_state(), o.new_state()
+    for i in range(32):
+        last = i == 31
+        (hga, lga, bga), (hgb, lgb, bgb) = g.step2(int(pa[i]), None, last, gb, int(pb[i]), None, last)
+        hoa, loa, hob, lob = o.step2(int(pa[i]), None, last, ob, int(pb[i]), None, last)
+        assert same(hga, hoa) and same(hgb, hob), i
+    assert same(lga, loa) and same(lgb, lob)
+    assert bga == oracle.top(loa) and bgb == oracle.top(lob)
+    ids_ga, ids_gb, _ = g.generate(bga, 256, b=gb, first_b=bgb)
+    ids_oa, ids_ob, _ = o.greedy2(ob, bga, bgb, 256)
+    assert np.array_equal(ids_ga, ids_oa) and np.array_equal(ids_gb, ids_ob)
+    (hga, lga, _), (hgb, lgb, _) = g.step2(int(ids_ga[-1]), None, True, gb, int(ids_gb[-1]), None, True)
+    hoa, loa, hob, lob = o.step2(int(ids_oa[-1]), None, True, ob, int(ids_ob[-1]), None, True)
+    assert same(hga, hoa) and same(lga, loa) and same(hgb, hob) and same(lgb, lob)
+
+
+def test_voice_frame_brain_half_long_context(model_dir):
+    """cfg 4's brain half (imi/core/flow.cpp:118, imi/core/seoul.cpp:208-350): the full Seoul-shaped model with a
+    4096-position context; slot A is prefilled to position 2048 with seeded words, slot B (the voice slot) with 24
+    embedding rows; then frames of step2 with A a greedy text step with scores and B a brain step fed an input
+    vector (the feedback row sum's place) without scores. Hidden states, A's scores and picks are bit for bit the
+    oracle's at every frame."""
+    import nunchi_amd
+    import oracle
+    from nunchi_amd import synth
+    path = synth.cached("brain", synth.SEOUL, 0, model_dir)
+    n_ctx = 4096
+    g = nunchi_amd.Brain(path, n_ctx=n_ctx)
+    o = oracle.Engine(path, threads=8, n_ctx=n_ctx)
+    words = _prompt(2048, synth.SEOUL.n_vocab, 21)
+    hg, lg, bg, _ = g.step_batch(words)
+    ho, lo, _ = o.step_batch(words)
+    assert same(hg, ho) and same(lg, lo) and bg == oracle.top(lo)
+    rng = np.random.default_rng(22)
+    vb = rng.standard_normal((24, synth.SEOUL.n_embd)).astype(np.float32)
+    gb, ob = g.new_state(), o.new_state()
+    g.swap_state(gb)
+    o.swap_state(ob)
+    g.step_batch(embd=vb, want_logits=False)
+    o.step_batch(embd=vb, want_logits=False)
+    g.swap_state(gb)
+    o.swap_state(ob)
+    assert g.pos == 2048 and gb.pos == 24
+    ta = bg
+    for frame in range(6):
+        fb = rng.standard_normal(synth.SEOUL.n_embd).astype(np.float32)
+        (hga, lga, bga), (hgb, _, _) = g.step2(int(ta), None, True, gb, -1, fb, False)
+        hoa, loa, hob, _ = o.step2(int(ta), None, True, ob, -1, fb, False)
+        assert same(hga, hoa) and same(lga, loa) and same(hgb, hob), frame
+        assert bga == oracle.top(loa), frame
+        ta = bga
+    assert g.pos == 2054 and gb.pos == 30
+
+
+def test_destroy_context_before_its_states_and_tables(tiny_model):
+    """The C ABI's ownership rule (include/seoul_hip.h): sh_destroy releases the device memory of the context's
+    remaining states and tables and detaches their handles; sh_state_free / sh_q4_free afterwards only free the
+    handles. Called in that order through the raw C functions, every call returns SH_OK, and a fresh context then
+    steps as before."""
+    import ctypes as C
+    import nunchi_amd
+    L = nunchi_amd.load_library()
+    ctx, st, tab = C.c_void_p(), C.c_void_p(), C.c_void_p()
+    assert L.sh_create(0, C.byref(ctx)) == 0
+    assert L.sh_load(ctx, tiny_model.encode(), 32) == 0
+    assert L.sh_state_new(ctx, C.byref(st)) == 0
+    q = np.ascontiguousarray(__import__("conftest").q4_random(64, 256, 3))
+    assert L.sh_q4_create(ctx, q.ctypes.data_as(C.c_void_p), 64, 256, C.byref(tab)) == 0
+    h = np.zeros(256, np.float32)
+    assert L.sh_step(ctx, st, 5, None, 0, h.ctypes.data_as(C.c_void_p), None, None) == 0
+    assert L.sh_destroy(ctx) == 0
+    assert L.sh_state_free(st) == 0
+    assert L.sh_q4_free(tab) == 0
+    g = nunchi_amd.Brain(tiny_model, n_ctx=32)
+    h2 = g.step(5, want_logits=False)[0]
+    assert same(h, h2)

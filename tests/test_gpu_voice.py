@@ -160,6 +160,9 @@ def test_device_sampling(tiny_voice):
     with pytest.raises(nunchi_amd.SeoulError):
         g.sample(np.zeros((0, g.n_cb), np.int32), [0.5, 1.0])
     assert g.sample(np.zeros((0, g.n_cb), np.int32), [0.0, 0.0])[0].tolist() == [0, 0]
+    # a pass is sampled once: its score rows now hold the penalised scores
+    with pytest.raises(nunchi_amd.SeoulError):
+        g.sample(np.zeros((0, g.n_cb), np.int32), [0.0, 0.0])
 
 
 def test_device_sampling_ragged_vocab(model_dir):

@@ -127,3 +127,69 @@ def test_engine_q4_1_tables_vs_float64_truth(model_dir):
     for i, t in enumerate(toks):
         h, lg = e.step(t)
         assert rel(h, hid_c[i]) < 5e-6 and rel(lg, lg_c[i]) < 5e-6
+
+
+def _feature_shape(**kw):
+    from nunchi_amd import synth
+    return synth.BrainShape(**{**synth.TINY.__dict__, **kw})
+
+
+FEATURES = {
+    # rope_freqs angle divisors (imi/core/seoul.cpp:19-28 with ff, ref_exact.py:41-48)
+    "rope_freqs": dict(rope_freqs=True),
+    # a sliding window of 3 positions on attention layer 1, its own RoPE base and no divisors (seoul.cpp:99-114,
+    # 288-295, 428-431); layer 3 stays global
+    "sliding_window": dict(sliding_window=3, swa_layers=(1,), rope_freqs=True),
+    # 7-tap short conv: 6 positions of conv memory (seoul.cpp:136-142, 407-423)
+    "conv_7_taps": dict(conv_kernel=7),
+    # head_dim 128: 8 query heads over 2 kv heads (a 1024-wide attention over n_embd 256; q|k|v|gate rows stay a
+    # multiple of 8, as imi's table build requires)
+    "head_dim_128": dict(n_head=8, n_head_kv=2, head_dim=128),
+}
+FEATURE_TOKENS = [5, 17, 300, 999, 0, 42, 640, 77]
+# model seeds whose 8 positions have no int8 code landing within fp32 rounding of a rounding boundary (such a code
+# differs between the two arithmetics and moves its position at the cut's own scale, ~1e-3; most seeds have one)
+FEATURE_SEEDS = {"rope_freqs": 44, "sliding_window": 44, "conv_7_taps": 47, "head_dim_128": 44}
+
+
+@pytest.mark.parametrize("feature", sorted(FEATURES))
+def test_engine_feature_paths_vs_float64_truth(model_dir, feature):
+    """The oracle's loader-feature paths against the float64 restatement with the cuts applied, position by
+    position past the window (8 positions, window 3), at the bound the Q4_0 and Q4_1 checks use.
+
+    With head_dim 128 the 1024 attention outputs per position are cut to int8 at every attention layer, and now and
+    then one of them lies within fp32 rounding of a rounding boundary, so that one code differs between the two
+    arithmetics and the position moves at the cut's own scale (~1e-3). There the bound is: every position within
+    2e-2 and at least 6 of the 8 within 5e-6. A wrong score scale, rope pairing or head grouping would move every
+    position from the second on (position 0 attends to itself alone, at angle 0), so it cannot pass."""
+    from nunchi_amd import synth
+    path = synth.cached("brain", _feature_shape(**FEATURES[feature]), FEATURE_SEEDS[feature], model_dir)
+    hid_c, lg_c = exact.brain(path, tokens=FEATURE_TOKENS, cut=True)
+    e = oracle.Engine(path, threads=3, n_ctx=32)
+    errs = []
+    for i, t in enumerate(FEATURE_TOKENS):
+        h, lg = e.step(t)
+        errs.append(max(rel(h, hid_c[i]), rel(lg, lg_c[i])))
+    if feature == "head_dim_128":
+        assert max(errs) < 2e-2 and sum(x < 5e-6 for x in errs) >= 6, errs
+    else:
+        assert max(errs) < 5e-6, errs
+
+
+@pytest.mark.parametrize("dropped", ["sliding_window", "rope_freqs"])
+def test_feature_pins_see_the_feature(model_dir, dropped):
+    """The pins above discriminate: the oracle on the windowed model (or the one with angle divisors) against the
+    float64 truth of the same weights without the window (or the divisors) is far outside the bound once the window
+    is passed (or from the second position)."""
+    from nunchi_amd import synth
+    kw = FEATURES["sliding_window"]
+    path = synth.cached("brain", _feature_shape(**kw), 44, model_dir)
+    other = dict(kw, sliding_window=0) if dropped == "sliding_window" else dict(kw, rope_freqs=False, swa_layers=())
+    path_other = synth.cached("brain", _feature_shape(**other), 44, model_dir)
+    hid_o, _ = exact.brain(path_other, tokens=FEATURE_TOKENS, cut=True)
+    e = oracle.Engine(path, threads=3, n_ctx=32)
+    worst = 0.0
+    for i, t in enumerate(FEATURE_TOKENS):
+        h, _ = e.step(t)
+        worst = max(worst, rel(h, hid_o[i]))
+    assert worst > 1e-3, (dropped, worst)

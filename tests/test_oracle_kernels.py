@@ -315,3 +315,29 @@ def test_q4_1_gemv_float64_and_scalar_and_two_inputs(rows, cols):
     q0 = np.zeros(blk.shape, dtype=[("d", "<f2"), ("qs", "u1", 16)])
     q0["d"], q0["qs"] = blk["d"], blk["qs"]
     assert not np.allclose(oracle.Q4Table(q0, rows, cols).gemv(x[0])[0], y0)
+
+
+def _imi_pick(lg):
+    """imi/core/hear.cpp:67-68 as written: best = 0; v replaces it only if logits[v] > logits[best]."""
+    best = 0
+    for v in range(1, len(lg)):
+        if lg[v] > lg[best]:
+            best = v
+    return best
+
+
+def test_top_follows_imi_loop_with_ties_and_nan():
+    """oracle.top against imi's literal greedy loop on scores with forced ties, NaNs (at 0, at the maximum,
+    everywhere) and infinities: the first maximum wins, a NaN never wins, a NaN at index 0 is never beaten."""
+    import oracle
+    rng = np.random.default_rng(5)
+    cases = [np.array([1.0, 3.0, 3.0, 2.0], np.float32), np.array([np.nan, 5.0, 7.0], np.float32),
+             np.array([1.0, np.nan, 3.0, np.nan, 3.0], np.float32), np.full(6, np.nan, np.float32),
+             np.array([-np.inf, -np.inf, np.nan], np.float32), np.array([-np.inf, np.nan, 2.0, np.inf, np.inf], np.float32),
+             np.array([0.0, -0.0, 0.0], np.float32)]
+    for _ in range(300):
+        a = rng.integers(-3, 4, size=int(rng.integers(1, 40))).astype(np.float32)   # many ties
+        a[rng.random(a.size) < 0.15] = np.nan
+        cases.append(a)
+    for a in cases:
+        assert oracle.top(a) == _imi_pick(a), a
