@@ -116,6 +116,13 @@ int sh_q4_gemv(sh_ctx* ctx, const sh_q4* t, const float* x, int n_in, float* y, 
  * to int8 per 32 columns (round half to even), each 32-column block's integer sum exact, then imi's per-row chains
  * over the blocks (imi_q4_group_batch, imi/core/tables.cpp:419-454); bit for bit sh_q4_gemv per input. */
 int sh_q4_gemm(sh_ctx* ctx, const sh_q4* t, const float* x, int n, float* y);
+/* sh_q4_gemm on device-resident buffers with no device allocation: x_dev[n][cols] in, y_dev[n][rows] out, the same
+ * numbers bit for bit. No counterpart in the reference; it is for callers that cannot allocate (code under HIP
+ * graph capture, serving loops with a fixed memory budget). The int8 cut of the input goes to a fixed scratch array
+ * of device memory the library holds on every device it runs on until the process ends (1.25 MiB per device), so
+ * n * cols <= 1048576 (else SH_E_ARG, nothing launched) and 1 <= n <= 512. Calls on one device share that scratch:
+ * calls that overlap on one device race. Enqueued on the context's stream without waiting (sh_sync waits). */
+int sh_q4_gemm_noalloc(sh_ctx* ctx, const sh_q4* t, const float* x_dev, int n, float* y_dev);
 /* Dequantized rows: out[n][cols] = (code - 8) * d of rows ids[n] (the input-row lookup of a tied word table,
  * imi/core/seoul.cpp:363, ggml_get_rows in imi/brain.cpp:161). Bit-exact. */
 int sh_q4_rows(sh_ctx* ctx, const sh_q4* t, const int32_t* ids, int n, float* out);

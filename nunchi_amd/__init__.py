@@ -22,7 +22,7 @@ EXPORTS = [
     "sh_last_error", "sh_create", "sh_destroy", "sh_load", "sh_info", "sh_check_model", "sh_state_new", "sh_state_free", "sh_state_reset",
     "sh_state_pos", "sh_state_set_pos", "sh_step", "sh_step2", "sh_step_batch", "sh_generate", "sh_bench_tables",
     "sh_bench_kernel",
-    "sh_q4_create", "sh_q4_free", "sh_q4_rows", "sh_q4_gemv", "sh_q4_gemm", "sh_q4_gemv_dev", "sh_q4_bench", "sh_q4_bench_kernel", "sh_expf", "sh_sync",
+    "sh_q4_create", "sh_q4_free", "sh_q4_rows", "sh_q4_gemv", "sh_q4_gemm", "sh_q4_gemm_noalloc", "sh_q4_gemv_dev", "sh_q4_bench", "sh_q4_bench_kernel", "sh_expf", "sh_sync",
     "sh_voice_load", "sh_voice_free", "sh_voice_info", "sh_voice_begin_frame", "sh_voice_base", "sh_voice_pass",
     "sh_voice_feedback", "sh_voice_sample",
 ]
@@ -85,6 +85,7 @@ def load_library(path: str = LIB_PATH):
         "sh_q4_gemv": (i, [vp, vp, vp, i, vp, i]),
         "sh_q4_gemv_dev": (i, [vp, vp, vp, i, vp, i]),
         "sh_q4_gemm": (i, [vp, vp, vp, i, vp]),
+        "sh_q4_gemm_noalloc": (i, [vp, vp, vp, i, vp]),
         "sh_q4_bench": (i, [vp, vp, i, i, i, i, P(d)]),
         "sh_q4_bench_kernel": (i, [vp, vp, i, i, i, i, P(d)]),
         "sh_expf": (i, [vp, vp, C.c_longlong, vp]),

@@ -28,6 +28,8 @@ hipError_t launch_q4_rows(const q4dev& T, const int32_t* ids, int n, float* out,
 hipError_t launch_expf(const float* x, float* y, long long n, hipStream_t s);
 // the longest contexts the decode and prefill attention kernels hold (their score rows live in LDS)
 int attn_max_ctx(int grp, int D);
+// the no-allocation product's per-device scratch address (sh_noalloc.hip), looked up once per device
+int noalloc_setup(int device);
 int pf_attn_max_ctx(int grp, int D);
 }
 

@@ -432,6 +432,8 @@ int sh_create(int device, sh_ctx** out) {
     HIPCHK(hipGetDeviceCount(&n));
     if (device < 0 || device >= n) return fail(SH_E_ARG, "sh_create: no such device");
     HIPCHK(hipSetDevice(device));
+    const int rs = noalloc_setup(device);   // the no-allocation entry point's scratch address on this device
+    if (rs != SH_OK) return rs;
     auto c = std::make_unique<sh_ctx>();
     c->device = device;
     HIPCHK(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
