@@ -22,7 +22,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-GATE_UP_TRAFFIC_BYTES = 19353293   # counters: FETCH_SIZE 9436.1 KiB x 1.9987 + WRITE_SIZE 40 KiB x 1.0 per launch
+GATE_UP_TRAFFIC_BYTES = 19275131   # counters: 149,528 128-B + 1,478 64-B read requests + 40 KiB WRITE_SIZE per launch
 N_CTX = 512
 PROMPT = 32
 
@@ -53,14 +53,14 @@ def gpu_decode(brain, steps, warmup, b2: bool):
     t0 = time.perf_counter()
     out = brain.generate(ba, steps, b=sb, first_b=bb or 0, a=sa)
     wall = time.perf_counter() - t0
-    ids, dev = (out[0], out[2]) if b2 else out
+    ids, dev = ((out[0], out[1]), out[2]) if b2 else out
     tokens = steps * (2 if b2 else 1)
     return tokens / wall, ids, dev, wall
 
 
 def cpu_decode(path, threads, steps, b2: bool, runs: int = 1):
     """imi's CPU path (the oracle restatement): `runs` conversations, each a 32-token prompt then `steps` greedy
-    ids; returns (tokens/s over the generated tokens of all runs, ids of run 0, seconds)."""
+    ids; returns (tokens/s over the generated tokens of all runs, ids of run 0 (B=2: both conversations'), seconds)."""
     import oracle
     eng = oracle.Engine(path, threads=threads, n_ctx=N_CTX)
     tok, secs, ids0 = 0, 0.0, None
@@ -73,6 +73,7 @@ def cpu_decode(path, threads, steps, b2: bool, runs: int = 1):
                 last = i == PROMPT - 1
                 _, la, _, lb = eng.step2(int(pa[i]), None, last, sb, int(pb[i]), None, last)
             oa, ob, t = eng.greedy2(sb, oracle.top(la), oracle.top(lb), steps)
+            oa = (oa, ob)
             tok += 2 * steps
         else:
             for i in range(PROMPT):
@@ -206,6 +207,93 @@ def cpu_prefill(path, threads):
     return time.perf_counter() - t0, lg
 
 
+def cpu_info():
+    """The host CPU as this process sees it: model name, logical CPUs in the affinity mask, the physical cores they
+    sit on and the SMT width (logical CPUs per core)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), model)
+    except OSError:
+        pass
+    aff = sorted(os.sched_getaffinity(0))
+    cores, smt = set(), 1
+    for c in aff:
+        base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+        try:
+            with open(base + "physical_package_id") as f1, open(base + "core_id") as f2:
+                cores.add((f1.read().strip(), f2.read().strip()))
+            with open(base + "thread_siblings_list") as f3:
+                sib = f3.read().strip()
+            smt = max(smt, sum(int(b) - int(a) + 1 if "-" in x else 1
+                               for x in sib.split(",") for a, b in [x.split("-") if "-" in x else (x, x)]))
+        except OSError:
+            pass
+    return {"model": model, "logical_cpus": len(aff), "physical_cores": len(cores) or None, "smt_width": smt}
+
+
+# one Seoul-shaped layer's linears (rows, cols), imi's table order: q, k, v, o, gate, up, down
+LAYER_TABLES = ((2048, 2048), (512, 2048), (512, 2048), (2048, 2048), (8192, 2048), (8192, 2048), (2048, 8192))
+LAYER_COPIES = 16   # distinct device copies in rotation: 16 x 34.2 MB, more than the 256 MB MALL holds
+
+
+def layer_weights():
+    from nunchi_amd import synth
+    rng = np.random.default_rng(300)
+    w = [synth.q4_0_random(rng, r, c) for r, c in LAYER_TABLES]
+    x = np.random.default_rng(301).standard_normal((2, 8192)).astype(np.float32)
+    return w, x
+
+
+def gpu_layer(ctx, reps):
+    """cfg 1 on the device: the layer's 7 tables through the kernel-level GEMV (imi's int8 cut per 32 columns),
+    LAYER_COPIES copies in rotation; returns per-layer microseconds at B=1 and B=2 and the B=2 outputs of copy 0."""
+    import nunchi_amd
+    w, x = layer_weights()
+    tabs = [nunchi_amd.Q4Table(ctx, w[i], r, c) for _ in range(LAYER_COPIES) for i, (r, c) in enumerate(LAYER_TABLES)]
+    out = [tabs[i].gemv(x[:, :c]) for i, (_, c) in enumerate(LAYER_TABLES)]
+    us1 = nunchi_amd.q4_bench(ctx, tabs, n_in=1, cut_mode=0, reps=reps) * len(LAYER_TABLES)
+    us2 = nunchi_amd.q4_bench(ctx, tabs, n_in=2, cut_mode=0, reps=reps) * len(LAYER_TABLES)
+    for t in tabs:
+        t._free()
+    return us1, us2, out
+
+
+def cpu_layer(threads, seconds=2.0):
+    """cfg 1 on the oracle (imi's group / group2 kernels on a `threads` team): per-layer microseconds at B=1 and
+    B=2 (each table's fastest rep of enough reps for about `seconds` in all), and the B=2 outputs."""
+    import oracle
+    w, x = layer_weights()
+    res, out = [], []
+    for n_in in (1, 2):
+        tot = 0.0
+        for i, (r, c) in enumerate(LAYER_TABLES):
+            t = oracle.Q4Table(w[i], r, c, threads=threads)
+            y, s1 = t.gemv(x[:n_in, :c], reps=3)
+            reps = max(3, int(seconds / len(LAYER_TABLES) / max(s1, 1e-6)))
+            _, sec = t.gemv(x[:n_in, :c], reps=reps)   # the fastest rep
+            tot += sec
+            if n_in == 2:
+                out.append(y)
+            del t
+        res.append(tot * 1e6)
+    return res[0], res[1], out
+
+
+def cpu_cfg0(threads, seconds=2.0):
+    """cfg 0 on the oracle: imi/kernels/q4x8's GEMV 8192 x 2048, the fastest of about `seconds` of reps on one table
+    (its figure of merit: table GB/s)."""
+    import oracle
+    from nunchi_amd import synth
+    q = synth.q4_0_random(np.random.default_rng(100), 8192, 2048)
+    x = np.random.default_rng(5).standard_normal(2048).astype(np.float32)
+    t = oracle.Q4x8Table(q, 8192, 2048, threads=threads)
+    _, s1 = t.gemv(x, reps=3)
+    reps = max(3, int(seconds / max(s1, 1e-6)))
+    _, sec = t.gemv(x, reps=reps)   # the fastest rep
+    return 8192 * 64 * 18 / sec / 1e9
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -217,9 +305,14 @@ def main():
     ap.add_argument("--voice-frames", type=int, default=64, help="timed voice frames (cfg 4); 0 = skip")
     ap.add_argument("--prefill-reps", type=int, default=10, help="timed hearing-window prefills (cfg 3); 0 = skip")
     ap.add_argument("--cpu-voice-frames", type=int, default=8)
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the decode runs and the in-step kernel timing (the launches a kernel trace of the step "
+                         "should average), no CPU legs")
     ap.add_argument("--counters-workload", action="store_true",
                     help="only the launches the hardware-counter runs read: a streaming kernel of known size (the "
-                         "exponential over 16 Mi floats: 64 MiB read, 64 MiB written) and 64 FFN gate|up launches")
+                         "exponential over 16 Mi floats: 64 MiB read, 64 MiB written), 64 read-only GEMVs of known "
+                         "size (8192 x 2048 Q4_0, 64 distinct copies: 9,437,184 table bytes each), 64 FFN gate|up "
+                         "launches and two hearing-window prefills")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (conversations shard across "
@@ -236,14 +329,31 @@ def main():
     if args.counters_workload:
         x = np.linspace(-10.0, 10.0, 16 << 20, dtype=np.float32)
         brain.ctx.expf(x)
+        copies = [nunchi_amd.Q4Table(brain.ctx, synth.q4_0_random(np.random.default_rng(100 + i), 8192, 2048), 8192, 2048)
+                  for i in range(64)]
+        nunchi_amd.q4_bench(brain.ctx, copies, n_in=1, cut_mode=1, reps=64)
+        rd = nunchi_amd.q4_bench_kernel(brain.ctx, copies, n_in=1, cut_mode=1, reps=64)
+        for t in copies:
+            t._free()
         gu = brain.bench_kernel("ffn_gate_up", n_in=1, reps=64)
+        pt, _, _ = gpu_prefill(brain, 1)
         print(json.dumps({"counters_workload": {"copy_bytes_read": int(x.nbytes), "copy_bytes_written": int(x.nbytes),
+                                                "read_gemv_table_bytes": 8192 * 64 * 18, "read_gemv_avg_us": round(rd, 3),
                                                 "ffn_gate_up_avg_us": round(gu["avg_us"], 3),
-                                                "ffn_gate_up_bytes_per_launch": int(gu["bytes_per_launch"])}}))
+                                                "ffn_gate_up_bytes_per_launch": int(gu["bytes_per_launch"]),
+                                                "prefill_ms": round(float(pt.min()) * 1e3, 3)}}))
         return
 
     tok_s_b1, ids_b1, dev_b1, wall_b1 = gpu_decode(brain, args.steps, args.warmup, b2=False)
     tok_s_b2, ids_b2, dev_b2, wall_b2 = gpu_decode(brain, args.steps, args.warmup, b2=True)
+    # the dominant kernel as it runs inside the step: inputs just written by the step's previous kernel, tables from
+    # HBM (16 launches per step over 32 steps)
+    gu_step = brain.bench_step_kernel("ffn_gate_up", n_in=1, steps=32)
+    if args.decode_only:
+        print(json.dumps({"decode_only": {"b1_tokens_per_s": round(tok_s_b1, 1), "b2_tokens_per_s": round(tok_s_b2, 1),
+                                          "ffn_gate_up_in_step_us": round(gu_step["avg_us"], 3),
+                                          "launches": gu_step["launches"]}}), flush=True)
+        return
 
     # the per-table kernels (the same stages as separate launches; the step kernel's fallback path)
     gu = brain.bench_kernel("ffn_gate_up", n_in=1, reps=64)
@@ -266,8 +376,12 @@ def main():
     cfg0_kernel_us = nunchi_amd.q4_bench_kernel(ctx, copies, n_in=1, cut_mode=1, reps=256)   # the kernel itself
     cfg0_bytes = 8192 * 64 * 18 + 2048 * 4 + 8192 * 4
     del copies
+    # cfg 1: one layer's linears, B=1 and B=2 (two inputs riding each table read)
+    l_us1, l_us2, l_out = gpu_layer(ctx, reps=16 * len(LAYER_TABLES) * 8)
+    layer_bytes = sum(r * c // 32 * 18 for r, c in LAYER_TABLES)
 
     gu_gbs = gu["bytes_per_launch"] / (gu["avg_us"] * 1e-6) / 1e9
+    gs_gbs = gu_step["bytes_per_launch"] / (gu_step["avg_us"] * 1e-6) / 1e9
     # algorithmic bytes of a decode step: every table once (device layout = file bytes: 16 B codes + 2 B scale per
     # 32 weights), the fp32 norm / conv vectors, and the K and V rows the step's attention reads (positions 0..pos of
     # n_attn layers x n_kv heads x D, fp16), averaged over the generated positions
@@ -301,21 +415,24 @@ def main():
         "step_hbm_fraction": {"b1": round(step_bytes * tok_s_b1 / 1e9 / HBM_PEAK_GBS, 4),
                               "b2": round(step_bytes * tok_s_b2 / 2 / 1e9 / HBM_PEAK_GBS, 4),
                               "bytes_per_step": int(step_bytes)},
-        # the dominant kernel of the step: FFN gate|up (16 launches per step, the largest share of its time), each
-        # launch timed alone with HIP events on the context's stream, rotating over the 16 layers' tables
+        # the dominant kernel of the step: FFN gate|up (16 launches per step, the largest share of its time), timed
+        # inside whole steps (events of each launch's own dispatch on the context's stream, 512 launches)
         "roofline": {
             "kernel": "k_gemv_norm<1, EPI_SWIGLU, 2> (FFN gate|up 16384 x 2048 Q4_0 with the post-norm residual, RMS "
                       "norm, int8 cut and SwiGLU fused; B=1)",
             "bound": "hbm",
-            "achieved": round(gu_gbs, 1),
+            "achieved": round(gs_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+            "frac": round(gs_gbs / HBM_PEAK_GBS, 4),
             # HBM bytes per launch from the FETCH_SIZE / WRITE_SIZE counter runs of `bench.py --counters-workload`,
-            # calibrated on a streaming kernel of known size (profiles/ffn_gate_up_counters_seoul.md)
+            # calibrated on a streaming kernel and a read-only GEMV of known sizes
             "traffic": GATE_UP_TRAFFIC_BYTES,
-            "launch_us": round(gu["avg_us"], 3),
-            "bytes_per_launch": int(gu["bytes_per_launch"]),
+            "launch_us": round(gu_step["avg_us"], 3),
+            "launches_timed": gu_step["launches"],
+            "bytes_per_launch": int(gu_step["bytes_per_launch"]),
+            "isolated_launch_us": round(gu["avg_us"], 3),
+            "isolated_frac": round(gu_gbs / HBM_PEAK_GBS, 4),
         },
         "kernels": {
             "ffn_gate_up_per_table": {"avg_us": round(gu["avg_us"], 3), "GBs": round(gu_gbs, 1), "frac": round(gu_gbs / HBM_PEAK_GBS, 4)},
@@ -328,6 +445,13 @@ def main():
             "layer_tables_b1": {"avg_launch_us": round(tables1["avg_launch_us"], 3), "ms_per_pass": round(tables1["ms_per_pass"], 4),
                                 "GBs": round(tables1["bytes_per_pass"] / tables1["launches"] / tables1["avg_launch_us"] / 1e3, 1)},
             "layer_tables_b2": {"avg_launch_us": round(tables2["avg_launch_us"], 3), "ms_per_pass": round(tables2["ms_per_pass"], 4)},
+            "cfg1_layer_linears": {"workload": "cfg1: one Seoul-shaped layer's linears q 2048x2048, k and v 512x2048, "
+                                                   "o 2048x2048, gate and up 8192x2048, down 2048x8192 in Q4_0 through the "
+                                                   "kernel-level GEMV (int8 cut per 32 columns), 16 copies in rotation",
+                                   "table_bytes": layer_bytes,
+                                   "b1_us": round(l_us1, 2), "b2_us": round(l_us2, 2),
+                                   "b2_GBs": round(layer_bytes / l_us2 / 1e3, 1),
+                                   "b2_frac": round(layer_bytes / l_us2 / 1e3 / HBM_PEAK_GBS, 4)},
             "cfg0_gemv_8192x2048": {"avg_us": round(cfg0_us, 3), "GBs": round(cfg0_bytes / cfg0_us / 1e3, 1),
                                     "frac": round(cfg0_bytes / cfg0_us / 1e3 / HBM_PEAK_GBS, 4),
                                     "kernel_us": round(cfg0_kernel_us, 3),
@@ -371,23 +495,45 @@ def main():
             "budget_ms": 80.0,
         }
     if not args.no_cpu:
-        aff = len(os.sched_getaffinity(0))
+        info = cpu_info()
+        aff = info["logical_cpus"]
         threads = args.cpu_threads or min(16, aff)
         cpu_steps = min(args.steps, 256)
         runs1, runs2 = args.cpu_runs, max(1, args.cpu_runs // 2)
         c1, cids, csecs = cpu_decode(path, threads, cpu_steps, b2=False, runs=runs1)
-        c2, _, csecs2 = cpu_decode(path, threads, cpu_steps, b2=True, runs=runs2)
-        same = bool(np.array_equal(cids[:len(ids_b1)], ids_b1[:len(cids)]))
+        c2, cids2, csecs2 = cpu_decode(path, threads, cpu_steps, b2=True, runs=runs2)
+        c4, _, csecs4 = cpu_decode(path, 4, cpu_steps, b2=False, runs=1)   # imi's own setting: 4 threads
+        n1, n2 = min(len(cids), len(ids_b1)), min(len(cids2[0]), len(ids_b2[0]))
+        same = bool(np.array_equal(cids[:n1], ids_b1[:n1]))
+        same2 = bool(np.array_equal(cids2[0][:n2], ids_b2[0][:n2]) and np.array_equal(cids2[1][:n2], ids_b2[1][:n2]))
         line["cpu_baseline"] = {
             "value": round(c1, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"cfg2 B=1: {runs1} conversations of a {PROMPT}-token seeded prompt then {cpu_steps} greedy ids "
                       f"({csecs:.1f} s generating); B=2: {runs2} step2 pairs of {cpu_steps} positions ({csecs2:.1f} s) = "
-                      f"{c2:.2f} tokens/s; {threads} threads of {aff} in the affinity mask; oracle/ C++ restatement of "
-                      "imi's AVX2 engine, x86-64-v3",
+                      f"{c2:.2f} tokens/s; 4 threads (imi's README setting): one conversation, {c4:.2f} tokens/s "
+                      f"({csecs4:.1f} s); {threads} threads of {aff} logical CPUs in the affinity mask "
+                      f"({info['physical_cores']} physical cores, SMT width {info['smt_width']}), {info['model']}; "
+                      "oracle/ C++ restatement of imi's AVX2 engine, x86-64-v3, imi's spinning thread team",
             "b2_value": round(c2, 2),
+            "four_thread_value": round(c4, 2),
+            "cpu": info,
         }
-        line["speedup_vs_cpu"] = {"b1": round(tok_s_b1 / c1, 1), "b2": round(tok_s_b2 / c2, 1)}
+        line["speedup_vs_cpu"] = {"b1": round(tok_s_b1 / c1, 1), "b2": round(tok_s_b2 / c2, 1),
+                                  "b1_vs_4_threads": round(tok_s_b1 / c4, 1)}
         line["greedy_ids_match_cpu"] = same
+        line["greedy_ids_match_cpu_b2"] = same2
+        # cfg 0 and cfg 1 on the CPU (imi's q4x8 figure of merit is table GB/s on one thread)
+        g1, gt = cpu_cfg0(1), cpu_cfg0(threads)
+        line["kernels"]["cfg0_gemv_8192x2048"]["cpu"] = {"GBs_1_thread": round(g1, 2), f"GBs_{threads}_threads": round(gt, 2),
+                                                         "kind": "port", "sample": "oracle q4x8 GEMV (imi/kernels/q4x8.cpp) "
+                                                         "8192 x 2048, fastest rep of about 2 s of reps on one table"}
+        cl1, cl2, cl_out = cpu_layer(threads)
+        line["kernels"]["cfg1_layer_linears"]["cpu"] = {
+            "b1_us": round(cl1, 1), "b2_us": round(cl2, 1), "cores": threads, "kind": "port",
+            "sample": "oracle group / group2 kernels (imi/core/tables.cpp), each table's fastest rep, about 2 s of reps per batch size"}
+        line["kernels"]["cfg1_layer_linears"]["speedup_vs_cpu"] = {"b1": round(cl1 / l_us1, 1), "b2": round(cl2 / l_us2, 1)}
+        line["kernels"]["cfg1_layer_linears"]["outputs_match_cpu"] = bool(all(
+            np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32)) for a, b in zip(l_out, cl_out)))
         if args.prefill_reps:
             csec, clg = cpu_prefill(path, threads)
             line["prefill"]["cpu"] = {"ms": round(csec * 1e3, 1), "cores": threads, "kind": "port",

@@ -17,6 +17,7 @@
  */
 #ifndef SEOUL_HIP_H
 #define SEOUL_HIP_H
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -37,6 +38,7 @@ typedef struct sh_ctx sh_ctx;       /* one model on one device */
 typedef struct sh_state sh_state;   /* one conversation's memory: K/V caches, conv memory, position */
 typedef struct sh_q4 sh_q4;         /* one Q4_0 table on the device (kernel-level API) */
 typedef struct sh_voice sh_voice;   /* the Q8_0 voice generator on the device */
+typedef struct sh_file sh_file;     /* one GGUF file read into host memory (imi_file) */
 
 typedef struct {
     int n_embd, n_vocab, n_head, n_head_kv, head_dim, n_ff, d_conv, n_ctx, n_layer, n_attn, n_swa;
@@ -47,6 +49,42 @@ typedef struct {
 
 /* Message of the last error on this thread ("" if none). */
 const char* sh_last_error(void);
+
+/* ---- GGUF file: imi_file::load / get / key_i / key_f / keep / drop_data (imi/model.h:12-36) ---- */
+/* The ggml_tensor fields imi's callers read. name points into the file object; data is the tensor's bytes in host
+ * memory: in the file's block, or in a copy of its own after sh_file_keep, or null once sh_file_drop_data let the
+ * block go and the tensor was not kept (its shape stays readable). */
+typedef struct {
+    const char* name;
+    int type;          /* ggml type id: 0 F32, 1 F16, 2 Q4_0, 3 Q4_1, 8 Q8_0, 14 Q6_K */
+    int n_dims;
+    int64_t ne[4];     /* ne[0] innermost; unused dimensions are 1 */
+    size_t nb[4];      /* ggml byte strides: nb[0] one element or block, nb[1] one row, ... */
+    void* data;
+} sh_tensor;
+
+/* imi_file::load (imi/model.cpp:48-106): header, keys and tensor table read, every tensor's bytes mapped. The
+ * repack argument of imi (a CPU kernel layout) has no counterpart: the engine makes the device layout itself. */
+int sh_file_load(const char* path, sh_file** out);
+int sh_file_free(sh_file* f);
+/* imi_file::get (model.cpp:108-115): SH_E_ARG when the file has no such tensor (imi stops when it is required) */
+int sh_file_get(const sh_file* f, const char* name, sh_tensor* out);
+/* imi_file::key_i (model.cpp:117-126): a u32, i32 or u64 key's value, else def */
+int64_t sh_file_key_i(const sh_file* f, const char* key, int64_t def);
+/* imi_file::key_f (model.cpp:128-131): an f32 key's value, else def */
+float sh_file_key_f(const sh_file* f, const char* key, float def);
+/* imi_file::keep (model.cpp:138-150): the tensor gets a 64-byte aligned copy of its bytes of its own */
+int sh_file_keep(sh_file* f, const char* name, sh_tensor* out);
+/* imi_file::drop_data (model.cpp:152-163): the file's block is let go; tensors not kept get data = null */
+int sh_file_drop_data(sh_file* f);
+/* the tensors in file order (imi walks them with ggml_get_first_tensor / ggml_get_next_tensor) */
+int sh_file_n_tensors(const sh_file* f);
+int sh_file_tensor(const sh_file* f, int i, sh_tensor* out);
+/* a key holding an array of integers or bools (imi reads these from the file's gguf context, e.g. the sliding-window
+ * pattern, imi/brain.cpp:32-36): its length (0 when absent or not an array); the first cap values go to out */
+int sh_file_key_arr(const sh_file* f, const char* key, int64_t* out, int cap);
+/* imi_file::data / size: every tensor's bytes as one block (null and 0 after drop_data) */
+int sh_file_block(const sh_file* f, const void** data, size_t* size);
 
 /* ---- engine: imi_seoul::load / reset / step / step2 / step_batch / new_state / swap_state ---- */
 int sh_create(int device, sh_ctx** out);
@@ -104,6 +142,13 @@ int sh_bench_tables(sh_ctx* ctx, int ncol, int reps, double* ms_per_pass, double
  * down, 2: word scores), launched reps times with real layer arguments rotating over the layers; avg_us = mean
  * kernel duration (events recorded around each kernel), bytes_per_launch = table + input + output bytes. */
 int sh_bench_kernel(sh_ctx* ctx, int kind, int n_in, int reps, double* avg_us, double* bytes_per_launch);
+
+/* The same kernels timed inside whole steps: two untimed, then `steps` timed steps (n_in conversations on fresh
+ * states, seeded token ids) enqueued without the graph, each launch of table kind `kind` (2: Q4_0 word table only)
+ * recording the events of its own dispatch; its input is what the step's previous kernel has just written, its
+ * table is read from HBM. avg_us = mean over the `launches` timed launches. */
+int sh_bench_step_kernel(sh_ctx* ctx, int kind, int n_in, int steps, double* avg_us, double* bytes_per_launch,
+                         int* launches);
 
 /* ---- kernel-level Q4_0 tables (imi/kernels/q4x8.h:14-18, imi/core/tables.h:103-138) ---- */
 /* q4_0: rows * cols/32 Q4_0 blocks (fp16 scale + 16 nibble bytes) as stored in GGUF; rows % 8 == 0. */

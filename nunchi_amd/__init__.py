@@ -21,10 +21,12 @@ SH_OK, SH_E_ARG, SH_E_HIP, SH_E_FILE, SH_E_SHAPE, SH_E_CONTEXT_FULL, SH_E_STATE,
 EXPORTS = [
     "sh_last_error", "sh_create", "sh_destroy", "sh_load", "sh_info", "sh_check_model", "sh_state_new", "sh_state_free", "sh_state_reset",
     "sh_state_pos", "sh_state_set_pos", "sh_step", "sh_step2", "sh_step_batch", "sh_generate", "sh_bench_tables",
-    "sh_bench_kernel",
+    "sh_bench_kernel", "sh_bench_step_kernel",
     "sh_q4_create", "sh_q4_free", "sh_q4_rows", "sh_q4_gemv", "sh_q4_gemm", "sh_q4_gemm_noalloc", "sh_q4_gemv_dev", "sh_q4_bench", "sh_q4_bench_kernel", "sh_expf", "sh_sync",
     "sh_voice_load", "sh_voice_free", "sh_voice_info", "sh_voice_begin_frame", "sh_voice_base", "sh_voice_pass",
     "sh_voice_feedback", "sh_voice_sample",
+    "sh_file_load", "sh_file_free", "sh_file_get", "sh_file_key_i", "sh_file_key_f", "sh_file_keep", "sh_file_drop_data",
+    "sh_file_n_tensors", "sh_file_tensor", "sh_file_key_arr", "sh_file_block",
 ]
 
 
@@ -46,6 +48,12 @@ class ModelInfo(C.Structure):
 class VoiceShape(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("n_embd", "n_vocab", "n_cb", "n_in", "n_head", "n_head_kv", "head_dim", "n_ff",
                                        "n_layer")] + [("table_bytes", C.c_longlong), ("feedback_bytes", C.c_longlong)]
+
+
+class Tensor(C.Structure):
+    """sh_tensor: the ggml tensor fields imi reads (type, n_dims, ne, nb, data, name)."""
+    _fields_ = [("name", C.c_char_p), ("type", C.c_int), ("n_dims", C.c_int), ("ne", C.c_int64 * 4),
+                ("nb", C.c_size_t * 4), ("data", C.c_void_p)]
 
 
 _lib = None
@@ -79,6 +87,7 @@ def load_library(path: str = LIB_PATH):
         "sh_generate": (i, [vp, vp, vp, C.c_int32, C.c_int32, i, vp, vp, P(d)]),
         "sh_bench_tables": (i, [vp, i, i, P(d), P(d), P(d), P(i)]),
         "sh_bench_kernel": (i, [vp, i, i, i, P(d), P(d)]),
+        "sh_bench_step_kernel": (i, [vp, i, i, i, P(d), P(d), P(i)]),
         "sh_q4_create": (i, [vp, vp, i, i, P(vp)]),
         "sh_q4_free": (i, [vp]),
         "sh_q4_rows": (i, [vp, vp, vp, i, vp]),
@@ -98,6 +107,17 @@ def load_library(path: str = LIB_PATH):
         "sh_voice_pass": (i, [vp, vp, vp, i, vp]),
         "sh_voice_feedback": (i, [vp, vp, vp]),
         "sh_voice_sample": (i, [vp, vp, i, vp, f, f, vp, vp]),
+        "sh_file_load": (i, [C.c_char_p, P(vp)]),
+        "sh_file_free": (i, [vp]),
+        "sh_file_get": (i, [vp, C.c_char_p, P(Tensor)]),
+        "sh_file_key_i": (C.c_int64, [vp, C.c_char_p, C.c_int64]),
+        "sh_file_key_f": (f, [vp, C.c_char_p, f]),
+        "sh_file_keep": (i, [vp, C.c_char_p, P(Tensor)]),
+        "sh_file_drop_data": (i, [vp]),
+        "sh_file_n_tensors": (i, [vp]),
+        "sh_file_tensor": (i, [vp, i, P(Tensor)]),
+        "sh_file_key_arr": (i, [vp, C.c_char_p, P(C.c_int64), i]),
+        "sh_file_block": (i, [vp, P(vp), P(C.c_size_t)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -124,6 +144,73 @@ def check_model(path: str, n_ctx: int = 1024) -> ModelInfo:
     info = ModelInfo()
     _check(L.sh_check_model(path.encode(), int(n_ctx), C.byref(info)))
     return info
+
+
+class File:
+    """A GGUF file read into host memory through the library (imi_file, imi/model.h:12-36): get / key_i / key_f /
+    keep / drop_data. No device is involved."""
+
+    def __init__(self, path: str):
+        L = load_library()
+        self.h = C.c_void_p()
+        _check(L.sh_file_load(path.encode(), C.byref(self.h)))
+
+    def close(self):
+        if getattr(self, "h", None) and self.h.value:
+            _lib.sh_file_free(self.h)
+            self.h = C.c_void_p()
+
+    def __del__(self):
+        self.close()
+
+    @staticmethod
+    def _desc(t: Tensor) -> dict:
+        return {"name": t.name.decode(), "type": t.type, "n_dims": t.n_dims, "ne": list(t.ne), "nb": list(t.nb),
+                "data": t.data}
+
+    def get(self, name: str) -> dict | None:
+        t = Tensor()
+        return self._desc(t) if _lib.sh_file_get(self.h, name.encode(), C.byref(t)) == SH_OK else None
+
+    def bytes_of(self, name: str) -> bytes | None:
+        """The tensor's bytes as the host holds them now (None once dropped and not kept)."""
+        d = self.get(name)
+        if d is None or not d["data"]:
+            return None
+        return C.string_at(d["data"], d["nb"][3] * d["ne"][3])
+
+    def key_i(self, key: str, default: int) -> int:
+        return int(_lib.sh_file_key_i(self.h, key.encode(), int(default)))
+
+    def key_f(self, key: str, default: float) -> float:
+        return float(_lib.sh_file_key_f(self.h, key.encode(), float(default)))
+
+    def key_arr(self, key: str) -> list:
+        n = _lib.sh_file_key_arr(self.h, key.encode(), None, 0)
+        out = (C.c_int64 * max(n, 1))()
+        _lib.sh_file_key_arr(self.h, key.encode(), out, n)
+        return list(out)[:n]
+
+    def keep(self, name: str) -> dict:
+        t = Tensor()
+        _check(_lib.sh_file_keep(self.h, name.encode(), C.byref(t)))
+        return self._desc(t)
+
+    def drop_data(self):
+        _check(_lib.sh_file_drop_data(self.h))
+
+    def block(self):
+        d, n = C.c_void_p(), C.c_size_t()
+        _check(_lib.sh_file_block(self.h, C.byref(d), C.byref(n)))
+        return d.value, n.value
+
+    def tensors(self) -> list:
+        out = []
+        for k in range(_lib.sh_file_n_tensors(self.h)):
+            t = Tensor()
+            _check(_lib.sh_file_tensor(self.h, k, C.byref(t)))
+            out.append(self._desc(t))
+        return out
 
 
 _live_contexts = weakref.WeakSet()
@@ -281,11 +368,21 @@ class Brain:
         _check(_lib.sh_bench_tables(self.ctx.h, int(ncol), int(reps), C.byref(ms), C.byref(us), C.byref(by), C.byref(nl)))
         return {"ms_per_pass": ms.value, "avg_launch_us": us.value, "bytes_per_pass": by.value, "launches": nl.value}
 
+    KERNELS = {"ffn_gate_up": 0, "ffn_down": 1, "word_scores": 2}
+
     def bench_kernel(self, kind: str, n_in: int = 1, reps: int = 64):
         """Mean duration (us) and bytes per launch of the step's GEMV for one table kind."""
         us, by = C.c_double(), C.c_double()
         _check(_lib.sh_bench_kernel(self.ctx.h, self.KERNELS[kind], int(n_in), int(reps), C.byref(us), C.byref(by)))
         return {"avg_us": us.value, "bytes_per_launch": by.value}
+
+    def bench_step_kernel(self, kind: str, n_in: int = 1, steps: int = 32):
+        """Mean duration (us) of one table kind's GEMV kernel inside whole steps (its inputs just written by the
+        step's previous kernel, its table read from HBM), bytes per launch and the number of launches timed."""
+        us, by, n = C.c_double(), C.c_double(), C.c_int()
+        _check(_lib.sh_bench_step_kernel(self.ctx.h, self.KERNELS[kind], int(n_in), int(steps), C.byref(us), C.byref(by),
+                                         C.byref(n)))
+        return {"avg_us": us.value, "bytes_per_launch": by.value, "launches": n.value}
 
 
 class Q4Table:

@@ -117,5 +117,9 @@ struct sh_ctx {
     float *pf_d = nullptr, *pf_s = nullptr, *pf_emb = nullptr;
     int32_t* pf_tok = nullptr;
     bool use_prefill = true;          // SEOUL_HIP_PREFILL=0: step_batch runs n single steps instead
+    // set while sh_bench_step_kernel runs steps without the graph: one kind of the step's GEMV launches (0 FFN
+    // gate|up, 1 FFN down, 2 Q4_0 word scores) records this event pair list around each kernel
+    std::vector<hipEvent_t>* probe_ev = nullptr;
+    int probe_kind = -1, probe_used = 0;
 };
 

@@ -127,6 +127,15 @@ void release_state_memory(sh_state* s) {
 
 namespace {
 
+// the event pair around this launch when sh_bench_step_kernel times this kind of launch (else none)
+void probe_events(sh_ctx* c, int kind, hipEvent_t* t0, hipEvent_t* t1) {
+    *t0 = *t1 = nullptr;
+    if (!c->probe_ev || c->probe_kind != kind || 2 * (size_t)(c->probe_used + 1) > c->probe_ev->size()) return;
+    *t0 = (*c->probe_ev)[2 * c->probe_used];
+    *t1 = (*c->probe_ev)[2 * c->probe_used + 1];
+    c->probe_used++;
+}
+
 int enqueue_step(sh_ctx* c, int M, bool want_logits) {
     const sh_model_info& I = c->info;
     const int E = I.n_embd;
@@ -221,7 +230,9 @@ int enqueue_step(sh_ctx* c, int M, bool want_logits) {
         f.units = units_of(L.gate_up, 2);
         f.out = c->act;
         f.out_ld = I.n_ff;
-        HIPCHK(launch_gemv(M, PRO_RESID_NORM, EPI_SWIGLU, grid_of(f.units), f, c->stream));
+        hipEvent_t p0, p1;
+        probe_events(c, 0, &p0, &p1);
+        HIPCHK(launch_gemv(M, PRO_RESID_NORM, EPI_SWIGLU, grid_of(f.units), f, c->stream, p0, p1));
         gemv_args d = base_args();
         d.W = L.down;
         d.units = units_of(L.down, 1);
@@ -229,7 +240,8 @@ int enqueue_step(sh_ctx* c, int M, bool want_logits) {
         d.src_ld = I.n_ff;
         d.out = c->fo;
         d.out_ld = E;
-        HIPCHK(launch_gemv(M, PRO_CUT, EPI_STORE, grid_of(d.units), d, c->stream));
+        probe_events(c, 1, &p0, &p1);
+        HIPCHK(launch_gemv(M, PRO_CUT, EPI_STORE, grid_of(d.units), d, c->stream, p0, p1));
         prev = &L;
     }
     final_args z{};
@@ -253,7 +265,11 @@ int enqueue_step(sh_ctx* c, int M, bool want_logits) {
         v.part_i = c->part_i;
         const int grid = c->vocab6.codes ? SH_Q6K_GRID : gemv_logits_grid(M, PRO_RESID_NORM, v, c->vocab_grid);
         if (c->vocab6.codes) HIPCHK(launch_scores_q6k(M, grid, v, c->stream));
-        else HIPCHK(launch_gemv(M, PRO_RESID_NORM, EPI_LOGITS, grid, v, c->stream));
+        else {
+            hipEvent_t p0, p1;
+            probe_events(c, 2, &p0, &p1);
+            HIPCHK(launch_gemv(M, PRO_RESID_NORM, EPI_LOGITS, grid, v, c->stream, p0, p1));
+        }
         z.part_v = c->part_v;
         z.part_i = c->part_i;
         z.n_part = grid;
@@ -1093,6 +1109,78 @@ int sh_bench_kernel(sh_ctx* c, int kind, int M, int reps, double* avg_us, double
 }
 
 // ---- kernel-level tables ----
+// One kind of the step's own GEMV launches timed inside whole steps (0 FFN gate|up, 1 FFN down, 2 Q4_0 word
+// scores): two untimed, then `steps` timed single (M = 1) or two-conversation steps run without the graph on fresh
+// states fed seeded token ids; each launch of that kind records the events of its own dispatch, and its input is
+// what the step's previous kernel has just written. Averages over every timed launch of that kind.
+int sh_bench_step_kernel(sh_ctx* c, int kind, int M, int steps, double* avg_us, double* bytes_per_launch, int* launches) {
+    if (!c || !c->loaded) return fail(SH_E_STATE, "sh_bench_step_kernel: no model loaded");
+    if (M < 1 || M > 2 || kind < 0 || kind > 2 || steps < 1 || steps + 2 > c->info.n_ctx)
+        return fail(SH_E_ARG, "sh_bench_step_kernel: kind in 0..2, M in {1, 2}, 1 <= steps <= n_ctx - 2");
+    if (kind == 2 && c->vocab6.codes) return fail(SH_E_ARG, "sh_bench_step_kernel: the word table is not Q4_0");
+    HIPCHK(hipSetDevice(c->device));
+    const sh_model_info& I = c->info;
+    const int per = kind == 2 ? 1 : (int)c->layers.size();
+    struct guard {
+        sh_ctx* c;
+        sh_state* st[2] = {nullptr, nullptr};
+        std::vector<hipEvent_t> ev;
+        ~guard() {
+            c->probe_ev = nullptr;
+            c->probe_kind = -1;
+            for (auto e : ev) (void)hipEventDestroy(e);
+            for (auto s : st)
+                if (s) (void)sh_state_free(s);
+        }
+    } g{c};
+    for (int m = 0; m < M; m++) {
+        const int rc = sh_state_new(c, &g.st[m]);
+        if (rc != SH_OK) return rc;
+    }
+    g.ev.reserve(2 * (size_t)per * steps);
+    for (size_t i = 0; i < 2 * (size_t)per * steps; i++) {
+        hipEvent_t e;
+        HIPCHK(hipEventCreate(&e));
+        g.ev.push_back(e);
+    }
+    for (int s = 0; s < steps + 2; s++) {
+        if (s == 2) {   // the first two steps warm the code and the tables' TLB entries
+            c->probe_ev = &g.ev;
+            c->probe_kind = kind;
+            c->probe_used = 0;
+        }
+        step_params& P = *c->P_host;
+        memset(&P, 0, sizeof P);
+        for (int m = 0; m < M; m++) {
+            P.token[m] = (int32_t)((7919LL * (s + 1) + 104729LL * m) % I.n_vocab);
+            fill_state(P, m, g.st[m]);
+        }
+        HIPCHK(hipMemcpyAsync(c->P_dev, &P, sizeof P, hipMemcpyHostToDevice, c->stream));
+        const int rc = enqueue_step(c, M, kind == 2);
+        if (rc != SH_OK) return rc;
+        HIPCHK(hipStreamSynchronize(c->stream));
+        for (int m = 0; m < M; m++) g.st[m]->pos++;
+    }
+    const int n = c->probe_used;
+    double ms = 0;
+    for (int i = 0; i < n; i++) {
+        float x;
+        HIPCHK(hipEventElapsedTime(&x, g.ev[2 * i], g.ev[2 * i + 1]));
+        ms += x;
+    }
+    double bytes = 0;
+    for (const layer_dev& L : c->layers) {
+        if (kind == 0) bytes += (double)L.gate_up.rows * L.gate_up.nb * 18 + 4.0 * M * (2 * I.n_embd + I.n_ff);
+        else if (kind == 1) bytes += (double)L.down.rows * L.down.nb * 18 + 4.0 * M * (I.n_ff + I.n_embd);
+    }
+    if (kind == 2) bytes = (double)c->vocab.rows * c->vocab.nb * 18 + 4.0 * M * (2 * I.n_embd + I.n_vocab);
+    else bytes /= (double)c->layers.size();
+    if (avg_us) *avg_us = n ? ms * 1e3 / n : 0.0;
+    if (bytes_per_launch) *bytes_per_launch = bytes;
+    if (launches) *launches = n;
+    return SH_OK;
+}
+
 int sh_q4_create(sh_ctx* c, const void* q4_0, int rows, int cols, sh_q4** out) {
     if (!c || !q4_0 || !out || rows <= 0 || rows % 8 || cols <= 0 || cols % 32) return fail(SH_E_ARG, "sh_q4_create: rows % 8 == 0, cols % 32 == 0");
     if (cols / 32 > 4 * 64) return fail(SH_E_SHAPE, "sh_q4_create: at most 8192 columns");
