@@ -31,14 +31,16 @@ struct cursor {
         return s;
     }
 };
-bool row_size(int type, int64_t ne0, size_t* out) {
+// bytes of one element (F32, F16) or one block (quantized types) and the values a block holds (ggml's type size
+// and block size)
+bool type_block(int type, size_t* bytes, int64_t* values) {
     switch (type) {
-        case GT_F32: *out = 4 * (size_t)ne0; return true;
-        case GT_F16: *out = 2 * (size_t)ne0; return true;
-        case GT_Q4_0: if (ne0 % 32) return false; *out = (size_t)ne0 / 32 * 18; return true;
-        case GT_Q4_1: if (ne0 % 32) return false; *out = (size_t)ne0 / 32 * 20; return true;
-        case GT_Q8_0: if (ne0 % 32) return false; *out = (size_t)ne0 / 32 * 34; return true;
-        case GT_Q6_K: if (ne0 % 256) return false; *out = (size_t)ne0 / 256 * 210; return true;
+        case GT_F32: *bytes = 4; *values = 1; return true;
+        case GT_F16: *bytes = 2; *values = 1; return true;
+        case GT_Q4_0: *bytes = 18; *values = 32; return true;
+        case GT_Q4_1: *bytes = 20; *values = 32; return true;
+        case GT_Q8_0: *bytes = 34; *values = 32; return true;
+        case GT_Q6_K: *bytes = 210; *values = 256; return true;
         default: return false;
     }
 }
@@ -99,9 +101,12 @@ bool gg_file::load(const std::string& path) {
         for (int d = 0; d < t.n_dims; d++) t.ne[d] = (int64_t)c.num<uint64_t>();
         t.type = (int)c.num<uint32_t>();
         t.offset = c.num<uint64_t>();
-        size_t row = 0;
-        if (!row_size(t.type, t.ne[0], &row)) { error = "tensor " + t.name + " has a type this engine does not read"; return false; }
-        t.nb[0] = 0;
+        size_t blk = 0;
+        int64_t per = 1;
+        if (!type_block(t.type, &blk, &per)) { error = "tensor " + t.name + " has a type this engine does not read"; return false; }
+        if (t.ne[0] % per) { error = "tensor " + t.name + " has rows that are not whole blocks"; return false; }
+        const size_t row = (size_t)(t.ne[0] / per) * blk;
+        t.nb[0] = blk;
         t.nb[1] = row;
         t.nb[2] = row * (size_t)t.ne[1];
         t.nb[3] = t.nb[2] * (size_t)t.ne[2];
@@ -110,6 +115,8 @@ bool gg_file::load(const std::string& path) {
     }
     if (!c.ok) { error = path + ": malformed GGUF header"; return false; }
     const size_t data0 = (c.at + alignment - 1) / alignment * alignment;
+    block = static_cast<const uint8_t*>(map) + data0;
+    block_size = map_size > data0 ? map_size - data0 : 0;
     for (auto& t : tensors) {
         if (data0 + t.offset + t.nbytes > map_size) { error = "short read on " + t.name; return false; }
         t.data = static_cast<const uint8_t*>(map) + data0 + t.offset;
@@ -130,6 +137,10 @@ int64_t gg_file::key_i(const std::string& name, int64_t def) const {
 float gg_file::key_f(const std::string& name, float def) const {
     for (const auto& k : kvs) if (k.key == name && k.type != 9 && k.type != 8) return (float)k.f;
     return def;
+}
+int gg_file::key_type(const std::string& name) const {
+    for (const auto& k : kvs) if (k.key == name) return k.type;
+    return -1;
 }
 std::vector<int64_t> gg_file::key_arr(const std::string& name) const {
     for (const auto& k : kvs) if (k.key == name && k.type == 9) return k.arr;
@@ -158,6 +169,8 @@ void gg_file::drop_data() {
     munmap(map, map_size);
     map = nullptr;
     map_size = 0;
+    block = nullptr;
+    block_size = 0;
 }
 gg_file::~gg_file() {
     if (map) munmap(map, map_size);

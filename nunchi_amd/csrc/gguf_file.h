@@ -16,7 +16,7 @@ struct gg_tensor {
     int type = 0;
     int n_dims = 0;
     int64_t ne[4] = {1, 1, 1, 1};   // ne[0] innermost
-    size_t nb[4] = {0, 0, 0, 0};    // byte strides (nb[1] = one row)
+    size_t nb[4] = {0, 0, 0, 0};    // ggml's byte strides: nb[0] = one element or block, nb[1] = one row
     size_t offset = 0, nbytes = 0;
     const void* data = nullptr;     // null once the file's block is dropped and the tensor was not kept
 };
@@ -28,9 +28,12 @@ struct gg_file {
     int64_t key_i(const std::string& name, int64_t def) const;
     float key_f(const std::string& name, float def) const;
     std::vector<int64_t> key_arr(const std::string& name) const;
+    int key_type(const std::string& name) const;                         // GGUF value type, -1 if absent
     const gg_tensor* keep(const std::string& name, bool required = true); // own copy of the bytes (model.cpp:138-150)
     void drop_data();                                                     // let the file's block go (model.cpp:152-163)
     std::string error;
+    const void* block = nullptr;   // every tensor's bytes (the mapped file from the data offset on), until drop_data
+    size_t block_size = 0;
     ~gg_file();
 
 private:

@@ -13,7 +13,7 @@ from conftest import ROOT
 
 def _declared():
     src = open(os.path.join(ROOT, "include", "seoul_hip.h")).read()
-    return sorted(set(re.findall(r"^(?:int|const char\*)\s+(sh_\w+)\(", src, re.M)))
+    return sorted(set(re.findall(r"^(?:int|int64_t|float|const char\*)\s+(sh_\w+)\(", src, re.M)))
 
 
 def test_library_exports_every_declared_symbol():
