@@ -23,6 +23,12 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 GATE_UP_TRAFFIC_BYTES = 19275131   # counters: 149,528 128-B + 1,478 64-B read requests + 40 KiB WRITE_SIZE per launch
+# matrix-core utilisation of the prefill's table products, rocprofv3's MfmaUtil per dispatch (MFMA busy cycles over
+# GUI-active cycles x SIMDs) from `rocprofv3 --pmc MfmaUtil --kernel-include-regex k_pf_ -- python3 bench.py
+# --prefill-only --prefill-reps 2`: a counter run, not measurable from inside this process
+PREFILL_MFMA_UTIL_PCT = {"ffn_gate_up k_pf_gemm_lds<1,false,4,32>": 29.4, "in_proj k_pf_gemm_lds<0,false,4,32>": 19.7,
+                         "2048-row tables k_pf_gemm_lds<0,false,4,16>": 19.3,
+                         "q|k|v|gate k_pf_gemm_lds<0,false,4,16>": 19.5}
 N_CTX = 512
 PROMPT = 32
 
@@ -308,6 +314,9 @@ def main():
     ap.add_argument("--decode-only", action="store_true",
                     help="only the decode runs and the in-step kernel timing (the launches a kernel trace of the step "
                          "should average), no CPU legs")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the hearing-window prefills (--prefill-reps timed after one untimed): the launches a "
+                         "kernel trace or counter run of the prefill reads")
     ap.add_argument("--counters-workload", action="store_true",
                     help="only the launches the hardware-counter runs read: a streaming kernel of known size (the "
                          "exponential over 16 Mi floats: 64 MiB read, 64 MiB written), 64 read-only GEMVs of known "
@@ -342,6 +351,13 @@ def main():
                                                 "ffn_gate_up_avg_us": round(gu["avg_us"], 3),
                                                 "ffn_gate_up_bytes_per_launch": int(gu["bytes_per_launch"]),
                                                 "prefill_ms": round(float(pt.min()) * 1e3, 3)}}))
+        return
+
+    if args.prefill_only:
+        pt, _, pbest = gpu_prefill(brain, max(1, args.prefill_reps))
+        print(json.dumps({"prefill_only": {"reps": int(len(pt)), "best_ms": round(float(pt.min()) * 1e3, 3),
+                                           "p50_ms": round(float(np.percentile(pt, 50)) * 1e3, 3), "best_id": int(pbest)}}),
+              flush=True)
         return
 
     tok_s_b1, ids_b1, dev_b1, wall_b1 = gpu_decode(brain, args.steps, args.warmup, b2=False)
@@ -474,6 +490,7 @@ def main():
             "positions_per_s": round(n_pf / float(np.percentile(pt, 50)), 1),
             "int8_tops": round(ops / float(np.percentile(pt, 50)) / 1e12, 2),
             "int8_peak_tops": 5000.0,
+            "mfma_util_pct_counter_run": PREFILL_MFMA_UTIL_PCT,
             "reps": int(len(pt)),
         }
     if args.voice_frames:

@@ -224,18 +224,32 @@ __global__ __launch_bounds__(256) void k_pf_gemm(pf_gemm_args a) {
 // LDS-staged form of the same product (taken when nb is a multiple of KC): per workgroup the operands of KC blocks
 // (64 rows of codes, their scales and, for Q4_1, minima; 64 positions of input codes and their (d, s)) are fetched
 // with wide coalesced loads into registers while the waves run the previous KC blocks from LDS, then stored to the
-// other half of a double buffer. The per-(row, position) arithmetic and its order are k_pf_gemm's.
-template <int EPI, bool HM, int KC>
+// other half of a double buffer, the codes already split into their low and high nibbles. The per-(row, position)
+// operations and their order are k_pf_gemm's; two of the three fp32 operations per (row, position, block) run on
+// the matrix cores as K = 1 outer products, v_mfma_f32_16x16x1_4b_f32, whose four 16 x 16 blocks are the wave's
+// (row tile, position tile) pairs: dd = d x dx (accumulator 0) and cor = fma(d, s, cor) (the running cor as the
+// accumulator, one product per block in block order). That operation rounds once, like fmaf: it equals the VALU's
+// fmaf bit for bit, denormals and the fused cancellation included (measured on 4.2 M cases); d x dx + 0 differs from
+// the product only in the sign of a zero, which the acc chain (started at +0) cannot see. Only acc =
+// fma(float(isum), dd, acc) stays on the VALU. A workgroup is 4 waves over 64 rows x 2 PW positions, a wave 32 rows x
+// PW positions: PW = 32 for tables with enough rows, 16 for the narrow ones (2048 rows: two waves per SIMD instead of
+// one), whose matrix-core blocks for the missing position tile are computed on a repeated position and dropped.
+template <int EPI, bool HM, int KC, int PW>
 __global__ __launch_bounds__(256, KC == 4 ? 3 : 2) void k_pf_gemm_lds(pf_gemm_args a) {
-    __shared__ u32x4 sA[2][64][KC + 1];     // row r's 16 code bytes of block j (row stride padded: no bank conflicts)
-    __shared__ u32x4 sB[2][KC][64][2];      // position p's 32 input codes of block j, 16-byte halves swapped when p & 8
+    typedef float v16f __attribute__((ext_vector_type(16)));
+    constexpr int P = 2 * PW, NTW = PW / 16;          // positions per workgroup; 16-position tiles per wave
+    constexpr int SA = 8 * KC + 2;                    // dwords per row: 32 nibble bytes per block + 2 (bank spread)
+    __shared__ __align__(16) unsigned sA[2][64 * SA]; // row r, block j: low nibbles of its 16 code bytes, then high
+    __shared__ u32x4 sB[2][KC][P][2];       // position p's 32 input codes of block j, 16-byte halves swapped when p & 8
     __shared__ __align__(16) uint16_t sD[2][KC][64];
     __shared__ __align__(16) uint16_t sM[2][KC][HM ? 64 : 8];
-    __shared__ float2 sX[2][KC][64];        // (d, s) of position p's block j
+    __shared__ float2 sX[2][KC][P];         // (d, s) of position p's block j
     const int t = threadIdx.x, lane = t & 63, w = t >> 6, li = lane & 15, lq = lane >> 4;
     const int rows = a.W.rows, n = a.n, nb = a.W.nb, nch = nb / KC, ng = rows / 8;
-    const int r0 = blockIdx.x * 64, p0 = blockIdx.y * 64, rl = (w & 1) * 32, pl = (w >> 1) * 32;
-    constexpr int NA = 64 * KC / 256, NBQ = 64 * KC * 2 / 256, NX = 64 * KC / 256;   // staging words per thread
+    const int r0 = blockIdx.x * 64, p0 = blockIdx.y * P, rl = (w & 1) * 32, pl = (w >> 1) * PW;
+    // staging words per thread (the (d, s) pairs of a narrow tile need only the first P * KC threads)
+    constexpr int NA = 64 * KC / 256, NBQ = P * KC * 2 / 256, NX = (P * KC + 255) / 256;
+    static_assert(NA >= 1 && NBQ >= 1 && 64 * KC % 256 == 0 && P * KC * 2 % 256 == 0, "KC too small for the staging");
     // this thread's staging sources, chunk 0 (rows and positions past the table / batch are clamped: their results
     // are dropped); chunk c adds c * KC blocks
     const u32x4* pa[NA];
@@ -248,13 +262,13 @@ __global__ __launch_bounds__(256, KC == 4 ? 3 : 2) void k_pf_gemm_lds(pf_gemm_ar
     }
 #pragma unroll
     for (int q = 0; q < NBQ; q++) {
-        const int idx = t + 256 * q, rem = idx % 128;
-        pb[q] = (const u32x4*)a.in.q + ((size_t)(idx / 128) * n + min(p0 + (rem >> 1), n - 1)) * 2 + (rem & 1);
+        const int idx = t + 256 * q, rem = idx % (2 * P);
+        pb[q] = (const u32x4*)a.in.q + ((size_t)(idx / (2 * P)) * n + min(p0 + (rem >> 1), n - 1)) * 2 + (rem & 1);
     }
 #pragma unroll
     for (int q = 0; q < NX; q++) {
-        const int idx = t + 256 * q;
-        px[q] = a.in.d + (size_t)(idx / 64) * n + min(p0 + idx % 64, n - 1);
+        const int idx = min(t + 256 * q, P * KC - 1);
+        px[q] = a.in.d + (size_t)(idx / P) * n + min(p0 + idx % P, n - 1);
     }
     const size_t pdo = (size_t)min(r0 / 8 + t / KC, ng - 1) * nb + t % KC, sdo = a.in.s - a.in.d;
     u32x4 ga[NA], gb[NBQ], gd = u32x4{0, 0, 0, 0}, gm = u32x4{0, 0, 0, 0};
@@ -273,18 +287,23 @@ __global__ __launch_bounds__(256, KC == 4 ? 3 : 2) void k_pf_gemm_lds(pf_gemm_ar
         for (int q = 0; q < NX; q++) {
             gxd[q] = px[q][(size_t)j0 * n];
             gxs[q] = px[q][(size_t)j0 * n + sdo];
-        }
+        }   // (threads past P * KC re-read the last pair; they store nothing)
     };
     auto stash = [&](int buf) {
 #pragma unroll
-        for (int q = 0; q < NA; q++) {
+        for (int q = 0; q < NA; q++) {   // byte k of the record: low nibble of code byte k (k < 16), high of k - 16
             const int idx = t + 256 * q;
-            sA[buf][idx / KC][idx % KC] = ga[q];
+            uint2* dst = (uint2*)&sA[buf][(idx / KC) * SA + 8 * (idx % KC)];
+            const u32x4 v = ga[q];
+            dst[0] = uint2{v.x & 0x0F0F0F0Fu, v.y & 0x0F0F0F0Fu};
+            dst[1] = uint2{v.z & 0x0F0F0F0Fu, v.w & 0x0F0F0F0Fu};
+            dst[2] = uint2{(v.x >> 4) & 0x0F0F0F0Fu, (v.y >> 4) & 0x0F0F0F0Fu};
+            dst[3] = uint2{(v.z >> 4) & 0x0F0F0F0Fu, (v.w >> 4) & 0x0F0F0F0Fu};
         }
 #pragma unroll
         for (int q = 0; q < NBQ; q++) {
-            const int idx = t + 256 * q, rem = idx % 128;
-            sB[buf][idx / 128][rem >> 1][(rem & 1) ^ ((rem >> 4) & 1)] = gb[q];
+            const int idx = t + 256 * q, rem = idx % (2 * P);
+            sB[buf][idx / (2 * P)][rem >> 1][(rem & 1) ^ ((rem >> 4) & 1)] = gb[q];
         }
         if (t < 8 * KC) {
             const int g = t / KC, jb = t % KC;
@@ -294,18 +313,20 @@ __global__ __launch_bounds__(256, KC == 4 ? 3 : 2) void k_pf_gemm_lds(pf_gemm_ar
 #pragma unroll
         for (int q = 0; q < NX; q++) {
             const int idx = t + 256 * q;
-            sX[buf][idx / 64][idx % 64] = float2{gxd[q], gxs[q]};
+            if (idx < P * KC) sX[buf][idx / P][idx % P] = float2{gxd[q], gxs[q]};
         }
     };
 
-    float acc[2][2][4], cor[2][2][4];
+    // lane l's accumulators: register k = 4 b + i of block b = 2 mt + nt holds row 4 (l / 16) + i of row tile mt
+    // at position l % 16 of position tile nt (the layout of both matrix-core results)
+    float acc[16];
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-        for (int nt = 0; nt < 2; nt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) { acc[mt][nt][i] = 0.0f; cor[mt][nt][i] = 0.0f; }
-    const int shift = (lq >> 1) * 4;   // columns 0-15: low nibbles, 16-31: high nibbles
+    for (int k = 0; k < 16; k++) acc[k] = 0.0f;
+    v16f cor = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    const v16f zero = cor;
+    // this lane's outer-product operands: row 16 mt + (l % 16) of the wave's rows for block b = l / 16 (mt = b / 2),
+    // position 16 nt + (l % 16) of its positions (nt = b % 2; with one position tile, nt = 0 again)
+    const int orow = rl + 16 * (lane >> 5) + li, opos = pl + 16 * (NTW == 2 ? (lane >> 4) & 1 : 0) + li;
     fetch(0);
     stash(0);
     __syncthreads();
@@ -314,39 +335,32 @@ __global__ __launch_bounds__(256, KC == 4 ? 3 : 2) void k_pf_gemm_lds(pf_gemm_ar
         if (c + 1 < nch) fetch(c + 1);
 #pragma unroll 2
         for (int jb = 0; jb < KC; jb++) {
-            i32x4 isum[2][2];
-            long cb[2];
+            i32x4 isum[2][NTW];
+            long cb[NTW];
 #pragma unroll
-            for (int nt = 0; nt < 2; nt++)   // (li & 8: the halves were swapped, which spreads the reads over the banks)
+            for (int nt = 0; nt < NTW; nt++)   // (li & 8: the halves were swapped, which spreads the reads over the banks)
                 cb[nt] = ((const long*)&sB[buf][jb][pl + 16 * nt + li][0])[lq ^ ((li >> 3) << 1)];
 #pragma unroll
-            for (int mt = 0; mt < 2; mt++) {
-                const uint2 ca = ((const uint2*)&sA[buf][rl + 16 * mt + li][jb])[lq & 1];
-                const unsigned lo = (ca.x >> shift) & 0x0F0F0F0Fu, hi = (ca.y >> shift) & 0x0F0F0F0Fu;
-                const long av = (long)((unsigned long)lo | ((unsigned long)hi << 32));
+            for (int mt = 0; mt < 2; mt++) {   // columns 8 (lq & 1) .. + 7, low nibbles for lq < 2, else high
+                const long av = *(const long*)&sA[buf][(rl + 16 * mt + li) * SA + 8 * jb + 2 * lq];
 #pragma unroll
-                for (int nt = 0; nt < 2; nt++)
+                for (int nt = 0; nt < NTW; nt++)
                     isum[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, cb[nt], i32x4{0, 0, 0, 0}, 0, 0, 0);
             }
-            float2 xz[2];
+            const float dl = h2f(sD[buf][jb][orow]);
+            const float ml = HM ? h2f(sM[buf][jb][HM ? orow : 0]) : dl;
+            const float2 xl = sX[buf][jb][opos];
+            const v16f dd = __builtin_amdgcn_mfma_f32_16x16x1f32(dl, xl.x, zero, 0, 0, 0);
+            cor = __builtin_amdgcn_mfma_f32_16x16x1f32(ml, xl.y, cor, 0, 0, 0);
 #pragma unroll
-            for (int nt = 0; nt < 2; nt++) xz[nt] = sX[buf][jb][pl + 16 * nt + li];
+            for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-            for (int mt = 0; mt < 2; mt++) {
-                const uint2 cs = *(const uint2*)&sD[buf][jb][rl + 16 * mt + 4 * lq];
-                const uint2 cm = HM ? *(const uint2*)&sM[buf][jb][HM ? rl + 16 * mt + 4 * lq : 0] : cs;
-                const float dd[4] = {h2f((uint16_t)(cs.x & 0xFFFFu)), h2f((uint16_t)(cs.x >> 16)),
-                                     h2f((uint16_t)(cs.y & 0xFFFFu)), h2f((uint16_t)(cs.y >> 16))};
-                const float mm[4] = {h2f((uint16_t)(cm.x & 0xFFFFu)), h2f((uint16_t)(cm.x >> 16)),
-                                     h2f((uint16_t)(cm.y & 0xFFFFu)), h2f((uint16_t)(cm.y >> 16))};
-#pragma unroll
-                for (int nt = 0; nt < 2; nt++)
+                for (int nt = 0; nt < NTW; nt++)
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
-                        acc[mt][nt][i] = fmaf((float)isum[mt][nt][i], dd[i] * xz[nt].x, acc[mt][nt][i]);
-                        cor[mt][nt][i] = fmaf(mm[i], xz[nt].y, cor[mt][nt][i]);
+                        const int k = 4 * (2 * mt + nt) + i;
+                        acc[k] = fmaf((float)isum[mt][nt][i], dd[k], acc[k]);
                     }
-            }
         }
         if (c + 1 < nch) stash(buf ^ 1);
         __syncthreads();
@@ -355,11 +369,14 @@ __global__ __launch_bounds__(256, KC == 4 ? 3 : 2) void k_pf_gemm_lds(pf_gemm_ar
 #pragma unroll
     for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-        for (int nt = 0; nt < 2; nt++) {
+        for (int nt = 0; nt < NTW; nt++) {
             const int p = pbase + 16 * nt + li, rr0 = rbase + 16 * mt + 4 * lq;
             float v[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) v[i] = HM ? acc[mt][nt][i] + cor[mt][nt][i] : fmaf(-8.0f, cor[mt][nt][i], acc[mt][nt][i]);
+            for (int i = 0; i < 4; i++) {
+                const int k = 4 * (2 * mt + nt) + i;
+                v[i] = HM ? acc[k] + cor[k] : fmaf(-8.0f, cor[k], acc[k]);
+            }
             if (EPI == EPI_SWIGLU) {
                 // rows 0-7 of the 16-row tile are a gate group, rows 8-15 the matching up group (lanes + 32)
                 float up[4];
@@ -605,7 +622,7 @@ hipError_t launch_pf_rows(int mode, const pf_rows_args& a, hipStream_t s) {
 }
 
 #ifndef PF_KC
-#define PF_KC 8   // blocks staged per step of the LDS-staged product
+#define PF_KC 4   // blocks staged per step of the LDS-staged product
 #endif
 // SEOUL_HIP_PF_PLAIN=1 keeps the products on the unstaged kernel (a comparison switch)
 static bool getenv_pf_plain() {
@@ -618,11 +635,18 @@ hipError_t launch_pf_gemm(int epi, const pf_gemm_args& a, hipStream_t s) {
     const dim3 grid((a.W.rows + 63) / 64, (a.n + 63) / 64);
     const bool hm = a.W.mins != nullptr;   // Q4_1 table
     if (a.W.nb % PF_KC == 0 && !getenv_pf_plain()) {
-        if (epi == EPI_SWIGLU && hm) hipLaunchKernelGGL((k_pf_gemm_lds<EPI_SWIGLU, true, PF_KC>), grid, dim3(256), 0, s, a);
-        else if (epi == EPI_SWIGLU) hipLaunchKernelGGL((k_pf_gemm_lds<EPI_SWIGLU, false, PF_KC>), grid, dim3(256), 0, s, a);
-        else if (epi == EPI_STORE && hm) hipLaunchKernelGGL((k_pf_gemm_lds<EPI_STORE, true, PF_KC>), grid, dim3(256), 0, s, a);
-        else if (epi == EPI_STORE) hipLaunchKernelGGL((k_pf_gemm_lds<EPI_STORE, false, PF_KC>), grid, dim3(256), 0, s, a);
+        // 16 positions per wave when 32 would leave fewer than two waves per SIMD
+        const bool narrow = (size_t)grid.x * grid.y * 4 < 2048;
+        const dim3 g16(grid.x, (a.n + 31) / 32);
+#define SH_PF_LDS(EPI_, HM_)                                                                                      \
+    if (narrow) hipLaunchKernelGGL((k_pf_gemm_lds<EPI_, HM_, PF_KC, 16>), g16, dim3(256), 0, s, a);            \
+    else hipLaunchKernelGGL((k_pf_gemm_lds<EPI_, HM_, PF_KC, 32>), grid, dim3(256), 0, s, a);
+        if (epi == EPI_SWIGLU && hm) { SH_PF_LDS(EPI_SWIGLU, true) }
+        else if (epi == EPI_SWIGLU) { SH_PF_LDS(EPI_SWIGLU, false) }
+        else if (epi == EPI_STORE && hm) { SH_PF_LDS(EPI_STORE, true) }
+        else if (epi == EPI_STORE) { SH_PF_LDS(EPI_STORE, false) }
         else return hipErrorInvalidValue;
+#undef SH_PF_LDS
         return hipGetLastError();
     }
     if (epi == EPI_SWIGLU && hm)
