@@ -98,15 +98,18 @@ SCHEDULE = (4, 4)     # masked passes of a frame: codebooks scored (and fixed) b
 TEMP, REP, REP_WIN = 0.4, 1.2, 64   # imi's sampling settings (imi/core/talk.cpp:131-133)
 
 
-def play_frames(step2, voice, tok_a, fb, frames, pick):
+def play_frames(step2, voice, tok_a, fb, frames, pick, codec=None):
     """Voice frames as imi's talk loop runs them (imi/core/talk.cpp:127-187) with slot A riding along
     (imi/core/flow.cpp:118): step2 (A: text step with scores, B: the voice brain step fed the last feedback row sum),
     begin_frame from B's hidden state, the masked passes over a shuffled codebook order (each samples its
     codebooks' codes with temperature 0.4 and repeat penalty 1.2 over the last 64 frames: `pick` runs the pass
-    and the sampling), then the feedback row sum. The shuffles and uniform draws come from one seeded generator (numpy's, in place of imi's mt19937), so
-    two runs with the same scores pick the same codes; an end-of-audio pick does not end the run. Returns
-    per-frame seconds, the step2 and generator shares, the codes of every frame and slot A's ids."""
-    tot, br, vo, codes_all, ids = [], [], [], [], []
+    and the sampling), then the codec turns the codes into the frame's samples (imi/core/talk.cpp:178-180) and the
+    feedback row sum is formed. The shuffles and uniform draws come from one seeded generator (numpy's, in place of
+    imi's mt19937), so two runs with the same scores pick the same codes; an end-of-audio pick does not end the run,
+    and codes past the codec's level table (the end-of-audio and other special codes, which end a real run) are
+    wrapped into it so every frame is decoded. Returns per-frame seconds, the step2 and generator shares, the codes of
+    every frame, slot A's ids, and the codec's shares and samples."""
+    tot, br, vo, codes_all, ids, cd, pcm = [], [], [], [], [], [], []
     rng = np.random.default_rng(7)
     for _ in range(frames):
         order = rng.permutation(voice.n_cb).astype(np.int32)
@@ -122,20 +125,32 @@ def play_frames(step2, voice, tok_a, fb, frames, pick):
             need = order[k:k + n]
             codes[need] = pick(voice, codes, need, window, u[k:k + n])
             k += n
-        fb = voice.feedback(codes)
         t2 = time.perf_counter()
-        tot.append(t2 - t0)
+        if codec is not None:
+            pcm.append(codec.frame(codes % codec_levels(codec)))
+        t3 = time.perf_counter()
+        fb = voice.feedback(codes)
+        t4 = time.perf_counter()
+        tot.append(t4 - t0)
         br.append(t1 - t0)
-        vo.append(t2 - t1)
+        vo.append((t2 - t1) + (t4 - t3))
+        cd.append(t3 - t2)
         codes_all.append(codes)
         ids.append(tok_a)
-    return np.array(tot), np.array(br), np.array(vo), np.array(codes_all), ids, tok_a, fb
+    return (np.array(tot), np.array(br), np.array(vo), np.array(codes_all), ids, tok_a, fb, np.array(cd),
+            np.concatenate(pcm) if pcm else np.zeros(0, np.float32))
 
 
-def gpu_voice_frames(brain_path, voice_path, frames, warmup):
+def codec_levels(codec) -> int:
+    """Rows of the codec's FSQ level table (the codes it takes)."""
+    return codec.info.n_codes if hasattr(codec, "info") else codec.n_codes
+
+
+def gpu_voice_frames(brain_path, voice_path, codec_path, frames, warmup):
     import nunchi_amd
     brain = nunchi_amd.Brain(brain_path, n_ctx=VOICE_CTX)
     voice = nunchi_amd.Voice(voice_path)
+    codec = nunchi_amd.Codec(codec_path)
     sa, sb = brain.new_state(), brain.new_state()
     pa = _prompt(2, brain.n_vocab)
     for i in range(PROMPT):
@@ -149,19 +164,21 @@ def gpu_voice_frames(brain_path, voice_path, frames, warmup):
     fb = voice.feedback(np.zeros(voice.n_cb, np.int32))
     ref = play_frames(step2, voice, int(ids[-1]), fb, frames + warmup,
                       lambda v, codes, need, win, u: (v.pass_(codes, need, scores=False),
-                                                      v.sample(win, u, TEMP, REP)[0])[1])
+                                                      v.sample(win, u, TEMP, REP)[0])[1], codec)
     # the timed frames are the frames after the warmup ones, in the same run (states keep advancing)
-    out = tuple(x[warmup:] for x in ref[:4]) + (ref[4][warmup:],)
-    info = {"table_bytes": voice.table_bytes, "n_cb": voice.n_cb}
+    out = tuple(x[warmup:] for x in ref[:4]) + (ref[4][warmup:], ref[7][warmup:])
+    info = {"table_bytes": voice.table_bytes, "n_cb": voice.n_cb, "codec_table_bytes": int(codec.info.table_bytes)}
+    codec.close()
     voice.close()
     brain.ctx.close()
     return out, ref, info
 
 
-def cpu_voice_frames(brain_path, voice_path, threads, frames):
+def cpu_voice_frames(brain_path, voice_path, codec_path, threads, frames):
     import oracle
     eng = oracle.Engine(brain_path, threads=threads, n_ctx=VOICE_CTX)
     voice = oracle.Voice(voice_path, threads=threads)
+    codec = oracle.Codec(codec_path)
     pa = _prompt(2, eng.n_vocab)
     for i in range(PROMPT):
         _, lg = eng.step(int(pa[i]), want_logits=i == PROMPT - 1)
@@ -175,7 +192,7 @@ def cpu_voice_frames(brain_path, voice_path, threads, frames):
     fb = voice.feedback(np.zeros(voice.n_cb, np.int32))
     return play_frames(step2, voice, int(ids[-1]), fb, frames,
                        lambda v, codes, need, win, u: oracle.voice_sample(v.pass_(codes, need), need, win, u, TEMP,
-                                                                          REP)[0])
+                                                                          REP)[0], codec)
 
 
 HEAR_EMB, HEAR_TOK = 384, 64   # the hearing window: audio-encoder rows, then words
@@ -495,13 +512,16 @@ def main():
         }
     if args.voice_frames:
         vpath = synth.cached("voice", synth.VOICE, 1)
-        (ft, fbr, fvo, fcodes, fids), fref, vinfo = gpu_voice_frames(path, vpath, args.voice_frames, 4)
+        cpath = synth.cached("codec", synth.CODEC, 2)
+        (ft, fbr, fvo, fcodes, fids, fcd), fref, vinfo = gpu_voice_frames(path, vpath, cpath, args.voice_frames, 4)
         line["voice_frame"] = {
             "workload": "cfg4: step2 of the cfg2 model (slot A: text step with scores at KV context 4096, from position "
                         f"{A_POS}; slot B: voice brain step fed the feedback row sum), then the Q8_0 generator "
                         "(6 layers, hidden 1024, FFN 4096, 16/4 heads x 64, 8 codebooks x 2048) in passes of 4 + 4 "
                         "codebooks in a shuffled order, each followed by sampling on the device (temperature 0.4, "
-                        "repeat penalty 1.2 over the last 64 frames), then the feedback row sum",
+                        "repeat penalty 1.2 over the last 64 frames), then the codec (12 codes -> FSQ -> 8 LFM layers "
+                        "on Q8_0, 512 wide, 5 short conv + 3 gated attention over 30 positions -> 1280-point inverse "
+                        "STFT, 1920 samples at 24 kHz) and the feedback row sum",
             "frames": int(len(ft)),
             "p50_ms": round(float(np.percentile(ft, 50)) * 1e3, 3),
             "p99_ms": round(float(np.percentile(ft, 99)) * 1e3, 3),
@@ -509,6 +529,8 @@ def main():
             "step2_p50_ms": round(float(np.percentile(fbr, 50)) * 1e3, 3),
             "generator_p50_ms": round(float(np.percentile(fvo, 50)) * 1e3, 3),
             "generator_table_bytes": int(vinfo["table_bytes"]),
+            "codec_p50_ms": round(float(np.percentile(fcd, 50)) * 1e3, 3),
+            "codec_table_bytes": vinfo["codec_table_bytes"],
             "budget_ms": 80.0,
         }
     if not args.no_cpu:
@@ -558,17 +580,22 @@ def main():
             line["prefill"]["speedup_vs_cpu"] = round(csec / float(np.percentile(pt, 50)), 1)
             line["prefill"]["scores_match_cpu"] = bool(np.array_equal(clg.view(np.uint32), plg.view(np.uint32)))
         if args.voice_frames and args.cpu_voice_frames:
-            ct, cbr, cvo, ccodes, cids, _, _ = cpu_voice_frames(path, vpath, threads, args.cpu_voice_frames)
+            ct, cbr, cvo, ccodes, cids, _, _, ccd, cpcm = cpu_voice_frames(path, vpath, cpath, threads, args.cpu_voice_frames)
             n = len(ct)
             line["voice_frame"]["cpu"] = {
                 "p50_ms": round(float(np.percentile(ct, 50)) * 1e3, 2),
                 "step2_p50_ms": round(float(np.percentile(cbr, 50)) * 1e3, 2),
                 "generator_p50_ms": round(float(np.percentile(cvo, 50)) * 1e3, 2),
-                "frames": n, "cores": threads, "kind": "port",
-                "sample": f"the first {n} frames of the same run on the oracle (C++ restatement of imi's engine and voice "
-                          "generator; its 8-codebook pass tables take imi's scalar generic order)",
+                "codec_p50_ms": round(float(np.percentile(ccd, 50)) * 1e3, 2),
+                "frames": n, "cores": threads, "codec_cores": 1, "kind": "port",
+                "sample": f"the first {n} frames of the same run on the oracle (C++ restatement of imi's engine, voice "
+                          "generator and codec; its 8-codebook pass tables take imi's scalar generic order; the codec "
+                          "restatement runs on one thread)",
             }
             line["voice_frame"]["codes_match_cpu"] = bool(np.array_equal(ccodes, fref[3][:n]) and cids == fref[4][:n])
+            gp = fref[8][:len(cpcm)]
+            line["voice_frame"]["pcm_rel_l2_vs_cpu"] = float(
+                np.sqrt(((gp.astype(np.float64) - cpcm) ** 2).sum() / max((cpcm.astype(np.float64) ** 2).sum(), 1e-30)))
     print(json.dumps(line), flush=True)
 
 

@@ -1,11 +1,11 @@
-// seoul_gpu.hpp — imi's engine API (imi/core/seoul.h:19-94, imi/brain.h:20-65), file API (imi/model.h:12-36) and
-// voice generator API (imi/core/voice.h:17-51) over libseoul_hip's C ABI.
+// seoul_gpu.hpp — imi's engine API (imi/core/seoul.h:19-94, imi/brain.h:20-65), file API (imi/model.h:12-36), voice
+// generator API (imi/core/voice.h:17-51) and codec API (imi/core/codec.h:17-65) over libseoul_hip's C ABI.
 //
 // Drop-in for the CPU engine: the same members and signatures, so imi's callers (greedy loops, the voice frame,
 // step2 riding) compile unchanged after
 //     #include "seoul_gpu.hpp"
 //     using seoul_hip::imi_seoul; using seoul_hip::imi_seoul_state; using seoul_hip::imi_voice;
-//     using seoul_hip::imi_brain; using seoul_hip::imi_file; using seoul_hip::imi_tensor;
+//     using seoul_hip::imi_brain; using seoul_hip::imi_file; using seoul_hip::imi_tensor; using seoul_hip::imi_codec;
 // and link -lseoul_hip. Header-only C++17; no HIP or torch types. The thread arguments of load() are accepted and
 // ignored (the device has no thread team). Errors follow imi: load() returns false and prints; a full context
 // prints "context full" and returns without stepping (imi/core/seoul.cpp:209,353,498).
@@ -442,6 +442,56 @@ private:
     sh_voice* v = nullptr;
     bool report(const char* what) const {
         fprintf(stderr, "seoul-hip: voice %s: %s\n", what, sh_last_error());
+        return false;
+    }
+};
+
+// imi_codec (imi/core/codec.h:17-65) over the same C ABI: the codec decoder on the device. frame() appends the
+// frame's samples to pcm (1920, less the start padding after a reset), flush() the tail the overlap holds back.
+// `threads` and `shared` (CPU thread team) are accepted and ignored.
+struct imi_codec {
+    int n_lvl = 0, n_cb = 12, n_embd = 0, n_ff = 0, n_head = 0, n_head_kv = 0, head_dim = 0, d_conv = 0;
+    int n_fs = 6, window = 30, n_fft = 1280, hop = 320, n_bins = 641;
+    float eps = 1e-5f, theta = 1e6f;
+    int n_threads = 4;
+
+    imi_codec() = default;
+    imi_codec(const imi_codec&) = delete;
+    imi_codec& operator=(const imi_codec&) = delete;
+    ~imi_codec() {
+        if (c) sh_codec_free(c);
+    }
+
+    bool load(const std::string& path, int threads, void* shared = nullptr, int device = 0) {   // codec.cpp:41-108
+        (void)shared;
+        n_threads = threads;
+        if (sh_codec_load(device, path.c_str(), &c) != SH_OK) return report("load");
+        sh_codec_shape I{};
+        sh_codec_info(c, &I);
+        n_lvl = I.n_lvl; n_embd = I.n_embd; n_ff = I.n_ff; n_head = I.n_head; n_head_kv = I.n_head_kv;
+        head_dim = I.head_dim; d_conv = I.d_conv; n_bins = I.n_bins;
+        return true;
+    }
+    void reset() {   // codec.cpp:110-119
+        if (sh_codec_reset(c) != SH_OK) report("reset");
+    }
+    void frame(const int32_t* codes, std::vector<float>& pcm) {   // codec.cpp:121-127
+        float buf[1920];
+        int n = 0;
+        if (sh_codec_frame(c, codes, buf, &n) != SH_OK) { report("frame"); return; }
+        pcm.insert(pcm.end(), buf, buf + n);
+    }
+    void flush(std::vector<float>& pcm) {   // codec.cpp:271-277
+        float buf[1280];
+        int n = 0;
+        if (sh_codec_flush(c, buf, &n) != SH_OK) { report("flush"); return; }
+        pcm.insert(pcm.end(), buf, buf + n);
+    }
+
+private:
+    sh_codec* c = nullptr;
+    bool report(const char* what) const {
+        fprintf(stderr, "seoul-hip: codec %s: %s\n", what, sh_last_error());
         return false;
     }
 };

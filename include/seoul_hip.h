@@ -14,6 +14,7 @@
  *   imi_q4x8 kernel API (cfg 0)     imi/kernels/q4x8.h:8-18
  *   imi_q4 table reads              imi/core/tables.h:103-138
  *   imi_voice generator             imi/core/voice.h:17-51
+ *   imi_codec decoder               imi/core/codec.h:17-65
  */
 #ifndef SEOUL_HIP_H
 #define SEOUL_HIP_H
@@ -39,6 +40,7 @@ typedef struct sh_state sh_state;   /* one conversation's memory: K/V caches, co
 typedef struct sh_q4 sh_q4;         /* one Q4_0 table on the device (kernel-level API) */
 typedef struct sh_voice sh_voice;   /* the Q8_0 voice generator on the device */
 typedef struct sh_file sh_file;     /* one GGUF file read into host memory (imi_file) */
+typedef struct sh_codec sh_codec;   /* the codec decoder on the device (codes -> 24 kHz samples) */
 
 typedef struct {
     int n_embd, n_vocab, n_head, n_head_kv, head_dim, n_ff, d_conv, n_ctx, n_layer, n_attn, n_swa;
@@ -49,6 +51,26 @@ typedef struct {
 
 /* Message of the last error on this thread ("" if none). */
 const char* sh_last_error(void);
+
+/* ---- codec decoder: imi_codec::load / reset / frame / flush (imi/core/codec.h:17-65) ---- */
+typedef struct {
+    int n_embd, n_ff, n_head, n_head_kv, head_dim, d_conv, n_layer, n_bins, n_lvl, n_q, n_codes;
+    long long table_bytes;          /* Q8_0 table bytes read per frame */
+} sh_codec_shape;
+
+/* Read a GGUF codec ("a.gen.wav." tensors: FSQ level table, quantizer projection, Q8_0 in_proj / out_proj and LFM
+ * layers of short conv or gated attention) onto `device` (imi/core/codec.cpp:41-108). n_embd up to 512, head_dim up
+ * to 128, 2 to 8 conv taps, 641 bins (n_fft 1280, hop 320). Own stream; independent of any brain context. */
+int sh_codec_load(int device, const char* gguf_path, sh_codec** out);
+int sh_codec_free(sh_codec* c);                                   /* imi_codec::~imi_codec (codec.cpp:279-282) */
+int sh_codec_info(const sh_codec* c, sh_codec_shape* out);
+/* codec.cpp:110-119: conv memory, attention window and overlap cleared, position 0, start padding re-armed */
+int sh_codec_reset(sh_codec* c);
+/* One frame of 12 codes (each in [0, n_codes)) -> its samples (codec.cpp:121-127): pcm needs room for 1920;
+ * *n_out = 1920, less the start padding on the first frames after a reset (1440 on the first). */
+int sh_codec_frame(sh_codec* c, const int32_t* codes, float* pcm, int* n_out);
+/* The end of speech (codec.cpp:271-277): the tail the overlap holds back, 480 samples; then a reset. */
+int sh_codec_flush(sh_codec* c, float* pcm, int* n_out);
 
 /* ---- GGUF file: imi_file::load / get / key_i / key_f / keep / drop_data (imi/model.h:12-36) ---- */
 /* The ggml_tensor fields imi's callers read. name points into the file object; data is the tensor's bytes in host

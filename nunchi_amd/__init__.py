@@ -27,6 +27,7 @@ EXPORTS = [
     "sh_voice_feedback", "sh_voice_sample",
     "sh_file_load", "sh_file_free", "sh_file_get", "sh_file_key_i", "sh_file_key_f", "sh_file_keep", "sh_file_drop_data",
     "sh_file_n_tensors", "sh_file_tensor", "sh_file_key_arr", "sh_file_block",
+    "sh_codec_load", "sh_codec_free", "sh_codec_info", "sh_codec_reset", "sh_codec_frame", "sh_codec_flush",
 ]
 
 
@@ -48,6 +49,11 @@ class ModelInfo(C.Structure):
 class VoiceShape(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("n_embd", "n_vocab", "n_cb", "n_in", "n_head", "n_head_kv", "head_dim", "n_ff",
                                        "n_layer")] + [("table_bytes", C.c_longlong), ("feedback_bytes", C.c_longlong)]
+
+
+class CodecShape(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("n_embd", "n_ff", "n_head", "n_head_kv", "head_dim", "d_conv", "n_layer", "n_bins",
+                                       "n_lvl", "n_q", "n_codes")] + [("table_bytes", C.c_longlong)]
 
 
 class Tensor(C.Structure):
@@ -118,6 +124,12 @@ def load_library(path: str = LIB_PATH):
         "sh_file_tensor": (i, [vp, i, P(Tensor)]),
         "sh_file_key_arr": (i, [vp, C.c_char_p, P(C.c_int64), i]),
         "sh_file_block": (i, [vp, P(vp), P(C.c_size_t)]),
+        "sh_codec_load": (i, [i, C.c_char_p, P(vp)]),
+        "sh_codec_free": (i, [vp]),
+        "sh_codec_info": (i, [vp, P(CodecShape)]),
+        "sh_codec_reset": (i, [vp]),
+        "sh_codec_frame": (i, [vp, vp, vp, P(i)]),
+        "sh_codec_flush": (i, [vp, vp, P(i)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -442,6 +454,46 @@ def q4_bench_kernel(ctx: Context, tables, n_in: int = 1, cut_mode: int = 0, reps
     us = C.c_double()
     _check(_lib.sh_q4_bench_kernel(ctx.h, arr, len(tables), int(n_in), int(cut_mode), int(reps), C.byref(us)))
     return us.value
+
+
+class Codec:
+    """The codec decoder on the device, shaped like imi_codec (imi/core/codec.h:17-65): frame(12 codes) -> the
+    frame's 24 kHz samples (1920, less the start padding after a reset), flush() -> the 480 held back, reset()."""
+
+    FRAME, TAIL = 1920, 480
+
+    def __init__(self, path: str, device: int = 0):
+        L = load_library()
+        self.h = C.c_void_p()
+        _check(L.sh_codec_load(int(device), path.encode(), C.byref(self.h)))
+        self.info = CodecShape()
+        _check(L.sh_codec_info(self.h, C.byref(self.info)))
+
+    def close(self):
+        if getattr(self, "h", None) and self.h.value:
+            _lib.sh_codec_free(self.h)
+            self.h = C.c_void_p()
+
+    def __del__(self):
+        self.close()
+
+    def reset(self):
+        _check(_lib.sh_codec_reset(self.h))
+
+    def frame(self, codes) -> np.ndarray:
+        codes = np.ascontiguousarray(codes, np.int32)
+        if codes.size != 12:
+            raise ValueError("a codec frame takes 12 codes")
+        out = np.zeros(self.FRAME, np.float32)
+        n = C.c_int()
+        _check(_lib.sh_codec_frame(self.h, _p(codes), _p(out), C.byref(n)))
+        return out[:n.value]
+
+    def flush(self) -> np.ndarray:
+        out = np.zeros(self.TAIL, np.float32)
+        n = C.c_int()
+        _check(_lib.sh_codec_flush(self.h, _p(out), C.byref(n)))
+        return out[:n.value]
 
 
 _live_voices = weakref.WeakSet()

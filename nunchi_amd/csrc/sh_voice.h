@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <vector>
 
 namespace sh {
 
@@ -103,6 +104,9 @@ struct vsample_args {
     int32_t* picks;         // device [n_need]
     double* keep;           // device [n_need] 1 - p[V - 1] / sum
 };
+
+// Q8_0 rows (each n_cols / 32 blocks of fp16 d + 32 int8) -> the device layout's codes and scales (host side)
+void repack_q8(const std::vector<const uint8_t*>& rows, int cols, std::vector<int8_t>& codes, std::vector<uint16_t>& scales);
 
 hipError_t launch_vtab(int P, int pro, int epi, const vtab_args& a, hipStream_t s);
 hipError_t launch_vsample(const vsample_args& a, int max_need, hipStream_t s);

@@ -523,6 +523,7 @@ hipError_t launch_vtab_kind(int pro, int epi, const vtab_args& a, hipStream_t s)
     if (pro == VP_NORM && epi == VE_STORE) return launch_vtab_p<P, VP_NORM, VE_STORE>(a, s);
     if (pro == VP_PLAIN && epi == VE_RESID) return launch_vtab_p<P, VP_PLAIN, VE_RESID>(a, s);
     if (pro == VP_NORM && epi == VE_SWIGLU) return launch_vtab_p<P, VP_NORM, VE_SWIGLU>(a, s);
+    if (pro == VP_PLAIN && epi == VE_STORE) return launch_vtab_p<P, VP_PLAIN, VE_STORE>(a, s);
     return hipErrorInvalidValue;
 }
 

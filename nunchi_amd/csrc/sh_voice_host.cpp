@@ -28,9 +28,11 @@ namespace {
         if (e_ != hipSuccess) return set_error(SH_E_HIP, std::string(#x) + ": " + hipGetErrorString(e_));       \
     } while (0)
 
+}  // namespace
+
 // Q8_0 rows (pointers to n_cols / 32 blocks of fp16 d + 32 int8 each) -> codes [G][nb][8][32], scales [G][nb][8]
 // (the grouping of imi_q8g::build, imi/core/tables.cpp:297-318, with the 32 codes of a block kept together)
-void repack_q8(const std::vector<const uint8_t*>& rows, int cols, std::vector<int8_t>& codes, std::vector<uint16_t>& scales) {
+void sh::repack_q8(const std::vector<const uint8_t*>& rows, int cols, std::vector<int8_t>& codes, std::vector<uint16_t>& scales) {
     const int R = (int)rows.size(), G = (R + 7) / 8, nb = cols / 32;
     codes.assign((size_t)G * nb * 8 * 32, 0);
     scales.assign((size_t)G * nb * 8, 0);
@@ -42,6 +44,8 @@ void repack_q8(const std::vector<const uint8_t*>& rows, int cols, std::vector<in
             memcpy(&codes[blk * 32], b + 2, 32);
         }
 }
+
+namespace {
 
 struct vlayer {
     q8dev qkvg, o, gate_up, down;

@@ -230,6 +230,80 @@ def write_voice(path: str, shape: VoiceShape = VOICE, seed: int = 1) -> str:
     return path
 
 
+@dataclass(frozen=True)
+class CodecShape:
+    """The codec decoder ("a.gen.wav." names as imi/core/codec.cpp:43-95 reads them). Fixed by imi: 12 codes per frame,
+    6 positions per frame, window 30, n_fft 1280, hop 320, 641 bins (imi/core/codec.h:1-5,34). Chosen here, as the
+    reference's files do not state them: the FSQ table's rows (2016, as imi/ref/codec_exact.py notes) and width (4),
+    the projection width (256), the FFN width, heads and the conv taps."""
+    n_embd: int = 512
+    n_ff: int = 2048
+    n_head: int = 8
+    n_head_kv: int = 8
+    head_dim: int = 64
+    conv_k: int = 4                  # taps of the depthwise conv (d_conv = conv_k - 1 rows of memory)
+    layers: str = "ccaccaca"         # per layer: c = short conv, a = gated attention over the window
+    n_codes: int = 2016              # rows of the FSQ level table
+    n_lvl: int = 4
+    n_cb: int = 12
+    n_q: int = 256                   # width of the quantizer's output projection
+    n_bins: int = 641
+
+
+CODEC = CodecShape()
+TINY_CODEC = CodecShape(n_embd=128, n_ff=256, n_head=2, n_head_kv=1, head_dim=64, layers="cac", n_codes=64, n_q=64)
+
+
+def write_codec(path: str, shape: CodecShape = CODEC, seed: int = 2) -> str:
+    """Q8_0 tables (scales |N(0, 0.02)| / 8 and int8 codes as the other files), fp32 FSQ levels uniform in [-1, 1],
+    projections and biases N(0, 0.1)-sized, norms 1 + 0.05 N(0, 1), conv taps N(0, 0.3), fp32 head gates N(0, 0.05);
+    the output bias puts the log magnitudes near -3 and the phases near 0."""
+    s = shape
+    E, D = s.n_embd, s.head_dim
+    w = GGUFWriter()
+    w.add_str("general.architecture", "lfm3-wav")
+    g = "a.gen.wav."
+
+    def q8(name, rows, cols):
+        w.add_tensor(g + name, T_Q8_0, (cols, rows), q8_0_random(_rng(seed, name), rows, cols))
+
+    def f32(name, arr, ne):
+        w.add_tensor(g + name, T_F32, ne, np.ascontiguousarray(arr, dtype=np.float32))
+
+    nq = s.n_cb * s.n_lvl
+    f32("quant.first.codebook.weight", _rng(seed, "lvl").uniform(-1.0, 1.0, (s.n_codes, s.n_lvl)), (s.n_lvl, s.n_codes))
+    f32("quant.first.out_proj.weight", _rng(seed, "qo").standard_normal((s.n_q, nq)) / np.sqrt(nq), (nq, s.n_q))
+    f32("quant.first.out_proj.bias", 0.1 * _rng(seed, "qob").standard_normal(s.n_q), (s.n_q,))
+    q8("tfm.in_proj.weight", E, s.n_q)
+    f32("tfm.in_proj.bias", 0.1 * _rng(seed, "inb").standard_normal(E), (E,))
+    for il, kind in enumerate(s.layers):
+        p = f"tfm.blk.{il}."
+        for n in ("ln1", "ln2", "attn_post_norm", "ffn_post_norm"):
+            f32(p + n + ".weight", _norm_w(_rng(seed, p + n), E), (E,))
+        if kind == "c":
+            f32(p + "conv_dw.weight", 0.3 * _rng(seed, p + "dw").standard_normal((E, s.conv_k)), (s.conv_k, E))
+            q8(p + "conv_pw1.weight", 3 * E, E)
+            q8(p + "conv_pw2.weight", E, E)
+        else:
+            f32(p + "attn_q_norm.weight", _norm_w(_rng(seed, p + "qn"), D), (D,))
+            f32(p + "attn_k_norm.weight", _norm_w(_rng(seed, p + "kn"), D), (D,))
+            q8(p + "attn_q.weight", s.n_head * D, E)
+            q8(p + "attn_k.weight", s.n_head_kv * D, E)
+            q8(p + "attn_v.weight", s.n_head_kv * D, E)
+            q8(p + "attn_out.weight", E, s.n_head * D)
+            f32(p + "attn_gate.weight", 0.05 * _rng(seed, p + "gate").standard_normal((s.n_head, E)), (E, s.n_head))
+        q8(p + "ffn_gate.weight", s.n_ff, E)
+        q8(p + "ffn_up.weight", s.n_ff, E)
+        q8(p + "ffn_down.weight", E, s.n_ff)
+    f32("tfm.output_norm.weight", _norm_w(_rng(seed, "onorm"), E), (E,))
+    q8("tfm.out_proj.weight", 2 * s.n_bins, E)
+    ob = np.concatenate([-3.0 + 0.5 * _rng(seed, "obm").standard_normal(s.n_bins),
+                         0.5 * _rng(seed, "obp").standard_normal(s.n_bins)])
+    f32("tfm.out_proj.bias", ob, (2 * s.n_bins,))
+    w.write(path)
+    return path
+
+
 def cached(kind: str, shape, seed: int, directory: str | None = None) -> str:
     """Write the model once per (kind, shape, seed) into a cache directory and return its path."""
     directory = directory or os.environ.get("NUNCHI_MODEL_DIR", "/tmp/nunchi_models")
@@ -238,6 +312,6 @@ def cached(kind: str, shape, seed: int, directory: str | None = None) -> str:
     path = os.path.join(directory, f"{kind}-{tag}.gguf")
     if not os.path.exists(path):
         tmp = f"{path}.{os.getpid()}.tmp"
-        (write_brain if kind == "brain" else write_voice)(tmp, shape, seed)
+        {"brain": write_brain, "voice": write_voice, "codec": write_codec}[kind](tmp, shape, seed)
         os.replace(tmp, path)
     return path

@@ -85,6 +85,13 @@ def lib():
         "orc_voice_feedback": (None, [vp, _i32p, _f32p]),
         "orc_voice_sample": (None, [_f32p, i, i, _i32p, _i32p, i, i, C.POINTER(C.c_double), f, f, _i32p,
                                     C.POINTER(C.c_double)]),
+        "orc_codec_load": (vp, [C.c_char_p]),
+        "orc_codec_free": (None, [vp]),
+        "orc_codec_info": (None, [vp, _i32p]),
+        "orc_codec_reset": (None, [vp]),
+        "orc_codec_frame": (i, [vp, _i32p, _f32p, vp]),
+        "orc_codec_flush": (i, [vp, _f32p]),
+        "orc_ifft": (None, [_f32p, _f32p, i, _f32p, _f32p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -356,6 +363,51 @@ def expf(x: np.ndarray) -> np.ndarray:
     y = np.empty_like(x)
     lib().orc_expf(x.reshape(-1), x.size, y.reshape(-1))
     return y
+
+
+class Codec:
+    """imi_codec restated (imi/core/codec.h:17-65): frame(12 codes) -> its PCM samples (and, with spec, the frame's
+    [6][2 * n_bins] log magnitudes and phases); flush() -> the tail the overlap holds back; reset()."""
+
+    HOP, N_FS = 320, 6
+
+    def __init__(self, path: str):
+        self.h = lib().orc_codec_load(path.encode())
+        if not self.h:
+            raise RuntimeError(f"oracle: cannot load {path}")
+        info = np.zeros(11, np.int32)
+        lib().orc_codec_info(self.h, info)
+        (self.n_embd, self.n_ff, self.n_head, self.n_head_kv, self.head_dim, self.d_conv, self.n_layer, self.n_bins,
+         self.n_lvl, self.n_q, _) = (int(v) for v in info)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().orc_codec_free(self.h)
+            self.h = None
+
+    def reset(self):
+        lib().orc_codec_reset(self.h)
+
+    def frame(self, codes, spec: bool = False):
+        codes = np.ascontiguousarray(codes, np.int32)
+        pcm = np.zeros(self.N_FS * self.HOP, np.float32)
+        sp = np.zeros((self.N_FS, 2 * self.n_bins), np.float32) if spec else None
+        n = lib().orc_codec_frame(self.h, codes, pcm, _ptr(sp))
+        return (pcm[:n], sp) if spec else pcm[:n]
+
+    def flush(self):
+        pcm = np.zeros(1280, np.float32)
+        n = lib().orc_codec_flush(self.h, pcm)
+        return pcm[:n]
+
+
+def ifft(x) -> np.ndarray:
+    """The codec's inverse DFT (imi/core/codec.cpp:25-39) of a complex vector, unnormalised."""
+    x = np.asarray(x, np.complex64)
+    re, im = np.ascontiguousarray(x.real, np.float32), np.ascontiguousarray(x.imag, np.float32)
+    ore, oim = np.zeros_like(re), np.zeros_like(im)
+    lib().orc_ifft(re, im, len(re), ore, oim)
+    return ore.astype(np.complex64) + 1j * oim
 
 
 def rel(a, b) -> float:

@@ -1,6 +1,7 @@
-"""ORACLE — test infrastructure only. Float64 "truth key" of the brain and the voice generator.
+"""ORACLE — test infrastructure only. Float64 "truth key" of the brain, the voice generator and the codec.
 
-Restates imi/ref/ref_exact.py:37-87 (brain) and imi/ref/gen_exact.py:27-54 (voice generator): the file's own
+Restates imi/ref/ref_exact.py:37-87 (brain), imi/ref/gen_exact.py:27-54 (voice generator) and
+imi/ref/codec_exact.py:23-72 (codec, whole-sequence form with numpy's inverse real FFT): the file's own
 dequantized weights, run in float64 with no input rounding. Used to pin the int8-cut restatement (liboracle) at the
 model level: a dropped term, a wrong sign or a transposed table moves it far outside the cut's error.
 Dequantization is written here from the GGUF block formats (closed forms), not shared with the product code.
@@ -208,3 +209,81 @@ def voice_pass(path: str, hidden, codes, eps=1e-5, theta=1e6):
         x = x + (gg / (1 + np.exp(-gg)) * (hh @ l["ffn_up"].T)) @ l["ffn_down"].T
     z = norm(norm(x, onorm), hnorm)
     return np.stack([embd[c] @ z[c] for c in range(P)])
+
+
+def codec(path: str, codes, eps=1e-5, win=30, theta=1e6, n_fft=1280, hop=320):
+    """PCM of a run of frames (codes [F][12]) in float64, as imi/ref/codec_exact.py:23-72 computes it: N = 6F
+    positions, the causal windowed attention over positions 0.., the conv over zeros before position 0, the inverse
+    real FFT (numpy), periodic Hann, overlap-add normalised by the summed squared window, (n_fft - hop) / 2 trimmed
+    at both ends: N * hop samples."""
+    W = Weights(path, "a.gen.wav.")
+    codes = np.asarray(codes, np.int64)
+    F, P = len(codes), 6
+    lvl = W("quant.first.codebook.weight")
+    x = lvl[codes].reshape(F, -1) @ W("quant.first.out_proj.weight").T + W("quant.first.out_proj.bias")
+    x = x @ W("tfm.in_proj.weight").T + W("tfm.in_proj.bias")
+    x = np.repeat(x, P, 0)
+    N = len(x)
+
+    def norm(v, w):
+        return v / np.sqrt((v * v).mean(-1, keepdims=True) + eps) * w
+
+    def rope(v, D):
+        half = D // 2
+        inv = theta ** (-np.arange(half) * 2.0 / D)
+        ang = np.arange(N)[:, None] * inv[None]
+        c, sn = np.cos(ang)[:, None], np.sin(ang)[:, None]
+        a, b = v[..., :half], v[..., half:]
+        return np.concatenate([a * c - b * sn, a * sn + b * c], -1)
+
+    il = 0
+    while W.has(f"tfm.blk.{il}.ln1.weight"):
+        p = f"tfm.blk.{il}."
+        h = norm(x, W(p + "ln1.weight"))
+        if W.has(p + "conv_dw.weight"):
+            bcx = h @ W(p + "conv_pw1.weight").T
+            E = x.shape[1]
+            b, c, xx = bcx[:, :E], bcx[:, E:2 * E], bcx[:, 2 * E:]
+            cw = W(p + "conv_dw.weight")
+            K = cw.shape[1]
+            bx = np.concatenate([np.zeros((K - 1, E)), b * xx])
+            co = np.stack([(bx[t:t + K] * cw.T).sum(0) for t in range(N)])
+            y = (c * co) @ W(p + "conv_pw2.weight").T
+        else:
+            qn = W(p + "attn_q_norm.weight")
+            D = qn.shape[0]
+            q = (h @ W(p + "attn_q.weight").T).reshape(N, -1, D)
+            k = (h @ W(p + "attn_k.weight").T).reshape(N, -1, D)
+            v = (h @ W(p + "attn_v.weight").T).reshape(N, -1, D)
+            H, Hk = q.shape[1], k.shape[1]
+            q, k = rope(norm(q, qn), D), rope(norm(k, W(p + "attn_k_norm.weight")), D)
+            g = 1 / (1 + np.exp(-(h @ W(p + "attn_gate.weight").T)))
+            a = np.zeros((N, H, D))
+            for t in range(N):
+                s0 = max(0, t - win + 1)
+                for hh in range(H):
+                    kv = hh // (H // Hk)
+                    sc = k[s0:t + 1, kv] @ q[t, hh] / np.sqrt(D)
+                    pr = np.exp(sc - sc.max())
+                    pr /= pr.sum()
+                    a[t, hh] = pr @ v[s0:t + 1, kv]
+            y = (a * g[:, :, None]).reshape(N, -1) @ W(p + "attn_out.weight").T
+        x = x + norm(y, W(p + "attn_post_norm.weight"))
+        h = norm(x, W(p + "ln2.weight"))
+        gg = h @ W(p + "ffn_gate.weight").T
+        x = x + norm((gg / (1 + np.exp(-gg)) * (h @ W(p + "ffn_up.weight").T)) @ W(p + "ffn_down.weight").T,
+                     W(p + "ffn_post_norm.weight"))
+        il += 1
+    out = norm(x, W("tfm.output_norm.weight")) @ W("tfm.out_proj.weight").T + W("tfm.out_proj.bias")
+    nb = out.shape[1] // 2
+    spec = np.exp(out[:, :nb]) * np.exp(1j * out[:, nb:])
+    hann = 0.5 * (1 - np.cos(2 * np.pi * np.arange(n_fft) / n_fft))
+    frames = np.fft.irfft(spec, n_fft, axis=1) * hann
+    total = (N - 1) * hop + n_fft
+    ola, ws = np.zeros(total), np.zeros(total)
+    for i in range(N):
+        ola[i * hop:i * hop + n_fft] += frames[i]
+        ws[i * hop:i * hop + n_fft] += hann ** 2
+    pcm = np.where(ws > 1e-8, ola / np.maximum(ws, 1e-30), ola)
+    pad = (n_fft - hop) // 2
+    return pcm[pad:pad + N * hop], out
