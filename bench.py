@@ -95,10 +95,11 @@ def cpu_decode(path, threads, steps, b2: bool, runs: int = 1):
 VOICE_CTX = 4096      # slot A's KV context in the voice frame
 A_POS = 2048          # slot A's position when the timed frames start
 SCHEDULE = (4, 4)     # masked passes of a frame: codebooks scored (and fixed) by each, in a shuffled order
+TALK_SCHEDULE = (6, 6)   # imi's schedule for its 12 codebooks (imi/core/talk.cpp:129)
 TEMP, REP, REP_WIN = 0.4, 1.2, 64   # imi's sampling settings (imi/core/talk.cpp:131-133)
 
 
-def play_frames(step2, voice, tok_a, fb, frames, pick, codec=None):
+def play_frames(step2, voice, tok_a, fb, frames, pick, schedule=SCHEDULE, codec=None):
     """Voice frames as imi's talk loop runs them (imi/core/talk.cpp:127-187) with slot A riding along
     (imi/core/flow.cpp:118): step2 (A: text step with scores, B: the voice brain step fed the last feedback row sum),
     begin_frame from B's hidden state, the masked passes over a shuffled codebook order (each samples its
@@ -121,7 +122,7 @@ def play_frames(step2, voice, tok_a, fb, frames, pick, codec=None):
         voice.begin_frame(hb)
         codes = np.full(voice.n_cb, -1, np.int32)
         k = 0
-        for n in SCHEDULE:
+        for n in schedule:
             need = order[k:k + n]
             codes[need] = pick(voice, codes, need, window, u[k:k + n])
             k += n
@@ -146,16 +147,17 @@ def codec_levels(codec) -> int:
     return codec.info.n_codes if hasattr(codec, "info") else codec.n_codes
 
 
-def gpu_voice_frames(brain_path, voice_path, codec_path, frames, warmup):
+def gpu_voice_frames(brain_path, voice_path, frames, warmup, a_pos=A_POS, schedule=SCHEDULE, codec_path=None):
+    """Voice frames on the device: slot A decodes greedily to position a_pos first, then the frames run."""
     import nunchi_amd
     brain = nunchi_amd.Brain(brain_path, n_ctx=VOICE_CTX)
     voice = nunchi_amd.Voice(voice_path)
-    codec = nunchi_amd.Codec(codec_path)
+    codec = nunchi_amd.Codec(codec_path) if codec_path else None
     sa, sb = brain.new_state(), brain.new_state()
     pa = _prompt(2, brain.n_vocab)
     for i in range(PROMPT):
         _, _, ba = brain.step(int(pa[i]), want_logits=i == PROMPT - 1, st=sa)
-    ids, _ = brain.generate(ba, A_POS - PROMPT, a=sa)
+    ids = brain.generate(ba, a_pos - PROMPT, a=sa)[0] if a_pos > PROMPT else np.array([ba], np.int32)
 
     def step2(tok, fb):
         (_, _, best), (hb, _, _) = brain.step2(tok, None, True, sb, -1, fb, False, a=sa)
@@ -164,25 +166,27 @@ def gpu_voice_frames(brain_path, voice_path, codec_path, frames, warmup):
     fb = voice.feedback(np.zeros(voice.n_cb, np.int32))
     ref = play_frames(step2, voice, int(ids[-1]), fb, frames + warmup,
                       lambda v, codes, need, win, u: (v.pass_(codes, need, scores=False),
-                                                      v.sample(win, u, TEMP, REP)[0])[1], codec)
+                                                      v.sample(win, u, TEMP, REP)[0])[1], schedule, codec)
     # the timed frames are the frames after the warmup ones, in the same run (states keep advancing)
     out = tuple(x[warmup:] for x in ref[:4]) + (ref[4][warmup:], ref[7][warmup:])
-    info = {"table_bytes": voice.table_bytes, "n_cb": voice.n_cb, "codec_table_bytes": int(codec.info.table_bytes)}
-    codec.close()
+    info = {"table_bytes": voice.table_bytes, "n_cb": voice.n_cb}
+    if codec is not None:
+        info["codec_table_bytes"] = int(codec.info.table_bytes)
+        codec.close()
     voice.close()
     brain.ctx.close()
     return out, ref, info
 
 
-def cpu_voice_frames(brain_path, voice_path, codec_path, threads, frames):
+def cpu_voice_frames(brain_path, voice_path, threads, frames, a_pos=A_POS, schedule=SCHEDULE, codec_path=None):
     import oracle
     eng = oracle.Engine(brain_path, threads=threads, n_ctx=VOICE_CTX)
     voice = oracle.Voice(voice_path, threads=threads)
-    codec = oracle.Codec(codec_path)
+    codec = oracle.Codec(codec_path) if codec_path else None
     pa = _prompt(2, eng.n_vocab)
     for i in range(PROMPT):
         _, lg = eng.step(int(pa[i]), want_logits=i == PROMPT - 1)
-    ids, _ = eng.greedy(oracle.top(lg), A_POS - PROMPT)
+    ids = eng.greedy(oracle.top(lg), a_pos - PROMPT)[0] if a_pos > PROMPT else np.array([oracle.top(lg)], np.int32)
     st = eng.new_state()
 
     def step2(tok, fb):
@@ -192,7 +196,7 @@ def cpu_voice_frames(brain_path, voice_path, codec_path, threads, frames):
     fb = voice.feedback(np.zeros(voice.n_cb, np.int32))
     return play_frames(step2, voice, int(ids[-1]), fb, frames,
                        lambda v, codes, need, win, u: oracle.voice_sample(v.pass_(codes, need), need, win, u, TEMP,
-                                                                          REP)[0], codec)
+                                                                          REP)[0], schedule, codec)
 
 
 HEAR_EMB, HEAR_TOK = 384, 64   # the hearing window: audio-encoder rows, then words
@@ -328,6 +332,8 @@ def main():
     ap.add_argument("--voice-frames", type=int, default=64, help="timed voice frames (cfg 4); 0 = skip")
     ap.add_argument("--prefill-reps", type=int, default=10, help="timed hearing-window prefills (cfg 3); 0 = skip")
     ap.add_argument("--cpu-voice-frames", type=int, default=8)
+    ap.add_argument("--talk-frames", type=int, default=32, help="timed talk frames (12-codebook generator + codec); 0 = skip")
+    ap.add_argument("--cpu-talk-frames", type=int, default=4)
     ap.add_argument("--decode-only", action="store_true",
                     help="only the decode runs and the in-step kernel timing (the launches a kernel trace of the step "
                          "should average), no CPU legs")
@@ -512,16 +518,13 @@ def main():
         }
     if args.voice_frames:
         vpath = synth.cached("voice", synth.VOICE, 1)
-        cpath = synth.cached("codec", synth.CODEC, 2)
-        (ft, fbr, fvo, fcodes, fids, fcd), fref, vinfo = gpu_voice_frames(path, vpath, cpath, args.voice_frames, 4)
+        (ft, fbr, fvo, fcodes, fids, _), fref, vinfo = gpu_voice_frames(path, vpath, args.voice_frames, 4)
         line["voice_frame"] = {
             "workload": "cfg4: step2 of the cfg2 model (slot A: text step with scores at KV context 4096, from position "
                         f"{A_POS}; slot B: voice brain step fed the feedback row sum), then the Q8_0 generator "
                         "(6 layers, hidden 1024, FFN 4096, 16/4 heads x 64, 8 codebooks x 2048) in passes of 4 + 4 "
                         "codebooks in a shuffled order, each followed by sampling on the device (temperature 0.4, "
-                        "repeat penalty 1.2 over the last 64 frames), then the codec (12 codes -> FSQ -> 8 LFM layers "
-                        "on Q8_0, 512 wide, 5 short conv + 3 gated attention over 30 positions -> 1280-point inverse "
-                        "STFT, 1920 samples at 24 kHz) and the feedback row sum",
+                        "repeat penalty 1.2 over the last 64 frames), and the feedback row sum",
             "frames": int(len(ft)),
             "p50_ms": round(float(np.percentile(ft, 50)) * 1e3, 3),
             "p99_ms": round(float(np.percentile(ft, 99)) * 1e3, 3),
@@ -529,9 +532,29 @@ def main():
             "step2_p50_ms": round(float(np.percentile(fbr, 50)) * 1e3, 3),
             "generator_p50_ms": round(float(np.percentile(fvo, 50)) * 1e3, 3),
             "generator_table_bytes": int(vinfo["table_bytes"]),
-            "codec_p50_ms": round(float(np.percentile(fcd, 50)) * 1e3, 3),
-            "codec_table_bytes": vinfo["codec_table_bytes"],
             "budget_ms": 80.0,
+        }
+    if args.talk_frames:
+        tpath = synth.cached("voice", synth.TALK_VOICE, 1)
+        cpath = synth.cached("codec", synth.CODEC, 2)
+        (tt, tbr, tvo, _, _, tcd), tref, tinfo = gpu_voice_frames(path, tpath, args.talk_frames, 4, PROMPT,
+                                                                  TALK_SCHEDULE, cpath)
+        line["talk_frame"] = {
+            "workload": "a whole talk frame as imi's talk loop runs it at the generator's own shape: step2 of the cfg2 "
+                        f"model (slot A from position {PROMPT}), the Q8_0 generator (3 layers, hidden 1024, FFN 4096, "
+                        "16/4 heads x 64, 12 codebooks x 2048) in passes of 6 + 6 codebooks with sampling on the "
+                        "device, then the codec (12 codes -> FSQ -> 8 LFM layers on Q8_0, 512 wide, 5 short conv + 3 "
+                        "gated attention over 30 positions -> 1280-point inverse STFT, 1920 samples at 24 kHz) and "
+                        "the feedback row sum",
+            "frames": int(len(tt)),
+            "p50_ms": round(float(np.percentile(tt, 50)) * 1e3, 3),
+            "p99_ms": round(float(np.percentile(tt, 99)) * 1e3, 3),
+            "step2_p50_ms": round(float(np.percentile(tbr, 50)) * 1e3, 3),
+            "generator_p50_ms": round(float(np.percentile(tvo, 50)) * 1e3, 3),
+            "codec_p50_ms": round(float(np.percentile(tcd, 50)) * 1e3, 3),
+            "generator_table_bytes": int(tinfo["table_bytes"]),
+            "codec_table_bytes": tinfo["codec_table_bytes"],
+            "audio_ms_per_frame": 80.0,
         }
     if not args.no_cpu:
         info = cpu_info()
@@ -580,22 +603,34 @@ def main():
             line["prefill"]["speedup_vs_cpu"] = round(csec / float(np.percentile(pt, 50)), 1)
             line["prefill"]["scores_match_cpu"] = bool(np.array_equal(clg.view(np.uint32), plg.view(np.uint32)))
         if args.voice_frames and args.cpu_voice_frames:
-            ct, cbr, cvo, ccodes, cids, _, _, ccd, cpcm = cpu_voice_frames(path, vpath, cpath, threads, args.cpu_voice_frames)
+            ct, cbr, cvo, ccodes, cids, _, _, _, _ = cpu_voice_frames(path, vpath, threads, args.cpu_voice_frames)
             n = len(ct)
             line["voice_frame"]["cpu"] = {
+                "p50_ms": round(float(np.percentile(ct, 50)) * 1e3, 2),
+                "step2_p50_ms": round(float(np.percentile(cbr, 50)) * 1e3, 2),
+                "generator_p50_ms": round(float(np.percentile(cvo, 50)) * 1e3, 2),
+                "frames": n, "cores": threads, "kind": "port",
+                "sample": f"the first {n} frames of the same run on the oracle (C++ restatement of imi's engine and voice "
+                          "generator; its 8-codebook pass tables take imi's scalar generic order)",
+            }
+            line["voice_frame"]["codes_match_cpu"] = bool(np.array_equal(ccodes, fref[3][:n]) and cids == fref[4][:n])
+        if args.talk_frames and args.cpu_talk_frames:
+            ct, cbr, cvo, ccodes, cids, _, _, ccd, cpcm = cpu_voice_frames(path, tpath, threads, args.cpu_talk_frames,
+                                                                           PROMPT, TALK_SCHEDULE, cpath)
+            n = len(ct)
+            line["talk_frame"]["cpu"] = {
                 "p50_ms": round(float(np.percentile(ct, 50)) * 1e3, 2),
                 "step2_p50_ms": round(float(np.percentile(cbr, 50)) * 1e3, 2),
                 "generator_p50_ms": round(float(np.percentile(cvo, 50)) * 1e3, 2),
                 "codec_p50_ms": round(float(np.percentile(ccd, 50)) * 1e3, 2),
                 "frames": n, "cores": threads, "codec_cores": 1, "kind": "port",
                 "sample": f"the first {n} frames of the same run on the oracle (C++ restatement of imi's engine, voice "
-                          "generator and codec; its 8-codebook pass tables take imi's scalar generic order; the codec "
-                          "restatement runs on one thread)",
+                          "generator with its 12-input AVX2 table order, and codec on one thread)",
             }
-            line["voice_frame"]["codes_match_cpu"] = bool(np.array_equal(ccodes, fref[3][:n]) and cids == fref[4][:n])
-            gp = fref[8][:len(cpcm)]
-            line["voice_frame"]["pcm_rel_l2_vs_cpu"] = float(
-                np.sqrt(((gp.astype(np.float64) - cpcm) ** 2).sum() / max((cpcm.astype(np.float64) ** 2).sum(), 1e-30)))
+            line["talk_frame"]["codes_match_cpu"] = bool(np.array_equal(ccodes, tref[3][:n]) and cids == tref[4][:n])
+            gp = tref[8][:len(cpcm)].astype(np.float64)
+            line["talk_frame"]["pcm_rel_l2_vs_cpu"] = float(
+                np.sqrt(((gp - cpcm) ** 2).sum() / max((cpcm.astype(np.float64) ** 2).sum(), 1e-30)))
     print(json.dumps(line), flush=True)
 
 

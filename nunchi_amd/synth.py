@@ -68,6 +68,7 @@ class VoiceShape:
 
 
 VOICE = VoiceShape()
+TALK_VOICE = VoiceShape(n_layer=3, n_cb=12)   # the generator's own shape: 12 codebooks (the codec's), 3 layers
 TINY_VOICE = VoiceShape(n_embd=256, n_layer=2, n_head=4, n_head_kv=2, head_dim=64, n_ff=512, n_vocab=256, n_cb=8,
                         n_in=256)
 

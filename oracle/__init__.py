@@ -375,10 +375,10 @@ class Codec:
         self.h = lib().orc_codec_load(path.encode())
         if not self.h:
             raise RuntimeError(f"oracle: cannot load {path}")
-        info = np.zeros(11, np.int32)
+        info = np.zeros(12, np.int32)
         lib().orc_codec_info(self.h, info)
         (self.n_embd, self.n_ff, self.n_head, self.n_head_kv, self.head_dim, self.d_conv, self.n_layer, self.n_bins,
-         self.n_lvl, self.n_q, _) = (int(v) for v in info)
+         self.n_lvl, self.n_q, _, self.n_codes) = (int(v) for v in info)
 
     def __del__(self):
         if getattr(self, "h", None):

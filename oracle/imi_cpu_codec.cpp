@@ -69,7 +69,7 @@ struct codec {
     std::vector<layer> layers;
     const float *lvl = nullptr, *qo_w = nullptr, *qo_b = nullptr, *in_b = nullptr, *out_b = nullptr, *out_norm = nullptr;
     q8gtab in_proj, out_proj;
-    int n_lvl = 0, n_cb = 12, n_embd = 0, n_ff = 0, n_head = 0, n_head_kv = 0, head_dim = 0, d_conv = 0, n_q = 0;
+    int n_codes = 0, n_lvl = 0, n_cb = 12, n_embd = 0, n_ff = 0, n_head = 0, n_head_kv = 0, head_dim = 0, d_conv = 0, n_q = 0;
     int n_fs = 6, window = 30, n_fft = 1280, hop = 320, n_bins = 641;
     float eps = 1e-5f, theta = 1e6f;
     // carried state
@@ -96,7 +96,7 @@ bool codec::load(const std::string& path) {   // imi/core/codec.cpp:41-108
     const gtensor* ip = f.get(g + "tfm.in_proj.weight");
     const gtensor* op = f.get(g + "tfm.out_proj.weight");
     if (!cb || !ip || !op) { fprintf(stderr, "oracle: codec tensor missing\n"); return false; }
-    lvl = f32(cb); n_lvl = (int)cb->ne[0];
+    lvl = f32(cb); n_lvl = (int)cb->ne[0]; n_codes = (int)cb->ne[1];
     qo_w = f32(f.get(g + "quant.first.out_proj.weight")); qo_b = f32(f.get(g + "quant.first.out_proj.bias"));
     in_b = f32(f.get(g + "tfm.in_proj.bias")); out_b = f32(f.get(g + "tfm.out_proj.bias"));
     out_norm = f32(f.get(g + "tfm.output_norm.weight"));
@@ -327,11 +327,11 @@ void* orc_codec_load(const char* path) {
     return c;
 }
 void orc_codec_free(void* h) { delete (codec*)h; }
-// n_embd, n_ff, n_head, n_head_kv, head_dim, d_conv, n_layer, n_bins, n_lvl, n_q, pos
+// n_embd, n_ff, n_head, n_head_kv, head_dim, d_conv, n_layer, n_bins, n_lvl, n_q, pos, n_codes
 void orc_codec_info(void* h, int* o) {
     auto* c = (codec*)h;
-    const int v[11] = {c->n_embd, c->n_ff, c->n_head, c->n_head_kv, c->head_dim, c->d_conv, (int)c->layers.size(),
-                       c->n_bins, c->n_lvl, c->n_q, c->pos};
+    const int v[12] = {c->n_embd, c->n_ff, c->n_head, c->n_head_kv, c->head_dim, c->d_conv, (int)c->layers.size(),
+                       c->n_bins, c->n_lvl, c->n_q, c->pos, c->n_codes};
     memcpy(o, v, sizeof(v));
 }
 void orc_codec_reset(void* h) { ((codec*)h)->reset(); }

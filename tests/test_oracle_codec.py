@@ -47,6 +47,8 @@ def test_ifft_matches_numpy_on_random_spectra():
 
 
 def test_stream_lengths(tiny_codec):
+    from nunchi_amd import synth
+    assert oracle.Codec(tiny_codec).n_codes == synth.TINY_CODEC.n_codes
     parts, tail = _decode(tiny_codec, np.random.default_rng(0).integers(0, 64, (3, 12)))
     assert [len(p) for p in parts] == [1440, 1920, 1920] and len(tail) == 480
 
