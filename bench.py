@@ -340,6 +340,9 @@ def main():
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the hearing-window prefills (--prefill-reps timed after one untimed): the launches a "
                          "kernel trace or counter run of the prefill reads")
+    ap.add_argument("--codec-only", type=int, default=0, metavar="FRAMES",
+                    help="only FRAMES codec frames (seeded codes, after 4 untimed), no brain: the launches a kernel "
+                         "trace of the codec reads")
     ap.add_argument("--counters-workload", action="store_true",
                     help="only the launches the hardware-counter runs read: a streaming kernel of known size (the "
                          "exponential over 16 Mi floats: 64 MiB read, 64 MiB written), 64 read-only GEMVs of known "
@@ -356,6 +359,18 @@ def main():
 
     import nunchi_amd
     from nunchi_amd import synth
+    if args.codec_only:
+        codec = nunchi_amd.Codec(synth.cached("codec", synth.CODEC, 2))
+        codes = np.random.default_rng(5).integers(0, codec.info.n_codes, (args.codec_only + 4, 12))
+        ts = []
+        for i, cc in enumerate(codes):
+            t0 = time.perf_counter()
+            codec.frame(cc)
+            if i >= 4:
+                ts.append(time.perf_counter() - t0)
+        print(json.dumps({"codec_only": {"frames": len(ts), "p50_ms": round(float(np.percentile(ts, 50)) * 1e3, 3),
+                                         "table_bytes": int(codec.info.table_bytes)}}), flush=True)
+        return
     path = synth.cached("brain", synth.SEOUL, 0)
     brain = nunchi_amd.Brain(path, n_ctx=N_CTX)
     if args.counters_workload:
