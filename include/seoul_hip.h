@@ -15,6 +15,7 @@
  *   imi_q4 table reads              imi/core/tables.h:103-138
  *   imi_voice generator             imi/core/voice.h:17-51
  *   imi_codec decoder               imi/core/codec.h:17-65
+ *   imi_ears audio encoder          imi/core/ears.h:17-51, imi_wg tables imi/core/tables.h:84-95
  */
 #ifndef SEOUL_HIP_H
 #define SEOUL_HIP_H
@@ -41,6 +42,7 @@ typedef struct sh_q4 sh_q4;         /* one Q4_0 table on the device (kernel-leve
 typedef struct sh_voice sh_voice;   /* the Q8_0 voice generator on the device */
 typedef struct sh_file sh_file;     /* one GGUF file read into host memory (imi_file) */
 typedef struct sh_codec sh_codec;   /* the codec decoder on the device (codes -> 24 kHz samples) */
+typedef struct sh_ears sh_ears;     /* the ears (audio encoder) on the device (16 kHz samples -> prefill rows) */
 
 typedef struct {
     int n_embd, n_vocab, n_head, n_head_kv, head_dim, n_ff, d_conv, n_ctx, n_layer, n_attn, n_swa;
@@ -71,6 +73,27 @@ int sh_codec_reset(sh_codec* c);
 int sh_codec_frame(sh_codec* c, const int32_t* codes, float* pcm, int* n_out);
 /* The end of speech (codec.cpp:271-277): the tail the overlap holds back, 480 samples; then a reset. */
 int sh_codec_flush(sh_codec* c, float* pcm, int* n_out);
+
+/* ---- ears (audio encoder): imi_ears::load / encode (imi/core/ears.h:17-51) ---- */
+typedef struct {
+    int n_mel, n_ch, n_embd, n_ff, n_head, n_head_kv, head_dim, window, n_out, d_conv, n_layer;
+    long long table_bytes;          /* float table bytes (F16 / F32 as in the file, plus the 402 x 400 DFT) */
+} sh_ears_shape;
+
+/* Read a GGUF ears file ("a.conv1d.*" F32 downsampler, "a.pre_encode.out", "a.blk.N.*" layers of short conv or
+ * windowed attention on F16 / F32 tables, "a.post_ln", "mm.a.mlp.*" projector; keys clip.audio.num_mel_bins,
+ * window_size, attention.head_count, attention.layer_norm_epsilon) onto `device` (imi/core/ears.cpp:40-138).
+ * n_mel a multiple of 8, n_embd a multiple of 32 up to 4096, head_dim a multiple of 32 up to 128, window 1 to 64. */
+int sh_ears_load(int device, const char* gguf_path, sh_ears** out);
+int sh_ears_free(sh_ears* e);
+int sh_ears_info(const sh_ears* e, sh_ears_shape* out);
+/* Positions and mel frames a clip of n_samples gives (ears.cpp:203-205); either pointer may be null. */
+int sh_ears_positions(const sh_ears* e, int n_samples, int* n_pos, int* n_frames);
+/* imi_ears::encode (ears.cpp:198-407): 16 kHz samples from the clip's start -> out [n_pos][n_out] (host memory,
+ * room for sh_ears_positions' count). Blocking. */
+int sh_ears_encode(sh_ears* e, const float* pcm, int n_samples, float* out, int* n_pos);
+/* The last encode's mel frames [n_frames][n_mel] (imi_ears::last_mel), into host memory. */
+int sh_ears_mel(const sh_ears* e, float* mel, int* n_frames);
 
 /* ---- GGUF file: imi_file::load / get / key_i / key_f / keep / drop_data (imi/model.h:12-36) ---- */
 /* The ggml_tensor fields imi's callers read. name points into the file object; data is the tensor's bytes in host

@@ -28,6 +28,7 @@ EXPORTS = [
     "sh_file_load", "sh_file_free", "sh_file_get", "sh_file_key_i", "sh_file_key_f", "sh_file_keep", "sh_file_drop_data",
     "sh_file_n_tensors", "sh_file_tensor", "sh_file_key_arr", "sh_file_block",
     "sh_codec_load", "sh_codec_free", "sh_codec_info", "sh_codec_reset", "sh_codec_frame", "sh_codec_flush",
+    "sh_ears_load", "sh_ears_free", "sh_ears_info", "sh_ears_positions", "sh_ears_encode", "sh_ears_mel",
 ]
 
 
@@ -54,6 +55,11 @@ class VoiceShape(C.Structure):
 class CodecShape(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("n_embd", "n_ff", "n_head", "n_head_kv", "head_dim", "d_conv", "n_layer", "n_bins",
                                        "n_lvl", "n_q", "n_codes")] + [("table_bytes", C.c_longlong)]
+
+
+class EarsShape(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("n_mel", "n_ch", "n_embd", "n_ff", "n_head", "n_head_kv", "head_dim", "window",
+                                       "n_out", "d_conv", "n_layer")] + [("table_bytes", C.c_longlong)]
 
 
 class Tensor(C.Structure):
@@ -130,6 +136,12 @@ def load_library(path: str = LIB_PATH):
         "sh_codec_reset": (i, [vp]),
         "sh_codec_frame": (i, [vp, vp, vp, P(i)]),
         "sh_codec_flush": (i, [vp, vp, P(i)]),
+        "sh_ears_load": (i, [i, C.c_char_p, P(vp)]),
+        "sh_ears_free": (i, [vp]),
+        "sh_ears_info": (i, [vp, P(EarsShape)]),
+        "sh_ears_positions": (i, [vp, i, P(i), P(i)]),
+        "sh_ears_encode": (i, [vp, vp, i, vp, P(i)]),
+        "sh_ears_mel": (i, [vp, vp, P(i)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -494,6 +506,47 @@ class Codec:
         n = C.c_int()
         _check(_lib.sh_codec_flush(self.h, _p(out), C.byref(n)))
         return out[:n.value]
+
+
+class Ears:
+    """The ears (audio encoder) on the device, shaped like imi_ears (imi/core/ears.h:17-51): encode(16 kHz samples)
+    -> [positions][n_out] rows for the brain's prefill; mel() -> the last encode's [frames][n_mel] log-mel frames."""
+
+    def __init__(self, path: str, device: int = 0):
+        L = load_library()
+        self.h = C.c_void_p()
+        _check(L.sh_ears_load(int(device), path.encode(), C.byref(self.h)))
+        self.info = EarsShape()
+        _check(L.sh_ears_info(self.h, C.byref(self.info)))
+
+    def close(self):
+        if getattr(self, "h", None) and self.h.value:
+            _lib.sh_ears_free(self.h)
+            self.h = C.c_void_p()
+
+    def __del__(self):
+        self.close()
+
+    def positions(self, n: int):
+        p, f = C.c_int(), C.c_int()
+        _check(_lib.sh_ears_positions(self.h, int(n), C.byref(p), C.byref(f)))
+        return p.value, f.value
+
+    def encode(self, pcm) -> np.ndarray:
+        pcm = np.ascontiguousarray(pcm, np.float32)
+        P, _ = self.positions(len(pcm))
+        out = np.zeros((P, self.info.n_out), np.float32)
+        n = C.c_int()
+        _check(_lib.sh_ears_encode(self.h, _p(pcm), len(pcm), _p(out), C.byref(n)))
+        assert n.value == P
+        return out
+
+    def mel(self, n_samples: int) -> np.ndarray:
+        _, F = self.positions(n_samples)
+        m = np.zeros((F, self.info.n_mel), np.float32)
+        n = C.c_int()
+        _check(_lib.sh_ears_mel(self.h, _p(m), C.byref(n)))
+        return m[:n.value]
 
 
 _live_voices = weakref.WeakSet()

@@ -1,0 +1,417 @@
+// Kernels of the ears (imi/core/ears.cpp:198-407) for gfx950. Every fp32 operation is the one the oracle
+// restatement of imi's ears performs, in the same order; the exceptions are the C library's erff (GELU) and the
+// double log10 of the mel, here the device's routines.
+//
+// The float tables run on the VALU in imi_wg_group12's order (imi/core/tables.cpp:522-556): one chain
+// acc = fma(w, x, acc) per row and position over the columns in order. A workgroup is 64 rows (one per lane) by
+// 4 waves x 4 positions: the 4 waves read the same weights (the second to fourth mostly from the L1), each lane
+// keeps 4 independent chains, a wave's 4 inputs per column are staged in LDS 128 columns at a time (one chunk
+// ahead) and read back as one broadcast 16-byte word, and each lane keeps 8 weight loads in flight.
+#include "sh_ears.h"
+#include "sh_device.h"
+
+namespace sh {
+namespace {
+
+constexpr int ET = 256;
+
+__device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }
+
+
+// 8 columns of one row, raw: F16 bits (one 16-byte load) or F32 (two)
+template <bool F32W> struct wraw;
+template <> struct wraw<false> { uint4 a; };
+template <> struct wraw<true> { float4 a, b; };
+
+template <bool F32W>
+__device__ __forceinline__ wraw<F32W> wload(const void* w, size_t at) {
+    wraw<F32W> r;
+    if constexpr (F32W) {
+        const float4* p = static_cast<const float4*>(w) + at * 2;
+        r.a = p[0];
+        r.b = p[1];
+    } else {
+        r.a = static_cast<const uint4*>(w)[at];
+    }
+    return r;
+}
+template <bool F32W>
+__device__ __forceinline__ void wconv(const wraw<F32W>& r, float (&o)[8]) {
+    if constexpr (F32W) {
+        o[0] = r.a.x; o[1] = r.a.y; o[2] = r.a.z; o[3] = r.a.w; o[4] = r.b.x; o[5] = r.b.y; o[6] = r.b.z; o[7] = r.b.w;
+    } else {
+        const unsigned v[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            o[2 * i] = h2f((uint16_t)(v[i] & 0xffffu));
+            o[2 * i + 1] = h2f((uint16_t)(v[i] >> 16));
+        }
+    }
+}
+
+template <int EPI, bool F32W>
+__global__ __launch_bounds__(ET) void k_etab(etab_args a) {
+    constexpr int KC = 128;   // columns of a wave's inputs staged per chunk (double-buffered in LDS)
+    constexpr int DW = 8;     // weight loads in flight, in 8-column steps
+    __shared__ float4 xs[ET / 64][2][KC];
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = blockIdx.x * 64 + lane, p0 = (blockIdx.y * 4 + wv) * EA_NP;
+    const int rp = a.W.rows_pad, K = a.W.cols, nk8 = K >> 3, nch = (K + KC - 1) / KC;
+    const size_t ldx = (size_t)a.ldx;
+    const int rr = r < rp ? r : rp - 1;   // lanes past the table read its last row (straight-line loads, nothing stored)
+    const float* xg = a.x + p0;
+    float4 st[KC / 64];
+    // every load below is unconditional (indices clamped into the buffers, values selected afterwards), so the
+    // compiler's wait counts stay exact and the weight ring really keeps DW loads in flight
+    auto gload = [&](int c) {
+#pragma unroll
+        for (int i = 0; i < KC / 64; i++) {
+            const int k = c * KC + lane + 64 * i, kk = k < K ? k : K - 1;
+            const float4 v = *reinterpret_cast<const float4*>(xg + (size_t)kk * ldx);
+            st[i] = k < K ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
+    auto lstore = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < KC / 64; i++) xs[wv][b][lane + 64 * i] = st[i];
+    };
+    gload(0);
+    wraw<F32W> wq[DW];
+#pragma unroll
+    for (int i = 0; i < DW; i++) wq[i] = wload<F32W>(a.W.w, (size_t)(i < nk8 ? i : nk8 - 1) * rp + rr);
+    lstore(0);
+    __builtin_amdgcn_wave_barrier();
+    float acc[EA_NP] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c = 0; c < nch; c++) {
+        gload(c + 1 < nch ? c + 1 : c);   // in flight while chunk c runs (the last chunk reloads itself, unused)
+        const float4* xc = xs[wv][c & 1];
+        const int kb0 = c * (KC / 8);
+#pragma unroll
+        for (int u = 0; u < KC / 8; u++) {   // kb = kb0 + u; the ring slot u % DW is static (KC / 8 is a multiple of DW)
+            const int kb = kb0 + u, kn = kb + DW < nk8 ? kb + DW : nk8 - 1;
+            float w[8];
+            wconv<F32W>(wq[u % DW], w);
+            wq[u % DW] = wload<F32W>(a.W.w, (size_t)kn * rp + rr);
+            if (kb < nk8) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float4 xv = xc[8 * u + j];
+                    acc[0] = fmaf(w[j], xv.x, acc[0]);
+                    acc[1] = fmaf(w[j], xv.y, acc[1]);
+                    acc[2] = fmaf(w[j], xv.z, acc[2]);
+                    acc[3] = fmaf(w[j], xv.w, acc[3]);
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        lstore((c + 1) & 1);
+        __builtin_amdgcn_wave_barrier();
+    }
+    if constexpr (EPI == EE_GLU || EPI == EE_POWER) {
+        constexpr int MASK = EPI == EE_GLU ? 8 : 1;
+        float o[EA_NP];
+#pragma unroll
+        for (int p = 0; p < EA_NP; p++) {
+            const float other = __shfl_xor(acc[p], MASK);
+            o[p] = EPI == EE_GLU ? silu(acc[p]) * other : fmaf(acc[p], acc[p], other * other);
+        }
+        const bool first = EPI == EE_GLU ? (r & 8) == 0 : (r & 1) == 0;
+        const int ro = EPI == EE_GLU ? (r >> 4) * 8 + (r & 7) : r >> 1;
+        if (first && ro < a.W.rows / 2) {
+            if (a.xt_out) {
+                *reinterpret_cast<float4*>(a.out + (size_t)ro * a.ldo + p0) = make_float4(o[0], o[1], o[2], o[3]);
+            } else {
+#pragma unroll
+                for (int p = 0; p < EA_NP; p++)
+                    if (p0 + p < a.P) a.out[(size_t)(p0 + p) * a.ldo + ro] = o[p];
+            }
+        }
+    } else {
+        if (r >= a.W.rows) return;
+        const float b = a.bias ? a.bias[r] : 0.0f;
+        float o[EA_NP];
+#pragma unroll
+        for (int p = 0; p < EA_NP; p++) {
+            const float v = acc[p] + b;
+            o[p] = EPI == EE_SILU ? silu(v) : EPI == EE_GELU ? gelu_erf(v) : v;
+        }
+        if (a.xt_out) {
+            float4* dst = reinterpret_cast<float4*>(a.out + (size_t)r * a.ldo + p0);
+            if constexpr (EPI == EE_ADD) {
+                const float4 c = *dst;
+                *dst = make_float4(c.x + o[0], c.y + o[1], c.z + o[2], c.w + o[3]);
+            } else {
+                *dst = make_float4(o[0], o[1], o[2], o[3]);
+            }
+        } else {
+#pragma unroll
+            for (int p = 0; p < EA_NP; p++) {
+                if (p0 + p >= a.P) break;
+                float* d = a.out + (size_t)(p0 + p) * a.ldo + r;
+                *d = EPI == EE_ADD ? *d + o[p] : o[p];
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(ET) void k_eframes(const float* pcm, int n, const float* hann, int n_fft, int hop,
+                                                int n_fr, float* fx, int ldf) {
+    const int fr = blockIdx.x * ET + threadIdx.x, k = blockIdx.y;
+    if (fr >= ldf) return;
+    const long i = (long)fr * hop + k;
+    fx[(size_t)k * ldf + fr] = fr < n_fr && i < n ? hann[k] * pcm[i] : 0.0f;
+}
+
+__global__ __launch_bounds__(ET) void k_emel(const float* pw, int ldp, const float* fb, int n_bin, int n_mel, int n_fr,
+                                             float* mel) {
+    const int fr = blockIdx.x * ET + threadIdx.x, m = blockIdx.y;
+    if (fr >= n_fr) return;
+    const float* w = fb + (size_t)m * n_bin;
+    double s = 0.0;
+    for (int b = 0; b < n_bin; b++) s = fma((double)w[b], (double)pw[(size_t)b * ldp + fr], s);
+    mel[(size_t)fr * n_mel + m] = (float)((log10(s < 1e-12 ? 1e-12 : s) + 4.0) / 4.0);
+}
+
+__global__ __launch_bounds__(ET) void k_econv0(const float* mel, int n_fr, int n_mel, const float* w9, const float* b,
+                                               int C, int T2, int F2, float* a0) {
+    const long idx = (long)blockIdx.x * ET + threadIdx.x;
+    if (idx >= (long)C * T2 * F2) return;
+    const int f = (int)(idx % F2), t = (int)((idx / F2) % T2), c = (int)(idx / ((long)F2 * T2));
+    float o = b[c];
+    for (int kh = 0; kh < 3; kh++)
+        for (int kw = 0; kw < 3; kw++) {
+            const int ti = 2 * t + kw - 1, fi = 2 * f + kh - 1;
+            if (ti < 0 || ti >= n_fr || fi < 0 || fi >= n_mel) continue;
+            o = fmaf(mel[(size_t)ti * n_mel + fi], w9[(size_t)(kh * 3 + kw) * C + c], o);
+        }
+    a0[idx] = silu(o);
+}
+
+__global__ __launch_bounds__(ET) void k_edw(const float* in, int Ti, int Fi, int ldi, const float* w9, const float* b,
+                                            int C, int To, int Fo, float* out, int ldo) {
+    const long idx = (long)blockIdx.x * ET + threadIdx.x;
+    if (idx >= (long)C * To * Fo) return;
+    const int f = (int)(idx % Fo), t = (int)((idx / Fo) % To), c = (int)(idx / ((long)Fo * To));
+    const float* src = in + (size_t)c * ldi;
+    float o = b[c];
+    for (int kh = 0; kh < 3; kh++)
+        for (int kw = 0; kw < 3; kw++) {
+            const int ti = 2 * t + kw - 1, fi = 2 * f + kh - 1;
+            if (ti < 0 || ti >= Ti || fi < 0 || fi >= Fi) continue;
+            o = fmaf(src[(size_t)ti * Fi + fi], w9[(size_t)(kh * 3 + kw) * C + c], o);
+        }
+    out[(size_t)c * ldo + (size_t)t * Fo + f] = o;
+}
+
+__global__ __launch_bounds__(ET) void k_eflat(const float* a, int lda, int F8, int P, float* xf, int ldf) {
+    const int p = blockIdx.x * ET + threadIdx.x, k = blockIdx.y;
+    if (p >= ldf) return;
+    const int c = k / F8, f = k - c * F8;
+    xf[(size_t)k * ldf + p] = p < P ? a[(size_t)c * lda + (size_t)p * F8 + f] : 0.0f;
+}
+
+// one wave per position
+__global__ __launch_bounds__(ET) void k_enorm(const float* x, const float* w, int E, int P, int ldh, float eps, float* h) {
+    const int lane = threadIdx.x & 63, p = blockIdx.x * (ET / 64) + (threadIdx.x >> 6);
+    if (p >= ldh) return;
+    if (p >= P) {
+        for (int e = lane; e < E; e += 64) h[(size_t)e * ldh + p] = 0.0f;
+        return;
+    }
+    const float* xp = x + (size_t)p * E;
+    const float s = rms_scale_wave(xp, E, eps);
+    for (int e = lane; e < E; e += 64) h[(size_t)e * ldh + p] = xp[e] * s * w[e];
+}
+
+__global__ __launch_bounds__(ET) void k_econv(const float* big, int ld, const float* w, int E, int d_conv, int P,
+                                              float* act, int lda) {
+    const int e = blockIdx.x * ET + threadIdx.x, p = blockIdx.y;
+    if (e >= E) return;
+    if (p >= P) { act[(size_t)e * lda + p] = 0.0f; return; }
+    float co = 0.0f;
+    for (int k = 0; k < d_conv; k++) {
+        const int t = p - (d_conv - 1) + k;
+        if (t < 0) continue;
+        const float* rw = big + (size_t)t * ld;
+        co = fmaf(w[(size_t)k * E + e], rw[e] * rw[2 * E + e], co);
+    }
+    act[(size_t)e * lda + p] = big[(size_t)p * ld + E + e] * co;
+}
+
+// one wave per (position, head slot): the n_head query heads, then the n_kv key heads
+template <int DPL>
+__global__ __launch_bounds__(ET) void k_eqk(float* big, int ld, int n_head, int n_kv, int D, const float* q_norm,
+                                            const float* k_norm, const float2* cs, int P, float eps) {
+    __shared__ float stg[ET / 64][EA_MAX_D];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, ns = n_head + n_kv;
+    const int u = blockIdx.x * (ET / 64) + wv;
+    if (u >= P * ns) return;
+    const int p = u / ns, sl = u - p * ns;
+    float* v = big + (size_t)p * ld + (sl < n_head ? sl * D : n_head * D + (sl - n_head) * D);
+    float r[DPL];
+    head_norm_rope<DPL>(v, sl < n_head ? q_norm : k_norm, stg[wv], cs + (size_t)p * (D / 2), D, eps, r);
+#pragma unroll
+    for (int c = 0; c < DPL; c++)
+        if (lane + 64 * c < D) v[lane + 64 * c] = r[c];
+}
+
+// one wave per (position, query head): lane t < nk scores key s0 + t (fma chain over the dimensions), the exponentials
+// are summed in key order by lane 0, lane i runs dimension i's chain o = fma(e_t, v_t, o) over the keys
+__global__ __launch_bounds__(ET) void k_eattn(const float* big, int ld, int n_head, int n_kv, int D, int window, int P,
+                                              float* act, int lda) {
+    __shared__ float qs[ET / 64][EA_MAX_D];
+    __shared__ float es[ET / 64][EA_MAX_WIN];
+    __shared__ float sums[ET / 64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int u = blockIdx.x * (ET / 64) + wv;
+    if (u >= P * n_head) return;
+    const int p = u / n_head, hh = u - p * n_head, kv = hh / (n_head / n_kv);
+    const int Hq = n_head * D, Hk = n_kv * D;
+    const int s0 = p - window + 1 > 0 ? p - window + 1 : 0, nk = p - s0 + 1;
+    for (int i = lane; i < D; i += 64) qs[wv][i] = big[(size_t)p * ld + hh * D + i];
+    __builtin_amdgcn_wave_barrier();
+    const float scale = 1.0f / sqrtf((float)D);
+    float sc = -__builtin_inff();
+    if (lane < nk) {
+        const float* k = big + (size_t)(s0 + lane) * ld + Hq + kv * D;
+        float s = 0.0f;
+        for (int i = 0; i < D; i++) s = fmaf(qs[wv][i], k[i], s);
+        sc = s * scale;
+    }
+    float mx = sc;
+    for (int o = 32; o > 0; o >>= 1) {
+        const float t = __shfl_xor(mx, o);
+        mx = mx < t ? t : mx;
+    }
+    if (lane < nk) es[wv][lane] = expf_glibc(sc - mx);
+    __builtin_amdgcn_wave_barrier();
+    if (lane == 0) {
+        float sum = 0.0f;
+        for (int t = 0; t < nk; t++) sum += es[wv][t];
+        sums[wv] = sum;
+    }
+    __builtin_amdgcn_wave_barrier();
+    const float sum = sums[wv];
+    for (int i = lane; i < D; i += 64) {
+        float o = 0.0f;
+        for (int t = 0; t < nk; t++) o = fmaf(es[wv][t], big[(size_t)(s0 + t) * ld + Hq + Hk + kv * D + i], o);
+        act[(size_t)(hh * D + i) * lda + p] = o / sum;
+    }
+}
+
+// one wave per position: h = x * rms(x) * post_ln into LDS; lane 0 forms the double mean and variance in order;
+// then fma((float)(h - mu) * inv, ln_w, ln_b)
+__global__ __launch_bounds__(ET) void k_efinal(const float* x, const float* post_ln, const float* ln_w,
+                                               const float* ln_b, int E, int P, float eps, float* h, int ldh) {
+    extern __shared__ float hs_all[];
+    __shared__ double st[ET / 64][2];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, p = blockIdx.x * (ET / 64) + wv;
+    if (p >= ldh) return;
+    if (p >= P) {
+        for (int e = lane; e < E; e += 64) h[(size_t)e * ldh + p] = 0.0f;
+        return;
+    }
+    float* hs = hs_all + (size_t)wv * E;
+    const float* xp = x + (size_t)p * E;
+    const float s = rms_scale_wave(xp, E, eps);
+    for (int e = lane; e < E; e += 64) hs[e] = xp[e] * s * post_ln[e];
+    __builtin_amdgcn_wave_barrier();
+    if (lane == 0) {
+        double mu = 0.0, var = 0.0;
+        for (int k = 0; k < E; k++) mu += (double)hs[k];
+        mu /= E;
+        for (int k = 0; k < E; k++) {
+            const double d = (double)hs[k] - mu;
+            var = fma(d, d, var);
+        }
+        st[wv][0] = mu;
+        st[wv][1] = (double)(float)(1.0 / sqrt(var / E + 1e-5));
+    }
+    __builtin_amdgcn_wave_barrier();
+    const double mu = st[wv][0];
+    const float inv = (float)st[wv][1];
+    for (int e = lane; e < E; e += 64) h[(size_t)e * ldh + p] = fmaf((float)((double)hs[e] - mu) * inv, ln_w[e], ln_b[e]);
+}
+
+inline unsigned blocks(long n) { return (unsigned)((n + ET - 1) / ET); }
+
+}  // namespace
+
+hipError_t launch_etab(int epi, const etab_args& a, hipStream_t s) {
+    if (a.W.cols % 8 || a.W.rows_pad % 8 || a.ldx % 16 || (a.xt_out && a.ldo % 4) ||
+        (epi == EE_GLU && a.W.rows_pad % 16))
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((a.W.rows_pad + 63) / 64), (unsigned)(a.ldx / 16));
+#define SH_ETAB(E)                                                                                        \
+    case E:                                                                                               \
+        if (a.W.f32) hipLaunchKernelGGL((k_etab<E, true>), grid, dim3(ET), 0, s, a);                      \
+        else hipLaunchKernelGGL((k_etab<E, false>), grid, dim3(ET), 0, s, a);                             \
+        break;
+    switch (epi) {
+        SH_ETAB(EE_STORE) SH_ETAB(EE_ADD) SH_ETAB(EE_SILU) SH_ETAB(EE_GELU) SH_ETAB(EE_GLU) SH_ETAB(EE_POWER)
+        default: return hipErrorInvalidValue;
+    }
+#undef SH_ETAB
+    return hipGetLastError();
+}
+
+hipError_t launch_eframes(const float* pcm, int n, const float* hann, int n_fft, int hop, int n_fr, float* fx, int ldf,
+                          hipStream_t s) {
+    hipLaunchKernelGGL(k_eframes, dim3(blocks(ldf), n_fft), dim3(ET), 0, s, pcm, n, hann, n_fft, hop, n_fr, fx, ldf);
+    return hipGetLastError();
+}
+hipError_t launch_emel(const float* pw, int ldp, const float* fb, int n_bin, int n_mel, int n_fr, float* mel,
+                       hipStream_t s) {
+    hipLaunchKernelGGL(k_emel, dim3(blocks(n_fr), n_mel), dim3(ET), 0, s, pw, ldp, fb, n_bin, n_mel, n_fr, mel);
+    return hipGetLastError();
+}
+hipError_t launch_econv0(const float* mel, int n_fr, int n_mel, const float* w9, const float* b, int C, float* a0,
+                         hipStream_t s) {
+    const int T2 = (n_fr + 1) / 2, F2 = n_mel / 2;
+    hipLaunchKernelGGL(k_econv0, dim3(blocks((long)C * T2 * F2)), dim3(ET), 0, s, mel, n_fr, n_mel, w9, b, C, T2, F2, a0);
+    return hipGetLastError();
+}
+hipError_t launch_edw(const float* in, int Ti, int Fi, int ldi, const float* w9, const float* b, int C, float* out,
+                      int ldo, hipStream_t s) {
+    const int To = (Ti + 1) / 2, Fo = Fi / 2;
+    hipLaunchKernelGGL(k_edw, dim3(blocks((long)C * To * Fo)), dim3(ET), 0, s, in, Ti, Fi, ldi, w9, b, C, To, Fo, out, ldo);
+    return hipGetLastError();
+}
+hipError_t launch_eflat(const float* a, int lda, int C, int F8, int P, float* xf, int ldf, hipStream_t s) {
+    hipLaunchKernelGGL(k_eflat, dim3(blocks(ldf), C * F8), dim3(ET), 0, s, a, lda, F8, P, xf, ldf);
+    return hipGetLastError();
+}
+hipError_t launch_enorm(const float* x, const float* w, int E, int P, float eps, float* h, int ldh, hipStream_t s) {
+    if (E % 32) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_enorm, dim3((unsigned)((ldh + 3) / 4)), dim3(ET), 0, s, x, w, E, P, ldh, eps, h);
+    return hipGetLastError();
+}
+hipError_t launch_econv(const float* big, int ld, const float* w, int E, int d_conv, int P, float* act, int lda,
+                        hipStream_t s) {
+    hipLaunchKernelGGL(k_econv, dim3(blocks(E), lda), dim3(ET), 0, s, big, ld, w, E, d_conv, P, act, lda);
+    return hipGetLastError();
+}
+hipError_t launch_eqk(float* big, int ld, int n_head, int n_kv, int D, const float* q_norm, const float* k_norm,
+                      const float2* cs, int P, float eps, hipStream_t s) {
+    if (D % 32 || D > EA_MAX_D) return hipErrorInvalidValue;
+    const unsigned g = (unsigned)(((long)P * (n_head + n_kv) + 3) / 4);
+    if (D > 64) hipLaunchKernelGGL((k_eqk<2>), dim3(g), dim3(ET), 0, s, big, ld, n_head, n_kv, D, q_norm, k_norm, cs, P, eps);
+    else hipLaunchKernelGGL((k_eqk<1>), dim3(g), dim3(ET), 0, s, big, ld, n_head, n_kv, D, q_norm, k_norm, cs, P, eps);
+    return hipGetLastError();
+}
+hipError_t launch_eattn(const float* big, int ld, int n_head, int n_kv, int D, int window, int P, float* act, int lda,
+                        hipStream_t s) {
+    if (D > EA_MAX_D || window < 1 || window > EA_MAX_WIN) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_eattn, dim3((unsigned)(((long)P * n_head + 3) / 4)), dim3(ET), 0, s, big, ld, n_head, n_kv, D,
+                       window, P, act, lda);
+    return hipGetLastError();
+}
+hipError_t launch_efinal(const float* x, const float* post_ln, const float* ln_w, const float* ln_b, int E, int P,
+                         float eps, float* h, int ldh, hipStream_t s) {
+    if (E % 32 || E > 4096) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_efinal, dim3((unsigned)((ldh + 3) / 4)), dim3(ET), (size_t)4 * E * sizeof(float), s, x, post_ln,
+                       ln_w, ln_b, E, P, eps, h, ldh);
+    return hipGetLastError();
+}
+
+}  // namespace sh

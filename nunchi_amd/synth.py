@@ -18,7 +18,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from .gguf import GGUFWriter, Q4_0_BLOCK, Q4_1_BLOCK, Q6_K_BLOCK, Q8_0_BLOCK, T_F32, T_Q4_0, T_Q4_1, T_Q6_K, T_Q8_0
+from .gguf import GGUFWriter, Q4_0_BLOCK, Q4_1_BLOCK, Q6_K_BLOCK, Q8_0_BLOCK, T_F16, T_F32, T_Q4_0, T_Q4_1, T_Q6_K, T_Q8_0
 
 
 @dataclass
@@ -305,6 +305,102 @@ def write_codec(path: str, shape: CodecShape = CODEC, seed: int = 2) -> str:
     return path
 
 
+@dataclass
+class EarsShape:
+    n_mel: int = 128
+    n_ch: int = 256                       # downsampler channels
+    n_embd: int = 768
+    n_ff: int = 2048
+    n_head: int = 12
+    n_head_kv: int = 12
+    head_dim: int = 64
+    d_conv: int = 3
+    layers: str = "ccaccaccaccaccacc"     # 17 layers: c = short conv, a = attention over the window
+    window: int = 32
+    n_out: int = 2048                     # the brain's width
+
+
+EARS = EarsShape()
+TINY_EARS = EarsShape(n_mel=64, n_ch=16, n_embd=128, n_ff=256, n_head=4, n_head_kv=2, head_dim=32, layers="cac",
+                      window=8, n_out=256)
+
+
+def write_ears(path: str, shape: EarsShape = EARS, seed: int = 3) -> str:
+    """The ears file's tensors as imi reads them (imi/core/ears.cpp:40-138): F32 downsampler convolutions
+    (3x3 taps N(0, 0.5) for the first, N(0, 0.4) depthwise, pointwise N(0, 1/C)), F16 tables N(0, 1/cols), norms
+    1 + 0.05 N(0, 1), conv taps N(0, 0.3), biases N(0, 0.05); keys for the mel count, window, heads and eps."""
+    s = shape
+    E, D, C = s.n_embd, s.head_dim, s.n_ch
+    w = GGUFWriter()
+    w.add_str("general.architecture", "clip")
+    w.add_u32("clip.audio.num_mel_bins", s.n_mel)
+    w.add_u32("clip.audio.window_size", s.window)
+    w.add_u32("clip.audio.attention.head_count", s.n_head)
+    w.add_f32("clip.audio.attention.layer_norm_epsilon", 1e-5)
+
+    def f16(name, rows, cols):
+        v = _rng(seed, name).standard_normal((rows, cols)) / np.sqrt(cols)
+        w.add_tensor(name, T_F16, (cols, rows), v.astype(np.float16))
+
+    def f32(name, arr, ne):
+        w.add_tensor(name, T_F32, ne, np.ascontiguousarray(arr, dtype=np.float32))
+
+    def bias(name, n):
+        f32(name, 0.05 * _rng(seed, name).standard_normal(n), (n,))
+
+    f32("a.conv1d.0.weight", 0.5 * _rng(seed, "c0").standard_normal((C, 1, 3, 3)), (3, 3, 1, C))
+    bias("a.conv1d.0.bias", C)
+    for i in (2, 5):
+        f32(f"a.conv1d.{i}.weight", 0.4 * _rng(seed, f"c{i}").standard_normal((C, 1, 3, 3)), (3, 3, 1, C))
+        bias(f"a.conv1d.{i}.bias", C)
+    for i in (3, 6):
+        f32(f"a.conv1d.{i}.weight", _rng(seed, f"c{i}").standard_normal((C, C, 1, 1)) / np.sqrt(C), (1, 1, C, C))
+        bias(f"a.conv1d.{i}.bias", C)
+    f16("a.pre_encode.out.weight", E, C * s.n_mel // 8)
+    bias("a.pre_encode.out.bias", E)
+    for il, kind in enumerate(s.layers):
+        p = f"a.blk.{il}."
+        for n in ("ln1", "ln2"):
+            f32(p + n + ".weight", _norm_w(_rng(seed, p + n), E), (E,))
+        if kind == "c":
+            f32(p + "conv_dw.weight", 0.3 * _rng(seed, p + "dw").standard_normal((E, s.d_conv)), (s.d_conv, E))
+            f16(p + "conv_pw1.weight", 3 * E, E)
+            f16(p + "conv_pw2.weight", E, E)
+        else:
+            f32(p + "attn_q_norm.weight", _norm_w(_rng(seed, p + "qn"), D), (D,))
+            f32(p + "attn_k_norm.weight", _norm_w(_rng(seed, p + "kn"), D), (D,))
+            f16(p + "attn_q.weight", s.n_head * D, E)
+            f16(p + "attn_k.weight", s.n_head_kv * D, E)
+            f16(p + "attn_v.weight", s.n_head_kv * D, E)
+            f16(p + "attn_out.weight", E, s.n_head * D)
+        f16(p + "ffn_gate.weight", s.n_ff, E)
+        f16(p + "ffn_up.weight", s.n_ff, E)
+        f16(p + "ffn_down.weight", E, s.n_ff)
+    f32("a.post_ln.weight", _norm_w(_rng(seed, "post_ln"), E), (E,))
+    f32("mm.a.mlp.0.weight", _norm_w(_rng(seed, "ln_w"), E), (E,))
+    bias("mm.a.mlp.0.bias", E)
+    f16("mm.a.mlp.1.weight", s.n_out, E)
+    bias("mm.a.mlp.1.bias", s.n_out)
+    f16("mm.a.mlp.3.weight", s.n_out, s.n_out)
+    bias("mm.a.mlp.3.bias", s.n_out)
+    w.write(path)
+    return path
+
+
+def clip(n: int, seed: int = 0) -> np.ndarray:
+    """n samples at 16 kHz of a seeded stand-in for speech: a few gliding partials with a syllable-rate envelope,
+    plus low noise, within [-1, 1]."""
+    rng = np.random.default_rng(seed)
+    t = np.arange(n) / 16000.0
+    y = np.zeros(n)
+    for _ in range(6):
+        f0, glide, amp = rng.uniform(100, 3000), rng.uniform(-200, 200), rng.uniform(0.05, 0.15)
+        y += amp * np.sin(2 * np.pi * (f0 * t + 0.5 * glide * t * t / max(t[-1], 1e-9)) + rng.uniform(0, 2 * np.pi))
+    y *= 0.6 + 0.4 * np.sin(2 * np.pi * 4.0 * t + rng.uniform(0, 2 * np.pi))
+    y += 0.01 * rng.standard_normal(n)
+    return np.clip(y, -1.0, 1.0).astype(np.float32)
+
+
 def cached(kind: str, shape, seed: int, directory: str | None = None) -> str:
     """Write the model once per (kind, shape, seed) into a cache directory and return its path."""
     directory = directory or os.environ.get("NUNCHI_MODEL_DIR", "/tmp/nunchi_models")
@@ -313,6 +409,6 @@ def cached(kind: str, shape, seed: int, directory: str | None = None) -> str:
     path = os.path.join(directory, f"{kind}-{tag}.gguf")
     if not os.path.exists(path):
         tmp = f"{path}.{os.getpid()}.tmp"
-        {"brain": write_brain, "voice": write_voice, "codec": write_codec}[kind](tmp, shape, seed)
+        {"brain": write_brain, "voice": write_voice, "codec": write_codec, "ears": write_ears}[kind](tmp, shape, seed)
         os.replace(tmp, path)
     return path

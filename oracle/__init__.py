@@ -92,6 +92,12 @@ def lib():
         "orc_codec_frame": (i, [vp, _i32p, _f32p, vp]),
         "orc_codec_flush": (i, [vp, _f32p]),
         "orc_ifft": (None, [_f32p, _f32p, i, _f32p, _f32p]),
+        "orc_ears_load": (vp, [C.c_char_p, i]),
+        "orc_ears_free": (None, [vp]),
+        "orc_ears_info": (None, [vp, _i32p]),
+        "orc_ears_positions": (i, [vp, i]),
+        "orc_ears_frames": (i, [vp, i]),
+        "orc_ears_encode": (i, [vp, _f32p, i, _f32p, vp, C.POINTER(C.c_double)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -425,3 +431,37 @@ def top(a) -> int:
     if a.size == 0 or np.isnan(a[0]):
         return 0
     return int(np.argmax(np.where(np.isnan(a), -np.inf, a)))
+
+
+class Ears:
+    """imi_ears restated (imi/core/ears.h:17-51): encode(16 kHz samples) -> [positions][n_out] rows for the brain's
+    prefill (and, with mel=True, the [frames][n_mel] log-mel frames the encoder read)."""
+
+    def __init__(self, path: str, threads: int = 4):
+        self.h = lib().orc_ears_load(path.encode(), int(threads))
+        if not self.h:
+            raise RuntimeError(f"oracle: cannot load ears from {path}")
+        info = np.zeros(11, np.int32)
+        lib().orc_ears_info(self.h, info)
+        (self.n_mel, self.n_ch, self.n_embd, self.n_ff, self.n_head, self.n_head_kv, self.head_dim, self.window,
+         self.n_out, self.d_conv, self.n_layer) = (int(v) for v in info)
+        self.secs = 0.0
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().orc_ears_free(self.h)
+            self.h = None
+
+    def positions(self, n: int) -> int:
+        return int(lib().orc_ears_positions(self.h, int(n)))
+
+    def encode(self, pcm, mel: bool = False):
+        pcm = np.ascontiguousarray(pcm, np.float32)
+        out = np.zeros((self.positions(len(pcm)), self.n_out), np.float32)
+        m = np.zeros((lib().orc_ears_frames(self.h, len(pcm)), self.n_mel), np.float32) if mel else None
+        secs = C.c_double(0)
+        P = lib().orc_ears_encode(self.h, pcm, len(pcm), out, _ptr(m), C.byref(secs))
+        assert P == out.shape[0]
+        self.secs = secs.value
+        return (out, m) if mel else out
+

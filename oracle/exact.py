@@ -1,7 +1,8 @@
-"""ORACLE — test infrastructure only. Float64 "truth key" of the brain, the voice generator and the codec.
+"""ORACLE — test infrastructure only. Float64 "truth key" of the brain, the voice generator, the codec and the ears.
 
-Restates imi/ref/ref_exact.py:37-87 (brain), imi/ref/gen_exact.py:27-54 (voice generator) and
-imi/ref/codec_exact.py:23-72 (codec, whole-sequence form with numpy's inverse real FFT): the file's own
+Restates imi/ref/ref_exact.py:37-87 (brain), imi/ref/gen_exact.py:27-54 (voice generator),
+imi/ref/codec_exact.py:23-72 (codec, whole-sequence form with numpy's inverse real FFT) and
+imi/ref/ears_exact.py:16-102 (ears, the mel with numpy's real FFT): the file's own
 dequantized weights, run in float64 with no input rounding. Used to pin the int8-cut restatement (liboracle) at the
 model level: a dropped term, a wrong sign or a transposed table moves it far outside the cut's error.
 Dequantization is written here from the GGUF block formats (closed forms), not shared with the product code.
@@ -287,3 +288,138 @@ def codec(path: str, codes, eps=1e-5, win=30, theta=1e6, n_fft=1280, hop=320):
     pcm = np.where(ws > 1e-8, ola / np.maximum(ws, 1e-30), ola)
     pad = (n_fft - hop) // 2
     return pcm[pad:pad + N * hop], out
+
+
+def ears(path: str, pcm, window: int | None = None, theta: float = 1e6, eps: float = 1e-5, mel_only: bool = False):
+    """Rows [positions][n_out] for 16 kHz samples in float64, as imi/ref/ears_exact.py:16-102 computes them: 400-sample
+    periodic Hann frames every 160 samples, |rfft|^2, Slaney mel filters, (log10 + 4) / 4; three stride-2 3x3
+    convolutions over [time][freq] with zero edges (SiLU; pointwise tables after the two depthwise ones); the
+    pre_encode projection of feature c * F8 + f; the causal layers (pre-norm short conv over b * x, or attention over
+    the last `window` positions with q/k norms and rope); the last norm, LayerNorm, GELU (erf) projector. `window`
+    and `theta` may be overridden to show what the comparison sees. Returns (rows, mel)."""
+    import math
+    f = GGUFFile(path)
+    W = Weights(path)
+    n_mel = int(f.key("clip.audio.num_mel_bins", 128))
+    win_n, hop, sr = 400, 160, 16000
+    y0 = np.asarray(pcm, np.float64)
+    n = len(y0)
+    n_pad = win_n if n <= win_n else n + (hop - (n - win_n) % hop) % hop
+    y = np.zeros(n_pad)
+    y[:n] = y0
+    n_fr = (n_pad - win_n) // hop + 1
+    hann = 0.5 * (1 - np.cos(2 * np.pi * np.arange(win_n) / win_n))
+    frames = np.stack([y[i * hop:i * hop + win_n] * hann for i in range(n_fr)])
+    spec = np.abs(np.fft.rfft(frames, win_n)) ** 2
+    lin, min_log_mel, step = 3 / 200, 15.0, math.log(6.4) / 27
+
+    def hz2mel(v):
+        return v * lin if v < 1000 else min_log_mel + math.log(v / 1000) / step
+
+    def mel2hz(m):
+        return m / lin if m < min_log_mel else 1000 * math.exp((m - min_log_mel) * step)
+
+    lo, hi = hz2mel(0.0), hz2mel(sr / 2)
+    pts = [mel2hz(lo + (hi - lo) * i / (n_mel + 1)) for i in range(n_mel + 2)]
+    freqs = np.arange(win_n // 2 + 1) * sr / win_n
+    fb = np.zeros((n_mel, win_n // 2 + 1))
+    for m in range(n_mel):
+        fl, fc, fr = pts[m:m + 3]
+        up = (freqs >= fl) & (freqs <= fc)
+        down = (freqs > fc) & (freqs <= fr)
+        fb[m, up] = (freqs[up] - fl) / (fc - fl)
+        fb[m, down] = (fr - freqs[down]) / (fr - fc)
+        fb[m] *= 2 / (fr - fl)
+    mel = (np.log10(np.maximum(spec @ fb.T, 1e-12)) + 4) / 4
+    if mel_only:
+        return None, mel
+
+    def conv_s2(a, w, b, depthwise):   # a [T][F][C]; w [oc][ic][kh][kw], kw along time
+        t_n, f_n, c_n = a.shape
+        to, fo = (t_n + 1) // 2, (f_n + 1) // 2
+        p = np.zeros((t_n + 2, f_n + 2, c_n))
+        p[1:t_n + 1, 1:f_n + 1] = a
+        out = np.zeros((to, fo, w.shape[0]))
+        for kh in range(3):
+            for kw in range(3):
+                patch = p[kw:kw + 2 * to:2, kh:kh + 2 * fo:2]
+                out += patch * w[:, 0, kh, kw] if depthwise else patch[..., :1] * w[:, 0, kh, kw]
+        return out + b.reshape(-1)
+
+    def silu(v):
+        return v / (1 + np.exp(-v))
+
+    def cw(name):
+        w = W(name)
+        return w.reshape(-1, 1, 3, 3)
+
+    def pw(a, name, bname):
+        w = W(name)
+        c = int(round(math.sqrt(w.size)))
+        return a @ w.reshape(c, c).T + W(bname).reshape(-1)
+
+    a = silu(conv_s2(mel[:, :, None], cw("a.conv1d.0.weight"), W("a.conv1d.0.bias"), False))
+    a = silu(pw(conv_s2(a, cw("a.conv1d.2.weight"), W("a.conv1d.2.bias"), True), "a.conv1d.3.weight", "a.conv1d.3.bias"))
+    a = silu(pw(conv_s2(a, cw("a.conv1d.5.weight"), W("a.conv1d.5.bias"), True), "a.conv1d.6.weight", "a.conv1d.6.bias"))
+    N = a.shape[0]
+    x = a.transpose(0, 2, 1).reshape(N, -1) @ W("a.pre_encode.out.weight").T + W("a.pre_encode.out.bias")
+    window = int(f.key("clip.audio.window_size", 32)) if window is None else window
+
+    def norm(v, w):
+        return v / np.sqrt((v * v).mean(-1, keepdims=True) + eps) * w
+
+    def rope(v, D):
+        half = D // 2
+        inv = theta ** (-np.arange(half) * 2.0 / D)
+        ang = np.arange(N)[:, None] * inv[None]
+        c, s_ = np.cos(ang)[:, None], np.sin(ang)[:, None]
+        p0, p1 = v[..., :half], v[..., half:]
+        return np.concatenate([p0 * c - p1 * s_, p0 * s_ + p1 * c], -1)
+
+    il = 0
+    while W.has(f"a.blk.{il}.ln1.weight"):
+        p = f"a.blk.{il}."
+        h = norm(x, W(p + "ln1.weight"))
+        E = x.shape[1]
+        if W.has(p + "conv_dw.weight"):
+            bcx = h @ W(p + "conv_pw1.weight").T
+            b, c, xx = bcx[:, :E], bcx[:, E:2 * E], bcx[:, 2 * E:]
+            w_dw = W(p + "conv_dw.weight")
+            K = w_dw.shape[1]
+            bx = np.concatenate([np.zeros((K - 1, E)), b * xx])
+            co = np.stack([(bx[t:t + K] * w_dw.T).sum(0) for t in range(N)])
+            yv = (c * co) @ W(p + "conv_pw2.weight").T
+        else:
+            qn = W(p + "attn_q_norm.weight")
+            D = qn.shape[0]
+            q = (h @ W(p + "attn_q.weight").T).reshape(N, -1, D)
+            k = (h @ W(p + "attn_k.weight").T).reshape(N, -1, D)
+            v = (h @ W(p + "attn_v.weight").T).reshape(N, -1, D)
+            H, Hk = q.shape[1], k.shape[1]
+            q, k = rope(norm(q, qn), D), rope(norm(k, W(p + "attn_k_norm.weight")), D)
+            att = np.zeros((N, H, D))
+            grp = H // Hk
+            for t in range(N):
+                s0 = max(0, t - window + 1)
+                for hh in range(H):
+                    kv = hh // grp
+                    sc = k[s0:t + 1, kv] @ q[t, hh] / np.sqrt(D)
+                    pr = np.exp(sc - sc.max())
+                    pr /= pr.sum()
+                    att[t, hh] = pr @ v[s0:t + 1, kv]
+            yv = att.reshape(N, -1) @ W(p + "attn_out.weight").T
+        x = x + yv
+        h = norm(x, W(p + "ln2.weight"))
+        g = h @ W(p + "ffn_gate.weight").T
+        x = x + (silu(g) * (h @ W(p + "ffn_up.weight").T)) @ W(p + "ffn_down.weight").T
+        il += 1
+    x = norm(x, W("a.post_ln.weight"))
+    mu = x.mean(-1, keepdims=True)
+    var = ((x - mu) ** 2).mean(-1, keepdims=True)
+    x = (x - mu) / np.sqrt(var + 1e-5) * W("mm.a.mlp.0.weight") + W("mm.a.mlp.0.bias")
+    x = x @ W("mm.a.mlp.1.weight").T + W("mm.a.mlp.1.bias")
+    erf = np.vectorize(math.erf)
+    x = 0.5 * x * (1 + erf(x / math.sqrt(2)))
+    x = x @ W("mm.a.mlp.3.weight").T + W("mm.a.mlp.3.bias")
+    return x, mel
+

@@ -9,12 +9,68 @@
 // Parity pins for each function live in tests/ (closed forms, brute force, invariants); see the header of
 // tests/test_oracle_*.py.
 #pragma once
+#include <immintrin.h>
+
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
+#include <functional>
 #include <string>
+#include <thread>
 #include <vector>
 
 namespace orc {
+
+// ---------------------------------------------------------------- thread team (shape of imi/core/team.h)
+struct team {
+    int n = 1;
+    std::vector<std::thread> th;
+    const std::function<void(int)>* job = nullptr;
+    alignas(64) std::atomic<int> gen{0};
+    alignas(64) std::atomic<int> done{0};
+    alignas(64) std::atomic<int> arrived{0};
+    alignas(64) std::atomic<int> phase{0};
+    std::atomic<bool> quit{false};
+    template <class F> static void wait_until(F ok) {
+        for (int spins = 0; !ok();) { if (spins < 20000) { _mm_pause(); spins++; } else std::this_thread::yield(); }
+    }
+    void start(int nt) {
+        n = nt < 1 ? 1 : nt;
+        for (int t = 1; t < n; t++)
+            th.emplace_back([this, t] {
+                int seen = 0;
+                for (;;) {
+                    wait_until([&] { return gen.load(std::memory_order_acquire) != seen; });
+                    seen = gen.load(std::memory_order_acquire);
+                    if (quit.load()) return;
+                    (*job)(t);
+                    done.fetch_add(1, std::memory_order_acq_rel);
+                }
+            });
+    }
+    void run(const std::function<void(int)>& f) {
+        job = &f;
+        done.store(0, std::memory_order_relaxed);
+        gen.fetch_add(1, std::memory_order_release);
+        f(0);
+        wait_until([&] { return done.load(std::memory_order_acquire) == n - 1; });
+    }
+    void sync() {   // spinning barrier (imi/core/team.h:39-48)
+        if (n == 1) return;
+        const int p = phase.load(std::memory_order_acquire);
+        if (arrived.fetch_add(1, std::memory_order_acq_rel) == n - 1) {
+            arrived.store(0, std::memory_order_relaxed);
+            phase.store(p + 1, std::memory_order_release);
+        } else {
+            wait_until([&] { return phase.load(std::memory_order_acquire) != p; });
+        }
+    }
+    ~team() {
+        quit.store(true);
+        gen.fetch_add(1, std::memory_order_release);
+        for (auto& t : th) t.join();
+    }
+};
 
 // ---- fp16 <-> fp32 (imi/core/tables.cpp:20-38) ----
 float    h2f(uint16_t h);          // exact, bit construction as imi_h2f
