@@ -225,6 +225,75 @@ def gpu_prefill(brain, reps):
     return np.array(times), lg, best
 
 
+HEAR_SAMPLES = 491760   # 30.7 s at 16 kHz: the ears give exactly the hearing window's 384 rows
+
+
+def ears_fma(info, n_pos, n_fr):
+    """fp32 multiply-adds of one encode (imi/core/ears.cpp:198-407): the DFT table, the three 3x3 convolutions, the
+    pointwise and pre_encode tables, every layer's tables, conv taps and attention (scores and weighted values over
+    the window), the projector; the mel filters' double multiply-adds are not counted."""
+    C, E, F8, F2, F4 = info.n_ch, info.n_embd, info.n_mel // 8, info.n_mel // 2, info.n_mel // 4
+    T2 = (n_fr + 1) // 2
+    T4 = (T2 + 1) // 2
+    H, Hk, D = info.n_head, info.n_head_kv, info.head_dim
+    f = 402 * 400 * n_fr + 9 * C * (T2 * F2 + T4 * F4 + n_pos * F8) + C * C * (T4 * F4 + n_pos * F8) + E * C * F8 * n_pos
+    n_conv = info.n_layer - info.n_attn
+    keys = sum(min(p + 1, info.window) for p in range(n_pos))
+    f += n_conv * ((3 * E * E + E * E + info.d_conv * E) * n_pos)
+    f += info.n_attn * (((H + 2 * Hk) * D * E + E * H * D) * n_pos + 2 * H * D * keys)
+    f += info.n_layer * 3 * info.n_ff * E * n_pos
+    f += (info.n_mid * E + info.n_out * info.n_mid) * n_pos
+    return f
+
+
+def gpu_hear(brain, ears_path, reps):
+    """The hearing window from sound: the ears encode a 30.7 s clip into 384 rows, then the rows and 64 seeded words
+    run as one causal prefill. Returns per-rep ears and prefill seconds (host buffers in and out, as imi's caller
+    passes them), the rows, the last scores and the chosen id."""
+    import nunchi_amd
+    from nunchi_amd import synth
+    ears = nunchi_amd.Ears(ears_path)
+    pcm = synth.clip(HEAR_SAMPLES, 1)
+    toks, emb = hearing_inputs(brain.n_vocab)
+    st = brain.new_state()
+    te, tp = [], []
+    for r in range(reps + 1):
+        st.reset()
+        t0 = time.perf_counter()
+        rows = ears.encode(pcm)
+        t1 = time.perf_counter()
+        emb[:HEAR_EMB] = rows
+        _, lg, best, _ = brain.step_batch(toks, emb, want_logits=True, st=st)
+        t2 = time.perf_counter()
+        if r:
+            te.append(t1 - t0)
+            tp.append(t2 - t1)
+    info = ears.info
+    ears.close()
+    return np.array(te), np.array(tp), rows, lg, best, info
+
+
+def cpu_hear(path, ears_path, threads):
+    import oracle
+    from nunchi_amd import synth
+    pcm = synth.clip(HEAR_SAMPLES, 1)
+    ears = oracle.Ears(ears_path, threads=threads)
+    rows = ears.encode(pcm)
+    rows = ears.encode(pcm)
+    te = ears.secs
+    toks, emb = hearing_inputs(97496)
+    emb[:HEAR_EMB] = rows
+    eng = oracle.Engine(path, threads=threads, n_ctx=N_CTX)
+    t0 = time.perf_counter()
+    _, lg, _ = eng.step_batch(toks, emb, want_logits=True)
+    return te, time.perf_counter() - t0, rows, lg
+
+
+def oracle_rel(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return np.sqrt(((a - b) ** 2).sum() / max((b ** 2).sum(), 1e-30))
+
+
 def cpu_prefill(path, threads):
     import oracle
     toks, emb = hearing_inputs(97496)
@@ -332,6 +401,10 @@ def main():
     ap.add_argument("--voice-frames", type=int, default=64, help="timed voice frames (cfg 4); 0 = skip")
     ap.add_argument("--prefill-reps", type=int, default=10, help="timed hearing-window prefills (cfg 3); 0 = skip")
     ap.add_argument("--cpu-voice-frames", type=int, default=8)
+    ap.add_argument("--hear-reps", type=int, default=5, help="timed hearing windows from sound (ears + prefill); 0 = skip")
+    ap.add_argument("--ears-only", type=int, default=0, metavar="REPS",
+                    help="only REPS ears encodes of the 30.7 s clip (after one untimed), no brain: the launches a kernel "
+                         "trace of the ears reads")
     ap.add_argument("--talk-frames", type=int, default=32, help="timed talk frames (12-codebook generator + codec); 0 = skip")
     ap.add_argument("--cpu-talk-frames", type=int, default=4)
     ap.add_argument("--decode-only", action="store_true",
@@ -359,6 +432,18 @@ def main():
 
     import nunchi_amd
     from nunchi_amd import synth
+    if args.ears_only:
+        ears = nunchi_amd.Ears(synth.cached("ears", synth.EARS, 3))
+        pcm = synth.clip(HEAR_SAMPLES, 1)
+        ts = []
+        for i in range(args.ears_only + 1):
+            t0 = time.perf_counter()
+            ears.encode(pcm)
+            if i:
+                ts.append(time.perf_counter() - t0)
+        print(json.dumps({"ears_only": {"reps": len(ts), "p50_ms": round(float(np.percentile(ts, 50)) * 1e3, 3),
+                                        "table_bytes": int(ears.info.table_bytes)}}), flush=True)
+        return
     if args.codec_only:
         codec = nunchi_amd.Codec(synth.cached("codec", synth.CODEC, 2))
         codes = np.random.default_rng(5).integers(0, codec.info.n_codes, (args.codec_only + 4, 12))
@@ -531,6 +616,27 @@ def main():
             "mfma_util_pct_counter_run": PREFILL_MFMA_UTIL_PCT,
             "reps": int(len(pt)),
         }
+    if args.hear_reps:
+        epath = synth.cached("ears", synth.EARS, 3)
+        te, tp, hrows, hlg, hbest, einfo = gpu_hear(brain, epath, args.hear_reps)
+        n_fr = (HEAR_SAMPLES - 400 + 159) // 160 + 1
+        fma = ears_fma(einfo, HEAR_EMB, n_fr)
+        e50 = float(np.percentile(te, 50))
+        line["hear"] = {
+            "workload": f"the hearing window from sound: {HEAR_SAMPLES / 16000:.2f} s of seeded 16 kHz samples through the "
+                        f"ears ({n_fr} mel frames of 128 bands, stride-2 downsampler to {HEAR_EMB} positions, "
+                        f"{einfo.n_layer} causal LFM layers ({einfo.n_attn} attention over {einfo.window} positions), "
+                        f"{einfo.n_embd} wide, F16 tables, projector to 2048), then the {HEAR_EMB} rows and "
+                        f"{HEAR_TOK} seeded words as one causal prefill of the cfg2 model",
+            "ears_p50_ms": round(e50 * 1e3, 3),
+            "prefill_p50_ms": round(float(np.percentile(tp, 50)) * 1e3, 3),
+            "total_p50_ms": round(float(np.percentile(te + tp, 50)) * 1e3, 3),
+            "ears_fma": int(fma),
+            "ears_tflops": round(2 * fma / e50 / 1e12, 2),
+            "fp32_valu_peak_tflops": 78.6,
+            "ears_table_bytes": int(einfo.table_bytes),
+            "reps": int(len(te)),
+        }
     if args.voice_frames:
         vpath = synth.cached("voice", synth.VOICE, 1)
         (ft, fbr, fvo, fcodes, fids, _), fref, vinfo = gpu_voice_frames(path, vpath, args.voice_frames, 4)
@@ -617,6 +723,15 @@ def main():
                                       "sample": "one hearing-window prefill on the oracle (imi's step_batch restated)"}
             line["prefill"]["speedup_vs_cpu"] = round(csec / float(np.percentile(pt, 50)), 1)
             line["prefill"]["scores_match_cpu"] = bool(np.array_equal(clg.view(np.uint32), plg.view(np.uint32)))
+        if args.hear_reps:
+            ce, cp, crows, clg2 = cpu_hear(path, epath, threads)
+            line["hear"]["cpu"] = {"ears_ms": round(ce * 1e3, 1), "prefill_ms": round(cp * 1e3, 1), "cores": threads,
+                                   "kind": "port", "sample": "one encode (after one untimed) and one prefill on the oracle "
+                                   "(imi's ears and step_batch restated, AVX2, imi's spinning thread team)"}
+            line["hear"]["speedup_vs_cpu"] = round((ce + cp) / float(np.percentile(te + tp, 50)), 1)
+            line["hear"]["rows_rel_l2_vs_cpu"] = float(oracle_rel(hrows, crows))
+            line["hear"]["scores_rel_l2_vs_cpu"] = float(oracle_rel(hlg, clg2))
+            line["hear"]["best_id_matches_cpu"] = bool(int(np.argmax(clg2)) == int(hbest))
         if args.voice_frames and args.cpu_voice_frames:
             ct, cbr, cvo, ccodes, cids, _, _, _, _ = cpu_voice_frames(path, vpath, threads, args.cpu_voice_frames)
             n = len(ct)

@@ -77,6 +77,8 @@ int sh_codec_flush(sh_codec* c, float* pcm, int* n_out);
 /* ---- ears (audio encoder): imi_ears::load / encode (imi/core/ears.h:17-51) ---- */
 typedef struct {
     int n_mel, n_ch, n_embd, n_ff, n_head, n_head_kv, head_dim, window, n_out, d_conv, n_layer;
+    int n_attn;                     /* attention layers (the others are short-conv layers) */
+    int n_mid;                      /* projector width (mm.a.mlp.1 rows) */
     long long table_bytes;          /* float table bytes (F16 / F32 as in the file, plus the 402 x 400 DFT) */
 } sh_ears_shape;
 

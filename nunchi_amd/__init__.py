@@ -59,7 +59,7 @@ class CodecShape(C.Structure):
 
 class EarsShape(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("n_mel", "n_ch", "n_embd", "n_ff", "n_head", "n_head_kv", "head_dim", "window",
-                                       "n_out", "d_conv", "n_layer")] + [("table_bytes", C.c_longlong)]
+                                       "n_out", "d_conv", "n_layer", "n_attn", "n_mid")] + [("table_bytes", C.c_longlong)]
 
 
 class Tensor(C.Structure):

@@ -45,9 +45,10 @@ hipError_t launch_etab(int epi, const etab_args& a, hipStream_t s);
 // fx[k][fr] = hann[k] * pcm[fr * hop + k] (0 past the clip or past n_fr), k < n_fft, fr < ldf
 hipError_t launch_eframes(const float* pcm, int n, const float* hann, int n_fft, int hop, int n_fr, float* fx, int ldf,
                           hipStream_t s);
-// mel[fr][m] = (log10(max(sum_b fb[m][b] pw[b][fr], 1e-12)) + 4) / 4, the sum an fma chain in double
-hipError_t launch_emel(const float* pw, int ldp, const float* fb, int n_bin, int n_mel, int n_fr, float* mel,
-                       hipStream_t s);
+// mel[fr][m] = (log10(max(sum_b fb[m][b] pw[b][fr], 1e-12)) + 4) / 4, the sum an fma chain in double over the
+// filter's nonzero bins span[m] = [lo, hi)
+hipError_t launch_emel(const float* pw, int ldp, const float* fb, const int2* span, int n_bin, int n_mel, int n_fr,
+                       float* mel, hipStream_t s);
 // first stride-2 3x3 conv of the mel image (one input channel) + SiLU: a0[c][t][f], t < T2, f < F2
 hipError_t launch_econv0(const float* mel, int n_fr, int n_mel, const float* w9, const float* b, int C, float* a0,
                          hipStream_t s);

@@ -17,6 +17,31 @@ constexpr int ET = 256;
 
 __device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }
 
+// imi_rms_scale (imi/core/vec.h:20-33) in its AVX2 op order by one half-wave over one row of n floats (n % 32 == 0):
+// lane P of the half runs the fma chain of x[32t + P]^2 over t (all loads issued first, 8 at a time), then
+// v_l = (a_l + a_{l+8}) + (a_{l+16} + a_{l+24}) and ((v0+v4) + (v2+v6)) + ((v1+v5) + (v3+v7)); every lane of the
+// half gets 1 / sqrtf(s / n + eps)
+__device__ __forceinline__ float rms_scale_half(const float* x, int n, float eps) {
+    const int lane = threadIdx.x & 63, hl = lane & 31, base = lane & 32;
+    const int nt = n / 32;
+    float a = 0.0f;
+    int t = 0;
+    for (; t + 8 <= nt; t += 8) {
+        float v[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) v[q] = x[32 * (t + q) + hl];
+#pragma unroll
+        for (int q = 0; q < 8; q++) a = fmaf(v[q], v[q], a);
+    }
+    for (; t < nt; t++) a = fmaf(x[32 * t + hl], x[32 * t + hl], a);
+    auto at = [&](float v, int l) { return __shfl(v, base + (l & 31)); };
+    const float v = (a + at(a, hl + 8)) + (at(a, hl + 16) + at(a, hl + 24));   // lanes 0..7 of the half
+    const float r = v + at(v, hl + 4);
+    const float q = r + at(r, hl + 2);
+    const float s = at(q, 0) + at(q, 1);
+    return 1.0f / sqrtf(s / (float)n + eps);
+}
+
 
 // 8 columns of one row, raw: F16 bits (one 16-byte load) or F32 (two)
 template <bool F32W> struct wraw;
@@ -162,44 +187,72 @@ __global__ __launch_bounds__(ET) void k_eframes(const float* pcm, int n, const f
     fx[(size_t)k * ldf + fr] = fr < n_fr && i < n ? hann[k] * pcm[i] : 0.0f;
 }
 
-__global__ __launch_bounds__(ET) void k_emel(const float* pw, int ldp, const float* fb, int n_bin, int n_mel, int n_fr,
-                                             float* mel) {
+// imi sums all n_bin terms in bin order; a term with a zero filter weight is fma(0, pw, s) = s exactly (pw is a sum of
+// two squares, finite and >= 0), so each mel only runs over its filter's nonzero bins [lo, hi), in order
+__global__ __launch_bounds__(ET) void k_emel(const float* pw, int ldp, const float* fb, const int2* span, int n_bin,
+                                             int n_mel, int n_fr, float* mel) {
     const int fr = blockIdx.x * ET + threadIdx.x, m = blockIdx.y;
     if (fr >= n_fr) return;
     const float* w = fb + (size_t)m * n_bin;
+    const int2 sp = span[m];
     double s = 0.0;
-    for (int b = 0; b < n_bin; b++) s = fma((double)w[b], (double)pw[(size_t)b * ldp + fr], s);
+    for (int b = sp.x; b < sp.y; b++) s = fma((double)w[b], (double)pw[(size_t)b * ldp + fr], s);
     mel[(size_t)fr * n_mel + m] = (float)((log10(s < 1e-12 ? 1e-12 : s) + 4.0) / 4.0);
 }
 
+// thread per (t, f) and 8 channels: the 9 taps' inputs are requested first (addresses clamped into the image) and
+// shared by the channels; a tap outside the image leaves o as it is (a select, not a multiply by zero, so o keeps its
+// bits exactly as imi's skipped tap does)
+constexpr int E0_CPT = 8;
 __global__ __launch_bounds__(ET) void k_econv0(const float* mel, int n_fr, int n_mel, const float* w9, const float* b,
                                                int C, int T2, int F2, float* a0) {
-    const long idx = (long)blockIdx.x * ET + threadIdx.x;
-    if (idx >= (long)C * T2 * F2) return;
-    const int f = (int)(idx % F2), t = (int)((idx / F2) % T2), c = (int)(idx / ((long)F2 * T2));
-    float o = b[c];
-    for (int kh = 0; kh < 3; kh++)
-        for (int kw = 0; kw < 3; kw++) {
-            const int ti = 2 * t + kw - 1, fi = 2 * f + kh - 1;
-            if (ti < 0 || ti >= n_fr || fi < 0 || fi >= n_mel) continue;
-            o = fmaf(mel[(size_t)ti * n_mel + fi], w9[(size_t)(kh * 3 + kw) * C + c], o);
+    const int i = blockIdx.x * ET + threadIdx.x, c0 = blockIdx.y * E0_CPT;
+    if (i >= T2 * F2) return;
+    const int t = i / F2, f = i - t * F2;
+    float v[9];
+    bool ok[9];
+#pragma unroll
+    for (int j = 0; j < 9; j++) {
+        const int ti = 2 * t + j % 3 - 1, fi = 2 * f + j / 3 - 1;   // j = kh * 3 + kw: kw along time, kh along freq
+        ok[j] = ti >= 0 && ti < n_fr && fi >= 0 && fi < n_mel;
+        const int tc = ti < 0 ? 0 : ti >= n_fr ? n_fr - 1 : ti, fc = fi < 0 ? 0 : fi >= n_mel ? n_mel - 1 : fi;
+        v[j] = mel[(size_t)tc * n_mel + fc];
+    }
+#pragma unroll
+    for (int cc = 0; cc < E0_CPT; cc++) {
+        const int c = c0 + cc;
+        if (c >= C) break;
+        float o = b[c];
+#pragma unroll
+        for (int j = 0; j < 9; j++) {
+            const float u = fmaf(v[j], w9[(size_t)j * C + c], o);
+            o = ok[j] ? u : o;
         }
-    a0[idx] = silu(o);
+        a0[(size_t)c * T2 * F2 + i] = silu(o);
+    }
 }
 
 __global__ __launch_bounds__(ET) void k_edw(const float* in, int Ti, int Fi, int ldi, const float* w9, const float* b,
                                             int C, int To, int Fo, float* out, int ldo) {
-    const long idx = (long)blockIdx.x * ET + threadIdx.x;
-    if (idx >= (long)C * To * Fo) return;
-    const int f = (int)(idx % Fo), t = (int)((idx / Fo) % To), c = (int)(idx / ((long)Fo * To));
+    const int i = blockIdx.x * ET + threadIdx.x, c = blockIdx.y;
+    if (i >= To * Fo) return;
+    const int t = i / Fo, f = i - t * Fo;
     const float* src = in + (size_t)c * ldi;
+    float v[9];
+    bool ok[9];
+#pragma unroll
+    for (int j = 0; j < 9; j++) {
+        const int ti = 2 * t + j % 3 - 1, fi = 2 * f + j / 3 - 1;
+        ok[j] = ti >= 0 && ti < Ti && fi >= 0 && fi < Fi;
+        const int tc = ti < 0 ? 0 : ti >= Ti ? Ti - 1 : ti, fc = fi < 0 ? 0 : fi >= Fi ? Fi - 1 : fi;
+        v[j] = src[(size_t)tc * Fi + fc];
+    }
     float o = b[c];
-    for (int kh = 0; kh < 3; kh++)
-        for (int kw = 0; kw < 3; kw++) {
-            const int ti = 2 * t + kw - 1, fi = 2 * f + kh - 1;
-            if (ti < 0 || ti >= Ti || fi < 0 || fi >= Fi) continue;
-            o = fmaf(src[(size_t)ti * Fi + fi], w9[(size_t)(kh * 3 + kw) * C + c], o);
-        }
+#pragma unroll
+    for (int j = 0; j < 9; j++) {
+        const float u = fmaf(v[j], w9[(size_t)j * C + c], o);
+        o = ok[j] ? u : o;
+    }
     out[(size_t)c * ldo + (size_t)t * Fo + f] = o;
 }
 
@@ -210,17 +263,21 @@ __global__ __launch_bounds__(ET) void k_eflat(const float* a, int lda, int F8, i
     xf[(size_t)k * ldf + p] = p < P ? a[(size_t)c * lda + (size_t)p * F8 + f] : 0.0f;
 }
 
-// one wave per position
+// a workgroup is 16 positions x 64 features: each wave forms 4 positions' scales in imi's order (every workgroup of a
+// position forms the same scale), then h is written feature-major, 16 positions (64 bytes) per feature row
 __global__ __launch_bounds__(ET) void k_enorm(const float* x, const float* w, int E, int P, int ldh, float eps, float* h) {
-    const int lane = threadIdx.x & 63, p = blockIdx.x * (ET / 64) + (threadIdx.x >> 6);
-    if (p >= ldh) return;
-    if (p >= P) {
-        for (int e = lane; e < E; e += 64) h[(size_t)e * ldh + p] = 0.0f;
-        return;
+    __shared__ float sc[16];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, p0 = blockIdx.x * 16, e0 = blockIdx.y * 64;
+    for (int q = 0; q < 2; q++) {   // half-wave hf forms position p0 + 4 wv + 2 q + hf
+        const int hf = lane >> 5, pq = wv * 4 + 2 * q + hf, p = p0 + pq;
+        const float s = rms_scale_half(x + (size_t)(p < P ? p : 0) * E, E, eps);
+        if ((lane & 31) == 0) sc[pq] = p < P ? s : 0.0f;
     }
-    const float* xp = x + (size_t)p * E;
-    const float s = rms_scale_wave(xp, E, eps);
-    for (int e = lane; e < E; e += 64) h[(size_t)e * ldh + p] = xp[e] * s * w[e];
+    __syncthreads();
+    const int pl = threadIdx.x & 15, p = p0 + pl;
+    const float s = sc[pl];
+    for (int e = e0 + (threadIdx.x >> 4); e < e0 + 64 && e < E; e += ET / 16)
+        h[(size_t)e * ldh + p] = p < P ? x[(size_t)p * E + e] * s * w[e] : 0.0f;
 }
 
 __global__ __launch_bounds__(ET) void k_econv(const float* big, int ld, const float* w, int E, int d_conv, int P,
@@ -360,21 +417,22 @@ hipError_t launch_eframes(const float* pcm, int n, const float* hann, int n_fft,
     hipLaunchKernelGGL(k_eframes, dim3(blocks(ldf), n_fft), dim3(ET), 0, s, pcm, n, hann, n_fft, hop, n_fr, fx, ldf);
     return hipGetLastError();
 }
-hipError_t launch_emel(const float* pw, int ldp, const float* fb, int n_bin, int n_mel, int n_fr, float* mel,
-                       hipStream_t s) {
-    hipLaunchKernelGGL(k_emel, dim3(blocks(n_fr), n_mel), dim3(ET), 0, s, pw, ldp, fb, n_bin, n_mel, n_fr, mel);
+hipError_t launch_emel(const float* pw, int ldp, const float* fb, const int2* span, int n_bin, int n_mel, int n_fr,
+                       float* mel, hipStream_t s) {
+    hipLaunchKernelGGL(k_emel, dim3(blocks(n_fr), n_mel), dim3(ET), 0, s, pw, ldp, fb, span, n_bin, n_mel, n_fr, mel);
     return hipGetLastError();
 }
 hipError_t launch_econv0(const float* mel, int n_fr, int n_mel, const float* w9, const float* b, int C, float* a0,
                          hipStream_t s) {
     const int T2 = (n_fr + 1) / 2, F2 = n_mel / 2;
-    hipLaunchKernelGGL(k_econv0, dim3(blocks((long)C * T2 * F2)), dim3(ET), 0, s, mel, n_fr, n_mel, w9, b, C, T2, F2, a0);
+    hipLaunchKernelGGL(k_econv0, dim3(blocks((long)T2 * F2), (C + E0_CPT - 1) / E0_CPT), dim3(ET), 0, s, mel, n_fr, n_mel,
+                       w9, b, C, T2, F2, a0);
     return hipGetLastError();
 }
 hipError_t launch_edw(const float* in, int Ti, int Fi, int ldi, const float* w9, const float* b, int C, float* out,
                       int ldo, hipStream_t s) {
     const int To = (Ti + 1) / 2, Fo = Fi / 2;
-    hipLaunchKernelGGL(k_edw, dim3(blocks((long)C * To * Fo)), dim3(ET), 0, s, in, Ti, Fi, ldi, w9, b, C, To, Fo, out, ldo);
+    hipLaunchKernelGGL(k_edw, dim3(blocks((long)To * Fo), C), dim3(ET), 0, s, in, Ti, Fi, ldi, w9, b, C, To, Fo, out, ldo);
     return hipGetLastError();
 }
 hipError_t launch_eflat(const float* a, int lda, int C, int F8, int P, float* xf, int ldf, hipStream_t s) {
@@ -383,7 +441,8 @@ hipError_t launch_eflat(const float* a, int lda, int C, int F8, int P, float* xf
 }
 hipError_t launch_enorm(const float* x, const float* w, int E, int P, float eps, float* h, int ldh, hipStream_t s) {
     if (E % 32) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_enorm, dim3((unsigned)((ldh + 3) / 4)), dim3(ET), 0, s, x, w, E, P, ldh, eps, h);
+    if (ldh % 16) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_enorm, dim3((unsigned)(ldh / 16), (unsigned)((E + 63) / 64)), dim3(ET), 0, s, x, w, E, P, ldh, eps, h);
     return hipGetLastError();
 }
 hipError_t launch_econv(const float* big, int ld, const float* w, int E, int d_conv, int P, float* act, int lda,

@@ -57,6 +57,7 @@ struct sh_ears {
     char* mem = nullptr;   // weights
     std::vector<elayer> layers;
     etab dft, c3, c6, pre, mlp1, mlp3;
+    const int2* fb_span = nullptr;   // per mel: the filter's nonzero bins [lo, hi)
     const float *hann = nullptr, *fb = nullptr, *c0_w = nullptr, *c0_b = nullptr, *c2_w = nullptr, *c2_b = nullptr,
                 *c3_b = nullptr, *c5_w = nullptr, *c5_b = nullptr, *c6_b = nullptr, *pre_b = nullptr,
                 *post_ln = nullptr, *ln_w = nullptr, *ln_b = nullptr, *mlp1_b = nullptr, *mlp3_b = nullptr;
@@ -198,7 +199,7 @@ int enqueue_encode(sh_ears* e, int n) {
     // mel (ears.cpp:211-238)
     ECHK(launch_eframes(e->pcm, n, e->hann, N_FFT, HOP, g.n_fr, e->fx, Pf, s));
     RUN(run_table(e, EE_POWER, e->dft, e->fx, Pf, g.n_fr, nullptr, e->pw, Pf, true));
-    ECHK(launch_emel(e->pw, Pf, e->fb, N_BIN, I.n_mel, g.n_fr, e->mel, s));
+    ECHK(launch_emel(e->pw, Pf, e->fb, e->fb_span, N_BIN, I.n_mel, g.n_fr, e->mel, s));
     // downsampler (ears.cpp:241-296), channel-major
     ECHK(launch_econv0(e->mel, g.n_fr, I.n_mel, e->c0_w, e->c0_b, C, e->a0, s));
     ECHK(launch_edw(e->a0, g.T2, g.F2, g.T2 * g.F2, e->c2_w, e->c2_b, C, e->a1, P4, s));
@@ -353,6 +354,7 @@ int sh_ears_load(int device, const char* path, sh_ears** out) {   // imi/core/ea
     }
     if (n_attn == 0) { I.head_dim = 0; I.n_head_kv = 0; }
     I.n_layer = (int)layers.size();
+    I.n_attn = n_attn;
     const gg_tensor *post = f.get("a.post_ln.weight", false), *lw = f.get("mm.a.mlp.0.weight", false),
                     *lb = f.get("mm.a.mlp.0.bias", false), *m1 = f.get("mm.a.mlp.1.weight", false),
                     *m1b = f.get("mm.a.mlp.1.bias", false), *m3 = f.get("mm.a.mlp.3.weight", false),
@@ -370,6 +372,7 @@ int sh_ears_load(int device, const char* path, sh_ears** out) {   // imi/core/ea
     e->device = device;
     e->eps = eps;
     e->n_mid = n_mid;
+    I.n_mid = n_mid;
     e->big_w = big_w;
     e->layers = std::move(layers);
     // the mel front end as imi builds it (ears.cpp:44-80)
@@ -407,6 +410,17 @@ int sh_ears_load(int device, const char* path, sh_ears** out) {   // imi/core/ea
     };
     vecs.push_back({nullptr, hann, N_FFT, &e->hann});
     vecs.push_back({nullptr, fbm, I.n_mel * N_BIN, &e->fb});
+    {
+        vec sp{nullptr, std::vector<float>((size_t)2 * I.n_mel), 2 * I.n_mel, reinterpret_cast<const float**>(&e->fb_span)};
+        for (int m = 0; m < I.n_mel; m++) {
+            int lo = 0, hi = 0;
+            for (int b = 0; b < N_BIN; b++)
+                if (fbm[(size_t)m * N_BIN + b] != 0.0f) { if (hi == 0) lo = b; hi = b + 1; }
+            const int32_t v[2] = {lo, hi};
+            memcpy(&sp.host[(size_t)2 * m], v, 8);
+        }
+        vecs.push_back(std::move(sp));
+    }
     taps9("a.conv1d.0.weight", &e->c0_w); v_of(f.get("a.conv1d.0.bias"), C, &e->c0_b);
     taps9("a.conv1d.2.weight", &e->c2_w); v_of(f.get("a.conv1d.2.bias"), C, &e->c2_b);
     taps9("a.conv1d.5.weight", &e->c5_w); v_of(f.get("a.conv1d.5.bias"), C, &e->c5_b);
