@@ -1,11 +1,13 @@
 // seoul_gpu.hpp — imi's engine API (imi/core/seoul.h:19-94, imi/brain.h:20-65), file API (imi/model.h:12-36), voice
-// generator API (imi/core/voice.h:17-51) and codec API (imi/core/codec.h:17-65) over libseoul_hip's C ABI.
+// generator API (imi/core/voice.h:17-51), codec API (imi/core/codec.h:17-65) and ears API (imi/core/ears.h:17-51)
+// over libseoul_hip's C ABI.
 //
 // Drop-in for the CPU engine: the same members and signatures, so imi's callers (greedy loops, the voice frame,
 // step2 riding) compile unchanged after
 //     #include "seoul_gpu.hpp"
 //     using seoul_hip::imi_seoul; using seoul_hip::imi_seoul_state; using seoul_hip::imi_voice;
 //     using seoul_hip::imi_brain; using seoul_hip::imi_file; using seoul_hip::imi_tensor; using seoul_hip::imi_codec;
+//     using seoul_hip::imi_ears;
 // and link -lseoul_hip. Header-only C++17; no HIP or torch types. The thread arguments of load() are accepted and
 // ignored (the device has no thread team). Errors follow imi: load() returns false and prints; a full context
 // prints "context full" and returns without stepping (imi/core/seoul.cpp:209,353,498).
@@ -492,6 +494,53 @@ private:
     sh_codec* c = nullptr;
     bool report(const char* what) const {
         fprintf(stderr, "seoul-hip: codec %s: %s\n", what, sh_last_error());
+        return false;
+    }
+};
+
+// imi_ears (imi/core/ears.h:17-51) over the same C ABI: the audio encoder on the device. encode() turns 16 kHz samples
+// from the clip's start into [n_pos][n_out] rows for the brain's step_batch and returns n_pos; last_mel holds the
+// encode's [n_frames][n_mel] log-mel frames. `threads` and `shared` (CPU thread team) are accepted and ignored; the
+// stage timers stay 0 (the whole encode is one device call).
+struct imi_ears {
+    int n_mel = 128, n_bin = 201, n_fft = 400, hop = 160, n_ch = 256, n_embd = 768, n_ff = 0, n_head = 0, n_head_kv = 0,
+        head_dim = 0, window = 32, n_out = 0, d_conv = 3;
+    float eps = 1e-5f, rope_theta = 1e6f;
+    int n_threads = 4;
+    double t_mel = 0, t_down = 0, t_layers = 0, t_proj = 0;
+    std::vector<float> last_mel;
+
+    imi_ears() = default;
+    imi_ears(const imi_ears&) = delete;
+    imi_ears& operator=(const imi_ears&) = delete;
+    ~imi_ears() {
+        if (e) sh_ears_free(e);
+    }
+
+    bool load(const std::string& path, int threads, void* shared = nullptr, int device = 0) {   // ears.cpp:40-138
+        (void)shared;
+        n_threads = threads;
+        if (sh_ears_load(device, path.c_str(), &e) != SH_OK) return report("load");
+        sh_ears_shape I{};
+        sh_ears_info(e, &I);
+        n_mel = I.n_mel; n_ch = I.n_ch; n_embd = I.n_embd; n_ff = I.n_ff; n_head = I.n_head; n_head_kv = I.n_head_kv;
+        head_dim = I.head_dim; window = I.window; n_out = I.n_out; d_conv = I.d_conv;
+        return true;
+    }
+    int encode(const float* pcm, int n, std::vector<float>& out) {   // ears.cpp:198-407
+        int P = 0, F = 0;
+        if (sh_ears_positions(e, n, &P, &F) != SH_OK) return report("encode"), 0;
+        out.resize((size_t)P * n_out);
+        if (sh_ears_encode(e, pcm, n, out.data(), &P) != SH_OK) return report("encode"), 0;
+        last_mel.resize((size_t)F * n_mel);
+        if (sh_ears_mel(e, last_mel.data(), &F) != SH_OK) report("mel");
+        return P;
+    }
+
+private:
+    sh_ears* e = nullptr;
+    bool report(const char* what) const {
+        fprintf(stderr, "seoul-hip: ears %s: %s\n", what, sh_last_error());
         return false;
     }
 };
