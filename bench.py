@@ -281,6 +281,7 @@ def cpu_hear(path, ears_path, threads):
     rows = ears.encode(pcm)
     rows = ears.encode(pcm)
     te = ears.secs
+    del ears   # its spinning thread team would compete with the engine's
     toks, emb = hearing_inputs(97496)
     emb[:HEAR_EMB] = rows
     eng = oracle.Engine(path, threads=threads, n_ctx=N_CTX)
