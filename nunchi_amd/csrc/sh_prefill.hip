@@ -32,19 +32,23 @@ __device__ __forceinline__ void cut_store(const pf_cut& c, int n, int j, int p, 
 // PFR_FIRST: x = the word's dequantized row (Q4_0: (code - 8) * d; Q6_K: imi_q6k_dequant_row) or the given embedding
 // row (imi/core/seoul.cpp:363-364);
 // PFR_RESID: x = fma(y * rms(y), w_post, x) (imi/core/vec.h:41-44); then h = x * rms(x) * w_pre, cut or stored
+// One wave per position, 4 positions per workgroup (no workgroup barriers): the wave stages its rows in LDS, runs both
+// norms' chains (rms_scale_wave, imi's AVX2 order) and cuts its blocks, a block per lane.
 template <int MODE>
 __global__ __launch_bounds__(256) void k_pf_rows(pf_rows_args a) {
-    __shared__ __attribute__((aligned(16))) float xs[2048];
-    __shared__ __attribute__((aligned(16))) float hs[2048];
-    __shared__ float red[2];
-    const int p = blockIdx.x, tid = threadIdx.x, E = a.E, nb = E / 32;
+    __shared__ __attribute__((aligned(16))) float xs_all[4][2048];
+    __shared__ __attribute__((aligned(16))) float hs_all[4][2048];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, p = blockIdx.x * 4 + wv, E = a.E, nb = E / 32;
+    if (p >= a.n) return;
+    float* xs = xs_all[wv];
+    float* hs = hs_all[wv];
     float* xr = a.x + (size_t)p * E;
     if (MODE == PFR_FIRST) {
         const int tok = a.tokens ? a.tokens[p] : -1;
         if (tok >= 0 && a.vocab6.codes) {
-            for (int j = tid; j < nb; j += 256) q6k_dequant32((const u32x4*)a.vocab6.codes, a.vocab6.d, a.vocab6.nbk, tok, j, xs + 32 * j);
+            for (int j = lane; j < nb; j += 64) q6k_dequant32((const u32x4*)a.vocab6.codes, a.vocab6.d, a.vocab6.nbk, tok, j, xs + 32 * j);
         } else if (tok >= 0) {
-            for (int j = tid; j < nb; j += 256) {
+            for (int j = lane; j < nb; j += 64) {
                 const u32x4 c = reinterpret_cast<const u32x4*>(a.vocab.codes)[(size_t)tok * nb + j];
                 const float d = h2f(reinterpret_cast<const uint16_t*>(a.vocab.scales)[((size_t)(tok >> 3) * nb + j) * 8 + (tok & 7)]);
                 const unsigned w[4] = {c.x, c.y, c.z, c.w};
@@ -56,41 +60,61 @@ __global__ __launch_bounds__(256) void k_pf_rows(pf_rows_args a) {
                 }
             }
         } else {
-            for (int i = tid; i < E; i += 256) xs[i] = a.embd[(size_t)p * E + i];
+            for (int i = 4 * lane; i < E; i += 256)
+                *reinterpret_cast<float4*>(xs + i) = *reinterpret_cast<const float4*>(a.embd + (size_t)p * E + i);
         }
-        __syncthreads();
-        for (int i = tid; i < E; i += 256) xr[i] = xs[i];
+        __builtin_amdgcn_wave_barrier();
+        for (int i = 4 * lane; i < E; i += 256) *reinterpret_cast<float4*>(xr + i) = *reinterpret_cast<const float4*>(xs + i);
     } else {
+        // every global operand of the position is requested first (one memory latency, not three)
+        constexpr int NQ = 2048 / 256;   // float4 words per lane at most
         const float* yr = a.y + (size_t)p * E;
-        for (int i = tid; i < E; i += 256) hs[i] = yr[i];
-        __syncthreads();
-        if (tid < 64) {
-            const float s = rms_scale_wave(static_cast<const float*>(hs), E, a.eps);
-            if (tid == 0) red[0] = s;
+        float4 y4[NQ], x4[NQ], wp[NQ];
+#pragma unroll
+        for (int q = 0; q < NQ; q++) {
+            const int i = 4 * lane + 256 * q;
+            if (i < E) {
+                y4[q] = *reinterpret_cast<const float4*>(yr + i);
+                x4[q] = *reinterpret_cast<const float4*>(xr + i);
+                wp[q] = *reinterpret_cast<const float4*>(a.w_post + i);
+            }
         }
-        __syncthreads();
-        const float sc1 = red[0];
-        for (int i = tid; i < E; i += 256) {
-            const float v = fmaf(hs[i] * sc1, a.w_post[i], xr[i]);
-            xs[i] = v;
-            xr[i] = v;
+#pragma unroll
+        for (int q = 0; q < NQ; q++)
+            if (4 * lane + 256 * q < E) *reinterpret_cast<float4*>(hs + 4 * lane + 256 * q) = y4[q];
+        __builtin_amdgcn_wave_barrier();
+        const float sc1 = rms_scale_wave(static_cast<const float*>(hs), E, a.eps);
+#pragma unroll
+        for (int q = 0; q < NQ; q++) {
+            const int i = 4 * lane + 256 * q;
+            if (i < E) {
+                const float4 v = make_float4(fmaf(y4[q].x * sc1, wp[q].x, x4[q].x), fmaf(y4[q].y * sc1, wp[q].y, x4[q].y),
+                                             fmaf(y4[q].z * sc1, wp[q].z, x4[q].z), fmaf(y4[q].w * sc1, wp[q].w, x4[q].w));
+                *reinterpret_cast<float4*>(xs + i) = v;
+                *reinterpret_cast<float4*>(xr + i) = v;
+            }
         }
-        __syncthreads();
+        __builtin_amdgcn_wave_barrier();
     }
-    if (tid < 64) {
-        const float s = rms_scale_wave(static_cast<const float*>(xs), E, a.eps);
-        if (tid == 0) red[1] = s;
-    }
-    __syncthreads();
-    const float sc2 = red[1];
-    for (int i = tid; i < E; i += 256) {
-        const float h = xs[i] * sc2 * a.w_pre[i];
-        hs[i] = h;
-        if (a.hidden) a.hidden[(size_t)p * E + i] = h;
+    constexpr int NQ2 = 2048 / 256;
+    float4 wq[NQ2];
+#pragma unroll
+    for (int q = 0; q < NQ2; q++)
+        if (4 * lane + 256 * q < E) wq[q] = *reinterpret_cast<const float4*>(a.w_pre + 4 * lane + 256 * q);
+    const float sc2 = rms_scale_wave(static_cast<const float*>(xs), E, a.eps);
+#pragma unroll
+    for (int q = 0; q < NQ2; q++) {
+        const int i = 4 * lane + 256 * q;
+        if (i < E) {
+            const float4 x4 = *reinterpret_cast<const float4*>(xs + i), w4 = wq[q];
+            const float4 h = make_float4(x4.x * sc2 * w4.x, x4.y * sc2 * w4.y, x4.z * sc2 * w4.z, x4.w * sc2 * w4.w);
+            *reinterpret_cast<float4*>(hs + i) = h;
+            if (a.hidden) *reinterpret_cast<float4*>(a.hidden + (size_t)p * E + i) = h;
+        }
     }
     if (!a.cut.q) return;
-    __syncthreads();
-    for (int j = tid; j < nb; j += 256) cut_store(a.cut, a.n, j, p, hs + 32 * j);
+    __builtin_amdgcn_wave_barrier();
+    for (int j = lane; j < nb; j += 64) cut_store(a.cut, a.n, j, p, hs + 32 * j);
 }
 
 // ---------------------------------------------------------------- cut of n rows
@@ -578,11 +602,29 @@ __global__ __launch_bounds__(256) void k_pf_attn(pf_attn_args a) {
     const uint16_t* vh = (const uint16_t*)vt;
     const int nitem = grp * D;                // (head, dimension) items, at most 4 per thread
     float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // a tile is TP * D / 8 16-byte words (at most 512: 2 per thread); the next tile's words are requested before the
+    // current tile's chains run
+    constexpr int WPT = (TW + 255) / 256;
+    u32x4 nv[WPT];
+    auto fetch = [&](int q0) {
+        const int nt = min(TP, nk - q0);
+#pragma unroll
+        for (int r = 0; r < WPT; r++) {
+            const int w = tid + 256 * r;
+            if (w < nt * (D / 8)) nv[r] = ((const u32x4*)(vc + (size_t)(s0 + q0) * D))[w];
+        }
+    };
+    fetch(0);
     for (int q0 = 0; q0 < nk; q0 += TP) {
         const int nt = min(TP, nk - q0);
         __syncthreads();
-        for (int w = tid; w < nt * (D / 8); w += 256) vt[w] = ((const u32x4*)(vc + (size_t)(s0 + q0) * D))[w];
+#pragma unroll
+        for (int r = 0; r < WPT; r++) {
+            const int w = tid + 256 * r;
+            if (w < nt * (D / 8)) vt[w] = nv[r];
+        }
         __syncthreads();
+        if (q0 + TP < nk) fetch(q0 + TP);
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             const int k = tid + 256 * c;
@@ -590,12 +632,22 @@ __global__ __launch_bounds__(256) void k_pf_attn(pf_attn_args a) {
                 const int hh = k / D, i = k - hh * D;
                 const float* av = sc + (size_t)hh * nks + q0;
                 float acc = o[c];
-                for (int t = 0; t < nt; t++) acc = fmaf(av[t], h2f(vh[t * D + i]), acc);
+                if (nt == TP) {   // a full tile: every operand requested before the chain runs
+                    float aa[TP], vv[TP];
+#pragma unroll
+                    for (int t = 0; t < TP; t++) {
+                        aa[t] = av[t];
+                        vv[t] = h2f(vh[t * D + i]);
+                    }
+#pragma unroll
+                    for (int t = 0; t < TP; t++) acc = fmaf(aa[t], vv[t], acc);
+                } else {
+                    for (int t = 0; t < nt; t++) acc = fmaf(av[t], h2f(vh[t * D + i]), acc);
+                }
                 o[c] = acc;
             }
         }
     }
-    (void)TW;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
         const int k = tid + 256 * c;
@@ -614,10 +666,11 @@ __global__ __launch_bounds__(256) void k_pf_attn(pf_attn_args a) {
 
 hipError_t launch_pf_rows(int mode, const pf_rows_args& a, hipStream_t s) {
     if (a.E % 32 || a.E > 2048 || a.n < 1) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((a.n + 3) / 4));
     if (mode == PFR_FIRST)
-        hipLaunchKernelGGL(k_pf_rows<PFR_FIRST>, dim3(a.n), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(k_pf_rows<PFR_FIRST>, grid, dim3(256), 0, s, a);
     else
-        hipLaunchKernelGGL(k_pf_rows<PFR_RESID>, dim3(a.n), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(k_pf_rows<PFR_RESID>, grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
