@@ -529,6 +529,13 @@ def main():
     vec_bytes = brain.vector_bytes
     gen_bytes = sum(brain.table_bytes + vec_bytes + 2 * kv_row * (PROMPT + i + 1) for i in range(args.steps))
     step_bytes = gen_bytes / args.steps
+    # what the dispatch path and HBM allow a kernel reading the cfg-0 table's bytes: an empty 1024 x 256 kernel and a
+    # pure read of 9,437,184 bytes (64 copies in rotation: every launch from HBM), each back to back on one stream
+    e_us = nunchi_amd.bench_empty(grid=1024, reps=1000)
+    r_us = nunchi_amd.bench_read(9437184, copies=64, grid=1152, reps=256)
+    cfg0_floor = {"empty_kernel_us": round(e_us, 3), "pure_read_us": round(r_us, 3),
+                  "pure_read_GBs": round(9437184 / r_us / 1e3, 1), "pure_read_frac": round(9437184 / r_us / 1e3 / HBM_PEAK_GBS, 4),
+                  "gemv_over_pure_read": round(cfg0_us / r_us, 3)}
     line = {
         "metric": "brain-step tokens/s (B=1,2) + Q4_0 GEMV HBM GB/s vs roofline, 1 MI355X",
         "value": round(tok_s_b1, 1),
@@ -596,7 +603,8 @@ def main():
                                     "frac": round(cfg0_bytes / cfg0_us / 1e3 / HBM_PEAK_GBS, 4),
                                     "kernel_us": round(cfg0_kernel_us, 3),
                                     "kernel_GBs": round(cfg0_bytes / cfg0_kernel_us / 1e3, 1),
-                                    "kernel_frac": round(cfg0_bytes / cfg0_kernel_us / 1e3 / HBM_PEAK_GBS, 4)},
+                                    "kernel_frac": round(cfg0_bytes / cfg0_kernel_us / 1e3 / HBM_PEAK_GBS, 4),
+                                    "floor": cfg0_floor},
         },
     }
     if args.prefill_reps:

@@ -227,6 +227,14 @@ int sh_q4_bench(sh_ctx* ctx, sh_q4* const* tables, int n_tables, int n_in, int c
  * front of it), averaged over `reps`; after sh_q4_bench on the same tables (which sizes the device input/output). */
 int sh_q4_bench_kernel(sh_ctx* ctx, sh_q4* const* tables, int n_tables, int n_in, int cut_mode, int reps, double* avg_kernel_us);
 
+/* Calibration: an empty kernel of `grid` x 256 threads launched `reps` times back to back on one stream (the
+ * dispatch cost any kernel pays), and a pure read of `bytes` (copies distinct buffers in rotation, so with
+ * copies * bytes above the 256 MB last-level cache every launch reads HBM; 2 x 16-byte loads in flight per thread,
+ * grid x 256 threads): microseconds per launch. No counterpart in the reference; they bound what a kernel reading the
+ * same bytes can reach. */
+int sh_bench_empty(int device, int grid, int reps, double* us_per_launch);
+int sh_bench_read(int device, long long bytes, int copies, int grid, int reps, double* us_per_launch);
+
 /* y[i] = e^x[i] with the exponential the kernels use (softmax, SiLU, head gates): bit for bit the C library's expf
  * that imi runs on (imi/core/seoul.cpp:48,447,451). */
 int sh_expf(sh_ctx* ctx, const float* x, long long n, float* y);

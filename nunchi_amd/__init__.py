@@ -29,6 +29,7 @@ EXPORTS = [
     "sh_file_n_tensors", "sh_file_tensor", "sh_file_key_arr", "sh_file_block",
     "sh_codec_load", "sh_codec_free", "sh_codec_info", "sh_codec_reset", "sh_codec_frame", "sh_codec_flush",
     "sh_ears_load", "sh_ears_free", "sh_ears_info", "sh_ears_positions", "sh_ears_encode", "sh_ears_mel",
+    "sh_bench_empty", "sh_bench_read",
 ]
 
 
@@ -136,6 +137,8 @@ def load_library(path: str = LIB_PATH):
         "sh_codec_reset": (i, [vp]),
         "sh_codec_frame": (i, [vp, vp, vp, P(i)]),
         "sh_codec_flush": (i, [vp, vp, P(i)]),
+        "sh_bench_empty": (i, [i, i, i, P(d)]),
+        "sh_bench_read": (i, [i, C.c_longlong, i, i, i, P(d)]),
         "sh_ears_load": (i, [i, C.c_char_p, P(vp)]),
         "sh_ears_free": (i, [vp]),
         "sh_ears_info": (i, [vp, P(EarsShape)]),
@@ -450,6 +453,22 @@ class Q4Table:
         y = np.zeros((x.shape[0], self.rows), np.float32)
         _check(_lib.sh_q4_gemm(self.ctx.h, self.h, _p(x), int(x.shape[0]), _p(y)))
         return y
+
+
+def bench_empty(device: int = 0, grid: int = 1024, reps: int = 1000) -> float:
+    """Microseconds per launch of an empty grid x 256 kernel, back to back on one stream."""
+    L = load_library()
+    us = C.c_double()
+    _check(L.sh_bench_empty(int(device), int(grid), int(reps), C.byref(us)))
+    return us.value
+
+
+def bench_read(nbytes: int, copies: int = 64, grid: int = 1152, reps: int = 256, device: int = 0) -> float:
+    """Microseconds per launch of a pure read of nbytes (copies distinct buffers in rotation), back to back."""
+    L = load_library()
+    us = C.c_double()
+    _check(L.sh_bench_read(int(device), int(nbytes), int(copies), int(grid), int(reps), C.byref(us)))
+    return us.value
 
 
 def q4_bench(ctx: Context, tables, n_in: int = 1, cut_mode: int = 0, reps: int = 200) -> float:

@@ -12,7 +12,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "libseoul_hip.so")
 SOURCES = ["csrc/sh_kernels.hip", "csrc/sh_voice.hip", "csrc/sh_prefill.hip", "csrc/sh_noalloc.hip", "csrc/sh_codec.hip",
-           "csrc/sh_ears.hip", "csrc/sh_engine.cpp", "csrc/sh_codec_host.cpp", "csrc/sh_ears_host.cpp",
+           "csrc/sh_ears.hip", "csrc/sh_calib.hip", "csrc/sh_engine.cpp", "csrc/sh_codec_host.cpp", "csrc/sh_ears_host.cpp",
            "csrc/sh_voice_host.cpp", "csrc/sh_prefill_host.cpp", "csrc/gguf_file.cpp", "csrc/sh_file.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

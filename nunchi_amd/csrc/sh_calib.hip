@@ -1,0 +1,109 @@
+// Calibration launches for the measurements: the cost of an empty dispatch and of a pure read of a buffer the size of
+// a table, each launched back to back on one stream, so a kernel's time can be set against what the dispatch path and
+// HBM allow for the same bytes.
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "../../include/seoul_hip.h"
+
+namespace sh {
+int set_error(int code, const std::string& msg);
+}
+using namespace sh;
+
+namespace {
+
+__global__ __launch_bounds__(256) void k_empty(unsigned* out) {
+    if (threadIdx.x > 1024) out[0] = 0;   // never true (256 threads): a dispatch with no work
+}
+
+// grid-stride read of n 16-byte words, 2 in flight per thread; one word of xor per workgroup (keeps the loads live)
+__global__ __launch_bounds__(256) void k_read(const uint4* __restrict__ a, size_t n, unsigned* out) {
+    const size_t stride = (size_t)gridDim.x * 512;
+    unsigned acc = 0;
+    for (size_t i = (size_t)blockIdx.x * 512 + threadIdx.x; i < n; i += stride) {
+        const uint4 v0 = a[i];
+        const uint4 v1 = i + 256 < n ? a[i + 256] : uint4{0, 0, 0, 0};
+        acc ^= v0.x ^ v0.y ^ v0.z ^ v0.w ^ v1.x ^ v1.y ^ v1.z ^ v1.w;
+    }
+    for (int o = 32; o > 0; o >>= 1) acc ^= __shfl_xor(acc, o);
+    __shared__ unsigned red[4];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) out[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
+}
+
+#define KCHK(x)                                                                                                 \
+    do {                                                                                                        \
+        const hipError_t e_ = (x);                                                                              \
+        if (e_ != hipSuccess) { err = e_; goto done; }                                                          \
+    } while (0)
+
+}  // namespace
+
+extern "C" {
+
+int sh_bench_empty(int device, int grid, int reps, double* us_per_launch) {
+    if (grid < 1 || grid > 65536 || reps < 1 || !us_per_launch) return set_error(SH_E_ARG, "sh_bench_empty: bad argument");
+    if (hipSetDevice(device) != hipSuccess) return set_error(SH_E_HIP, "sh_bench_empty: device");
+    hipError_t err = hipSuccess;
+    unsigned* out = nullptr;
+    hipStream_t s = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    float ms = 0;
+    KCHK(hipMalloc((void**)&out, 4));
+    KCHK(hipStreamCreate(&s));
+    KCHK(hipEventCreate(&e0));
+    KCHK(hipEventCreate(&e1));
+    for (int i = 0; i < 16; i++) hipLaunchKernelGGL(k_empty, dim3(grid), dim3(256), 0, s, out);
+    KCHK(hipEventRecord(e0, s));
+    for (int i = 0; i < reps; i++) hipLaunchKernelGGL(k_empty, dim3(grid), dim3(256), 0, s, out);
+    KCHK(hipEventRecord(e1, s));
+    KCHK(hipEventSynchronize(e1));
+    KCHK(hipEventElapsedTime(&ms, e0, e1));
+    *us_per_launch = 1e3 * ms / reps;
+done:
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (s) (void)hipStreamDestroy(s);
+    if (out) (void)hipFree(out);
+    return err == hipSuccess ? SH_OK : set_error(SH_E_HIP, std::string("sh_bench_empty: ") + hipGetErrorString(err));
+}
+
+int sh_bench_read(int device, long long bytes, int copies, int grid, int reps, double* us_per_launch) {
+    if (bytes < 16 || bytes % 16 || copies < 1 || (long long)copies * bytes > (4ll << 30) || grid < 1 || grid > 65536 ||
+        reps < 1 || !us_per_launch)
+        return set_error(SH_E_ARG, "sh_bench_read: bad argument (bytes a multiple of 16, copies * bytes <= 4 GiB)");
+    if (hipSetDevice(device) != hipSuccess) return set_error(SH_E_HIP, "sh_bench_read: device");
+    hipError_t err = hipSuccess;
+    uint4* a = nullptr;
+    unsigned* out = nullptr;
+    hipStream_t s = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    float ms = 0;
+    const size_t n = (size_t)bytes / 16;
+    KCHK(hipMalloc((void**)&a, (size_t)bytes * copies));
+    KCHK(hipMemset(a, 1, (size_t)bytes * copies));
+    KCHK(hipMalloc((void**)&out, (size_t)grid * 4));
+    KCHK(hipStreamCreate(&s));
+    KCHK(hipEventCreate(&e0));
+    KCHK(hipEventCreate(&e1));
+    for (int c = 0; c < copies; c++) hipLaunchKernelGGL(k_read, dim3(grid), dim3(256), 0, s, a + (size_t)c * n, n, out);
+    KCHK(hipEventRecord(e0, s));
+    for (int r = 0; r < reps; r++)
+        hipLaunchKernelGGL(k_read, dim3(grid), dim3(256), 0, s, a + (size_t)(r % copies) * n, n, out);
+    KCHK(hipEventRecord(e1, s));
+    KCHK(hipEventSynchronize(e1));
+    KCHK(hipEventElapsedTime(&ms, e0, e1));
+    *us_per_launch = 1e3 * ms / reps;
+done:
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (s) (void)hipStreamSynchronize(s), (void)hipStreamDestroy(s);
+    if (out) (void)hipFree(out);
+    if (a) (void)hipFree(a);
+    return err == hipSuccess ? SH_OK : set_error(SH_E_HIP, std::string("sh_bench_read: ") + hipGetErrorString(err));
+}
+
+}  // extern "C"

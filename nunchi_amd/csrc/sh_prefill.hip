@@ -259,7 +259,7 @@ __global__ __launch_bounds__(256) void k_pf_gemm(pf_gemm_args a) {
 // PW positions: PW = 32 for tables with enough rows, 16 for the narrow ones (2048 rows: two waves per SIMD instead of
 // one), whose matrix-core blocks for the missing position tile are computed on a repeated position and dropped.
 template <int EPI, bool HM, int KC, int PW>
-__global__ __launch_bounds__(256, KC == 4 ? 3 : 2) void k_pf_gemm_lds(pf_gemm_args a) {
+__global__ __launch_bounds__(256, (KC == 4 && PW == 32) ? 3 : 2) void k_pf_gemm_lds(pf_gemm_args a) {
     typedef float v16f __attribute__((ext_vector_type(16)));
     constexpr int P = 2 * PW, NTW = PW / 16;          // positions per workgroup; 16-position tiles per wave
     constexpr int SA = 8 * KC + 2;                    // dwords per row: 32 nibble bytes per block + 2 (bank spread)
@@ -357,7 +357,9 @@ __global__ __launch_bounds__(256, KC == 4 ? 3 : 2) void k_pf_gemm_lds(pf_gemm_ar
     for (int c = 0; c < nch; c++) {
         const int buf = c & 1;
         if (c + 1 < nch) fetch(c + 1);
-#pragma unroll 2
+        // the narrow tiles (fewer than 2 workgroups per CU) take a whole chunk's blocks in one unrolled body, their
+        // LDS reads and matrix-core products all issued ahead of the chains (the register room 2 workgroups per CU allow)
+#pragma unroll(PW == 16 ? KC : 2)
         for (int jb = 0; jb < KC; jb++) {
             i32x4 isum[2][NTW];
             long cb[NTW];

@@ -171,3 +171,12 @@ def test_bad_arguments_rejected(ctx):
     t = nunchi_amd.Q4Table(ctx, blk, 8, 64)
     with pytest.raises(nunchi_amd.SeoulError):
         t.rows_dequant([8])
+
+
+def test_calibration_launches():
+    """The dispatch and pure-read calibration launches run and refuse bad sizes."""
+    import nunchi_amd
+    assert 0.0 < nunchi_amd.bench_empty(grid=64, reps=20) < 1e4
+    assert 0.0 < nunchi_amd.bench_read(1 << 20, copies=2, grid=64, reps=8) < 1e5
+    with pytest.raises(nunchi_amd.SeoulError):
+        nunchi_amd.bench_read(1000, copies=2)   # not a multiple of 16
