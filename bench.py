@@ -417,6 +417,10 @@ def main():
     ap.add_argument("--codec-only", type=int, default=0, metavar="FRAMES",
                     help="only FRAMES codec frames (seeded codes, after 4 untimed), no brain: the launches a kernel "
                          "trace of the codec reads")
+    ap.add_argument("--floor-only", action="store_true",
+                    help="only the cfg-0 GEMV (8192 x 2048 Q4_0, 64 copies in rotation) next to an empty dispatch and a "
+                         "pure read of the same 9,437,184 bytes, each back to back: the launches a kernel trace of the "
+                         "floor reads")
     ap.add_argument("--counters-workload", action="store_true",
                     help="only the launches the hardware-counter runs read: a streaming kernel of known size (the "
                          "exponential over 16 Mi floats: 64 MiB read, 64 MiB written), 64 read-only GEMVs of known "
@@ -433,6 +437,18 @@ def main():
 
     import nunchi_amd
     from nunchi_amd import synth
+    if args.floor_only:
+        ctx = nunchi_amd.Context()
+        copies = [nunchi_amd.Q4Table(ctx, synth.q4_0_random(np.random.default_rng(100 + i), 8192, 2048), 8192, 2048)
+                  for i in range(64)]
+        g_us = nunchi_amd.q4_bench(ctx, copies, n_in=1, cut_mode=1, reps=640)
+        e_us = nunchi_amd.bench_empty(grid=1024, reps=1000)
+        r_us, st = nunchi_amd.bench_read(9437184, copies=64, grid=1152, reps=640, stamps=True)
+        print(json.dumps({"floor_only": {"gemv_us": round(g_us, 3), "empty_kernel_us": round(e_us, 3),
+                                         "pure_read_us": round(r_us, 3), "pure_read_last_start_us": round(st[0], 2),
+                                         "pure_read_first_bytes_us": round(st[1], 2),
+                                         "pure_read_last_end_us": round(st[2], 2)}}), flush=True)
+        return
     if args.ears_only:
         ears = nunchi_amd.Ears(synth.cached("ears", synth.EARS, 3))
         pcm = synth.clip(HEAR_SAMPLES, 1)
@@ -532,8 +548,10 @@ def main():
     # what the dispatch path and HBM allow a kernel reading the cfg-0 table's bytes: an empty 1024 x 256 kernel and a
     # pure read of 9,437,184 bytes (64 copies in rotation: every launch from HBM), each back to back on one stream
     e_us = nunchi_amd.bench_empty(grid=1024, reps=1000)
-    r_us = nunchi_amd.bench_read(9437184, copies=64, grid=1152, reps=256)
+    r_us, r_st = nunchi_amd.bench_read(9437184, copies=64, grid=1152, reps=256, stamps=True)
     cfg0_floor = {"empty_kernel_us": round(e_us, 3), "pure_read_us": round(r_us, 3),
+                  "pure_read_timeline_us": {"last_wg_start": round(r_st[0], 2), "first_bytes_p50": round(r_st[1], 2),
+                                            "last_wg_end": round(r_st[2], 2)},
                   "pure_read_GBs": round(9437184 / r_us / 1e3, 1), "pure_read_frac": round(9437184 / r_us / 1e3 / HBM_PEAK_GBS, 4),
                   "gemv_over_pure_read": round(cfg0_us / r_us, 3)}
     line = {

@@ -230,10 +230,12 @@ int sh_q4_bench_kernel(sh_ctx* ctx, sh_q4* const* tables, int n_tables, int n_in
 /* Calibration: an empty kernel of `grid` x 256 threads launched `reps` times back to back on one stream (the
  * dispatch cost any kernel pays), and a pure read of `bytes` (copies distinct buffers in rotation, so with
  * copies * bytes above the 256 MB last-level cache every launch reads HBM; 2 x 16-byte loads in flight per thread,
- * grid x 256 threads): microseconds per launch. No counterpart in the reference; they bound what a kernel reading the
- * same bytes can reach. */
+ * grid x 256 threads): microseconds per launch. stamps (nullable, 3 doubles) gets one more launch's timeline from the
+ * device clock: the last workgroup's start, the median workgroup's first loads back, the last workgroup's end, each in
+ * microseconds after the first workgroup started. No counterpart in the reference; they bound what a kernel reading
+ * the same bytes can reach. */
 int sh_bench_empty(int device, int grid, int reps, double* us_per_launch);
-int sh_bench_read(int device, long long bytes, int copies, int grid, int reps, double* us_per_launch);
+int sh_bench_read(int device, long long bytes, int copies, int grid, int reps, double* us_per_launch, double* stamps);
 
 /* y[i] = e^x[i] with the exponential the kernels use (softmax, SiLU, head gates): bit for bit the C library's expf
  * that imi runs on (imi/core/seoul.cpp:48,447,451). */

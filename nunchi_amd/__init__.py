@@ -138,7 +138,7 @@ def load_library(path: str = LIB_PATH):
         "sh_codec_frame": (i, [vp, vp, vp, P(i)]),
         "sh_codec_flush": (i, [vp, vp, P(i)]),
         "sh_bench_empty": (i, [i, i, i, P(d)]),
-        "sh_bench_read": (i, [i, C.c_longlong, i, i, i, P(d)]),
+        "sh_bench_read": (i, [i, C.c_longlong, i, i, i, P(d), vp]),
         "sh_ears_load": (i, [i, C.c_char_p, P(vp)]),
         "sh_ears_free": (i, [vp]),
         "sh_ears_info": (i, [vp, P(EarsShape)]),
@@ -463,12 +463,16 @@ def bench_empty(device: int = 0, grid: int = 1024, reps: int = 1000) -> float:
     return us.value
 
 
-def bench_read(nbytes: int, copies: int = 64, grid: int = 1152, reps: int = 256, device: int = 0) -> float:
-    """Microseconds per launch of a pure read of nbytes (copies distinct buffers in rotation), back to back."""
+def bench_read(nbytes: int, copies: int = 64, grid: int = 1152, reps: int = 256, device: int = 0, stamps: bool = False):
+    """Microseconds per launch of a pure read of nbytes (copies distinct buffers in rotation), back to back; with
+    stamps, also one launch's (last workgroup start, median first loads back, last workgroup end) in microseconds after
+    the first workgroup started."""
     L = load_library()
     us = C.c_double()
-    _check(L.sh_bench_read(int(device), int(nbytes), int(copies), int(grid), int(reps), C.byref(us)))
-    return us.value
+    st = np.zeros(3, np.float64)
+    _check(L.sh_bench_read(int(device), int(nbytes), int(copies), int(grid), int(reps), C.byref(us),
+                           st.ctypes.data if stamps else None))
+    return (us.value, tuple(float(v) for v in st)) if stamps else us.value
 
 
 def q4_bench(ctx: Context, tables, n_in: int = 1, cut_mode: int = 0, reps: int = 200) -> float:

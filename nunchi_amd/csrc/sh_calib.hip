@@ -3,7 +3,9 @@
 // HBM allow for the same bytes.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <string>
+#include <vector>
 
 #include "../../include/seoul_hip.h"
 
@@ -18,20 +20,32 @@ __global__ __launch_bounds__(256) void k_empty(unsigned* out) {
     if (threadIdx.x > 1024) out[0] = 0;   // never true (256 threads): a dispatch with no work
 }
 
-// grid-stride read of n 16-byte words, 2 in flight per thread; one word of xor per workgroup (keeps the loads live)
-__global__ __launch_bounds__(256) void k_read(const uint4* __restrict__ a, size_t n, unsigned* out) {
+// grid-stride read of n 16-byte words, 2 in flight per thread; one word of xor per workgroup (keeps the loads live).
+// With st: thread 0 of each workgroup records the 100 MHz real-time clock at its start, when its first loads are back,
+// and at its end.
+__global__ __launch_bounds__(256) void k_read(const uint4* __restrict__ a, size_t n, unsigned* out, unsigned long long* st) {
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    unsigned long long t1 = 0;
     const size_t stride = (size_t)gridDim.x * 512;
     unsigned acc = 0;
     for (size_t i = (size_t)blockIdx.x * 512 + threadIdx.x; i < n; i += stride) {
         const uint4 v0 = a[i];
         const uint4 v1 = i + 256 < n ? a[i + 256] : uint4{0, 0, 0, 0};
         acc ^= v0.x ^ v0.y ^ v0.z ^ v0.w ^ v1.x ^ v1.y ^ v1.z ^ v1.w;
+        if (t1 == 0) t1 = __builtin_amdgcn_s_memrealtime() | 1;   // (after the loads' data is used)
     }
     for (int o = 32; o > 0; o >>= 1) acc ^= __shfl_xor(acc, o);
     __shared__ unsigned red[4];
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
     __syncthreads();
-    if (threadIdx.x == 0) out[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
+    if (threadIdx.x == 0) {
+        out[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
+        if (st) {
+            st[3 * blockIdx.x] = t0;
+            st[3 * blockIdx.x + 1] = t1 ? t1 : t0;
+            st[3 * blockIdx.x + 2] = __builtin_amdgcn_s_memrealtime();
+        }
+    }
 }
 
 #define KCHK(x)                                                                                                 \
@@ -71,7 +85,7 @@ done:
     return err == hipSuccess ? SH_OK : set_error(SH_E_HIP, std::string("sh_bench_empty: ") + hipGetErrorString(err));
 }
 
-int sh_bench_read(int device, long long bytes, int copies, int grid, int reps, double* us_per_launch) {
+int sh_bench_read(int device, long long bytes, int copies, int grid, int reps, double* us_per_launch, double* stamps) {
     if (bytes < 16 || bytes % 16 || copies < 1 || (long long)copies * bytes > (4ll << 30) || grid < 1 || grid > 65536 ||
         reps < 1 || !us_per_launch)
         return set_error(SH_E_ARG, "sh_bench_read: bad argument (bytes a multiple of 16, copies * bytes <= 4 GiB)");
@@ -79,6 +93,8 @@ int sh_bench_read(int device, long long bytes, int copies, int grid, int reps, d
     hipError_t err = hipSuccess;
     uint4* a = nullptr;
     unsigned* out = nullptr;
+    unsigned long long* st = nullptr;
+    std::vector<unsigned long long> h;
     hipStream_t s = nullptr;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     float ms = 0;
@@ -89,19 +105,40 @@ int sh_bench_read(int device, long long bytes, int copies, int grid, int reps, d
     KCHK(hipStreamCreate(&s));
     KCHK(hipEventCreate(&e0));
     KCHK(hipEventCreate(&e1));
-    for (int c = 0; c < copies; c++) hipLaunchKernelGGL(k_read, dim3(grid), dim3(256), 0, s, a + (size_t)c * n, n, out);
+    KCHK(hipMalloc((void**)&st, (size_t)grid * 24));
+    for (int c = 0; c < copies; c++)
+        hipLaunchKernelGGL(k_read, dim3(grid), dim3(256), 0, s, a + (size_t)c * n, n, out, (unsigned long long*)nullptr);
     KCHK(hipEventRecord(e0, s));
     for (int r = 0; r < reps; r++)
-        hipLaunchKernelGGL(k_read, dim3(grid), dim3(256), 0, s, a + (size_t)(r % copies) * n, n, out);
+        hipLaunchKernelGGL(k_read, dim3(grid), dim3(256), 0, s, a + (size_t)(r % copies) * n, n, out, (unsigned long long*)nullptr);
     KCHK(hipEventRecord(e1, s));
     KCHK(hipEventSynchronize(e1));
     KCHK(hipEventElapsedTime(&ms, e0, e1));
     *us_per_launch = 1e3 * ms / reps;
+    if (stamps) {   // one more launch (the next copy in rotation, from HBM), stamped
+        hipLaunchKernelGGL(k_read, dim3(grid), dim3(256), 0, s, a + (size_t)(reps % copies) * n, n, out, st);
+        KCHK(hipStreamSynchronize(s));
+        h.resize((size_t)3 * grid);
+        KCHK(hipMemcpy(h.data(), st, h.size() * 8, hipMemcpyDeviceToHost));
+        unsigned long long s0 = ~0ull, s0max = 0, emax = 0;
+        std::vector<double> first;
+        for (int g = 0; g < grid; g++) {
+            s0 = std::min(s0, h[3 * g]);
+            s0max = std::max(s0max, h[3 * g]);
+            emax = std::max(emax, h[3 * g + 2]);
+            first.push_back(0.01 * (double)(h[3 * g + 1] - h[3 * g]));
+        }
+        std::sort(first.begin(), first.end());
+        stamps[0] = 0.01 * (double)(s0max - s0);        // last workgroup start, after the first
+        stamps[1] = first[first.size() / 2];            // first loads back (median over workgroups)
+        stamps[2] = 0.01 * (double)(emax - s0);         // last workgroup end, after the first start
+    }
 done:
     if (e0) (void)hipEventDestroy(e0);
     if (e1) (void)hipEventDestroy(e1);
     if (s) (void)hipStreamSynchronize(s), (void)hipStreamDestroy(s);
     if (out) (void)hipFree(out);
+    if (st) (void)hipFree(st);
     if (a) (void)hipFree(a);
     return err == hipSuccess ? SH_OK : set_error(SH_E_HIP, std::string("sh_bench_read: ") + hipGetErrorString(err));
 }
