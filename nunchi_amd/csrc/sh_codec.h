@@ -75,6 +75,7 @@ struct cistft_args {
     float* ola;              // [n_fft] carried
     float* wsum;             // [n_fft] carried
     float* pcm;              // [P][hop] samples before the start trim
+    float* frames;           // [P][n_fft] work: each STFT frame's inverse transform, real part / n_fft
 };
 
 hipError_t launch_cfsq(const cfsq_args& a, hipStream_t s);

@@ -93,6 +93,7 @@ __global__ __launch_bounds__(CX_NT) void k_cattn(cattn_args a) {
     constexpr int W1 = CX_WIN - 1, NK = W1 + CX_P;
     __shared__ float K[NK][CX_MAX_D], V[NK][CX_MAX_D], Q[CX_P][CX_MAX_D];
     __shared__ float xs[CX_P][CX_MAX_E];
+    __shared__ float gws[CX_MAX_E], l1s[CX_MAX_E];
     __shared__ float sc[CX_P][CX_WIN];
     __shared__ float sm[CX_P], gt[CX_P], hs[CX_P];
     const int hh = blockIdx.x, grp = a.n_head / a.n_kv, kv = hh / grp, D = a.D, E = a.E, t = threadIdx.x;
@@ -118,6 +119,10 @@ __global__ __launch_bounds__(CX_NT) void k_cattn(cattn_args a) {
     for (int i = t; i < CX_P * E; i += CX_NT) {
         const int p = i / E, e = i - p * E;
         xs[p][e] = a.x[(size_t)p * E + e];
+    }
+    for (int e = t; e < E; e += CX_NT) {   // the head gate's operands, for its in-order chain
+        gws[e] = a.gate_w[(size_t)hh * E + e];
+        l1s[e] = a.ln1[e];
     }
     __syncthreads();
     for (int ri = w; ri < 3 * CX_P; ri += CX_NT / 64) {   // the frame's keys, the queries, the input rows' scales
@@ -159,9 +164,8 @@ __global__ __launch_bounds__(CX_NT) void k_cattn(cattn_args a) {
     if (t >= 64 && t < 64 + CX_P) {   // head gate of position p (a wave the score threads leave free)
         const int p = t - 64;
         const float s = hs[p];
-        const float* gw = a.gate_w + (size_t)hh * E;
         float g = 0.0f;
-        for (int e = 0; e < E; e++) g = fmaf(gw[e], xs[p][e] * s * a.ln1[e], g);
+        for (int e = 0; e < E; e++) g = fmaf(gws[e], xs[p][e] * s * l1s[e], g);
         gt[p] = 1.0f / (1.0f + expf_glibc(-g));
     }
     __syncthreads();
@@ -204,52 +208,59 @@ __device__ __forceinline__ float2 cmul(float2 a, float2 b) { return float2{fmaf(
 __device__ __forceinline__ float2 cadd(float2 a, float2 b) { return float2{a.x + b.x, a.y + b.y}; }
 __device__ __forceinline__ float2 csub(float2 a, float2 b) { return float2{a.x - b.x, a.y - b.y}; }
 
-// one workgroup runs the frame's 6 STFT frames in order (the overlap carries between them). Per frame: the spectrum
+// one workgroup per STFT frame p (the frames are independent until the overlap-add): the spectrum
 // X_k = polar(expf(l_k), phi_k) and its conjugate mirror; the inverse DFT as imi's recursion computes it, unrolled
 // into stages: the 256 five-point sums (leaf L reads elements bitrev8(L) + 256 j, j = 0 .. 4, with twiddles
-// ((j k) % 5) * 256) and 8 butterfly levels (node size 1280 >> d uses twiddles k << d); then the windowed
-// overlap-add, hop samples out, and the overlap shifted by hop.
-__global__ __launch_bounds__(1024) void k_cistft(cistft_args a) {
+// ((j k) % 5) * 256) and 8 butterfly levels (node size 1280 >> d uses twiddles k << d); the real part / n_fft
+// into frames[p]
+__global__ __launch_bounds__(1024) void k_cifft(cistft_args a) {
     __shared__ float2 X[CX_NFFT], O[CX_NFFT], tw[CX_NFFT];
+    const int t = threadIdx.x, p = blockIdx.x;
+    for (int i = t; i < CX_NFFT; i += 1024) tw[i] = a.tw[i];
+    const float* lp = a.spec + (size_t)p * 2 * CX_NB;
+    for (int k = t; k < CX_NB; k += 1024) {
+        const float r = expf_glibc(lp[k] + a.bias[k]);
+        const double ph = (double)(lp[CX_NB + k] + a.bias[CX_NB + k]);
+        X[k] = float2{r * (float)cos(ph), r * (float)sin(ph)};
+    }
+    __syncthreads();
+    for (int k = t + 1; k < CX_NB - 1; k += 1024) X[CX_NFFT - k] = float2{X[k].x, -X[k].y};
+    __syncthreads();
+    for (int m = t; m < CX_NFFT; m += 1024) {
+        const int L = m / 5, k = m - 5 * L, off = (int)(__builtin_bitreverse32((unsigned)L) >> 24);
+        float2 s = float2{0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < 5; j++) s = cadd(s, cmul(X[off + 256 * j], tw[((j * k) % 5) * 256]));
+        O[m] = s;
+    }
+    __syncthreads();
+    for (int d = 7; d >= 0; d--) {
+        const int n = CX_NFFT >> d, h = n >> 1;
+        if (t < CX_NFFT / 2) {
+            const int node = t / h, k = t - node * h, base = node * n;
+            const float2 e = O[base + k], o = cmul(O[base + k + h], tw[k << d]);
+            O[base + k] = cadd(e, o);
+            O[base + k + h] = csub(e, o);
+        }
+        __syncthreads();
+    }
+    for (int j = t; j < CX_NFFT; j += 1024) a.frames[(size_t)p * CX_NFFT + j] = O[j].x / (float)CX_NFFT;
+}
+
+// the overlap-add of the frame's P STFT frames in order (codec.cpp:262-269): ola += frame * hann, wsum += hann^2,
+// hop samples out (ola / wsum where wsum > 1e-8), then both shifted by hop
+__global__ __launch_bounds__(1024) void k_cola(cistft_args a) {
     __shared__ float hn[CX_NFFT], ol[CX_NFFT], ws[CX_NFFT];
     const int t = threadIdx.x;
     for (int i = t; i < CX_NFFT; i += 1024) {
-        tw[i] = a.tw[i];
         hn[i] = a.hann[i];
         ol[i] = a.ola[i];
         ws[i] = a.wsum[i];
     }
     __syncthreads();
     for (int p = 0; p < CX_P; p++) {
-        const float* lp = a.spec + (size_t)p * 2 * CX_NB;
-        for (int k = t; k < CX_NB; k += 1024) {
-            const float r = expf_glibc(lp[k] + a.bias[k]);
-            const double ph = (double)(lp[CX_NB + k] + a.bias[CX_NB + k]);
-            X[k] = float2{r * (float)cos(ph), r * (float)sin(ph)};
-        }
-        __syncthreads();
-        for (int k = t + 1; k < CX_NB - 1; k += 1024) X[CX_NFFT - k] = float2{X[k].x, -X[k].y};
-        __syncthreads();
-        for (int m = t; m < CX_NFFT; m += 1024) {
-            const int L = m / 5, k = m - 5 * L, off = (int)(__builtin_bitreverse32((unsigned)L) >> 24);
-            float2 s = float2{0.0f, 0.0f};
-#pragma unroll
-            for (int j = 0; j < 5; j++) s = cadd(s, cmul(X[off + 256 * j], tw[((j * k) % 5) * 256]));
-            O[m] = s;
-        }
-        __syncthreads();
-        for (int d = 7; d >= 0; d--) {
-            const int n = CX_NFFT >> d, h = n >> 1;
-            if (t < CX_NFFT / 2) {
-                const int node = t / h, k = t - node * h, base = node * n;
-                const float2 e = O[base + k], o = cmul(O[base + k + h], tw[k << d]);
-                O[base + k] = cadd(e, o);
-                O[base + k + h] = csub(e, o);
-            }
-            __syncthreads();
-        }
         for (int j = t; j < CX_NFFT; j += 1024) {
-            ol[j] = fmaf(O[j].x / (float)CX_NFFT, hn[j], ol[j]);
+            ol[j] = fmaf(a.frames[(size_t)p * CX_NFFT + j], hn[j], ol[j]);
             ws[j] = fmaf(hn[j], hn[j], ws[j]);
         }
         __syncthreads();
@@ -302,7 +313,8 @@ hipError_t launch_cresid(const cresid_args& a, hipStream_t s) {
     return hipGetLastError();
 }
 hipError_t launch_cistft(const cistft_args& a, hipStream_t s) {
-    hipLaunchKernelGGL(k_cistft, dim3(1), dim3(1024), 0, s, a);
+    hipLaunchKernelGGL(k_cifft, dim3(CX_P), dim3(1024), 0, s, a);
+    hipLaunchKernelGGL(k_cola, dim3(1), dim3(1024), 0, s, a);
     return hipGetLastError();
 }
 

@@ -51,6 +51,7 @@ struct sh_codec {
     const float* hann = nullptr;
     float *ola = nullptr, *wsum = nullptr;
     float *v = nullptr, *x = nullptr, *big = nullptr, *u = nullptr, *act = nullptr, *y = nullptr, *spec = nullptr, *pcm = nullptr;
+    float* frames = nullptr;   // [P][n_fft] the frame's inverse transforms before the overlap-add
     size_t state_bytes = 0;
     char* state = nullptr;                     // conv memory, rings, overlap: cleared by reset
     cframe_in* in_dev = nullptr;
@@ -109,7 +110,7 @@ int enqueue_frame(sh_codec* c) {
         CCHK(launch_cresid(cresid_args{c->y, L.post2, c->x, E, c->eps}, c->stream));
     }
     CCHK(tab(c->out_proj, VP_NORM, VE_STORE, c->x, E, c->out_norm, c->spec, 2 * I.n_bins));
-    CCHK(launch_cistft(cistft_args{c->spec, c->out_b, c->tw, c->hann, c->ola, c->wsum, c->pcm}, c->stream));
+    CCHK(launch_cistft(cistft_args{c->spec, c->out_b, c->tw, c->hann, c->ola, c->wsum, c->pcm, c->frames}, c->stream));
     return SH_OK;
 }
 
@@ -279,6 +280,7 @@ int sh_codec_load(int device, const char* path, sh_codec** out) {   // imi/core/
     room((size_t)CX_P * E * 4);                                   // y
     room((size_t)CX_P * 2 * CX_NB * 4);                           // spec
     room((size_t)CX_P * CX_HOP * 4);                              // pcm
+    room((size_t)CX_P * CX_NFFT * 4);                             // frames
     room(sizeof(cframe_in));
     hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipMalloc(&c->mem, need);
@@ -353,6 +355,7 @@ int sh_codec_load(int device, const char* path, sh_codec** out) {   // imi/core/
     c->act = reinterpret_cast<float*>(take((size_t)CX_P * std::max(nq, I.n_ff) * 4));
     c->y = reinterpret_cast<float*>(take((size_t)CX_P * E * 4));
     c->spec = reinterpret_cast<float*>(take((size_t)CX_P * 2 * CX_NB * 4));
+    c->frames = reinterpret_cast<float*>(take((size_t)CX_P * CX_NFFT * 4));
     c->pcm = reinterpret_cast<float*>(take((size_t)CX_P * CX_HOP * 4));
     c->in_dev = reinterpret_cast<cframe_in*>(take(sizeof(cframe_in)));
     if (used > need) { release(c); return set_error(SH_E_NOMEM, "sh_codec_load: internal layout error"); }

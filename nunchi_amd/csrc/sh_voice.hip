@@ -238,42 +238,93 @@ __global__ __launch_bounds__(VX_THREADS) void k_vtab_fold(vtab_args a) {
 }
 
 // scaled order (imi/core/tables.cpp:324-365, P = 12 or 6): thread (row, position) runs one chain over all columns
-// of fma(float(w) * d, x, acc); two row groups per workgroup
+// of fma(float(w) * d, x, acc); two row groups (16 rows) per workgroup. The workgroup stages 256 columns at a time,
+// one chunk ahead: each thread loads one 16-byte word of codes (16 columns of one row's block) and the block's scale
+// and stores the 16 products float(w) * d (exact: an int8 times an fp16 has at most 19 significant bits) to LDS, and
+// the positions' inputs (normed first for a VP_NORM table) go position-major beside them; a chain step then reads
+// 4 columns of its row and 4 of its position as one 16-byte LDS word each.
 template <int P, int PRO, int EPI>
 __global__ __launch_bounds__(VX_THREADS) void k_vtab_scaled(vtab_args a) {
-    constexpr int PP = vx_pp(P), XJ = vx_xj(P);
-    static_assert(16 * P <= VX_THREADS, "one thread per (row, position)");
-    __shared__ __attribute__((aligned(16))) float xs[VX_NJ * XJ];
+    constexpr int WC = 256, WS = WC + 4, NBK = WC / 32;   // columns per chunk, LDS row stride, blocks per chunk
+    constexpr int NXQ = (P * (WC / 4) + VX_THREADS - 1) / VX_THREADS;   // input 16-byte words per thread per chunk
+    static_assert(16 * P <= VX_THREADS && 2 * NBK * 8 * 2 == VX_THREADS, "one code word per thread per chunk");
+    __shared__ __attribute__((aligned(16))) float sW[2][16 * WS];
+    __shared__ __attribute__((aligned(16))) float sX[2][P * WS];
     __shared__ float scl[VX_MAX_P];
     __shared__ float ev[16 * VX_MAX_P];
     const int t = threadIdx.x, rl = t / P, c = t - rl * P;
-    const int nb = a.W.nb, g0 = blockIdx.x * 2, g = g0 + (rl >> 3), r8 = rl & 7;
-    const bool live = t < 16 * P && 8 * g < a.W.rows_pad;
+    const int nb = a.W.nb, K = a.W.cols, ng = a.W.rows_pad / 8, nch = (K + WC - 1) / WC, g0 = blockIdx.x * 2;
+    // staging role: group gg, block jb of the chunk, row r8 of the group, half h of the block's 32 codes
+    const int gg = t >> 7, jb = (t >> 4) & 7, r8 = (t >> 1) & 7, h = t & 1;
+    const int grp = min(g0 + gg, ng - 1);   // (a workgroup's second group past the table reads the last one; dropped)
     if (PRO == VP_NORM) {
         position_scales<P>(a, scl);
         __syncthreads();
     }
-    float acc = 0.0f;
-    for (int q = 0; q * VX_NJ < nb; q++) {
-        const int nbc = min(VX_NJ, nb - q * VX_NJ);
-        if (q) __syncthreads();
-        stage_chunk<P, PRO>(xs, a, q, nbc, scl);
-        __syncthreads();
-        if (live) {
-            for (int jl = 0; jl < nbc; jl++) {
-                const size_t blk = ((size_t)g * nb + q * VX_NJ + jl) * 8 + r8;
-                const float d = h2f(a.W.scales[blk]);
-                const u32x4* cp = reinterpret_cast<const u32x4*>(a.W.codes + blk * 32);
-                const u32x4 h0 = cp[0], h1 = cp[1];
-                const unsigned wd[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
-                const float* xb = xs + jl * XJ + c;
+    u32x4 gq;
+    uint16_t gs;
+    f32x4 gx[NXQ];
+    auto fetch = [&](int q) {   // every load unconditional, indices clamped into the buffers
+        const int j = min(q * NBK + jb, nb - 1);
+        const size_t blk = ((size_t)grp * nb + j) * 8 + r8;
+        gq = reinterpret_cast<const u32x4*>(a.W.codes + blk * 32)[h];
+        gs = a.W.scales[blk];
 #pragma unroll
-                for (int kk = 0; kk < 32; kk++) {
-                    const float wv = (float)(int)(signed char)(wd[kk >> 2] >> (8 * (kk & 3))) * d;
-                    acc = fmaf(wv, xb[kk * PP], acc);
+        for (int s = 0; s < NXQ; s++) {
+            const int idx = min(t + VX_THREADS * s, P * (WC / 4) - 1), p = idx / (WC / 4), k = min(q * WC + 4 * (idx % (WC / 4)), K - 4);
+            gx[s] = *reinterpret_cast<const f32x4*>(a.src + (size_t)p * a.src_ld + k);
+        }
+    };
+    auto stash = [&](int b, int q) {
+        const bool ok = q * NBK + jb < nb;   // a block past the table's columns stores zeros (never read)
+        const float d = h2f(gs);
+        const unsigned wv[4] = {gq.x, gq.y, gq.z, gq.w};
+        float* dst = &sW[b][(8 * gg + r8) * WS + 32 * jb + 16 * h];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            f32x4 o;
+            o.x = ok ? (float)(int)(signed char)(wv[i] & 0xFFu) * d : 0.0f;
+            o.y = ok ? (float)(int)(signed char)((wv[i] >> 8) & 0xFFu) * d : 0.0f;
+            o.z = ok ? (float)(int)(signed char)((wv[i] >> 16) & 0xFFu) * d : 0.0f;
+            o.w = ok ? (float)(int)(signed char)(wv[i] >> 24) * d : 0.0f;
+            *reinterpret_cast<f32x4*>(dst + 4 * i) = o;
+        }
+#pragma unroll
+        for (int s = 0; s < NXQ; s++) {
+            const int idx = t + VX_THREADS * s;
+            if (idx < P * (WC / 4)) {
+                const int p = idx / (WC / 4), k4 = idx % (WC / 4), col = q * WC + 4 * k4;
+                f32x4 e = gx[s];
+                if (PRO == VP_NORM && col < K) {
+                    const f32x4 nw = *reinterpret_cast<const f32x4*>(a.norm_w + col);
+                    e.x = e.x * scl[p] * nw.x; e.y = e.y * scl[p] * nw.y;
+                    e.z = e.z * scl[p] * nw.z; e.w = e.w * scl[p] * nw.w;
                 }
+                *reinterpret_cast<f32x4*>(&sX[b][p * WS + 4 * k4]) = e;
             }
         }
+    };
+    fetch(0);
+    stash(0, 0);
+    __syncthreads();
+    float acc = 0.0f;
+    const bool live = t < 16 * P;
+    const int rr = live ? rl : 0, cc = live ? c : 0;
+    for (int q = 0; q < nch; q++) {
+        const int b = q & 1, nk4 = min(WC, K - q * WC) / 4;
+        if (q + 1 < nch) fetch(q + 1);
+        const float* wrow = &sW[b][rr * WS];
+        const float* xrow = &sX[b][cc * WS];
+        for (int k4 = 0; k4 < nk4; k4++) {
+            const f32x4 w = *reinterpret_cast<const f32x4*>(wrow + 4 * k4);
+            const f32x4 x = *reinterpret_cast<const f32x4*>(xrow + 4 * k4);
+            acc = fmaf(w.x, x.x, acc);
+            acc = fmaf(w.y, x.y, acc);
+            acc = fmaf(w.z, x.z, acc);
+            acc = fmaf(w.w, x.w, acc);
+        }
+        if (q + 1 < nch) stash(b ^ 1, q + 1);
+        __syncthreads();
     }
     table_epilogue<P, EPI, 16>(a, g0, acc, ev);
 }
