@@ -392,7 +392,8 @@ static size_t gemv_cut_lds(int M, int nb) {
 // ---------------------------------------------------------------- Q4_0 GEMV behind the post-norm residual
 // (x += norm(y) * w_post; h = norm(x) * w_pre; imi/core/seoul.cpp:462-475, imi/core/vec.h:20-44), 512 threads per
 // workgroup, a chunk of upw units (UG groups of 8 rows each) per workgroup and step of its loop:
-//  - the prologue's input vectors are requested first, then the first chunk's weights;
+//  - the prologue's input vectors are requested first; the first chunk's weights once y is in LDS (requested at
+//    kernel start, the 256 workgroups' weight streams held every workgroup's inputs back by about 1.5 us);
 //  - prologue: the E-value vectors are read once per workgroup, one wave per conversation runs imi's AVX2-order norm
 //    chains over them in LDS (held transposed, 16-byte reads: rms_scale_xt), every thread updates and normalises its
 //    4 values, and the 8 threads of
@@ -494,8 +495,7 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
         w[8] = __builtin_nontemporal_load((const u32x4*)a.W.scales + (size_t)g * nb + jw);
         if (HM) w[HM ? 9 : 8] = __builtin_nontemporal_load((const u32x4*)a.W.mins + (size_t)g * nb + jw);
     };
-    // ---- prologue: its inputs are requested first (a wave's loads complete in order, so the norm work can start
-    // while the weights that follow are still streaming in) ----
+    // ---- prologue: its inputs are requested first, the weights once the inputs have arrived ----
     // (every load on every path: threads past the E / 4 quads re-read the last one, and a workgroup past the last
     // chunk loads that chunk, so the compiler's wait counts stay exact)
     f32x4 xv[M], yv[M];
@@ -513,7 +513,7 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
     const f32x4 wp = EMB ? f32x4{0, 0, 0, 0} : ((const f32x4*)a.w_post)[tq], wq = ((const f32x4*)a.w_pre)[tq];
     const uint64_t etab = kExp2Tab[t & 31];   // (SwiGLU) copied to LDS once the dots have waited for the weights
     int k = blockIdx.x;
-    load_chunk(k < nchunk ? k : nchunk - 1);
+    if (EMB) load_chunk(k < nchunk ? k : nchunk - 1);
     // the conv epilogue's taps and memory of this thread's channel (one chunk per workgroup), after the weights
     constexpr int CMAX = 8;
     float cw[CMAX + 1], cst[CMAX];
@@ -533,6 +533,7 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
 #pragma unroll
             for (int m = 0; m < M; m++) put_xt(l_v + m * 32 * XLD, t, yv[m]);
         __syncthreads();
+        load_chunk(k < nchunk ? k : nchunk - 1);
         if ((t >> 6) < M) {
             const float sc = rms_xt(l_v + (t >> 6) * 32 * XLD, E, a.eps);
             if ((t & 63) == 0) l_sc[t >> 6] = sc;
