@@ -2,11 +2,7 @@
 // restatement of imi's ears performs, in the same order; the exceptions are the C library's erff (GELU) and the
 // double log10 of the mel, here the device's routines.
 //
-// The float tables run on the VALU in imi_wg_group12's order (imi/core/tables.cpp:522-556): one chain
-// acc = fma(w, x, acc) per row and position over the columns in order. A workgroup is 64 rows (one per lane) by
-// 4 waves x 4 positions: the 4 waves read the same weights (the second to fourth mostly from the L1), each lane
-// keeps 4 independent chains, a wave's 4 inputs per column are staged in LDS 128 columns at a time (one chunk
-// ahead) and read back as one broadcast 16-byte word, and each lane keeps 8 weight loads in flight.
+// The float tables run on the matrix cores in imi_wg_group12's order (k_etab below).
 #include "sh_ears.h"
 #include "sh_device.h"
 
@@ -74,106 +70,125 @@ __device__ __forceinline__ void wconv(const wraw<F32W>& r, float (&o)[8]) {
     }
 }
 
-template <int EPI, bool F32W>
+// The float tables on the matrix cores, in imi_wg_group12's order (imi/core/tables.cpp:522-556): one chain
+// acc = fma(w, x, acc) per row and position over the columns in order. v_mfma_f32_4x4x1_16b_f32 forms
+// d[l][i] = fma(a[4 (l / 4) + i], b[l], c[l][i]) with one rounding, bit for bit the VALU's fmaf (measured over 10^6
+// random cases with denormals, signed zeros and fused cancellation), so one instruction per column advances 16 blocks
+// of 4 rows x 4 positions of those chains by one step each, in column order. Lane l supplies its own row's weight (a)
+// and the input of position l % 4 (b); it holds rows 4 (l / 4) .. + 3 of position l % 4. A workgroup is 64 rows by
+// 4 waves x NMF position quads (NMF instructions per column and wave, one weight conversion); a wave keeps DW weight
+// loads in flight and stages its inputs position-major in LDS 128 columns at a time (one chunk ahead), 8 columns read
+// per 16-byte pair (a broadcast of the same word to every lane would cost the LDS its full return bandwidth). Every
+// global load is unconditional (indices clamped into the buffers; no product reads a column past the table, whose
+// width is a multiple of 8), so the compiler's wait counts stay exact.
+template <int EPI, bool F32W, int NMF>
 __global__ __launch_bounds__(ET) void k_etab(etab_args a) {
-    constexpr int KC = 128;   // columns of a wave's inputs staged per chunk (double-buffered in LDS)
-    constexpr int DW = 8;     // weight loads in flight, in 8-column steps
-    __shared__ float4 xs[ET / 64][2][KC];
-    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int r = blockIdx.x * 64 + lane, p0 = (blockIdx.y * 4 + wv) * EA_NP;
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    constexpr int KC = 128, KCP = KC + 4, DW = 8, NP = 4 * NMF;
+    __shared__ __align__(16) float xs[ET / 64][2][NP][KCP];
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), q = lane & 3;
+    const int r = blockIdx.x * 64 + lane, p0 = (blockIdx.y * 4 + wv) * NP;
     const int rp = a.W.rows_pad, K = a.W.cols, nk8 = K >> 3, nch = (K + KC - 1) / KC;
     const size_t ldx = (size_t)a.ldx;
-    const int rr = r < rp ? r : rp - 1;   // lanes past the table read its last row (straight-line loads, nothing stored)
-    const float* xg = a.x + p0;
-    float4 st[KC / 64];
-    // every load below is unconditional (indices clamped into the buffers, values selected afterwards), so the
-    // compiler's wait counts stay exact and the weight ring really keeps DW loads in flight
-    auto gload = [&](int c) {
-#pragma unroll
-        for (int i = 0; i < KC / 64; i++) {
-            const int k = c * KC + lane + 64 * i, kk = k < K ? k : K - 1;
-            const float4 v = *reinterpret_cast<const float4*>(xg + (size_t)kk * ldx);
-            st[i] = k < K ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
-    };
-    auto lstore = [&](int b) {
-#pragma unroll
-        for (int i = 0; i < KC / 64; i++) xs[wv][b][lane + 64 * i] = st[i];
-    };
-    gload(0);
+    const int rr = r < rp ? r : rp - 1;   // lanes past the table read its last row (nothing stored)
+    float4 st[KC / 64][NMF];
     wraw<F32W> wq[DW];
 #pragma unroll
     for (int i = 0; i < DW; i++) wq[i] = wload<F32W>(a.W.w, (size_t)(i < nk8 ? i : nk8 - 1) * rp + rr);
-    lstore(0);
-    __builtin_amdgcn_wave_barrier();
-    float acc[EA_NP] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int c = 0; c < nch; c++) {
-        gload(c + 1 < nch ? c + 1 : c);   // in flight while chunk c runs (the last chunk reloads itself, unused)
-        const float4* xc = xs[wv][c & 1];
-        const int kb0 = c * (KC / 8);
+    v4f acc[NMF];
 #pragma unroll
-        for (int u = 0; u < KC / 8; u++) {   // kb = kb0 + u; the ring slot u % DW is static (KC / 8 is a multiple of DW)
-            const int kb = kb0 + u, kn = kb + DW < nk8 ? kb + DW : nk8 - 1;
-            float w[8];
-            wconv<F32W>(wq[u % DW], w);
-            wq[u % DW] = wload<F32W>(a.W.w, (size_t)kn * rp + rr);
-            if (kb < nk8) {
+    for (int m = 0; m < NMF; m++) acc[m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c = -1; c < nch; c++) {
+        // chunk c + 1's inputs are requested (clamped to the last chunk), chunk c runs from LDS, then c + 1 is stored
+        {
+            const int cn = c + 1 < nch ? c + 1 : nch - 1;
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const float4 xv = xc[8 * u + j];
-                    acc[0] = fmaf(w[j], xv.x, acc[0]);
-                    acc[1] = fmaf(w[j], xv.y, acc[1]);
-                    acc[2] = fmaf(w[j], xv.z, acc[2]);
-                    acc[3] = fmaf(w[j], xv.w, acc[3]);
+            for (int i = 0; i < KC / 64; i++) {
+                const int k = min(cn * KC + lane + 64 * i, K - 1);
+#pragma unroll
+                for (int m = 0; m < NMF; m++) {
+                    const int pm = min(p0 + 4 * m, a.ldx - 4);
+                    st[i][m] = *reinterpret_cast<const float4*>(a.x + (size_t)k * ldx + pm);
+                }
+            }
+        }
+        if (c >= 0) {
+            const float* xc = &xs[wv][c & 1][0][0];
+            const int kb0 = c * (KC / 8);
+#pragma unroll
+            for (int u = 0; u < KC / 8; u++) {   // the ring slot u % DW is static (KC / 8 is a multiple of DW)
+                const int kb = kb0 + u, kn = kb + DW < nk8 ? kb + DW : nk8 - 1;
+                float w[8];
+                wconv<F32W>(wq[u % DW], w);
+                wq[u % DW] = wload<F32W>(a.W.w, (size_t)kn * rp + rr);
+                if (kb < nk8) {
+                    float xv[NMF][8];
+#pragma unroll
+                    for (int m = 0; m < NMF; m++) {
+                        const float* xp = xc + (4 * m + q) * KCP + 8 * u;
+                        const float4 x0 = *reinterpret_cast<const float4*>(xp), x1 = *reinterpret_cast<const float4*>(xp + 4);
+                        xv[m][0] = x0.x; xv[m][1] = x0.y; xv[m][2] = x0.z; xv[m][3] = x0.w;
+                        xv[m][4] = x1.x; xv[m][5] = x1.y; xv[m][6] = x1.z; xv[m][7] = x1.w;
+                    }
+#pragma unroll
+                    for (int j = 0; j < 8; j++)
+#pragma unroll
+                        for (int m = 0; m < NMF; m++) acc[m] = __builtin_amdgcn_mfma_f32_4x4x1f32(w[j], xv[m][j], acc[m], 0, 0, 0);
                 }
             }
         }
         __builtin_amdgcn_wave_barrier();
-        lstore((c + 1) & 1);
+        if (c + 1 < nch) {
+#pragma unroll
+            for (int i = 0; i < KC / 64; i++)
+#pragma unroll
+                for (int m = 0; m < NMF; m++) {
+                    float* xw = &xs[wv][(c + 1) & 1][4 * m][lane + 64 * i];
+                    xw[0] = st[i][m].x;
+                    xw[KCP] = st[i][m].y;
+                    xw[2 * KCP] = st[i][m].z;
+                    xw[3 * KCP] = st[i][m].w;
+                }
+        }
         __builtin_amdgcn_wave_barrier();
     }
-    if constexpr (EPI == EE_GLU || EPI == EE_POWER) {
-        constexpr int MASK = EPI == EE_GLU ? 8 : 1;
-        float o[EA_NP];
+    // lane l holds rows rb .. rb + 3 of position p0 + 4 m + l % 4 (rb = the workgroup's first row + 4 (l / 4))
+    const int rb = blockIdx.x * 64 + 4 * (lane >> 2);
+    const bool xt = a.xt_out;
+    const int pend = xt ? min(a.ldx, a.ldo) : a.P;   // the feature-major output also fills the padded positions
+    auto put = [&](int row, int p, float v) {
+        float* d = xt ? a.out + (size_t)row * a.ldo + p : a.out + (size_t)p * a.ldo + row;
+        *d = EPI == EE_ADD ? *d + v : v;
+    };
 #pragma unroll
-        for (int p = 0; p < EA_NP; p++) {
-            const float other = __shfl_xor(acc[p], MASK);
-            o[p] = EPI == EE_GLU ? silu(acc[p]) * other : fmaf(acc[p], acc[p], other * other);
-        }
-        const bool first = EPI == EE_GLU ? (r & 8) == 0 : (r & 1) == 0;
-        const int ro = EPI == EE_GLU ? (r >> 4) * 8 + (r & 7) : r >> 1;
-        if (first && ro < a.W.rows / 2) {
-            if (a.xt_out) {
-                *reinterpret_cast<float4*>(a.out + (size_t)ro * a.ldo + p0) = make_float4(o[0], o[1], o[2], o[3]);
-            } else {
+    for (int m = 0; m < NMF; m++) {
+        const int p = p0 + 4 * m + q;
+        if constexpr (EPI == EE_GLU) {   // rows 0-7 of each 16 are gates, 8-15 the matching ups (lanes + 8)
+            v4f up;
 #pragma unroll
-                for (int p = 0; p < EA_NP; p++)
-                    if (p0 + p < a.P) a.out[(size_t)(p0 + p) * a.ldo + ro] = o[p];
+            for (int i = 0; i < 4; i++) up[i] = __shfl_xor(acc[m][i], 8);
+            if ((lane & 8) == 0 && p < pend) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int row = rb + i, ro = (row >> 4) * 8 + (row & 7);
+                    if (ro < a.W.rows / 2) put(ro, p, silu(acc[m][i]) * up[i]);
+                }
             }
-        }
-    } else {
-        if (r >= a.W.rows) return;
-        const float b = a.bias ? a.bias[r] : 0.0f;
-        float o[EA_NP];
+        } else if constexpr (EPI == EE_POWER) {   // rows (2j, 2j + 1) = (re, im) of bin j
+            if (p < pend) {
 #pragma unroll
-        for (int p = 0; p < EA_NP; p++) {
-            const float v = acc[p] + b;
-            o[p] = EPI == EE_SILU ? silu(v) : EPI == EE_GELU ? gelu_erf(v) : v;
-        }
-        if (a.xt_out) {
-            float4* dst = reinterpret_cast<float4*>(a.out + (size_t)r * a.ldo + p0);
-            if constexpr (EPI == EE_ADD) {
-                const float4 c = *dst;
-                *dst = make_float4(c.x + o[0], c.y + o[1], c.z + o[2], c.w + o[3]);
-            } else {
-                *dst = make_float4(o[0], o[1], o[2], o[3]);
+                for (int h = 0; h < 2; h++) {
+                    const int ro = (rb >> 1) + h;
+                    if (ro < a.W.rows / 2) put(ro, p, fmaf(acc[m][2 * h], acc[m][2 * h], acc[m][2 * h + 1] * acc[m][2 * h + 1]));
+                }
             }
-        } else {
+        } else if (p < pend) {
 #pragma unroll
-            for (int p = 0; p < EA_NP; p++) {
-                if (p0 + p >= a.P) break;
-                float* d = a.out + (size_t)(p0 + p) * a.ldo + r;
-                *d = EPI == EE_ADD ? *d + o[p] : o[p];
+            for (int i = 0; i < 4; i++) {
+                const int row = rb + i;
+                if (row >= a.W.rows) break;
+                const float v = acc[m][i] + (a.bias ? a.bias[row] : 0.0f);
+                put(row, p, EPI == EE_SILU ? silu(v) : EPI == EE_GELU ? gelu_erf(v) : v);
             }
         }
     }
@@ -398,17 +413,26 @@ hipError_t launch_etab(int epi, const etab_args& a, hipStream_t s) {
     if (a.W.cols % 8 || a.W.rows_pad % 8 || a.ldx % 16 || (a.xt_out && a.ldo % 4) ||
         (epi == EE_GLU && a.W.rows_pad % 16))
         return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((a.W.rows_pad + 63) / 64), (unsigned)(a.ldx / 16));
+    const unsigned gx = (unsigned)((a.W.rows_pad + 63) / 64);
+    // position quads per wave: the most that keeps enough waves in flight (the chains are as long as the table is wide)
+    const auto waves = [&](int nmf) { return 4L * gx * ((a.ldx + 16 * nmf - 1) / (16 * nmf)); };
+    const int nmf = waves(4) >= 2048 ? 4 : waves(2) >= 2048 ? 2 : 1;
+    const dim3 grid(gx, (unsigned)((a.ldx + 16 * nmf - 1) / (16 * nmf)));
 #define SH_ETAB(E)                                                                                        \
     case E:                                                                                               \
-        if (a.W.f32) hipLaunchKernelGGL((k_etab<E, true>), grid, dim3(ET), 0, s, a);                      \
-        else hipLaunchKernelGGL((k_etab<E, false>), grid, dim3(ET), 0, s, a);                             \
+        if (a.W.f32) {                                                                                    \
+            if (nmf == 4) SH_ETAB_MF(E, true, 4); else if (nmf == 2) SH_ETAB_MF(E, true, 2); else SH_ETAB_MF(E, true, 1); \
+        } else {                                                                                          \
+            if (nmf == 4) SH_ETAB_MF(E, false, 4); else if (nmf == 2) SH_ETAB_MF(E, false, 2); else SH_ETAB_MF(E, false, 1); \
+        }                                                                                                 \
         break;
+#define SH_ETAB_MF(E, F, N) hipLaunchKernelGGL((k_etab<E, F, N>), grid, dim3(ET), 0, s, a)
     switch (epi) {
         SH_ETAB(EE_STORE) SH_ETAB(EE_ADD) SH_ETAB(EE_SILU) SH_ETAB(EE_GELU) SH_ETAB(EE_GLU) SH_ETAB(EE_POWER)
         default: return hipErrorInvalidValue;
     }
 #undef SH_ETAB
+#undef SH_ETAB_MF
     return hipGetLastError();
 }
 
