@@ -22,7 +22,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-GATE_UP_TRAFFIC_BYTES = 19275131   # counters: 149,528 128-B + 1,478 64-B read requests + 40 KiB WRITE_SIZE per launch
+GATE_UP_TRAFFIC_BYTES = 19_275_117   # counters: 149,528 128-B + 1,478 64-B read requests + 40 KiB WRITE_SIZE per launch
 # matrix-core utilisation of the prefill's table products, rocprofv3's MfmaUtil per dispatch (MFMA busy cycles over
 # GUI-active cycles x SIMDs) from `rocprofv3 --pmc MfmaUtil --kernel-include-regex k_pf_ -- python3 bench.py
 # --prefill-only --prefill-reps 2`: a counter run, not measurable from inside this process
