@@ -344,16 +344,24 @@ def layer_weights():
 
 def gpu_layer(ctx, reps):
     """cfg 1 on the device: the layer's 7 tables through the kernel-level GEMV (imi's int8 cut per 32 columns),
-    LAYER_COPIES copies in rotation; returns per-layer microseconds at B=1 and B=2 and the B=2 outputs of copy 0."""
+    LAYER_COPIES copies in rotation, one launch per table and grouped (sh_q4_gemv_group: the six 2048-wide tables in
+    one launch, down in another); returns per-layer microseconds at B=1 and B=2 for both, the B=2 outputs of copy 0,
+    and whether the grouped outputs equal the per-table ones bit for bit."""
     import nunchi_amd
     w, x = layer_weights()
+    nt = len(LAYER_TABLES)
     tabs = [nunchi_amd.Q4Table(ctx, w[i], r, c) for _ in range(LAYER_COPIES) for i, (r, c) in enumerate(LAYER_TABLES)]
     out = [tabs[i].gemv(x[:, :c]) for i, (_, c) in enumerate(LAYER_TABLES)]
-    us1 = nunchi_amd.q4_bench(ctx, tabs, n_in=1, cut_mode=0, reps=reps) * len(LAYER_TABLES)
-    us2 = nunchi_amd.q4_bench(ctx, tabs, n_in=2, cut_mode=0, reps=reps) * len(LAYER_TABLES)
+    grouped = nunchi_amd.q4_gemv_group(ctx, tabs[:nt], [x[:, :c] for _, c in LAYER_TABLES])
+    same = all(np.array_equal(g.view(np.uint32), o.view(np.uint32)) for g, o in zip(grouped, out))
+    us1 = nunchi_amd.q4_bench(ctx, tabs, n_in=1, cut_mode=0, reps=reps) * nt
+    us2 = nunchi_amd.q4_bench(ctx, tabs, n_in=2, cut_mode=0, reps=reps) * nt
+    sets = [tabs[k * nt:(k + 1) * nt] for k in range(LAYER_COPIES)]
+    g1 = nunchi_amd.q4_group_bench(ctx, sets, n_in=1, cut_mode=0, reps=reps // nt)
+    g2 = nunchi_amd.q4_group_bench(ctx, sets, n_in=2, cut_mode=0, reps=reps // nt)
     for t in tabs:
         t._free()
-    return us1, us2, out
+    return us1, us2, out, g1, g2, same
 
 
 def cpu_layer(threads, seconds=2.0):
@@ -533,7 +541,7 @@ def main():
     cfg0_bytes = 8192 * 64 * 18 + 2048 * 4 + 8192 * 4
     del copies
     # cfg 1: one layer's linears, B=1 and B=2 (two inputs riding each table read)
-    l_us1, l_us2, l_out = gpu_layer(ctx, reps=16 * len(LAYER_TABLES) * 8)
+    l_us1, l_us2, l_out, lg_us1, lg_us2, l_group_same = gpu_layer(ctx, reps=16 * len(LAYER_TABLES) * 8)
     layer_bytes = sum(r * c // 32 * 18 for r, c in LAYER_TABLES)
 
     gu_gbs = gu["bytes_per_launch"] / (gu["avg_us"] * 1e-6) / 1e9
@@ -616,7 +624,11 @@ def main():
                                    "table_bytes": layer_bytes,
                                    "b1_us": round(l_us1, 2), "b2_us": round(l_us2, 2),
                                    "b2_GBs": round(layer_bytes / l_us2 / 1e3, 1),
-                                   "b2_frac": round(layer_bytes / l_us2 / 1e3 / HBM_PEAK_GBS, 4)},
+                                   "b2_frac": round(layer_bytes / l_us2 / 1e3 / HBM_PEAK_GBS, 4),
+                                   "grouped": {"launches_per_layer": 2, "b1_us": round(lg_us1, 2), "b2_us": round(lg_us2, 2),
+                                               "b2_GBs": round(layer_bytes / lg_us2 / 1e3, 1),
+                                               "b2_frac": round(layer_bytes / lg_us2 / 1e3 / HBM_PEAK_GBS, 4),
+                                               "outputs_equal_per_table": bool(l_group_same)}},
             "cfg0_gemv_8192x2048": {"avg_us": round(cfg0_us, 3), "GBs": round(cfg0_bytes / cfg0_us / 1e3, 1),
                                     "frac": round(cfg0_bytes / cfg0_us / 1e3 / HBM_PEAK_GBS, 4),
                                     "kernel_us": round(cfg0_kernel_us, 3),
@@ -741,7 +753,9 @@ def main():
         line["kernels"]["cfg1_layer_linears"]["cpu"] = {
             "b1_us": round(cl1, 1), "b2_us": round(cl2, 1), "cores": threads, "kind": "port",
             "sample": "oracle group / group2 kernels (imi/core/tables.cpp), each table's fastest rep, about 2 s of reps per batch size"}
-        line["kernels"]["cfg1_layer_linears"]["speedup_vs_cpu"] = {"b1": round(cl1 / l_us1, 1), "b2": round(cl2 / l_us2, 1)}
+        line["kernels"]["cfg1_layer_linears"]["speedup_vs_cpu"] = {"b1": round(cl1 / l_us1, 1), "b2": round(cl2 / l_us2, 1),
+                                                                   "grouped_b1": round(cl1 / lg_us1, 1),
+                                                                   "grouped_b2": round(cl2 / lg_us2, 1)}
         line["kernels"]["cfg1_layer_linears"]["outputs_match_cpu"] = bool(all(
             np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32)) for a, b in zip(l_out, cl_out)))
         if args.prefill_reps:

@@ -220,6 +220,22 @@ int sh_q4_gemm_noalloc(sh_ctx* ctx, const sh_q4* t, const float* x_dev, int n, f
 int sh_q4_rows(sh_ctx* ctx, const sh_q4* t, const int32_t* ids, int n, float* out);
 /* Same on device-resident buffers (no copies, no synchronisation): x_dev, y_dev are device pointers. */
 int sh_q4_gemv_dev(sh_ctx* ctx, const sh_q4* t, const float* x_dev, int n_in, float* y_dev, int cut_mode);
+/* Several tables at once (a layer's linears, each with its own input): y[i][n_in][rows_i] = tables[i] x[i][n_in][cols_i]
+ * for i < n, each output bit for bit sh_q4_gemv's for that table (the same kernel body and operands). Tables of one
+ * width (cols 2048, 4096 or 8192) and one format share a launch, up to 8 per launch, so a layer's seven linears
+ * (six 2048-wide tables and the 8192-wide down) cost two dispatches instead of seven. The reference runs the same
+ * products table by table (imi_q4_group / imi_q4_group2, imi/core/tables.h:103-138); this entry point has no single
+ * counterpart there. Host buffers; the call waits. */
+int sh_q4_gemv_group(sh_ctx* ctx, int n, sh_q4* const* tables, const float* const* x, float* const* y, int n_in,
+                     int cut_mode);
+/* Same on device-resident buffers, enqueued on the context's stream without waiting. */
+int sh_q4_gemv_group_dev(sh_ctx* ctx, int n, sh_q4* const* tables, const float* const* x_dev, float* const* y_dev,
+                         int n_in, int cut_mode);
+/* Time `reps` grouped calls over n_sets sets of n tables (tables[s * n + i]: table i of set s), the sets in
+ * rotation so that none is resident in the 256 MB MALL when they are larger; inputs resident, zeros.
+ * avg_us = mean time per call (all of a set's launches, back to back). */
+int sh_q4_group_bench(sh_ctx* ctx, int n_sets, int n, sh_q4* const* tables, int n_in, int cut_mode, int reps,
+                      double* avg_us);
 /* Time `reps` launches of the GEMV over `n_tables` tables in turn (tables[i] read in rotation so that none is
  * resident in the 256 MB MALL when the set is larger), inputs resident; avg_launch_us = mean launch duration. */
 int sh_q4_bench(sh_ctx* ctx, sh_q4* const* tables, int n_tables, int n_in, int cut_mode, int reps, double* avg_launch_us);

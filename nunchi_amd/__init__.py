@@ -22,7 +22,8 @@ EXPORTS = [
     "sh_last_error", "sh_create", "sh_destroy", "sh_load", "sh_info", "sh_check_model", "sh_state_new", "sh_state_free", "sh_state_reset",
     "sh_state_pos", "sh_state_set_pos", "sh_step", "sh_step2", "sh_step_batch", "sh_generate", "sh_bench_tables",
     "sh_bench_kernel", "sh_bench_step_kernel",
-    "sh_q4_create", "sh_q4_free", "sh_q4_rows", "sh_q4_gemv", "sh_q4_gemm", "sh_q4_gemm_noalloc", "sh_q4_gemv_dev", "sh_q4_bench", "sh_q4_bench_kernel", "sh_expf", "sh_sync",
+    "sh_q4_create", "sh_q4_free", "sh_q4_rows", "sh_q4_gemv", "sh_q4_gemm", "sh_q4_gemm_noalloc", "sh_q4_gemv_dev", "sh_q4_bench", "sh_q4_bench_kernel",
+    "sh_q4_gemv_group", "sh_q4_gemv_group_dev", "sh_q4_group_bench", "sh_expf", "sh_sync",
     "sh_voice_load", "sh_voice_free", "sh_voice_info", "sh_voice_begin_frame", "sh_voice_base", "sh_voice_pass",
     "sh_voice_feedback", "sh_voice_sample",
     "sh_file_load", "sh_file_free", "sh_file_get", "sh_file_key_i", "sh_file_key_f", "sh_file_keep", "sh_file_drop_data",
@@ -110,6 +111,9 @@ def load_library(path: str = LIB_PATH):
         "sh_q4_gemm_noalloc": (i, [vp, vp, vp, i, vp]),
         "sh_q4_bench": (i, [vp, vp, i, i, i, i, P(d)]),
         "sh_q4_bench_kernel": (i, [vp, vp, i, i, i, i, P(d)]),
+        "sh_q4_gemv_group": (i, [vp, i, vp, vp, vp, i, i]),
+        "sh_q4_gemv_group_dev": (i, [vp, i, vp, vp, vp, i, i]),
+        "sh_q4_group_bench": (i, [vp, i, i, vp, i, i, i, P(d)]),
         "sh_expf": (i, [vp, vp, C.c_longlong, vp]),
         "sh_sync": (i, [vp]),
         "sh_voice_load": (i, [i, C.c_char_p, P(vp)]),
@@ -488,6 +492,32 @@ def q4_bench_kernel(ctx: Context, tables, n_in: int = 1, cut_mode: int = 0, reps
     arr = (C.c_void_p * len(tables))(*[t.h.value for t in tables])
     us = C.c_double()
     _check(_lib.sh_q4_bench_kernel(ctx.h, arr, len(tables), int(n_in), int(cut_mode), int(reps), C.byref(us)))
+    return us.value
+
+
+def q4_gemv_group(ctx: Context, tables, xs, cut_mode: int = 0):
+    """Every table's GEMV in grouped launches (tables of one width share a launch): xs[i] is [n_in][cols_i] (or one
+    vector); returns the outputs [n_in][rows_i] (or vectors), each bit for bit Q4Table.gemv's."""
+    one = np.asarray(xs[0]).ndim == 1
+    xs = [np.ascontiguousarray(x, np.float32).reshape(-1, t.cols) for x, t in zip(xs, tables)]
+    n_in = xs[0].shape[0]
+    ys = [np.zeros((n_in, t.rows), np.float32) for t in tables]
+    n = len(tables)
+    th = (C.c_void_p * n)(*[t.h.value for t in tables])
+    xp = (C.c_void_p * n)(*[x.ctypes.data for x in xs])
+    yp = (C.c_void_p * n)(*[y.ctypes.data for y in ys])
+    _check(_lib.sh_q4_gemv_group(ctx.h, n, th, xp, yp, int(n_in), int(cut_mode)))
+    return [y[0] for y in ys] if one else ys
+
+
+def q4_group_bench(ctx: Context, sets, n_in: int = 1, cut_mode: int = 0, reps: int = 200) -> float:
+    """Mean time (us) of one grouped call over a set of tables (sets: equal-length lists, in rotation), inputs
+    resident on the device."""
+    n = len(sets[0])
+    flat = [t.h.value for s in sets for t in s]
+    arr = (C.c_void_p * len(flat))(*flat)
+    us = C.c_double()
+    _check(_lib.sh_q4_group_bench(ctx.h, len(sets), n, arr, int(n_in), int(cut_mode), int(reps), C.byref(us)))
     return us.value
 
 

@@ -16,6 +16,7 @@ int run_prefill(sh_ctx* c, sh_state* st, const int32_t* tokens, const float* emb
                 float* hidden_last, float* logits, float* hidden_all, int32_t* best);
 
 hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hipStream_t s, hipEvent_t t0 = nullptr, hipEvent_t t1 = nullptr);
+hipError_t launch_gemv_group(int M, bool half, const gemv_group_args& g, hipStream_t s, hipEvent_t t0 = nullptr, hipEvent_t t1 = nullptr);
 // workgroups of a word-score launch (the argmax partials k_final reduces), at most max_grid
 int gemv_logits_grid(int M, int pro, const gemv_args& a, int max_grid);
 hipError_t launch_attn(int M, const attn_args& a, hipStream_t s);

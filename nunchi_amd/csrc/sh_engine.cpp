@@ -1285,6 +1285,120 @@ int sh_q4_gemv(sh_ctx* c, const sh_q4* t, const float* x, int n_in, float* y, in
     return SH_OK;
 }
 
+namespace {
+// the tables in launches of up to GEMV_GROUP_MAX tables of one width and format, in the order given
+int q4_group_launch(sh_ctx* c, int n, sh_q4* const* t, const float* const* x, float* const* y, int n_in, int cut_mode) {
+    if (!c || n < 1 || !t || !x || !y || n_in < 1 || n_in > 2 || cut_mode < 0 || cut_mode > 1 || (cut_mode == 1 && n_in != 1))
+        return fail(SH_E_ARG, "sh_q4_gemv_group: bad argument");
+    for (int i = 0; i < n; i++) {
+        if (!t[i] || !x[i] || !y[i]) return fail(SH_E_ARG, "sh_q4_gemv_group: null table or buffer");
+        if (t[i]->ctx != c) return fail(SH_E_STATE, "sh_q4_gemv_group: table belongs to another context");
+        const int nb = t[i]->t.nb;
+        if (nb != 64 && nb != 128 && nb != 256) return fail(SH_E_SHAPE, "sh_q4_gemv_group: cols must be 2048, 4096 or 8192");
+        if (cut_mode == 1 && t[i]->t.mins) return fail(SH_E_ARG, "sh_q4_gemv_group: the half-away cut is for Q4_0 tables");
+    }
+    std::vector<char> done(n, 0);
+    for (int i = 0; i < n; i++) {
+        if (done[i]) continue;
+        gemv_group_args g{};
+        g.start[0] = 0;
+        for (int j = i; j < n && g.n < GEMV_GROUP_MAX; j++) {
+            if (done[j] || t[j]->t.nb != t[i]->t.nb || (t[j]->t.mins != nullptr) != (t[i]->t.mins != nullptr)) continue;
+            g.W[g.n] = t[j]->t;
+            g.src[g.n] = x[j];
+            g.out[g.n] = y[j];
+            g.start[g.n + 1] = g.start[g.n] + t[j]->t.rows / 8;
+            g.n++;
+            done[j] = 1;
+        }
+        HIPCHK(launch_gemv_group(n_in, cut_mode == 1, g, c->stream));
+    }
+    return SH_OK;
+}
+}  // namespace
+
+int sh_q4_gemv_group_dev(sh_ctx* c, int n, sh_q4* const* tables, const float* const* x_dev, float* const* y_dev, int n_in,
+                         int cut_mode) {
+    if (!c) return fail(SH_E_ARG, "sh_q4_gemv_group_dev: bad argument");
+    HIPCHK(hipSetDevice(c->device));
+    return q4_group_launch(c, n, tables, x_dev, y_dev, n_in, cut_mode);
+}
+
+int sh_q4_gemv_group(sh_ctx* c, int n, sh_q4* const* tables, const float* const* x, float* const* y, int n_in, int cut_mode) {
+    if (!c || n < 1 || !tables || !x || !y || n_in < 1 || n_in > 2) return fail(SH_E_ARG, "sh_q4_gemv_group: bad argument");
+    for (int i = 0; i < n; i++)
+        if (!tables[i] || !x[i] || !y[i]) return fail(SH_E_ARG, "sh_q4_gemv_group: null table or buffer");
+    HIPCHK(hipSetDevice(c->device));
+    size_t total = 0;
+    std::vector<size_t> xo(n), yo(n);
+    for (int i = 0; i < n; i++) {
+        xo[i] = total;
+        total += (size_t)n_in * tables[i]->t.cols;
+        yo[i] = total;
+        total += (size_t)n_in * tables[i]->t.rows;
+    }
+    float* buf = nullptr;
+    HIPCHK(hipMalloc(&buf, total * sizeof(float)));
+    std::vector<const float*> dx(n);
+    std::vector<float*> dy(n);
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < n && e == hipSuccess; i++) {
+        dx[i] = buf + xo[i];
+        dy[i] = buf + yo[i];
+        e = hipMemcpyAsync(buf + xo[i], x[i], sizeof(float) * n_in * tables[i]->t.cols, hipMemcpyHostToDevice, c->stream);
+    }
+    int rc = e == hipSuccess ? q4_group_launch(c, n, tables, dx.data(), dy.data(), n_in, cut_mode) : SH_E_HIP;
+    for (int i = 0; i < n && rc == SH_OK && e == hipSuccess; i++)
+        e = hipMemcpyAsync(y[i], dy[i], sizeof(float) * n_in * tables[i]->t.rows, hipMemcpyDeviceToHost, c->stream);
+    const hipError_t es = hipStreamSynchronize(c->stream);
+    (void)hipFree(buf);
+    if (rc != SH_OK) return rc;
+    if (e != hipSuccess || es != hipSuccess)
+        return fail(SH_E_HIP, std::string("sh_q4_gemv_group: ") + hipGetErrorString(e != hipSuccess ? e : es));
+    return SH_OK;
+}
+
+int sh_q4_group_bench(sh_ctx* c, int n_sets, int n, sh_q4* const* tables, int n_in, int cut_mode, int reps, double* avg_us) {
+    if (!c || n_sets < 1 || n < 1 || !tables || reps < 1 || n_in < 1 || n_in > 2) return fail(SH_E_ARG, "sh_q4_group_bench: bad argument");
+    HIPCHK(hipSetDevice(c->device));
+    size_t need = 0;   // every table of a set reads its own slice of the input buffer and writes its own output slice
+    size_t xo = 0, yo = 0;
+    for (int i = 0; i < n; i++) {
+        xo += (size_t)n_in * tables[i]->t.cols;
+        yo += (size_t)n_in * tables[i]->t.rows;
+    }
+    need = xo > yo ? xo : yo;
+    if (c->bench_cap < need) {
+        HIPCHK(regrow2(&c->bench_x, &c->bench_y, need));
+        HIPCHK(hipMemset(c->bench_x, 0, need * 4));
+        c->bench_cap = need;
+    }
+    std::vector<const float*> dx(n);
+    std::vector<float*> dy(n);
+    xo = yo = 0;
+    for (int i = 0; i < n; i++) {
+        dx[i] = c->bench_x + xo;
+        dy[i] = c->bench_y + yo;
+        xo += (size_t)n_in * tables[i]->t.cols;
+        yo += (size_t)n_in * tables[i]->t.rows;
+    }
+    for (int s = 0; s < n_sets; s++) {   // warm-up: one pass over every set
+        const int rc = q4_group_launch(c, n, tables + (size_t)s * n, dx.data(), dy.data(), n_in, cut_mode);
+        if (rc != SH_OK) return rc;
+    }
+    HIPCHK(hipEventRecord(c->ev0, c->stream));
+    for (int r = 0; r < reps; r++) {
+        const int rc = q4_group_launch(c, n, tables + (size_t)(r % n_sets) * n, dx.data(), dy.data(), n_in, cut_mode);
+        if (rc != SH_OK) return rc;
+    }
+    HIPCHK(hipEventRecord(c->ev1, c->stream));
+    HIPCHK(hipEventSynchronize(c->ev1));
+    float ms;
+    HIPCHK(hipEventElapsedTime(&ms, c->ev0, c->ev1));
+    if (avg_us) *avg_us = ms * 1e3 / reps;
+    return SH_OK;
+}
+
 int sh_q4_bench(sh_ctx* c, sh_q4* const* tables, int n_tables, int n_in, int cut_mode, int reps, double* avg_us) {
     if (!c || !tables || n_tables < 1 || reps < 1) return fail(SH_E_ARG, "sh_q4_bench: bad argument");
     HIPCHK(hipSetDevice(c->device));

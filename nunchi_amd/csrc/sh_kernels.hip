@@ -264,8 +264,9 @@ __global__ __launch_bounds__(64) void k_gemv(gemv_args a) {
 //    corr = 8 d sum (imi/kernels/q4x8.cpp:45-77).
 // HM: the table is Q4_1 (imi/core/tables.cpp:127-143 with HAS_M): the correction chain takes the block minimum m in
 // place of d and the row ends as acc + cor
-template <int M, bool HALF, int NB, bool HM = false>
-__global__ __launch_bounds__(256) void k_gemv_cut(gemv_args a) {
+// g: the table's 8-row group this workgroup computes
+template <int M, bool HALF, int NB, bool HM>
+__device__ __forceinline__ void gemv_cut_body(const gemv_args& a, const int g) {
     constexpr int TPB = 256 / NB, VPT = 32 / TPB, RPT = NB / 32, ST = NB + 4;
     extern __shared__ __align__(16) float lds[];
     int* l_xq = (int*)lds;                      // [M][NB][8] int8 codes of the cut input, 4 per word
@@ -274,7 +275,7 @@ __global__ __launch_bounds__(256) void k_gemv_cut(gemv_args a) {
     float* l_op = l_s + M * ST;                 // [M][8][ST] float(isum)
     float* l_oq = l_op + M * 8 * ST;            // [M][8][ST] d * dx
     float* l_dd = l_oq + M * 8 * ST;            // [8][ST] d
-    const int t = threadIdx.x, lane = t & 63, g = blockIdx.x;
+    const int t = threadIdx.x, lane = t & 63;
     // input share first: block jc, values part * VPT .. + VPT - 1
     const int jc = t / TPB, part = t - jc * TPB;
     f32x4 xin[M][VPT / 4];
@@ -382,6 +383,29 @@ __global__ __launch_bounds__(256) void k_gemv_cut(gemv_args a) {
         const int m = lane >> 3, r = lane & 7;
         a.out[(size_t)m * a.out_ld + 8 * g + r] = HALF ? chain - cor : HM ? chain + cor : fmaf(-8.0f, cor, chain);
     }
+}
+
+template <int M, bool HALF, int NB, bool HM = false>
+__global__ __launch_bounds__(256) void k_gemv_cut(gemv_args a) {
+    gemv_cut_body<M, HALF, NB, HM>(a, blockIdx.x);
+}
+
+// several tables of one width in one launch: workgroup b computes group b - start[t] of table t (start[t] <= b <
+// start[t + 1]), with the same code and operands as k_gemv_cut on that table alone
+template <int M, bool HALF, int NB, bool HM = false>
+__global__ __launch_bounds__(256) void k_gemv_cut_group(gemv_group_args G) {
+    const int b = blockIdx.x;
+    int t = 0;
+#pragma unroll
+    for (int i = 1; i < GEMV_GROUP_MAX; i++)
+        if (i < G.n && b >= G.start[i]) t = i;
+    gemv_args a{};
+    a.W = G.W[t];
+    a.src = G.src[t];
+    a.src_ld = a.W.cols;
+    a.out = G.out[t];
+    a.out_ld = a.W.rows;
+    gemv_cut_body<M, HALF, NB, HM>(a, b - G.start[t]);
 }
 
 static size_t gemv_cut_lds(int M, int nb) {
@@ -1594,6 +1618,33 @@ hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hi
     SH_GEMV_CASE(1, 1, PRO_RESID_NORM, EPI_LOGITS, 1) SH_GEMV_CASE(2, 1, PRO_RESID_NORM, EPI_LOGITS, 1)
     SH_GEMV_CASE(1, 1, PRO_CUT, EPI_LOGITS, 1)
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemv_group(int M, bool half, const gemv_group_args& g, hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
+    if (g.n < 1 || g.n > GEMV_GROUP_MAX || M < 1 || M > 2 || (half && M != 1)) return hipErrorInvalidValue;
+    const int nb = g.W[0].nb;
+    const bool hm = g.W[0].mins != nullptr;
+    if (half && hm) return hipErrorInvalidValue;
+    if (g.start[0] != 0) return hipErrorInvalidValue;
+    for (int i = 0; i < g.n; i++)   // one width and one format per launch; every table whole groups of 8 rows
+        if (g.W[i].nb != nb || (g.W[i].mins != nullptr) != hm || g.W[i].rows % 8 || g.W[i].rows < 8 ||
+            g.start[i + 1] - g.start[i] != g.W[i].rows / 8 || !g.src[i] || !g.out[i])
+            return hipErrorInvalidValue;
+    const void* fn = nullptr;
+#define SH_GRP_FN(M_, H_, NB_) if (M == M_ && half == H_ && nb == NB_ && !hm) fn = (const void*)k_gemv_cut_group<M_, H_, NB_>;
+#define SH_GRP_FN1(M_, NB_) if (M == M_ && nb == NB_ && hm) fn = (const void*)k_gemv_cut_group<M_, false, NB_, true>;
+    SH_GRP_FN(1, false, 64) SH_GRP_FN(1, false, 128) SH_GRP_FN(1, false, 256)
+    SH_GRP_FN(1, true, 64) SH_GRP_FN(1, true, 128) SH_GRP_FN(1, true, 256)
+    SH_GRP_FN(2, false, 64) SH_GRP_FN(2, false, 128) SH_GRP_FN(2, false, 256)
+    SH_GRP_FN1(1, 64) SH_GRP_FN1(1, 128) SH_GRP_FN1(1, 256) SH_GRP_FN1(2, 64) SH_GRP_FN1(2, 128) SH_GRP_FN1(2, 256)
+#undef SH_GRP_FN
+#undef SH_GRP_FN1
+    if (!fn) return hipErrorInvalidValue;
+    void* args[] = {const_cast<gemv_group_args*>(&g)};
+    const dim3 gr(g.start[g.n]), bl(256);
+    const size_t lds = gemv_cut_lds(M, nb);
+    if (t0) return hipExtLaunchKernel(fn, gr, bl, args, lds, s, t0, t1, 0);
+    return hipLaunchKernel(fn, gr, bl, args, lds, s);
 }
 
 hipError_t launch_q4_rows(const q4dev& T, const int32_t* ids, int n, float* out, hipStream_t s) {

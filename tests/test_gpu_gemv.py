@@ -9,6 +9,7 @@
   float64 value of the same int8-cut input
 - two inputs riding one read give each input exactly its one-input result (imi/core/tables.cpp:145-163)
 - imi/kernels/q4x8.cpp's input cut (roundf, half away from zero) on cut_mode 1
+- several tables in grouped launches (sh_q4_gemv_group) give each table exactly its own GEMV
 """
 import numpy as np
 import pytest
@@ -101,6 +102,35 @@ def test_gemv_two_inputs_match_oracle_group2(ctx):
     got = nunchi_amd.Q4Table(ctx, blk, rows, cols).gemv(x)
     orc, _ = oracle.Q4Table(blk, rows, cols, threads=4).gemv(x)
     assert np.array_equal(got.view(np.uint32), orc.view(np.uint32))
+
+
+def test_group_equals_each_table_alone(ctx):
+    """sh_q4_gemv_group: a layer's seven linears (cfg 1 shapes, 2048- and 8192-wide), 4096-wide tables and more
+    tables of one width than one launch takes (9 of 2048 columns), at one and two inputs and with q4x8's cut: every
+    output equals the table's own sh_q4_gemv bit for bit; the first is also checked against the oracle."""
+    import nunchi_amd
+    import oracle
+    shapes = [(2048, 2048), (512, 2048), (512, 2048), (2048, 2048), (8192, 2048), (8192, 2048), (2048, 8192),
+              (1024, 4096), (8, 2048), (64, 2048), (264, 4096), (16, 2048)]
+    tabs, blks = [], []
+    for i, (r, c) in enumerate(shapes):
+        blks.append(q4_random(r, c, seed=300 + i))
+        tabs.append(nunchi_amd.Q4Table(ctx, blks[-1], r, c))
+    rng = np.random.default_rng(301)
+    for n_in, cut in ((1, 0), (2, 0), (1, 1)):
+        xs = [rng.standard_normal((n_in, c)).astype(np.float32) for _, c in shapes]
+        got = nunchi_amd.q4_gemv_group(ctx, tabs, xs, cut_mode=cut)
+        for t, x, y in zip(tabs, xs, got):
+            assert y.shape == (n_in, t.rows)
+            assert np.array_equal(y.view(np.uint32), t.gemv(x, cut_mode=cut).reshape(n_in, -1).view(np.uint32))
+        if cut == 0:
+            orc, _ = oracle.Q4Table(blks[0], *shapes[0], threads=4).gemv(xs[0] if n_in == 2 else xs[0][0])
+            assert np.array_equal(got[0].reshape(orc.shape).view(np.uint32), orc.view(np.uint32))
+    with pytest.raises(nunchi_amd.SeoulError):   # q4x8's cut takes one input
+        nunchi_amd.q4_gemv_group(ctx, tabs[:2], [np.zeros((2, 2048), np.float32)] * 2, cut_mode=1)
+    with pytest.raises(nunchi_amd.SeoulError):   # 1024 columns: no kernel width
+        nunchi_amd.q4_gemv_group(ctx, [nunchi_amd.Q4Table(ctx, q4_random(8, 1024, seed=1), 8, 1024)],
+                                 [np.zeros(1024, np.float32)])
 
 
 def test_expf_is_the_c_library(ctx):
