@@ -625,7 +625,7 @@ def main():
                                    "b1_us": round(l_us1, 2), "b2_us": round(l_us2, 2),
                                    "b2_GBs": round(layer_bytes / l_us2 / 1e3, 1),
                                    "b2_frac": round(layer_bytes / l_us2 / 1e3 / HBM_PEAK_GBS, 4),
-                                   "grouped": {"launches_per_layer": 2, "b1_us": round(lg_us1, 2), "b2_us": round(lg_us2, 2),
+                                   "grouped": {"launches_per_layer": {"b1": 1, "b2": 2}, "b1_us": round(lg_us1, 2), "b2_us": round(lg_us2, 2),
                                                "b2_GBs": round(layer_bytes / lg_us2 / 1e3, 1),
                                                "b2_frac": round(layer_bytes / lg_us2 / 1e3 / HBM_PEAK_GBS, 4),
                                                "outputs_equal_per_table": bool(l_group_same)}},

@@ -221,9 +221,9 @@ int sh_q4_rows(sh_ctx* ctx, const sh_q4* t, const int32_t* ids, int n, float* ou
 /* Same on device-resident buffers (no copies, no synchronisation): x_dev, y_dev are device pointers. */
 int sh_q4_gemv_dev(sh_ctx* ctx, const sh_q4* t, const float* x_dev, int n_in, float* y_dev, int cut_mode);
 /* Several tables at once (a layer's linears, each with its own input): y[i][n_in][rows_i] = tables[i] x[i][n_in][cols_i]
- * for i < n, each output bit for bit sh_q4_gemv's for that table (the same kernel body and operands). Tables of one
- * width (cols 2048, 4096 or 8192) and one format share a launch, up to 8 per launch, so a layer's seven linears
- * (six 2048-wide tables and the 8192-wide down) cost two dispatches instead of seven. The reference runs the same
+ * for i < n, each output bit for bit sh_q4_gemv's for that table (the same kernel body and operands). Widths
+ * 2048, 4096 or 8192 columns; up to 8 tables per launch (one width per launch for two inputs), so a layer's seven
+ * linears cost one dispatch (two at n_in = 2) instead of seven. The reference runs the same
  * products table by table (imi_q4_group / imi_q4_group2, imi/core/tables.h:103-138); this entry point has no single
  * counterpart there. Host buffers; the call waits. */
 int sh_q4_gemv_group(sh_ctx* ctx, int n, sh_q4* const* tables, const float* const* x, float* const* y, int n_in,

@@ -10,6 +10,8 @@
 #include "sh_device.h"
 #include "sh_kernels.h"
 
+#include <algorithm>
+
 namespace sh {
 
 // ---------------------------------------------------------------- helpers
@@ -390,9 +392,10 @@ __global__ __launch_bounds__(256) void k_gemv_cut(gemv_args a) {
     gemv_cut_body<M, HALF, NB, HM>(a, blockIdx.x);
 }
 
-// several tables of one width in one launch: workgroup b computes group b - start[t] of table t (start[t] <= b <
-// start[t + 1]), with the same code and operands as k_gemv_cut on that table alone
-template <int M, bool HALF, int NB, bool HM = false>
+// several tables in one launch: workgroup b computes group b - start[t] of table t (start[t] <= b < start[t + 1]),
+// with the same code and operands as k_gemv_cut on that table alone. NBF: the launch's one width in blocks, or 0 for
+// tables of several widths (the body for the table's width chosen per workgroup, at the widest body's registers)
+template <int M, bool HALF, bool HM, int NBF>
 __global__ __launch_bounds__(256) void k_gemv_cut_group(gemv_group_args G) {
     const int b = blockIdx.x;
     int t = 0;
@@ -405,7 +408,11 @@ __global__ __launch_bounds__(256) void k_gemv_cut_group(gemv_group_args G) {
     a.src_ld = a.W.cols;
     a.out = G.out[t];
     a.out_ld = a.W.rows;
-    gemv_cut_body<M, HALF, NB, HM>(a, b - G.start[t]);
+    const int g = b - G.start[t];
+    if (NBF) gemv_cut_body<M, HALF, NBF ? NBF : 64, HM>(a, g);
+    else if (a.W.nb == 64) gemv_cut_body<M, HALF, 64, HM>(a, g);
+    else if (a.W.nb == 128) gemv_cut_body<M, HALF, 128, HM>(a, g);
+    else gemv_cut_body<M, HALF, 256, HM>(a, g);
 }
 
 static size_t gemv_cut_lds(int M, int nb) {
@@ -1622,27 +1629,30 @@ hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hi
 
 hipError_t launch_gemv_group(int M, bool half, const gemv_group_args& g, hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
     if (g.n < 1 || g.n > GEMV_GROUP_MAX || M < 1 || M > 2 || (half && M != 1)) return hipErrorInvalidValue;
-    const int nb = g.W[0].nb;
     const bool hm = g.W[0].mins != nullptr;
     if (half && hm) return hipErrorInvalidValue;
     if (g.start[0] != 0) return hipErrorInvalidValue;
-    for (int i = 0; i < g.n; i++)   // one width and one format per launch; every table whole groups of 8 rows
-        if (g.W[i].nb != nb || (g.W[i].mins != nullptr) != hm || g.W[i].rows % 8 || g.W[i].rows < 8 ||
-            g.start[i + 1] - g.start[i] != g.W[i].rows / 8 || !g.src[i] || !g.out[i])
+    size_t lds = 0;
+    for (int i = 0; i < g.n; i++) {   // one format per launch; widths 64, 128 or 256 blocks; whole groups of 8 rows
+        const int nb = g.W[i].nb;
+        if ((nb != 64 && nb != 128 && nb != 256) || (g.W[i].mins != nullptr) != hm || g.W[i].rows % 8 ||
+            g.W[i].rows < 8 || g.start[i + 1] - g.start[i] != g.W[i].rows / 8 || !g.src[i] || !g.out[i])
             return hipErrorInvalidValue;
+        lds = std::max(lds, gemv_cut_lds(M, nb));
+    }
+    int nbf = g.W[0].nb;
+    for (int i = 1; i < g.n; i++)
+        if (g.W[i].nb != nbf) nbf = 0;
     const void* fn = nullptr;
-#define SH_GRP_FN(M_, H_, NB_) if (M == M_ && half == H_ && nb == NB_ && !hm) fn = (const void*)k_gemv_cut_group<M_, H_, NB_>;
-#define SH_GRP_FN1(M_, NB_) if (M == M_ && nb == NB_ && hm) fn = (const void*)k_gemv_cut_group<M_, false, NB_, true>;
-    SH_GRP_FN(1, false, 64) SH_GRP_FN(1, false, 128) SH_GRP_FN(1, false, 256)
-    SH_GRP_FN(1, true, 64) SH_GRP_FN(1, true, 128) SH_GRP_FN(1, true, 256)
-    SH_GRP_FN(2, false, 64) SH_GRP_FN(2, false, 128) SH_GRP_FN(2, false, 256)
-    SH_GRP_FN1(1, 64) SH_GRP_FN1(1, 128) SH_GRP_FN1(1, 256) SH_GRP_FN1(2, 64) SH_GRP_FN1(2, 128) SH_GRP_FN1(2, 256)
-#undef SH_GRP_FN
-#undef SH_GRP_FN1
+#define SH_GRP(M_, H_, HM_)                                                                                        \
+    if (M == M_ && half == H_ && hm == HM_)                                                                        \
+        fn = nbf == 64 ? (const void*)k_gemv_cut_group<M_, H_, HM_, 64> : nbf == 128 ? (const void*)k_gemv_cut_group<M_, H_, HM_, 128> \
+           : nbf == 256 ? (const void*)k_gemv_cut_group<M_, H_, HM_, 256> : (const void*)k_gemv_cut_group<M_, H_, HM_, 0>;
+    SH_GRP(1, false, false) SH_GRP(1, true, false) SH_GRP(2, false, false) SH_GRP(1, false, true) SH_GRP(2, false, true)
+#undef SH_GRP
     if (!fn) return hipErrorInvalidValue;
     void* args[] = {const_cast<gemv_group_args*>(&g)};
     const dim3 gr(g.start[g.n]), bl(256);
-    const size_t lds = gemv_cut_lds(M, nb);
     if (t0) return hipExtLaunchKernel(fn, gr, bl, args, lds, s, t0, t1, 0);
     return hipLaunchKernel(fn, gr, bl, args, lds, s);
 }
