@@ -1371,6 +1371,46 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
                 vr[c] = vT + (size_t)(j & 1) * D * TV + (size_t)(lane + 64 * c) * TV;
             }
             int p = 0;
+            // 32 positions at a time, the next group's weights and values read from LDS before this group's chain
+            // runs (register double buffer, static indices; the last group re-reads itself, unused)
+            auto load32 = [&](int p32, float (&aa)[32], unsigned (&vv)[DPL][16]) {
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const f32x4 x = *(const f32x4*)(ar + p32 + 4 * q);
+                    aa[4 * q] = x.x; aa[4 * q + 1] = x.y; aa[4 * q + 2] = x.z; aa[4 * q + 3] = x.w;
+                }
+#pragma unroll
+                for (int c = 0; c < DPL; c++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const u32x4 w = *(const u32x4*)(vr[c] + 8 * (((p32 >> 3) + q) ^ fz[c]));
+                        vv[c][4 * q] = w.x; vv[c][4 * q + 1] = w.y; vv[c][4 * q + 2] = w.z; vv[c][4 * q + 3] = w.w;
+                    }
+            };
+            auto chain32 = [&](const float (&aa)[32], const unsigned (&vv)[DPL][16]) {
+#pragma unroll
+                for (int c = 0; c < DPL; c++)
+#pragma unroll
+                    for (int u = 0; u < 32; u++)
+                        o[c] = fmaf(aa[u], h2f((uint16_t)((vv[c][u >> 1] >> (16 * (u & 1))) & 0xFFFFu)), o[c]);
+            };
+            if (nt >= 32) {
+                float a0[32], a1[32];
+                unsigned v0[DPL][16], v1[DPL][16];
+                load32(0, a0, v0);
+                for (;;) {
+                    const bool more = p + 64 <= nt;
+                    load32(more ? p + 32 : p, a1, v1);
+                    chain32(a0, v0);
+                    p += 32;
+                    if (!more) break;
+                    const bool more2 = p + 64 <= nt;
+                    load32(more2 ? p + 32 : p, a0, v0);
+                    chain32(a1, v1);
+                    p += 32;
+                    if (!more2) break;
+                }
+            }
             for (; p + 8 <= nt; p += 8) {
                 const f32x4 a0 = *(const f32x4*)(ar + p), a1 = *(const f32x4*)(ar + p + 4);
                 const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
