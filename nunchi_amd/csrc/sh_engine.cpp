@@ -1286,7 +1286,8 @@ int sh_q4_gemv(sh_ctx* c, const sh_q4* t, const float* x, int n_in, float* y, in
 }
 
 namespace {
-// the tables in launches of up to GEMV_GROUP_MAX tables of one format (and, for two inputs, one width)
+// the tables (Q4_0, as sh_q4_create makes them) in launches of up to GEMV_GROUP_MAX tables (one width per launch
+// for two inputs)
 int q4_group_launch(sh_ctx* c, int n, sh_q4* const* t, const float* const* x, float* const* y, int n_in, int cut_mode) {
     if (!c || n < 1 || !t || !x || !y || n_in < 1 || n_in > 2 || cut_mode < 0 || cut_mode > 1 || (cut_mode == 1 && n_in != 1))
         return fail(SH_E_ARG, "sh_q4_gemv_group: bad argument");
@@ -1295,7 +1296,6 @@ int q4_group_launch(sh_ctx* c, int n, sh_q4* const* t, const float* const* x, fl
         if (t[i]->ctx != c) return fail(SH_E_STATE, "sh_q4_gemv_group: table belongs to another context");
         const int nb = t[i]->t.nb;
         if (nb != 64 && nb != 128 && nb != 256) return fail(SH_E_SHAPE, "sh_q4_gemv_group: cols must be 2048, 4096 or 8192");
-        if (cut_mode == 1 && t[i]->t.mins) return fail(SH_E_ARG, "sh_q4_gemv_group: the half-away cut is for Q4_0 tables");
     }
     // the widest tables first within a launch: their workgroups are the longest, so they start first
     std::vector<int> order(n);
@@ -1309,7 +1309,7 @@ int q4_group_launch(sh_ctx* c, int n, sh_q4* const* t, const float* const* x, fl
         g.start[0] = 0;
         for (int oj = oi; oj < n && g.n < GEMV_GROUP_MAX; oj++) {
             const int j = order[oj];
-            if (done[j] || (t[j]->t.mins != nullptr) != (t[i]->t.mins != nullptr)) continue;
+            if (done[j]) continue;
             if (n_in == 2 && t[j]->t.nb != t[i]->t.nb) continue;   // measured: two inputs run faster one width per launch
             g.W[g.n] = t[j]->t;
             g.src[g.n] = x[j];

@@ -69,7 +69,7 @@ struct gemv_args {
     q6dev W6;                  // k_scores_q6k: the Q6_K word table
 };
 
-// several kernel-level GEMVs of one format (Q4_0 or Q4_1) in one launch: table t's 8-row groups are workgroups
+// several kernel-level Q4_0 GEMVs in one launch: table t's 8-row groups are workgroups
 // start[t] .. start[t + 1] - 1 (start[0] = 0, start[t + 1] - start[t] = W[t].rows / 8); src[t] [M][cols], out[t] [M][rows]
 constexpr int GEMV_GROUP_MAX = 8;
 struct gemv_group_args {

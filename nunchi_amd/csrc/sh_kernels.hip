@@ -393,9 +393,9 @@ __global__ __launch_bounds__(256) void k_gemv_cut(gemv_args a) {
 }
 
 // several tables in one launch: workgroup b computes group b - start[t] of table t (start[t] <= b < start[t + 1]),
-// with the same code and operands as k_gemv_cut on that table alone. NBF: the launch's one width in blocks, or 0 for
+// with the same code and operands as k_gemv_cut on that (Q4_0) table alone. NBF: the launch's one width in blocks, or 0 for
 // tables of several widths (the body for the table's width chosen per workgroup, at the widest body's registers)
-template <int M, bool HALF, bool HM, int NBF>
+template <int M, bool HALF, int NBF>
 __global__ __launch_bounds__(256) void k_gemv_cut_group(gemv_group_args G) {
     const int b = blockIdx.x;
     int t = 0;
@@ -409,10 +409,10 @@ __global__ __launch_bounds__(256) void k_gemv_cut_group(gemv_group_args G) {
     a.out = G.out[t];
     a.out_ld = a.W.rows;
     const int g = b - G.start[t];
-    if (NBF) gemv_cut_body<M, HALF, NBF ? NBF : 64, HM>(a, g);
-    else if (a.W.nb == 64) gemv_cut_body<M, HALF, 64, HM>(a, g);
-    else if (a.W.nb == 128) gemv_cut_body<M, HALF, 128, HM>(a, g);
-    else gemv_cut_body<M, HALF, 256, HM>(a, g);
+    if (NBF) gemv_cut_body<M, HALF, NBF ? NBF : 64, false>(a, g);
+    else if (a.W.nb == 64) gemv_cut_body<M, HALF, 64, false>(a, g);
+    else if (a.W.nb == 128) gemv_cut_body<M, HALF, 128, false>(a, g);
+    else gemv_cut_body<M, HALF, 256, false>(a, g);
 }
 
 static size_t gemv_cut_lds(int M, int nb) {
@@ -1669,13 +1669,11 @@ hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hi
 
 hipError_t launch_gemv_group(int M, bool half, const gemv_group_args& g, hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
     if (g.n < 1 || g.n > GEMV_GROUP_MAX || M < 1 || M > 2 || (half && M != 1)) return hipErrorInvalidValue;
-    const bool hm = g.W[0].mins != nullptr;
-    if (half && hm) return hipErrorInvalidValue;
     if (g.start[0] != 0) return hipErrorInvalidValue;
     size_t lds = 0;
-    for (int i = 0; i < g.n; i++) {   // one format per launch; widths 64, 128 or 256 blocks; whole groups of 8 rows
+    for (int i = 0; i < g.n; i++) {   // Q4_0 tables of 64, 128 or 256 blocks per row, whole groups of 8 rows
         const int nb = g.W[i].nb;
-        if ((nb != 64 && nb != 128 && nb != 256) || (g.W[i].mins != nullptr) != hm || g.W[i].rows % 8 ||
+        if ((nb != 64 && nb != 128 && nb != 256) || g.W[i].mins || g.W[i].rows % 8 ||
             g.W[i].rows < 8 || g.start[i + 1] - g.start[i] != g.W[i].rows / 8 || !g.src[i] || !g.out[i])
             return hipErrorInvalidValue;
         lds = std::max(lds, gemv_cut_lds(M, nb));
@@ -1684,11 +1682,11 @@ hipError_t launch_gemv_group(int M, bool half, const gemv_group_args& g, hipStre
     for (int i = 1; i < g.n; i++)
         if (g.W[i].nb != nbf) nbf = 0;
     const void* fn = nullptr;
-#define SH_GRP(M_, H_, HM_)                                                                                        \
-    if (M == M_ && half == H_ && hm == HM_)                                                                        \
-        fn = nbf == 64 ? (const void*)k_gemv_cut_group<M_, H_, HM_, 64> : nbf == 128 ? (const void*)k_gemv_cut_group<M_, H_, HM_, 128> \
-           : nbf == 256 ? (const void*)k_gemv_cut_group<M_, H_, HM_, 256> : (const void*)k_gemv_cut_group<M_, H_, HM_, 0>;
-    SH_GRP(1, false, false) SH_GRP(1, true, false) SH_GRP(2, false, false) SH_GRP(1, false, true) SH_GRP(2, false, true)
+#define SH_GRP(M_, H_)                                                                                             \
+    if (M == M_ && half == H_)                                                                                     \
+        fn = nbf == 64 ? (const void*)k_gemv_cut_group<M_, H_, 64> : nbf == 128 ? (const void*)k_gemv_cut_group<M_, H_, 128> \
+           : nbf == 256 ? (const void*)k_gemv_cut_group<M_, H_, 256> : (const void*)k_gemv_cut_group<M_, H_, 0>;
+    SH_GRP(1, false) SH_GRP(1, true) SH_GRP(2, false)
 #undef SH_GRP
     if (!fn) return hipErrorInvalidValue;
     void* args[] = {const_cast<gemv_group_args*>(&g)};
