@@ -423,8 +423,9 @@ static size_t gemv_cut_lds(int M, int nb) {
 // ---------------------------------------------------------------- Q4_0 GEMV behind the post-norm residual
 // (x += norm(y) * w_post; h = norm(x) * w_pre; imi/core/seoul.cpp:462-475, imi/core/vec.h:20-44), 512 threads per
 // workgroup, a chunk of upw units (UG groups of 8 rows each) per workgroup and step of its loop:
-//  - the prologue's input vectors are requested first; the first chunk's weights once y is in LDS (requested at
-//    kernel start, the 256 workgroups' weight streams held every workgroup's inputs back by about 1.5 us);
+//  - the prologue's input vectors are requested first, then half of the first chunk's code rows, the rest of the
+//    chunk once y is in LDS (the whole chunk requested at kernel start, the 256 workgroups' weight streams held
+//    every workgroup's inputs back by about 1.5 us);
 //  - prologue: the E-value vectors are read once per workgroup, one wave per conversation runs imi's AVX2-order norm
 //    chains over them in LDS (held transposed, 16-byte reads: rms_scale_xt), every thread updates and normalises its
 //    4 values, and the 8 threads of
@@ -518,15 +519,18 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
     // all 9 (Q4_1: 10) loads are issued on every path (rows past this thread's share and absent groups re-read a row
     // it owns, which the caches serve), so the compiler counts them exactly and the prologue waits only for its own
     // inputs
-    auto load_chunk = [&](int k) {
+    auto load_rows = [&](int k, int r0, int r1) {
         const int g = min(k * G + (wt ? gi : 0), gtot - 1), s0 = wt ? sub * rpt : 0;
         const u32x4* cp = (const u32x4*)a.W.codes + (size_t)(8 * g + s0) * nb + jw;
 #pragma unroll
-        for (int r = 0; r < 8; r++) w[r] = __builtin_nontemporal_load(cp + (size_t)(r < rpt ? r : 0) * nb);
-        w[8] = __builtin_nontemporal_load((const u32x4*)a.W.scales + (size_t)g * nb + jw);
-        if (HM) w[HM ? 9 : 8] = __builtin_nontemporal_load((const u32x4*)a.W.mins + (size_t)g * nb + jw);
+        for (int r = r0; r < r1; r++) w[r] = __builtin_nontemporal_load(cp + (size_t)(r < rpt ? r : 0) * nb);
+        if (r1 == 8 && r0 < 8) {
+            w[8] = __builtin_nontemporal_load((const u32x4*)a.W.scales + (size_t)g * nb + jw);
+            if (HM) w[HM ? 9 : 8] = __builtin_nontemporal_load((const u32x4*)a.W.mins + (size_t)g * nb + jw);
+        }
     };
-    // ---- prologue: its inputs are requested first, the weights once the inputs have arrived ----
+    auto load_chunk = [&](int k) { load_rows(k, 0, 8); };
+    // ---- prologue: its inputs are requested first, most of the weights once the inputs have arrived ----
     // (every load on every path: threads past the E / 4 quads re-read the last one, and a workgroup past the last
     // chunk loads that chunk, so the compiler's wait counts stay exact)
     f32x4 xv[M], yv[M];
@@ -545,6 +549,12 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
     const uint64_t etab = kExp2Tab[t & 31];   // (SwiGLU) copied to LDS once the dots have waited for the weights
     int k = blockIdx.x;
     if (EMB) load_chunk(k < nchunk ? k : nchunk - 1);
+    // the first kEarlyRows code rows of the first chunk go out right behind the inputs, the rest (and the scales) once
+    // y is in LDS: the memory system streams weights while the inputs arrive without the whole chunk queued ahead of
+    // them (decode B=1 2188 -> 2211 tokens/s with 4 rows; 2, 3, 5, 6 and all 8 rows with the scales measured no
+    // better or slower)
+    constexpr int kEarlyRows = 4;
+    if (!EMB) load_rows(k < nchunk ? k : nchunk - 1, 0, kEarlyRows);
     // the conv epilogue's taps and memory of this thread's channel (one chunk per workgroup), after the weights
     constexpr int CMAX = 8;
     float cw[CMAX + 1], cst[CMAX];
@@ -564,7 +574,7 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
 #pragma unroll
             for (int m = 0; m < M; m++) put_xt(l_v + m * 32 * XLD, t, yv[m]);
         __syncthreads();
-        load_chunk(k < nchunk ? k : nchunk - 1);
+        load_rows(k < nchunk ? k : nchunk - 1, kEarlyRows, 8);
         if ((t >> 6) < M) {
             const float sc = rms_xt(l_v + (t >> 6) * 32 * XLD, E, a.eps);
             if ((t & 63) == 0) l_sc[t >> 6] = sc;
