@@ -452,10 +452,25 @@ def main():
         g_us = nunchi_amd.q4_bench(ctx, copies, n_in=1, cut_mode=1, reps=640)
         e_us = nunchi_amd.bench_empty(grid=1024, reps=1000)
         r_us, st = nunchi_amd.bench_read(9437184, copies=64, grid=1152, reps=640, stamps=True)
+        # the decode step as if every launch were a pure read of its table: each table size read back to back from
+        # HBM (enough copies in rotation to exceed the 256 MB MALL), times its launches per B=1 step, plus an empty
+        # dispatch for each of the 6 attention launches and the end-of-step launch
+        tables = {"ffn_gate_up": (16384 * 64 * 18, 16), "ffn_down": (2048 * 256 * 18, 16),
+                  "conv_in_proj": (6144 * 64 * 18, 10), "o_out_proj": (2048 * 64 * 18, 16),
+                  "qkvg": (3104 * 64 * 18, 6), "word_scores": (97496 * 64 * 18, 1)}
+        reads = {}
+        for name, (nbytes, _) in tables.items():
+            copies = max(2, min(64, -(-600_000_000 // nbytes)))
+            reads[name] = nunchi_amd.bench_read(nbytes, copies=copies, grid=max(256, nbytes // 8192),
+                                                reps=max(64, min(640, int(2e9 // nbytes))))
+        floor_us = sum(reads[k] * n for k, (_, n) in tables.items()) + 7 * e_us
         print(json.dumps({"floor_only": {"gemv_us": round(g_us, 3), "empty_kernel_us": round(e_us, 3),
                                          "pure_read_us": round(r_us, 3), "pure_read_last_start_us": round(st[0], 2),
                                          "pure_read_first_bytes_us": round(st[1], 2),
-                                         "pure_read_last_end_us": round(st[2], 2)}}), flush=True)
+                                         "pure_read_last_end_us": round(st[2], 2),
+                                         "step_table_reads_us": {k: round(v, 3) for k, v in reads.items()},
+                                         "step_read_floor_us": round(floor_us, 1),
+                                         "step_read_floor_tokens_per_s": round(1e6 / floor_us, 1)}}), flush=True)
         return
     if args.ears_only:
         ears = nunchi_amd.Ears(synth.cached("ears", synth.EARS, 3))

@@ -423,9 +423,9 @@ static size_t gemv_cut_lds(int M, int nb) {
 // ---------------------------------------------------------------- Q4_0 GEMV behind the post-norm residual
 // (x += norm(y) * w_post; h = norm(x) * w_pre; imi/core/seoul.cpp:462-475, imi/core/vec.h:20-44), 512 threads per
 // workgroup, a chunk of upw units (UG groups of 8 rows each) per workgroup and step of its loop:
-//  - the prologue's input vectors are requested first, then half of the first chunk's code rows, the rest of the
-//    chunk once y is in LDS (the whole chunk requested at kernel start, the 256 workgroups' weight streams held
-//    every workgroup's inputs back by about 1.5 us);
+//  - the prologue's input vectors are requested first (FFN gate|up and word scores: then half of the first chunk's
+//    code rows), the rest of the chunk once y is in LDS (the whole chunk requested at kernel start, the 256
+//    workgroups' weight streams held every workgroup's inputs back by about 1.5 us);
 //  - prologue: the E-value vectors are read once per workgroup, one wave per conversation runs imi's AVX2-order norm
 //    chains over them in LDS (held transposed, 16-byte reads: rms_scale_xt), every thread updates and normalises its
 //    4 values, and the 8 threads of
@@ -551,9 +551,10 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
     if (EMB) load_chunk(k < nchunk ? k : nchunk - 1);
     // the first kEarlyRows code rows of the first chunk go out right behind the inputs, the rest (and the scales) once
     // y is in LDS: the memory system streams weights while the inputs arrive without the whole chunk queued ahead of
-    // them (decode B=1 2188 -> 2211 tokens/s with 4 rows; 2, 3, 5, 6 and all 8 rows with the scales measured no
-    // better or slower)
-    constexpr int kEarlyRows = 4;
+    // them. Half of a thread's 8 rows for the FFN gate|up and word-score tables (decode B=1 2188 -> 2211 tokens/s; 2,
+    // 3, 5, 6 or all 8 rows with the scales measured no better or slower); none for the conv in_proj and q|k|v|gate
+    // tables, whose threads hold 4 and 2 rows (early rows there measured slower: B=1 2210 -> 2226 without them)
+    constexpr int kEarlyRows = (EPI == EPI_SWIGLU || EPI == EPI_LOGITS) ? 4 : 0;
     if (!EMB) load_rows(k < nchunk ? k : nchunk - 1, 0, kEarlyRows);
     // the conv epilogue's taps and memory of this thread's channel (one chunk per workgroup), after the weights
     constexpr int CMAX = 8;
