@@ -281,6 +281,18 @@ __device__ __forceinline__ float rms_scale_xt(Ptr xt, float eps) {
     return 1.0f / sqrtf(s / (float)(128 * NQ) + eps);
 }
 
+// A pointer a kernel reads from memory (the step parameter block: K/V caches, conv memory, output ids) is generic to
+// the compiler, so every access through it becomes a flat instruction, and a flat load counts against the LDS wait
+// counter as well as the vector-memory one: each wait for an LDS result then also waits for that load to come back
+// from memory. The pointers held there are all device memory; this says so (the cast to the global address space
+// lets the compiler use global instructions for every access through the result, which keeps the address space in
+// its type: a cast back to a generic pointer would be folded away with it).
+#define SH_GLOBAL __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ SH_GLOBAL T* global_ptr(T* p) {
+    return (SH_GLOBAL T*)p;
+}
+
 // dot_h (imi/core/seoul.cpp:29-39): 8 FMA chains over columns i % 8, then the 8-lane horizontal sum
 template <int D>
 __device__ __forceinline__ float dot_h8(const float* q, const float* k) {

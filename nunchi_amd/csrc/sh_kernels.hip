@@ -217,7 +217,7 @@ __global__ __launch_bounds__(64) void k_gemv(gemv_args a) {
             const float cc = __shfl(outv, (lane + 8) & 63), xx = __shfl(outv, (lane + 16) & 63);
             if (lane < M * R && k < 8) {
                 const int e = 8 * u + k, E = a.E, dc = a.d_conv;
-                float* st = a.P->conv[m] + (size_t)a.conv_layer * dc * E;
+                SH_GLOBAL float* st = global_ptr(a.P->conv[m]) + (size_t)a.conv_layer * dc * E;
                 const float bx = outv * xx;
                 float uu = outv * xx * a.conv_w[(size_t)dc * E + e];
                 for (int t = 0; t < dc; t++) uu = fmaf(st[(size_t)t * E + e], a.conv_w[(size_t)t * E + e], uu);
@@ -563,11 +563,22 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
         const int m = t / R, r = t - m * R, ui = r / 24, i = r - 24 * ui, dc = a.d_conv;
         const bool mine = t < C && i < 8 && k < nchunk;
         const int e = mine ? 8 * (k * upw + ui) + i : 0;
-        const float* stt = a.P->conv[mine ? m : 0] + (size_t)a.conv_layer * dc * E;
+        // both conversations' memory pointers read as uniform values, every tap and memory load issued (indices
+        // clamped to the kernel's taps, unused values dropped afterwards), so the loads need no branch and the
+        // compiler's wait counts stay exact
+        SH_GLOBAL float* const c0 = global_ptr(a.P->conv[0]);
+        SH_GLOBAL float* const c1 = M > 1 ? global_ptr(a.P->conv[M - 1]) : c0;
+        const SH_GLOBAL float* stt = (mine && m ? c1 : c0) + (size_t)a.conv_layer * dc * E;
 #pragma unroll
-        for (int q = 0; q <= CMAX; q++) cw[q] = q <= dc ? a.conv_w[(size_t)q * E + e] : 0.0f;
+        for (int q = 0; q <= CMAX; q++) {
+            const float v = a.conv_w[(size_t)min(q, dc) * E + e];
+            cw[q] = q <= dc ? v : 0.0f;
+        }
 #pragma unroll
-        for (int q = 0; q < CMAX; q++) cst[q] = q < dc ? stt[(size_t)q * E + e] : 0.0f;
+        for (int q = 0; q < CMAX; q++) {
+            const float v = stt[(size_t)min(q, dc - 1) * E + e];
+            cst[q] = q < dc ? v : 0.0f;
+        }
     }
 
     if (!EMB) {   // x += norm(y) * w_post (imi_norm_mul_add)
@@ -721,7 +732,7 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
                     if (i < 8) {
                         const int e = 8 * (u0 + ui) + i, dc = a.d_conv;
                         const float cc = l_out[t + 8], xx = l_out[t + 16];
-                        float* stt = a.P->conv[m] + (size_t)a.conv_layer * dc * E;
+                        SH_GLOBAL float* stt = global_ptr(a.P->conv[m]) + (size_t)a.conv_layer * dc * E;
                         const float bx = v * xx;
                         float wdc = cw[0];
 #pragma unroll
@@ -1022,8 +1033,8 @@ __global__ __launch_bounds__(256) void k_attn(attn_args a) {
     const int Hq = a.n_head * D, kvd = a.n_kv * D, grp = a.n_head / a.n_kv;
     const int pos = a.P->pos[m];
     const int s0 = a.n_swa > 0 ? max(0, pos - a.n_swa + 1) : 0, nk = pos - s0 + 1;
-    uint16_t* kc = a.P->kc[m] + ((size_t)a.layer_ai * a.n_kv + g) * a.n_ctx * D;
-    uint16_t* vc = a.P->vc[m] + ((size_t)a.layer_ai * a.n_kv + g) * a.n_ctx * D;
+    SH_GLOBAL uint16_t* kc = global_ptr(a.P->kc[m]) + ((size_t)a.layer_ai * a.n_kv + g) * a.n_ctx * D;
+    SH_GLOBAL uint16_t* vc = global_ptr(a.P->vc[m]) + ((size_t)a.layer_ai * a.n_kv + g) * a.n_ctx * D;
     const float* row = a.qkv + (size_t)m * a.ld_qkv;
     float* q_s = lds;                               // [grp][D]
     float* sc = q_s + grp * D;                      // [grp][n_ctx]
@@ -1059,7 +1070,7 @@ __global__ __launch_bounds__(256) void k_attn(attn_args a) {
 
     const float scale = 1.0f / sqrtf((float)D);
     for (int t = tid; t < nk; t += 256) {
-        const uint16_t* kt = kc + (size_t)(s0 + t) * D;
+        const SH_GLOBAL uint16_t* kt = kc + (size_t)(s0 + t) * D;
         float kf[D];
 #pragma unroll
         for (int i0 = 0; i0 < D; i0 += 8) {
@@ -1142,8 +1153,8 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
     const int pos = a.P->pos[m];
     const int s0 = a.n_swa > 0 ? max(0, pos - a.n_swa + 1) : 0, nk = pos - s0 + 1;
     const int ntile = (nk + TV - 1) / TV;
-    uint16_t* kc = a.P->kc[m] + ((size_t)a.layer_ai * a.n_kv + g) * a.n_ctx * D;
-    uint16_t* vc = a.P->vc[m] + ((size_t)a.layer_ai * a.n_kv + g) * a.n_ctx * D;
+    SH_GLOBAL uint16_t* kc = global_ptr(a.P->kc[m]) + ((size_t)a.layer_ai * a.n_kv + g) * a.n_ctx * D;
+    SH_GLOBAL uint16_t* vc = global_ptr(a.P->vc[m]) + ((size_t)a.layer_ai * a.n_kv + g) * a.n_ctx * D;
     const float* row = a.qkv + (size_t)m * a.ld_qkv;
     float* q_s = lds;                              // [D]
     float* k_s = q_s + D;                          // [D] this position's key as the cache holds it
@@ -1161,10 +1172,10 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
     {
         const int p0 = min(t, last), p1 = min(t + NT, last);
 #pragma unroll
-        for (int i = 0; i < KW; i++) ka[i] = ((const u32x4*)(kc + (size_t)(s0 + p0) * D))[i];
+        for (int i = 0; i < KW; i++) ka[i] = ((const SH_GLOBAL u32x4*)(kc + (size_t)(s0 + p0) * D))[i];
         if (AHEAD2)
 #pragma unroll
-            for (int i = 0; i < KW; i++) kb[AHEAD2 ? i : 0] = ((const u32x4*)(kc + (size_t)(s0 + p1) * D))[i];
+            for (int i = 0; i < KW; i++) kb[AHEAD2 ? i : 0] = ((const SH_GLOBAL u32x4*)(kc + (size_t)(s0 + p1) * D))[i];
     }
     // value staging: loader lt = t - 256 holds positions 8 * pb .. + 7 of a tile, dimensions 8 * kq .. + 7
     const int lt = t - 256, kq = lt & (KW - 1), pb = lt / KW;
@@ -1175,7 +1186,7 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
 #pragma unroll
         for (int r = 0; r < 8; r++) {
             const int p = min(j * TV + 8 * pb + r, last);
-            vw[r] = ((const u32x4*)(vc + (size_t)(s0 + p) * D))[kq];
+            vw[r] = ((const SH_GLOBAL u32x4*)(vc + (size_t)(s0 + p) * D))[kq];
         }
     };
     auto store_tile = [&](int j) {   // (this position's row replaced by its v)
@@ -1254,7 +1265,7 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
     for (int p = t; p < nk; p += NT) {
         if (D > 64 && p != t) {   // D 128: this pass's row requested here (no prefetch registers to spare)
 #pragma unroll
-            for (int i = 0; i < KW; i++) ka[i] = ((const u32x4*)(kc + (size_t)(s0 + min(p, last)) * D))[i];
+            for (int i = 0; i < KW; i++) ka[i] = ((const SH_GLOBAL u32x4*)(kc + (size_t)(s0 + min(p, last)) * D))[i];
         }
         if (D > 64) {   // dot_h's 8 chains over columns i % 8, a word (8 columns) at a time
             float acc[8];
@@ -1282,7 +1293,7 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
         u32x4 kn[KW];
         const int pn = min(p + (AHEAD2 ? 2 : 1) * NT, last);
 #pragma unroll
-        for (int i = 0; i < KW; i++) kn[i] = ((const u32x4*)(kc + (size_t)(s0 + pn) * D))[i];
+        for (int i = 0; i < KW; i++) kn[i] = ((const SH_GLOBAL u32x4*)(kc + (size_t)(s0 + pn) * D))[i];
         float kf[D];
         if (p == nk - 1) {
 #pragma unroll
@@ -1537,7 +1548,7 @@ __global__ __launch_bounds__(256) void k_final(final_args a) {
         if (tid == 0) {
             a.P->best[m] = best;
             if (a.advance) {
-                if (a.P->greedy && a.P->out_tok[m]) a.P->out_tok[m][a.P->n_done] = best;
+                if (a.P->greedy && a.P->out_tok[m]) global_ptr(a.P->out_tok[m])[a.P->n_done] = best;
                 if (a.P->greedy) a.P->token[m] = best;
                 a.P->pos[m] += 1;
             }
