@@ -1167,7 +1167,27 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
     const float2* cs = a.rope_cs + (size_t)pos * half;
     const int last = max(nk - 2, 0);               // last cache row written by an earlier step
 
-    // ---- requests first ----
+    // ---- requests first: waves 0 and 1 their q / k values, norm weights and rotation entries (head sizes up to 64;
+    // at 128 the registers would spill), then every thread its key rows. Loads complete in order, so with the key
+    // rows requested first the norm below waited for them to come back from memory, while the q / k operands come
+    // from the previous kernel's output ----
+    constexpr bool EARLY_QK = D <= 64;
+    const bool is_k = __builtin_amdgcn_readfirstlane(wv) == 1;   // (wave-uniform: the operand pointers stay scalar)
+    float xq[DPL], wq[DPL], vq[DPL];
+    float2 cq[DPL];
+    auto load_qk = [&]() {
+        const float* src = is_k ? row + Hq + g * D : row + h * D;
+        const float* w = is_k ? a.k_norm : a.q_norm;
+#pragma unroll
+        for (int c = 0; c < DPL; c++) {
+            const int e = min(lane + 64 * c, D - 1);   // (lanes past D re-read the last value; they use none)
+            xq[c] = src[e];
+            wq[c] = w[e];
+            cq[c] = cs[e < half ? e : e - half];
+            vq[c] = row[Hq + kvd + g * D + e];   // this position's v (cache row written by the k wave)
+        }
+    };
+    if (EARLY_QK && wv < 2) load_qk();
     u32x4 ka[KW], kb[AHEAD2 ? KW : 1];
     {
         const int p0 = min(t, last), p1 = min(t + NT, last);
@@ -1223,35 +1243,35 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
     }
     // ---- q (wave 0) and this position's k, v (wave 1): norm + NEOX rope (imi/core/seoul.cpp:19-28) ----
     if (wv < 2) {   // lane holds dimensions lane + 64 c; at D 128 a rope pair (i, i + 64) sits in one lane
-        const bool is_k = wv == 1;
-        const float* src = is_k ? row + Hq + g * D : row + h * D;
-        const float* w = is_k ? a.k_norm : a.q_norm;
+        if (!EARLY_QK) load_qk();
         float* st = stg + wv * D;
         float x[DPL], n[DPL];
 #pragma unroll
         for (int c = 0; c < DPL; c++) {
             const int e = lane + 64 * c;
-            x[c] = e < D ? src[e] : 0.0f;
+            x[c] = e < D ? xq[c] : 0.0f;
             if (e < D) st[e] = x[c];
         }
         __builtin_amdgcn_wave_barrier();
         const float s = rms_scale_wave(st, D, a.eps);
 #pragma unroll
-        for (int c = 0; c < DPL; c++) n[c] = lane + 64 * c < D ? x[c] * s * w[lane + 64 * c] : 0.0f;
+        for (int c = 0; c < DPL; c++) n[c] = lane + 64 * c < D ? x[c] * s * wq[c] : 0.0f;
         const float sh = __shfl(n[0], lane < half ? lane + half : lane - half);
 #pragma unroll
         for (int c = 0; c < DPL; c++) {
             const int e = lane + 64 * c;
             if (e < D) {
                 const float other = DPL == 2 ? n[c ^ 1] : sh;
-                const float2 cz = cs[e < half ? e : e - half];
+                const float2 cz = cq[c];
                 const float r = e < half ? fmaf(n[c], cz.x, -(other * cz.y)) : fmaf(other, cz.y, n[c] * cz.x);
                 if (is_k) {
                     const uint16_t kh = f2h(r);
                     k_s[e] = h2f(kh);
                     if (hh == 0) {
                         kc[(size_t)pos * D + e] = kh;
-                        vc[(size_t)pos * D + e] = f2h(row[Hq + kvd + g * D + e]);
+                        float v = vq[c];
+                        asm volatile("" : "+v"(v));   // (keeps the conversion, and the wait for v, here)
+                        vc[(size_t)pos * D + e] = f2h(v);
                     }
                 } else {
                     q_s[e] = r;
