@@ -252,6 +252,14 @@ int sh_q4_bench_kernel(sh_ctx* ctx, sh_q4* const* tables, int n_tables, int n_in
  * the same bytes can reach. */
 int sh_bench_empty(int device, int grid, int reps, double* us_per_launch);
 int sh_bench_read(int device, long long bytes, int copies, int grid, int reps, double* us_per_launch, double* stamps);
+/* Calibration: `launches` launches of `grid` workgroups back to back on one stream; xcc[l * grid + b] = the XCD
+ * (hardware register XCC_ID) workgroup b of launch l ran on. Calibration: whether a launch finds in the L2 what the
+ * launch before it read: `pairs` times, launch A and then launch B read the same 72 KB slot per workgroup (256
+ * workgroups, 18.9 MB, cached loads; *same_xcd counts workgroups of B on the XCD of A's workgroup with the same index,
+ * summed over pairs), and B alone reads slots no launch has read. us_second / us_alone: B's event time, averaged.
+ * Under rocprofv3's TCC_HIT / TCC_MISS counters B misses every line either way. No counterpart in the reference. */
+int sh_bench_xcc(int device, int grid, int launches, int* xcc);
+int sh_bench_l2_reuse(int device, int pairs, double* us_second, double* us_alone, int* same_xcd);
 
 /* y[i] = e^x[i] with the exponential the kernels use (softmax, SiLU, head gates): bit for bit the C library's expf
  * that imi runs on (imi/core/seoul.cpp:48,447,451). */

@@ -30,7 +30,7 @@ EXPORTS = [
     "sh_file_n_tensors", "sh_file_tensor", "sh_file_key_arr", "sh_file_block",
     "sh_codec_load", "sh_codec_free", "sh_codec_info", "sh_codec_reset", "sh_codec_frame", "sh_codec_flush",
     "sh_ears_load", "sh_ears_free", "sh_ears_info", "sh_ears_positions", "sh_ears_encode", "sh_ears_mel",
-    "sh_bench_empty", "sh_bench_read",
+    "sh_bench_empty", "sh_bench_read", "sh_bench_xcc", "sh_bench_l2_reuse",
 ]
 
 
@@ -143,6 +143,8 @@ def load_library(path: str = LIB_PATH):
         "sh_codec_flush": (i, [vp, vp, P(i)]),
         "sh_bench_empty": (i, [i, i, i, P(d)]),
         "sh_bench_read": (i, [i, C.c_longlong, i, i, i, P(d), vp]),
+        "sh_bench_xcc": (i, [i, i, i, vp]),
+        "sh_bench_l2_reuse": (i, [i, i, P(d), P(d), P(i)]),
         "sh_ears_load": (i, [i, C.c_char_p, P(vp)]),
         "sh_ears_free": (i, [vp]),
         "sh_ears_info": (i, [vp, P(EarsShape)]),
@@ -477,6 +479,23 @@ def bench_read(nbytes: int, copies: int = 64, grid: int = 1152, reps: int = 256,
     _check(L.sh_bench_read(int(device), int(nbytes), int(copies), int(grid), int(reps), C.byref(us),
                            st.ctypes.data if stamps else None))
     return (us.value, tuple(float(v) for v in st)) if stamps else us.value
+
+
+def bench_xcc(grid: int = 256, launches: int = 4, device: int = 0) -> np.ndarray:
+    """XCD of each workgroup over `launches` launches back to back: array [launches][grid]."""
+    L = load_library()
+    out = np.zeros((int(launches), int(grid)), np.int32)
+    _check(L.sh_bench_xcc(int(device), int(grid), int(launches), out.ctypes.data))
+    return out
+
+
+def bench_l2_reuse(pairs: int = 8, device: int = 0) -> dict:
+    """A launch reading what the launch before it read (same 72 KB slot per workgroup) against one reading fresh
+    slots: event microseconds of each, and how many workgroups ran on the same XCD as their counterpart."""
+    L = load_library()
+    a, b, same = C.c_double(), C.c_double(), C.c_int()
+    _check(L.sh_bench_l2_reuse(int(device), int(pairs), C.byref(a), C.byref(b), C.byref(same)))
+    return {"second_read_us": a.value, "fresh_read_us": b.value, "same_xcd": same.value, "workgroups": 256 * int(pairs)}
 
 
 def q4_bench(ctx: Context, tables, n_in: int = 1, cut_mode: int = 0, reps: int = 200) -> float:

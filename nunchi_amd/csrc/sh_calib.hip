@@ -48,6 +48,39 @@ __global__ __launch_bounds__(256) void k_read(const uint4* __restrict__ a, size_
     }
 }
 
+// the XCD (accelerator complex die) each workgroup runs on: hardware register XCC_ID, read by the scalar unit
+__global__ __launch_bounds__(64) void k_xcc(int* out) {
+    unsigned v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(v));
+    if (threadIdx.x == 0) out[blockIdx.x] = (int)v;
+}
+
+// one 72 KB slot per workgroup (512 threads x 9 x 16 B), slot (b + shift) % grid, ordinary (cached) or non-temporal
+// loads; thread 0 records the workgroup's XCD
+typedef unsigned u32x4c __attribute__((ext_vector_type(4)));
+constexpr int L2_SLOT_WORDS = 4608;
+__global__ __launch_bounds__(512) void k_pull(const u32x4c* base, int shift, int nt, unsigned* out, int* xid) {
+    const int g = gridDim.x, b = (blockIdx.x + shift) % g;
+    const u32x4c* p = base + (size_t)b * L2_SLOT_WORDS + threadIdx.x;
+    u32x4c v[9];
+    if (nt) {
+#pragma unroll
+        for (int q = 0; q < 9; q++) v[q] = __builtin_nontemporal_load(p + 512 * q);
+    } else {
+#pragma unroll
+        for (int q = 0; q < 9; q++) v[q] = p[512 * q];
+    }
+    unsigned acc = 0;
+#pragma unroll
+    for (int q = 0; q < 9; q++) acc ^= v[q].x ^ v[q].y ^ v[q].z ^ v[q].w;
+    if (acc == 0x9E3779B9u) out[blockIdx.x] = acc;   // (keeps the loads)
+    if (threadIdx.x == 0) {
+        unsigned x;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(x));
+        xid[blockIdx.x] = (int)x;
+    }
+}
+
 #define KCHK(x)                                                                                                 \
     do {                                                                                                        \
         const hipError_t e_ = (x);                                                                              \
@@ -141,6 +174,79 @@ done:
     if (st) (void)hipFree(st);
     if (a) (void)hipFree(a);
     return err == hipSuccess ? SH_OK : set_error(SH_E_HIP, std::string("sh_bench_read: ") + hipGetErrorString(err));
+}
+
+int sh_bench_xcc(int device, int grid, int launches, int* xcc) {
+    if (grid < 1 || grid > 65536 || launches < 1 || launches > 64 || !xcc) return set_error(SH_E_ARG, "sh_bench_xcc: bad argument");
+    if (hipSetDevice(device) != hipSuccess) return set_error(SH_E_HIP, "sh_bench_xcc: device");
+    hipError_t err = hipSuccess;
+    int* out = nullptr;
+    hipStream_t s = nullptr;
+    KCHK(hipMalloc((void**)&out, sizeof(int) * (size_t)grid * launches));
+    KCHK(hipStreamCreate(&s));
+    for (int l = 0; l < launches; l++) hipLaunchKernelGGL(k_xcc, dim3(grid), dim3(64), 0, s, out + (size_t)l * grid);
+    KCHK(hipStreamSynchronize(s));
+    KCHK(hipMemcpy(xcc, out, sizeof(int) * (size_t)grid * launches, hipMemcpyDeviceToHost));
+done:
+    if (s) (void)hipStreamSynchronize(s), (void)hipStreamDestroy(s);
+    if (out) (void)hipFree(out);
+    return err == hipSuccess ? SH_OK : set_error(SH_E_HIP, std::string("sh_bench_xcc: ") + hipGetErrorString(err));
+}
+
+int sh_bench_l2_reuse(int device, int pairs, double* us_second, double* us_alone, int* same_xcd) {
+    if (pairs < 1 || pairs > 64 || !us_second || !us_alone || !same_xcd) return set_error(SH_E_ARG, "sh_bench_l2_reuse: bad argument");
+    if (hipSetDevice(device) != hipSuccess) return set_error(SH_E_HIP, "sh_bench_l2_reuse: device");
+    const int grid = 256;
+    const size_t region = (size_t)grid * L2_SLOT_WORDS;   // 16-byte words: 18.9 MB
+    hipError_t err = hipSuccess;
+    u32x4c* buf = nullptr;
+    unsigned* out = nullptr;
+    int* xid = nullptr;
+    hipStream_t s = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    std::vector<int> h(2 * grid);
+    double t2 = 0, t1 = 0;
+    int same = 0;
+    KCHK(hipMalloc((void**)&buf, region * 16 * (size_t)(2 * pairs)));
+    KCHK(hipMemset(buf, 1, region * 16 * (size_t)(2 * pairs)));
+    KCHK(hipMalloc((void**)&out, 4 * grid));
+    KCHK(hipMalloc((void**)&xid, sizeof(int) * 2 * grid));
+    KCHK(hipStreamCreate(&s));
+    KCHK(hipEventCreate(&e0));
+    KCHK(hipEventCreate(&e1));
+    for (int i = 0; i < pairs; i++) {
+        float ms = 0;
+        u32x4c* ra = buf + region * (size_t)(2 * i);
+        u32x4c* rb = ra + region;
+        // A then B over the same slots (workgroup b reads slot b in both), cached loads in both
+        hipLaunchKernelGGL(k_pull, dim3(grid), dim3(512), 0, s, ra, 0, 0, out, xid);
+        KCHK(hipEventRecord(e0, s));
+        hipLaunchKernelGGL(k_pull, dim3(grid), dim3(512), 0, s, ra, 0, 0, out, xid + grid);
+        KCHK(hipEventRecord(e1, s));
+        KCHK(hipEventSynchronize(e1));
+        KCHK(hipEventElapsedTime(&ms, e0, e1));
+        t2 += ms;
+        KCHK(hipMemcpy(h.data(), xid, sizeof(int) * 2 * grid, hipMemcpyDeviceToHost));
+        for (int b = 0; b < grid; b++) same += h[b] == h[grid + b];
+        // B alone on slots no launch has read
+        KCHK(hipEventRecord(e0, s));
+        hipLaunchKernelGGL(k_pull, dim3(grid), dim3(512), 0, s, rb, 0, 0, out, xid + grid);
+        KCHK(hipEventRecord(e1, s));
+        KCHK(hipEventSynchronize(e1));
+        KCHK(hipEventElapsedTime(&ms, e0, e1));
+        t1 += ms;
+    }
+    *us_second = 1e3 * t2 / pairs;
+    *us_alone = 1e3 * t1 / pairs;
+    *same_xcd = same;
+done:
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (s) (void)hipStreamSynchronize(s), (void)hipStreamDestroy(s);
+    if (xid) (void)hipFree(xid);
+    if (out) (void)hipFree(out);
+    if (buf) (void)hipFree(buf);
+    return err == hipSuccess ? SH_OK : set_error(SH_E_HIP, std::string("sh_bench_l2_reuse: ") + hipGetErrorString(err));
 }
 
 }  // extern "C"
