@@ -533,7 +533,7 @@ struct imi_ears {
         out.resize((size_t)P * n_out);
         if (sh_ears_encode(e, pcm, n, out.data(), &P) != SH_OK) return report("encode"), 0;
         last_mel.resize((size_t)F * n_mel);
-        if (sh_ears_mel(e, last_mel.data(), &F) != SH_OK) report("mel");
+        if (sh_ears_mel(e, last_mel.data(), F, &F) != SH_OK) report("mel");
         return P;
     }
 

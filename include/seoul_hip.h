@@ -94,8 +94,9 @@ int sh_ears_positions(const sh_ears* e, int n_samples, int* n_pos, int* n_frames
 /* imi_ears::encode (ears.cpp:198-407): 16 kHz samples from the clip's start -> out [n_pos][n_out] (host memory,
  * room for sh_ears_positions' count). Blocking. */
 int sh_ears_encode(sh_ears* e, const float* pcm, int n_samples, float* out, int* n_pos);
-/* The last encode's mel frames [n_frames][n_mel] (imi_ears::last_mel), into host memory. */
-int sh_ears_mel(const sh_ears* e, float* mel, int* n_frames);
+/* The last encode's mel frames [n_frames][n_mel] (imi_ears::last_mel), into host memory that holds cap_frames
+ * frames: SH_E_ARG (nothing written) when the last encode has more. mel may be null to ask for *n_frames only. */
+int sh_ears_mel(const sh_ears* e, float* mel, int cap_frames, int* n_frames);
 
 /* ---- GGUF file: imi_file::load / get / key_i / key_f / keep / drop_data (imi/model.h:12-36) ---- */
 /* The ggml_tensor fields imi's callers read. name points into the file object; data is the tensor's bytes in host
@@ -213,7 +214,10 @@ int sh_q4_gemm(sh_ctx* ctx, const sh_q4* t, const float* x, int n, float* y);
  * graph capture, serving loops with a fixed memory budget). The int8 cut of the input goes to a fixed scratch array
  * of device memory the library holds on every device it runs on until the process ends (1.25 MiB per device), so
  * n * cols <= 1048576 (else SH_E_ARG, nothing launched) and 1 <= n <= 512. Calls on one device share that scratch:
- * calls that overlap on one device race. Enqueued on the context's stream without waiting (sh_sync waits). */
+ * calls of one context are ordered by its stream, and a call from a context other than the device's last user waits on
+ * its own stream for an event recorded after that call (an event made at sh_create, no device memory). Under graph
+ * capture of the context's stream no event is used: captured calls of two contexts replaying at once on one device
+ * race. Enqueued on the context's stream without waiting (sh_sync waits). */
 int sh_q4_gemm_noalloc(sh_ctx* ctx, const sh_q4* t, const float* x_dev, int n, float* y_dev);
 /* Dequantized rows: out[n][cols] = (code - 8) * d of rows ids[n] (the input-row lookup of a tied word table,
  * imi/core/seoul.cpp:363, ggml_get_rows in imi/brain.cpp:161). Bit-exact. */

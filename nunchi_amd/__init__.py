@@ -150,7 +150,7 @@ def load_library(path: str = LIB_PATH):
         "sh_ears_info": (i, [vp, P(EarsShape)]),
         "sh_ears_positions": (i, [vp, i, P(i), P(i)]),
         "sh_ears_encode": (i, [vp, vp, i, vp, P(i)]),
-        "sh_ears_mel": (i, [vp, vp, P(i)]),
+        "sh_ears_mel": (i, [vp, vp, i, P(i)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -613,12 +613,13 @@ class Ears:
         assert n.value == P
         return out
 
-    def mel(self, n_samples: int) -> np.ndarray:
-        _, F = self.positions(n_samples)
-        m = np.zeros((F, self.info.n_mel), np.float32)
+    def mel(self) -> np.ndarray:
+        """The last encode's mel frames [n_frames][n_mel], sized from that encode's frame count."""
         n = C.c_int()
-        _check(_lib.sh_ears_mel(self.h, _p(m), C.byref(n)))
-        return m[:n.value]
+        _check(_lib.sh_ears_mel(self.h, None, 0, C.byref(n)))
+        m = np.zeros((n.value, self.info.n_mel), np.float32)
+        _check(_lib.sh_ears_mel(self.h, _p(m), int(n.value), C.byref(n)))
+        return m
 
 
 _live_voices = weakref.WeakSet()

@@ -86,39 +86,60 @@ bool gg_file::load(const std::string& path) {
         if (k.type == 9) {
             const int et = (int)c.num<uint32_t>();
             const uint64_t n = c.num<uint64_t>();
+            if (n > c.size - c.at) c.ok = false;   // every element takes at least one byte
             for (uint64_t e = 0; e < n && c.ok; e++) { kv tmp; scalar(et, tmp); k.arr.push_back(tmp.i); }
         } else {
             scalar(k.type, k);
         }
-        if (k.key == "general.alignment" && k.i > 0) alignment = (size_t)k.i;
+        if (k.key == "general.alignment") {
+            // a power of two no larger than the file (ggml's gguf reader refuses any other)
+            if (k.type == 9 || k.type == 8 || k.i <= 0 || (uint64_t)k.i > map_size || (k.i & (k.i - 1)) != 0) {
+                error = path + ": bad general.alignment";
+                return false;
+            }
+            alignment = (size_t)k.i;
+        }
         kvs.push_back(std::move(k));
     }
     for (uint64_t i = 0; i < n_tensors && c.ok; i++) {
         gg_tensor t;
         t.name = c.str();
-        t.n_dims = (int)c.num<uint32_t>();
-        if (t.n_dims < 1 || t.n_dims > 4) { c.ok = false; break; }
+        const uint32_t nd = c.num<uint32_t>();
+        if (!c.ok || nd < 1 || nd > 4) { c.ok = false; break; }
+        t.n_dims = (int)nd;
         for (int d = 0; d < t.n_dims; d++) t.ne[d] = (int64_t)c.num<uint64_t>();
         t.type = (int)c.num<uint32_t>();
         t.offset = c.num<uint64_t>();
+        if (!c.ok) break;
+        for (int d = 0; d < 4; d++)
+            if (t.ne[d] < 0) { error = "tensor " + t.name + " has a negative dimension"; return false; }
         size_t blk = 0;
         int64_t per = 1;
         if (!type_block(t.type, &blk, &per)) { error = "tensor " + t.name + " has a type this engine does not read"; return false; }
         if (t.ne[0] % per) { error = "tensor " + t.name + " has rows that are not whole blocks"; return false; }
-        const size_t row = (size_t)(t.ne[0] / per) * blk;
+        // byte strides and size, refused when any product overflows
+        size_t row = 0, n2 = 0, n3 = 0, all = 0;
+        if (__builtin_mul_overflow((size_t)(t.ne[0] / per), blk, &row) || __builtin_mul_overflow(row, (size_t)t.ne[1], &n2) ||
+            __builtin_mul_overflow(n2, (size_t)t.ne[2], &n3) || __builtin_mul_overflow(n3, (size_t)t.ne[3], &all)) {
+            error = "tensor " + t.name + " is too large";
+            return false;
+        }
         t.nb[0] = blk;
         t.nb[1] = row;
-        t.nb[2] = row * (size_t)t.ne[1];
-        t.nb[3] = t.nb[2] * (size_t)t.ne[2];
-        t.nbytes = t.nb[3] * (size_t)t.ne[3];
+        t.nb[2] = n2;
+        t.nb[3] = n3;
+        t.nbytes = all;
         tensors.push_back(std::move(t));
     }
     if (!c.ok) { error = path + ": malformed GGUF header"; return false; }
+    // (c.at <= map_size and alignment <= map_size, so the sum does not wrap)
     const size_t data0 = (c.at + alignment - 1) / alignment * alignment;
+    if (data0 > map_size) { error = path + ": no data block"; return false; }
     block = static_cast<const uint8_t*>(map) + data0;
-    block_size = map_size > data0 ? map_size - data0 : 0;
+    block_size = map_size - data0;
     for (auto& t : tensors) {
-        if (data0 + t.offset + t.nbytes > map_size) { error = "short read on " + t.name; return false; }
+        // offset and size each within the block, compared without sums that could wrap
+        if (t.offset > block_size || t.nbytes > block_size - t.offset) { error = "short read on " + t.name; return false; }
         t.data = static_cast<const uint8_t*>(map) + data0 + t.offset;
     }
     return true;

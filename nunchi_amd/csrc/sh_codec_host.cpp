@@ -410,12 +410,15 @@ int sh_codec_frame(sh_codec* c, const int32_t* codes, float* pcm, int* n_out) { 
     CCHK(hipMemcpyAsync(c->in_dev, &in, sizeof in, hipMemcpyHostToDevice, c->stream));
     if (c->use_graph) {
         if (!c->graph) {
-            hipGraph_t g;
+            hipGraph_t g = nullptr;
             CCHK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
             const int rc = enqueue_frame(c);
             const hipError_t e = hipStreamEndCapture(c->stream, &g);
-            if (rc != SH_OK) return rc;
-            if (e != hipSuccess) return set_error(SH_E_HIP, std::string("sh_codec_frame: capture: ") + hipGetErrorString(e));
+            if (rc != SH_OK || e != hipSuccess) {   // (the captured graph, if any, is not kept)
+                if (g) (void)hipGraphDestroy(g);
+                if (rc != SH_OK) return rc;
+                return set_error(SH_E_HIP, std::string("sh_codec_frame: capture: ") + hipGetErrorString(e));
+            }
             const hipError_t ei = hipGraphInstantiate(&c->graph, g, nullptr, nullptr, 0);
             (void)hipGraphDestroy(g);
             if (ei != hipSuccess) { c->graph = nullptr; return set_error(SH_E_HIP, std::string("sh_codec_frame: instantiate: ") + hipGetErrorString(ei)); }

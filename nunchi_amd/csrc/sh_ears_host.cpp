@@ -534,12 +534,16 @@ int sh_ears_encode(sh_ears* e, const float* pcm, int n, float* out, int* n_pos) 
     return SH_OK;
 }
 
-int sh_ears_mel(const sh_ears* e, float* mel, int* n_frames) {
-    if (!e || !mel) return set_error(SH_E_ARG, "sh_ears_mel: bad argument");
+int sh_ears_mel(const sh_ears* e, float* mel, int cap_frames, int* n_frames) {
+    if (!e || (!mel && !n_frames) || cap_frames < 0) return set_error(SH_E_ARG, "sh_ears_mel: bad argument");
     if (!e->mel || e->last_frames == 0) return set_error(SH_E_STATE, "sh_ears_mel: nothing encoded yet");
+    if (n_frames) *n_frames = e->last_frames;
+    if (!mel) return SH_OK;   // the frame count only
+    if (e->last_frames > cap_frames)
+        return set_error(SH_E_ARG, "sh_ears_mel: the last encode has " + std::to_string(e->last_frames) +
+                                       " frames, the buffer holds " + std::to_string(cap_frames));
     ECHK(hipSetDevice(e->device));
     ECHK(hipMemcpy(mel, e->mel, (size_t)e->last_frames * e->info.n_mel * 4, hipMemcpyDeviceToHost));
-    if (n_frames) *n_frames = e->last_frames;
     return SH_OK;
 }
 

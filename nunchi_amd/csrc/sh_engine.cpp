@@ -293,12 +293,15 @@ int get_graph(sh_ctx* c, int M, bool want_logits, hipGraphExec_t* out) {
     }
     hipGraphExec_t& g = c->graph[M][want_logits ? 1 : 0];
     if (!g) {
-        hipGraph_t graph;
+        hipGraph_t graph = nullptr;
         HIPCHK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
         const int rc = enqueue_step(c, M, want_logits);
         hipError_t e = hipStreamEndCapture(c->stream, &graph);
-        if (rc != SH_OK) return rc;
-        if (e != hipSuccess) return fail(SH_E_HIP, std::string("graph capture: ") + hipGetErrorString(e));
+        if (rc != SH_OK || e != hipSuccess) {   // (the captured graph, if any, is not kept)
+            if (graph) (void)hipGraphDestroy(graph);
+            if (rc != SH_OK) return rc;
+            return fail(SH_E_HIP, std::string("graph capture: ") + hipGetErrorString(e));
+        }
         e = hipGraphInstantiate(&g, graph, nullptr, nullptr, 0);
         (void)hipGraphDestroy(graph);
         if (e != hipSuccess) { g = nullptr; return fail(SH_E_HIP, std::string("graph instantiate: ") + hipGetErrorString(e)); }

@@ -1,8 +1,12 @@
 // The kernel-level batch product (sh_q4_gemm) for callers that cannot allocate device memory: code under HIP
 // graph capture, serving loops with a fixed memory budget. Its one work buffer, the int8 cut of the input
 // (block-major codes, scales and d * sum per 32 columns), lives in a fixed array of device memory, one copy per
-// device, held until the process ends. Every call on a device uses that device's copy, so calls that overlap on one
-// device race; each call's cut kernel writes every entry its product reads, so nothing needs clearing between calls.
+// device, held until the process ends. Every call on a device uses that device's copy: calls of one context are
+// ordered by its stream, and a call from another context than the device's last user first waits (on its own stream)
+// for an event recorded after that last call, so contexts on one device do not overwrite each other's cut. Each call's
+// cut kernel writes every entry its product reads, so nothing needs clearing between calls. Under graph capture of
+// the context's stream no event is recorded or waited for: calls from two contexts captured into graphs that replay
+// at the same time on one device race.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -23,6 +27,8 @@ static __device__ __align__(256) unsigned char scratch[NA_BYTES];
 constexpr int NA_MAX_DEVICES = 64;
 std::mutex g_mu;
 unsigned char* g_ptr[NA_MAX_DEVICES] = {};   // the array's address on each device (0 until set up)
+hipEvent_t g_ev[NA_MAX_DEVICES] = {};        // recorded after each call on the device
+const sh_ctx* g_last[NA_MAX_DEVICES] = {};   // the context of that call (compared only, never dereferenced)
 
 }  // namespace
 
@@ -35,7 +41,11 @@ int noalloc_setup(int device) {
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p) return set_error(SH_E_HIP, std::string("noalloc: hipGetSymbolAddress: ") + hipGetErrorString(e));
+    hipEvent_t ev = nullptr;
+    const hipError_t ee = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (ee != hipSuccess) return set_error(SH_E_HIP, std::string("noalloc: hipEventCreate: ") + hipGetErrorString(ee));
     g_ptr[device] = static_cast<unsigned char*>(p);
+    g_ev[device] = ev;
     return SH_OK;
 }
 
@@ -51,13 +61,17 @@ extern "C" int sh_q4_gemm_noalloc(sh_ctx* c, const sh_q4* t, const float* x_dev,
     if (codes > NA_MAX_CODES)
         return set_error(SH_E_ARG, "sh_q4_gemm_noalloc: n * cols = " + std::to_string(codes) + " is above the scratch maximum of " +
                                        std::to_string(NA_MAX_CODES));
-    unsigned char* base = nullptr;
-    {
-        std::lock_guard<std::mutex> lk(g_mu);
-        base = (c->device >= 0 && c->device < NA_MAX_DEVICES) ? g_ptr[c->device] : nullptr;
-    }
+    // (the lock is held over the wait, both launches and the record, so two threads' calls cannot interleave)
+    std::lock_guard<std::mutex> lk(g_mu);
+    const int dev = c->device;
+    unsigned char* base = (dev >= 0 && dev < NA_MAX_DEVICES) ? g_ptr[dev] : nullptr;
     if (!base) return set_error(SH_E_STATE, "sh_q4_gemm_noalloc: no scratch on this context's device");
-    hipError_t e = hipSetDevice(c->device);
+    hipError_t e = hipSetDevice(dev);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (e == hipSuccess) e = hipStreamIsCapturing(c->stream, &cap);
+    const bool capturing = cap != hipStreamCaptureStatusNone;
+    // another context's call may still be reading the scratch: this stream waits for it
+    if (e == hipSuccess && !capturing && g_last[dev] && g_last[dev] != c) e = hipStreamWaitEvent(c->stream, g_ev[dev], 0);
     const pf_cut cut{reinterpret_cast<int8_t*>(base), reinterpret_cast<float*>(base + NA_MAX_CODES),
                      reinterpret_cast<float*>(base + NA_MAX_CODES + NA_SCALE_BYTES)};
     if (e == hipSuccess) e = launch_pf_cut(pf_cutk_args{x_dev, W.cols, W.cols, n, cut}, c->stream);
@@ -68,6 +82,10 @@ extern "C" int sh_q4_gemm_noalloc(sh_ctx* c, const sh_q4* t, const float* x_dev,
     g.out = y_dev;
     g.out_ld = W.rows;
     if (e == hipSuccess) e = launch_pf_gemm(EPI_STORE, g, c->stream);
+    if (e == hipSuccess && !capturing) {
+        e = hipEventRecord(g_ev[dev], c->stream);
+        if (e == hipSuccess) g_last[dev] = c;
+    }
     if (e != hipSuccess) return set_error(SH_E_HIP, std::string("sh_q4_gemm_noalloc: ") + hipGetErrorString(e));
     return SH_OK;
 }

@@ -431,8 +431,11 @@ int sh_voice_pass(sh_voice* v, const int32_t* codes, const int32_t* need, int n_
             VCHK(hipStreamBeginCapture(v->stream, hipStreamCaptureModeThreadLocal));
             const int rc = enqueue_pass(v);
             const hipError_t ec = hipStreamEndCapture(v->stream, &gr);
-            if (rc != SH_OK) { if (gr) (void)hipGraphDestroy(gr); return rc; }
-            VCHK(ec);
+            if (rc != SH_OK || ec != hipSuccess) {   // (the captured graph, if any, is not kept)
+                if (gr) (void)hipGraphDestroy(gr);
+                if (rc != SH_OK) return rc;
+                VCHK(ec);
+            }
             const hipError_t ei = hipGraphInstantiate(&v->graph, gr, nullptr, nullptr, 0);
             (void)hipGraphDestroy(gr);
             VCHK(ei);

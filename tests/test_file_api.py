@@ -164,3 +164,54 @@ def test_cpp_brain_caller_on_gpu(tiny_model, tmp_path):
         want.append(oracle.top(lg))
     assert ids == want, (ids, want)
     assert "pos 12" in out.stdout and "reset repeats 1" in out.stdout
+
+
+def _crafted_gguf(path, *, alignment=32, align_type=4, ne=(64, 2), gtype=0, offset=0, data_bytes=512):
+    """One F32 (or other) tensor after a general.alignment key, every field written as given (not checked here)."""
+    def s(x):
+        b = x.encode()
+        return struct.pack("<Q", len(b)) + b
+    out = bytearray(struct.pack("<IIQQ", 0x46554747, 3, 1, 1))
+    out += s("general.alignment") + struct.pack("<I", align_type)
+    out += struct.pack("<I" if align_type == 4 else "<Q", alignment)
+    out += s("t") + struct.pack("<I", len(ne))
+    for d in ne:
+        out += struct.pack("<Q", d & 0xFFFFFFFFFFFFFFFF)
+    out += struct.pack("<IQ", gtype, offset & 0xFFFFFFFFFFFFFFFF)
+    out += b"\0" * ((-len(out)) % 32) + b"\1" * data_bytes
+    with open(path, "wb") as f:
+        f.write(out)
+
+
+@pytest.mark.parametrize("case", [
+    dict(offset=1 << 63),                       # offset past the file
+    dict(offset=(1 << 64) - 64),                # offset that wraps the data start + offset sum
+    dict(offset=64, data_bytes=512),            # in range, but the tensor runs past the end
+    dict(ne=(64, -2)),                          # negative dimension
+    dict(ne=(1 << 40, 1 << 30)),                # byte size overflows 64 bits
+    dict(ne=(32, 1 << 40, 1 << 30), gtype=2),   # Q4_0 row count times rows overflows
+    dict(alignment=3),                          # not a power of two
+    dict(alignment=0),                          # zero
+    dict(alignment=1 << 40, align_type=10),     # larger than the file
+    dict(ne=(), data_bytes=0),                  # no dimensions
+    dict(ne=(1, 1, 1, 1, 1)),                   # more than 4 dimensions
+])
+def test_malformed_headers_are_refused(tmp_path, case):
+    """imi loads through ggml's gguf reader, which refuses these headers; the build's reader returns SH_E_FILE for
+    each (no pointer outside the mapping is ever formed)."""
+    import nunchi_amd
+    p = str(tmp_path / "bad.gguf")
+    _crafted_gguf(p, **case)
+    with pytest.raises(nunchi_amd.SeoulError) as e:
+        nunchi_amd.File(p)
+    assert e.value.code == nunchi_amd.SH_E_FILE
+
+
+def test_crafted_header_control_loads(tmp_path):
+    """The same writer with sane fields loads, so the refusals above are about the field each one breaks."""
+    import nunchi_amd
+    p = str(tmp_path / "ok.gguf")
+    _crafted_gguf(p)
+    f = nunchi_amd.File(p)
+    t = f.get("t")
+    assert t is not None and tuple(t["ne"][:2]) == (64, 2)

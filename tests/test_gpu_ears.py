@@ -29,7 +29,7 @@ def test_tiny_ears_matches_oracle(tiny_ears, n):
     out = g.encode(pcm)
     ref, mel = oracle.Ears(tiny_ears, threads=4).encode(pcm, mel=True)
     assert out.shape == ref.shape
-    assert oracle.rel(g.mel(n), mel) < TOL
+    assert oracle.rel(g.mel(), mel) < TOL
     assert oracle.rel(out, ref) < TOL, oracle.rel(out, ref)
 
 
@@ -62,3 +62,26 @@ def test_bad_arguments_are_refused(tiny_ears):
     g = nunchi_amd.Ears(tiny_ears)
     with pytest.raises(nunchi_amd.SeoulError):
         g.encode(np.zeros(0, np.float32))
+
+
+def test_mel_buffer_capacity_is_checked(tiny_ears):
+    """sh_ears_mel writes only into a buffer that holds the last encode's frames: after a long clip, a buffer sized
+    for a short one is refused with nothing written, and the binding sizes its buffer from the last encode."""
+    import ctypes as C
+    import nunchi_amd
+    from nunchi_amd import synth
+    g = nunchi_amd.Ears(tiny_ears)
+    long_n, short_n = 7 * 16000 + 123, 16000
+    g.encode(synth.clip(long_n, 5))
+    _, f_long = g.positions(long_n)
+    _, f_short = g.positions(short_n)
+    assert f_short < f_long
+    lib = nunchi_amd.load_library()
+    buf = np.full((f_short + 1, g.info.n_mel), 7.0, np.float32)   # one guard frame past the capacity
+    n = C.c_int(-1)
+    rc = lib.sh_ears_mel(g.h, buf.ctypes.data, f_short, C.byref(n))
+    assert rc == nunchi_amd.SH_E_ARG
+    assert n.value == f_long
+    assert np.all(buf == 7.0)
+    m = g.mel()
+    assert m.shape == (f_long, g.info.n_mel)

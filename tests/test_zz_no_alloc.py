@@ -83,3 +83,37 @@ def test_noalloc_gemm_refuses_above_the_scratch():
     assert b"scratch" in nunchi_amd.load_library().sh_last_error()
     rc, y = _noalloc(ctx, t, x[:128])   # exactly at the limit
     assert rc == 0 and _same(y, t.gemm(x[:128]))
+
+
+def test_noalloc_two_contexts_on_one_device():
+    """Two contexts on device 0 share the device's scratch: the second context's call, enqueued while the first one's
+    may still run, waits for it, so both products equal their allocating counterparts bit for bit."""
+    import nunchi_amd
+    L, H = nunchi_amd.load_library(), _hip()
+    ca, cb = nunchi_amd.Context(0), nunchi_amd.Context(0)
+    ta, tb = _table(ca, 2048, 2048, 8), _table(cb, 1024, 2048, 9)
+    rng = np.random.default_rng(11)
+    xa = rng.standard_normal((448, 2048)).astype(np.float32)
+    xb = rng.standard_normal((400, 2048)).astype(np.float32)
+    bufs = []
+    try:
+        def dev(a):
+            p = C.c_void_p()
+            assert H.hipMalloc(C.byref(p), a.nbytes) == 0
+            bufs.append(p)
+            assert H.hipMemcpy(p, a.ctypes.data_as(C.c_void_p), a.nbytes, 1) == 0
+            return p
+        ya = np.full((448, ta.rows), np.nan, np.float32)
+        yb = np.full((400, tb.rows), np.nan, np.float32)
+        xad, xbd, yad, ybd = dev(xa), dev(xb), dev(ya), dev(yb)
+        for _ in range(3):   # a, b, a, b, ... with no wait between the two contexts' calls
+            assert L.sh_q4_gemm_noalloc(ca.h, ta.h, xad, 448, yad) == 0
+            assert L.sh_q4_gemm_noalloc(cb.h, tb.h, xbd, 400, ybd) == 0
+        assert L.sh_sync(ca.h) == 0 and L.sh_sync(cb.h) == 0
+        assert H.hipMemcpy(ya.ctypes.data_as(C.c_void_p), yad, ya.nbytes, 2) == 0
+        assert H.hipMemcpy(yb.ctypes.data_as(C.c_void_p), ybd, yb.nbytes, 2) == 0
+        assert _same(ya, ta.gemm(xa))
+        assert _same(yb, tb.gemm(xb))
+    finally:
+        for p in bufs:
+            H.hipFree(p)
