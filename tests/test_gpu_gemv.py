@@ -75,6 +75,17 @@ def test_gemv_exact_regime_bitwise(ctx, rows, cols):
     assert np.array_equal(got, orc)
 
 
+def _cut_dequant(x):
+    """imi's input cut (imi/core/vec.h:47-75) as float64 values q * d: per 32 values d = amax / 127 and
+    q = rint(x / d) in float32 arithmetic, as the engine computes them."""
+    x32 = np.asarray(x, np.float32).reshape(-1, 32)
+    d = (np.abs(x32).max(-1, keepdims=True) / np.float32(127)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        idv = np.where(d != 0, np.float32(1) / d, np.float32(0)).astype(np.float32)
+    q = np.rint((x32 * idv).astype(np.float32))
+    return (q.astype(np.float64) * d.astype(np.float64)).reshape(np.shape(x))
+
+
 @pytest.mark.parametrize("rows,cols", [(8192, 2048), (2048, 2048), (512, 2048), (2048, 8192), (3104, 2048), (64, 7680), (16, 64)])
 def test_gemv_matches_imi_arithmetic(ctx, rows, cols):
     import nunchi_amd
@@ -85,8 +96,7 @@ def test_gemv_matches_imi_arithmetic(ctx, rows, cols):
     orc, _ = oracle.Q4Table(blk, rows, cols, threads=4).gemv(x)
     assert np.array_equal(got.view(np.uint32), orc.view(np.uint32))
     # float64 of the same int8-cut input: both approximate it to fp32 accuracy
-    from oracle.exact import cut_dequant
-    ref = _dequant(blk, rows, cols) @ cut_dequant(x)
+    ref = _dequant(blk, rows, cols) @ _cut_dequant(x)
     scale = np.sqrt((ref ** 2).mean())
     assert np.abs(got - ref).max() < 1e-5 * scale + 1e-30
     assert np.abs(orc - ref).max() < 1e-5 * scale + 1e-30

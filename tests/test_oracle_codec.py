@@ -10,7 +10,8 @@ import numpy as np
 import pytest
 
 import oracle
-from oracle import exact
+# (the float64 restatements stay off the GPU box: without them this CPU-only module is skipped)
+exact = pytest.importorskip("oracle.exact")
 
 TOL = 5e-5   # float32 pipeline (fma chains, float sums) against float64: measured 4.9e-6 (tiny) and 1.1e-5 (full)
 

@@ -10,7 +10,8 @@ import numpy as np
 import pytest
 
 import oracle
-from oracle import exact
+# (the float64 restatements stay off the GPU box: without them this CPU-only module is skipped)
+exact = pytest.importorskip("oracle.exact")
 
 TOL = 5e-5   # float32 pipeline against float64: measured 2.0e-6 (tiny, 3 s) and 9.3e-6 (full shape, 30.7 s)
 
