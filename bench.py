@@ -93,6 +93,7 @@ def cpu_decode(path, threads, steps, b2: bool, runs: int = 1):
 
 
 VOICE_CTX = 4096      # slot A's KV context in the voice frame
+VOICE_WARMUP = 4      # untimed frames before the timed ones (slot B starts at position 0)
 A_POS = 2048          # slot A's position when the timed frames start
 SCHEDULE = (4, 4)     # masked passes of a frame: codebooks scored (and fixed) by each, in a shuffled order
 TALK_SCHEDULE = (6, 6)   # imi's schedule for its 12 codebooks (imi/core/talk.cpp:129)
@@ -429,6 +430,12 @@ def main():
                     help="only the cfg-0 GEMV (8192 x 2048 Q4_0, 64 copies in rotation) next to an empty dispatch and a "
                          "pure read of the same 9,437,184 bytes, each back to back: the launches a kernel trace of the "
                          "floor reads")
+    ap.add_argument("--layer-only", action="store_true",
+                    help="only cfg 1 (one layer's 7 linears through the kernel-level GEMV at B=1 and B=2, per table and "
+                         "grouped, 16 copies in rotation): the launches a kernel trace of cfg 1 reads")
+    ap.add_argument("--voice-only", type=int, default=0, metavar="FRAMES",
+                    help="only cfg 4: FRAMES voice frames (step2 at KV context 2048+, generator passes of 4 + 4 with "
+                         "sampling, after 4 untimed): the launches a kernel trace of the whole frame reads")
     ap.add_argument("--counters-workload", action="store_true",
                     help="only the launches the hardware-counter runs read: a streaming kernel of known size (the "
                          "exponential over 16 Mi floats: 64 MiB read, 64 MiB written), 64 read-only GEMVs of known "
@@ -497,7 +504,20 @@ def main():
                                          "table_bytes": int(codec.info.table_bytes)}}), flush=True)
         return
     path = synth.cached("brain", synth.SEOUL, 0)
+    if args.voice_only:
+        vpath = synth.cached("voice", synth.VOICE, 1)
+        (ft, fbr, fvo, _, _, _), _, vinfo = gpu_voice_frames(path, vpath, args.voice_only, VOICE_WARMUP)
+        print(json.dumps({"voice_only": {"frames": int(len(ft)), "p50_ms": round(float(np.percentile(ft, 50)) * 1e3, 3),
+                                         "step2_p50_ms": round(float(np.percentile(fbr, 50)) * 1e3, 3),
+                                         "generator_p50_ms": round(float(np.percentile(fvo, 50)) * 1e3, 3)}}), flush=True)
+        return
     brain = nunchi_amd.Brain(path, n_ctx=N_CTX)
+    if args.layer_only:
+        l_us1, l_us2, _, lg_us1, lg_us2, same = gpu_layer(brain.ctx, reps=16 * len(LAYER_TABLES) * 8)
+        print(json.dumps({"layer_only": {"b1_us": round(l_us1, 2), "b2_us": round(l_us2, 2), "grouped_b1_us": round(lg_us1, 2),
+                                         "grouped_b2_us": round(lg_us2, 2), "grouped_equal_per_table": bool(same)}}),
+              flush=True)
+        return
     if args.counters_workload:
         x = np.linspace(-10.0, 10.0, 16 << 20, dtype=np.float32)
         brain.ctx.expf(x)
@@ -552,6 +572,7 @@ def main():
     ctx = brain.ctx
     copies = [nunchi_amd.Q4Table(ctx, synth.q4_0_random(np.random.default_rng(100 + i), 8192, 2048), 8192, 2048) for i in range(64)]
     cfg0_us = nunchi_amd.q4_bench(ctx, copies, n_in=1, cut_mode=1, reps=640)           # per call, back to back
+    cfg0_graph_us = nunchi_amd.q4_bench_graph(ctx, copies, n_in=1, cut_mode=1, passes=10)  # replayed from a graph
     cfg0_kernel_us = nunchi_amd.q4_bench_kernel(ctx, copies, n_in=1, cut_mode=1, reps=256)   # the kernel itself
     cfg0_bytes = 8192 * 64 * 18 + 2048 * 4 + 8192 * 4
     del copies
@@ -616,6 +637,7 @@ def main():
             # HBM bytes per launch from the FETCH_SIZE / WRITE_SIZE counter runs of `bench.py --counters-workload`,
             # calibrated on a streaming kernel and a read-only GEMV of known sizes
             "traffic": GATE_UP_TRAFFIC_BYTES,
+            "traffic_source": "counter run (not this process): profiles/ffn_gate_up_counters_seoul.md",
             "launch_us": round(gu_step["avg_us"], 3),
             "launches_timed": gu_step["launches"],
             "bytes_per_launch": int(gu_step["bytes_per_launch"]),
@@ -646,6 +668,11 @@ def main():
                                                "outputs_equal_per_table": bool(l_group_same)}},
             "cfg0_gemv_8192x2048": {"avg_us": round(cfg0_us, 3), "GBs": round(cfg0_bytes / cfg0_us / 1e3, 1),
                                     "frac": round(cfg0_bytes / cfg0_us / 1e3 / HBM_PEAK_GBS, 4),
+                                    # the same 640 launches captured in one HIP graph (64 copies in order) and
+                                    # replayed back to back
+                                    "graph_avg_us": round(cfg0_graph_us, 3),
+                                    "graph_GBs": round(cfg0_bytes / cfg0_graph_us / 1e3, 1),
+                                    "graph_frac": round(cfg0_bytes / cfg0_graph_us / 1e3 / HBM_PEAK_GBS, 4),
                                     "kernel_us": round(cfg0_kernel_us, 3),
                                     "kernel_GBs": round(cfg0_bytes / cfg0_kernel_us / 1e3, 1),
                                     "kernel_frac": round(cfg0_bytes / cfg0_kernel_us / 1e3 / HBM_PEAK_GBS, 4),
@@ -668,6 +695,7 @@ def main():
             "int8_tops": round(ops / float(np.percentile(pt, 50)) / 1e12, 2),
             "int8_peak_tops": 5000.0,
             "mfma_util_pct_counter_run": PREFILL_MFMA_UTIL_PCT,
+            "mfma_util_source": "counter run (not this process): profiles/prefill_hearing_window_seoul.md",
             "reps": int(len(pt)),
         }
     if args.hear_reps:
@@ -693,7 +721,22 @@ def main():
         }
     if args.voice_frames:
         vpath = synth.cached("voice", synth.VOICE, 1)
-        (ft, fbr, fvo, fcodes, fids, _), fref, vinfo = gpu_voice_frames(path, vpath, args.voice_frames, 4)
+        (ft, fbr, fvo, fcodes, fids, _), fref, vinfo = gpu_voice_frames(path, vpath, args.voice_frames, VOICE_WARMUP)
+        # algorithmic bytes of a frame: the step2 (every brain table once, the word table for slot A's scores, the
+        # fp32 vectors, and the K and V rows each slot's attention reads at its position), then the generator (its
+        # proj_in once, its layer tables once per pass, the 8 score tables of the frame's codebooks once each)
+        vs = synth.VOICE
+        q8 = lambda rows, cols: (rows + 7) // 8 * 8 * (cols // 32) * 34
+        heads_b = vs.n_cb * q8(vs.n_vocab, vs.n_embd)
+        proj_b = q8(vs.n_cb * vs.n_embd, vs.n_in)
+        layers_b = int(vinfo["table_bytes"]) - heads_b - proj_b
+        gen_b = proj_b + len(SCHEDULE) * layers_b + heads_b
+        kv_row = brain.n_attn * brain.n_head_kv * brain.head_dim * 2
+        nfr = len(ft)
+        kv_b = sum(2 * kv_row * ((A_POS + VOICE_WARMUP + f + 1) + (VOICE_WARMUP + f + 1)) for f in range(nfr)) / nfr
+        brain_b = brain.table_bytes + brain.vector_bytes + kv_b
+        frame_b = brain_b + gen_b
+        p50 = float(np.percentile(ft, 50))
         line["voice_frame"] = {
             "workload": "cfg4: step2 of the cfg2 model (slot A: text step with scores at KV context 4096, from position "
                         f"{A_POS}; slot B: voice brain step fed the feedback row sum), then the Q8_0 generator "
@@ -707,6 +750,9 @@ def main():
             "step2_p50_ms": round(float(np.percentile(fbr, 50)) * 1e3, 3),
             "generator_p50_ms": round(float(np.percentile(fvo, 50)) * 1e3, 3),
             "generator_table_bytes": int(vinfo["table_bytes"]),
+            "bytes_per_frame": {"step2": int(brain_b), "generator": int(gen_b), "total": int(frame_b)},
+            "GBs_at_p50": round(frame_b / p50 / 1e9, 1),
+            "hbm_frac_at_p50": round(frame_b / p50 / 1e9 / HBM_PEAK_GBS, 4),
             "budget_ms": 80.0,
         }
     if args.talk_frames:

@@ -246,6 +246,10 @@ int sh_q4_bench(sh_ctx* ctx, sh_q4* const* tables, int n_tables, int n_in, int c
 /* The kernel's own duration: each launch timed alone by events recorded around the kernel (no dispatch gap in
  * front of it), averaged over `reps`; after sh_q4_bench on the same tables (which sizes the device input/output). */
 int sh_q4_bench_kernel(sh_ctx* ctx, sh_q4* const* tables, int n_tables, int n_in, int cut_mode, int reps, double* avg_kernel_us);
+/* The same launches back to back replayed from a captured HIP graph: one pass over the tables (one launch each, in
+ * order) captured once and replayed `passes` times; avg_launch_us = the replays' event time over passes * n_tables.
+ * After sh_q4_bench on the same tables. */
+int sh_q4_bench_graph(sh_ctx* ctx, sh_q4* const* tables, int n_tables, int n_in, int cut_mode, int passes, double* avg_launch_us);
 
 /* Calibration: an empty kernel of `grid` x 256 threads launched `reps` times back to back on one stream (the
  * dispatch cost any kernel pays), and a pure read of `bytes` (copies distinct buffers in rotation, so with

@@ -22,7 +22,7 @@ EXPORTS = [
     "sh_last_error", "sh_create", "sh_destroy", "sh_load", "sh_info", "sh_check_model", "sh_state_new", "sh_state_free", "sh_state_reset",
     "sh_state_pos", "sh_state_set_pos", "sh_step", "sh_step2", "sh_step_batch", "sh_generate", "sh_bench_tables",
     "sh_bench_kernel", "sh_bench_step_kernel",
-    "sh_q4_create", "sh_q4_free", "sh_q4_rows", "sh_q4_gemv", "sh_q4_gemm", "sh_q4_gemm_noalloc", "sh_q4_gemv_dev", "sh_q4_bench", "sh_q4_bench_kernel",
+    "sh_q4_create", "sh_q4_free", "sh_q4_rows", "sh_q4_gemv", "sh_q4_gemm", "sh_q4_gemm_noalloc", "sh_q4_gemv_dev", "sh_q4_bench", "sh_q4_bench_kernel", "sh_q4_bench_graph",
     "sh_q4_gemv_group", "sh_q4_gemv_group_dev", "sh_q4_group_bench", "sh_expf", "sh_sync",
     "sh_voice_load", "sh_voice_free", "sh_voice_info", "sh_voice_begin_frame", "sh_voice_base", "sh_voice_pass",
     "sh_voice_feedback", "sh_voice_sample",
@@ -111,6 +111,7 @@ def load_library(path: str = LIB_PATH):
         "sh_q4_gemm_noalloc": (i, [vp, vp, vp, i, vp]),
         "sh_q4_bench": (i, [vp, vp, i, i, i, i, P(d)]),
         "sh_q4_bench_kernel": (i, [vp, vp, i, i, i, i, P(d)]),
+        "sh_q4_bench_graph": (i, [vp, vp, i, i, i, i, P(d)]),
         "sh_q4_gemv_group": (i, [vp, i, vp, vp, vp, i, i]),
         "sh_q4_gemv_group_dev": (i, [vp, i, vp, vp, vp, i, i]),
         "sh_q4_group_bench": (i, [vp, i, i, vp, i, i, i, P(d)]),
@@ -503,6 +504,15 @@ def q4_bench(ctx: Context, tables, n_in: int = 1, cut_mode: int = 0, reps: int =
     arr = (C.c_void_p * len(tables))(*[t.h.value for t in tables])
     us = C.c_double()
     _check(_lib.sh_q4_bench(ctx.h, arr, len(tables), int(n_in), int(cut_mode), int(reps), C.byref(us)))
+    return us.value
+
+
+def q4_bench_graph(ctx: Context, tables, n_in: int = 1, cut_mode: int = 0, passes: int = 10) -> float:
+    """Mean launch time (us) of the GEMV over `tables` when one pass over them (a launch per table) is captured into a
+    HIP graph and replayed `passes` times back to back; after q4_bench on the same tables."""
+    arr = (C.c_void_p * len(tables))(*[t.h.value for t in tables])
+    us = C.c_double()
+    _check(_lib.sh_q4_bench_graph(ctx.h, arr, len(tables), int(n_in), int(cut_mode), int(passes), C.byref(us)))
     return us.value
 
 

@@ -1439,6 +1439,40 @@ int sh_q4_bench(sh_ctx* c, sh_q4* const* tables, int n_tables, int n_in, int cut
     return SH_OK;
 }
 
+int sh_q4_bench_graph(sh_ctx* c, sh_q4* const* tables, int n_tables, int n_in, int cut_mode, int passes, double* avg_us) {
+    if (!c || !tables || n_tables < 1 || passes < 1) return fail(SH_E_ARG, "sh_q4_bench_graph: bad argument");
+    HIPCHK(hipSetDevice(c->device));
+    for (int i = 0; i < n_tables; i++) {
+        const size_t need = (size_t)n_in * (tables[i]->t.cols > tables[i]->t.rows ? tables[i]->t.cols : tables[i]->t.rows);
+        if (c->bench_cap < need) return fail(SH_E_STATE, "sh_q4_bench_graph: run sh_q4_bench on these tables first");
+    }
+    // one pass over the tables, captured once: every launch a graph node behind the one before it
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    HIPCHK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    int rc = SH_OK;
+    for (int i = 0; i < n_tables && rc == SH_OK; i++) rc = q4_gemv_launch(c, tables[i], c->bench_x, n_in, c->bench_y, cut_mode, nullptr, nullptr);
+    hipError_t e = hipStreamEndCapture(c->stream, &graph);
+    if (rc != SH_OK || e != hipSuccess) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return rc != SH_OK ? rc : fail(SH_E_HIP, std::string("sh_q4_bench_graph: capture: ") + hipGetErrorString(e));
+    }
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) return fail(SH_E_HIP, std::string("sh_q4_bench_graph: instantiate: ") + hipGetErrorString(e));
+    float ms = 0;
+    e = hipGraphLaunch(exec, c->stream);   // warm-up pass
+    if (e == hipSuccess) e = hipEventRecord(c->ev0, c->stream);
+    for (int p = 0; p < passes && e == hipSuccess; p++) e = hipGraphLaunch(exec, c->stream);
+    if (e == hipSuccess) e = hipEventRecord(c->ev1, c->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(c->ev1);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, c->ev0, c->ev1);
+    (void)hipGraphExecDestroy(exec);
+    if (e != hipSuccess) return fail(SH_E_HIP, std::string("sh_q4_bench_graph: ") + hipGetErrorString(e));
+    if (avg_us) *avg_us = ms * 1e3 / ((double)passes * n_tables);
+    return SH_OK;
+}
+
 int sh_q4_bench_kernel(sh_ctx* c, sh_q4* const* tables, int n_tables, int n_in, int cut_mode, int reps, double* avg_us) {
     if (!c || !tables || n_tables < 1 || reps < 1) return fail(SH_E_ARG, "sh_q4_bench_kernel: bad argument");
     HIPCHK(hipSetDevice(c->device));
