@@ -20,6 +20,8 @@ hipError_t launch_gemv_group(int M, bool half, const gemv_group_args& g, hipStre
 // workgroups of a word-score launch (the argmax partials k_final reduces), at most max_grid
 int gemv_logits_grid(int M, int pro, const gemv_args& a, int max_grid);
 hipError_t launch_attn(int M, const attn_args& a, hipStream_t s);
+// whether the FFN gate|up launch can publish its SwiGLU output cut to int8 for the down launch (PRO_PRECUT)
+bool swiglu_cut_takes(int M, const gemv_args& gate_up, const gemv_args& down);
 // word scores over a Q6_K table (a.W6): prologue from x_in/y_in/w_post/w_pre (or src, already normed), logits to
 // a.out when set, per-workgroup first maxima to part_v / part_i [M][grid]
 constexpr int SH_Q6K_GRID = 256;   // k_scores_q6k workgroups: one per compute unit, each looping over tiles
@@ -96,6 +98,8 @@ struct sh_ctx {
     arena work;
     float *xbuf[2] = {nullptr, nullptr}, *y = nullptr, *u = nullptr, *qkv = nullptr, *att = nullptr, *act = nullptr, *fo = nullptr;
     float *hidden = nullptr, *logits = nullptr, *embd_stage = nullptr, *part_v = nullptr;
+    int8_t* act_q = nullptr;          // the FFN activation cut to int8 per 32 channels [2][n_ff], with d and s [2][n_ff / 32]
+    float *act_d = nullptr, *act_s = nullptr;
     int* part_i = nullptr;
     int32_t* gen_out = nullptr;       // device-side greedy ids [2][gen_cap]
     int gen_cap = 0;
@@ -118,6 +122,8 @@ struct sh_ctx {
     float *pf_d = nullptr, *pf_s = nullptr, *pf_emb = nullptr;
     int32_t* pf_tok = nullptr;
     bool use_prefill = true;          // SEOUL_HIP_PREFILL=0: step_batch runs n single steps instead
+    // the FFN gate|up launch cuts its output for the down launch (SEOUL_HIP_PRECUT=0: down cuts the floats itself)
+    bool use_precut = true;
     // set while sh_bench_step_kernel runs steps without the graph: one kind of the step's GEMV launches (0 FFN
     // gate|up, 1 FFN down, 2 Q4_0 word scores) records this event pair list around each kernel
     std::vector<hipEvent_t>* probe_ev = nullptr;

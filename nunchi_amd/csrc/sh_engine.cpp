@@ -230,9 +230,6 @@ int enqueue_step(sh_ctx* c, int M, bool want_logits) {
         f.units = units_of(L.gate_up, 2);
         f.out = c->act;
         f.out_ld = I.n_ff;
-        hipEvent_t p0, p1;
-        probe_events(c, 0, &p0, &p1);
-        HIPCHK(launch_gemv(M, PRO_RESID_NORM, EPI_SWIGLU, grid_of(f.units), f, c->stream, p0, p1));
         gemv_args d = base_args();
         d.W = L.down;
         d.units = units_of(L.down, 1);
@@ -240,8 +237,22 @@ int enqueue_step(sh_ctx* c, int M, bool want_logits) {
         d.src_ld = I.n_ff;
         d.out = c->fo;
         d.out_ld = E;
+        int dpro = PRO_CUT;
+        if (c->use_precut && swiglu_cut_takes(M, f, d)) {   // gate|up cuts the activation once for every down workgroup
+            f.upw = 4;
+            f.outq = c->act_q;
+            f.outd = c->act_d;
+            f.outs = c->act_s;
+            d.src_q = c->act_q;
+            d.src_d = c->act_d;
+            d.src_s = c->act_s;
+            dpro = PRO_PRECUT;
+        }
+        hipEvent_t p0, p1;
+        probe_events(c, 0, &p0, &p1);
+        HIPCHK(launch_gemv(M, PRO_RESID_NORM, EPI_SWIGLU, grid_of(f.units), f, c->stream, p0, p1));
         probe_events(c, 1, &p0, &p1);
-        HIPCHK(launch_gemv(M, PRO_CUT, EPI_STORE, grid_of(d.units), d, c->stream, p0, p1));
+        HIPCHK(launch_gemv(M, dpro, EPI_STORE, grid_of(d.units), d, c->stream, p0, p1));
         prev = &L;
     }
     final_args z{};
@@ -465,6 +476,8 @@ int sh_create(int device, sh_ctx** out) {
     c->use_graphs = !(g && g[0] == '0');
     const char* pf = getenv("SEOUL_HIP_PREFILL");
     c->use_prefill = !(pf && strcmp(pf, "0") == 0);
+    const char* pc = getenv("SEOUL_HIP_PRECUT");
+    c->use_precut = !(pc && strcmp(pc, "0") == 0);
     *out = c.release();
     return SH_OK;
 }
@@ -709,8 +722,8 @@ int sh_load(sh_ctx* c, const char* path, int n_ctx) {
     const int Hq = I.n_head * I.head_dim;
     const size_t fl = sizeof(float);
     const size_t work_need = fl * (2 * 2 * E + 2 * E + 2 * E + 2 * (size_t)c->nqkv + 2 * (size_t)Hq + 2 * (size_t)I.n_ff + 2 * E + 2 * E +
-                                   2 * (size_t)I.n_vocab + 2 * E + 2 * (size_t)c->vocab_grid) +
-                             sizeof(int) * 2 * (size_t)c->vocab_grid + 32 * 256;
+                                   2 * (size_t)I.n_vocab + 2 * E + 2 * (size_t)c->vocab_grid + 2 * 2 * (size_t)(I.n_ff / 32 + 1)) +
+                             sizeof(int) * 2 * (size_t)c->vocab_grid + 2 * (size_t)I.n_ff + 32 * 256;
     HIPCHK(hipMalloc((void**)&c->work.base, work_need));
     c->work.size = work_need;
     HIPCHK(hipMemset(c->work.base, 0, work_need));
@@ -728,6 +741,9 @@ int sh_load(sh_ctx* c, const char* path, int n_ctx) {
     c->embd_stage = fa(2 * E);
     c->part_v = fa(2 * (size_t)c->vocab_grid);
     c->part_i = static_cast<int*>(c->work.take(sizeof(int) * 2 * (size_t)c->vocab_grid));
+    c->act_q = static_cast<int8_t*>(c->work.take(2 * (size_t)I.n_ff));
+    c->act_d = fa(2 * (size_t)(I.n_ff / 32 + 1));
+    c->act_s = fa(2 * (size_t)(I.n_ff / 32 + 1));
     if (!c->part_i) return fail(SH_E_NOMEM, "sh_load: work arena overflow");
     HIPCHK(hipDeviceSynchronize());
     c->loaded = true;

@@ -19,7 +19,7 @@ struct step_params {
     int32_t* out_tok[2];    // ids chosen in a device-side loop, or null
 };
 
-enum { PRO_CUT = 0, PRO_CUT_HALF_AWAY = 1, PRO_EMBED_NORM = 2, PRO_RESID_NORM = 3 };
+enum { PRO_CUT = 0, PRO_CUT_HALF_AWAY = 1, PRO_EMBED_NORM = 2, PRO_RESID_NORM = 3, PRO_PRECUT = 4 };
 enum { EPI_STORE = 0, EPI_SWIGLU = 1, EPI_CONV = 2, EPI_LOGITS = 3 };
 
 // one Q4_0 table in the device layout: codes [rows][nb][16 B] (the file's nibble bytes, scales split off),
@@ -67,6 +67,16 @@ struct gemv_args {
     step_params* P;
     int upw;                   // k_gemv_norm: units per workgroup (chunk), 0 = pick
     q6dev W6;                  // k_scores_q6k: the Q6_K word table
+    // EPI_SWIGLU with outq set: the SwiGLU output also cut to int8 per 32 channels (imi_cut32) by the workgroup that
+    // forms them (4 units per chunk: a chunk's 32 channels are one cut block): codes [M][out_ld], d and s = d * sum
+    // of the codes [M][out_ld / 32]
+    int8_t* outq;
+    float* outd;
+    float* outs;
+    // PRO_PRECUT: the input arrives cut (codes [M][src_ld], d and s [M][src_ld / 32]), as such an epilogue wrote it
+    const int8_t* src_q;
+    const float* src_d;
+    const float* src_s;
 };
 
 // several kernel-level Q4_0 GEMVs in one launch: table t's 8-row groups are workgroups

@@ -267,9 +267,11 @@ __global__ __launch_bounds__(64) void k_gemv(gemv_args a) {
 // HM: the table is Q4_1 (imi/core/tables.cpp:127-143 with HAS_M): the correction chain takes the block minimum m in
 // place of d and the row ends as acc + cor
 // g: the table's 8-row group this workgroup computes
-template <int M, bool HALF, int NB, bool HM>
+// PRE: the input arrives cut (PRO_PRECUT: codes, d and s as the FFN gate|up epilogue wrote them); the prologue only
+// stages them
+template <int M, bool HALF, int NB, bool HM, bool PRE = false>
 __device__ __forceinline__ void gemv_cut_body(const gemv_args& a, const int g) {
-    constexpr int TPB = 256 / NB, VPT = 32 / TPB, RPT = NB / 32, ST = NB + 4;
+    constexpr int TPB = 256 / NB, VPT = 32 / TPB, RPT = NB / 32, ST = NB + 4, IPT = 8 / TPB;
     extern __shared__ __align__(16) float lds[];
     int* l_xq = (int*)lds;                      // [M][NB][8] int8 codes of the cut input, 4 per word
     float* l_dx = lds + M * NB * 8;             // [M][NB]
@@ -280,12 +282,32 @@ __device__ __forceinline__ void gemv_cut_body(const gemv_args& a, const int g) {
     const int t = threadIdx.x, lane = t & 63;
     // input share first: block jc, values part * VPT .. + VPT - 1
     const int jc = t / TPB, part = t - jc * TPB;
-    f32x4 xin[M][VPT / 4];
+    f32x4 xin[PRE ? 1 : M][VPT / 4];
+    u32x4 qin[PRE ? M : 1][(IPT + 3) / 4];   // PRE: this thread's IPT dwords (4 codes each) of block jc
+    float din[M], sin_[M];
+    if (PRE) {
+        static_assert(IPT == 8 || IPT == 4 || IPT == 2, "cut dwords per thread");
 #pragma unroll
-    for (int m = 0; m < M; m++) {
-        const f32x4* src = (const f32x4*)(a.src + (size_t)m * a.src_ld + 32 * jc + VPT * part);
+        for (int m = 0; m < M; m++) {
+            const unsigned* qs = (const unsigned*)(a.src_q + (size_t)m * a.src_ld + 32 * jc) + IPT * part;
+            if (IPT >= 4) {
 #pragma unroll
-        for (int k = 0; k < VPT / 4; k++) xin[m][k] = src[k];
+                for (int k = 0; k < IPT / 4; k++) qin[m][k] = ((const u32x4*)qs)[k];
+            } else {
+                typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+                const u32x2 v2 = *(const u32x2*)qs;
+                qin[m][0] = u32x4{v2.x, v2.y, 0u, 0u};
+            }
+            din[m] = a.src_d[(size_t)m * NB + jc];
+            sin_[m] = a.src_s[(size_t)m * NB + jc];
+        }
+    } else {
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const f32x4* src = (const f32x4*)(a.src + (size_t)m * a.src_ld + 32 * jc + VPT * part);
+#pragma unroll
+            for (int k = 0; k < VPT / 4; k++) xin[PRE ? 0 : m][k] = src[k];
+        }
     }
     // then the weights: rows sub * RPT .. + RPT - 1 of block jw
     const int jw = t % NB, sub = t / NB;
@@ -296,13 +318,26 @@ __device__ __forceinline__ void gemv_cut_body(const gemv_args& a, const int g) {
     const u32x4 s8 = __builtin_nontemporal_load((const u32x4*)a.W.scales + (size_t)g * NB + jw);
     u32x4 m8 = s8;
     if (HM) m8 = __builtin_nontemporal_load((const u32x4*)a.W.mins + (size_t)g * NB + jw);
-    // the cut of block jc by its TPB threads
+    // the cut of block jc by its TPB threads (PRE: staged as it arrived)
 #pragma unroll
     for (int m = 0; m < M; m++) {
+        if (PRE) {
+#pragma unroll
+            for (int w = 0; w < IPT; w++) {
+                const u32x4 q4 = qin[m][w >> 2];
+                l_xq[(m * NB + jc) * 8 + IPT * part + w] = (int)((w & 3) == 0 ? q4.x : (w & 3) == 1 ? q4.y : (w & 3) == 2 ? q4.z : q4.w);
+            }
+            if (part == 0) {
+                l_dx[m * NB + jc] = din[m];
+                l_s[m * ST + jc] = sin_[m];
+            }
+            continue;
+        }
         float v[VPT];
 #pragma unroll
         for (int k = 0; k < VPT / 4; k++) {
-            v[4 * k] = xin[m][k].x; v[4 * k + 1] = xin[m][k].y; v[4 * k + 2] = xin[m][k].z; v[4 * k + 3] = xin[m][k].w;
+            const f32x4 xk = xin[PRE ? 0 : m][k];
+            v[4 * k] = xk.x; v[4 * k + 1] = xk.y; v[4 * k + 2] = xk.z; v[4 * k + 3] = xk.w;
         }
         float amax = 0.0f;
 #pragma unroll
@@ -387,9 +422,9 @@ __device__ __forceinline__ void gemv_cut_body(const gemv_args& a, const int g) {
     }
 }
 
-template <int M, bool HALF, int NB, bool HM = false>
+template <int M, bool HALF, int NB, bool HM = false, bool PRE = false>
 __global__ __launch_bounds__(256) void k_gemv_cut(gemv_args a) {
-    gemv_cut_body<M, HALF, NB, HM>(a, blockIdx.x);
+    gemv_cut_body<M, HALF, NB, HM, PRE>(a, blockIdx.x);
 }
 
 // several tables in one launch: workgroup b computes group b - start[t] of table t (start[t] <= b < start[t + 1]),
@@ -509,6 +544,7 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
     float* l_sc = l_out + C;                       // [16] norm scales, reduction scratch
     int* l_si = (int*)(l_sc + 16);                 // [16]
     uint64_t* l_exp = (uint64_t*)(l_si + 16);      // [32] the exponential's table (SwiGLU)
+    float* l_lg = (float*)(l_exp + 32);            // word scores: [chunks of this workgroup][C], written after the loop
 
     const int gtot = a.W.rows / 8, nchunk = (a.units + upw - 1) / upw;
     // this thread's share of a chunk's weights: rows sub * rpt .. + rpt - 1 of group gi, block jw
@@ -516,20 +552,50 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
     const bool wt = t < np * (8 / rpt);
     const int sub = t / np, pr = t - sub * np, gi = pr / nb, jw = pr - gi * nb;
     u32x4 w[HM ? 10 : 9];
-    // all 9 (Q4_1: 10) loads are issued on every path (rows past this thread's share and absent groups re-read a row
-    // it owns, which the caches serve), so the compiler counts them exactly and the prologue waits only for its own
-    // inputs
+    // all 9 (Q4_1: 10) loads are issued on every path (the slots past this thread's share read the group's other rows,
+    // never an address another slot reads: the compiler would fold two loads of one address into one load and a
+    // register copy, and wait for the load at the copy), so the compiler counts them exactly and the prologue waits
+    // only for its own inputs
     auto load_rows = [&](int k, int r0, int r1) {
         const int g = min(k * G + (wt ? gi : 0), gtot - 1), s0 = wt ? sub * rpt : 0;
         const u32x4* cp = (const u32x4*)a.W.codes + (size_t)(8 * g + s0) * nb + jw;
 #pragma unroll
-        for (int r = r0; r < r1; r++) w[r] = __builtin_nontemporal_load(cp + (size_t)(r < rpt ? r : 0) * nb);
+        for (int r = r0; r < r1; r++) w[r] = __builtin_nontemporal_load(cp + (ptrdiff_t)(((s0 + r) & 7) - s0) * nb);
         if (r1 == 8 && r0 < 8) {
             w[8] = __builtin_nontemporal_load((const u32x4*)a.W.scales + (size_t)g * nb + jw);
             if (HM) w[HM ? 9 : 8] = __builtin_nontemporal_load((const u32x4*)a.W.mins + (size_t)g * nb + jw);
         }
     };
     auto load_chunk = [&](int k) { load_rows(k, 0, 8); };
+    // the word scores keep two chunks in flight: chunk k + grid lands in w2 while chunk k is worked; a chunk past the
+    // table is a stand-in load of the table's first word by every lane (one cache line), so every path issues the
+    // same loads and the compiler's wait counts stay exact
+    u32x4 w2[HM ? 10 : 9];
+    auto load_to = [&](u32x4 (&dst)[HM ? 10 : 9], int k) {
+        // (rm = 1 for a chunk of the table, 0 past it; the stand-in reads word r of the table's first line: distinct
+        // addresses, so no two loads fold into one)
+        const int rm = k < nchunk ? 1 : 0;
+        const int g = min(min(k, nchunk - 1) * G + (wt ? gi : 0), gtot - 1), s0 = wt ? sub * rpt : 0;
+        const u32x4* cp = (const u32x4*)a.W.codes;
+        const ptrdiff_t base = rm * ((ptrdiff_t)(8 * g + s0) * nb + jw);
+#pragma unroll
+        for (int r = 0; r < 8; r++)
+            dst[r] = __builtin_nontemporal_load(cp + base + rm * ((ptrdiff_t)(((s0 + r) & 7) - s0) * nb) + (1 - rm) * r);
+        const ptrdiff_t so = rm * ((ptrdiff_t)g * nb + jw);
+        dst[8] = __builtin_nontemporal_load((const u32x4*)a.W.scales + so);
+        if (HM) dst[HM ? 9 : 8] = __builtin_nontemporal_load((const u32x4*)a.W.mins + so);
+    };
+    // the rest of the first chunk: only this thread's own rows (rpt of them), then the scales. Loads past rpt would be
+    // duplicates that each cost the address unit as much as a real 1 KB wave load (a 2-row share issued 9 loads)
+    auto load_own_rows = [&](int k, int r0) {
+        const int g = min(k * G + (wt ? gi : 0), gtot - 1), s0 = wt ? sub * rpt : 0;
+        const u32x4* cp = (const u32x4*)a.W.codes + (size_t)(8 * g + s0) * nb + jw;
+#pragma unroll
+        for (int r = r0; r < 8; r++)
+            if (r < rpt) w[r] = __builtin_nontemporal_load(cp + (size_t)r * nb);
+        w[8] = __builtin_nontemporal_load((const u32x4*)a.W.scales + (size_t)g * nb + jw);
+        if (HM) w[HM ? 9 : 8] = __builtin_nontemporal_load((const u32x4*)a.W.mins + (size_t)g * nb + jw);
+    };
     // ---- prologue: its inputs are requested first, most of the weights once the inputs have arrived ----
     // (every load on every path: threads past the E / 4 quads re-read the last one, and a workgroup past the last
     // chunk loads that chunk, so the compiler's wait counts stay exact)
@@ -549,17 +615,11 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
     const uint64_t etab = kExp2Tab[t & 31];   // (SwiGLU) copied to LDS once the dots have waited for the weights
     int k = blockIdx.x;
     if (EMB) load_chunk(k < nchunk ? k : nchunk - 1);
-    // the first kEarlyRows code rows of the first chunk go out right behind the inputs, the rest (and the scales) once
-    // y is in LDS: the memory system streams weights while the inputs arrive without the whole chunk queued ahead of
-    // them. Half of a thread's 8 rows for the FFN gate|up and word-score tables (decode B=1 2188 -> 2211 tokens/s; 2,
-    // 3, 5, 6 or all 8 rows with the scales measured no better or slower); none for the conv in_proj and q|k|v|gate
-    // tables, whose threads hold 4 and 2 rows (early rows there measured slower: B=1 2210 -> 2226 without them)
-    constexpr int kEarlyRows = (EPI == EPI_SWIGLU || EPI == EPI_LOGITS) ? 4 : 0;
-    if (!EMB) load_rows(k < nchunk ? k : nchunk - 1, 0, kEarlyRows);
-    // the conv epilogue's taps and memory of this thread's channel (one chunk per workgroup), after the weights
+    // the conv epilogue's taps and memory of this thread's channel (one chunk per workgroup), right behind the inputs,
+    // by the waves that hold conv channels only (the others would issue 17 clamped loads each for nothing)
     constexpr int CMAX = 8;
     float cw[CMAX + 1], cst[CMAX];
-    if (EPI == EPI_CONV) {
+    if (EPI == EPI_CONV && __builtin_amdgcn_readfirstlane(t >> 6) < (C + 63) / 64) {
         const int m = t / R, r = t - m * R, ui = r / 24, i = r - 24 * ui, dc = a.d_conv;
         const bool mine = t < C && i < 8 && k < nchunk;
         const int e = mine ? 8 * (k * upw + ui) + i : 0;
@@ -569,24 +629,38 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
         SH_GLOBAL float* const c0 = global_ptr(a.P->conv[0]);
         SH_GLOBAL float* const c1 = M > 1 ? global_ptr(a.P->conv[M - 1]) : c0;
         const SH_GLOBAL float* stt = (mine && m ? c1 : c0) + (size_t)a.conv_layer * dc * E;
+        // (taps past d_conv hold a clamped duplicate the epilogue never reads: no select here, which would wait for
+        // every load right away)
 #pragma unroll
-        for (int q = 0; q <= CMAX; q++) {
-            const float v = a.conv_w[(size_t)min(q, dc) * E + e];
-            cw[q] = q <= dc ? v : 0.0f;
-        }
+        for (int q = 0; q <= CMAX; q++) cw[q] = a.conv_w[(size_t)min(q, dc) * E + e];
 #pragma unroll
-        for (int q = 0; q < CMAX; q++) {
-            const float v = stt[(size_t)min(q, dc - 1) * E + e];
-            cst[q] = q < dc ? v : 0.0f;
-        }
+        for (int q = 0; q < CMAX; q++) cst[q] = stt[(size_t)min(q, dc - 1) * E + e];
     }
+    // then the first kEarlyRows code rows of the first chunk, the rest (and the scales) once y is in LDS: the memory
+    // system streams weights while the inputs arrive without the whole chunk queued ahead of them. Half of a thread's
+    // 8 rows for the FFN gate|up and word-score tables (decode B=1 2188 -> 2211 tokens/s; 2, 3, 5, 6 or all 8 rows with
+    // the scales measured no better or slower); all of a thread's rows for the q|k|v|gate (2 at 2048 columns) and
+    // conv in_proj (4) tables, which no longer issue duplicate row loads behind them
+    constexpr int kEarlyRows = (EPI == EPI_SWIGLU || EPI == EPI_LOGITS || EPI == EPI_CONV) ? 4 : 2;
+    if (!EMB) load_rows(k < nchunk ? k : nchunk - 1, 0, kEarlyRows);
 
     if (!EMB) {   // x += norm(y) * w_post (imi_norm_mul_add)
         if (t < nq)
 #pragma unroll
             for (int m = 0; m < M; m++) put_xt(l_v + m * 32 * XLD, t, yv[m]);
         __syncthreads();
-        load_rows(k < nchunk ? k : nchunk - 1, kEarlyRows, 8);
+        // x, the norm weights (and the exponential's table entry) were requested with y, before any weight row:
+        // taken here, so the waits for them below do not count the weight loads, whose number is this thread's row
+        // count (the dots then wait for every load, as they need all of them)
+#pragma unroll
+        for (int m = 0; m < M; m++) asm volatile("" ::"v"(xv[m].x));
+        asm volatile("" ::"v"(wp.x), "v"(wq.x), "v"((unsigned)etab));
+        if (EPI == EPI_LOGITS) {
+            load_rows(k < nchunk ? k : nchunk - 1, kEarlyRows, 8);
+            load_to(w2, k + (int)gridDim.x);
+        } else {
+            load_own_rows(k < nchunk ? k : nchunk - 1, kEarlyRows);
+        }
         if ((t >> 6) < M) {
             const float sc = rms_xt(l_v + (t >> 6) * 32 * XLD, E, a.eps);
             if ((t & 63) == 0) l_sc[t >> 6] = sc;
@@ -602,11 +676,15 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
         }
         __syncthreads();
     }
+    // (the word scores store x and the hidden state after their chunk loop: a store pending between the weight loads
+    // and the dots would make the compiler wait for every load there, the next chunk's included)
+    constexpr bool late_stores = EPI == EPI_LOGITS;
+    f32x4 hsave[late_stores ? M : 1];
     if (t < nq)
 #pragma unroll
         for (int m = 0; m < M; m++) {
             put_xt(l_v + m * 32 * XLD, t, xv[m]);
-            if (blockIdx.x == 0 && a.x_out) ((f32x4*)(a.x_out + (size_t)m * E))[t] = xv[m];
+            if (!late_stores && blockIdx.x == 0 && a.x_out) ((f32x4*)(a.x_out + (size_t)m * E))[t] = xv[m];
         }
     __syncthreads();
     if ((t >> 6) < M) {   // h = norm(x) * w_pre (imi_norm_mul)
@@ -620,7 +698,8 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
         for (int m = 0; m < M; m++) {
             const float sc = l_sc[4 + m];
             float h[4] = {xv[m].x * sc * wq.x, xv[m].y * sc * wq.y, xv[m].z * sc * wq.z, xv[m].w * sc * wq.w};
-            if (a.hidden_out && blockIdx.x == 0) ((f32x4*)(a.hidden_out + (size_t)m * E))[t] = f32x4{h[0], h[1], h[2], h[3]};
+            if (late_stores) hsave[late_stores ? m : 0] = f32x4{h[0], h[1], h[2], h[3]};
+            else if (a.hidden_out && blockIdx.x == 0) ((f32x4*)(a.hidden_out + (size_t)m * E))[t] = f32x4{h[0], h[1], h[2], h[3]};
             float amax = fmaxf(fmaxf(fabsf(h[0]), fabsf(h[1])), fmaxf(fabsf(h[2]), fabsf(h[3])));
             amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(amax), 0xB1, 0xF, 0xF, true)));
             amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(amax), 0x4E, 0xF, 0xF, true)));
@@ -651,7 +730,7 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
     int best_i[M];
 #pragma unroll
     for (int m = 0; m < M; m++) { best_v[m] = -INFINITY; best_i[m] = 0x7fffffff; }
-    for (; k < nchunk; k += gridDim.x) {
+    auto chunk = [&](u32x4 (&w)[HM ? 10 : 9], const int k, const int ci) {
         const int u0 = k * upw, g0 = k * G, gv = min(G, gtot - g0);   // groups of this chunk that exist
         // ---- dots: exact integer sums of this thread's rows, chain operands to LDS ----
         if (wt && gi < gv) {
@@ -683,7 +762,7 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
         }
         if (EPI == EPI_SWIGLU && t < 32) l_exp[t] = etab;
         __syncthreads();
-        if (k + (int)gridDim.x < nchunk) load_chunk(k + gridDim.x);   // in flight during the chains
+        if (EPI == EPI_LOGITS) load_to(w, k + 2 * (int)gridDim.x);   // in flight during this and the next chunk
         // ---- chains ----
         const bool acc_lane = t < C, cor_lane = t >= 256 && t - 256 < C;
         float chain = 0.0f;
@@ -718,6 +797,7 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
         if (acc_lane) l_out[c] = HM ? chain + l_cor[c] : fmaf(-8.0f, l_cor[c], chain);
         __syncthreads();
         // ---- epilogue: thread c < C holds row r of the chunk for input m ----
+        float act = 0.0f;   // EPI_SWIGLU: this thread's channel output (threads on up rows: 0)
         if (t < C) {
             const int m = t / R, r = t - m * R;
             const float v = l_out[t];
@@ -726,7 +806,10 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
                     a.out[(size_t)m * a.out_ld + 8 * g0 + r] = v;
                 } else if (EPI == EPI_SWIGLU) {   // unit = (gate group, up group) of 8 channels
                     const int ui = r >> 4, i = r & 15;
-                    if (i < 8) a.out[(size_t)m * a.out_ld + 8 * (u0 + ui) + i] = silu_t(v, (const uint64_t*)l_exp) * l_out[t + 8];
+                    if (i < 8) {
+                        act = silu_t(v, (const uint64_t*)l_exp) * l_out[t + 8];
+                        a.out[(size_t)m * a.out_ld + 8 * (u0 + ui) + i] = act;
+                    }
                 } else if (EPI == EPI_CONV) {     // unit = (b, c, x) groups of 8 channels
                     const int ui = r / 24, i = r - 24 * ui;
                     if (i < 8) {
@@ -751,15 +834,76 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
                     }
                 } else {   // EPI_LOGITS
                     const int row = 8 * g0 + r;
-                    if (a.out) a.out[(size_t)m * a.out_ld + row] = v;
+                    if (a.out) l_lg[ci * C + t] = v;   // (to the output after the chunk loop)
 #pragma unroll
                     for (int mm = 0; mm < M; mm++)
                         if (mm == m && (v > best_v[mm] || (v == best_v[mm] && row < best_i[mm]))) { best_v[mm] = v; best_i[mm] = row; }
                 }
             }
         }
+        // the next table's input cut here (imi_cut32, imi/core/vec.h:47-75): with 4 units per chunk, wave m holds
+        // conversation m's 32 channels of this chunk (one cut block); amax and the code sum are order-free reductions,
+        // d = amax / 127, id = d ? 1 / d : 0, q = rint(x * id), s = d * sum, as the cut in the next kernel's prologue
+        if (EPI == EPI_SWIGLU && a.outq && t < C) {
+            // the block's channels sit in lanes 16 j + i (i < 8) of the wave: 8-lane reductions by DPP, then the four
+            // groups' lanes 0, 16, 32, 48 read as scalars
+            float am = fabsf(act);
+            am = fmaxf(am, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(am), 0xB1, 0xF, 0xF, true)));
+            am = fmaxf(am, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(am), 0x4E, 0xF, 0xF, true)));
+            am = fmaxf(am, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(am), 0x141, 0xF, 0xF, true)));
+            const int ai = __float_as_int(am);
+            const float amax = fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(ai, 0)), __int_as_float(__builtin_amdgcn_readlane(ai, 16))),
+                                     fmaxf(__int_as_float(__builtin_amdgcn_readlane(ai, 32)), __int_as_float(__builtin_amdgcn_readlane(ai, 48))));
+            const float d = amax / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            const int q = (int)rintf(act * id);
+            int sq = q;
+            sq += __builtin_amdgcn_update_dpp(0, sq, 0xB1, 0xF, 0xF, true);
+            sq += __builtin_amdgcn_update_dpp(0, sq, 0x4E, 0xF, 0xF, true);
+            sq += __builtin_amdgcn_update_dpp(0, sq, 0x141, 0xF, 0xF, true);
+            const int sum = (__builtin_amdgcn_readlane(sq, 0) + __builtin_amdgcn_readlane(sq, 16)) +
+                            (__builtin_amdgcn_readlane(sq, 32) + __builtin_amdgcn_readlane(sq, 48));
+            const int m = t / R, r = t - m * R, ui = r >> 4, i = r & 15;
+            const int nblk = a.out_ld / 32;
+            if (i < 8) a.outq[(size_t)m * a.out_ld + 8 * (u0 + ui) + i] = (int8_t)q;
+            if ((t & 63) == 0) {
+                a.outd[(size_t)m * nblk + u0 / 4] = d;
+                a.outs[(size_t)m * nblk + u0 / 4] = d * (float)sum;
+            }
+        }
         __syncthreads();
+    };
+    if (EPI == EPI_LOGITS) {   // chunks k, k + grid, ... alternating between the two register sets
+        int ci = 0;
+        if (k < nchunk) {   // (the first chunk ahead of the loop, so the loop's two halves start alike)
+            chunk(w, k, ci++);
+            k += gridDim.x;
+        }
+        for (;;) {
+            if (k >= nchunk) break;
+            chunk(w2, k, ci++);
+            k += gridDim.x;
+            if (k >= nchunk) break;
+            chunk(w, k, ci++);
+            k += gridDim.x;
+        }
+        // the scores kept in LDS (stores in the loop would leave the compiler unable to wait for just the older chunk)
+        if (a.out && t < C) {
+            const int m = t / R, r = t - m * R;
+            for (int c2 = 0; c2 < ci; c2++) {
+                const int g0 = ((int)blockIdx.x + c2 * (int)gridDim.x) * G;
+                if (r < 8 * min(G, gtot - g0)) a.out[(size_t)m * a.out_ld + 8 * g0 + r] = l_lg[c2 * C + t];
+            }
+        }
+    } else if (k < nchunk) {   // (every other table: one chunk per workgroup)
+        chunk(w, k, 0);
     }
+    if (late_stores && blockIdx.x == 0 && t < nq)
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            if (a.x_out) ((f32x4*)(a.x_out + (size_t)m * E))[t] = xv[m];
+            if (a.hidden_out) ((f32x4*)(a.hidden_out + (size_t)m * E))[t] = hsave[late_stores ? m : 0];
+        }
     if (EPI == EPI_LOGITS) {   // the workgroup's first maximum per input
 #pragma unroll
         for (int m = 0; m < M; m++) {
@@ -786,10 +930,12 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
     }
 }
 
-static size_t gemv_norm_lds(int M, int E, int nb, int G) {
+// chunks_per_wg: the word scores' chunks per workgroup (their scores wait in LDS until the chunk loop ends), else 0
+static size_t gemv_norm_lds(int M, int E, int nb, int G, int chunks_per_wg = 0) {
     const size_t st = (size_t)(((nb + 3) & ~3) + 4), R = 8 * (size_t)G, C = M * R;
     (void)E;
-    return sizeof(float) * ((size_t)M * 32 * XLD + (size_t)M * nb * 8 + (size_t)M * nb + M * st + 2 * M * R * st + R * st + 2 * C + 32 + 64);
+    return sizeof(float) * ((size_t)M * 32 * XLD + (size_t)M * nb * 8 + (size_t)M * nb + M * st + 2 * M * R * st + R * st + 2 * C + 32 + 64 +
+                            (size_t)chunks_per_wg * C);
 }
 
 // ---------------------------------------------------------------- word scores over a Q6_K table
@@ -1634,6 +1780,12 @@ hipError_t launch_scores_q6k(int M, int grid, const gemv_args& a, hipStream_t s,
     return hipExtLaunchKernel(fn, dim3(grid), dim3(512), args, lds, s, t0, t1, 0);
 }
 
+bool swiglu_cut_takes(int M, const gemv_args& gate_up, const gemv_args& down) {
+    return (M == 1 || M == 2) && norm_kernel_takes(M, PRO_RESID_NORM, gate_up, 2) && !gate_up.W.mins && gate_up.units % 4 == 0 &&
+           gate_up.units >= 4 && !down.W.mins && down.W.rows % 8 == 0 &&
+           (down.W.nb == 64 || down.W.nb == 128 || down.W.nb == 256) && down.W.cols == 8 * gate_up.units;
+}
+
 hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
     const int nbl = (a.W.nb + 63) / 64;
     const int ug = epi == EPI_SWIGLU ? 2 : epi == EPI_CONV ? 3 : 1;
@@ -1642,7 +1794,9 @@ hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hi
         // units per chunk: 8 groups for the word scores (looped), else enough that one round of workgroups (one
         // per compute unit: the register use allows one 512-thread workgroup per unit) covers the table
         const int cap = 8 / ug, want = (a.units + 255) / 256;
-        b.upw = epi == EPI_LOGITS ? 8 : (want < 1 ? 1 : want > cap ? cap : want);
+        b.upw = a.upw > 0 ? a.upw : epi == EPI_LOGITS ? 8 : (want < 1 ? 1 : want > cap ? cap : want);
+        // the cut epilogue needs every chunk to be one whole 32-channel block
+        if (a.outq && (epi != EPI_SWIGLU || b.upw != 4 || a.units % 4 != 0 || a.W.mins)) return hipErrorInvalidValue;
         const int nchunk = (a.units + b.upw - 1) / b.upw;
         const void* fn = nullptr;
         const bool hm = a.W.mins != nullptr;
@@ -1658,7 +1812,7 @@ hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hi
 #undef SH_NORM_FN
         }
         if (!fn) return hipErrorInvalidValue;
-        const size_t lds = gemv_norm_lds(M, a.E, a.W.nb, b.upw * ug);
+        const size_t lds = gemv_norm_lds(M, a.E, a.W.nb, b.upw * ug, epi == EPI_LOGITS ? (nchunk + grid - 1) / grid : 0);
         if (lds > 160 * 1024) return hipErrorInvalidValue;
         if (lds > 64 * 1024) {
             const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -1671,6 +1825,20 @@ hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hi
     }
     // the plain tables (input cut, rows stored): one workgroup per 8-row group, the grid is the group count
     const int nb = a.W.nb;
+    if (pro == PRO_PRECUT) {   // the input arrives cut: Q4_0 tables of 64, 128 or 256 blocks
+        if (epi != EPI_STORE || a.W.mins || a.W.rows % 8 != 0 || !a.src_q || !a.src_d || !a.src_s || (M != 1 && M != 2))
+            return hipErrorInvalidValue;
+        const void* fn = nullptr;
+#define SH_PRE_FN(M_, NB_) if (M == M_ && nb == NB_) fn = (const void*)k_gemv_cut<M_, false, NB_, false, true>;
+        SH_PRE_FN(1, 64) SH_PRE_FN(1, 128) SH_PRE_FN(1, 256) SH_PRE_FN(2, 64) SH_PRE_FN(2, 128) SH_PRE_FN(2, 256)
+#undef SH_PRE_FN
+        if (!fn) return hipErrorInvalidValue;
+        void* args[] = {const_cast<gemv_args*>(&a)};
+        const dim3 gr(a.W.rows / 8), bl(256);
+        const size_t lds = gemv_cut_lds(M, nb);
+        if (t0) return hipExtLaunchKernel(fn, gr, bl, args, lds, s, t0, t1, 0);
+        return hipLaunchKernel(fn, gr, bl, args, lds, s);
+    }
     if (epi == EPI_STORE && (pro == PRO_CUT || pro == PRO_CUT_HALF_AWAY) && (nb == 64 || nb == 128 || nb == 256) &&
         a.W.rows % 8 == 0 && (M == 1 || (M == 2 && pro == PRO_CUT))) {
         const bool half = pro == PRO_CUT_HALF_AWAY, hm = a.W.mins != nullptr;
