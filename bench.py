@@ -64,6 +64,33 @@ def gpu_decode(brain, steps, warmup, b2: bool):
     return tokens / wall, ids, dev, wall
 
 
+def real_seoul_decode(steps, warmup):
+    """Greedy decode on the shape of the released Seoul files (24 layers, 16/4 x 128 heads, FFN 7680, 7-tap conv,
+    rope_freqs, window 256 on 4 of the 8 attention layers, Q6_K tied word table), B=1 and B=2."""
+    import nunchi_amd
+    from nunchi_amd import synth
+    shp = synth.REAL_SEOUL
+    rb = nunchi_amd.Brain(synth.cached("brain", shp, 0), n_ctx=N_CTX)
+    t1, _, d1, _ = gpu_decode(rb, steps, warmup, b2=False)
+    t2, _, d2, _ = gpu_decode(rb, steps, warmup, b2=True)
+    # algorithmic bytes of a step: every table once, the fp32 vectors, the K and V rows the attention layers read
+    # (window layers at most 256 positions), averaged over the generated positions
+    kv_head = rb.n_head_kv * rb.head_dim * 2
+    n_full = rb.n_attn - len(shp.swa_layers)
+    kv = sum(2 * kv_head * (n_full * (PROMPT + i + 1) + len(shp.swa_layers) * min(PROMPT + i + 1, shp.sliding_window))
+             for i in range(steps)) / steps
+    step_b = rb.table_bytes + rb.vector_bytes + kv
+    out = {"workload": "Seoul file shape: 24 layers (16 short-conv k=7, 8 GQA 16/4 x 128 with q/k norms and gates, "
+                       "rope_freqs divisors, window 256 on layers 2/8/14/20), FFN 7680, tied Q6_K vocab 97496 x 2048, "
+                       f"fp16 KV ctx {N_CTX}; {PROMPT}-token seeded prompt then {steps} greedy ids on device",
+           "b1_tokens_per_s": round(t1, 1), "b2_tokens_per_s": round(t2, 1),
+           "device_ms_per_step": {"b1": round(d1 * 1e3 / steps, 4), "b2": round(d2 * 1e3 / steps, 4)},
+           "bytes_per_step": int(step_b),
+           "hbm_fraction": {"b1": round(step_b * t1 / 1e9 / HBM_PEAK_GBS, 4), "b2": round(step_b * t2 / 2 / 1e9 / HBM_PEAK_GBS, 4)}}
+    del rb
+    return out
+
+
 def cpu_decode(path, threads, steps, b2: bool, runs: int = 1):
     """imi's CPU path (the oracle restatement): `runs` conversations, each a 32-token prompt then `steps` greedy
     ids; returns (tokens/s over the generated tokens of all runs, ids of run 0 (B=2: both conversations'), seconds)."""
@@ -436,6 +463,9 @@ def main():
     ap.add_argument("--voice-only", type=int, default=0, metavar="FRAMES",
                     help="only cfg 4: FRAMES voice frames (step2 at KV context 2048+, generator passes of 4 + 4 with "
                          "sampling, after 4 untimed): the launches a kernel trace of the whole frame reads")
+    ap.add_argument("--real-steps", type=int, default=128,
+                    help="timed greedy ids on the Seoul file shape (24 layers, FFN 7680, Q6_K vocab); 0 = skip")
+    ap.add_argument("--real-only", action="store_true", help="only the Seoul-file-shape decode")
     ap.add_argument("--counters-workload", action="store_true",
                     help="only the launches the hardware-counter runs read: a streaming kernel of known size (the "
                          "exponential over 16 Mi floats: 64 MiB read, 64 MiB written), 64 read-only GEMVs of known "
@@ -446,7 +476,7 @@ def main():
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (conversations shard across "
               "GPUs with no exchange; see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
-    if PROMPT + max(args.steps, args.warmup) > N_CTX:
+    if PROMPT + max(args.steps, args.warmup, args.real_steps) > N_CTX:
         print(f"bench.py: prompt + steps must fit the context of {N_CTX}", file=sys.stderr)
         sys.exit(2)
 
@@ -502,6 +532,9 @@ def main():
                 ts.append(time.perf_counter() - t0)
         print(json.dumps({"codec_only": {"frames": len(ts), "p50_ms": round(float(np.percentile(ts, 50)) * 1e3, 3),
                                          "table_bytes": int(codec.info.table_bytes)}}), flush=True)
+        return
+    if args.real_only:
+        print(json.dumps({"real_only": real_seoul_decode(max(1, args.real_steps), args.warmup)}), flush=True)
         return
     path = synth.cached("brain", synth.SEOUL, 0)
     if args.voice_only:
@@ -679,6 +712,8 @@ def main():
                                     "floor": cfg0_floor},
         },
     }
+    if args.real_steps:
+        line["real_seoul_decode"] = real_seoul_decode(args.real_steps, args.warmup)
     if args.prefill_reps:
         pt, plg, pbest = gpu_prefill(brain, args.prefill_reps)
         n_pf = HEAR_EMB + HEAR_TOK

@@ -268,10 +268,13 @@ __global__ __launch_bounds__(64) void k_gemv(gemv_args a) {
 // place of d and the row ends as acc + cor
 // g: the table's 8-row group this workgroup computes
 // PRE: the input arrives cut (PRO_PRECUT: codes, d and s as the FFN gate|up epilogue wrote them); the prologue only
-// stages them
-template <int M, bool HALF, int NB, bool HM, bool PRE = false>
+// stages them. NR: the table has nb = a.W.nb blocks per row, a multiple of 16 below NB (an FFN of 7680 gives a 240-block
+// down table): the body keeps NB's thread layout, threads past nb read the last block (their LDS slots are never
+// read), strides and the chain's length follow nb
+template <int M, bool HALF, int NB, bool HM, bool PRE = false, bool NR = false>
 __device__ __forceinline__ void gemv_cut_body(const gemv_args& a, const int g) {
     constexpr int TPB = 256 / NB, VPT = 32 / TPB, RPT = NB / 32, ST = NB + 4, IPT = 8 / TPB;
+    const int nbr = NR ? a.W.nb : NB;   // blocks per row
     extern __shared__ __align__(16) float lds[];
     int* l_xq = (int*)lds;                      // [M][NB][8] int8 codes of the cut input, 4 per word
     float* l_dx = lds + M * NB * 8;             // [M][NB]
@@ -281,7 +284,7 @@ __device__ __forceinline__ void gemv_cut_body(const gemv_args& a, const int g) {
     float* l_dd = l_oq + M * 8 * ST;            // [8][ST] d
     const int t = threadIdx.x, lane = t & 63;
     // input share first: block jc, values part * VPT .. + VPT - 1
-    const int jc = t / TPB, part = t - jc * TPB;
+    const int jc = t / TPB, part = t - jc * TPB, jcl = NR ? min(jc, nbr - 1) : jc;
     f32x4 xin[PRE ? 1 : M][VPT / 4];
     u32x4 qin[PRE ? M : 1][(IPT + 3) / 4];   // PRE: this thread's IPT dwords (4 codes each) of block jc
     float din[M], sin_[M];
@@ -289,7 +292,7 @@ __device__ __forceinline__ void gemv_cut_body(const gemv_args& a, const int g) {
         static_assert(IPT == 8 || IPT == 4 || IPT == 2, "cut dwords per thread");
 #pragma unroll
         for (int m = 0; m < M; m++) {
-            const unsigned* qs = (const unsigned*)(a.src_q + (size_t)m * a.src_ld + 32 * jc) + IPT * part;
+            const unsigned* qs = (const unsigned*)(a.src_q + (size_t)m * a.src_ld + 32 * jcl) + IPT * part;
             if (IPT >= 4) {
 #pragma unroll
                 for (int k = 0; k < IPT / 4; k++) qin[m][k] = ((const u32x4*)qs)[k];
@@ -298,26 +301,26 @@ __device__ __forceinline__ void gemv_cut_body(const gemv_args& a, const int g) {
                 const u32x2 v2 = *(const u32x2*)qs;
                 qin[m][0] = u32x4{v2.x, v2.y, 0u, 0u};
             }
-            din[m] = a.src_d[(size_t)m * NB + jc];
-            sin_[m] = a.src_s[(size_t)m * NB + jc];
+            din[m] = a.src_d[(size_t)m * nbr + jcl];
+            sin_[m] = a.src_s[(size_t)m * nbr + jcl];
         }
     } else {
 #pragma unroll
         for (int m = 0; m < M; m++) {
-            const f32x4* src = (const f32x4*)(a.src + (size_t)m * a.src_ld + 32 * jc + VPT * part);
+            const f32x4* src = (const f32x4*)(a.src + (size_t)m * a.src_ld + 32 * jcl + VPT * part);
 #pragma unroll
             for (int k = 0; k < VPT / 4; k++) xin[PRE ? 0 : m][k] = src[k];
         }
     }
     // then the weights: rows sub * RPT .. + RPT - 1 of block jw
-    const int jw = t % NB, sub = t / NB;
+    const int jw = t % NB, sub = t / NB, jwl = NR ? min(jw, nbr - 1) : jw;
     u32x4 c[RPT];
-    const u32x4* codes = (const u32x4*)a.W.codes + (size_t)(8 * g + sub * RPT) * NB + jw;
+    const u32x4* codes = (const u32x4*)a.W.codes + (size_t)(8 * g + sub * RPT) * nbr + jwl;
 #pragma unroll
-    for (int k = 0; k < RPT; k++) c[k] = __builtin_nontemporal_load(codes + (size_t)k * NB);
-    const u32x4 s8 = __builtin_nontemporal_load((const u32x4*)a.W.scales + (size_t)g * NB + jw);
+    for (int k = 0; k < RPT; k++) c[k] = __builtin_nontemporal_load(codes + (size_t)k * nbr);
+    const u32x4 s8 = __builtin_nontemporal_load((const u32x4*)a.W.scales + (size_t)g * nbr + jwl);
     u32x4 m8 = s8;
-    if (HM) m8 = __builtin_nontemporal_load((const u32x4*)a.W.mins + (size_t)g * NB + jw);
+    if (HM) m8 = __builtin_nontemporal_load((const u32x4*)a.W.mins + (size_t)g * nbr + jwl);
     // the cut of block jc by its TPB threads (PRE: staged as it arrived)
 #pragma unroll
     for (int m = 0; m < M; m++) {
@@ -400,7 +403,8 @@ __device__ __forceinline__ void gemv_cut_body(const gemv_args& a, const int g) {
         const int k = acc_lane ? lane : lane - 8 * M, m = k >> 3, r = k & 7;
         const f32x4* ap = (const f32x4*)(acc_lane ? l_op + (m * 8 + r) * ST : l_dd + r * ST);
         const f32x4* bp = (const f32x4*)(acc_lane ? l_oq + (m * 8 + r) * ST : l_s + m * ST);
-        for (int q0 = 0; q0 < NB / 4; q0 += 16) {   // per 64 blocks: the reads of the next 6 quads in flight
+        const int nq = nbr / 4;
+        for (int q0 = 0; q0 + 16 <= nq; q0 += 16) {   // per 64 blocks: the reads of the next 6 quads in flight
             f32x4 qa[16], qb[16];
 #pragma unroll
             for (int q = 0; q < 6; q++) { qa[q] = ap[q0 + q]; qb[q] = bp[q0 + q]; }
@@ -414,6 +418,14 @@ __device__ __forceinline__ void gemv_cut_body(const gemv_args& a, const int g) {
                 chain = fmaf(qa[q].w, qb[q].w, chain);
             }
         }
+        if (NR)   // the last nb % 64 blocks, in order
+            for (int q = nq & ~15; q < nq; q++) {
+                const f32x4 x = ap[q], y = bp[q];
+                chain = fmaf(x.x, y.x, chain);
+                chain = fmaf(x.y, y.y, chain);
+                chain = fmaf(x.z, y.z, chain);
+                chain = fmaf(x.w, y.w, chain);
+            }
     }
     const float cor = __shfl(chain, (lane + 8 * M) & 63);
     if (acc_lane) {
@@ -422,9 +434,9 @@ __device__ __forceinline__ void gemv_cut_body(const gemv_args& a, const int g) {
     }
 }
 
-template <int M, bool HALF, int NB, bool HM = false, bool PRE = false>
+template <int M, bool HALF, int NB, bool HM = false, bool PRE = false, bool NR = false>
 __global__ __launch_bounds__(256) void k_gemv_cut(gemv_args a) {
-    gemv_cut_body<M, HALF, NB, HM, PRE>(a, blockIdx.x);
+    gemv_cut_body<M, HALF, NB, HM, PRE, NR>(a, blockIdx.x);
 }
 
 // several tables in one launch: workgroup b computes group b - start[t] of table t (start[t] <= b < start[t + 1]),
@@ -449,6 +461,9 @@ __global__ __launch_bounds__(256) void k_gemv_cut_group(gemv_group_args G) {
     else if (a.W.nb == 128) gemv_cut_body<M, HALF, 128, false>(a, g);
     else gemv_cut_body<M, HALF, 256, false>(a, g);
 }
+
+// widths the 256-block cut body takes with a runtime block count: multiples of 16 between 128 and 256
+static bool nb_runtime256(int nb) { return nb > 128 && nb < 256 && nb % 16 == 0; }
 
 static size_t gemv_cut_lds(int M, int nb) {
     const size_t st = (size_t)nb + 4;
@@ -1783,7 +1798,7 @@ hipError_t launch_scores_q6k(int M, int grid, const gemv_args& a, hipStream_t s,
 bool swiglu_cut_takes(int M, const gemv_args& gate_up, const gemv_args& down) {
     return (M == 1 || M == 2) && norm_kernel_takes(M, PRO_RESID_NORM, gate_up, 2) && !gate_up.W.mins && gate_up.units % 4 == 0 &&
            gate_up.units >= 4 && !down.W.mins && down.W.rows % 8 == 0 &&
-           (down.W.nb == 64 || down.W.nb == 128 || down.W.nb == 256) && down.W.cols == 8 * gate_up.units;
+           (down.W.nb == 64 || down.W.nb == 128 || down.W.nb == 256 || nb_runtime256(down.W.nb)) && down.W.cols == 8 * gate_up.units;
 }
 
 hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
@@ -1832,18 +1847,22 @@ hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hi
 #define SH_PRE_FN(M_, NB_) if (M == M_ && nb == NB_) fn = (const void*)k_gemv_cut<M_, false, NB_, false, true>;
         SH_PRE_FN(1, 64) SH_PRE_FN(1, 128) SH_PRE_FN(1, 256) SH_PRE_FN(2, 64) SH_PRE_FN(2, 128) SH_PRE_FN(2, 256)
 #undef SH_PRE_FN
+        if (nb_runtime256(nb)) fn = M == 1 ? (const void*)k_gemv_cut<1, false, 256, false, true, true> : (const void*)k_gemv_cut<2, false, 256, false, true, true>;
         if (!fn) return hipErrorInvalidValue;
         void* args[] = {const_cast<gemv_args*>(&a)};
         const dim3 gr(a.W.rows / 8), bl(256);
-        const size_t lds = gemv_cut_lds(M, nb);
+        const size_t lds = gemv_cut_lds(M, nb_runtime256(nb) ? 256 : nb);
         if (t0) return hipExtLaunchKernel(fn, gr, bl, args, lds, s, t0, t1, 0);
         return hipLaunchKernel(fn, gr, bl, args, lds, s);
     }
-    if (epi == EPI_STORE && (pro == PRO_CUT || pro == PRO_CUT_HALF_AWAY) && (nb == 64 || nb == 128 || nb == 256) &&
+    if (epi == EPI_STORE && (pro == PRO_CUT || pro == PRO_CUT_HALF_AWAY) &&
+        (nb == 64 || nb == 128 || nb == 256 || (nb_runtime256(nb) && pro == PRO_CUT && !a.W.mins)) &&
         a.W.rows % 8 == 0 && (M == 1 || (M == 2 && pro == PRO_CUT))) {
         const bool half = pro == PRO_CUT_HALF_AWAY, hm = a.W.mins != nullptr;
         if (half && hm) return hipErrorInvalidValue;   // q4x8's cut is for Q4_0 tables only
         const void* fn = nullptr;
+        if (nb_runtime256(nb) && !half && !hm)   // 240-style widths: the 256-block body with the runtime count
+            fn = M == 1 ? (const void*)k_gemv_cut<1, false, 256, false, false, true> : (const void*)k_gemv_cut<2, false, 256, false, false, true>;
 #define SH_CUT_FN(M_, H_, NB_) if (M == M_ && half == H_ && nb == NB_) fn = (const void*)k_gemv_cut<M_, H_, NB_>;
 #define SH_CUT_FN1(M_, NB_) if (M == M_ && nb == NB_) fn = (const void*)k_gemv_cut<M_, false, NB_, true>;
         if (hm) {
@@ -1857,7 +1876,7 @@ hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hi
 #undef SH_CUT_FN1
         void* args[] = {const_cast<gemv_args*>(&a)};
         const dim3 gr(a.W.rows / 8), bl(256);
-        const size_t lds = gemv_cut_lds(M, nb);
+        const size_t lds = gemv_cut_lds(M, nb_runtime256(nb) ? 256 : nb);
         if (t0) return hipExtLaunchKernel(fn, gr, bl, args, lds, s, t0, t1, 0);
         return hipLaunchKernel(fn, gr, bl, args, lds, s);
     }

@@ -47,6 +47,13 @@ class BrainShape:
 
 
 SEOUL = BrainShape()
+# the shape of the released Seoul brain files as imi's loader reads their keys (imi/core/seoul.cpp:93-142): 24 layers,
+# 16 query / 4 key-value heads of 128, FFN 7680, 7-tap short conv, rope_freqs divisors and a Q6_K tied word table.
+# The files' layer pattern is not published in the reference: attention every third layer from 2, the window of 256
+# on every other attention layer (the pattern key's "sliding" entries), the rest short-conv blocks
+REAL_SEOUL = BrainShape(n_layer=24, attn_layers=(2, 5, 8, 11, 14, 17, 20, 23), n_head=16, n_head_kv=4, head_dim=128,
+                        n_ff=7680, conv_kernel=7, vocab_type="q6_k", rope_freqs=True, sliding_window=256,
+                        swa_layers=(2, 8, 14, 20))
 # small model with every feature of the path, for tests that must finish in seconds on the CPU oracle
 TINY = BrainShape(n_embd=256, n_layer=4, attn_layers=(1, 3), n_head=8, n_head_kv=2, head_dim=32, n_ff=512,
                   n_vocab=1000, conv_kernel=3)

@@ -62,7 +62,8 @@ def test_rows_dequant_bit_exact(ctx):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("rows,cols", [(8192, 2048), (2048, 8192), (3104, 2048), (8, 32), (24, 96), (64, 7680)])
+@pytest.mark.parametrize("rows,cols", [(8192, 2048), (2048, 8192), (3104, 2048), (8, 32), (24, 96), (64, 7680), (2048, 7680),
+                                       (16, 4608)])
 def test_gemv_exact_regime_bitwise(ctx, rows, cols):
     import nunchi_amd
     import oracle
@@ -86,7 +87,8 @@ def _cut_dequant(x):
     return (q.astype(np.float64) * d.astype(np.float64)).reshape(np.shape(x))
 
 
-@pytest.mark.parametrize("rows,cols", [(8192, 2048), (2048, 2048), (512, 2048), (2048, 8192), (3104, 2048), (64, 7680), (16, 64)])
+@pytest.mark.parametrize("rows,cols", [(8192, 2048), (2048, 2048), (512, 2048), (2048, 8192), (3104, 2048), (64, 7680),
+                                       (2048, 7680), (16, 4608), (16, 64)])
 def test_gemv_matches_imi_arithmetic(ctx, rows, cols):
     import nunchi_amd
     import oracle
@@ -102,11 +104,11 @@ def test_gemv_matches_imi_arithmetic(ctx, rows, cols):
     assert np.abs(orc - ref).max() < 1e-5 * scale + 1e-30
 
 
-def test_gemv_two_inputs_match_oracle_group2(ctx):
+@pytest.mark.parametrize("rows,cols", [(2048, 8192), (2048, 7680)])
+def test_gemv_two_inputs_match_oracle_group2(ctx, rows, cols):
     """imi_q4_group2 (imi/core/tables.cpp:145-163) on the oracle side, the two-input kernel on the GPU."""
     import nunchi_amd
     import oracle
-    rows, cols = 2048, 8192
     blk = q4_random(rows, cols, seed=21)
     x = np.random.default_rng(22).standard_normal((2, cols)).astype(np.float32)
     got = nunchi_amd.Q4Table(ctx, blk, rows, cols).gemv(x)
