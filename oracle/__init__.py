@@ -54,6 +54,8 @@ def lib():
         "orc_engine_greedy2": (d, [vp, vp, i, i, i, _i32p, _i32p]),
         "orc_engine_cache": (None, [vp, i, _u16p, _u16p]),
         "orc_engine_conv_state": (None, [vp, i, _f32p]),
+        "orc_engine_trace_cuts": (None, [vp, i]),
+        "orc_engine_take_cuts": (C.c_size_t, [vp, vp, C.c_size_t]),
         "orc_h2f": (f, [C.c_uint16]),
         "orc_q8k_from": (None, [_f32p, i, _i8p, _f32p, C.POINTER(C.c_int16)]),
         "orc_q6k_dequant_row": (None, [_u8p, i, _f32p]),
@@ -187,6 +189,17 @@ class Engine:
         k, v = np.zeros(n, np.uint16), np.zeros(n, np.uint16)
         lib().orc_engine_cache(self.h, ai, k, v)
         return k.reshape(self.n_ctx, -1), v.reshape(self.n_ctx, -1)
+
+    def trace_cuts(self, on: bool = True):
+        """Record the int8 codes of every input cut the following single steps make (cleared when started)."""
+        lib().orc_engine_trace_cuts(self.h, int(on))
+
+    def take_cuts(self) -> np.ndarray:
+        """The codes recorded since the trace started or was last taken, in the order the steps cut them."""
+        n = lib().orc_engine_take_cuts(self.h, None, 0)
+        out = np.zeros(n, np.int8)
+        lib().orc_engine_take_cuts(self.h, _ptr(out), n)
+        return out
 
     def conv_state(self, il: int):
         out = np.zeros(self.d_conv * self.n_embd, np.float32)

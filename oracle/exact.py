@@ -80,12 +80,54 @@ def cut_dequant(x: np.ndarray) -> np.ndarray:
     return (q.astype(np.float64) * d.astype(np.float64)).reshape(np.shape(x))
 
 
-def brain(path: str, tokens=None, embd=None, cut: bool = False):
+def forced_cut(x: np.ndarray, codes: np.ndarray, tol: float = 0.02):
+    """A cut whose int8 codes are given (teacher forcing): the scale d = amax / 127 of the float64 values x as the
+    cut computes it, the codes checked as a rounding of x / d (each within 0.5 + tol of it, so a code may differ from
+    x's own rounding only where x / d lies within tol of a rounding boundary), returned as float64 codes * d and the
+    number of codes that differ from x's own rounding."""
+    x32 = np.asarray(x, np.float32).reshape(*np.shape(x)[:-1], -1, 32)
+    q = np.asarray(codes, np.int8).reshape(x32.shape).astype(np.float64)
+    d = (np.abs(x32).max(-1, keepdims=True) / np.float32(127)).astype(np.float32).astype(np.float64)
+    x64 = np.asarray(x, np.float64).reshape(x32.shape)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        r = np.where(d != 0, x64 / d, 0.0)
+    bad = np.abs(r - q) > 0.5 + tol
+    if bad.any():
+        i = np.argwhere(bad)[0]
+        raise AssertionError(f"forced code {q[tuple(i)]:.0f} is no rounding of x / d = {r[tuple(i)]:.6f}")
+    own = np.rint((x32 * np.where(d != 0, np.float32(1) / d.astype(np.float32), np.float32(0))).astype(np.float32))
+    return (q * d).reshape(np.shape(x)), int((own != q).sum())
+
+
+def forced_half(x: np.ndarray, half: np.ndarray, rtol: float = 1e-5) -> np.ndarray:
+    """An fp16 rounding whose results are given (the engine's key / value cache): each checked within half an fp16
+    ulp of the float64 value plus rtol times the largest magnitude of its head row (the last axis: the fp32 norm,
+    RoPE angle and sums before the rounding err on the row's scale, not the element's), returned as float64."""
+    h = np.asarray(half, np.uint16).view(np.float16).reshape(np.shape(x))
+    x = np.asarray(x, np.float64)
+    ulp = np.spacing(np.abs(h)).astype(np.float64)
+    err = np.abs(h.astype(np.float64) - x)
+    lim = 0.5 * ulp + rtol * np.abs(x).max(-1, keepdims=True)
+    if (err > lim).any():
+        i = tuple(np.argwhere(err > lim)[0])
+        raise AssertionError(f"forced fp16 {float(h[i])!r} is no rounding of {float(x[i])!r}")
+    return h.astype(np.float64)
+
+
+def brain(path: str, tokens=None, embd=None, cut: bool = False, forced: dict | None = None):
     """Hidden states and logits for every position of one sequence, float64 (ref_exact.py:37-87).
 
     cut=True also cuts every table input to int8 per 32 exactly where imi's engine does (imi/core/seoul.cpp:405,
     415, 457, 465, 469, 480) and rounds keys and values through fp16 as its cache does, so what is left between
-    this and the engine is fp32 rounding alone."""
+    this and the engine is fp32 rounding alone.
+
+    forced (with cut=True): the engine's own int8 codes and fp16 keys and values, {"cuts": the codes of every cut of
+    the steps at these positions in the order one step makes them (attention-norm input, conv or attention output,
+    FFN-norm input and SwiGLU output per layer, then the hidden state for the word scores), "kv": {attention layer
+    index: (keys, values) as fp16 bits [position][kv heads x D]}}. Each is checked as a rounding of the float64 value
+    (forced_cut, forced_half) and then used in its place, so that a code the two arithmetics round apart (an fp32
+    value within rounding of a boundary) does not move the positions after it; forced["flips"] returns the number
+    of such codes."""
     C = cut_dequant if cut else (lambda v: v)
     W = Weights(path)
     kv = W.f.kv
@@ -99,6 +141,28 @@ def brain(path: str, tokens=None, embd=None, cut: bool = False):
     emb = W("token_embd.weight")
     X = emb[np.asarray(tokens)] if tokens is not None else np.asarray(embd, np.float64)
     T = X.shape[0]
+    site = None
+    if forced is not None:
+        assert cut, "forced cuts replace the cuts of cut=True"
+        E, Hq, n_ff = X.shape[1], H * D, W("blk.0.ffn_gate.weight").shape[0]
+        widths = []
+        for il in range(n_layer):
+            widths += [E, E if W.has(f"blk.{il}.shortconv.conv.weight") else Hq, E, n_ff]
+        widths.append(E)
+        flat = np.asarray(forced["cuts"], np.int8)
+        assert flat.size == T * sum(widths), (flat.size, T, sum(widths))
+        cols = np.cumsum([0] + widths)
+        per = flat.reshape(T, -1)
+        forced["flips"] = 0
+        sites = iter(range(len(widths)))
+
+        def site(v):
+            j = next(sites)
+            out, n = forced_cut(v, per[:, cols[j]:cols[j + 1]])
+            forced["flips"] += n
+            return out
+        C = site
+    ai = -1
 
     def norm(x, w):
         return x / np.sqrt((x * x).mean(-1, keepdims=True) + eps) * w
@@ -136,7 +200,12 @@ def brain(path: str, tokens=None, embd=None, cut: bool = False):
             sw = swa_pat[il] if il < len(swa_pat) else False
             q = rope(q, base_swa if sw else base, None if sw else ff)
             k = rope(k, base_swa if sw else base, None if sw else ff)
-            if cut:   # the engine keeps keys and values in an fp16 cache (imi/core/seoul.cpp:438)
+            ai += 1
+            if forced is not None:
+                kf, vf = forced["kv"][ai]
+                k = forced_half(k, np.asarray(kf)[:T].reshape(k.shape))
+                v = forced_half(v, np.asarray(vf)[:T].reshape(v.shape))
+            elif cut:   # the engine keeps keys and values in an fp16 cache (imi/core/seoul.cpp:438)
                 k = k.astype(np.float32).astype(np.float16).astype(np.float64)
                 v = v.astype(np.float32).astype(np.float16).astype(np.float64)
             a = np.zeros((T, H, D))

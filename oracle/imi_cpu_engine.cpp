@@ -166,6 +166,10 @@ struct engine {
     static constexpr int NB = 64;
     std::vector<float> bX, bH, bBig, bY, bAct;
     q8b bq;
+    // the int8 codes of every input cut a single step makes, in the order it makes them (thread 0's copy: every
+    // thread cuts the same input alike), kept while trace_cuts is set; the float64 model takes them as its own cuts
+    bool trace_cuts = false;
+    std::vector<int8_t> cut_trace;
 
     bool load(const std::string& path, int threads, int ctx_len);
     void embed(int32_t token, const float* embd, float* x) const;
@@ -397,10 +401,14 @@ void engine::run(int tid, int32_t token, const float* embd, bool want_logits) {
             }
     };
     auto sync = [&] { tm.sync(); };
+    auto cut = [&](const float* v, int n) {
+        T.qi.from(v, n);
+        if (tid == 0 && trace_cuts) cut_trace.insert(cut_trace.end(), T.qi.q.begin(), T.qi.q.begin() + n);
+    };
     for (size_t il = 0; il < layers.size(); il++) {
         const layer& L = layers[il];
         norm_mul(x, L.attn_norm, T.h.data(), E, eps);
-        T.qi.from(T.h.data(), E);
+        cut(T.h.data(), E);
         if (L.conv) {
             table(L.in_proj, bcx.data());
             sync();
@@ -409,7 +417,7 @@ void engine::run(int tid, int32_t token, const float* embd, bool want_logits) {
             for (int e = 0; e < E; e++) u[e] = b[e] * xx[e] * w[d_conv * E + e];
             for (int k = 0; k < d_conv; k++) for (int e = 0; e < E; e++) u[e] = fmaf(st[k * E + e], w[k * E + e], u[e]);
             for (int e = 0; e < E; e++) u[e] *= cc[e];
-            T.qi.from(u, E);
+            cut(u, E);
             table(L.out_proj, y.data());
             sync();
             if (tid == 0) {   // the conv memory slides one step
@@ -423,16 +431,16 @@ void engine::run(int tid, int32_t token, const float* embd, bool want_logits) {
             for (int g = tid; g < n_head_kv; g += n_threads)
                 attend(L, qkv.data(), own.k_cache[L.ai].data(), own.v_cache[L.ai].data(), own.pos, g, att.data(), T.t.data());
             sync();
-            T.qi.from(att.data(), Hq);
+            cut(att.data(), Hq);
             table(L.o, y.data());
             sync();
         }
         norm_mul_add(y.data(), L.post_attn_norm, x, E, eps);
         norm_mul(x, L.ffn_norm, T.h.data(), E, eps);
-        T.qi.from(T.h.data(), E);
+        cut(T.h.data(), E);
         table_ffn(L.gate_up, act.data());
         sync();
-        T.qi.from(act.data(), n_ff);
+        cut(act.data(), n_ff);
         table(L.down, fo.data());
         sync();
         norm_mul_add(fo.data(), L.post_ffn_norm, x, E, eps);
@@ -441,6 +449,8 @@ void engine::run(int tid, int32_t token, const float* embd, bool want_logits) {
     norm_mul(x, out_norm, hid, E, eps);
     if (tid == 0) memcpy(own.hidden.data(), hid, (size_t)E * sizeof(float));
     if (want_logits) word_scores(T, hid, own.logits.data(), ctr[c++]);
+    if (want_logits && !vocab_q6k && tid == 0 && trace_cuts)   // the word scores' cut of the hidden state
+        cut_trace.insert(cut_trace.end(), T.qi.q.begin(), T.qi.q.begin() + E);
 }
 
 void engine::step2(int32_t ta, const float* ea, bool la, state& b, int32_t tb, const float* eb, bool lb) {   // seoul.cpp:208-220
@@ -981,6 +991,21 @@ void orc_engine_cache(void* h, int ai, uint16_t* k, uint16_t* v) {
     auto* e = (engine*)h;
     memcpy(k, e->own.k_cache[ai].data(), e->own.k_cache[ai].size() * 2);
     memcpy(v, e->own.v_cache[ai].data(), e->own.v_cache[ai].size() * 2);
+}
+// the cut trace of single steps: on != 0 starts it (empty), on == 0 stops it; take copies out up to cap codes, clears
+// the trace and returns how many it held (out == nullptr: only the count, nothing cleared)
+void orc_engine_trace_cuts(void* h, int on) {
+    auto* e = (engine*)h;
+    e->trace_cuts = on != 0;
+    e->cut_trace.clear();
+}
+size_t orc_engine_take_cuts(void* h, int8_t* out, size_t cap) {
+    auto* e = (engine*)h;
+    const size_t n = e->cut_trace.size();
+    if (!out) return n;
+    memcpy(out, e->cut_trace.data(), std::min(n, cap));
+    e->cut_trace.clear();
+    return n;
 }
 void orc_engine_conv_state(void* h, int il, float* out) {
     auto* e = (engine*)h;

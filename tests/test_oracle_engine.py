@@ -1,8 +1,11 @@
 """Pins of the oracle's engine (imi/core/seoul.cpp, imi/core/voice.cpp restated) at the model level:
 
 - against the float64 restatement of imi/ref/ref_exact.py with imi's int8 cuts and fp16 cache applied at the same
-  points (exact.brain(cut=True)): what remains is fp32 rounding, ~1e-6; without the cuts the gap is the cut error
-  itself (a few per cent on random weights), and the greedy choice agrees
+  points (exact.brain(cut=True)), the cuts teacher-forced: the float64 model takes the engine's own int8 codes and
+  fp16 keys and values after checking each as a rounding of its own float64 value (so a code the two arithmetics
+  round apart, an fp32 value within rounding of a boundary, cannot move the positions after it). What remains is
+  fp32 rounding, ~1e-6, for any model seed; without the cuts the gap is the cut error itself (a few per cent on
+  random weights), and the greedy choice agrees
 - the voice generator against imi/ref/gen_exact.py restated (no input cut: ~1e-6)
 - invariants the reference states: results independent of thread count (imi/core/team.h, seoul.cpp:370-379),
   step2 == two steps (seoul.cpp:222-224), step_batch == n steps, reset, context full (seoul.cpp:353)
@@ -20,25 +23,68 @@ def _same(a, b):
     return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
 
 
+def forced_run(path, tokens=None, embd=None, threads=3):
+    """The oracle's single steps over a sequence with its cut trace on, and the float64 model teacher-forced with
+    those cuts: (hidden [T][E], scores [T][V]) of each, and the number of forced codes that differ from the float64
+    values' own rounding."""
+    n = len(tokens) if tokens is not None else len(embd)
+    e = oracle.Engine(path, threads=threads, n_ctx=max(32, n))
+    e.trace_cuts(True)
+    hs, ls = [], []
+    for i in range(n):
+        h, lg = e.step(int(tokens[i]) if tokens is not None else -1, None if embd is None else embd[i])
+        hs.append(h)
+        ls.append(lg)
+    n_attn = sum(1 for il in range(e.n_layer) if _is_attn(path, il))
+    forced = {"cuts": e.take_cuts(), "kv": {ai: e.kv_cache(ai) for ai in range(n_attn)}}
+    hid_c, lg_c = exact.brain(path, tokens=tokens, embd=embd, cut=True, forced=forced)
+    return np.array(hs), np.array(ls), hid_c, lg_c, forced["flips"]
+
+
+def _is_attn(path, il):
+    from nunchi_amd.gguf import GGUFFile
+    return f"blk.{il}.attn_q.weight" in GGUFFile(path).tensors
+
+
 def test_engine_vs_float64_truth(tiny_model):
-    toks = [5, 17, 300, 999, 0, 42, 42, 7]
-    hid_c, lg_c = exact.brain(tiny_model, tokens=toks, cut=True)
+    toks = [5, 17, 300, 999, 0, 42, 42, 7, 640, 77, 3, 500]
+    hs, ls, hid_c, lg_c, _ = forced_run(tiny_model, tokens=toks)
     hid_x, lg_x = exact.brain(tiny_model, tokens=toks, cut=False)
-    e = oracle.Engine(tiny_model, threads=3, n_ctx=32)
-    for i, t in enumerate(toks):
-        h, lg = e.step(t)
-        assert rel(h, hid_c[i]) < 5e-6 and rel(lg, lg_c[i]) < 5e-6
-        assert rel(h, hid_x[i]) < 0.15
-        assert oracle.top(lg) == int(np.argmax(lg_c[i]))
+    for i in range(len(toks)):
+        assert rel(hs[i], hid_c[i]) < 5e-6 and rel(ls[i], lg_c[i]) < 5e-6, i
+        assert rel(hs[i], hid_x[i]) < 0.15
+        assert oracle.top(ls[i]) == int(np.argmax(lg_c[i]))
 
 
 def test_engine_embedding_input_vs_truth(tiny_model):
-    e = oracle.Engine(tiny_model, threads=2, n_ctx=16)
-    emb = np.random.default_rng(3).standard_normal((4, e.n_embd)).astype(np.float32)
-    hid_c, lg_c = exact.brain(tiny_model, embd=emb, cut=True)
-    for i in range(4):
-        h, lg = e.step(-1, emb[i])
-        assert rel(h, hid_c[i]) < 5e-6 and rel(lg, lg_c[i]) < 5e-6
+    emb = np.random.default_rng(3).standard_normal((6, 256)).astype(np.float32)
+    hs, ls, hid_c, lg_c, _ = forced_run(tiny_model, embd=emb)
+    for i in range(len(emb)):
+        assert rel(hs[i], hid_c[i]) < 5e-6 and rel(ls[i], lg_c[i]) < 5e-6, i
+
+
+def test_forced_cuts_are_checked():
+    """The teacher-forced cut takes only codes that round the float64 values: a code off by one away from a
+    rounding boundary, or an fp16 key one ulp off, is refused."""
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((3, 64))
+    d = np.abs(x.astype(np.float32)).reshape(3, 2, 32).max(-1, keepdims=True) / np.float32(127)
+    own = np.rint(x.reshape(3, 2, 32) / d.astype(np.float64)).astype(np.int8).reshape(3, 64)
+    out, flips = exact.forced_cut(x, own)
+    assert flips == 0 and np.abs(out - x).max() <= 0.51 * float(d.max())
+    r = (x.reshape(3, 2, 32) / d.astype(np.float64)).reshape(3, 64)
+    j = int(np.argmax(np.abs(np.abs(r - np.rint(r)) - 0.5)))   # the value farthest from a boundary
+    bad = own.copy()
+    bad.flat[j] += 1 if bad.flat[j] < 127 else -1
+    with pytest.raises(AssertionError):
+        exact.forced_cut(x, bad)
+    k = rng.standard_normal((2, 4, 64))
+    h = k.astype(np.float16)
+    assert np.array_equal(exact.forced_half(k, h.view(np.uint16)), h.astype(np.float64))
+    off = h.copy()
+    off[1, 2, 5] = np.nextafter(off[1, 2, 5], np.float16(np.inf))
+    with pytest.raises(AssertionError):
+        exact.forced_half(k, off.view(np.uint16))
 
 
 def test_voice_pass_vs_truth(tiny_voice):
@@ -114,20 +160,16 @@ def test_reset_and_context_full(tiny_model):
     assert all(_same(x, y) for x, y in zip(first, again))
 
 
-def test_engine_q4_1_tables_vs_float64_truth(model_dir):
-    """Every layer table Q4_1: the restatement against the float64 model with the cuts applied. (Over longer runs an
-    int8 code eventually lands on the other side of a rounding boundary in one of the two arithmetics and the
-    positions after it differ at the cut's own scale, ~1e-3, for Q4_0 and Q4_1 models alike; these five positions
-    have no such flip, and a wrong m term would show at the first.)"""
+@pytest.mark.parametrize("seed", [41, 1, 2])
+def test_engine_q4_1_tables_vs_float64_truth(model_dir, seed):
+    """Every layer table Q4_1: the restatement against the float64 model with the cuts applied (teacher-forced); a
+    wrong m term would show at the first position."""
     from nunchi_amd import synth
     shape = synth.BrainShape(**{**synth.TINY.__dict__, "layer_type": "q4_1"})
-    path = synth.cached("brain", shape, 41, model_dir)
-    toks = [5, 17, 300, 999, 0]
-    hid_c, lg_c = exact.brain(path, tokens=toks, cut=True)
-    e = oracle.Engine(path, threads=3, n_ctx=32)
-    for i, t in enumerate(toks):
-        h, lg = e.step(t)
-        assert rel(h, hid_c[i]) < 5e-6 and rel(lg, lg_c[i]) < 5e-6
+    path = synth.cached("brain", shape, seed, model_dir)
+    hs, ls, hid_c, lg_c, _ = forced_run(path, tokens=FEATURE_TOKENS)
+    for i in range(len(FEATURE_TOKENS)):
+        assert rel(hs[i], hid_c[i]) < 5e-6 and rel(ls[i], lg_c[i]) < 5e-6, i
 
 
 def _feature_shape(**kw):
@@ -147,50 +189,41 @@ FEATURES = {
     # multiple of 8, as imi's table build requires)
     "head_dim_128": dict(n_head=8, n_head_kv=2, head_dim=128),
 }
-FEATURE_TOKENS = [5, 17, 300, 999, 0, 42, 640, 77]
-# model seeds whose 8 positions have no int8 code landing within fp32 rounding of a rounding boundary (such a code
-# differs between the two arithmetics and moves its position at the cut's own scale, ~1e-3; most seeds have one)
-FEATURE_SEEDS = {"rope_freqs": 44, "sliding_window": 44, "conv_7_taps": 47, "head_dim_128": 44}
+FEATURE_TOKENS = [5, 17, 300, 999, 0, 42, 640, 77, 3, 500, 12, 801]
 
 
+@pytest.mark.parametrize("seed", [1, 2, 3])
 @pytest.mark.parametrize("feature", sorted(FEATURES))
-def test_engine_feature_paths_vs_float64_truth(model_dir, feature):
-    """The oracle's loader-feature paths against the float64 restatement with the cuts applied, position by
-    position past the window (8 positions, window 3), at the bound the Q4_0 and Q4_1 checks use.
-
-    With head_dim 128 the 1024 attention outputs per position are cut to int8 at every attention layer, and now and
-    then one of them lies within fp32 rounding of a rounding boundary, so that one code differs between the two
-    arithmetics and the position moves at the cut's own scale (~1e-3). There the bound is: every position within
-    2e-2 and at least 6 of the 8 within 5e-6. A wrong score scale, rope pairing or head grouping would move every
-    position from the second on (position 0 attends to itself alone, at angle 0), so it cannot pass."""
+def test_engine_feature_paths_vs_float64_truth(model_dir, feature, seed):
+    """The oracle's loader-feature paths against the float64 restatement with the cuts applied (teacher-forced),
+    position by position past the window (12 positions, window 3), every position within 5e-6 for every model seed.
+    A wrong score scale, rope pairing or head grouping would move every position from the second on (position 0
+    attends to itself alone, at angle 0)."""
     from nunchi_amd import synth
-    path = synth.cached("brain", _feature_shape(**FEATURES[feature]), FEATURE_SEEDS[feature], model_dir)
-    hid_c, lg_c = exact.brain(path, tokens=FEATURE_TOKENS, cut=True)
-    e = oracle.Engine(path, threads=3, n_ctx=32)
-    errs = []
-    for i, t in enumerate(FEATURE_TOKENS):
-        h, lg = e.step(t)
-        errs.append(max(rel(h, hid_c[i]), rel(lg, lg_c[i])))
-    if feature == "head_dim_128":
-        assert max(errs) < 2e-2 and sum(x < 5e-6 for x in errs) >= 6, errs
-    else:
-        assert max(errs) < 5e-6, errs
+    path = synth.cached("brain", _feature_shape(**FEATURES[feature]), seed, model_dir)
+    hs, ls, hid_c, lg_c, _ = forced_run(path, tokens=FEATURE_TOKENS)
+    errs = [max(rel(hs[i], hid_c[i]), rel(ls[i], lg_c[i])) for i in range(len(FEATURE_TOKENS))]
+    assert max(errs) < 5e-6, errs
 
 
 @pytest.mark.parametrize("dropped", ["sliding_window", "rope_freqs"])
 def test_feature_pins_see_the_feature(model_dir, dropped):
     """The pins above discriminate: the oracle on the windowed model (or the one with angle divisors) against the
-    float64 truth of the same weights without the window (or the divisors) is far outside the bound once the window
-    is passed (or from the second position)."""
+    float64 truth of the same weights without the window (or the divisors), teacher-forced with the oracle's own
+    cuts, either refuses the cuts (a forced code or fp16 key is no rounding of the truth's value) or is far outside
+    the bound once the window is passed (or from the second position)."""
     from nunchi_amd import synth
     kw = FEATURES["sliding_window"]
     path = synth.cached("brain", _feature_shape(**kw), 44, model_dir)
     other = dict(kw, sliding_window=0) if dropped == "sliding_window" else dict(kw, rope_freqs=False, swa_layers=())
     path_other = synth.cached("brain", _feature_shape(**other), 44, model_dir)
-    hid_o, _ = exact.brain(path_other, tokens=FEATURE_TOKENS, cut=True)
     e = oracle.Engine(path, threads=3, n_ctx=32)
-    worst = 0.0
-    for i, t in enumerate(FEATURE_TOKENS):
-        h, _ = e.step(t)
-        worst = max(worst, rel(h, hid_o[i]))
+    e.trace_cuts(True)
+    hs = [e.step(t)[0] for t in FEATURE_TOKENS]
+    forced = {"cuts": e.take_cuts(), "kv": {ai: e.kv_cache(ai) for ai in range(2)}}
+    try:
+        hid_o, _ = exact.brain(path_other, tokens=FEATURE_TOKENS, cut=True, forced=forced)
+    except AssertionError:
+        return
+    worst = max(rel(h, hid_o[i]) for i, h in enumerate(hs))
     assert worst > 1e-3, (dropped, worst)
