@@ -22,7 +22,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-GATE_UP_TRAFFIC_BYTES = 19_275_117   # counters: 149,528 128-B + 1,478 64-B read requests + 40 KiB WRITE_SIZE per launch
+GATE_UP_TRAFFIC_BYTES = 19_302_765   # counters: 149,528 128-B + 1,525.7 64-B read requests + 64 KiB WRITE_SIZE per launch
 # matrix-core utilisation of the prefill's table products, rocprofv3's MfmaUtil per dispatch (MFMA busy cycles over
 # GUI-active cycles x SIMDs) from `rocprofv3 --pmc MfmaUtil --kernel-include-regex k_pf_ -- python3 bench.py
 # --prefill-only --prefill-reps 2`: a counter run, not measurable from inside this process
@@ -62,6 +62,11 @@ def gpu_decode(brain, steps, warmup, b2: bool):
     ids, dev = ((out[0], out[1]), out[2]) if b2 else out
     tokens = steps * (2 if b2 else 1)
     return tokens / wall, ids, dev, wall
+
+
+def _progress(msg):
+    """One line on stderr as each part of the run ends (the JSON result stays alone on stdout)."""
+    print(f"bench.py: {msg}", file=sys.stderr, flush=True)
 
 
 def real_seoul_decode(steps, warmup):
@@ -578,6 +583,7 @@ def main():
 
     tok_s_b1, ids_b1, dev_b1, wall_b1 = gpu_decode(brain, args.steps, args.warmup, b2=False)
     tok_s_b2, ids_b2, dev_b2, wall_b2 = gpu_decode(brain, args.steps, args.warmup, b2=True)
+    _progress(f"decode B=1 {tok_s_b1:.1f}, B=2 {tok_s_b2:.1f} tokens/s")
     # the dominant kernel as it runs inside the step: inputs just written by the step's previous kernel, tables from
     # HBM (16 launches per step over 32 steps)
     gu_step = brain.bench_step_kernel("ffn_gate_up", n_in=1, steps=32)
@@ -601,6 +607,7 @@ def main():
     ws6_2 = q6_brain.bench_kernel("word_scores", n_in=2, reps=8)
     del q6_brain
 
+    _progress("per-table kernels timed")
     # cfg 0: one Q4_0 x fp32 GEMV 8192 x 2048 with imi/kernels/q4x8 semantics, 64 distinct weight copies in rotation
     ctx = brain.ctx
     copies = [nunchi_amd.Q4Table(ctx, synth.q4_0_random(np.random.default_rng(100 + i), 8192, 2048), 8192, 2048) for i in range(64)]
@@ -712,8 +719,10 @@ def main():
                                     "floor": cfg0_floor},
         },
     }
+    _progress("cfg 0 and cfg 1 timed")
     if args.real_steps:
         line["real_seoul_decode"] = real_seoul_decode(args.real_steps, args.warmup)
+        _progress("Seoul file shape decode timed")
     if args.prefill_reps:
         pt, plg, pbest = gpu_prefill(brain, args.prefill_reps)
         n_pf = HEAR_EMB + HEAR_TOK
@@ -733,6 +742,7 @@ def main():
             "mfma_util_source": "counter run (not this process): profiles/prefill_hearing_window_seoul.md",
             "reps": int(len(pt)),
         }
+    _progress("prefill timed")
     if args.hear_reps:
         epath = synth.cached("ears", synth.EARS, 3)
         te, tp, hrows, hlg, hbest, einfo = gpu_hear(brain, epath, args.hear_reps)
@@ -754,6 +764,7 @@ def main():
             "ears_table_bytes": int(einfo.table_bytes),
             "reps": int(len(te)),
         }
+    _progress("hearing from sound timed")
     if args.voice_frames:
         vpath = synth.cached("voice", synth.VOICE, 1)
         (ft, fbr, fvo, fcodes, fids, _), fref, vinfo = gpu_voice_frames(path, vpath, args.voice_frames, VOICE_WARMUP)
@@ -790,6 +801,7 @@ def main():
             "hbm_frac_at_p50": round(frame_b / p50 / 1e9 / HBM_PEAK_GBS, 4),
             "budget_ms": 80.0,
         }
+    _progress("voice frames timed")
     if args.talk_frames:
         tpath = synth.cached("voice", synth.TALK_VOICE, 1)
         cpath = synth.cached("codec", synth.CODEC, 2)
@@ -812,6 +824,7 @@ def main():
             "codec_table_bytes": tinfo["codec_table_bytes"],
             "audio_ms_per_frame": 80.0,
         }
+    _progress("talk frames timed")
     if not args.no_cpu:
         info = cpu_info()
         aff = info["logical_cpus"]

@@ -1052,6 +1052,30 @@ int sh_bench_tables(sh_ctx* c, int ncol, int reps, double* ms_per_pass, double* 
 
 // The step's own kernel for one table kind, launched with a real layer's arguments, rotating over the layers so
 // successive launches read different tables (more than the 256 MB MALL in total); each launch timed by itself.
+// bytes one FFN launch moves for M conversations: the table once, the fp32 vectors it reads and writes, and, when
+// gate|up cuts the activation for down (pre-cut), the int8 codes and per-32 (d, s) pairs gate|up writes and down
+// reads in place of the activation's floats
+static double ffn_launch_bytes(const sh_ctx* c, const layer_dev& L, int kind, int M, bool precut) {
+    const double E = c->info.n_embd, F = c->info.n_ff, cut = M * (F + 8.0 * (F / 32));
+    if (kind == 0) return (double)L.gate_up.rows * L.gate_up.nb * 18 + 4.0 * M * (2 * E + F) + (precut ? cut : 0.0);
+    return (double)L.down.rows * L.down.nb * 18 + 4.0 * M * E + (precut ? cut : 4.0 * M * F);
+}
+
+// whether the step runs layer L's FFN with the pre-cut (as enqueue_step decides)
+static bool ffn_precut(const sh_ctx* c, const layer_dev& L, int M) {
+    if (!c->use_precut) return false;
+    gemv_args f{}, d{};
+    f.E = c->info.n_embd;
+    f.x_in = c->xbuf[0];
+    f.y_in = c->y;
+    f.w_post = L.post_attn_norm;
+    f.W = L.gate_up;
+    f.units = L.gate_up.rows / 16;
+    f.out_ld = c->info.n_ff;
+    d.W = L.down;
+    return swiglu_cut_takes(M, f, d);
+}
+
 int sh_bench_kernel(sh_ctx* c, int kind, int M, int reps, double* avg_us, double* bytes_per_launch) {
     if (!c || !c->loaded) return fail(SH_E_STATE, "sh_bench_kernel: no model loaded");
     if (M < 1 || M > 2 || reps < 1 || kind < 0 || kind > 2) return fail(SH_E_ARG, "sh_bench_kernel: bad argument");
@@ -1082,8 +1106,15 @@ int sh_bench_kernel(sh_ctx* c, int kind, int M, int reps, double* avg_us, double
                 a.out = c->act;
                 a.out_ld = I.n_ff;
                 pro = PRO_RESID_NORM; epi = EPI_SWIGLU;
-                bytes += (double)L.gate_up.rows * L.gate_up.nb * 18 + 4.0 * M * (2 * E + I.n_ff);
-            } else if (kind == 1) {   // FFN down, input cut in the prologue
+                const bool pc = ffn_precut(c, L, M);
+                if (pc) {   // as in the step: the activation cut for down in the epilogue
+                    a.upw = 4;
+                    a.outq = c->act_q;
+                    a.outd = c->act_d;
+                    a.outs = c->act_s;
+                }
+                bytes += ffn_launch_bytes(c, L, 0, M, pc);
+            } else if (kind == 1) {   // FFN down: input cut in the prologue, or taken as gate|up cut it
                 a.W = L.down;
                 a.units = L.down.rows / 8;
                 a.src = c->act;
@@ -1091,7 +1122,14 @@ int sh_bench_kernel(sh_ctx* c, int kind, int M, int reps, double* avg_us, double
                 a.out = c->fo;
                 a.out_ld = E;
                 pro = PRO_CUT; epi = EPI_STORE;
-                bytes += (double)L.down.rows * L.down.nb * 18 + 4.0 * M * (I.n_ff + E);
+                const bool pc = ffn_precut(c, L, M);
+                if (pc) {
+                    a.src_q = c->act_q;
+                    a.src_d = c->act_d;
+                    a.src_s = c->act_s;
+                    pro = PRO_PRECUT;
+                }
+                bytes += ffn_launch_bytes(c, L, 1, M, pc);
             } else {                  // word scores over the tied table
                 a.x_in = c->xbuf[0];
                 a.y_in = c->fo;
@@ -1188,10 +1226,8 @@ int sh_bench_step_kernel(sh_ctx* c, int kind, int M, int steps, double* avg_us, 
         ms += x;
     }
     double bytes = 0;
-    for (const layer_dev& L : c->layers) {
-        if (kind == 0) bytes += (double)L.gate_up.rows * L.gate_up.nb * 18 + 4.0 * M * (2 * I.n_embd + I.n_ff);
-        else if (kind == 1) bytes += (double)L.down.rows * L.down.nb * 18 + 4.0 * M * (I.n_ff + I.n_embd);
-    }
+    for (const layer_dev& L : c->layers)
+        if (kind != 2) bytes += ffn_launch_bytes(c, L, kind, M, ffn_precut(c, L, M));
     if (kind == 2) bytes = (double)c->vocab.rows * c->vocab.nb * 18 + 4.0 * M * (2 * I.n_embd + I.n_vocab);
     else bytes /= (double)c->layers.size();
     if (avg_us) *avg_us = n ? ms * 1e3 / n : 0.0;
