@@ -540,8 +540,10 @@ __device__ __forceinline__ f32x4 embed_quad(const gemv_args& a, int m, int t, in
     return f32x4{v[0], v[1], v[2], v[3]};
 }
 
-// HM: Q4_1 table, as k_gemv_cut. EMB: the layer-0 form, whose input is the embedding row (no residual to add)
-template <int M, int EPI, int UG, bool HM = false, bool EMB = false>
+// HM: Q4_1 table, as k_gemv_cut. EMB: the layer-0 form, whose input is the embedding row (no residual to add).
+// RPT: rows per thread when the launch fixes it (8: a chunk of at least 5 groups of 64 blocks; the row and scale
+// indices are then compile-time), 0 = from the chunk's shape
+template <int M, int EPI, int UG, bool HM = false, bool EMB = false, int RPT = 0>
 __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
     extern __shared__ __align__(16) float lds[];
     const int E = a.E, nb = a.W.nb, st = ((nb + 3) & ~3) + 4;
@@ -563,7 +565,7 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
 
     const int gtot = a.W.rows / 8, nchunk = (a.units + upw - 1) / upw;
     // this thread's share of a chunk's weights: rows sub * rpt .. + rpt - 1 of group gi, block jw
-    const int np = G * nb, rpt = np <= 64 ? 1 : np <= 128 ? 2 : np <= 256 ? 4 : 8;
+    const int np = G * nb, rpt = RPT ? RPT : np <= 64 ? 1 : np <= 128 ? 2 : np <= 256 ? 4 : 8;
     const bool wt = t < np * (8 / rpt);
     const int sub = t / np, pr = t - sub * np, gi = pr / nb, jw = pr - gi * nb;
     u32x4 w[HM ? 10 : 9];
@@ -670,12 +672,10 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
 #pragma unroll
         for (int m = 0; m < M; m++) asm volatile("" ::"v"(xv[m].x));
         asm volatile("" ::"v"(wp.x), "v"(wq.x), "v"((unsigned)etab));
-        if (EPI == EPI_LOGITS) {
-            load_rows(k < nchunk ? k : nchunk - 1, kEarlyRows, 8);
-            load_to(w2, k + (int)gridDim.x);
-        } else {
-            load_own_rows(k < nchunk ? k : nchunk - 1, kEarlyRows);
-        }
+        // (the word scores request the rest of their first two chunks after the prologue: a wave cannot issue loads
+        // faster than the compute unit's earlier requests drain, so 14 loads per thread ahead of the prologue's
+        // barriers held every barrier until about 100 KB had arrived, 2.7 us)
+        if (EPI != EPI_LOGITS) load_own_rows(k < nchunk ? k : nchunk - 1, kEarlyRows);
         if ((t >> 6) < M) {
             const float sc = rms_xt(l_v + (t >> 6) * 32 * XLD, E, a.eps);
             if ((t & 63) == 0) l_sc[t >> 6] = sc;
@@ -740,12 +740,17 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
         }
     }
     __syncthreads();
+    if (EPI == EPI_LOGITS) {
+        load_rows(k < nchunk ? k : nchunk - 1, kEarlyRows, 8);
+        load_to(w2, k + (int)gridDim.x);
+    }
 
     float best_v[M];
     int best_i[M];
 #pragma unroll
     for (int m = 0; m < M; m++) { best_v[m] = -INFINITY; best_i[m] = 0x7fffffff; }
-    auto chunk = [&](u32x4 (&w)[HM ? 10 : 9], const int k, const int ci) {
+    // pf: the word scores request chunk k + 2 grid into this chunk's registers once its dots are done
+    auto chunk = [&](u32x4 (&w)[HM ? 10 : 9], const int k, const int ci, const bool pf) {
         const int u0 = k * upw, g0 = k * G, gv = min(G, gtot - g0);   // groups of this chunk that exist
         // ---- dots: exact integer sums of this thread's rows, chain operands to LDS ----
         if (wt && gi < gv) {
@@ -777,7 +782,7 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
         }
         if (EPI == EPI_SWIGLU && t < 32) l_exp[t] = etab;
         __syncthreads();
-        if (EPI == EPI_LOGITS) load_to(w, k + 2 * (int)gridDim.x);   // in flight during this and the next chunk
+        if (EPI == EPI_LOGITS && pf) load_to(w, k + 2 * (int)gridDim.x);   // in flight during this and the next chunk
         // ---- chains ----
         const bool acc_lane = t < C, cor_lane = t >= 256 && t - 256 < C;
         float chain = 0.0f;
@@ -890,17 +895,28 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
     };
     if (EPI == EPI_LOGITS) {   // chunks k, k + grid, ... alternating between the two register sets
         int ci = 0;
-        if (k < nchunk) {   // (the first chunk ahead of the loop, so the loop's two halves start alike)
-            chunk(w, k, ci++);
+        // the first six chunks straight-line (a word table of 97,496 rows gives a workgroup at most six): inside a
+        // loop the compiler waits for every load at the first use of a chunk's registers, the next chunk's included.
+        // The last two request nothing (a request past the table would be a stand-in load that the kernel's end
+        // waits for)
+#pragma unroll
+        for (int it = 0; it < 6; it++) {
+            if (k >= nchunk) break;
+            if (it & 1) chunk(w2, k, ci++, it < 4);
+            else chunk(w, k, ci++, it < 4);
             k += gridDim.x;
         }
-        for (;;) {
-            if (k >= nchunk) break;
-            chunk(w2, k, ci++);
-            k += gridDim.x;
-            if (k >= nchunk) break;
-            chunk(w, k, ci++);
-            k += gridDim.x;
+        if (k < nchunk) {   // (larger tables: the rest in a loop, two chunks in flight again)
+            load_to(w, k);
+            load_to(w2, k + (int)gridDim.x);
+            for (;;) {
+                if (k >= nchunk) break;
+                chunk(w, k, ci++, true);
+                k += gridDim.x;
+                if (k >= nchunk) break;
+                chunk(w2, k, ci++, true);
+                k += gridDim.x;
+            }
         }
         // the scores kept in LDS (stores in the loop would leave the compiler unable to wait for just the older chunk)
         if (a.out && t < C) {
@@ -911,7 +927,7 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
             }
         }
     } else if (k < nchunk) {   // (every other table: one chunk per workgroup)
-        chunk(w, k, 0);
+        chunk(w, k, 0, false);
     }
     if (late_stores && blockIdx.x == 0 && t < nq)
 #pragma unroll
@@ -1821,7 +1837,16 @@ hipError_t launch_gemv(int M, int pro, int epi, int grid, const gemv_args& a, hi
             SH_EMB_FN(1, EPI_STORE, 1) SH_EMB_FN(1, EPI_CONV, 3) SH_EMB_FN(2, EPI_STORE, 1) SH_EMB_FN(2, EPI_CONV, 3)
 #undef SH_EMB_FN
         } else {
-#define SH_NORM_FN(M_, EPI_, UG_) if (M == M_ && epi == EPI_) fn = hm ? (const void*)k_gemv_norm<M_, EPI_, UG_, true> : (const void*)k_gemv_norm<M_, EPI_, UG_>;
+            // the rows per thread the chunk gives (as the kernel derives them); the shapes the decode step runs take
+            // a kernel with them fixed at compile time (row and scale indices then static, no per-row branches)
+            const int np = b.upw * ug * a.W.nb, rptv = np <= 64 ? 1 : np <= 128 ? 2 : np <= 256 ? 4 : 8;
+#define SH_NORM_R(M_, EPI_, UG_, R_) if (!fn && !hm && M == M_ && epi == EPI_ && rptv == R_ && np <= 512) fn = (const void*)k_gemv_norm<M_, EPI_, UG_, false, false, R_>;
+            SH_NORM_R(1, EPI_STORE, 1, 2) SH_NORM_R(1, EPI_STORE, 1, 8) SH_NORM_R(1, EPI_SWIGLU, 2, 8) SH_NORM_R(1, EPI_CONV, 3, 4)
+            SH_NORM_R(1, EPI_CONV, 3, 8) SH_NORM_R(1, EPI_LOGITS, 1, 8)
+            SH_NORM_R(2, EPI_STORE, 1, 2) SH_NORM_R(2, EPI_STORE, 1, 8) SH_NORM_R(2, EPI_SWIGLU, 2, 8) SH_NORM_R(2, EPI_CONV, 3, 4)
+            SH_NORM_R(2, EPI_CONV, 3, 8) SH_NORM_R(2, EPI_LOGITS, 1, 8)
+#undef SH_NORM_R
+#define SH_NORM_FN(M_, EPI_, UG_) if (!fn && M == M_ && epi == EPI_) fn = hm ? (const void*)k_gemv_norm<M_, EPI_, UG_, true> : (const void*)k_gemv_norm<M_, EPI_, UG_>;
             SH_NORM_FN(1, EPI_STORE, 1) SH_NORM_FN(1, EPI_SWIGLU, 2) SH_NORM_FN(1, EPI_CONV, 3) SH_NORM_FN(1, EPI_LOGITS, 1)
             SH_NORM_FN(2, EPI_STORE, 1) SH_NORM_FN(2, EPI_SWIGLU, 2) SH_NORM_FN(2, EPI_CONV, 3) SH_NORM_FN(2, EPI_LOGITS, 1)
 #undef SH_NORM_FN
