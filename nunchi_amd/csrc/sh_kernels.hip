@@ -1465,24 +1465,35 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
             for (int i = 0; i < KW; i++) ka[i] = ((const SH_GLOBAL u32x4*)(kc + (size_t)(s0 + min(p, last)) * D))[i];
         }
         if (D > 64) {   // dot_h's 8 chains over columns i % 8, a word (8 columns) at a time
+            // (q read from LDS in the loop, and the position's own key row (from LDS) and the cache rows (converted
+            // from the registers) in two loops: with one loop holding both, all 128 key values were converted ahead of
+            // the products and the kernel went past 256 registers into scratch)
+            asm volatile("" ::: "memory");
             float acc[8];
 #pragma unroll
             for (int l = 0; l < 8; l++) acc[l] = 0.0f;
+            if (p == nk - 1) {
 #pragma unroll
-            for (int i = 0; i < KW; i++) {
-                const f32x4 qa = *(const f32x4*)(q_s + 8 * i), qb = *(const f32x4*)(q_s + 8 * i + 4);
-                const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-                float kv[8];
-                if (p == nk - 1) {
+                for (int i = 0; i < KW; i++) {
+                    const f32x4 qa = *(const f32x4*)(q_s + 8 * i), qb = *(const f32x4*)(q_s + 8 * i + 4);
                     const f32x4 ka4 = *(const f32x4*)(k_s + 8 * i), kb4 = *(const f32x4*)(k_s + 8 * i + 4);
-                    kv[0] = ka4.x; kv[1] = ka4.y; kv[2] = ka4.z; kv[3] = ka4.w; kv[4] = kb4.x; kv[5] = kb4.y; kv[6] = kb4.z; kv[7] = kb4.w;
-                } else {
+                    const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+                    const float kv[8] = {ka4.x, ka4.y, ka4.z, ka4.w, kb4.x, kb4.y, kb4.z, kb4.w};
+#pragma unroll
+                    for (int l = 0; l < 8; l++) acc[l] = fmaf(qv[l], kv[l], acc[l]);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < KW; i++) {
+                    const f32x4 qa = *(const f32x4*)(q_s + 8 * i), qb = *(const f32x4*)(q_s + 8 * i + 4);
+                    const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
                     const unsigned w4[4] = {ka[i].x, ka[i].y, ka[i].z, ka[i].w};
+                    float kv[8];
 #pragma unroll
                     for (int e = 0; e < 8; e++) kv[e] = h2f((uint16_t)((w4[e >> 1] >> (16 * (e & 1))) & 0xFFFFu));
-                }
 #pragma unroll
-                for (int l = 0; l < 8; l++) acc[l] = fmaf(qv[l], kv[l], acc[l]);
+                    for (int l = 0; l < 8; l++) acc[l] = fmaf(qv[l], kv[l], acc[l]);
+                }
             }
             sc[p] = (((acc[0] + acc[4]) + (acc[2] + acc[6])) + ((acc[1] + acc[5]) + (acc[3] + acc[7]))) * scale;
             continue;
