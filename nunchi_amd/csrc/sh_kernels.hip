@@ -672,10 +672,12 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
 #pragma unroll
         for (int m = 0; m < M; m++) asm volatile("" ::"v"(xv[m].x));
         asm volatile("" ::"v"(wp.x), "v"(wq.x), "v"((unsigned)etab));
-        // (the word scores request the rest of their first two chunks after the prologue: a wave cannot issue loads
-        // faster than the compute unit's earlier requests drain, so 14 loads per thread ahead of the prologue's
-        // barriers held every barrier until about 100 KB had arrived, 2.7 us)
+        // (the word scores request the rest of their first chunk two rows at a time between the prologue's barriers
+        // and their second chunk after the prologue: a wave cannot issue loads faster than the compute unit's earlier
+        // requests drain, so 14 loads per thread ahead of the prologue's barriers held every barrier until about
+        // 100 KB had arrived, 2.7 us, while two rows per phase drain within it)
         if (EPI != EPI_LOGITS) load_own_rows(k < nchunk ? k : nchunk - 1, kEarlyRows);
+        else load_rows(k < nchunk ? k : nchunk - 1, kEarlyRows, 6);
         if ((t >> 6) < M) {
             const float sc = rms_xt(l_v + (t >> 6) * 32 * XLD, E, a.eps);
             if ((t & 63) == 0) l_sc[t >> 6] = sc;
@@ -695,6 +697,7 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
     // and the dots would make the compiler wait for every load there, the next chunk's included)
     constexpr bool late_stores = EPI == EPI_LOGITS;
     f32x4 hsave[late_stores ? M : 1];
+    if (EPI == EPI_LOGITS) load_rows(k < nchunk ? k : nchunk - 1, 6, 8);
     if (t < nq)
 #pragma unroll
         for (int m = 0; m < M; m++) {
@@ -740,10 +743,7 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
         }
     }
     __syncthreads();
-    if (EPI == EPI_LOGITS) {
-        load_rows(k < nchunk ? k : nchunk - 1, kEarlyRows, 8);
-        load_to(w2, k + (int)gridDim.x);
-    }
+    if (EPI == EPI_LOGITS) load_to(w2, k + (int)gridDim.x);
 
     float best_v[M];
     int best_i[M];
