@@ -826,6 +826,11 @@ def main():
         }
     _progress("talk frames timed")
     if not args.no_cpu:
+        import oracle
+        # the CPU path built for this host (-O3 -march=native; the portable x86-64-v3 build if that fails)
+        native = oracle.use_native()
+        cpu_build = "-O3 -march=native on this host" if native else "-O3 -march=x86-64-v3 (portable build)"
+        _progress(f"CPU path built: {cpu_build}")
         info = cpu_info()
         aff = info["logical_cpus"]
         threads = args.cpu_threads or min(16, aff)
@@ -844,7 +849,8 @@ def main():
                       f"{c2:.2f} tokens/s; 4 threads (imi's README setting): one conversation, {c4:.2f} tokens/s "
                       f"({csecs4:.1f} s); {threads} threads of {aff} logical CPUs in the affinity mask "
                       f"({info['physical_cores']} physical cores, SMT width {info['smt_width']}), {info['model']}; "
-                      "oracle/ C++ restatement of imi's AVX2 engine, x86-64-v3, imi's spinning thread team",
+                      f"oracle/ C++ restatement of imi's AVX2 engine, {cpu_build}, imi's spinning thread team",
+            "build": cpu_build,
             "b2_value": round(c2, 2),
             "four_thread_value": round(c4, 2),
             "cpu": info,

@@ -29,6 +29,25 @@ def build(force: bool = False) -> str:
     return LIB_PATH
 
 
+NATIVE_PATH = os.path.join(HERE, "_native", "liboracle.so")
+
+
+def use_native(timeout: float = 240.0) -> bool:
+    """Build the oracle for this host's CPU (oracle/Makefile `native`: -O3 -march=native, the same sources and flags
+    otherwise) and load that library from now on: for timing the CPU path (every fma is written out and no reduction
+    is reordered, so its numbers are the portable build's). False, keeping the portable library, if the build fails or
+    a library is already loaded."""
+    global LIB_PATH
+    if _lib is not None:
+        return LIB_PATH == NATIVE_PATH
+    try:
+        subprocess.run(["make", "-s", "-C", HERE, "native"], check=True, timeout=timeout, capture_output=True)
+    except (subprocess.SubprocessError, OSError):
+        return False
+    LIB_PATH = NATIVE_PATH
+    return True
+
+
 def lib():
     global _lib
     if _lib is not None:
