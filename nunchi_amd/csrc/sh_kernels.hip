@@ -691,7 +691,7 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
             xv[m].z = fmaf(yv[m].z * sc, wp.z, xv[m].z);
             xv[m].w = fmaf(yv[m].w * sc, wp.w, xv[m].w);
         }
-        __syncthreads();
+        // (no barrier before x overwrites y in LDS: y's only reader, the first norm, finished before the barrier above)
     }
     // (the word scores store x and the hidden state after their chunk loop: a store pending between the weight loads
     // and the dots would make the compiler wait for every load there, the next chunk's included)
