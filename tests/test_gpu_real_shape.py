@@ -77,3 +77,21 @@ def test_real_step2(engines):
         assert same(ha, hoa) and same(hb, hob) and same(la, loa), i
         if i % 2 == 0:
             assert same(lb, lob), i
+
+
+def test_real_shape_down_cut_in_its_own_prologue(real_model, monkeypatch):
+    """SEOUL_HIP_PRECUT=0: the 240-block down table cuts its input in its own prologue (the 256-block cut body with the
+    runtime block count) instead of taking gate|up's cut; the same numbers bit for bit."""
+    import nunchi_amd
+    import oracle
+    path, shape = real_model
+    monkeypatch.setenv("SEOUL_HIP_PRECUT", "0")   # read when the context is created
+    g = nunchi_amd.Brain(path, n_ctx=64)
+    o = oracle.Engine(path, threads=16, n_ctx=64)
+    for i, t in enumerate(_prompt(6, shape.n_vocab, 56)):
+        hg, lg, bg = g.step(int(t))
+        ho, lo = o.step(int(t))
+        assert same(hg, ho) and same(lg, lo), i
+    ids_g, _ = g.generate(bg, 16)
+    ids_o, _ = o.greedy(bg, 16)
+    assert np.array_equal(ids_g, ids_o)
