@@ -41,9 +41,9 @@ class BrainShape:
     swa_layers: tuple = ()                        # attention layers with the window and the swa RoPE base
     rope_base_swa: float = 1e4
     layer_type: str = "q4_0"                      # layer tables: "q4_0", or "q4_1" (code * d + m)
-    vocab_edits: tuple = ()                       # Q4_0 word table edits after drawing: ("copy", src, dst) copies row
-                                                  # src over row dst (equal scores), ("nan", row) sets that row's
-                                                  # block scales to fp16 NaN (a NaN score)
+    vocab_edits: tuple = ()                       # word table edits after drawing: ("copy", src, dst) copies row src
+                                                  # over row dst (equal scores), ("nan", row) sets that row's block
+                                                  # scales (Q4_0 d, Q6_K super-block d) to fp16 NaN (a NaN score)
 
 
 SEOUL = BrainShape()
@@ -158,10 +158,12 @@ def write_brain(path: str, shape: BrainShape = SEOUL, seed: int = 0) -> str:
         w.add_tensor(name, T_F32, ne, np.ascontiguousarray(arr, dtype=np.float32))
 
     if s.vocab_type == "q6_k":
-        w.add_tensor("token_embd.weight", T_Q6_K, (E, s.n_vocab), q6_k_random(_rng(seed, "token_embd.weight"), s.n_vocab, E))
+        blk = q6_k_random(_rng(seed, "token_embd.weight"), s.n_vocab, E)
+        nb = E // 256
     else:
         blk = q4_0_random(_rng(seed, "token_embd.weight"), s.n_vocab, E)
         nb = E // 32
+    if s.vocab_edits:
         for ed in s.vocab_edits:
             if ed[0] == "copy":
                 blk[ed[2] * nb:(ed[2] + 1) * nb] = blk[ed[1] * nb:(ed[1] + 1) * nb]
@@ -169,7 +171,7 @@ def write_brain(path: str, shape: BrainShape = SEOUL, seed: int = 0) -> str:
                 blk["d"][ed[1] * nb:(ed[1] + 1) * nb] = np.float16(np.nan)
             else:
                 raise ValueError(f"unknown word-table edit {ed!r}")
-        w.add_tensor("token_embd.weight", T_Q4_0, (E, s.n_vocab), blk)
+    w.add_tensor("token_embd.weight", T_Q6_K if s.vocab_type == "q6_k" else T_Q4_0, (E, s.n_vocab), blk)
     f32("output_norm.weight", _norm_w(_rng(seed, "output_norm.weight"), E), (E,))
     if s.rope_freqs:
         ff = (1.0 + 3.0 * _rng(seed, "rope_freqs.weight").random(D // 2)).astype(np.float32)

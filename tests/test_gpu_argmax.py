@@ -1,5 +1,5 @@
 """GPU greedy pick against imi's rule (imi/core/hear.cpp:67-68: best = 0, then v replaces it only if
-logits[v] > logits[best]) on word tables edited to force the cases random scores never reach: an exact tie at the
+logits[v] > logits[best]) on word tables (Q4_0 and Q6_K) edited to force the cases random scores never reach: an exact tie at the
 maximum (rows copied, so their scores are bit-identical) between workgroups and inside one 8-row group, a NaN
 score at index 0 (imi keeps 0), and a NaN at the maximum (imi skips it). The prompt never reads an edited row, so
 the hidden states, and every score but the edited rows', are those of the unedited model. Steps run with sh_step /
@@ -14,9 +14,15 @@ pytestmark = pytest.mark.gpu
 PROMPT = [101, 202, 303, 404, 505, 606]
 
 
-def _shape(edits=()):
+def _shape(edits=(), vocab_type="q4_0"):
     from nunchi_amd import synth
-    return synth.BrainShape(n_layer=4, attn_layers=(1, 3), n_vocab=4096, vocab_edits=tuple(edits))
+    return synth.BrainShape(n_layer=4, attn_layers=(1, 3), n_vocab=4096, vocab_edits=tuple(edits), vocab_type=vocab_type)
+
+
+@pytest.fixture(scope="module", params=["q4_0", "q6_k"])
+def vocab_type(request):
+    """The word table as BASELINE's synthetic model has it (Q4_0) and as imi's engine requires it (Q6_K)."""
+    return request.param
 
 
 def _oracle_scores(path):
@@ -49,10 +55,10 @@ def _same_scores(a, b):
 
 
 @pytest.fixture(scope="module")
-def base_top(model_dir):
+def base_top(model_dir, vocab_type):
     from nunchi_amd import synth
     import oracle
-    path = synth.cached("brain", _shape(), 11, model_dir)
+    path = synth.cached("brain", _shape((), vocab_type), 11, model_dir)
     lg = _oracle_scores(path)
     r = oracle.top(lg)
     masked = lg.copy()
@@ -70,12 +76,12 @@ def _cases(r, second):
     return cases
 
 
-def test_greedy_pick_ties_and_nan(model_dir, base_top):
+def test_greedy_pick_ties_and_nan(model_dir, base_top, vocab_type):
     from nunchi_amd import synth
     import oracle
     r, second = base_top
     for name, edits, want in _cases(r, second):
-        path = synth.cached("brain", _shape(edits), 11, model_dir)
+        path = synth.cached("brain", _shape(edits, vocab_type), 11, model_dir)
         lo = _oracle_scores(path)
         assert oracle.top(lo) == want, name
         lg, best = _gpu_pick(path)
@@ -83,11 +89,11 @@ def test_greedy_pick_ties_and_nan(model_dir, base_top):
         assert best == want, (name, best, want)
 
 
-def test_greedy_pick_ties_two_conversations(model_dir, base_top):
+def test_greedy_pick_ties_two_conversations(model_dir, base_top, vocab_type):
     from nunchi_amd import synth
     r, second = base_top
     for name, edits, want in _cases(r, second)[:2]:
-        path = synth.cached("brain", _shape(edits), 11, model_dir)
+        path = synth.cached("brain", _shape(edits, vocab_type), 11, model_dir)
         la, ba, lb, bb = _gpu_pick(path, two=True)
         assert ba == want and bb == want, (name, ba, bb, want)
         assert _same_scores(la, lb)

@@ -20,7 +20,7 @@ def same(a, b) -> bool:
 
 
 @pytest.mark.parametrize("rows,cols,n", [(256, 2048, 1), (256, 2048, 2), (392, 256, 17), (2048, 8192, 64),
-                                         (512, 2048, 130), (64, 1024, 512)])
+                                         (512, 2048, 130), (64, 1024, 512), (2048, 7680, 448), (64, 4608, 17)])
 def test_gemm_matches_batch_kernel(rows, cols, n):
     """Matrix-core product vs the oracle's batch kernel (64 inputs at a time) and vs the GPU's own GEMV."""
     import nunchi_amd
