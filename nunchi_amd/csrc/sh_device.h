@@ -196,28 +196,45 @@ __device__ __forceinline__ float rms_scale_wave(Ptr x, int n, float eps) {
 // position (imi/core/seoul.cpp:19-28). One wave; lane holds dimensions lane + 64 c (c < DPL), so at D 128 a rope pair
 // (i, i + 64) sits in one lane and at D <= 64 the partner comes by a shuffle. stg: D floats of staging.
 template <int DPL, class Ptr>
-__device__ __forceinline__ void head_norm_rope(const float* src, const float* w, Ptr stg, const float2* cs, int D, float eps, float* r) {
+__device__ __forceinline__ void norm_rope_vals(const float (&x)[DPL], const float (&w)[DPL], Ptr stg, const float2 (&cz)[DPL],
+                                               int D, float eps, float* r) {
     const int lane = threadIdx.x & 63, half = D / 2;
-    float x[DPL], n[DPL];
+    float n[DPL];
 #pragma unroll
-    for (int c = 0; c < DPL; c++) {
-        const int e = lane + 64 * c;
-        x[c] = e < D ? src[e] : 0.0f;
-        if (e < D) stg[e] = x[c];
-    }
+    for (int c = 0; c < DPL; c++)
+        if (lane + 64 * c < D) stg[lane + 64 * c] = x[c];
     __builtin_amdgcn_wave_barrier();
     const float s = rms_scale_wave(stg, D, eps);
 #pragma unroll
-    for (int c = 0; c < DPL; c++) n[c] = lane + 64 * c < D ? x[c] * s * w[lane + 64 * c] : 0.0f;
+    for (int c = 0; c < DPL; c++) n[c] = lane + 64 * c < D ? x[c] * s * w[c] : 0.0f;
     const float sh = __shfl(n[0], lane < half ? lane + half : lane - half);
 #pragma unroll
     for (int c = 0; c < DPL; c++) {
         const int e = lane + 64 * c;
         const float other = DPL == 2 ? n[c ^ 1] : sh;
-        const float2 cz = cs[e < half ? e : (e < D ? e - half : 0)];
-        r[c] = e < half ? fmaf(n[c], cz.x, -(other * cz.y)) : fmaf(other, cz.y, n[c] * cz.x);
+        r[c] = e < half ? fmaf(n[c], cz[c].x, -(other * cz[c].y)) : fmaf(other, cz[c].y, n[c] * cz[c].x);
     }
     __builtin_amdgcn_wave_barrier();
+}
+// the operands of one head row: its values (0 past D), the norm weights, the rotation entries of this lane's dimensions
+template <int DPL>
+__device__ __forceinline__ void norm_rope_load(const float* src, const float* w, const float2* cs, int D, float (&x)[DPL],
+                                               float (&wv)[DPL], float2 (&cz)[DPL]) {
+    const int lane = threadIdx.x & 63, half = D / 2;
+#pragma unroll
+    for (int c = 0; c < DPL; c++) {
+        const int e = lane + 64 * c;
+        x[c] = e < D ? src[e] : 0.0f;
+        wv[c] = e < D ? w[e] : 0.0f;
+        cz[c] = cs[e < half ? e : (e < D ? e - half : 0)];
+    }
+}
+template <int DPL, class Ptr>
+__device__ __forceinline__ void head_norm_rope(const float* src, const float* w, Ptr stg, const float2* cs, int D, float eps, float* r) {
+    float x[DPL], wv[DPL];
+    float2 cz[DPL];
+    norm_rope_load<DPL>(src, w, cs, D, x, wv, cz);
+    norm_rope_vals<DPL>(x, wv, stg, cz, D, eps, r);
 }
 
 // cross-lane moves on the VALU (DPP), no LDS round trip: lane i gets lane i ^ 1, i ^ 2 (within a quad), 7 - i

@@ -6,6 +6,9 @@
 #include "sh_device.h"
 #include "sh_prefill.h"
 
+#include <algorithm>
+#include <cstdlib>
+
 namespace sh {
 namespace {
 
@@ -664,6 +667,284 @@ __global__ __launch_bounds__(256) void k_pf_attn(pf_attn_args a) {
     if (tid < nblk) cut_store(a.cut, a.n, cb0 + tid, p, o_s + 32 * tid);
 }
 
+// The same attention with its products on the matrix cores, for groups of at most 4 query heads per kv head: a
+// workgroup takes 4 consecutive positions of one kv head (the last positions, with the most keys, first), their
+// 4 x 4 (position, head) pairs being 16 rows R = 4 (position) + (head) (head slots past the group are zero and
+// dropped). The fp32 K = 1 matrix ops used round once, like fmaf, and equal the VALU's fmaf bit for bit (the prefill
+// tables run their scale chains on them).
+// Scores, v_mfma_f32_16x16x1_4b_f32 (lane l supplies row l % 16 of block l / 16 (A) and column l % 16 of block l / 16
+// (B); register 4 b + i of lane l holds block b's row 4 (l / 16) + i, column l % 16): dot_h's 8 chains (chain j over
+// dimensions j, j + 8, ...), 16 keys per tile, block b holding chain 2 b (one instruction) and 2 b + 1 (the other)
+// at each step m, so lane l takes key l % 16 and the fp16 pair at dimensions 8 m + 2 (l / 16), + 1 (the 4 lanes of a
+// key read consecutive words of its row), and every chain of a (row, key) ends in one lane: ((a0 + a4) + (a2 + a6)) +
+// ((a1 + a5) + (a3 + a7)) runs in registers. Every key of the 4 positions' union is scored; each row's softmax reads
+// its own range. Values: o = fma(a_t, V_t, o) over each position's keys in order, a wave per position (below).
+template <int D>
+__global__ __launch_bounds__(256) void k_pf_attn_mf(pf_attn_args a) {
+    typedef float v16f __attribute__((ext_vector_type(16)));
+    extern __shared__ float lds[];
+    constexpr int NM = D / 8, DPL = (D + 63) / 64, NWV = (D + 63) / 64, CH = 8, TPV = 64, VPT = TPV * D / 8 / 256;
+    constexpr int KR = D > 64 ? 2 : 4;   // key tiles in flight per wave
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6), g = blockIdx.y;
+    const int grp = a.n_head / a.n_kv, Hq = a.n_head * D, kvd = a.n_kv * D;
+    // the longest key ranges (last positions) first
+    const int p0 = 4 * ((int)gridDim.x - 1 - (int)blockIdx.x), plast = min(p0 + 3, a.n - 1);
+    auto win0 = [&](int at) { return a.n_swa > 0 ? max(0, at - a.n_swa + 1) : 0; };
+    // (score rows 4 floats past a multiple of 32 apart: a wave's 4 rows of one key in distinct LDS banks)
+    const int sU = win0(a.pos0 + p0), nkU = a.pos0 + plast - sU + 1, ldk = ((nkU + 31) & ~31) + 4;
+    const uint16_t* kc = a.kc + ((size_t)g * a.n_ctx + sU) * D;
+    const uint16_t* vc = a.vc + ((size_t)g * a.n_ctx + sU) * D;
+    uint64_t* etab = (uint64_t*)lds;   // expf's table (a copy in LDS: no memory round trip inside the softmax)
+    float* q_s = lds + 64;             // [16][D] query rows, later the gated outputs [4][grp * D]
+    float* gate_s = q_s + 16 * D;      // [16]
+    float* sc = gate_s + 16;           // [16][ldk] scores, then weights; the rows' norm staging before the scores
+    u32x4* vt_s = (u32x4*)(sc + 16 * ldk + 4 * D);   // 2 value tiles [TPV][D] fp16
+    const float scale = 1.0f / sqrtf((float)D);
+    // wave w makes and normalises rows w + 4 k (head w of position k, a head slot past the group being zero)
+    const bool hv = wv < grp;
+    const int hq = min(wv, grp - 1);
+    int r0[4], r1[4];   // row k's keys (union-relative)
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int at = a.pos0 + min(p0 + k, a.n - 1);
+        r0[k] = win0(at) - sU;
+        r1[k] = at - sU;
+    }
+
+    const uint64_t et = kExp2Tab[tid & 31];
+    const float gin = a.qkv[(size_t)min(p0 + ((tid >> 2) & 3), a.n - 1) * a.ld + Hq + 2 * kvd + g * grp +
+                            min(tid & 3, grp - 1)];   // (threads 0-15: the head gates' inputs)
+    // this wave's key tiles (tile tt = wv + 4 it covers keys 16 tt ..), then its 4 query rows' operands
+    const int ntile = (nkU + 15) >> 4, nit = ntile > wv ? (ntile - wv + 3) >> 2 : 0;
+    const int cb = lane >> 4, kk = lane & 15;
+    unsigned kw[KR][NM];
+    auto kload = [&](unsigned (&w)[NM], int it) {
+        const unsigned* kr = (const unsigned*)(kc + (size_t)min(16 * (wv + 4 * it) + kk, nkU - 1) * D) + cb;
+#pragma unroll
+        for (int m = 0; m < NM; m++) w[m] = kr[4 * m];
+    };
+#pragma unroll
+    for (int r = 0; r < KR; r++) kload(kw[r], r);
+    {
+        float xq[4][DPL], wq[DPL];
+        float2 cz[4][DPL];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int pr = min(p0 + k, a.n - 1);
+            norm_rope_load<DPL>(a.qkv + (size_t)pr * a.ld + (g * grp + hq) * D, a.q_norm,
+                                a.rope_cs + (size_t)(a.pos0 + pr) * (D / 2), D, xq[k], wq, cz[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            float r[DPL];
+            norm_rope_vals<DPL>(xq[k], wq, sc + wv * D, cz[k], D, a.eps, r);
+#pragma unroll
+            for (int c = 0; c < DPL; c++)
+                if (lane + 64 * c < D) q_s[(wv + 4 * k) * D + lane + 64 * c] = hv ? r[c] : 0.0f;
+        }
+    }
+    if (tid < 32) etab[tid] = et;
+    __syncthreads();
+
+    // scores of 16 rows x 16 keys per tile
+    {
+        float qa[NM], qb[NM];
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+            const float2 v = *(const float2*)&q_s[kk * D + 8 * m + 2 * cb];
+            qa[m] = v.x;
+            qb[m] = v.y;
+        }
+        auto tile = [&](const unsigned (&w)[NM], int it) {
+            v16f lo, hi;
+#pragma unroll
+            for (int k = 0; k < 16; k++) lo[k] = hi[k] = 0.0f;
+#pragma unroll
+            for (int m = 0; m < NM; m++) {
+                lo = __builtin_amdgcn_mfma_f32_16x16x1f32(qa[m], h2f((uint16_t)(w[m] & 0xFFFFu)), lo, 0, 0, 0);
+                hi = __builtin_amdgcn_mfma_f32_16x16x1f32(qb[m], h2f((uint16_t)(w[m] >> 16)), hi, 0, 0, 0);
+            }
+            const int t = 16 * (wv + 4 * it) + kk;
+            if (t < nkU) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float s = ((lo[i] + lo[8 + i]) + (lo[4 + i] + lo[12 + i])) +
+                                    ((hi[i] + hi[8 + i]) + (hi[4 + i] + hi[12 + i]));
+                    sc[(4 * cb + i) * ldk + t] = s * scale;
+                }
+            }
+        };
+        for (int it0 = 0; it0 < nit; it0 += KR) {
+#pragma unroll
+            for (int r = 0; r < KR; r++) {
+                if (it0 + r < nit) tile(kw[r], it0 + r);
+                kload(kw[r], it0 + r + KR);   // (past the wave's tiles: the last key's row again, a cache hit)
+            }
+        }
+    }
+    __syncthreads();
+
+    // values stream through LDS in tiles of TPV keys over the union, fetched by every thread two tiles ahead (16-byte
+    // words into registers, then stored to the tile's buffer); the first two tiles are requested before the softmax
+    const int ntv = (nkU + TPV - 1) / TPV;
+    u32x4 vw[2][VPT];
+    auto vfetch = [&](u32x4 (&w)[VPT], int i) {
+#pragma unroll
+        for (int r = 0; r < VPT; r++) {
+            const int q = tid + 256 * r, t = min(TPV * i + q / (D / 8), nkU - 1);
+            w[r] = ((const u32x4*)(vc + (size_t)t * D))[q % (D / 8)];
+        }
+    };
+    vfetch(vw[0], 0);
+    vfetch(vw[1], 1);
+
+    // softmax per row over its own keys: max, e_t = glibc expf(s_t - max), the double sum of e_t in position order
+    // (its exact-sum shortcut: when every e_t is a multiple of 2^(B - 51), B = floor(log2 sum), any order gives the
+    // same double, so the wave's tree sum is used), then a_t = e_t * inv in place. The wave's 4 rows run side by
+    // side (their ranges differ by at most 3 keys at either end); the in-order sums of the rows that need them run
+    // side by side in lanes 0-3, 8 keys' values read ahead of their adds.
+    if (tid < 16) gate_s[tid] = 1.0f / (1.0f + expf_glibc_t(-gin, etab));   // head gates
+    float* sw = sc + (size_t)wv * ldk;   // row k of this wave at sw + 4 k ldk
+    double wpart[4] = {1.0, 1.0, 1.0, 1.0};
+    int wlow[4] = {1 << 20, 1 << 20, 1 << 20, 1 << 20};
+    if (hv) {
+        float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        for (int t = r0[0] + lane; t <= r1[3]; t += 64) {
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                if (t >= r0[k] && t <= r1[k]) mx[k] = fmaxf(mx[k], sw[4 * k * ldk + t]);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            mx[k] = wave_max(mx[k]);
+            wpart[k] = 0.0;
+        }
+        for (int t = r0[0] + lane; t <= r1[3]; t += 64) {
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                if (t >= r0[k] && t <= r1[k]) {
+                    const float e = expf_glibc_t(sw[4 * k * ldk + t] - mx[k], etab);
+                    sw[4 * k * ldk + t] = e;
+                    wpart[k] += (double)e;
+                    wlow[k] = min(wlow[k], low_bit_exp(e));
+                }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                wpart[k] += __shfl_xor(wpart[k], o);
+                wlow[k] = min(wlow[k], __shfl_xor(wlow[k], o));
+            }
+    }
+    __builtin_amdgcn_wave_barrier();
+    float inv = 0.0f;
+    if (lane < 4 && hv) {
+        double part = wpart[0];
+        int lowb = wlow[0], q0 = r0[0], q1 = r1[0];
+#pragma unroll
+        for (int k = 1; k < 4; k++)
+            if (lane == k) {
+                part = wpart[k];
+                lowb = wlow[k];
+                q0 = r0[k];
+                q1 = r1[k];
+            }
+        int ex;
+        (void)frexp(part, &ex);
+        if (lowb < ex - 1 - 51) {   // some e_t below the exact unit: add in position order, as imi's loop
+            const float* s = sw + (size_t)4 * lane * ldk;
+            double sum = 0.0;
+            int t = q0;
+            for (; t + 8 <= q1 + 1; t += 8) {
+                float v[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[j] = s[t + j];
+#pragma unroll
+                for (int j = 0; j < 8; j++) sum += (double)v[j];
+            }
+            for (; t <= q1; t++) sum += (double)s[t];
+            part = sum;
+        }
+        inv = (float)(1.0 / part);
+    }
+    {
+        float ik[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) ik[k] = __shfl(inv, k);
+        if (hv)
+            for (int t = r0[0] + lane; t <= r1[3]; t += 64) {
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    if (t >= r0[k] && t <= r1[k]) sw[4 * k * ldk + t] = sw[4 * k * ldk + t] * ik[k];
+            }
+    }
+    __syncthreads();
+
+    // values: wave w runs position w's chains over its own keys in order, v_mfma_f32_4x4x1_16b_f32 (d[l][i] =
+    // fma(a[4 (l / 4) + i], b[l], c[l][i]), one rounding, bit for bit fmaf): lane l supplies head l % 4's weight and
+    // the value of dimension l (of each 64), and holds head i's output of dimension l in register i; a chunk of CH
+    // keys at either end of the wave's range takes the keys outside it as a zero weight times a zero value (o + 0 =
+    // o: o starts at +0 and so never becomes -0)
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    v4f o[NWV];
+#pragma unroll
+    for (int c = 0; c < NWV; c++) o[c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    const int w0 = r0[wv], w1 = r1[wv];
+    const float* aw = sc + (size_t)(4 * wv + (lane & 3)) * ldk;
+    // (two tiles per pass, so that each register set is named at compile time; a pass past the last tile stores and
+    // fetches clamped rows that nothing reads)
+    for (int i0 = 0; i0 < ntv; i0 += 2) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int i = i0 + h;
+            u32x4* vb = vt_s + (size_t)h * (TPV * D / 8);
+            const uint16_t* vh = (const uint16_t*)vb;
+#pragma unroll
+            for (int r = 0; r < VPT; r++) vb[tid + 256 * r] = vw[h][r];
+            __syncthreads();
+            vfetch(vw[h], i + 2);
+            if (i < ntv) {
+#pragma unroll
+                for (int c = 0; c < TPV / CH; c++) {
+                    const int tb = TPV * i + CH * c;
+                    if (tb + CH - 1 < w0 || tb > w1) continue;
+                    const bool full = tb >= w0 && tb + CH - 1 <= w1;
+                    const float4 a0 = *(const float4*)(aw + tb), a1 = *(const float4*)(aw + tb + 4);
+                    const float av[CH] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+                    unsigned vv[NWV][CH];
+#pragma unroll
+                    for (int j = 0; j < CH; j++)
+#pragma unroll
+                        for (int cc = 0; cc < NWV; cc++) vv[cc][j] = vh[(CH * c + j) * D + min(64 * cc + lane, D - 1)];
+#pragma unroll
+                    for (int j = 0; j < CH; j++) {
+                        const bool in = full || (tb + j >= w0 && tb + j <= w1);
+#pragma unroll
+                        for (int cc = 0; cc < NWV; cc++)
+                            o[cc] = __builtin_amdgcn_mfma_f32_4x4x1f32(in ? av[j] : 0.0f, in ? h2f((uint16_t)vv[cc][j]) : 0.0f,
+                                                                       o[cc], 0, 0, 0);
+                    }
+                }
+            }
+        }
+    }
+    // gated outputs, position-major [4][grp * D] in q_s (free since the scores)
+#pragma unroll
+    for (int cc = 0; cc < NWV; cc++) {
+        const int d = 64 * cc + lane;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (i < grp && d < D) q_s[(wv * grp + i) * D + d] = o[cc][i] * gate_s[4 * wv + i];
+    }
+    __syncthreads();
+    const int nblk = grp * D / 32, cb0 = g * nblk;
+    for (int k = tid; k < 4 * nblk; k += 256) {
+        const int pq = k / nblk, j = k - pq * nblk;
+        if (p0 + pq < a.n) cut_store(a.cut, a.n, cb0 + j, p0 + pq, q_s + pq * grp * D + 32 * j);
+    }
+}
+
 }  // namespace
 
 hipError_t launch_pf_rows(int mode, const pf_rows_args& a, hipStream_t s) {
@@ -757,10 +1038,35 @@ int pf_attn_max_ctx(int grp, int D) {
     return lo;
 }
 
+// LDS of the matrix-core attention: expf's table, 16 query rows (then the gated outputs), 16 gates, 16 score rows over the
+// widest key union of the launch and the 4 rows' norm staging past them, two value tiles of 64 keys
+static size_t pf_attn_mf_lds(const pf_attn_args& a) {
+    const int nku = a.n_swa > 0 ? std::min(a.pos0 + a.n, a.n_swa + 3) : a.pos0 + a.n, ldk = ((nku + 31) & ~31) + 4;
+    return sizeof(float) * (64 + (size_t)16 * a.D + 16 + (size_t)16 * ldk + 4 * (size_t)a.D) + 2 * 64 * (size_t)a.D * 2;
+}
+
 hipError_t launch_pf_attn(const pf_attn_args& a, hipStream_t s) {
     const int grp = a.n_head / a.n_kv;
+    if (a.n < 1 || a.n_head % a.n_kv) return hipErrorInvalidValue;
+    // the matrix-core form for groups of at most 4 heads (SEOUL_HIP_PF_ATTN_VALU=1 keeps the VALU form: a comparison
+    // switch, read per launch)
+    const char* ev = getenv("SEOUL_HIP_PF_ATTN_VALU");
+    const size_t mlds = pf_attn_mf_lds(a);
+    if (grp <= 4 && mlds <= 160 * 1024 && !(ev && ev[0] == '1')) {
+        const void* fn = a.D == 128 ? (const void*)k_pf_attn_mf<128> : a.D == 64 ? (const void*)k_pf_attn_mf<64>
+                       : a.D == 32 ? (const void*)k_pf_attn_mf<32> : nullptr;
+        if (fn) {
+            if (mlds > 64 * 1024) {
+                const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)mlds);
+                if (e != hipSuccess) return e;
+            }
+            pf_attn_args b = a;
+            void* args[] = {&b};
+            return hipLaunchKernel(fn, dim3((a.n + 3) / 4, a.n_kv), dim3(256), args, mlds, s);
+        }
+    }
     const size_t lds = pf_attn_lds(grp, a.D, a.pos0 + a.n);
-    if (lds > 160 * 1024 || a.n < 1) return hipErrorInvalidValue;
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
     const void* fn = a.D == 128 ? (const void*)k_pf_attn<128> : a.D == 64 ? (const void*)k_pf_attn<64>
                    : a.D == 32 ? (const void*)k_pf_attn<32> : nullptr;
     if (!fn) return hipErrorInvalidValue;

@@ -101,6 +101,28 @@ def test_seoul_width_prefill(mid_model):
     _check_batch(mid_model, tokens=_prompt(100, 4096, 10))
 
 
+@pytest.mark.parametrize("E,heads,D,window", [(256, (8, 4), 32, 0), (256, (8, 1), 32, 0), (256, (8, 8), 32, 0),
+                                              (512, (8, 4), 64, 3), (512, (8, 2), 64, 6)])
+def test_prefill_head_groups_and_windows(model_dir, E, heads, D, window):
+    """Query heads per kv head 2, 8 (past the matrix-core attention's 4: the VALU form) and 1, and windows shorter
+    than the key ranges of a workgroup's 4 positions (their ranges then differ at both ends). The attention is as
+    wide as n_embd, as in imi's files: imi's step_batch cuts the attention rows for the o table at the n_embd width it
+    last set (imi/core/seoul.cpp:546-554, 623), so a narrower or wider attention would make imi's batch disagree with
+    its own steps."""
+    from nunchi_amd import synth
+    shape = synth.BrainShape(n_embd=E, n_layer=3, attn_layers=(1, 2), n_head=heads[0], n_head_kv=heads[1],
+                             head_dim=D, n_ff=512, n_vocab=1000, sliding_window=window,
+                             swa_layers=(1,) if window else ())
+    path = synth.cached("brain", shape, 21, model_dir)
+    _check_batch(path, tokens=_prompt(45, 1000, 22), pre=_prompt(3, 1000, 23))
+
+
+def test_prefill_attention_valu_form(tiny_model, monkeypatch):
+    """The VALU attention (SEOUL_HIP_PF_ATTN_VALU=1, read per launch) gives the same numbers as the oracle too."""
+    monkeypatch.setenv("SEOUL_HIP_PF_ATTN_VALU", "1")
+    _check_batch(tiny_model, tokens=_prompt(40, 1000, 24))
+
+
 def test_prefill_context_full(tiny_model):
     import nunchi_amd
     g = nunchi_amd.Brain(tiny_model, n_ctx=64)
