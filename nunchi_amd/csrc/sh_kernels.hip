@@ -1338,7 +1338,8 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
     float* red = k_s + D;                          // [32]
     double* red_d = (double*)(red + 32);           // [8]
     int* red_i = (int*)(red_d + 8);                // [8]
-    float* stg = (float*)(red_i + 8);              // [2][D] norm staging of waves 0 and 1
+    uint64_t* etab = (uint64_t*)(red_i + 8);       // [32] expf's table (an LDS copy: no memory round trip in the softmax)
+    float* stg = (float*)(etab + 32);              // [2][D] norm staging of waves 0 and 1
     float* sc = stg + 2 * D;                       // [n_ctx] scores, then e_t, then a_t
     uint16_t* vT = (uint16_t*)(sc + ((a.n_ctx + 3) & ~3));   // [2][D][TV] fp16 value tiles, dimension-major
     const float2* cs = a.rope_cs + (size_t)pos * half;
@@ -1349,6 +1350,8 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
     // rows requested first the norm below waited for them to come back from memory, while the q / k operands come
     // from the previous kernel's output ----
     constexpr bool EARLY_QK = D <= 64;
+    const uint64_t et = kExp2Tab[t & 31];          // (first: the waits for it and the gate input need nothing later)
+    const float gin = row[Hq + 2 * kvd + h];
     const bool is_k = __builtin_amdgcn_readfirstlane(wv) == 1;   // (wave-uniform: the operand pointers stay scalar)
     float xq[DPL], wq[DPL], vq[DPL];
     float2 cq[DPL];
@@ -1456,6 +1459,7 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
             }
         }
     }
+    if (t < 32) etab[t] = et;
     __syncthreads();
     // ---- scores ----
     const float scale = 1.0f / sqrtf((float)D);
@@ -1541,7 +1545,7 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
     double part = 0.0;
     int lowb = 1 << 20;
     for (int p = t; p < nk; p += NT) {
-        const float e = expf_glibc(sc[p] - mx);
+        const float e = expf_glibc_t(sc[p] - mx, etab);
         sc[p] = e;
         part += (double)e;
         lowb = min(lowb, low_bit_exp(e));
@@ -1670,7 +1674,7 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
         __syncthreads();
     }
     if (wv == 0 && lane < D) {
-        const float gate = 1.0f / (1.0f + expf_glibc(-row[Hq + 2 * kvd + h]));
+        const float gate = 1.0f / (1.0f + expf_glibc_t(-gin, etab));
 #pragma unroll
         for (int c = 0; c < DPL; c++)
             if (lane + 64 * c < D) a.att[(size_t)m * Hq + h * D + lane + 64 * c] = o[c] * gate;
@@ -1679,7 +1683,7 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
 
 static size_t attn_head_lds(int D, int n_ctx) {
     const size_t tv = D > 64 ? attn_detail::tile_positions<128>() : attn_detail::tile_positions<64>();
-    return sizeof(float) * (4 * (size_t)D + 32 + 16 + 8 + (((size_t)n_ctx + 3) & ~(size_t)3)) + 2 * (size_t)D * tv * sizeof(uint16_t);
+    return sizeof(float) * (4 * (size_t)D + 32 + 16 + 8 + 64 + (((size_t)n_ctx + 3) & ~(size_t)3)) + 2 * (size_t)D * tv * sizeof(uint16_t);
 }
 
 // the longest context the decode attention holds: its score row (one float per position) and two value tiles share
