@@ -271,6 +271,7 @@ __global__ __launch_bounds__(256, (KC == 4 && PW == 32) ? 3 : 2) void k_pf_gemm_
     __shared__ __align__(16) uint16_t sD[2][KC][64];
     __shared__ __align__(16) uint16_t sM[2][KC][HM ? 64 : 8];
     __shared__ float2 sX[2][KC][P];         // (d, s) of position p's block j
+    __shared__ uint64_t sE[EPI == EPI_SWIGLU ? 32 : 1];   // expf's table for the SwiGLU epilogue (an LDS copy)
     const int t = threadIdx.x, lane = t & 63, w = t >> 6, li = lane & 15, lq = lane >> 4;
     const int rows = a.W.rows, n = a.n, nb = a.W.nb, nch = nb / KC, ng = rows / 8;
     const int r0 = blockIdx.x * 64, p0 = blockIdx.y * P, rl = (w & 1) * 32, pl = (w >> 1) * PW;
@@ -354,8 +355,10 @@ __global__ __launch_bounds__(256, (KC == 4 && PW == 32) ? 3 : 2) void k_pf_gemm_
     // this lane's outer-product operands: row 16 mt + (l % 16) of the wave's rows for block b = l / 16 (mt = b / 2),
     // position 16 nt + (l % 16) of its positions (nt = b % 2; with one position tile, nt = 0 again)
     const int orow = rl + 16 * (lane >> 5) + li, opos = pl + 16 * (NTW == 2 ? (lane >> 4) & 1 : 0) + li;
+    const uint64_t et = EPI == EPI_SWIGLU ? kExp2Tab[t & 31] : 0;   // (requested first: its wait needs nothing later)
     fetch(0);
     stash(0);
+    if (EPI == EPI_SWIGLU && t < 32) sE[t] = et;
     __syncthreads();
     for (int c = 0; c < nch; c++) {
         const int buf = c & 1;
@@ -414,7 +417,7 @@ __global__ __launch_bounds__(256, (KC == 4 && PW == 32) ? 3 : 2) void k_pf_gemm_
                 if (lq < 2 && p < n && rbase + 16 * mt < rows) {
                     float* o = a.out + (size_t)p * a.out_ld + (rbase + 16 * mt) / 2 + 4 * lq;
 #pragma unroll
-                    for (int i = 0; i < 4; i++) o[i] = silu(v[i]) * up[i];
+                    for (int i = 0; i < 4; i++) o[i] = silu_t(v[i], sE) * up[i];
                 }
             } else if (p < n) {
                 float* o = a.out + (size_t)p * a.out_ld + rr0;
