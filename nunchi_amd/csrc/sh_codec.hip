@@ -96,8 +96,10 @@ __global__ __launch_bounds__(CX_NT) void k_cattn(cattn_args a) {
     __shared__ float gws[CX_MAX_E], l1s[CX_MAX_E];
     __shared__ float sc[CX_P][CX_WIN];
     __shared__ float sm[CX_P], gt[CX_P], hs[CX_P];
+    __shared__ uint64_t cE[32];   // expf's table (an LDS copy: no memory round trip in the gate or the softmax)
     const int hh = blockIdx.x, grp = a.n_head / a.n_kv, kv = hh / grp, D = a.D, E = a.E, t = threadIdx.x;
     const int kvd = a.n_kv * D, nq = a.n_head * D, pos = a.in->pos, w = t >> 6, lane = t & 63, half = D / 2;
+    const uint64_t et = kExp2Tab[t & 31];   // (requested first: its wait needs nothing later)
     for (int i = t; i < W1 * D; i += CX_NT) {
         const int j = i / D, d = i - j * D, ps = pos - W1 + j;
         float kx = 0.0f, vx = 0.0f;
@@ -124,6 +126,7 @@ __global__ __launch_bounds__(CX_NT) void k_cattn(cattn_args a) {
         gws[e] = a.gate_w[(size_t)hh * E + e];
         l1s[e] = a.ln1[e];
     }
+    if (t < 32) cE[t] = et;
     __syncthreads();
     for (int ri = w; ri < 3 * CX_P; ri += CX_NT / 64) {   // the frame's keys, the queries, the input rows' scales
         if (ri < 2 * CX_P) {
@@ -166,7 +169,7 @@ __global__ __launch_bounds__(CX_NT) void k_cattn(cattn_args a) {
         const float s = hs[p];
         float g = 0.0f;
         for (int e = 0; e < E; e++) g = fmaf(gws[e], xs[p][e] * s * l1s[e], g);
-        gt[p] = 1.0f / (1.0f + expf_glibc(-g));
+        gt[p] = 1.0f / (1.0f + expf_glibc_t(-g, cE));
     }
     __syncthreads();
     if (t < CX_P) {
@@ -175,7 +178,7 @@ __global__ __launch_bounds__(CX_NT) void k_cattn(cattn_args a) {
         float sum = 0.0f;
         for (int j = 0; j < CX_WIN; j++) {
             const float v = sc[t][j];
-            const float ex = v == -__builtin_inff() ? 0.0f : expf_glibc(v - mx);
+            const float ex = v == -__builtin_inff() ? 0.0f : expf_glibc_t(v - mx, cE);
             sc[t][j] = ex;
             sum += ex;
         }

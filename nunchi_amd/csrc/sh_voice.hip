@@ -56,14 +56,18 @@ __device__ __forceinline__ void stage_chunk(float* xs, const vtab_args& a, int q
 }
 
 // results of the workgroup's NR rows (from group g0 on): thread t holds row t / P, position t % P
+// et: this thread's entry of expf's table (thread t holds entry t % 32), requested when the kernel starts; the
+// SwiGLU epilogue reads the table from LDS (no memory round trip at the end)
 template <int P, int EPI, int NR>
-__device__ __forceinline__ void table_epilogue(const vtab_args& a, int g0, float acc, float* ev) {
+__device__ __forceinline__ void table_epilogue(const vtab_args& a, int g0, float acc, float* ev, uint64_t et) {
     const int t = threadIdx.x, frow = t / P, fc = t - frow * P;
     if (EPI == VE_SWIGLU) {   // groups g0 (gate rows) and g0 + 1 (up rows): out[p][4 g0 + r] (voice.cpp:150-156)
         static_assert(EPI != VE_SWIGLU || NR == 16, "gate and up groups side by side");
+        __shared__ uint64_t vE[32];
         if (t < 16 * P) ev[t] = acc;
+        if (t < 32) vE[t] = et;
         __syncthreads();
-        if (t < 8 * P) a.out[(size_t)fc * a.out_ld + 4 * g0 + frow] = silu(ev[t]) * ev[8 * P + t];
+        if (t < 8 * P) a.out[(size_t)fc * a.out_ld + 4 * g0 + frow] = silu_t(ev[t], vE) * ev[8 * P + t];
     } else {
         const int row = 8 * g0 + frow;
         if (t < NR * P && row < a.W.rows) {
@@ -105,6 +109,7 @@ __device__ __forceinline__ void block_sums(const float* xb, const u32x4 (&w)[R][
 // the block's 32 columns for every position; then thread (row, position) folds acc = fma(d, s, acc) block by block
 template <int P, int PRO, int EPI>
 __global__ __launch_bounds__(VX_THREADS) void k_vtab_gen(vtab_args a) {
+    const uint64_t et = EPI == VE_SWIGLU ? kExp2Tab[threadIdx.x & 31] : 0;   // (first: its wait needs nothing later)
     constexpr int R = EPI == VE_SWIGLU ? 2 : 1;   // row groups per workgroup
     constexpr int PP = vx_pp(P), XJ = vx_xj(P);
     static_assert(8 * R * P <= VX_THREADS, "one folding thread per (row, position)");
@@ -156,7 +161,7 @@ __global__ __launch_bounds__(VX_THREADS) void k_vtab_gen(vtab_args a) {
             for (int i = 0; i < nbc; i++) acc = fmaf(dp[i], sp[i], acc);
         }
     }
-    table_epilogue<P, EPI, 8 * R>(a, g0, acc, ev);
+    table_epilogue<P, EPI, 8 * R>(a, g0, acc, ev, et);
 }
 
 // the generic order split over the input's 1024-column chunks, for tables wider than one chunk (the down table):
@@ -203,6 +208,7 @@ __global__ __launch_bounds__(VX_THREADS) void k_vtab_part(vtab_args a) {
 
 template <int P, int EPI>
 __global__ __launch_bounds__(VX_THREADS) void k_vtab_fold(vtab_args a) {
+    const uint64_t et = EPI == VE_SWIGLU ? kExp2Tab[threadIdx.x & 31] : 0;   // (first: its wait needs nothing later)
     __shared__ float ss[8 * P * VX_SS];
     __shared__ float ds[8 * VX_SS];
     __shared__ float ev[16 * VX_MAX_P];
@@ -234,7 +240,7 @@ __global__ __launch_bounds__(VX_THREADS) void k_vtab_fold(vtab_args a) {
             for (int i = 0; i < nbc; i++) acc = fmaf(dp[i], sp[i], acc);
         }
     }
-    table_epilogue<P, EPI, 8>(a, g0, acc, ev);
+    table_epilogue<P, EPI, 8>(a, g0, acc, ev, et);
 }
 
 // scaled order (imi/core/tables.cpp:324-365, P = 12 or 6): thread (row, position) runs one chain over all columns
@@ -245,6 +251,7 @@ __global__ __launch_bounds__(VX_THREADS) void k_vtab_fold(vtab_args a) {
 // 4 columns of its row and 4 of its position as one 16-byte LDS word each.
 template <int P, int PRO, int EPI>
 __global__ __launch_bounds__(VX_THREADS) void k_vtab_scaled(vtab_args a) {
+    const uint64_t et = EPI == VE_SWIGLU ? kExp2Tab[threadIdx.x & 31] : 0;   // (first: its wait needs nothing later)
     constexpr int WC = 256, WS = WC + 4, NBK = WC / 32;   // columns per chunk, LDS row stride, blocks per chunk
     constexpr int NXQ = (P * (WC / 4) + VX_THREADS - 1) / VX_THREADS;   // input 16-byte words per thread per chunk
     static_assert(16 * P <= VX_THREADS && 2 * NBK * 8 * 2 == VX_THREADS, "one code word per thread per chunk");
@@ -326,7 +333,7 @@ __global__ __launch_bounds__(VX_THREADS) void k_vtab_scaled(vtab_args a) {
         if (q + 1 < nch) stash(b ^ 1, q + 1);
         __syncthreads();
     }
-    table_epilogue<P, EPI, 16>(a, g0, acc, ev);
+    table_epilogue<P, EPI, 16>(a, g0, acc, ev, et);
 }
 
 // single-input order (imi/core/tables.cpp:366-382): 4 threads per row, thread o runs the chain over columns
@@ -383,14 +390,18 @@ __global__ __launch_bounds__(VX_THREADS) void k_vattn(vattn_args a) {
     __shared__ float qq[VX_MAX_P][VX_MAX_D], kk[VX_MAX_P][VX_MAX_D];
     __shared__ float sc[VX_MAX_P][VX_MAX_P + 1];
     __shared__ float sm[VX_MAX_P], gt[VX_MAX_P];
+    __shared__ uint64_t vE[32];   // expf's table (an LDS copy: no memory round trip in the softmax)
     const int P = a.P, D = a.D, hh = blockIdx.x, kv = hh / (a.n_head / a.n_kv);
     const int Hq = a.n_head * D, Hk = a.n_kv * D, t = threadIdx.x;
+    const uint64_t et = kExp2Tab[t & 31];   // (requested first, with the head gate's input)
+    const float gin = a.qkv[(size_t)min(t, P - 1) * a.n_qkv + Hq + 2 * Hk + hh];
     for (int i = t; i < P * D; i += VX_THREADS) {
         const int p = i / D, e = i - p * D;
         const float* r = a.qkv + (size_t)p * a.n_qkv;
         qq[p][e] = r[hh * D + e];
         kk[p][e] = r[Hq + kv * D + e];
     }
+    if (t < 32) vE[t] = et;
     __syncthreads();
     const int w = t >> 6, lane = t & 63, half = D / 2;
     for (int ri = w; ri < 2 * P; ri += VX_THREADS / 64) {
@@ -418,12 +429,12 @@ __global__ __launch_bounds__(VX_THREADS) void k_vattn(vattn_args a) {
         for (int u = 0; u < P; u++) mx = mx < sc[t][u] ? sc[t][u] : mx;   // std::max(mx, sc)
         float sum = 0.0f;
         for (int u = 0; u < P; u++) {
-            const float e = expf_glibc(sc[t][u] - mx);
+            const float e = expf_glibc_t(sc[t][u] - mx, vE);
             sc[t][u] = e;
             sum += e;
         }
         sm[t] = sum;
-        gt[t] = 1.0f / (1.0f + expf_glibc(-a.qkv[(size_t)t * a.n_qkv + Hq + 2 * Hk + hh]));
+        gt[t] = 1.0f / (1.0f + expf_glibc_t(-gin, vE));
     }
     __syncthreads();
     for (int i = t; i < P * D; i += VX_THREADS) {
