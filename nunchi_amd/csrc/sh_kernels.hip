@@ -1732,6 +1732,8 @@ __global__ __launch_bounds__(256) void k_final(final_args a) {
         }
         int best = -1;
         if (a.part_v) {
+            // score 0 requested with the partials (imi's rule below needs it)
+            const float l0 = a.logits ? a.logits[(size_t)m * a.ld_logits] : 0.0f;
             float v = -INFINITY;
             int bi = 0x7fffffff;
             for (int k = tid; k < a.n_part; k += 256) {
@@ -1739,22 +1741,26 @@ __global__ __launch_bounds__(256) void k_final(final_args a) {
                 const int oi = a.part_i[m * a.n_part + k];
                 if (ov > v || (ov == v && oi < bi)) { v = ov; bi = oi; }
             }
-            red_v[tid] = v;
-            red_i[tid] = bi;
-            __syncthreads();
-            for (int o = 128; o > 0; o >>= 1) {
-                if (tid < o) {
-                    const float ov = red_v[tid + o];
-                    const int oi = red_i[tid + o];
-                    if (ov > red_v[tid] || (ov == red_v[tid] && oi < red_i[tid])) { red_v[tid] = ov; red_i[tid] = oi; }
-                }
-                __syncthreads();
+            // (greater score, or equal score and lower row, wins: a total order on the partials, none of them NaN, so
+            // any reduction order picks the same row) by shuffles within each wave, then the 4 waves' picks
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const float ov = __shfl_xor(v, o);
+                const int oi = __shfl_xor(bi, o);
+                if (ov > v || (ov == v && oi < bi)) { v = ov; bi = oi; }
             }
+            if ((tid & 63) == 0) { red_v[tid >> 6] = v; red_i[tid >> 6] = bi; }
+            __syncthreads();
+            v = red_v[0];
+            bi = red_i[0];
+#pragma unroll
+            for (int w = 1; w < 4; w++)
+                if (red_v[w] > v || (red_v[w] == v && red_i[w] < bi)) { v = red_v[w]; bi = red_i[w]; }
             // imi's loop (imi/core/hear.cpp:67-68): best = 0, then v replaces it only if logits[v] > logits[best].
             // The partials give the first maximum over the scores that are not NaN; imi keeps 0 when score 0 is NaN
             // (nothing compares greater than it) and when every score is NaN (the partials then hold no row)
-            best = red_i[0];
-            if (best < 0 || best >= a.ld_logits || (a.logits && isnan(a.logits[(size_t)m * a.ld_logits]))) best = 0;
+            best = bi;
+            if (best < 0 || best >= a.ld_logits || (a.logits && isnan(l0))) best = 0;
             __syncthreads();
         }
         if (tid == 0) {
