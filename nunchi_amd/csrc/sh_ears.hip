@@ -86,7 +86,10 @@ __global__ __launch_bounds__(ET) void k_etab(etab_args a) {
     typedef float v4f __attribute__((ext_vector_type(4)));
     constexpr int KC = 128, KCP = KC + 4, DW = 8, NP = 4 * NMF;
     __shared__ __align__(16) float xs[ET / 64][2][NP][KCP];
+    constexpr bool EXPE = EPI == EE_GLU || EPI == EE_SILU;   // epilogues that take e^x
+    __shared__ uint64_t eE[ET / 64][EXPE ? 32 : 1];         // expf's table, a copy per wave (no memory round trip)
     const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), q = lane & 3;
+    const uint64_t et = EXPE ? kExp2Tab[lane & 31] : 0;      // (requested first: its wait needs nothing later)
     const int r = blockIdx.x * 64 + lane, p0 = (blockIdx.y * 4 + wv) * NP;
     const int rp = a.W.rows_pad, K = a.W.cols, nk8 = K >> 3, nch = (K + KC - 1) / KC;
     const size_t ldx = (size_t)a.ldx;
@@ -154,6 +157,9 @@ __global__ __launch_bounds__(ET) void k_etab(etab_args a) {
     }
     // lane l holds rows rb .. rb + 3 of position p0 + 4 m + l % 4 (rb = the workgroup's first row + 4 (l / 4))
     const int rb = blockIdx.x * 64 + 4 * (lane >> 2);
+    if (EXPE && lane < 32) eE[wv][EXPE ? lane : 0] = et;
+    __builtin_amdgcn_wave_barrier();
+    const uint64_t* etab = eE[wv];
     const bool xt = a.xt_out;
     const int pend = xt ? min(a.ldx, a.ldo) : a.P;   // the feature-major output also fills the padded positions
     auto put = [&](int row, int p, float v) {
@@ -171,7 +177,7 @@ __global__ __launch_bounds__(ET) void k_etab(etab_args a) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int row = rb + i, ro = (row >> 4) * 8 + (row & 7);
-                    if (ro < a.W.rows / 2) put(ro, p, silu(acc[m][i]) * up[i]);
+                    if (ro < a.W.rows / 2) put(ro, p, silu_t(acc[m][i], etab) * up[i]);
                 }
             }
         } else if constexpr (EPI == EE_POWER) {   // rows (2j, 2j + 1) = (re, im) of bin j
@@ -188,7 +194,7 @@ __global__ __launch_bounds__(ET) void k_etab(etab_args a) {
                 const int row = rb + i;
                 if (row >= a.W.rows) break;
                 const float v = acc[m][i] + (a.bias ? a.bias[row] : 0.0f);
-                put(row, p, EPI == EE_SILU ? silu(v) : EPI == EE_GELU ? gelu_erf(v) : v);
+                put(row, p, EPI == EE_SILU ? silu_t(v, etab) : EPI == EE_GELU ? gelu_erf(v) : v);
             }
         }
     }
