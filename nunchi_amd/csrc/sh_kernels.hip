@@ -1320,7 +1320,6 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
     constexpr int half = D / 2, KW = D / 8;        // 16-byte words per cache row
     constexpr int DPL = (D + 63) / 64;             // dimensions per lane in the per-head wave work (lane + 64 c)
     constexpr bool AHEAD2 = false;                 // key rows two passes ahead (registers: the value tile comes first)
-    constexpr bool EARLY_V = D <= 64;              // value tile 0 requested at the start (D 128: after the scores)
     constexpr int NL = (TV / 8) * KW;              // loader threads: one 8-position x 8-dimension block each
     static_assert(NL <= 256 && TV / 8 <= 32, "value staging layout");
     extern __shared__ __align__(16) float lds[];
@@ -1345,11 +1344,10 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
     const float2* cs = a.rope_cs + (size_t)pos * half;
     const int last = max(nk - 2, 0);               // last cache row written by an earlier step
 
-    // ---- requests first: waves 0 and 1 their q / k values, norm weights and rotation entries (head sizes up to 64;
-    // at 128 the registers would spill), then every thread its key rows. Loads complete in order, so with the key
-    // rows requested first the norm below waited for them to come back from memory, while the q / k operands come
-    // from the previous kernel's output ----
-    constexpr bool EARLY_QK = D <= 64;
+    // ---- requests first: waves 0 and 1 their q / k values, norm weights and rotation entries, then every thread its
+    // key rows, then the loaders value tile 0. Loads complete in order, so with the key rows requested first the norm
+    // below waited for them to come back from memory, while the q / k operands come from the previous kernel's
+    // output (at head size 128 the early requests fit the 256 registers a 512-thread workgroup allows: 165) ----
     const uint64_t et = kExp2Tab[t & 31];          // (first: the waits for it and the gate input need nothing later)
     const float gin = row[Hq + 2 * kvd + h];
     const bool is_k = __builtin_amdgcn_readfirstlane(wv) == 1;   // (wave-uniform: the operand pointers stay scalar)
@@ -1367,7 +1365,7 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
             vq[c] = row[Hq + kvd + g * D + e];   // this position's v (cache row written by the k wave)
         }
     };
-    if (EARLY_QK && wv < 2) load_qk();
+    if (wv < 2) load_qk();
     u32x4 ka[KW], kb[AHEAD2 ? KW : 1];
     {
         const int p0 = min(t, last), p1 = min(t + NT, last);
@@ -1416,14 +1414,13 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
         }
     };
 
-    if (EARLY_V && loader) {   // tile 0 requested with the key rows (cache rows of earlier steps)
+    if (loader) {   // tile 0 requested with the key rows (cache rows of earlier steps)
         load_tile(0);
         vn0 = ((const f32x4*)(row + Hq + kvd + g * D))[2 * kq];
         vn1 = ((const f32x4*)(row + Hq + kvd + g * D))[2 * kq + 1];
     }
     // ---- q (wave 0) and this position's k, v (wave 1): norm + NEOX rope (imi/core/seoul.cpp:19-28) ----
     if (wv < 2) {   // lane holds dimensions lane + 64 c; at D 128 a rope pair (i, i + 64) sits in one lane
-        if (!EARLY_QK) load_qk();
         float* st = stg + wv * D;
         float x[DPL], n[DPL];
 #pragma unroll
@@ -1526,11 +1523,6 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
 #pragma unroll
             for (int i = 0; i < KW; i++) ka[i] = kn[i];
         }
-    }
-    if (!EARLY_V && loader) {   // tile 0 requested (to LDS once the softmax is done)
-        load_tile(0);
-        vn0 = ((const f32x4*)(row + Hq + kvd + g * D))[2 * kq];
-        vn1 = ((const f32x4*)(row + Hq + kvd + g * D))[2 * kq + 1];
     }
     __syncthreads();
     // ---- softmax ----
