@@ -656,9 +656,10 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
     // then the first kEarlyRows code rows of the first chunk, the rest (and the scales) once y is in LDS: the memory
     // system streams weights while the inputs arrive without the whole chunk queued ahead of them. Half of a thread's
     // 8 rows for the FFN gate|up and word-score tables (decode B=1 2188 -> 2211 tokens/s; 2, 3, 5, 6 or all 8 rows with
-    // the scales measured no better or slower); all of a thread's rows for the q|k|v|gate (2 at 2048 columns) and
-    // conv in_proj (4) tables, which no longer issue duplicate row loads behind them
-    constexpr int kEarlyRows = (EPI == EPI_SWIGLU || EPI == EPI_LOGITS || EPI == EPI_CONV) ? 4 : 2;
+    // the scales measured no better or slower); all of a thread's rows for the q|k|v|gate table (2 at 2048 columns);
+    // one of the 4 for conv in_proj, whose conv taps and memory are requested ahead of its rows (B=2 +0.2 % against
+    // all 4; 2 no better)
+    constexpr int kEarlyRows = (EPI == EPI_SWIGLU || EPI == EPI_LOGITS) ? 4 : EPI == EPI_CONV ? 1 : 2;
     if (!EMB) load_rows(k < nchunk ? k : nchunk - 1, 0, kEarlyRows);
 
     if (!EMB) {   // x += norm(y) * w_post (imi_norm_mul_add)
