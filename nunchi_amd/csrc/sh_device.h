@@ -246,6 +246,29 @@ __device__ __forceinline__ float dppf(float v) {
 template <int CTRL>
 __device__ __forceinline__ int dppi(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true); }
 constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_MIRROR8 = 0x141, DPP_MIRROR16 = 0x140;
+template <int CTRL>
+__device__ __forceinline__ double dppd(double v) {
+    const long long b = __double_as_longlong(v);
+    const int lo = dppi<CTRL>((int)b), hi = dppi<CTRL>((int)(b >> 32));
+    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ double readlane_d(double v, int l) {
+    const long long b = __double_as_longlong(v);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)b, l), hi = (unsigned)__builtin_amdgcn_readlane((int)(b >> 32), l);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+// the wave's maximum in every lane (the wave fully active): four DPP levels leave each 16-lane row's maximum in all
+// of its lanes, then the four rows' values are combined (no LDS round trip, unlike a shuffle tree)
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, dppf<DPP_XOR1>(v));
+    v = fmaxf(v, dppf<DPP_XOR2>(v));
+    v = fmaxf(v, dppf<DPP_MIRROR8>(v));
+    v = fmaxf(v, dppf<DPP_MIRROR16>(v));
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
 
 // imi_rms_scale (imi/core/vec.h:20-33) of n = 128 NQ values held transposed (value i at row i % 32, column i / 32,
 // rows LD floats apart; 16-byte aligned rows), by one wave. imi's order: 32 FMA chains, chain P

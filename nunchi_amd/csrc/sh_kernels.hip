@@ -1296,11 +1296,13 @@ __global__ __launch_bounds__(256) void k_attn(attn_args a) {
 //  - softmax: max, e_t = glibc expf(s_t - max), and the double sum of e_t in position order. When every e_t is a
 //    multiple of 2^(B - 51), B = floor(log2(sum)), every partial sum in any order is exact (a multiple of that unit
 //    below 2^(B + 2) has at most 53 significant bits), so the in-order double sum equals the block's tree sum; else
-//    thread 0 adds in position order;
-//  - a_t = e_t * inv; o = fma(a_t, V_t, o) in order over t by lane i of wave 0 (one chain per dimension). Waves
-//    4-7 stage value tiles of 256 positions into LDS transposed (dimension-major, 16-byte slots XOR-swizzled so that
-//    both the staging writes and the chain's 8-position reads are free of bank conflicts), double-buffered: tile
-//    j + 1 is written and tile j + 2 requested while wave 0 runs tile j;
+//    wave 0 adds in position order. The maximum and the sums reduce within each wave by DPP; inv = 1 / sum is
+//    formed on wave 0 alone, which needs it;
+//  - a_t = e_t * inv; o = fma(a_t, V_t, o) in order over t by lane i of wave 0 (one chain per dimension, a_t formed
+//    as the chain reads e_t). Waves 4-7 stage value tiles of 256 positions into LDS transposed (dimension-major,
+//    16-byte slots XOR-swizzled so that both the staging writes and the chain's 8-position reads are free of bank
+//    conflicts), double-buffered: tile 0 is written during the scores, tile j + 1 written and tile j + 2 requested
+//    while wave 0 runs tile j;
 //  - times the sigmoid head gate.
 namespace attn_detail {
 constexpr int NT = 512;                                        // threads
@@ -1525,11 +1527,15 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
             for (int i = 0; i < KW; i++) ka[i] = kn[i];
         }
     }
+    if (loader) {   // tile 0 to LDS, tile 1 requested (waves 4-7 hold no scores below 256 positions)
+        store_tile(0);
+        if (ntile > 1) load_tile(1);
+    }
     __syncthreads();
     // ---- softmax ----
     float mx = -INFINITY;
     for (int p = t; p < nk; p += NT) mx = fmaxf(mx, sc[p]);
-    mx = wave_max(mx);
+    mx = wave_max_dpp(mx);
     if (lane == 0) red[wv] = mx;
     __syncthreads();
     mx = red[0];
@@ -1543,14 +1549,26 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
         part += (double)e;
         lowb = min(lowb, low_bit_exp(e));
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        part += __shfl_xor(part, o);
-        lowb = min(lowb, __shfl_xor(lowb, o));
-    }
-    if (lane == 0) { red_d[wv] = part; red_i[wv] = lowb; }
+    // wave totals: DPP levels within each 16-lane row, then the four rows (the tree's order is free: its total is
+    // used only when every partial sum is exact)
+    part += dppd<DPP_XOR1>(part);
+    lowb = min(lowb, dppi<DPP_XOR1>(lowb));
+    part += dppd<DPP_XOR2>(part);
+    lowb = min(lowb, dppi<DPP_XOR2>(lowb));
+    part += dppd<DPP_MIRROR8>(part);
+    lowb = min(lowb, dppi<DPP_MIRROR8>(lowb));
+    part += dppd<DPP_MIRROR16>(part);
+    lowb = min(lowb, dppi<DPP_MIRROR16>(lowb));
+    // (the lane reads stay outside the lane-0 branch: inside it the last level's adds may be moved into the branch
+    // too, leaving lanes 16, 32 and 48 with their 8-lane values)
+    const double wsum = (readlane_d(part, 0) + readlane_d(part, 16)) + (readlane_d(part, 32) + readlane_d(part, 48));
+    const int wlow = min(min(__builtin_amdgcn_readlane(lowb, 0), __builtin_amdgcn_readlane(lowb, 16)),
+                         min(__builtin_amdgcn_readlane(lowb, 32), __builtin_amdgcn_readlane(lowb, 48)));
+    if (lane == 0) { red_d[wv] = wsum; red_i[wv] = wlow; }
     __syncthreads();
-    if (t == 0) {
+    // 1 / sum on wave 0 only, which runs the value chains: no barrier after it (every lane computes the same value)
+    float inv = 0.0f;
+    if (wv == 0) {
         double tot = 0.0;
         int lb = 1 << 20;
 #pragma unroll
@@ -1570,18 +1588,8 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
             for (; p < nk; p++) sum += (double)sc[p];
             tot = sum;
         }
-        red[8] = (float)(1.0 / tot);
+        inv = (float)(1.0 / tot);
     }
-    __syncthreads();
-    {
-        const float inv = red[8];
-        for (int p = t; p < nk; p += NT) sc[p] = sc[p] * inv;
-    }
-    if (loader) {   // tile 0 to LDS, tile 1 requested
-        store_tile(0);
-        if (ntile > 1) load_tile(1);
-    }
-    __syncthreads();
     // ---- o = sum_t fma(a_t, V_t, o), lane i of wave 0; tiles double-buffered through LDS ----
     float o[DPL];
 #pragma unroll
@@ -1604,7 +1612,7 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
 #pragma unroll
                 for (int q = 0; q < 8; q++) {
                     const f32x4 x = *(const f32x4*)(ar + p32 + 4 * q);
-                    aa[4 * q] = x.x; aa[4 * q + 1] = x.y; aa[4 * q + 2] = x.z; aa[4 * q + 3] = x.w;
+                    aa[4 * q] = x.x * inv; aa[4 * q + 1] = x.y * inv; aa[4 * q + 2] = x.z * inv; aa[4 * q + 3] = x.w * inv;
                 }
 #pragma unroll
                 for (int c = 0; c < DPL; c++)
@@ -1640,7 +1648,8 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
             }
             for (; p + 8 <= nt; p += 8) {
                 const f32x4 a0 = *(const f32x4*)(ar + p), a1 = *(const f32x4*)(ar + p + 4);
-                const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+                const float av[8] = {a0.x * inv, a0.y * inv, a0.z * inv, a0.w * inv,
+                                     a1.x * inv, a1.y * inv, a1.z * inv, a1.w * inv};
 #pragma unroll
                 for (int c = 0; c < DPL; c++) {
                     const u32x4 w = *(const u32x4*)(vr[c] + 8 * ((p >> 3) ^ fz[c]));
@@ -1656,7 +1665,7 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
                     const unsigned ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
                     for (int u = 0; u < 8; u++)
-                        if (p + u < nt) o[c] = fmaf(ar[p + u], h2f((uint16_t)((ws[u >> 1] >> (16 * (u & 1))) & 0xFFFFu)), o[c]);
+                        if (p + u < nt) o[c] = fmaf(ar[p + u] * inv, h2f((uint16_t)((ws[u >> 1] >> (16 * (u & 1))) & 0xFFFFu)), o[c]);
                 }
             }
         }
