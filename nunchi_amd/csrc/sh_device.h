@@ -121,12 +121,6 @@ template <class TabPtr>
 __device__ __forceinline__ float expf_glibc_t(float x, TabPtr tab) {
     const uint32_t ux = __float_as_uint(x);
     const uint32_t abstop = (ux >> 20) & 0x7ffu;
-    if (abstop >= 0x42bu) {                         // |x| >= 88 or nan
-        if (ux == 0xff800000u) return 0.0f;         // -inf
-        if (abstop >= 0x7f8u) return x + x;         // +inf or nan
-        if (x > 0x1.62e42ep6f) return __builtin_inff();
-        if (x < -0x1.9fe368p6f) return 0.0f;
-    }
     const double inv_ln2_32 = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32, c2 = 0x1.62e42ff0c52d6p-1 / 32;
     const double xd = (double)x;
@@ -140,7 +134,15 @@ __device__ __forceinline__ float expf_glibc_t(float x, TabPtr tab) {
     const double r2 = r * r;
     double y = __builtin_fma(c2, r, 1.0);
     y = __builtin_fma(z, r2, y);
-    return (float)(y * sc);
+    // the special cases (|x| >= 88, inf, nan) as selects over the main path's value, the test taken first applied
+    // last: no branches, so the evaluations of several values interleave (the main path's table index stays in
+    // 0..31 for any input)
+    float e = (float)(y * sc);
+    e = x < -0x1.9fe368p6f ? 0.0f : e;
+    e = x > 0x1.62e42ep6f ? __builtin_inff() : e;
+    e = abstop >= 0x7f8u ? x + x : e;               // +inf or nan
+    e = ux == 0xff800000u ? 0.0f : e;               // -inf
+    return e;
 }
 
 __device__ __forceinline__ float expf_glibc(float x) { return expf_glibc_t(x, kExp2Tab); }

@@ -410,14 +410,16 @@ __global__ __launch_bounds__(256, (KC == 4 && PW == 32) ? 3 : 2) void k_pf_gemm_
                 v[i] = HM ? acc[k] + cor[k] : fmaf(-8.0f, cor[k], acc[k]);
             }
             if (EPI == EPI_SWIGLU) {
-                // rows 0-7 of the 16-row tile are a gate group, rows 8-15 the matching up group (lanes + 32)
-                float up[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) up[i] = __shfl_xor(v[i], 32);
-                if (lq < 2 && p < n && rbase + 16 * mt < rows) {
-                    float* o = a.out + (size_t)p * a.out_ld + (rbase + 16 * mt) / 2 + 4 * lq;
-#pragma unroll
-                    for (int i = 0; i < 4; i++) o[i] = silu_t(v[i], sE) * up[i];
+                // rows 0-7 of the 16-row tile are a gate group, rows 8-15 the matching up group (lanes + 32): lane l
+                // (lq < 2) forms channels 4 lq, 4 lq + 1 of the tile's 8 and lane l + 32 channels 4 lq + 2, 4 lq + 3,
+                // each sending its partner the two values that one needs, so every lane evaluates two activations
+                const bool lo = lq < 2;
+                const float s0 = __shfl_xor(lo ? v[2] : v[0], 32), s1 = __shfl_xor(lo ? v[3] : v[1], 32);
+                const float g0 = lo ? v[0] : s0, g1 = lo ? v[1] : s1, u0 = lo ? s0 : v[2], u1 = lo ? s1 : v[3];
+                if (p < n && rbase + 16 * mt < rows) {
+                    float* o = a.out + (size_t)p * a.out_ld + (rbase + 16 * mt) / 2 + 4 * (lq & 1) + (lo ? 0 : 2);
+                    o[0] = silu_t(g0, sE) * u0;
+                    o[1] = silu_t(g1, sE) * u1;
                 }
             } else if (p < n) {
                 float* o = a.out + (size_t)p * a.out_ld + rr0;
