@@ -629,7 +629,10 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
         }
     }
     const f32x4 wp = EMB ? f32x4{0, 0, 0, 0} : ((const f32x4*)a.w_post)[tq], wq = ((const f32x4*)a.w_pre)[tq];
-    const uint64_t etab = kExp2Tab[t & 31];   // (SwiGLU) copied to LDS once the dots have waited for the weights
+    // (SwiGLU only: copied to LDS once the dots have waited for the weights. Elsewhere an unused half of the loaded
+    // pair was a register the compiler reused at once, which made it wait for the inputs before the first weight
+    // rows were requested)
+    const uint64_t etab = EPI == EPI_SWIGLU ? kExp2Tab[t & 31] : 0;
     int k = blockIdx.x;
     if (EMB) load_chunk(k < nchunk ? k : nchunk - 1);
     // the conv epilogue's taps and memory of this thread's channel (one chunk per workgroup), right behind the inputs,
