@@ -11,6 +11,7 @@
 #include "sh_kernels.h"
 
 #include <algorithm>
+#include <cstddef>
 
 namespace sh {
 
@@ -1715,6 +1716,15 @@ __global__ __launch_bounds__(256) void k_final(final_args a) {
     __shared__ int red_i[256];
     const int tid = threadIdx.x, E = a.E;
     float* l_x = lds;   // [E]
+    // the parameter-block words thread 0 updates at the end, requested before everything else, one per lane of wave
+    // 0 (lanes 0-7: token, pos, best, n_done, greedy; 8-11: the two out_tok pointers) and taken by lane reads after
+    // the pick: read there, each was one more memory round trip in a row (this kernel is their only writer)
+    static_assert(offsetof(step_params, pos) == 8 && offsetof(step_params, n_done) == 24 &&
+                  offsetof(step_params, greedy) == 28 && offsetof(step_params, out_tok) == 80, "step_params layout");
+    SH_GLOBAL step_params* const P = global_ptr(a.P);
+    const int pv = ((const SH_GLOBAL int*)P)[tid < 8 ? tid : tid < 12 ? 12 + tid : 0];
+    int bests[M];
+#pragma unroll
     for (int m = 0; m < M; m++) {
         if (a.hidden_out && a.x_in) {
             if (a.y_in) {
@@ -1737,8 +1747,10 @@ __global__ __launch_bounds__(256) void k_final(final_args a) {
         }
         int best = -1;
         if (a.part_v) {
-            // score 0 requested with the partials (imi's rule below needs it)
-            const float l0 = a.logits ? a.logits[(size_t)m * a.ld_logits] : 0.0f;
+            // score 0 requested with the partials (imi's rule below needs it), by a load on every path (without scores
+            // it reads a partial, unused): a conditional load had its NaN test, and a wait for it, before the partials
+            // were requested
+            const float l0 = (a.logits ? a.logits : a.part_v)[a.logits ? (size_t)m * a.ld_logits : 0];
             float v = -INFINITY;
             int bi = 0x7fffffff;
             for (int k = tid; k < a.n_part; k += 256) {
@@ -1768,16 +1780,30 @@ __global__ __launch_bounds__(256) void k_final(final_args a) {
             if (best < 0 || best >= a.ld_logits || (a.logits && isnan(l0))) best = 0;
             __syncthreads();
         }
-        if (tid == 0) {
-            a.P->best[m] = best;
+        bests[m] = best;
+    }
+    // (the lane reads stay outside the thread-0 branch, so the loads above run on all of wave 0's lanes)
+    const int n_done = __builtin_amdgcn_readlane(pv, 6), greedy = __builtin_amdgcn_readlane(pv, 7);
+    int pos_m[M];
+    int32_t* out_m[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        pos_m[m] = __builtin_amdgcn_readlane(pv, 2 + m);
+        out_m[m] = (int32_t*)(((unsigned long long)(unsigned)__builtin_amdgcn_readlane(pv, 9 + 2 * m) << 32) |
+                              (unsigned)__builtin_amdgcn_readlane(pv, 8 + 2 * m));
+    }
+    if (tid == 0) {
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            P->best[m] = bests[m];
             if (a.advance) {
-                if (a.P->greedy && a.P->out_tok[m]) global_ptr(a.P->out_tok[m])[a.P->n_done] = best;
-                if (a.P->greedy) a.P->token[m] = best;
-                a.P->pos[m] += 1;
+                if (greedy && out_m[m]) global_ptr(out_m[m])[n_done] = bests[m];
+                if (greedy) P->token[m] = bests[m];
+                P->pos[m] = pos_m[m] + 1;
             }
         }
+        if (a.advance) P->n_done = n_done + 1;
     }
-    if (tid == 0 && a.advance) a.P->n_done += 1;
 }
 
 // e^x of n floats with the kernels' exponential (for checks against the C library)
