@@ -45,6 +45,7 @@ struct pf_gemm_args {
     pf_cut in;              // the input, cut (W.nb blocks)
     float* out;             // EPI_STORE: [n][out_ld] rows of W; EPI_SWIGLU: [n][out_ld] silu(gate) * up channels
     int out_ld;
+    pf_cut outc;            // EPI_SWIGLU with outc.q set: the channels cut (out_ld / 32 blocks) instead of stored
 };
 
 struct pf_cutk_args {       // cut of n rows of K floats
@@ -76,6 +77,9 @@ struct pf_attn_args {       // causal attention of n positions (keys and values 
 
 hipError_t launch_pf_rows(int mode, const pf_rows_args& a, hipStream_t s);
 hipError_t launch_pf_gemm(int epi, const pf_gemm_args& a, hipStream_t s);
+// whether launch_pf_gemm takes EPI_SWIGLU with the cut output for these arguments (the staged kernel, whole 64-row
+// workgroups, each one 32-channel block)
+bool pf_swiglu_cut_takes(const pf_gemm_args& a);
 hipError_t launch_pf_cut(const pf_cutk_args& a, hipStream_t s);
 hipError_t launch_pf_conv(const pf_conv_args& a, hipStream_t s);
 hipError_t launch_pf_kv(const pf_attn_args& a, hipStream_t s);

@@ -35,17 +35,27 @@ __device__ __forceinline__ void cut_store(const pf_cut& c, int n, int j, int p, 
 // PFR_FIRST: x = the word's dequantized row (Q4_0: (code - 8) * d; Q6_K: imi_q6k_dequant_row) or the given embedding
 // row (imi/core/seoul.cpp:363-364);
 // PFR_RESID: x = fma(y * rms(y), w_post, x) (imi/core/vec.h:41-44); then h = x * rms(x) * w_pre, cut or stored
-// One wave per position, 4 positions per workgroup (no workgroup barriers): the wave stages its rows in LDS, runs both
-// norms' chains (rms_scale_wave, imi's AVX2 order) and cuts its blocks, a block per lane.
+// One wave per position, PFR_PPW positions per workgroup (no workgroup barriers): the wave stages its rows in LDS,
+// runs both norms' chains (rms_scale_wave, imi's AVX2 order) and cuts its blocks, a block per lane. One position per
+// workgroup spreads a window's positions over every compute unit: each position reads 32 KB (y, x and both norm
+// weights), and 4 per workgroup on 112 units waited on the units' read rate (8.0 against 8.4 us per launch).
+constexpr int PFR_PPW = 1;
 template <int MODE>
-__global__ __launch_bounds__(256) void k_pf_rows(pf_rows_args a) {
-    __shared__ __attribute__((aligned(16))) float xs_all[4][2048];
-    __shared__ __attribute__((aligned(16))) float hs_all[4][2048];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, p = blockIdx.x * 4 + wv, E = a.E, nb = E / 32;
+__global__ __launch_bounds__(64 * PFR_PPW) void k_pf_rows(pf_rows_args a) {
+    __shared__ __attribute__((aligned(16))) float xs_all[PFR_PPW][2048];
+    __shared__ __attribute__((aligned(16))) float hs_all[PFR_PPW][2048];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, p = blockIdx.x * PFR_PPW + wv, E = a.E, nb = E / 32;
     if (p >= a.n) return;
     float* xs = xs_all[wv];
     float* hs = hs_all[wv];
     float* xr = a.x + (size_t)p * E;
+    // the second norm's weights requested first too: behind the first norm they were one more memory round trip.
+    // Every operand load is issued on every path (words past E re-read the last one, unused), so the compiler's
+    // waits count exactly and never include the stores of x below
+    constexpr int NQ2 = 2048 / 256;   // float4 words per lane at most
+    float4 wq[NQ2];
+#pragma unroll
+    for (int q = 0; q < NQ2; q++) wq[q] = *reinterpret_cast<const float4*>(a.w_pre + min(4 * lane + 256 * q, E - 4));
     if (MODE == PFR_FIRST) {
         const int tok = a.tokens ? a.tokens[p] : -1;
         if (tok >= 0 && a.vocab6.codes) {
@@ -75,12 +85,10 @@ __global__ __launch_bounds__(256) void k_pf_rows(pf_rows_args a) {
         float4 y4[NQ], x4[NQ], wp[NQ];
 #pragma unroll
         for (int q = 0; q < NQ; q++) {
-            const int i = 4 * lane + 256 * q;
-            if (i < E) {
-                y4[q] = *reinterpret_cast<const float4*>(yr + i);
-                x4[q] = *reinterpret_cast<const float4*>(xr + i);
-                wp[q] = *reinterpret_cast<const float4*>(a.w_post + i);
-            }
+            const int i = min(4 * lane + 256 * q, E - 4);
+            y4[q] = *reinterpret_cast<const float4*>(yr + i);
+            x4[q] = *reinterpret_cast<const float4*>(xr + i);
+            wp[q] = *reinterpret_cast<const float4*>(a.w_post + i);
         }
 #pragma unroll
         for (int q = 0; q < NQ; q++)
@@ -90,20 +98,17 @@ __global__ __launch_bounds__(256) void k_pf_rows(pf_rows_args a) {
 #pragma unroll
         for (int q = 0; q < NQ; q++) {
             const int i = 4 * lane + 256 * q;
-            if (i < E) {
-                const float4 v = make_float4(fmaf(y4[q].x * sc1, wp[q].x, x4[q].x), fmaf(y4[q].y * sc1, wp[q].y, x4[q].y),
-                                             fmaf(y4[q].z * sc1, wp[q].z, x4[q].z), fmaf(y4[q].w * sc1, wp[q].w, x4[q].w));
-                *reinterpret_cast<float4*>(xs + i) = v;
-                *reinterpret_cast<float4*>(xr + i) = v;
-            }
+            x4[q] = make_float4(fmaf(y4[q].x * sc1, wp[q].x, x4[q].x), fmaf(y4[q].y * sc1, wp[q].y, x4[q].y),
+                                fmaf(y4[q].z * sc1, wp[q].z, x4[q].z), fmaf(y4[q].w * sc1, wp[q].w, x4[q].w));
+            if (i < E) *reinterpret_cast<float4*>(xs + i) = x4[q];
+        }
+#pragma unroll
+        for (int q = 0; q < NQ; q++) {   // (x to memory once every operand load has been consumed)
+            const int i = 4 * lane + 256 * q;
+            if (i < E) *reinterpret_cast<float4*>(xr + i) = x4[q];
         }
         __builtin_amdgcn_wave_barrier();
     }
-    constexpr int NQ2 = 2048 / 256;
-    float4 wq[NQ2];
-#pragma unroll
-    for (int q = 0; q < NQ2; q++)
-        if (4 * lane + 256 * q < E) wq[q] = *reinterpret_cast<const float4*>(a.w_pre + 4 * lane + 256 * q);
     const float sc2 = rms_scale_wave(static_cast<const float*>(xs), E, a.eps);
 #pragma unroll
     for (int q = 0; q < NQ2; q++) {
@@ -398,6 +403,10 @@ __global__ __launch_bounds__(256, (KC == 4 && PW == 32) ? 3 : 2) void k_pf_gemm_
         __syncthreads();
     }
     const int rbase = r0 + rl, pbase = p0 + pl;
+    // EPI_SWIGLU with outc: the workgroup's 64 rows are one 32-channel cut block of the output; its activations are
+    // staged in LDS (the code tiles' space, free after the last chunk's barrier), [position][channel], 33 floats apart
+    const bool cut_out = EPI == EPI_SWIGLU && a.outc.q != nullptr;
+    float* act = reinterpret_cast<float*>(&sA[0][0]);
 #pragma unroll
     for (int mt = 0; mt < 2; mt++)
 #pragma unroll
@@ -416,8 +425,12 @@ __global__ __launch_bounds__(256, (KC == 4 && PW == 32) ? 3 : 2) void k_pf_gemm_
                 const bool lo = lq < 2;
                 const float s0 = __shfl_xor(lo ? v[2] : v[0], 32), s1 = __shfl_xor(lo ? v[3] : v[1], 32);
                 const float g0 = lo ? v[0] : s0, g1 = lo ? v[1] : s1, u0 = lo ? s0 : v[2], u1 = lo ? s1 : v[3];
-                if (p < n && rbase + 16 * mt < rows) {
-                    float* o = a.out + (size_t)p * a.out_ld + (rbase + 16 * mt) / 2 + 4 * (lq & 1) + (lo ? 0 : 2);
+                const int ch = (rl + 16 * mt) / 2 + 4 * (lq & 1) + (lo ? 0 : 2);   // channel within the workgroup's 32
+                if (cut_out) {   // to LDS for the block cut below
+                    act[(pl + 16 * nt + li) * 33 + ch] = silu_t(g0, sE) * u0;
+                    act[(pl + 16 * nt + li) * 33 + ch + 1] = silu_t(g1, sE) * u1;
+                } else if (p < n && rbase + 16 * mt < rows) {
+                    float* o = a.out + (size_t)p * a.out_ld + r0 / 2 + ch;
                     o[0] = silu_t(g0, sE) * u0;
                     o[1] = silu_t(g1, sE) * u1;
                 }
@@ -428,6 +441,42 @@ __global__ __launch_bounds__(256, (KC == 4 && PW == 32) ? 3 : 2) void k_pf_gemm_
                     if (rr0 + i < rows) o[i] = v[i];
             }
         }
+    if (EPI == EPI_SWIGLU && cut_out) {
+        // the cut of each position's block (imi_cut32's values, as cut_store): thread (position, quarter) holds 8
+        // channels; amax and the code sum are order-free reductions, over the quad of lanes by DPP
+        static_assert(sizeof(sA) >= (size_t)P * 33 * sizeof(float), "activation staging");
+        __syncthreads();
+        const int jb = r0 / 64;
+        for (int e = t; e < P * 4; e += 256) {   // (P * 4 is 256 or 128: whole waves)
+            const int pp = e >> 2, qq = e & 3, p = p0 + pp;
+            float x8[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) x8[k] = act[pp * 33 + 8 * qq + k];
+            float am = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; k++) am = fmaxf(am, fabsf(x8[k]));
+            am = fmaxf(am, dppf<DPP_XOR1>(am));
+            am = fmaxf(am, dppf<DPP_XOR2>(am));
+            const float d = am / 127.0f, id = d != 0.0f ? 1.0f / d : 0.0f;
+            unsigned w2[2] = {0u, 0u};
+            int sum = 0;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int q = (int)rintf(x8[k] * id);
+                sum += q;
+                w2[k >> 2] |= ((unsigned)q & 0xFFu) << (8 * (k & 3));
+            }
+            sum += dppi<DPP_XOR1>(sum);
+            sum += dppi<DPP_XOR2>(sum);
+            if (p < n) {
+                *reinterpret_cast<uint2*>(a.outc.q + ((size_t)jb * n + p) * 32 + 8 * qq) = uint2{w2[0], w2[1]};
+                if (qq == 0) {
+                    a.outc.d[(size_t)jb * n + p] = d;
+                    a.outc.s[(size_t)jb * n + p] = d * (float)sum;
+                }
+            }
+        }
+    }
 }
 
 // ---------------------------------------------------------------- gated short conv along positions
@@ -954,11 +1003,11 @@ __global__ __launch_bounds__(256) void k_pf_attn_mf(pf_attn_args a) {
 
 hipError_t launch_pf_rows(int mode, const pf_rows_args& a, hipStream_t s) {
     if (a.E % 32 || a.E > 2048 || a.n < 1) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((a.n + 3) / 4));
+    const dim3 grid((unsigned)((a.n + PFR_PPW - 1) / PFR_PPW));
     if (mode == PFR_FIRST)
-        hipLaunchKernelGGL(k_pf_rows<PFR_FIRST>, grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL(k_pf_rows<PFR_FIRST>, grid, dim3(64 * PFR_PPW), 0, s, a);
     else
-        hipLaunchKernelGGL(k_pf_rows<PFR_RESID>, grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL(k_pf_rows<PFR_RESID>, grid, dim3(64 * PFR_PPW), 0, s, a);
     return hipGetLastError();
 }
 
@@ -971,8 +1020,13 @@ static bool getenv_pf_plain() {
     return v != 0;
 }
 
+bool pf_swiglu_cut_takes(const pf_gemm_args& a) {
+    return a.n >= 1 && a.W.rows % 64 == 0 && a.out_ld * 2 == a.W.rows && a.W.nb % PF_KC == 0 && !getenv_pf_plain();
+}
+
 hipError_t launch_pf_gemm(int epi, const pf_gemm_args& a, hipStream_t s) {
     if (a.n < 1 || a.W.rows % 8 || (epi == EPI_SWIGLU && a.W.rows % 16)) return hipErrorInvalidValue;
+    if (a.outc.q && (epi != EPI_SWIGLU || !a.outc.d || !a.outc.s || !pf_swiglu_cut_takes(a))) return hipErrorInvalidValue;
     const dim3 grid((a.W.rows + 63) / 64, (a.n + 63) / 64);
     const bool hm = a.W.mins != nullptr;   // Q4_1 table
     if (a.W.nb % PF_KC == 0 && !getenv_pf_plain()) {

@@ -64,19 +64,23 @@ int enqueue_chunk(sh_ctx* c, sh_state* st, int m, bool have_tokens, bool have_em
     r.w_pre = c->layers[0].attn_norm;
     r.cut = cut;
     PCHK(launch_pf_rows(PFR_FIRST, r, s));
-    auto gemm = [&](const q4dev& W, int epi, float* out, int ld) {
+    auto gemm = [&](const q4dev& W, int epi, float* out, int ld, const pf_cut& in) {
         pf_gemm_args g{};
         g.W = W;
         g.n = m;
-        g.in = cut;
+        g.in = in;
         g.out = out;
         g.out_ld = ld;
         return launch_pf_gemm(epi, g, s);
     };
+    // the FFN activations' cut, written by the gate|up products themselves into the activation buffer's space (their
+    // input cut is still being read meanwhile, so not the shared cut buffer)
+    const size_t nact = (size_t)PF_MAX_N * I.n_ff;
+    const pf_cut act_cut{(int8_t*)c->pf_act, (float*)((char*)c->pf_act + nact), (float*)((char*)c->pf_act + nact + nact / 8)};
     for (size_t il = 0; il < c->layers.size(); il++) {
         const layer_dev& L = c->layers[il];
         if (L.conv) {
-            PCHK(gemm(L.in_proj, EPI_STORE, c->pf_big, 3 * E));
+            PCHK(gemm(L.in_proj, EPI_STORE, c->pf_big, 3 * E, cut));
             pf_conv_args cv{};
             cv.bcx = c->pf_big;
             cv.w = L.conv_w;
@@ -86,9 +90,9 @@ int enqueue_chunk(sh_ctx* c, sh_state* st, int m, bool have_tokens, bool have_em
             cv.d_conv = I.d_conv;
             cv.cut = cut;
             PCHK(launch_pf_conv(cv, s));
-            PCHK(gemm(L.out_proj, EPI_STORE, c->pf_y, E));
+            PCHK(gemm(L.out_proj, EPI_STORE, c->pf_y, E, cut));
         } else {
-            PCHK(gemm(L.qkvg, EPI_STORE, c->pf_big, c->nqkv));
+            PCHK(gemm(L.qkvg, EPI_STORE, c->pf_big, c->nqkv, cut));
             pf_attn_args t{};
             t.qkv = c->pf_big;
             t.ld = c->nqkv;
@@ -108,17 +112,28 @@ int enqueue_chunk(sh_ctx* c, sh_state* st, int m, bool have_tokens, bool have_em
             t.cut = cut;
             PCHK(launch_pf_kv(t, s));
             PCHK(launch_pf_attn(t, s));
-            PCHK(gemm(L.o, EPI_STORE, c->pf_y, E));
+            PCHK(gemm(L.o, EPI_STORE, c->pf_y, E, cut));
         }
         pf_rows_args f = r;
         f.w_post = L.post_attn_norm;
         f.y = c->pf_y;
         f.w_pre = L.ffn_norm;
         PCHK(launch_pf_rows(PFR_RESID, f, s));
-        PCHK(gemm(L.gate_up, EPI_SWIGLU, c->pf_act, I.n_ff));
-        pf_cutk_args ck{c->pf_act, I.n_ff, I.n_ff, m, cut};
-        PCHK(launch_pf_cut(ck, s));
-        PCHK(gemm(L.down, EPI_STORE, c->pf_y, E));
+        pf_gemm_args gu{};
+        gu.W = L.gate_up;
+        gu.n = m;
+        gu.in = cut;
+        gu.out_ld = I.n_ff;
+        gu.outc = act_cut;
+        if (pf_swiglu_cut_takes(gu)) {   // SwiGLU and the cut in the products' epilogue
+            PCHK(launch_pf_gemm(EPI_SWIGLU, gu, s));
+            PCHK(gemm(L.down, EPI_STORE, c->pf_y, E, act_cut));
+        } else {
+            PCHK(gemm(L.gate_up, EPI_SWIGLU, c->pf_act, I.n_ff, cut));
+            pf_cutk_args ck{c->pf_act, I.n_ff, I.n_ff, m, cut};
+            PCHK(launch_pf_cut(ck, s));
+            PCHK(gemm(L.down, EPI_STORE, c->pf_y, E, cut));
+        }
         pf_rows_args z = r;
         z.y = c->pf_y;
         z.w_post = L.post_ffn_norm;
