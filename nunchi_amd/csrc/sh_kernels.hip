@@ -1012,6 +1012,23 @@ __global__ __launch_bounds__(512) void k_scores_q6k(gemv_args a) {
     const u32x4* codes = (const u32x4*)a.W6.codes;
     int tile = blockIdx.x * 8 + wv;
     const int tstep = gridDim.x * 8;
+    // ---- prologue: its inputs requested first, by loads on every path (operands a call does not give re-read the
+    // first input, unused): a conditional load left the compiler waiting for every earlier load, and the first
+    // tile's weights (about 100 KB per workgroup) requested ahead of the inputs held them back ----
+    const int tq = t < nq ? t : nq - 1;
+    const float* const xb = a.src ? a.src : a.x_in;
+    const size_t xld = a.src ? (size_t)a.src_ld : (size_t)E;
+    const float* const yb = a.y_in ? a.y_in : xb;
+    const size_t yld = a.y_in ? (size_t)E : xld;
+    f32x4 xv[M], yv[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        xv[m] = ((const f32x4*)(xb + (size_t)m * xld))[tq];
+        yv[m] = ((const f32x4*)(yb + (size_t)m * yld))[tq];
+    }
+    const f32x4 wq = ((const f32x4*)(a.w_pre ? a.w_pre : xb))[tq];
+    const f32x4 wp = ((const f32x4*)(a.w_post ? a.w_post : xb))[tq];
+    __builtin_amdgcn_sched_barrier(0);   // (the tile's loads stay behind the inputs')
     u32x4 w[NW];
     auto load_tile = [&](int tl) {   // (a wave past the last tile re-reads the last one)
         const u32x4* b = codes + (size_t)min(tl, ntile - 1) * NW * 64 + lane;
@@ -1021,22 +1038,12 @@ __global__ __launch_bounds__(512) void k_scores_q6k(gemv_args a) {
     load_tile(tile);
     float dw = h2f(a.W6.d[(size_t)min(tile, ntile - 1) * 64 + lane]);
 
-    // ---- prologue ----
-    const int tq = t < nq ? t : nq - 1;
     f32x4 hv[M];
     if (a.src) {
 #pragma unroll
-        for (int m = 0; m < M; m++) hv[m] = ((const f32x4*)(a.src + (size_t)m * a.src_ld))[tq];
+        for (int m = 0; m < M; m++) hv[m] = xv[m];
     } else {
-        f32x4 xv[M], yv[M];
-#pragma unroll
-        for (int m = 0; m < M; m++) {
-            xv[m] = ((const f32x4*)(a.x_in + (size_t)m * E))[tq];
-            yv[m] = a.y_in ? ((const f32x4*)(a.y_in + (size_t)m * E))[tq] : f32x4{0, 0, 0, 0};
-        }
-        const f32x4 wq = ((const f32x4*)a.w_pre)[tq];
         if (a.y_in) {   // x += norm(y) * w_post (imi_norm_mul_add)
-            const f32x4 wp = ((const f32x4*)a.w_post)[tq];
             if (t < nq)
 #pragma unroll
                 for (int m = 0; m < M; m++) put_xt(l_v + m * 32 * XLD, t, yv[m]);
