@@ -26,9 +26,9 @@ GATE_UP_TRAFFIC_BYTES = 19_302_765   # counters: 149,528 128-B + 1,525.7 64-B re
 # matrix-core utilisation of the prefill's table products, rocprofv3's MfmaUtil per dispatch (MFMA busy cycles over
 # GUI-active cycles x SIMDs) from `rocprofv3 --pmc MfmaUtil --kernel-include-regex k_pf_ -- python3 bench.py
 # --prefill-only --prefill-reps 2`: a counter run, not measurable from inside this process
-PREFILL_MFMA_UTIL_PCT = {"ffn_gate_up k_pf_gemm_lds<1,false,4,32>": 29.4, "in_proj k_pf_gemm_lds<0,false,4,32>": 19.7,
-                         "2048-row tables k_pf_gemm_lds<0,false,4,16>": 19.3,
-                         "q|k|v|gate k_pf_gemm_lds<0,false,4,16>": 19.5}
+PREFILL_MFMA_UTIL_PCT = {"ffn_gate_up k_pf_gemm_lds<1,false,4,32>": 30.7, "in_proj k_pf_gemm_lds<0,false,4,32>": 19.5,
+                         "2048-row tables k_pf_gemm_lds<0,false,4,16>": 20.8,
+                         "q|k|v|gate k_pf_gemm_lds<0,false,4,16>": 20.5}
 N_CTX = 512
 PROMPT = 32
 
