@@ -22,6 +22,14 @@ struct pf_cut {
 
 enum { PFR_FIRST = 0, PFR_RESID = 1 };
 
+struct pf_conv_args {       // gated short conv along positions, then the cut of its output
+    const float* bcx;       // [n][3E] in_proj output: per 8 channels, 8 b rows, 8 c rows, 8 x rows
+    const float* w;         // [d_conv + 1][E] taps, the newest last
+    float* state;           // [d_conv][E] this layer's conv memory, oldest tap first
+    int n, E, d_conv;
+    pf_cut cut;
+};
+
 // one workgroup per position: the layer's first norm (after the embedding) or the post-norm residual, then the
 // norm in front of the next table and its cut (or the output norm into hidden rows)
 struct pf_rows_args {
@@ -37,6 +45,8 @@ struct pf_rows_args {
     const float* w_pre;     // h = norm(x) * w_pre
     pf_cut cut;             // cut of h (q null: none)
     float* hidden;          // [n][E] h rows (null: none)
+    pf_conv_args conv;      // PFR_RESID with conv.state set: a conv layer's memory update (the last d_conv positions'
+                            // b x values) done by extra workgroups of this launch, after the conv has read the memory
 };
 
 struct pf_gemm_args {
@@ -54,13 +64,6 @@ struct pf_cutk_args {       // cut of n rows of K floats
     pf_cut cut;
 };
 
-struct pf_conv_args {       // gated short conv along positions, then the cut of its output
-    const float* bcx;       // [n][3E] in_proj output: per 8 channels, 8 b rows, 8 c rows, 8 x rows
-    const float* w;         // [d_conv + 1][E] taps, the newest last
-    float* state;           // [d_conv][E] this layer's conv memory, oldest tap first
-    int n, E, d_conv;
-    pf_cut cut;
-};
 
 struct pf_attn_args {       // causal attention of n positions (keys and values of all of them in the cache first)
     const float* qkv;       // [n][ld]: q (H*D) | k (Hk*D) | v (Hk*D) | gate (H)
@@ -81,7 +84,8 @@ hipError_t launch_pf_gemm(int epi, const pf_gemm_args& a, hipStream_t s);
 // workgroups, each one 32-channel block)
 bool pf_swiglu_cut_takes(const pf_gemm_args& a);
 hipError_t launch_pf_cut(const pf_cutk_args& a, hipStream_t s);
-hipError_t launch_pf_conv(const pf_conv_args& a, hipStream_t s);
+// the conv along positions and its cut; the conv memory update rides on the next launch_pf_rows (its conv field)
+hipError_t launch_pf_conv_lanes(const pf_conv_args& a, hipStream_t s);
 hipError_t launch_pf_kv(const pf_attn_args& a, hipStream_t s);
 hipError_t launch_pf_attn(const pf_attn_args& a, hipStream_t s);
 

@@ -31,6 +31,24 @@ __device__ __forceinline__ void cut_store(const pf_cut& c, int n, int j, int p, 
     c.s[(size_t)j * n + p] = d * (float)sum;
 }
 
+// the conv memory after a batch (imi/core/seoul.cpp:562-577): tap tt of channel e becomes b x of position n - d_conv + tt,
+// or, for a batch shorter than the memory, the memory's own tap tt + n; increasing tt reads only taps not yet rewritten
+__device__ __forceinline__ void conv_state_update(const pf_conv_args& a, int e) {
+    if (e >= a.E) return;
+    const int ub = 24 * (e >> 3) + (e & 7), dc = a.d_conv, E = a.E;
+    for (int tt = 0; tt < dc; tt++) {
+        const int q = a.n - dc + tt;
+        float v;
+        if (q >= 0) {
+            const float* rq = a.bcx + (size_t)q * 3 * E + ub;
+            v = rq[0] * rq[16];
+        } else {
+            v = a.state[(size_t)(tt + a.n) * E + e];
+        }
+        a.state[(size_t)tt * E + e] = v;
+    }
+}
+
 // ---------------------------------------------------------------- per-position norms
 // PFR_FIRST: x = the word's dequantized row (Q4_0: (code - 8) * d; Q6_K: imi_q6k_dequant_row) or the given embedding
 // row (imi/core/seoul.cpp:363-364);
@@ -45,6 +63,11 @@ __global__ __launch_bounds__(64 * PFR_PPW) void k_pf_rows(pf_rows_args a) {
     __shared__ __attribute__((aligned(16))) float xs_all[PFR_PPW][2048];
     __shared__ __attribute__((aligned(16))) float hs_all[PFR_PPW][2048];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, p = blockIdx.x * PFR_PPW + wv, E = a.E, nb = E / 32;
+    const int nwg = (a.n + PFR_PPW - 1) / PFR_PPW;
+    if (MODE == PFR_RESID && (int)blockIdx.x >= nwg) {   // the conv memory update's workgroups (a.conv.state set)
+        conv_state_update(a.conv, ((int)blockIdx.x - nwg) * 64 * PFR_PPW + (int)threadIdx.x);
+        return;
+    }
     if (p >= a.n) return;
     float* xs = xs_all[wv];
     float* hs = hs_all[wv];
@@ -526,22 +549,6 @@ __global__ __launch_bounds__(256) void k_pf_conv_lanes(pf_conv_args a) {
 }
 
 // the conv memory after the batch: its last d_conv b x values (older memory where the batch is shorter)
-__global__ __launch_bounds__(256) void k_pf_conv_state(pf_conv_args a) {
-    const int e = blockIdx.x * 256 + threadIdx.x;
-    if (e >= a.E) return;
-    const int ub = 24 * (e >> 3) + (e & 7), dc = a.d_conv, E = a.E;
-    for (int tt = 0; tt < dc; tt++) {   // increasing tt reads only taps not yet rewritten
-        const int q = a.n - dc + tt;
-        float v;
-        if (q >= 0) {
-            const float* rq = a.bcx + (size_t)q * 3 * E + ub;
-            v = rq[0] * rq[16];
-        } else {
-            v = a.state[(size_t)(tt + a.n) * E + e];
-        }
-        a.state[(size_t)tt * E + e] = v;
-    }
-}
 
 // ---------------------------------------------------------------- attention
 // keys and values of the batch into the fp16 cache: k = rope(norm(k) * k_norm) at the position (imi/core/seoul.cpp:
@@ -1003,7 +1010,9 @@ __global__ __launch_bounds__(256) void k_pf_attn_mf(pf_attn_args a) {
 
 hipError_t launch_pf_rows(int mode, const pf_rows_args& a, hipStream_t s) {
     if (a.E % 32 || a.E > 2048 || a.n < 1) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((a.n + PFR_PPW - 1) / PFR_PPW));
+    const int extra = mode == PFR_RESID && a.conv.state ? (a.conv.E + 64 * PFR_PPW - 1) / (64 * PFR_PPW) : 0;
+    if (extra && (a.conv.E % 32 || a.conv.n < 1 || a.conv.d_conv < 1 || !a.conv.bcx)) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((a.n + PFR_PPW - 1) / PFR_PPW + extra));
     if (mode == PFR_FIRST)
         hipLaunchKernelGGL(k_pf_rows<PFR_FIRST>, grid, dim3(64 * PFR_PPW), 0, s, a);
     else
@@ -1064,15 +1073,13 @@ hipError_t launch_pf_cut(const pf_cutk_args& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_pf_conv(const pf_conv_args& a, hipStream_t s) {
+hipError_t launch_pf_conv_lanes(const pf_conv_args& a, hipStream_t s) {
     if (a.E % 32 || a.n < 1 || a.d_conv < 1) return hipErrorInvalidValue;
     const long long total = (long long)a.n * a.E;   // a thread per (position, channel)
     hipLaunchKernelGGL(k_pf_conv_lanes, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_pf_conv_state, dim3((a.E + 255) / 256), dim3(256), 0, s, a);
     return hipGetLastError();
 }
+
 
 hipError_t launch_pf_kv(const pf_attn_args& a, hipStream_t s) {
     if (a.D > 128 || a.D % 32 || a.n < 1) return hipErrorInvalidValue;

@@ -79,9 +79,9 @@ int enqueue_chunk(sh_ctx* c, sh_state* st, int m, bool have_tokens, bool have_em
     const pf_cut act_cut{(int8_t*)c->pf_act, (float*)((char*)c->pf_act + nact), (float*)((char*)c->pf_act + nact + nact / 8)};
     for (size_t il = 0; il < c->layers.size(); il++) {
         const layer_dev& L = c->layers[il];
+        pf_conv_args cv{};   // (a conv layer: its memory update rides on the next rows launch)
         if (L.conv) {
             PCHK(gemm(L.in_proj, EPI_STORE, c->pf_big, 3 * E, cut));
-            pf_conv_args cv{};
             cv.bcx = c->pf_big;
             cv.w = L.conv_w;
             cv.state = st->conv + (size_t)L.ci * I.d_conv * E;
@@ -89,7 +89,7 @@ int enqueue_chunk(sh_ctx* c, sh_state* st, int m, bool have_tokens, bool have_em
             cv.E = E;
             cv.d_conv = I.d_conv;
             cv.cut = cut;
-            PCHK(launch_pf_conv(cv, s));
+            PCHK(launch_pf_conv_lanes(cv, s));
             PCHK(gemm(L.out_proj, EPI_STORE, c->pf_y, E, cut));
         } else {
             PCHK(gemm(L.qkvg, EPI_STORE, c->pf_big, c->nqkv, cut));
@@ -115,6 +115,7 @@ int enqueue_chunk(sh_ctx* c, sh_state* st, int m, bool have_tokens, bool have_em
             PCHK(gemm(L.o, EPI_STORE, c->pf_y, E, cut));
         }
         pf_rows_args f = r;
+        f.conv = cv;
         f.w_post = L.post_attn_norm;
         f.y = c->pf_y;
         f.w_pre = L.ffn_norm;
