@@ -1577,9 +1577,11 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
                          min(__builtin_amdgcn_readlane(lowb, 32), __builtin_amdgcn_readlane(lowb, 48)));
     if (lane == 0) { red_d[wv] = wsum; red_i[wv] = wlow; }
     __syncthreads();
-    // 1 / sum on wave 0 only, which runs the value chains: no barrier after it (every lane computes the same value)
-    float inv = 0.0f;
+    // 1 / sum on wave 0 only, which runs the value chains: no barrier after it (every lane computes the same value);
+    // the head gate there too, ahead of the chains, whose dependent steps leave room for its instructions
+    float inv = 0.0f, gate = 0.0f;
     if (wv == 0) {
+        gate = 1.0f / (1.0f + expf_glibc_t(-gin, etab));
         double tot = 0.0;
         int lb = 1 << 20;
 #pragma unroll
@@ -1687,7 +1689,6 @@ __global__ __launch_bounds__(512) void k_attn_head(attn_args a) {
         __syncthreads();
     }
     if (wv == 0 && lane < D) {
-        const float gate = 1.0f / (1.0f + expf_glibc_t(-gin, etab));
 #pragma unroll
         for (int c = 0; c < DPL; c++)
             if (lane + 64 * c < D) a.att[(size_t)m * Hq + h * D + lane + 64 * c] = o[c] * gate;
