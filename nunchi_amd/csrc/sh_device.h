@@ -194,6 +194,29 @@ __device__ __forceinline__ float rms_scale_wave(Ptr x, int n, float eps) {
     return 1.0f / sqrtf(s / (float)n + eps);
 }
 
+// rms_scale_wave's values (the same chains and combine) for a row of exactly 32 NT values in global memory: every
+// operand is requested before the chains start (one memory round trip; fetched a batch ahead of the chains, as from
+// LDS, each batch of a row from memory was a round trip of its own)
+template <int NT, class Ptr>
+__device__ __forceinline__ float rms_scale_wave_g(Ptr x, float eps) {
+    constexpr int n = 32 * NT;
+    const int lane = threadIdx.x & 63;
+    float a = 0.0f;
+    if (lane < 32) {
+        float v[NT];
+#pragma unroll
+        for (int t = 0; t < NT; t++) v[t] = x[32 * t + lane];
+#pragma unroll
+        for (int t = 0; t < NT; t++) a = fmaf(v[t], v[t], a);
+    }
+    const float a1 = __shfl(a, (lane + 8) & 63), a2 = __shfl(a, (lane + 16) & 63), a3 = __shfl(a, (lane + 24) & 63);
+    const float v = (a + a1) + (a2 + a3);            // lanes 0..7
+    const float r = v + __shfl(v, (lane + 4) & 63);  // lanes 0..3: v_l + v_{l+4}
+    const float q = r + __shfl(r, (lane + 2) & 63);  // lane 0: (r0 + r2), lane 1: (r1 + r3)
+    const float s = __shfl(q, 0) + __shfl(q, 1);
+    return 1.0f / sqrtf(s / (float)n + eps);
+}
+
 // q or k of one head: norm (imi's order) times its weight, then the NEOX rope with the host's cos/sin row of this
 // position (imi/core/seoul.cpp:19-28). One wave; lane holds dimensions lane + 64 c (c < DPL), so at D 128 a rope pair
 // (i, i + 64) sits in one lane and at D <= 64 the partner comes by a shuffle. stg: D floats of staging.

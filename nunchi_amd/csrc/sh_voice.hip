@@ -22,7 +22,8 @@ template <int P>
 __device__ __forceinline__ void position_scales(const vtab_args& a, float* scl) {
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     for (int p = w; p < P; p += VX_THREADS / 64) {
-        const float s = rms_scale_wave(a.src + (size_t)p * a.src_ld, a.W.cols, a.eps);
+        const float* row = a.src + (size_t)p * a.src_ld;
+        const float s = a.W.cols == 1024 ? rms_scale_wave_g<32>(row, a.eps) : rms_scale_wave(row, a.W.cols, a.eps);
         if (lane == 0) scl[p] = s;
     }
 }
