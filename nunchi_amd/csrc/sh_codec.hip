@@ -199,7 +199,7 @@ __global__ __launch_bounds__(CX_NT) void k_cresid(cresid_args a) {
     const float* y = a.y + (size_t)p * a.E;
     float* x = a.x + (size_t)p * a.E;
     if (threadIdx.x < 64) {
-        const float s = rms_scale_wave(y, a.E, a.eps);
+        const float s = a.E == 512 ? rms_scale_wave_g<16>(y, a.eps) : rms_scale_wave(y, a.E, a.eps);
         if (threadIdx.x == 0) sc = s;
     }
     __syncthreads();

@@ -391,7 +391,7 @@ __global__ __launch_bounds__(ET) void k_efinal(const float* x, const float* post
     }
     float* hs = hs_all + (size_t)wv * E;
     const float* xp = x + (size_t)p * E;
-    const float s = rms_scale_wave(xp, E, eps);
+    const float s = E == 768 ? rms_scale_wave_g<24>(xp, eps) : rms_scale_wave(xp, E, eps);
     for (int e = lane; e < E; e += 64) hs[e] = xp[e] * s * post_ln[e];
     __builtin_amdgcn_wave_barrier();
     if (lane == 0) {

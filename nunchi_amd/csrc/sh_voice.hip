@@ -349,7 +349,7 @@ __global__ __launch_bounds__(VX_THREADS) void k_vone(vone_args a, int cols) {
         if (set >= *a.n_need) return;
         cb = a.need[set];
         src = a.src + (size_t)cb * cols;
-        const float s1 = rms_scale_wave(src, cols, a.eps);
+        const float s1 = cols == 1024 ? rms_scale_wave_g<32>(src, a.eps) : rms_scale_wave(src, cols, a.eps);
         for (int k = threadIdx.x; k < cols; k += VX_THREADS) xs[k] = src[k] * s1 * a.out_norm[k];
         __syncthreads();
         const float s2 = rms_scale_wave(static_cast<const float*>(xs), cols, a.eps);
