@@ -47,7 +47,34 @@ int prefill_buffers(sh_ctx* c) {
 }
 
 // one chunk of m <= PF_MAX_N positions starting at the state's position
-int enqueue_chunk(sh_ctx* c, sh_state* st, int m, bool have_tokens, bool have_embd) {
+// the word scores' workgroups for the prefill's last position (the decode step's kernel and grid)
+int prefill_scores_grid(sh_ctx* c, const gemv_args& v) {
+    return c->vocab6.codes ? SH_Q6K_GRID : gemv_logits_grid(1, PRO_RESID_NORM, v, c->vocab_grid);
+}
+
+gemv_args prefill_scores_args(sh_ctx* c, const layer_dev& last, int m) {
+    const int E = c->info.n_embd;
+    gemv_args v{};
+    v.P = c->P_dev;
+    v.E = E;
+    v.eps = c->eps;
+    v.x_in = c->pf_x + (size_t)(m - 1) * E;   // (x before the last FFN residual: the kernel adds it itself)
+    v.y_in = c->pf_y + (size_t)(m - 1) * E;
+    v.w_post = last.post_ffn_norm;
+    v.w_pre = c->out_norm;
+    v.W = c->vocab;
+    v.W6 = c->vocab6;
+    v.units = c->vocab.rows / 8;
+    v.out = c->logits;
+    v.out_ld = c->info.n_vocab;
+    v.part_v = c->part_v;
+    v.part_i = c->part_i;
+    return v;
+}
+
+// scores: the last position's word scores with the decode step's kernel (its prologue forms the output norm of the
+// last FFN residual itself), launched before the last rows kernel updates x in place
+int enqueue_chunk(sh_ctx* c, sh_state* st, int m, bool have_tokens, bool have_embd, bool scores) {
     const sh_model_info& I = c->info;
     const int E = I.n_embd, D = I.head_dim, Hq = I.n_head * D;
     hipStream_t s = c->stream;
@@ -138,6 +165,12 @@ int enqueue_chunk(sh_ctx* c, sh_state* st, int m, bool have_tokens, bool have_em
         pf_rows_args z = r;
         z.y = c->pf_y;
         z.w_post = L.post_ffn_norm;
+        if (scores && il + 1 == c->layers.size()) {
+            const gemv_args v = prefill_scores_args(c, L, m);
+            const int grid = prefill_scores_grid(c, v);
+            if (c->vocab6.codes) PCHK(launch_scores_q6k(1, grid, v, s));
+            else PCHK(launch_gemv(1, PRO_RESID_NORM, EPI_LOGITS, grid, v, s));
+        }
         if (il + 1 < c->layers.size()) {
             z.w_pre = c->layers[il + 1].attn_norm;
         } else {   // the output norm: hidden rows, no cut
@@ -175,7 +208,7 @@ int run_prefill(sh_ctx* c, sh_state* st, const int32_t* tokens, const float* emb
         const int m = std::min(PF_MAX_N, n - i0);
         if (tokens) PCHK(hipMemcpyAsync(c->pf_tok, tokens + i0, (size_t)m * 4, hipMemcpyHostToDevice, c->stream));
         if (embd) PCHK(hipMemcpyAsync(c->pf_emb, embd + (size_t)i0 * E, (size_t)m * E * 4, hipMemcpyHostToDevice, c->stream));
-        const int rc = enqueue_chunk(c, st, m, tokens != nullptr, embd != nullptr);
+        const int rc = enqueue_chunk(c, st, m, tokens != nullptr, embd != nullptr, want_logits && i0 + m == n);
         if (rc != SH_OK) return rc;
         if (hidden_all) PCHK(hipMemcpyAsync(hidden_all + (size_t)i0 * E, c->pf_hid, (size_t)m * E * 4, hipMemcpyDeviceToHost, c->stream));
         // the host arrays of this chunk are read before the next chunk's copies overwrite the device buffers
@@ -186,23 +219,8 @@ int run_prefill(sh_ctx* c, sh_state* st, const int32_t* tokens, const float* emb
     const float* hl = c->pf_hid + (size_t)(last_m - 1) * E;
     if (hidden_last) PCHK(hipMemcpyAsync(hidden_last, hl, (size_t)E * 4, hipMemcpyDeviceToHost, c->stream));
     int32_t b = -1;
-    if (want_logits) {
-        gemv_args v{};
-        v.W = c->vocab;
-        v.units = c->vocab.rows / 8;
-        v.src = hl;
-        v.src_ld = E;
-        v.out = c->logits;
-        v.out_ld = I.n_vocab;
-        v.part_v = c->part_v;
-        v.part_i = c->part_i;
-        v.E = E;
-        v.eps = c->eps;
-        v.P = c->P_dev;
-        v.W6 = c->vocab6;
-        const int grid = c->vocab6.codes ? SH_Q6K_GRID : v.units < c->vocab_grid ? v.units : c->vocab_grid;
-        if (c->vocab6.codes) PCHK(launch_scores_q6k(1, grid, v, c->stream));   // src: the last hidden row, normed
-        else PCHK(launch_gemv(1, PRO_CUT, EPI_LOGITS, grid, v, c->stream));
+    if (want_logits) {   // (the scores themselves were launched in the last chunk)
+        const int grid = prefill_scores_grid(c, prefill_scores_args(c, c->layers.back(), last_m));
         final_args z{};
         z.E = E;
         z.eps = c->eps;
