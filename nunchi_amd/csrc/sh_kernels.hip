@@ -1731,6 +1731,20 @@ __global__ __launch_bounds__(256) void k_final(final_args a) {
                   offsetof(step_params, greedy) == 28 && offsetof(step_params, out_tok) == 80, "step_params layout");
     SH_GLOBAL step_params* const P = global_ptr(a.P);
     const int pv = ((const SH_GLOBAL int*)P)[tid < 8 ? tid : tid < 12 ? 12 + tid : 0];
+    // every conversation's first partial and score 0 requested before the picks too (at two conversations the
+    // second's loads otherwise went out after the first's pick); score 0 by a load on every path (without scores it
+    // reads a partial, unused: a conditional load had its NaN test, and a wait for it, ahead of the partials)
+    float pv0[M], l0v[M];
+    int pi0[M];
+    if (a.part_v) {
+        const int k0 = tid < a.n_part ? tid : a.n_part - 1;
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            pv0[m] = a.part_v[m * a.n_part + k0];
+            pi0[m] = a.part_i[m * a.n_part + k0];
+            l0v[m] = (a.logits ? a.logits : a.part_v)[a.logits ? (size_t)m * a.ld_logits : 0];
+        }
+    }
     int bests[M];
 #pragma unroll
     for (int m = 0; m < M; m++) {
@@ -1755,13 +1769,10 @@ __global__ __launch_bounds__(256) void k_final(final_args a) {
         }
         int best = -1;
         if (a.part_v) {
-            // score 0 requested with the partials (imi's rule below needs it), by a load on every path (without scores
-            // it reads a partial, unused): a conditional load had its NaN test, and a wait for it, before the partials
-            // were requested
-            const float l0 = (a.logits ? a.logits : a.part_v)[a.logits ? (size_t)m * a.ld_logits : 0];
-            float v = -INFINITY;
-            int bi = 0x7fffffff;
-            for (int k = tid; k < a.n_part; k += 256) {
+            const float l0 = m == 0 ? l0v[0] : l0v[M - 1];   // (score 0, which imi's rule below needs)
+            float v = tid < a.n_part ? (m == 0 ? pv0[0] : pv0[M - 1]) : -INFINITY;
+            int bi = tid < a.n_part ? (m == 0 ? pi0[0] : pi0[M - 1]) : 0x7fffffff;
+            for (int k = tid + 256; k < a.n_part; k += 256) {
                 const float ov = a.part_v[m * a.n_part + k];
                 const int oi = a.part_i[m * a.n_part + k];
                 if (ov > v || (ov == v && oi < bi)) { v = ov; bi = oi; }
