@@ -819,20 +819,32 @@ __global__ __launch_bounds__(512) void k_gemv_norm(gemv_args a) {
             if (cor_lane) l_cor[c] = chain;
         }
         __syncthreads();
-        if (acc_lane) l_out[c] = HM ? chain + l_cor[c] : fmaf(-8.0f, l_cor[c], chain);
-        __syncthreads();
+        // the row's value stays in the acc lane's register. The conv epilogue reads rows 8 and 16 lanes on, across a
+        // wave's end, through LDS and a barrier; a SwiGLU gate row (lane i < 8 of a 16-lane unit, units aligned to 16
+        // lanes) takes its up row from lane i + 8 of the same DPP row, a shift computed by every lane outside the
+        // branches (the register pin keeps the compiler from folding the shift into a user under a narrower mask)
+        const float outv = acc_lane ? (HM ? chain + l_cor[c] : fmaf(-8.0f, l_cor[c], chain)) : 0.0f;
+        float upv = 0.0f;
+        if (EPI == EPI_SWIGLU) {
+            upv = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(outv), 0x108, 0xF, 0xF, true));
+            asm volatile("" : "+v"(upv));
+        }
+        if (EPI == EPI_CONV) {
+            if (acc_lane) l_out[c] = outv;
+            __syncthreads();
+        }
         // ---- epilogue: thread c < C holds row r of the chunk for input m ----
         float act = 0.0f;   // EPI_SWIGLU: this thread's channel output (threads on up rows: 0)
         if (t < C) {
             const int m = t / R, r = t - m * R;
-            const float v = l_out[t];
+            const float v = outv;
             if (r < 8 * gv) {
                 if (EPI == EPI_STORE) {
                     a.out[(size_t)m * a.out_ld + 8 * g0 + r] = v;
                 } else if (EPI == EPI_SWIGLU) {   // unit = (gate group, up group) of 8 channels
                     const int ui = r >> 4, i = r & 15;
                     if (i < 8) {
-                        act = silu_t(v, (const uint64_t*)l_exp) * l_out[t + 8];
+                        act = silu_t(v, (const uint64_t*)l_exp) * upv;
                         a.out[(size_t)m * a.out_ld + 8 * (u0 + ui) + i] = act;
                     }
                 } else if (EPI == EPI_CONV) {     // unit = (b, c, x) groups of 8 channels
