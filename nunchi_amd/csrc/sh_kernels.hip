@@ -1779,39 +1779,51 @@ __global__ __launch_bounds__(256) void k_final(final_args a) {
             for (int i = tid; i < E; i += 256) a.hidden_out[m * E + i] = l_x[i] * sc2 * a.w_out[i];
             __syncthreads();
         }
-        int best = -1;
-        if (a.part_v) {
-            const float l0 = m == 0 ? l0v[0] : l0v[M - 1];   // (score 0, which imi's rule below needs)
-            float v = tid < a.n_part ? (m == 0 ? pv0[0] : pv0[M - 1]) : -INFINITY;
-            int bi = tid < a.n_part ? (m == 0 ? pi0[0] : pi0[M - 1]) : 0x7fffffff;
+    }
+    // the picks of every conversation at once (their shuffle trees interleave; one LDS exchange and barrier for all)
+#pragma unroll
+    for (int m = 0; m < M; m++) bests[m] = -1;
+    if (a.part_v) {
+        float v[M];
+        int bi[M];
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            v[m] = tid < a.n_part ? pv0[m] : -INFINITY;
+            bi[m] = tid < a.n_part ? pi0[m] : 0x7fffffff;
             for (int k = tid + 256; k < a.n_part; k += 256) {
                 const float ov = a.part_v[m * a.n_part + k];
                 const int oi = a.part_i[m * a.n_part + k];
-                if (ov > v || (ov == v && oi < bi)) { v = ov; bi = oi; }
+                if (ov > v[m] || (ov == v[m] && oi < bi[m])) { v[m] = ov; bi[m] = oi; }
             }
-            // (greater score, or equal score and lower row, wins: a total order on the partials, none of them NaN, so
-            // any reduction order picks the same row) by shuffles within each wave, then the 4 waves' picks
+        }
+        // (greater score, or equal score and lower row, wins: a total order on the partials, none of them NaN, so
+        // any reduction order picks the same row) by shuffles within each wave, then the 4 waves' picks
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const float ov = __shfl_xor(v, o);
-                const int oi = __shfl_xor(bi, o);
-                if (ov > v || (ov == v && oi < bi)) { v = ov; bi = oi; }
+        for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                const float ov = __shfl_xor(v[m], o);
+                const int oi = __shfl_xor(bi[m], o);
+                if (ov > v[m] || (ov == v[m] && oi < bi[m])) { v[m] = ov; bi[m] = oi; }
             }
-            if ((tid & 63) == 0) { red_v[tid >> 6] = v; red_i[tid >> 6] = bi; }
-            __syncthreads();
-            v = red_v[0];
-            bi = red_i[0];
+        if ((tid & 63) == 0)
+#pragma unroll
+            for (int m = 0; m < M; m++) { red_v[4 * m + (tid >> 6)] = v[m]; red_i[4 * m + (tid >> 6)] = bi[m]; }
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            float bv = red_v[4 * m];
+            int bj = red_i[4 * m];
 #pragma unroll
             for (int w = 1; w < 4; w++)
-                if (red_v[w] > v || (red_v[w] == v && red_i[w] < bi)) { v = red_v[w]; bi = red_i[w]; }
+                if (red_v[4 * m + w] > bv || (red_v[4 * m + w] == bv && red_i[4 * m + w] < bj)) { bv = red_v[4 * m + w]; bj = red_i[4 * m + w]; }
             // imi's loop (imi/core/hear.cpp:67-68): best = 0, then v replaces it only if logits[v] > logits[best].
             // The partials give the first maximum over the scores that are not NaN; imi keeps 0 when score 0 is NaN
             // (nothing compares greater than it) and when every score is NaN (the partials then hold no row)
-            best = bi;
-            if (best < 0 || best >= a.ld_logits || (a.logits && isnan(l0))) best = 0;
-            __syncthreads();
+            int best = bj;
+            if (best < 0 || best >= a.ld_logits || (a.logits && isnan(l0v[m]))) best = 0;
+            bests[m] = best;
         }
-        bests[m] = best;
     }
     // (the lane reads stay outside the thread-0 branch, so the loads above run on all of wave 0's lanes)
     const int n_done = __builtin_amdgcn_readlane(pv, 6), greedy = __builtin_amdgcn_readlane(pv, 7);
